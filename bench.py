@@ -1,0 +1,295 @@
+#!/usr/bin/env python
+"""Benchmark of the MI355X ring-attention compute path.
+
+Headline (BASELINE.json ``metric``): the simulated P=8 zigzag-causal ring of
+configs[2] (S=131072, 16384 tokens per rank as two 8192 chunks, H=16 MHA, D=128,
+bf16) forward + backward on ONE GPU, reported as TFLOP/s of algorithmic work
+(FA2 convention: 4*D*H per attended pair forward, 10*D*H backward; masked pairs
+are not counted). One step = one full emulated ring forward + reverse-ring
+backward over synthetic inputs already resident in HBM.
+
+The JSON line also carries the roofline of the dominant kernel (HIP events around
+every launch on the launching stream), the per-kernel breakdown, the HBM-bound
+kernels (zigzag shard of q/k/v at configs[2], standalone LSE merge at configs[1],
+cp_linear_scan fwd+bwd at configs[4]) and the CPU baseline: the oracle (torch CPU
+fp32 restatement of the reference ``math`` path) timed on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import subprocess
+import sys
+import time
+
+import torch
+
+BF16_PEAK_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CU x 4096 FLOP/clk x 2.4 GHz)
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+
+
+def _sync():
+    torch.cuda.synchronize()
+
+
+def _gen(shape, seed, dtype=torch.bfloat16, scale=1.0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+    if scale != 1.0:
+        x.mul_(scale)
+    return x.to(dtype)
+
+
+def _time(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    _sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    _sync()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+# ---------------------------------------------------------------- configs[2] ring
+def ring_workload(steps, warmup):
+    from ringmaster_amd.ring.schedule import ring_pairs_per_rank
+    from ringmaster_amd.ring.zigzag import KernelTimer, zigzag_ring_attention
+
+    P, S, H, D = 8, 131072, 16, 128
+    L = S // P
+    q = _gen((P, 1, H, L, D), 1).requires_grad_(True)
+    k = _gen((P, 1, H, L, D), 2).requires_grad_(True)
+    v = _gen((P, 1, H, L, D), 3).requires_grad_(True)
+    dout = _gen((P, 1, L, H, D), 4)
+    pairs = P * ring_pairs_per_rank(P, L)
+    assert pairs == S * (S + 1) // 2
+    flops = 14 * D * H * pairs
+    timer = KernelTimer()
+
+    def step(t=None):
+        out = zigzag_ring_attention(q, k, v, timer=t)
+        torch.autograd.grad(out, (q, k, v), dout)
+
+    for _ in range(warmup):
+        step()
+    _sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(timer)
+    _sync()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    # per-kernel averages over the timed region; algorithmic FLOPs per launch:
+    # each launch is one ring step over all P ranks = pairs / P
+    per_launch_pairs = pairs / P
+    kern = {}
+    credit = {"attn_fwd": 4, "attn_bwd_dkdv": 8, "attn_bwd_dq": 2}
+    for name in ("attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq", "attn_bwd_delta"):
+        m = timer.mean_ms(name)
+        if m is None:
+            continue
+        n = timer.count(name) // steps
+        entry = {"mean_ms": round(m, 4), "launches_per_step": n,
+                 "ms_per_step": round(m * n, 3)}
+        if name in credit:
+            tf = credit[name] * D * H * per_launch_pairs / (m * 1e-3) / 1e12
+            entry["algorithmic_tflops"] = round(tf, 1)
+            entry["frac_bf16_peak"] = round(tf / BF16_PEAK_TFLOPS, 4)
+        kern[name] = entry
+    dom = max((n for n in credit if n in kern), key=lambda n: kern[n]["ms_per_step"])
+    roof = {"kernel": dom, "bound": "mfma", "achieved": kern[dom]["algorithmic_tflops"],
+            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": kern[dom]["frac_bf16_peak"], "traffic": None,
+            "algorithmic_flop_per_launch": credit[dom] * D * H * per_launch_pairs}
+    return {"ms": ms, "flops": flops, "kernels": kern, "roofline": roof,
+            "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2)}
+
+
+# ---------------------------------------------------------------- HBM-bound kernels
+def shard_workload(steps, warmup):
+    from ringmaster_amd.shard import zigzag_shard
+
+    P, S, H, D = 8, 131072, 16, 128
+    xs = [_gen((1, S, H, D), i) for i in (1, 2, 3)]
+    nbytes = 3 * 2 * xs[0].numel() * 2
+    ms = _time(lambda: [zigzag_shard(x, P) for x in xs], steps, warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del xs
+    return {"ms": round(ms, 4), "bytes": nbytes, "GB/s": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def merge_workload(steps, warmup):
+    from ringmaster_amd.ring.merge import update_out_and_lse
+
+    S, H, D = 16384, 32, 128
+    out = _gen((1, S, H, D), 6, torch.float32)
+    lse = _gen((1, S, H, 1), 7, torch.float32)
+    blk = _gen((1, S, H, D), 8)
+    blk_lse = _gen((1, H, S), 9, torch.float32)
+    nbytes = 677_380_096
+    ms = _time(lambda: update_out_and_lse(out, lse, blk, blk_lse), steps, warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "bytes": nbytes, "GB/s": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def scan_workload(steps, warmup):
+    from ringmaster_amd.strategies.state_passing import linear_scan_backward, linear_scan_forward
+
+    L, d, G, P = 256, 64 * 64 * 128, 64, 8
+    g = torch.Generator(device="cuda").manual_seed(5)
+    A = -torch.exp(torch.rand(G, generator=g, device="cuda") * math.log(16.0))
+    dt = torch.nn.functional.softplus(torch.randn(1, L, G, generator=g, device="cuda"))
+    a = torch.exp(A * dt).contiguous()                   # per-chunk, per-head decay
+    b = torch.randn(1, L, d, generator=g, device="cuda")  # chunk states
+    dh = torch.randn(1, L, d, generator=g, device="cuda")
+    h = linear_scan_forward(a, b, P)
+    fwd_ms = _time(lambda: linear_scan_forward(a, b, P), steps, warmup)
+    bwd_ms = _time(lambda: linear_scan_backward(a, h, dh, P), steps, warmup)
+    fb, bb = 1_073_807_360, 1_610_612_736
+    tot = fb + bb
+    gbs = tot / ((fwd_ms + bwd_ms) * 1e-3) / 1e9
+    return {"fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4), "bytes": tot,
+            "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "fwd_GB/s": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
+            "bwd_GB/s": round(bb / (bwd_ms * 1e-3) / 1e9, 1)}
+
+
+def block_workload(steps, warmup):
+    """one non-causal ring step, Hq=32/Hkv=8, 16384^2, D=128, fwd+bwd, merged
+    into a running fp32 (out, lse) from a prior step."""
+    from ringmaster_amd import abi
+    from ringmaster_amd.ring import ops
+
+    S, Hq, Hkv, D = 16384, 32, 8, 128
+    sc = 1.0 / math.sqrt(D)
+    q, k, v = _gen((1, S, Hq, D), 1, scale=sc), _gen((1, S, Hkv, D), 2, scale=sc), \
+        _gen((1, S, Hkv, D), 3, scale=sc)
+    dout = _gen((1, S, Hq, D), 4)
+    acc = _gen((1, S, Hq, D), 6, torch.float32)
+    acc_lse = _gen((1, Hq, S), 7, torch.float32)
+    out = torch.empty((1, S, Hq, D), dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty((1, Hq, S), device="cuda")
+    delta = torch.empty((1, Hq, S), device="cuda")
+    dq = torch.empty((1, S, Hq, D), device="cuda")
+    dk = torch.empty((1, S, Hkv, D), device="cuda")
+    dv = torch.empty_like(dk)
+
+    def step():
+        ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_ACC_FINAL, out=out, lse=lse,
+                                 acc_out=acc, acc_lse=acc_lse)], scale=sc, mask=abi.MASK_FULL)
+        ops.attn_bwd_delta(out, dout, delta, Hkv)
+        ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta,
+                                 dq_mode=abi.GRAD_WRITE_F32, dkv_mode=abi.GRAD_WRITE_F32,
+                                 dq_acc=dq, dk_acc=dk, dv_acc=dv)], scale=sc, mask=abi.MASK_FULL)
+
+    ms = _time(step, steps, warmup)
+    flops = 14 * D * Hq * S * S
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 3), "flops": flops, "TFLOP/s": round(tf, 1),
+            "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(heads=1):
+    """Oracle (torch CPU fp32 restatement of the reference math path): rank 0's complete
+    ring fwd+bwd at configs[2] (P=8, L=16384, D=128) for ``heads`` head(s). Zigzag gives
+    every rank the same pairs, so the rate extrapolates to the whole job."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import ring_math as rm
+    from ringmaster_amd.ring.schedule import ring_pairs_per_rank
+
+    P, L, D = 8, 16384, 128
+    g = torch.Generator().manual_seed(1)
+    mk = lambda: [torch.randn(1, heads, L, D, generator=g) for _ in range(P)]  # noqa: E731
+    qs, ks, vs = mk(), mk(), mk()
+    dos = [torch.randn(1, L, heads, D, generator=g) for _ in range(P)]
+    t0 = time.perf_counter()
+    outs, lses = rm.zigzag_ring_forward(qs, ks, vs, ranks=[0])
+    rm.zigzag_ring_backward(dos, qs, ks, vs, outs, lses, ranks=[0])
+    sec = time.perf_counter() - t0
+    flops = 14 * D * heads * ring_pairs_per_rank(P, L)
+    return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle rank 0 of 8, {heads} head(s), full zigzag ring fwd+bwd at "
+                      f"L=16384, D=128, fp32 torch CPU ({sec:.1f} s; os.cpu_count()="
+                      f"{os.cpu_count()})",
+            "seconds": round(sec, 2)}
+
+
+def _clocks():
+    try:
+        out = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True,
+                             timeout=20).stdout
+        return [ln.strip() for ln in out.splitlines() if "sclk" in ln or "mclk" in ln][:4]
+    except Exception:
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-extras", action="store_true", help="skip the HBM-bound kernels")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=1)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
+              "and emulates the P-rank ring inside one process (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    ring = ring_workload(args.steps, args.warmup)
+    torch.cuda.empty_cache()
+    extras = {}
+    if not args.no_extras:
+        extras["shard_qkv_configs2"] = shard_workload(10, 2)
+        torch.cuda.empty_cache()
+        extras["lse_merge_configs1"] = merge_workload(20, 3)
+        torch.cuda.empty_cache()
+        extras["cp_linear_scan_configs4"] = scan_workload(10, 2)
+        torch.cuda.empty_cache()
+        extras["block_configs1"] = block_workload(3, 1)
+        torch.cuda.empty_cache()
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_heads)
+
+    value = ring["flops"] / (ring["ms"] * 1e-3) / 1e12
+    line = {
+        "metric": "ring fwd+bwd TFLOP/s (% bf16 MFMA peak) at 16k/rank P=8 zigzag, 1 GPU",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ring["ms"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) bf16 q/k/v/dout generated on device (seeds 1-4)",
+        "config": {"workload": "configs[2]: simulated P=8 zigzag-causal ring fwd+bwd, S=131072 "
+                               "(16384/rank as two 8192 chunks), H=16 MHA, D=128, bf16",
+                   "world": 8, "seq_len": 131072, "heads": 16, "head_dim": 128,
+                   "global_batch": 1, "parallelism": "emulated ring P=8 on 1 GPU"},
+        "frac_bf16_peak": round(value / BF16_PEAK_TFLOPS, 4),
+        "roofline": ring["roofline"],
+        "cpu_baseline": cpu,
+        "kernels": ring["kernels"],
+        "extras": extras,
+        "peak_mem_gib": ring["peak_mem_gib"],
+        "clocks": _clocks(),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

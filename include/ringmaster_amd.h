@@ -1,0 +1,207 @@
+/*
+ * ringmaster_amd — C ABI of the MI355X (gfx950) ring-attention compute path.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element strides and sizes (no torch types);
+ *   - validates its arguments on the host before any launch and returns 0 on
+ *     success or a negative RMX_E* code (the message is in rmx_last_error());
+ *   - never throws, aborts or frees across the ABI; all memory is owned by the
+ *     caller;
+ *   - launches asynchronously on the caller's HIP stream (a hipStream_t passed
+ *     as void*; NULL is the default stream);
+ *   - keeps no mutable global state apart from the per-thread error string.
+ *
+ * Tensor conventions follow the reference ring path: q/k/v/out are
+ * [batch, seq, heads, dim] with arbitrary element strides for the first three
+ * axes and a contiguous last axis; lse is [batch, heads, seq] fp32 (natural
+ * log) with a contiguous seq axis. bf16 tensors are passed as uint16_t bit
+ * patterns.
+ */
+#ifndef RINGMASTER_AMD_H
+#define RINGMASTER_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RMX_ABI_VERSION 1
+
+/* error codes */
+#define RMX_OK 0
+#define RMX_EINVAL (-1)   /* bad argument: maps to ValueError */
+#define RMX_EUNSUPPORTED (-2) /* valid but not implemented here: NotImplementedError */
+#define RMX_EDEVICE (-3)  /* HIP runtime / launch failure: RuntimeError */
+
+/* block mask kinds (ring/kernels.py:64-67, ring/varlen_blocks.py:51-58) */
+#define RMX_MASK_FULL 0   /* every (q, k) pair attends */
+#define RMX_MASK_CAUSAL 1 /* bottom-right aligned causal: k <= q + (sk - sq) */
+#define RMX_MASK_DOC 2    /* doc[qg] == doc[kg] && kg <= qg on global indices */
+
+/* forward epilogue modes (online-softmax merge, ring/merge.py:20-31) */
+#define RMX_FWD_WRITE 0       /* out/lse := this block's (out, lse) */
+#define RMX_FWD_ACC_INIT 1    /* acc_out/acc_lse := this block (first ring step) */
+#define RMX_FWD_ACC_MERGE 2   /* acc := merge(acc, block) */
+#define RMX_FWD_ACC_FINAL 3   /* out(bf16)/lse := merge(acc, block); acc untouched */
+
+/* backward gradient output modes */
+#define RMX_GRAD_WRITE_BF16 0 /* grad_bf16 := this block's gradient */
+#define RMX_GRAD_WRITE_F32 1  /* grad_acc := this block's gradient */
+#define RMX_GRAD_ACC_F32 2    /* grad_acc += this block's gradient */
+#define RMX_GRAD_ACC_FINAL 3  /* grad_bf16 := grad_acc + this block's gradient */
+#define RMX_GRAD_NONE 4       /* this gradient is not computed (its kernel is not launched
+                                 when no problem of the call asks for it) */
+
+#define RMX_MAX_BATCHED 16    /* problems per launch; more are split by the library */
+
+/* Layout shared by every problem of one batched attention call. */
+typedef struct rmx_attn_layout {
+  int32_t batch, hq, hkv, head_dim; /* hq % hkv == 0 (GQA: kv_head = q_head / (hq/hkv)) */
+  float scale;                      /* softmax scale (1/sqrt(head_dim) by default) */
+  int32_t mask;                     /* RMX_MASK_* */
+  /* element strides (batch, seq, head) */
+  int64_t q_sb, q_ss, q_sh;
+  int64_t k_sb, k_ss, k_sh;
+  int64_t v_sb, v_ss, v_sh;
+  int64_t o_sb, o_ss, o_sh;   /* bf16 out, dout and the bf16 gradient of q */
+  int64_t a_sb, a_ss, a_sh;   /* fp32 running out / fp32 dq accumulator */
+  int64_t l_sb, l_sh;         /* lse, acc_lse, delta: [batch, head, seq], seq stride 1 */
+  int64_t dk_sb, dk_ss, dk_sh; /* bf16 dk/dv outputs */
+  int64_t ka_sb, ka_ss, ka_sh; /* fp32 dk/dv accumulators */
+} rmx_attn_layout;
+
+/* One block-attention forward problem: q[sq] attends k/v[sk]. */
+typedef struct rmx_fwd_problem {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* out;        /* bf16, may be NULL in ACC_INIT/ACC_MERGE */
+  float* lse;           /* fp32 [b, hq, sq], may be NULL in ACC_INIT/ACC_MERGE */
+  float* acc_out;       /* fp32 running out (ACC_* modes) */
+  float* acc_lse;       /* fp32 running lse (ACC_* modes) */
+  const int32_t* q_gidx; /* RMX_MASK_DOC: global token index of each q row (strictly increasing) */
+  const int32_t* k_gidx; /* RMX_MASK_DOC: global token index of each k row (strictly increasing) */
+  const int32_t* doc;    /* RMX_MASK_DOC: document id per global token (non-decreasing) */
+  int32_t sq, sk;
+  int32_t mode;          /* RMX_FWD_* */
+} rmx_fwd_problem;
+
+/* One block-attention backward problem, using the GLOBAL (merged) out/lse. */
+typedef struct rmx_bwd_problem {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* dout;  /* bf16, o_* strides */
+  const float* lse;      /* fp32 [b, hq, sq] global lse */
+  const float* delta;    /* fp32 [b, hq, sq] rowsum(dout * out_global) */
+  float* dq_acc;         /* fp32, a_* strides (F32 modes) */
+  uint16_t* dq;          /* bf16, o_* strides (WRITE_BF16 / ACC_FINAL) */
+  float* dk_acc;         /* fp32, ka_* strides */
+  float* dv_acc;
+  uint16_t* dk;          /* bf16, dk_* strides */
+  uint16_t* dv;
+  const int32_t* q_gidx;
+  const int32_t* k_gidx;
+  const int32_t* doc;
+  int32_t sq, sk;
+  int32_t dq_mode;       /* RMX_GRAD_* */
+  int32_t dkv_mode;      /* RMX_GRAD_* */
+} rmx_bwd_problem;
+
+int32_t rmx_abi_version(void);
+const char* rmx_last_error(void);
+
+/*
+ * Batched block-attention forward: softmax(scale*Q K^T + mask) V and its fp32
+ * LSE for each problem, with the online-softmax merge into a running fp32
+ * (out, lse) fused into the epilogue.
+ * Replaces the Dao `_flash_attn_forward` op the zigzag ring calls
+ * (ring/zigzag.py:131,134,138 via ring/p2p_attn.py:27-62) together with the
+ * `_merge_full`/`_merge_slice` that follows it (ring/zigzag.py:49-67), and
+ * backs the block provider contract of ring/kernels.py:28-85.
+ */
+int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* problems,
+                     int32_t nproblems, void* stream);
+
+/*
+ * delta[b, h, s] = sum_d dout * out for each problem (FlashAttention-2 backward
+ * preprocess). `out` uses the o_* strides.
+ */
+int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const uint16_t* out,
+                           const uint16_t* dout, float* delta, int32_t sq, void* stream);
+
+/*
+ * Batched block-attention backward with the global out/lse (ring identity,
+ * ring/p2p_attn.py:243-281): dQ, dK, dV of each problem, GQA folded over the
+ * q-head group. Replaces the Dao `_flash_attn_backward` calls of
+ * ring/zigzag.py:219,230,239 and the bf16 `+=` accumulations around them.
+ * Problems of one call must not write the same dk/dv rows (a ring step visits
+ * each KV block once).
+ */
+int32_t rmx_attn_bwd(const rmx_attn_layout* layout, const rmx_bwd_problem* problems,
+                     int32_t nproblems, void* stream);
+
+/*
+ * Standalone online-softmax merge, `update_out_and_lse` (ring/merge.py:20-31):
+ *   new = logaddexp(lse, blk_lse); out = e^(lse-new) out + e^(blk_lse-new) blk_out.
+ * out: fp32 [b, s, h, d] (strides o_*), lse: fp32 [b, s, h] (strides l_*),
+ * blk_out: bf16 (blk_is_f32 == 0) or fp32 [b, s, h, d] (strides bo_*),
+ * blk_lse: fp32 [b, h, s] (strides bl_*). init != 0: out/lse := block
+ * (the `out is None` branch, ring/merge.py:27-28). Updated in place.
+ */
+int32_t rmx_lse_merge(float* out, float* lse, const void* blk_out, int32_t blk_is_f32,
+                      const float* blk_lse, int32_t batch, int32_t seq, int32_t heads,
+                      int32_t head_dim, const int64_t* o_strides /*3*/,
+                      const int64_t* l_strides /*3*/, const int64_t* bo_strides /*3*/,
+                      const int64_t* bl_strides /*2: batch, head*/, int32_t init,
+                      void* stream);
+
+/*
+ * Zigzag (head_tail) shard of `batch` rows of `seq` tokens over `world` ranks:
+ * rank r receives chunks r and 2*world-1-r of the sequence padded to a multiple
+ * of 2*world (balancers.py:18-29, shard.py:150-176), early chunk first. Each
+ * token is a row of row_bytes bytes; src is [batch, seq, row] with batch stride
+ * src_bstride bytes. rank < 0: dst is [world, batch, local, row] (every shard);
+ * rank >= 0: dst is [batch, local, row] (that rank's shard only). Rows past
+ * `seq` (the padding) are copied from pad_row, a device row of row_bytes bytes,
+ * or zero-filled when pad_row is NULL (shard.py:130-147).
+ */
+int32_t rmx_zigzag_gather(const void* src, void* dst, int32_t batch, int32_t seq,
+                          int32_t world, int32_t rank, int64_t row_bytes, int64_t src_bstride,
+                          const void* pad_row, void* stream);
+
+/* Inverse of rmx_zigzag_gather for rank < 0: dst[batch, seq, row] (batch stride
+ * dst_bstride bytes) from the [world, batch, local, row] shards, the unshard of
+ * tests/test_zigzag_shard.py:39-43; padding rows are dropped. */
+int32_t rmx_zigzag_scatter(const void* src, void* dst, int32_t batch, int32_t seq,
+                           int32_t world, int64_t row_bytes, int64_t dst_bstride,
+                           void* stream);
+
+/*
+ * Context-parallel linear scan h_t = a_t h_{t-1} + b_t emulated over `world`
+ * contiguous shards of length L/world (strategies/state_passing.py:19-59): each
+ * shard scans from zero, the shards' (decay, carry) pairs are prefix-combined
+ * in rank order and the correction h += cumA * H_in is applied.
+ * a: fp32 [batch, L, groups] with `groups` dividing d (a[b,t,g] applies to the
+ * d/groups consecutive channels of group g; groups == d is elementwise);
+ * b, h: fp32 [batch, L, d] contiguous. chunk_state (nullable): fp32
+ * [world, batch, 2, d] receives each shard's (A_r broadcast, B_r).
+ */
+int32_t rmx_linear_scan_fwd(const float* a, const float* b, float* h, float* chunk_state,
+                            int32_t batch, int32_t L, int32_t d, int32_t groups,
+                            int32_t world, void* stream);
+
+/*
+ * Gradient of rmx_linear_scan_fwd: given dh and the forward h, writes
+ * db [batch, L, d] and ADDS da [batch, L, groups] (caller zero-fills da).
+ */
+int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* dh, float* da,
+                            float* db, int32_t batch, int32_t L, int32_t d, int32_t groups,
+                            int32_t world, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RINGMASTER_AMD_H */

@@ -1,0 +1,293 @@
+"""CPU restatement of the reference ring-attention math (test infrastructure only).
+
+Follows ring/kernels.py:52-78 (math_block), ring/merge.py:13-31 (merge),
+ring/zigzag.py:40-67,86-120,151-254 (zigzag schedule, forward and reverse-ring
+backward), ring/p2p_attn.py:243-281 (explicit global-lse block backward) and
+ring/varlen_blocks.py:45-80,176-200 (document masks). The P ranks of the ring are
+emulated in one process: a ring hop is an index into per-rank lists, the dK/dV
+accumulators travel with their KV block exactly as the reference's
+``_shift_sync`` moves them.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+NEG_INF = float("-inf")
+
+
+# ---------------------------------------------------------------- blocks
+def math_block(q, k, v, *, causal, scaling, dropout=0.0, window=None):
+    """Explicit-softmax block (ring/kernels.py:52-78). q/k/v [b, s, h, d] -> (out, lse)."""
+    qt, kt, vt = (t.transpose(1, 2).float() for t in (q, k, v))
+    if qt.shape[1] != kt.shape[1]:
+        if qt.shape[1] % kt.shape[1]:
+            raise ValueError("Query heads must be divisible by KV heads")
+        rep = qt.shape[1] // kt.shape[1]
+        kt, vt = (t.repeat_interleave(rep, dim=1) for t in (kt, vt))
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(qt.shape[-1])
+    scores = (qt @ kt.transpose(-1, -2)) * scale
+    sq, sk = scores.shape[-2], scores.shape[-1]
+    if causal:
+        keep = torch.ones(sq, sk, dtype=torch.bool).tril(sk - sq)
+        scores = scores.masked_fill(~keep, NEG_INF)
+    if window is not None:
+        left = window[0]
+        iq = torch.arange(sq).unsqueeze(1) + (sk - sq)
+        ik = torch.arange(sk).unsqueeze(0)
+        scores = scores.masked_fill(iq - ik > left, NEG_INF)
+    lse = torch.logsumexp(scores, dim=-1)
+    probs = torch.exp(scores - lse.unsqueeze(-1))
+    if dropout:
+        probs = torch.nn.functional.dropout(probs, p=dropout)
+    out = probs @ vt
+    return out.transpose(1, 2).to(q.dtype), lse
+
+
+def _repeat_kv(t, n_heads):
+    """[b, s, Hkv, d] -> [b, s, Hq, d] (ring/varlen_blocks.py:61-66)."""
+    if t.shape[2] == n_heads:
+        return t
+    return t.repeat_interleave(n_heads // t.shape[2], dim=2)
+
+
+def doc_ids_from_cu(cu_seqlens):
+    """Per-token document id (ring/varlen_blocks.py:45-48)."""
+    seg = cu_seqlens.to(torch.int64).diff()
+    return torch.repeat_interleave(torch.arange(seg.numel()), seg)
+
+
+def additive_doc_mask(q_gidx, k_gidx, doc_ids, causal: bool):
+    """0 where same document (and k <= q if causal), else -inf (ring/varlen_blocks.py:51-58)."""
+    allow = doc_ids[q_gidx].unsqueeze(1) == doc_ids[k_gidx].unsqueeze(0)
+    if causal:
+        allow = allow & (k_gidx.unsqueeze(0) <= q_gidx.unsqueeze(1))
+    return torch.where(allow, torch.zeros(()), torch.full((), NEG_INF))
+
+
+def masked_block_fwd(q, k, v, add_mask, scale):
+    """(out, lse) with an additive mask; lse -inf for rows with no key (ring/varlen_blocks.py:69-80)."""
+    qf = q.transpose(1, 2).float()
+    kf = _repeat_kv(k, q.shape[2]).transpose(1, 2).float()
+    vf = _repeat_kv(v, q.shape[2]).transpose(1, 2).float()
+    scores = (qf @ kf.transpose(-1, -2)) * scale + add_mask
+    lse = torch.logsumexp(scores, dim=-1)
+    safe = torch.where(torch.isinf(lse), torch.zeros_like(lse), lse)
+    p = torch.exp(scores - safe.unsqueeze(-1))
+    out = p @ vf
+    return out.transpose(1, 2).to(q.dtype), lse
+
+
+def masked_block_bwd(d_out, q, k, v, out, lse, add_mask, scale):
+    """dq, dk, dv of one block from the GLOBAL out/lse, GQA folded
+    (ring/varlen_blocks.py:176-200, identity of ring/p2p_attn.py:243-281)."""
+    nq = q.shape[2]
+    qf = q.transpose(1, 2).float()
+    kf = _repeat_kv(k, nq).transpose(1, 2).float()
+    vf = _repeat_kv(v, nq).transpose(1, 2).float()
+    dof = d_out.transpose(1, 2).float()
+    of = out.transpose(1, 2).float()
+    scores = (qf @ kf.transpose(-1, -2)) * scale + add_mask
+    p = torch.exp(scores - lse.unsqueeze(-1))
+    delta = (dof * of).sum(-1, keepdim=True)
+    dv = p.transpose(-1, -2) @ dof
+    dp = dof @ vf.transpose(-1, -2)
+    ds = p * (dp - delta)
+    dq = (ds @ kf) * scale
+    dk = (ds.transpose(-1, -2) @ qf) * scale
+    hkv = k.shape[2]
+    if hkv != nq:
+        dk = dk.unflatten(1, (hkv, nq // hkv)).sum(2)
+        dv = dv.unflatten(1, (hkv, nq // hkv)).sum(2)
+    return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2)
+
+
+def causal_mask(sq, sk):
+    """Additive bottom-right causal mask (ring/kernels.py:64-67)."""
+    keep = torch.ones(sq, sk, dtype=torch.bool).tril(sk - sq)
+    return torch.where(keep, torch.zeros(()), torch.full((), NEG_INF))
+
+
+# ---------------------------------------------------------------- merge
+def lse_to_bshd(block_lse, like):
+    """[b, h, s] -> [b, s, h, 1] fp32 (ring/merge.py:13-17)."""
+    if block_lse.dim() == 3 and block_lse.shape[1] == like.shape[2]:
+        block_lse = block_lse.transpose(1, 2)
+    return block_lse.unsqueeze(-1).contiguous().to(torch.float32)
+
+
+def update_out_and_lse(out, lse, block_out, block_lse):
+    """Online-softmax merge (ring/merge.py:20-31)."""
+    block_lse = lse_to_bshd(block_lse, block_out)
+    block_out = block_out.to(torch.float32)
+    if out is None:
+        return block_out, block_lse
+    new_lse = torch.logaddexp(lse, block_lse)
+    out = torch.exp(lse - new_lse) * out + torch.exp(block_lse - new_lse) * block_out
+    return out, new_lse
+
+
+def merge_slice(out, lse, block_out, block_lse, sl):
+    """In-place merge of a partial block into rows ``sl`` (ring/zigzag.py:59-67)."""
+    blk_lse = lse_to_bshd(block_lse, block_out)
+    blk_out = block_out.to(torch.float32)
+    o, lo = out[:, sl], lse[:, sl]
+    new = torch.logaddexp(lo, blk_lse)
+    out[:, sl] = torch.exp(lo - new) * o + torch.exp(blk_lse - new) * blk_out
+    lse[:, sl] = new
+    return out, lse
+
+
+# ---------------------------------------------------------------- zigzag ring
+def zigzag_gidx(rank, half, world):
+    """Global token indices of rank's two chunks, early then late (ring/zigzag.py:40-46)."""
+    return torch.cat([torch.arange(rank * half, (rank + 1) * half),
+                      torch.arange((2 * world - 1 - rank) * half, (2 * world - rank) * half)])
+
+
+def _block_fwd(qd, k, v, scale, mask):
+    return masked_block_fwd(qd, k, v, mask, scale)
+
+
+def zigzag_ring_forward(qs, ks, vs, scaling=None, cu_seqlens=None, ranks=None):
+    """Emulated zigzag ring forward (ring/zigzag.py:70-149).
+
+    qs/ks/vs: per-rank lists of interface tensors [b, H, L, d]. Returns per-rank
+    out [b, L, H, d] (in q.dtype) and lse [b, H, L] fp32. Dense inputs use the
+    three step cases (causal local block, early KV half, late Q half); packed
+    inputs use global-index document masks for every block (:86-120). ``ranks``
+    restricts the computation to those ranks' queries (others are None)."""
+    world = len(qs)
+    d = qs[0].shape[-1]
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(d)
+    qd = [q.transpose(1, 2).float() for q in qs]
+    kd = [k.transpose(1, 2).float() for k in ks]
+    vd = [v.transpose(1, 2).float() for v in vs]
+    L = qd[0].shape[1]
+    half = L // 2
+    doc = doc_ids_from_cu(cu_seqlens) if cu_seqlens is not None else None
+    outs, lses = [None] * world, [None] * world
+    for rank in (range(world) if ranks is None else ranks):
+        g = zigzag_gidx(rank, half, world)
+        out = lse = None
+        for s in range(world):
+            rem = (rank - s) % world
+            ck, cv = kd[rem], vd[rem]
+            if s == 0:
+                m = (additive_doc_mask(g, g, doc, True) if doc is not None
+                     else causal_mask(L, L))
+                bo, bl = _block_fwd(qd[rank], ck, cv, scale, m)
+                out, lse = update_out_and_lse(out, lse, bo, bl)
+            elif s <= rank:
+                kg = torch.arange(rem * half, (rem + 1) * half)
+                m = additive_doc_mask(g, kg, doc, True) if doc is not None else 0.0
+                bo, bl = _block_fwd(qd[rank], ck[:, :half], cv[:, :half], scale, m)
+                out, lse = update_out_and_lse(out, lse, bo, bl)
+            else:
+                m = (additive_doc_mask(g[half:], zigzag_gidx(rem, half, world), doc, True)
+                     if doc is not None else 0.0)
+                bo, bl = _block_fwd(qd[rank][:, half:], ck, cv, scale, m)
+                out, lse = merge_slice(out, lse, bo, bl, slice(half, None))
+        outs[rank] = out.to(qs[0].dtype)
+        lses[rank] = lse.squeeze(-1).transpose(1, 2).contiguous()
+    return outs, lses
+
+
+def zigzag_ring_backward(d_outs, qs, ks, vs, outs, lses, scaling=None, cu_seqlens=None,
+                         ranks=None):
+    """Emulated reverse-ring backward with the global out/lse (ring/zigzag.py:151-254).
+
+    d_outs/outs: per-rank [b, L, H, d]; lses [b, H, L]. The dK/dV accumulator that
+    leaves rank r after each step is the one rank r+1 continues (the
+    ``_shift_sync`` hop, ring/zigzag.py:199-200), so block ``rem`` gathers its
+    gradient from every rank that visits it. Returns per-rank (dq, dk, dv) in the
+    interface layout [b, H, L, d], fp32. ``ranks`` restricts the work to those
+    ranks' queries (their dq, and only their share of every dK/dV)."""
+    world = len(qs)
+    d = qs[0].shape[-1]
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(d)
+    qd = [q.transpose(1, 2).float() for q in qs]
+    kd = [k.transpose(1, 2).float() for k in ks]
+    vd = [v.transpose(1, 2).float() for v in vs]
+    L = qd[0].shape[1]
+    half = L // 2
+    doc = doc_ids_from_cu(cu_seqlens) if cu_seqlens is not None else None
+    dq = [torch.zeros_like(q) for q in qd]
+    # cur_dk[r]: the accumulator rank r holds at the current step (travels with KV)
+    cur_dk = [torch.zeros_like(k) for k in kd]
+    cur_dv = [torch.zeros_like(v) for v in vd]
+    active = range(world) if ranks is None else ranks
+    for s in range(world):
+        for rank in active:
+            rem = (rank - s) % world
+            g = zigzag_gidx(rank, half, world)
+            dod, out, lse = d_outs[rank].float(), outs[rank].float(), lses[rank]
+            ck, cv = kd[rem], vd[rem]
+            if s == 0:
+                m = additive_doc_mask(g, g, doc, True) if doc is not None else causal_mask(L, L)
+                dqb, dkb, dvb = masked_block_bwd(dod, qd[rank], ck, cv, out, lse, m, scale)
+                dq[rank] += dqb
+                cur_dk[rank] += dkb
+                cur_dv[rank] += dvb
+            elif s <= rank:
+                kg = torch.arange(rem * half, (rem + 1) * half)
+                m = additive_doc_mask(g, kg, doc, True) if doc is not None else 0.0
+                dqb, dk0, dv0 = masked_block_bwd(dod, qd[rank], ck[:, :half], cv[:, :half],
+                                                 out, lse, m, scale)
+                dq[rank] += dqb
+                cur_dk[rank][:, :half] += dk0
+                cur_dv[rank][:, :half] += dv0
+            else:
+                m = (additive_doc_mask(g[half:], zigzag_gidx(rem, half, world), doc, True)
+                     if doc is not None else 0.0)
+                dq1, dkb, dvb = masked_block_bwd(dod[:, half:], qd[rank][:, half:], ck, cv,
+                                                 out[:, half:], lse[:, :, half:], m, scale)
+                dq[rank][:, half:] += dq1
+                cur_dk[rank] += dkb
+                cur_dv[rank] += dvb
+        # _shift_sync: rank r+1 receives what rank r held
+        cur_dk = [cur_dk[(r - 1) % world] for r in range(world)]
+        cur_dv = [cur_dv[(r - 1) % world] for r in range(world)]
+    # after P hops every accumulator is back at its owner
+    return ([t.transpose(1, 2) for t in dq], [t.transpose(1, 2) for t in cur_dk],
+            [t.transpose(1, 2) for t in cur_dv])
+
+
+def full_attention(q, k, v, *, causal=True, scaling=None, cu_seqlens=None):
+    """Brute-force attention over the whole sequence in the caller's dtype (use
+    fp64 to pin). q/k/v [b, S, H, d] -> out [b, S, H, d], lse [b, H, S]."""
+    S = q.shape[1]
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
+    g = torch.arange(S)
+    if cu_seqlens is not None:
+        m = additive_doc_mask(g, g, doc_ids_from_cu(cu_seqlens), causal).to(q.dtype)
+    elif causal:
+        m = causal_mask(S, S).to(q.dtype)
+    else:
+        m = torch.zeros(S, S, dtype=q.dtype)
+    qf, kf, vf = q.transpose(1, 2), _repeat_kv(k, q.shape[2]).transpose(1, 2), \
+        _repeat_kv(v, q.shape[2]).transpose(1, 2)
+    scores = (qf @ kf.transpose(-1, -2)) * scale + m
+    lse = torch.logsumexp(scores, dim=-1)
+    out = torch.softmax(scores, dim=-1) @ vf
+    return out.transpose(1, 2), lse
+
+
+def attention_rows(q_rows, k, v, q_pos, *, scaling=None, causal=True):
+    """Exact attention for selected query rows against the full K/V (fp64-capable spot
+    check at sizes where full attention is too large). q_rows [b, n, H, d], q_pos [n]
+    global positions, k/v [b, S, Hkv, d]. Returns out [b, n, H, d], lse [b, H, n]."""
+    S = k.shape[1]
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(q_rows.shape[-1])
+    kf = _repeat_kv(k, q_rows.shape[2]).transpose(1, 2)
+    vf = _repeat_kv(v, q_rows.shape[2]).transpose(1, 2)
+    qf = q_rows.transpose(1, 2)
+    scores = (qf @ kf.transpose(-1, -2)) * scale
+    if causal:
+        allow = torch.arange(S).unsqueeze(0) <= q_pos.unsqueeze(1)
+        scores = scores.masked_fill(~allow, NEG_INF)
+    lse = torch.logsumexp(scores, dim=-1)
+    out = torch.softmax(scores, dim=-1) @ vf
+    return out.transpose(1, 2), lse

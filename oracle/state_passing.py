@@ -1,0 +1,102 @@
+"""CPU restatement of the recurrent state passing (test infrastructure only).
+
+Follows strategies/state_passing.py:19-59 (local scan, ``cp_linear_scan`` with the
+all-gather of (A_r, B_r) emulated as a list over ranks), the Mamba2 SSD reference
+of tests/test_mamba_cp.py:16-32, and ``cp_state_prefix`` / ``mamba2_cp_correction``
+(strategies/mamba.py:68-139). Autograd-capable (torch ops only).
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def local_linear_scan(a, b):
+    """h_t = a_t h_{t-1} + b_t from zero (strategies/state_passing.py:19-26). a, b: [batch, L, d]."""
+    h = torch.zeros_like(b[:, 0])
+    out = []
+    for t in range(a.shape[1]):
+        h = a[:, t] * h + b[:, t]
+        out.append(h)
+    return torch.stack(out, dim=1)
+
+
+def local_linear_scan_vec(a, b):
+    """Same recurrence, vectorised over d with a Python loop over t (for larger L*d)."""
+    h = torch.zeros_like(b[:, 0])
+    out = torch.empty_like(b)
+    for t in range(a.shape[1]):
+        h = a[:, t] * h + b[:, t]
+        out[:, t] = h
+    return out
+
+
+def cp_linear_scan_emulated(a, b, world, scan=local_linear_scan):
+    """cp_linear_scan for every rank of a ``world``-rank group, in one process
+    (strategies/state_passing.py:29-59). a, b: full [batch, L, d]; returns full h."""
+    L = a.shape[1]
+    if L % world:
+        raise ValueError("L not divisible by world")
+    n = L // world
+    locs, cums, pairs = [], [], []
+    for r in range(world):
+        sa, sb = a[:, r * n:(r + 1) * n], b[:, r * n:(r + 1) * n]
+        local_h = scan(sa, sb)
+        cum_a = torch.cumprod(sa, dim=1)
+        locs.append(local_h)
+        cums.append(cum_a)
+        pairs.append((cum_a[:, -1], local_h[:, -1]))  # all-gathered (A_r, B_r)
+    outs = []
+    for r in range(world):
+        h_in = torch.zeros_like(pairs[r][1])
+        for j in range(r):
+            h_in = pairs[j][0] * h_in + pairs[j][1]
+        outs.append(locs[r] + cums[r] * h_in.unsqueeze(1))
+    return torch.cat(outs, dim=1)
+
+
+def ssd_reference(x, dt, A, B, C):
+    """Mamba2 SSD: h_t = exp(A dt_t) h_{t-1} + (dt_t B_t) (x) x_t; y_t = C_t . h_t
+    (tests/test_mamba_cp.py:16-32). x [b,T,H,d], dt [b,T,H], A [H], B/C [b,T,G,n]."""
+    bsz, T, H, d = x.shape
+    G, n = B.shape[2], B.shape[3]
+    hpg = H // G
+    Bx = B.repeat_interleave(hpg, dim=2)
+    Cx = C.repeat_interleave(hpg, dim=2)
+    h = torch.zeros(bsz, H, d, n, dtype=x.dtype)
+    outs = []
+    for t in range(T):
+        dA = torch.exp(A * dt[:, t])
+        inp = dt[:, t][:, :, None, None] * x[:, t][:, :, :, None] * Bx[:, t][:, :, None, :]
+        h = dA[:, :, None, None] * h + inp
+        y = (Cx[:, t][:, :, None, :] * h).sum(-1)
+        outs.append(y.reshape(bsz, H * d))
+    return torch.stack(outs, 1), h
+
+
+def cp_state_prefix_emulated(finals, decays):
+    """H_in for every rank from per-rank (B_r = final state, A_r = chunk decay [b, H])
+    (strategies/mamba.py:68-98): H_in_r = sum_{j<r} (prod_{j<k<r} A_k) B_j."""
+    world = len(finals)
+    prefixes = []
+    for r in range(world):
+        h_prev = torch.zeros_like(finals[r])
+        for j in range(r):
+            h_prev = decays[j][..., None, None] * h_prev + finals[j]
+        prefixes.append(h_prev)
+    return prefixes
+
+
+def mamba2_cp_correction(out, h_final, C, cum_A, h_prev, num_heads, head_dim):
+    """y_t += C_t . (exp(cumA_t) H_in); state += exp(cumA_last) H_in (strategies/mamba.py:101-139)."""
+    if not h_prev.any():
+        return out, h_final
+    B, T, _ = out.shape
+    hpg = num_heads // C.shape[2]
+    decay = torch.exp(cum_A).float()
+    prop = decay[:, :, :, None, None] * h_prev[:, None].float()
+    Cx = C.float().repeat_interleave(hpg, dim=2)
+    dy = torch.einsum("bthn,bthdn->bthd", Cx, prop).reshape(B, T, num_heads * head_dim)
+    corrected = out + dy.to(out.dtype)
+    h = h_final + (decay[:, -1, :, None, None] * h_prev.float()).to(h_final.dtype)
+    return corrected, h

@@ -1,0 +1,275 @@
+// extern "C" entry points of libringmaster_amd.so (declared in
+// include/ringmaster_amd.h). Every argument is validated here, on the host,
+// before anything is launched; errors are reported as negative codes with a
+// per-thread message and nothing ever throws across the ABI.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "rmx_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int dev_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return RMX_OK;
+  return fail(RMX_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_layout(const rmx_attn_layout* L) {
+  if (!L) return fail(RMX_EINVAL, "layout is NULL");
+  if (L->batch < 0 || L->hq <= 0 || L->hkv <= 0)
+    return fail(RMX_EINVAL, "batch/heads must be positive (batch=%d hq=%d hkv=%d)", L->batch, L->hq,
+                L->hkv);
+  if (L->hq % L->hkv)
+    return fail(RMX_EINVAL, "Query heads must be divisible by KV heads (hq=%d hkv=%d)", L->hq,
+                L->hkv);
+  if (L->head_dim != 64 && L->head_dim != 128)
+    return fail(RMX_EUNSUPPORTED, "head_dim %d is not supported (64 or 128)", L->head_dim);
+  if (!(L->scale > 0.f) || !std::isfinite(L->scale))
+    return fail(RMX_EINVAL, "softmax scale must be finite and positive (got %g)", (double)L->scale);
+  if (L->mask < RMX_MASK_FULL || L->mask > RMX_MASK_DOC)
+    return fail(RMX_EINVAL, "unknown mask kind %d", L->mask);
+  const int64_t bf[] = {L->q_sb, L->q_ss, L->q_sh, L->k_sb, L->k_ss, L->k_sh,
+                        L->v_sb, L->v_ss, L->v_sh, L->o_sb, L->o_ss, L->o_sh,
+                        L->dk_sb, L->dk_ss, L->dk_sh};
+  for (int64_t s : bf)
+    if (s < 0 || s % 8)
+      return fail(RMX_EINVAL, "bf16 element strides must be non-negative multiples of 8 (got %lld)",
+                  (long long)s);
+  const int64_t f4[] = {L->a_sb, L->a_ss, L->a_sh, L->ka_sb, L->ka_ss, L->ka_sh};
+  for (int64_t s : f4)
+    if (s < 0 || s % 4)
+      return fail(RMX_EINVAL, "fp32 element strides must be non-negative multiples of 4 (got %lld)",
+                  (long long)s);
+  if (L->l_sb < 0 || L->l_sh < 0) return fail(RMX_EINVAL, "lse strides must be non-negative");
+  return RMX_OK;
+}
+
+int check_bf16(const void* p, const char* name) {
+  if (!p) return fail(RMX_EINVAL, "%s is NULL", name);
+  if (!aligned(p, 16)) return fail(RMX_EINVAL, "%s must be 16-byte aligned", name);
+  return RMX_OK;
+}
+
+int check_doc(const rmx_attn_layout* L, const int32_t* qg, const int32_t* kg, const int32_t* doc) {
+  if (L->mask != RMX_MASK_DOC) return RMX_OK;
+  if (!qg || !kg || !doc) return fail(RMX_EINVAL, "RMX_MASK_DOC needs q_gidx, k_gidx and doc");
+  return RMX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t rmx_abi_version(void) { return RMX_ABI_VERSION; }
+
+const char* rmx_last_error(void) { return g_err.c_str(); }
+
+int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* problems,
+                     int32_t nproblems, void* stream) {
+  int rc = check_layout(layout);
+  if (rc) return rc;
+  if (nproblems < 0 || (nproblems > 0 && !problems))
+    return fail(RMX_EINVAL, "bad problem list (n=%d)", nproblems);
+  for (int i = 0; i < nproblems; ++i) {
+    const rmx_fwd_problem& p = problems[i];
+    if (p.sq < 0 || p.sk < 0) return fail(RMX_EINVAL, "problem %d: negative length", i);
+    if (p.sq == 0) continue;
+    if ((rc = check_bf16(p.q, "q"))) return rc;
+    if (p.sk > 0) {
+      if ((rc = check_bf16(p.k, "k"))) return rc;
+      if ((rc = check_bf16(p.v, "v"))) return rc;
+    }
+    if ((rc = check_doc(layout, p.q_gidx, p.k_gidx, p.doc))) return rc;
+    switch (p.mode) {
+      case RMX_FWD_WRITE:
+      case RMX_FWD_ACC_FINAL:
+        if ((rc = check_bf16(p.out, "out"))) return rc;
+        if (p.mode == RMX_FWD_ACC_FINAL && (!p.acc_out || !p.acc_lse))
+          return fail(RMX_EINVAL, "problem %d: ACC_FINAL needs acc_out and acc_lse", i);
+        break;
+      case RMX_FWD_ACC_INIT:
+      case RMX_FWD_ACC_MERGE:
+        if (!p.acc_out || !p.acc_lse)
+          return fail(RMX_EINVAL, "problem %d: accumulating modes need acc_out and acc_lse", i);
+        break;
+      default:
+        return fail(RMX_EINVAL, "problem %d: unknown forward mode %d", i, p.mode);
+    }
+    if (p.acc_out && !aligned(p.acc_out, 16))
+      return fail(RMX_EINVAL, "acc_out must be 16-byte aligned");
+  }
+  for (int i = 0; i < nproblems; i += RMX_MAX_BATCHED) {
+    const int n = nproblems - i < RMX_MAX_BATCHED ? nproblems - i : RMX_MAX_BATCHED;
+    rc = dev_status(rmx::launch_attn_fwd(*layout, problems + i, n, (hipStream_t)stream),
+                    "rmx_attn_fwd launch");
+    if (rc) return rc;
+  }
+  return RMX_OK;
+}
+
+int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const uint16_t* out,
+                           const uint16_t* dout, float* delta, int32_t sq, void* stream) {
+  int rc = check_layout(layout);
+  if (rc) return rc;
+  if (sq < 0) return fail(RMX_EINVAL, "negative sequence length");
+  if (sq == 0 || layout->batch == 0) return RMX_OK;
+  if ((rc = check_bf16(out, "out"))) return rc;
+  if ((rc = check_bf16(dout, "dout"))) return rc;
+  if (!delta) return fail(RMX_EINVAL, "delta is NULL");
+  return dev_status(rmx::launch_attn_bwd_delta(*layout, out, dout, delta, sq, (hipStream_t)stream),
+                    "rmx_attn_bwd_delta launch");
+}
+
+int32_t rmx_attn_bwd(const rmx_attn_layout* layout, const rmx_bwd_problem* problems,
+                     int32_t nproblems, void* stream) {
+  int rc = check_layout(layout);
+  if (rc) return rc;
+  if (nproblems < 0 || (nproblems > 0 && !problems))
+    return fail(RMX_EINVAL, "bad problem list (n=%d)", nproblems);
+  for (int i = 0; i < nproblems; ++i) {
+    const rmx_bwd_problem& p = problems[i];
+    if (p.sq < 0 || p.sk < 0) return fail(RMX_EINVAL, "problem %d: negative length", i);
+    if (p.sq == 0 || p.sk == 0) continue;
+    if ((rc = check_bf16(p.q, "q"))) return rc;
+    if ((rc = check_bf16(p.k, "k"))) return rc;
+    if ((rc = check_bf16(p.v, "v"))) return rc;
+    if ((rc = check_bf16(p.dout, "dout"))) return rc;
+    if (!p.lse || !p.delta) return fail(RMX_EINVAL, "problem %d: lse and delta are required", i);
+    if ((rc = check_doc(layout, p.q_gidx, p.k_gidx, p.doc))) return rc;
+    const int modes[2] = {p.dq_mode, p.dkv_mode};
+    for (int m = 0; m < 2; ++m) {
+      const int mode = modes[m];
+      if (mode < RMX_GRAD_WRITE_BF16 || mode > RMX_GRAD_NONE)
+        return fail(RMX_EINVAL, "problem %d: unknown gradient mode %d", i, mode);
+      if (mode == RMX_GRAD_NONE) continue;
+      const bool need_acc = mode != RMX_GRAD_WRITE_BF16;
+      const bool need_bf = mode == RMX_GRAD_WRITE_BF16 || mode == RMX_GRAD_ACC_FINAL;
+      if (m == 0) {
+        if (need_acc && (!p.dq_acc || !aligned(p.dq_acc, 16)))
+          return fail(RMX_EINVAL, "problem %d: dq_acc missing or misaligned", i);
+        if (need_bf && (rc = check_bf16(p.dq, "dq"))) return rc;
+      } else {
+        if (need_acc && (!p.dk_acc || !p.dv_acc))
+          return fail(RMX_EINVAL, "problem %d: dk_acc/dv_acc missing", i);
+        if (need_bf && (!p.dk || !p.dv)) return fail(RMX_EINVAL, "problem %d: dk/dv missing", i);
+      }
+    }
+  }
+  for (int i = 0; i < nproblems; i += RMX_MAX_BATCHED) {
+    const int n = nproblems - i < RMX_MAX_BATCHED ? nproblems - i : RMX_MAX_BATCHED;
+    rc = dev_status(rmx::launch_attn_bwd(*layout, problems + i, n, (hipStream_t)stream),
+                    "rmx_attn_bwd launch");
+    if (rc) return rc;
+  }
+  return RMX_OK;
+}
+
+int32_t rmx_lse_merge(float* out, float* lse, const void* blk_out, int32_t blk_is_f32,
+                      const float* blk_lse, int32_t batch, int32_t seq, int32_t heads,
+                      int32_t head_dim, const int64_t* o_strides, const int64_t* l_strides,
+                      const int64_t* bo_strides, const int64_t* bl_strides, int32_t init,
+                      void* stream) {
+  if (batch < 0 || seq < 0 || heads < 0) return fail(RMX_EINVAL, "negative shape");
+  if (head_dim <= 0 || head_dim % 8)
+    return fail(RMX_EUNSUPPORTED, "head_dim must be a positive multiple of 8 (got %d)", head_dim);
+  if ((int64_t)batch * seq * heads == 0) return RMX_OK;
+  if (!out || !lse || !blk_out || !blk_lse) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!o_strides || !l_strides || !bo_strides || !bl_strides)
+    return fail(RMX_EINVAL, "NULL stride array");
+  if (!aligned(out, 16) || !aligned(blk_out, 16))
+    return fail(RMX_EINVAL, "out and blk_out must be 16-byte aligned");
+  for (int i = 0; i < 3; ++i) {
+    if (o_strides[i] % 4) return fail(RMX_EINVAL, "out strides must be multiples of 4");
+    if (bo_strides[i] % (blk_is_f32 ? 4 : 8))
+      return fail(RMX_EINVAL, "blk_out strides must keep 16-byte alignment");
+  }
+  return dev_status(rmx::launch_lse_merge(out, lse, blk_out, blk_is_f32, blk_lse, batch, seq, heads,
+                                          head_dim, o_strides, l_strides, bo_strides, bl_strides,
+                                          init, (hipStream_t)stream),
+                    "rmx_lse_merge launch");
+}
+
+int32_t rmx_zigzag_gather(const void* src, void* dst, int32_t batch, int32_t seq, int32_t world,
+                          int32_t rank, int64_t row_bytes, int64_t src_bstride,
+                          const void* pad_row, void* stream) {
+  if (world <= 0) return fail(RMX_EINVAL, "world must be positive (got %d)", world);
+  if (rank >= world) return fail(RMX_EINVAL, "rank %d out of range for world %d", rank, world);
+  if (batch < 0 || seq < 0 || row_bytes < 0) return fail(RMX_EINVAL, "negative shape");
+  if ((int64_t)batch * seq == 0 || row_bytes == 0) return RMX_OK;
+  if (!src || !dst) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (src_bstride < (int64_t)seq * row_bytes && batch > 1)
+    return fail(RMX_EINVAL, "batch stride smaller than one sequence");
+  return dev_status(rmx::launch_zigzag(src, dst, batch, seq, world, rank, row_bytes, src_bstride,
+                                       pad_row, 0, (hipStream_t)stream),
+                    "rmx_zigzag_gather launch");
+}
+
+int32_t rmx_zigzag_scatter(const void* src, void* dst, int32_t batch, int32_t seq, int32_t world,
+                           int64_t row_bytes, int64_t dst_bstride, void* stream) {
+  if (world <= 0) return fail(RMX_EINVAL, "world must be positive (got %d)", world);
+  if (batch < 0 || seq < 0 || row_bytes < 0) return fail(RMX_EINVAL, "negative shape");
+  if ((int64_t)batch * seq == 0 || row_bytes == 0) return RMX_OK;
+  if (!src || !dst) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (dst_bstride < (int64_t)seq * row_bytes && batch > 1)
+    return fail(RMX_EINVAL, "batch stride smaller than one sequence");
+  return dev_status(rmx::launch_zigzag(src, dst, batch, seq, world, -1, row_bytes, dst_bstride,
+                                       nullptr, 1, (hipStream_t)stream),
+                    "rmx_zigzag_scatter launch");
+}
+
+static int check_scan(int batch, int L, int d, int groups, int world) {
+  if (batch < 0 || L < 0 || d < 0) return fail(RMX_EINVAL, "negative shape");
+  if (world <= 0) return fail(RMX_EINVAL, "world must be positive (got %d)", world);
+  if (L % world) return fail(RMX_EINVAL, "sequence length %d not divisible by world %d", L, world);
+  if (groups <= 0 || (d > 0 && d % groups))
+    return fail(RMX_EINVAL, "groups (%d) must divide d (%d)", groups, d);
+  return RMX_OK;
+}
+
+int32_t rmx_linear_scan_fwd(const float* a, const float* b, float* h, float* chunk_state,
+                            int32_t batch, int32_t L, int32_t d, int32_t groups, int32_t world,
+                            void* stream) {
+  int rc = check_scan(batch, L, d, groups, world);
+  if (rc) return rc;
+  if ((int64_t)batch * L * d == 0) return RMX_OK;
+  if (!a || !b || !h) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!aligned(a, 16) || !aligned(b, 16) || !aligned(h, 16))
+    return fail(RMX_EINVAL, "a, b and h must be 16-byte aligned");
+  return dev_status(
+      rmx::launch_linear_scan_fwd(a, b, h, chunk_state, batch, L, d, groups, world,
+                                  (hipStream_t)stream),
+      "rmx_linear_scan_fwd launch");
+}
+
+int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* dh, float* da, float* db,
+                            int32_t batch, int32_t L, int32_t d, int32_t groups, int32_t world,
+                            void* stream) {
+  int rc = check_scan(batch, L, d, groups, world);
+  if (rc) return rc;
+  if ((int64_t)batch * L * d == 0) return RMX_OK;
+  if (!a || !h || !dh || !da || !db) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!aligned(a, 16) || !aligned(h, 16) || !aligned(dh, 16) || !aligned(da, 16) ||
+      !aligned(db, 16))
+    return fail(RMX_EINVAL, "scan tensors must be 16-byte aligned");
+  return dev_status(rmx::launch_linear_scan_bwd(a, h, dh, da, db, batch, L, d, groups, world,
+                                                (hipStream_t)stream),
+                    "rmx_linear_scan_bwd launch");
+}
+
+}  // extern "C"

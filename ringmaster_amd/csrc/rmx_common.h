@@ -1,0 +1,109 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of ringmaster_amd.
+//
+// MFMA conventions used throughout (v_mfma_f32_32x32x16_bf16, one wave of 64
+// lanes, lane = 32*hl + l32):
+//   A operand (32 rows x 16 k): lane holds row l32, 8 k-values;
+//   B operand (16 k x 32 cols): lane holds col l32, 8 k-values;
+//   C/D (32 x 32 fp32, 16 regs): lane holds col l32, reg r holds row
+//       8*(r/4) + 4*hl + (r%4).
+// The k-order inside an operand only has to agree between A and B, so every
+// kernel feeds element i of lane-half hl with k = 8*hl + i.
+//
+// A C/D tile whose rows were produced from A-rows permuted by sigma (swap of
+// index bits 2 and 3) holds, in lane (hl, l32), reg r, the logical row
+//   16*(r/8) + 8*hl + (r%8),
+// i.e. regs 0..7 and 8..15 are two runs of 8 consecutive rows. That is exactly
+// the k-layout of the next MFMA's operand, so softmax probabilities and dS
+// feed the second GEMM straight from registers with no LDS round trip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rmx {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// sigma: swap bits 2 and 3 of a row index (an involution on 0..31).
+__device__ __forceinline__ int sigma(int m) {
+  return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1);
+}
+
+// Logical row/col held by register r of lane-half hl in a sigma-permuted C tile.
+__device__ __forceinline__ int sig_row(int hl, int r) { return 16 * (r >> 3) + 8 * hl + (r & 7); }
+// Row held by register r of lane-half hl in a plain C tile.
+__device__ __forceinline__ int c_row(int hl, int r) { return 8 * (r >> 2) + 4 * hl + (r & 3); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// Pack 8 floats to a bf16x8 operand.
+__device__ __forceinline__ bf16x8 pack8(float v0, float v1, float v2, float v3, float v4, float v5,
+                                        float v6, float v7) {
+  u32x4 u;
+  u[0] = pack_bf2(v0, v1);
+  u[1] = pack_bf2(v2, v3);
+  u[2] = pack_bf2(v4, v5);
+  u[3] = pack_bf2(v6, v7);
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+__device__ __forceinline__ bf16x8 zero_bf16x8() {
+  u32x4 u = {0u, 0u, 0u, 0u};
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// LDS tiles of bf16 rows, 16-byte chunks XOR-swizzled by row so that the
+// 8-lane groups of a ds_read_b128 hit distinct bank quads.
+//  * "row" tiles ([rows][dim], read by sigma-permuted A operands):
+//    swizzle f(row) = (row & 3) | ((row >> 1) & 4)  (rows r and r^12 differ).
+//  * "t" tiles ([dim][keys], read by rows d = l32): swizzle g(row) = row & 7.
+__device__ __forceinline__ int swz_row(int row) { return (row & 3) | ((row >> 1) & 4); }
+__device__ __forceinline__ int swz_t(int row) { return row & 7; }
+
+// 16-byte global load/store helpers (bf16x8 / u32x4 bit patterns).
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Cross-half exchange: value held by lane l ^ 32.
+__device__ __forceinline__ float xhalf(float v) { return __shfl_xor(v, 32, 64); }
+
+// Map a linear workgroup index so that consecutive logical tiles land on the
+// same XCD (the dispatcher deals workgroups round-robin over the 8 XCDs).
+// Requires gridDim.x % 8 == 0.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  const int per = nblocks >> 3;
+  return (bid & 7) * per + (bid >> 3);
+}
+
+}  // namespace rmx

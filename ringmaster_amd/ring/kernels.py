@@ -1,0 +1,147 @@
+"""Block-attention provider ``mi355x_hip`` and the Dao-signature op pair.
+
+``mi355x_hip_block`` keeps the provider contract of the reference's ``PROVIDERS``
+(ring/kernels.py:28-85): ``fn(q, k, v, *, causal, scaling, dropout,
+attn_implementation, window) -> (out [b, sq, h, d] in q.dtype, lse [b, h, sq]
+fp32)``, q/k/v ``[b, s, h, d]``, GQA by ``kv_head = q_head // (hq/hkv)``, causal
+bottom-right aligned (ring/kernels.py:64-67). It is autograd-aware like
+``hf_kernels``/``math``; the lse output is not differentiable (as with flash).
+
+``flash_ops()`` returns ``(fwd, bwd)`` with the positional signatures of the Dao
+low-level ops that the ring schedules call (ring/p2p_attn.py:27-62,
+ring/zigzag.py:131,219): ``fwd`` allocates ``(out, lse)``; ``bwd`` writes into the
+caller's ``dq, dk, dv`` with the global out/lse.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from ringmaster_amd import abi
+from ringmaster_amd.ring import ops
+
+
+def _validate(q, k, v, dropout, window, softcap=0.0, alibi=None):
+    abi.require_device(q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q/k/v must be [batch, seq, heads, dim]")
+    if q.shape[2] % k.shape[2]:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise NotImplementedError(f"mi355x_hip blocks compute in bf16 (got {q.dtype})")
+    if q.shape[-1] not in (64, 128):
+        raise NotImplementedError(f"head_dim {q.shape[-1]} is not supported (64 or 128)")
+    if dropout:
+        raise NotImplementedError("mi355x_hip blocks do not implement attention dropout")
+    if window is not None and tuple(window) not in ((-1, -1),):
+        raise NotImplementedError("mi355x_hip blocks do not implement sliding windows")
+    if softcap:
+        raise NotImplementedError("mi355x_hip blocks do not implement softcap")
+    if alibi is not None:
+        raise NotImplementedError("mi355x_hip blocks do not implement ALiBi")
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """Keep views whose strides the kernels accept; copy anything else once."""
+    if (t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1])
+            and t.data_ptr() % 16 == 0):
+        return t
+    return t.contiguous()
+
+
+def block_forward(q, k, v, scale: float, causal: bool):
+    """(out bf16 [b, sq, hq, d], lse fp32 [b, hq, sq]) of one block."""
+    b, sq, hq, d = q.shape
+    out = torch.empty((b, sq, hq, d), dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty((b, hq, sq), dtype=torch.float32, device=q.device)
+    ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_WRITE, out=out, lse=lse)],
+                 scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL)
+    return out, lse
+
+
+def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None, dk=None, dv=None):
+    """dq, dk, dv (bf16) of one block using the given (global) out/lse; returns delta too."""
+    b, sq, hq, d = q.shape
+    hkv = k.shape[2]
+    if dout.stride() != out.stride():
+        # the delta kernel reads out and dout with one set of strides
+        dout = torch.empty_like(out).copy_(dout)
+    delta = torch.empty((b, hq, sq), dtype=torch.float32, device=q.device)
+    ops.attn_bwd_delta(out, dout, delta, hkv)
+    dq_t = dq if (dq is not None and dq.stride() == dout.stride()) else torch.empty_like(dout)
+    dk_t = dk if (dk is not None and dk.is_contiguous()) else torch.empty(
+        k.shape, dtype=torch.bfloat16, device=k.device)
+    dv_t = dv if (dv is not None and dv.stride() == dk_t.stride()) else torch.empty_like(dk_t)
+    ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta,
+                             dq_mode=abi.GRAD_WRITE_BF16, dkv_mode=abi.GRAD_WRITE_BF16,
+                             dq=dq_t, dk=dk_t, dv=dv_t)],
+                 scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL)
+    for dst, src in ((dq, dq_t), (dk, dk_t), (dv, dv_t)):
+        if dst is not None and dst is not src:
+            dst.copy_(src)
+    return (dq if dq is not None else dq_t, dk if dk is not None else dk_t,
+            dv if dv is not None else dv_t, delta)
+
+
+class _HipBlockAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, causal, scale):
+        q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+        out, lse = block_forward(q, k, v, scale, causal)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.causal, ctx.scale = causal, scale
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv, _ = block_backward(_kernel_ready(dout), q, k, v, out, lse, ctx.scale,
+                                       ctx.causal)
+        return dq, dk, dv, None, None
+
+
+def mi355x_hip_block(q, k, v, *, causal, scaling, dropout=0.0, attn_implementation=None,
+                     window=None):
+    """q/k/v: [b, s, h, d] bf16 on the MI355X. Returns (out [b,s,h,d], lse [b,h,s])."""
+    _validate(q, k, v, dropout, window)
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
+    return _HipBlockAttention.apply(q, k, v, bool(causal), float(scale))
+
+
+PROVIDERS = {
+    "mi355x_hip": mi355x_hip_block,
+}
+
+
+# -- Dao-signature op pair (positional arguments as called at ring/zigzag.py:131,219) --
+def _flash_attn_forward(q, k, v, dropout_p, softmax_scale, causal, window_size_left=-1,
+                        window_size_right=-1, softcap=0.0, alibi_slopes=None,
+                        return_softmax=False):
+    _validate(q, k, v, dropout_p,
+              None if (window_size_left, window_size_right) == (-1, -1)
+              else (window_size_left, window_size_right), softcap, alibi_slopes)
+    if return_softmax:
+        raise NotImplementedError("return_softmax is not supported")
+    out, lse = block_forward(_kernel_ready(q), _kernel_ready(k), _kernel_ready(v),
+                             float(softmax_scale), bool(causal))
+    return out, lse, None, None
+
+
+def _flash_attn_backward(dout, q, k, v, out, lse, dq, dk, dv, dropout_p, softmax_scale, causal,
+                         window_size_left=-1, window_size_right=-1, softcap=0.0,
+                         alibi_slopes=None, deterministic=False, rng_state=None):
+    _validate(q, k, v, dropout_p,
+              None if (window_size_left, window_size_right) == (-1, -1)
+              else (window_size_left, window_size_right), softcap, alibi_slopes)
+    _, _, _, delta = block_backward(_kernel_ready(dout), _kernel_ready(q), _kernel_ready(k),
+                                    _kernel_ready(v), _kernel_ready(out), lse,
+                                    float(softmax_scale), bool(causal), dq, dk, dv)
+    return dq, dk, dv, delta
+
+
+def flash_ops():
+    """(fwd, bwd) low-level ops, the drop-in for ``_flash_ops()`` (ring/p2p_attn.py:27-35)."""
+    return _flash_attn_forward, _flash_attn_backward

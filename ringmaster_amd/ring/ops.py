@@ -1,0 +1,177 @@
+"""Tensor-level wrappers of the batched block-attention kernels.
+
+A *job* is one block problem of the C ABI: ``q[sq]`` attends ``k/v[sk]`` with
+tensors given as ``[batch, seq, heads, dim]`` views (any strides on the first
+three axes, contiguous ``dim``), lse-like tensors as ``[batch, heads, seq]``
+views with a contiguous ``seq`` axis. All jobs of one call share the layout
+(strides) of each tensor kind, as the per-rank views of one stacked tensor do,
+and are launched together (up to 16 per kernel launch).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+
+import torch
+
+from ringmaster_amd import abi
+
+
+@dataclasses.dataclass
+class FwdJob:
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    mode: int = abi.FWD_WRITE
+    out: torch.Tensor | None = None
+    lse: torch.Tensor | None = None
+    acc_out: torch.Tensor | None = None
+    acc_lse: torch.Tensor | None = None
+    q_gidx: torch.Tensor | None = None
+    k_gidx: torch.Tensor | None = None
+    doc: torch.Tensor | None = None
+
+
+@dataclasses.dataclass
+class BwdJob:
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    dout: torch.Tensor
+    lse: torch.Tensor
+    delta: torch.Tensor
+    dq_mode: int
+    dkv_mode: int
+    dq_acc: torch.Tensor | None = None
+    dq: torch.Tensor | None = None
+    dk_acc: torch.Tensor | None = None
+    dv_acc: torch.Tensor | None = None
+    dk: torch.Tensor | None = None
+    dv: torch.Tensor | None = None
+    q_gidx: torch.Tensor | None = None
+    k_gidx: torch.Tensor | None = None
+    doc: torch.Tensor | None = None
+
+
+_ROLES = {
+    # role -> (layout field prefix, number of strides, dtype)
+    "q": ("q", 3, torch.bfloat16),
+    "k": ("k", 3, torch.bfloat16),
+    "v": ("v", 3, torch.bfloat16),
+    "out": ("o", 3, torch.bfloat16),
+    "dout": ("o", 3, torch.bfloat16),
+    "dq": ("o", 3, torch.bfloat16),
+    "acc_out": ("a", 3, torch.float32),
+    "dq_acc": ("a", 3, torch.float32),
+    "lse": ("l", 2, torch.float32),
+    "acc_lse": ("l", 2, torch.float32),
+    "delta": ("l", 2, torch.float32),
+    "dk": ("dk", 3, torch.bfloat16),
+    "dv": ("dk", 3, torch.bfloat16),
+    "dk_acc": ("ka", 3, torch.float32),
+    "dv_acc": ("ka", 3, torch.float32),
+}
+
+
+def _fill_layout(jobs, batch, hq, hkv, head_dim, scale, mask) -> abi.AttnLayout:
+    lay = abi.AttnLayout()
+    lay.batch, lay.hq, lay.hkv, lay.head_dim = batch, hq, hkv, head_dim
+    lay.scale = float(scale)
+    lay.mask = mask
+    seen: dict[str, tuple] = {}
+    for job in jobs:
+        for role, (prefix, n, dtype) in _ROLES.items():
+            t = getattr(job, role, None)
+            if t is None:
+                continue
+            if t.dtype != dtype:
+                raise ValueError(f"{role} must be {dtype} (got {t.dtype})")
+            abi.require_device(t)
+            if n == 3:
+                if t.dim() != 4 or t.stride(3) != 1:
+                    raise ValueError(f"{role} must be [batch, seq, heads, dim] with contiguous dim")
+                st = (t.stride(0), t.stride(1), t.stride(2))
+            else:
+                if t.dim() != 3 or (t.shape[2] > 1 and t.stride(2) != 1):
+                    raise ValueError(f"{role} must be [batch, heads, seq] with contiguous seq")
+                st = (t.stride(0), t.stride(1))
+            if prefix in seen and seen[prefix] != st:
+                raise ValueError(f"all {prefix}-kind tensors of one call must share strides "
+                                 f"({seen[prefix]} vs {st} for {role})")
+            seen[prefix] = st
+    for prefix, st in seen.items():
+        names = ("_sb", "_ss", "_sh") if len(st) == 3 else ("_sb", "_sh")
+        for nm, s in zip(names, st):
+            setattr(lay, prefix + nm, int(s))
+    return lay
+
+
+def _check_shapes(q, k, v, batch, hq, hkv, d):
+    if q.shape[0] != batch or q.shape[2] != hq or q.shape[3] != d:
+        raise ValueError(f"q shape {tuple(q.shape)} does not match the call layout")
+    if k.shape[0] != batch or k.shape[2] != hkv or k.shape[3] != d or v.shape != k.shape:
+        raise ValueError(f"k/v shapes {tuple(k.shape)}/{tuple(v.shape)} do not match")
+
+
+def _int32(t):
+    if t is None:
+        return None
+    if t.dtype != torch.int32 or not t.is_contiguous():
+        raise ValueError("index tensors must be contiguous int32")
+    abi.require_device(t)
+    return t.data_ptr()
+
+
+def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int) -> None:
+    """Launch the batched block forward (rmx_attn_fwd) for ``jobs``."""
+    if not jobs:
+        return
+    q0, k0 = jobs[0].q, jobs[0].k
+    batch, hq, d, hkv = q0.shape[0], q0.shape[2], q0.shape[3], k0.shape[2]
+    for j in jobs:
+        _check_shapes(j.q, j.k, j.v, batch, hq, hkv, d)
+    lay = _fill_layout(jobs, batch, hq, hkv, d, scale, mask)
+    arr = (abi.FwdProblem * len(jobs))()
+    for i, j in enumerate(jobs):
+        p = arr[i]
+        p.q, p.k, p.v = j.q.data_ptr(), j.k.data_ptr(), j.v.data_ptr()
+        p.out, p.lse = abi.ptr(j.out), abi.ptr(j.lse)
+        p.acc_out, p.acc_lse = abi.ptr(j.acc_out), abi.ptr(j.acc_lse)
+        p.q_gidx, p.k_gidx, p.doc = _int32(j.q_gidx), _int32(j.k_gidx), _int32(j.doc)
+        p.sq, p.sk, p.mode = j.q.shape[1], j.k.shape[1], j.mode
+    abi.check(abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, len(jobs), abi.stream_of(q0)))
+
+
+def attn_bwd_delta(out: torch.Tensor, dout: torch.Tensor, delta: torch.Tensor, hkv: int) -> None:
+    """delta[b, h, s] = sum_d dout * out (fp32). out/dout: [b, s, h, d] bf16 with equal strides."""
+    batch, sq, hq, d = out.shape
+    if dout.shape != out.shape or dout.stride() != out.stride():
+        raise ValueError("out and dout must share shape and strides")
+    job = FwdJob(q=out, k=out[:, :0, :hkv], v=out[:, :0, :hkv], out=out, lse=delta)
+    lay = _fill_layout([job], batch, hq, hkv, d, 1.0, abi.MASK_FULL)
+    abi.check(abi.lib().rmx_attn_bwd_delta(ctypes.byref(lay), out.data_ptr(), dout.data_ptr(),
+                                           delta.data_ptr(), sq, abi.stream_of(out)))
+
+
+def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int) -> None:
+    """Launch the batched block backward (rmx_attn_bwd) for ``jobs``."""
+    if not jobs:
+        return
+    q0, k0 = jobs[0].q, jobs[0].k
+    batch, hq, d, hkv = q0.shape[0], q0.shape[2], q0.shape[3], k0.shape[2]
+    for j in jobs:
+        _check_shapes(j.q, j.k, j.v, batch, hq, hkv, d)
+    lay = _fill_layout(jobs, batch, hq, hkv, d, scale, mask)
+    arr = (abi.BwdProblem * len(jobs))()
+    for i, j in enumerate(jobs):
+        p = arr[i]
+        p.q, p.k, p.v, p.dout = j.q.data_ptr(), j.k.data_ptr(), j.v.data_ptr(), j.dout.data_ptr()
+        p.lse, p.delta = j.lse.data_ptr(), j.delta.data_ptr()
+        p.dq_acc, p.dq = abi.ptr(j.dq_acc), abi.ptr(j.dq)
+        p.dk_acc, p.dv_acc = abi.ptr(j.dk_acc), abi.ptr(j.dv_acc)
+        p.dk, p.dv = abi.ptr(j.dk), abi.ptr(j.dv)
+        p.q_gidx, p.k_gidx, p.doc = _int32(j.q_gidx), _int32(j.k_gidx), _int32(j.doc)
+        p.sq, p.sk = j.q.shape[1], j.k.shape[1]
+        p.dq_mode, p.dkv_mode = j.dq_mode, j.dkv_mode
+    abi.check(abi.lib().rmx_attn_bwd(ctypes.byref(lay), arr, len(jobs), abi.stream_of(q0)))

@@ -1,0 +1,91 @@
+"""Zigzag ring schedule as per-step lists of block problems (pure host logic).
+
+Restates the step cases of ``ZigzagRingAttention`` (ring/zigzag.py:9-14,127-143 and
+the backward :212-252). Rank ``r`` holds zigzag chunks ``r`` (early, rows
+``[0, h)``) and ``2P-1-r`` (late, rows ``[h, 2h)``); at step ``s`` it sees the KV
+block of rank ``(r - s) mod P`` (ring/zigzag.py:93, direction ring/p2p_attn.py:65-69):
+
+* ``s == 0``       local block, causal on the concatenated ``2h x 2h`` block;
+* ``1 <= s <= r``  all Q rows x the early half ``[0, h)`` of the remote KV;
+* ``s > r``        the late Q rows ``[h, 2h)`` x the whole remote KV.
+
+The forward additionally tags each block with whether it is the first / last
+ring step that touches its Q rows, so the kernel epilogue can initialise the
+running fp32 (out, lse) at the first touch and emit the final bf16 out + lse at
+the last one. Early rows are last touched at step ``r``, late rows at ``P-1``;
+when the two halves of one block disagree the block is split by rows (for the
+causal step-0 block: early rows x keys ``[0, h)``, late rows x keys ``[0, 2h)``,
+both bottom-right causal, which is exactly the global causal mask again).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+
+@dataclasses.dataclass(frozen=True)
+class Block:
+    rank: int
+    q_lo: int
+    q_hi: int
+    kv_rank: int
+    k_lo: int
+    k_hi: int
+    causal: bool
+    first: bool = True
+    last: bool = True
+
+    @property
+    def pairs(self) -> int:
+        """Attended (q, k) pairs of this block (bottom-right causal when ``causal``)."""
+        sq, sk = self.q_hi - self.q_lo, self.k_hi - self.k_lo
+        if not self.causal:
+            return sq * sk
+        off = sk - sq
+        return sum(max(0, min(sk, i + off + 1)) for i in range(sq))
+
+
+def zigzag_schedule(world: int, local_len: int, *, split_final: bool) -> list[list[Block]]:
+    """Blocks of every ring step. ``split_final=False`` gives one block per rank per
+    step (what the backward uses: each KV block is then visited once per step)."""
+    if world < 1:
+        raise ValueError("world must be positive")
+    if local_len % 2:
+        raise ValueError(f"local length {local_len} must hold two equal zigzag chunks")
+    h = local_len // 2
+    steps: list[list[Block]] = []
+    for s in range(world):
+        blocks: list[Block] = []
+        for r in range(world):
+            rem = (r - s) % world
+            e_first = l_first = s == 0
+            e_last = s == r
+            l_last = s == world - 1
+            if s == 0:
+                if not split_final or e_last == l_last:
+                    blocks.append(Block(r, 0, 2 * h, rem, 0, 2 * h, True, True, e_last and l_last))
+                else:
+                    blocks.append(Block(r, 0, h, rem, 0, h, True, e_first, e_last))
+                    blocks.append(Block(r, h, 2 * h, rem, 0, 2 * h, True, l_first, l_last))
+            elif s <= r:
+                if not split_final or e_last == l_last:
+                    blocks.append(Block(r, 0, 2 * h, rem, 0, h, False, False, e_last and l_last))
+                else:
+                    blocks.append(Block(r, 0, h, rem, 0, h, False, False, e_last))
+                    blocks.append(Block(r, h, 2 * h, rem, 0, h, False, False, l_last))
+            else:
+                blocks.append(Block(r, h, 2 * h, rem, 0, 2 * h, False, False, l_last))
+        steps.append(blocks)
+    return steps
+
+
+def zigzag_gidx(rank: int, half: int, world: int) -> list[int]:
+    """Global token indices of ``rank``'s two chunks, early then late (ring/zigzag.py:40-46)."""
+    return (list(range(rank * half, (rank + 1) * half))
+            + list(range((2 * world - 1 - rank) * half, (2 * world - rank) * half)))
+
+
+def ring_pairs_per_rank(world: int, local_len: int) -> int:
+    """Pairs each rank attends: L(L+1)/2 + (P-1) * 2h^2, equal on every rank."""
+    h = local_len // 2
+    return local_len * (local_len + 1) // 2 + (world - 1) * 2 * h * h

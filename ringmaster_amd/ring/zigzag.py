@@ -1,0 +1,237 @@
+"""Zigzag (head_tail) ring attention, P ranks emulated in one process on one MI355X.
+
+Mirrors ``ZigzagRingAttention`` (ring/zigzag.py:70-260): the same three step
+cases, the online-softmax merge, and the reverse-ring backward that uses the
+GLOBAL merged out/lse for every block and lets the dK/dV accumulators travel
+with their KV block to the owner. Differences that come from running every rank
+on one GPU (no collectives, one process):
+
+* inputs are the per-rank interface tensors stacked on a leading rank axis,
+  ``q/k/v [P, b, H, L, d]`` (each ``[b, H, L, d]`` exactly as the reference
+  receives it); the output is ``[P, b, L, H, d]``, grads ``[P, b, H, L, d]``;
+* a ring hop is index arithmetic: at step ``s`` rank ``r`` reads the KV block
+  of rank ``(r - s) mod P`` in place from HBM (one remote block resident per
+  rank per step, within the reference's 2-block prefetch budget), and the
+  dK/dV accumulator of that block is updated in place at its owner's slot;
+* each ring step is ONE batched kernel launch over all P ranks (their per-rank
+  problems share the launch), forward and backward;
+* the merge is fused into the forward epilogue, the first/last touch of each
+  row group initialises/finalises in-kernel, and gradients accumulate in fp32
+  (the reference accumulates in bf16, ring/zigzag.py:165-168).
+
+Packed sequences (``cu_seqlens``) use document masks on global indices for every
+block (ring/zigzag.py:86-120,170-209); dense inputs use the causal / full cases.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from ringmaster_amd import abi
+from ringmaster_amd.ring import ops
+from ringmaster_amd.ring.schedule import zigzag_gidx, zigzag_schedule
+
+
+def doc_ids_from_cu(cu_seqlens: torch.Tensor, device) -> torch.Tensor:
+    """Per-token document id over the full sequence (ring/varlen_blocks.py:45-48)."""
+    seg = cu_seqlens.to(device=device, dtype=torch.int64).diff()
+    return torch.repeat_interleave(
+        torch.arange(seg.numel(), device=device, dtype=torch.int32), seg).contiguous()
+
+
+def _fwd_mode(first: bool, last: bool) -> int:
+    if first and last:
+        return abi.FWD_WRITE
+    if first:
+        return abi.FWD_ACC_INIT
+    if last:
+        return abi.FWD_ACC_FINAL
+    return abi.FWD_ACC_MERGE
+
+
+class _Ctx:
+    """Per-call tensors shared by the forward and backward passes."""
+
+    def __init__(self, q, k, scale, doc):
+        self.P, self.b, self.hq, self.L, self.d = q.shape
+        self.hkv = k.shape[2]
+        self.half = self.L // 2
+        self.scale = scale
+        self.doc = doc
+        self.gidx = None
+        if doc is not None:
+            rows = [zigzag_gidx(r, self.half, self.P) for r in range(self.P)]
+            self.gidx = torch.tensor(rows, dtype=torch.int32).to(q.device)
+
+    def mask(self, step: int) -> int:
+        if self.doc is not None:
+            return abi.MASK_DOC
+        return abi.MASK_CAUSAL if step == 0 else abi.MASK_FULL
+
+    def idx(self, rank, lo, hi):
+        return None if self.gidx is None else self.gidx[rank, lo:hi]
+
+
+class KernelTimer:
+    """HIP-event timing of individual kernel launches on the launching stream.
+
+    ``with timer("attn_fwd"):`` brackets one launch; ``mean_ms(name)`` averages the
+    recorded launches after a synchronize."""
+
+    def __init__(self):
+        self.events: dict[str, list] = {}
+
+    def __call__(self, name):
+        timer = self
+
+        class _Span:
+            def __enter__(self):
+                self.a = torch.cuda.Event(enable_timing=True)
+                self.b = torch.cuda.Event(enable_timing=True)
+                self.a.record()
+
+            def __exit__(self, *exc):
+                self.b.record()
+                timer.events.setdefault(name, []).append((self.a, self.b))
+
+        return _Span()
+
+    def mean_ms(self, name):
+        spans = self.events.get(name, [])
+        if not spans:
+            return None
+        return sum(a.elapsed_time(b) for a, b in spans) / len(spans)
+
+    def count(self, name):
+        return len(self.events.get(name, []))
+
+    def clear(self):
+        self.events.clear()
+
+
+class _NoTimer:
+    def __call__(self, name):
+        return self
+
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_TIMER = _NoTimer()
+
+
+def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=None):
+    """Emulated zigzag ring forward. q/k/v: [P, b, H, L, d] bf16 (interface layout per rank).
+    Returns (out [P, b, L, H, d] bf16, lse [P, b, H, L] fp32)."""
+    timer = timer or _NO_TIMER
+    c = _Ctx(q, k, scale, doc)
+    qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)  # [P, b, L, H, d] views
+    dev = q.device
+    out = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
+    acc = acc_lse = None
+    if c.P > 1:
+        acc = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.float32, device=dev)
+        acc_lse = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
+    for s, blocks in enumerate(zigzag_schedule(c.P, c.L, split_final=True)):
+        jobs = []
+        for bl in blocks:
+            r, kr = bl.rank, bl.kv_rank
+            qs, ks = slice(bl.q_lo, bl.q_hi), slice(bl.k_lo, bl.k_hi)
+            jobs.append(ops.FwdJob(
+                q=qd[r][:, qs], k=kd[kr][:, ks], v=vd[kr][:, ks],
+                mode=_fwd_mode(bl.first, bl.last),
+                out=out[r][:, qs], lse=lse[r][:, :, qs],
+                acc_out=None if acc is None else acc[r][:, qs],
+                acc_lse=None if acc_lse is None else acc_lse[r][:, :, qs],
+                q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
+                doc=c.doc))
+        with timer("attn_fwd"):
+            ops.attn_fwd(jobs, scale=scale, mask=c.mask(s))
+    return out, lse
+
+
+def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | None = None,
+                  timer=None):
+    """Reverse-ring backward with the global out/lse. dout/out: [P, b, L, H, d] bf16.
+    Returns fp32 (dq [P, b, L, Hq, d], dk, dv [P, b, L, Hkv, d]). Each step launches the
+    KV-major dK/dV kernel and the Q-major dQ kernel over all ranks."""
+    timer = timer or _NO_TIMER
+    c = _Ctx(q, k, scale, doc)
+    qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)
+    dev = q.device
+    if dout.stride() != out.stride():
+        dout = torch.empty_like(out).copy_(dout)
+    delta = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
+    flat = (c.P * c.b, c.L, c.hq, c.d)
+    with timer("attn_bwd_delta"):
+        ops.attn_bwd_delta(out.reshape(flat), dout.reshape(flat),
+                           delta.reshape(c.P * c.b, c.hq, c.L), c.hkv)
+    dq = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.float32, device=dev)
+    dk = torch.empty((c.P, c.b, c.L, c.hkv, c.d), dtype=torch.float32, device=dev)
+    dv = torch.empty_like(dk)
+    for s, blocks in enumerate(zigzag_schedule(c.P, c.L, split_final=False)):
+        mode = abi.GRAD_WRITE_F32 if s == 0 else abi.GRAD_ACC_F32
+        kv_jobs, q_jobs = [], []
+        for bl in blocks:
+            r, kr = bl.rank, bl.kv_rank
+            qs, ks = slice(bl.q_lo, bl.q_hi), slice(bl.k_lo, bl.k_hi)
+            common = dict(
+                q=qd[r][:, qs], k=kd[kr][:, ks], v=vd[kr][:, ks], dout=dout[r][:, qs],
+                lse=lse[r][:, :, qs], delta=delta[r][:, :, qs],
+                q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
+                doc=c.doc)
+            kv_jobs.append(ops.BwdJob(dq_mode=abi.GRAD_NONE, dkv_mode=mode,
+                                      dk_acc=dk[kr][:, ks], dv_acc=dv[kr][:, ks], **common))
+            q_jobs.append(ops.BwdJob(dq_mode=mode, dkv_mode=abi.GRAD_NONE,
+                                     dq_acc=dq[r][:, qs], **common))
+        with timer("attn_bwd_dkdv"):
+            ops.attn_bwd(kv_jobs, scale=scale, mask=c.mask(s))
+        with timer("attn_bwd_dq"):
+            ops.attn_bwd(q_jobs, scale=scale, mask=c.mask(s))
+    return dq, dk, dv
+
+
+class EmulatedZigzagRing(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, scale, doc, timer):
+        out, lse = ring_forward(q, k, v, scale, doc, timer)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.scale, ctx.doc, ctx.timer = scale, doc, timer
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = ring_backward(d_out, q, k, v, out, lse, ctx.scale, ctx.doc, ctx.timer)
+        # fp32 accumulators -> q.dtype, returned in the interface layout [P, b, H, L, d]
+        return (dq.to(q.dtype).transpose(2, 3), dk.to(k.dtype).transpose(2, 3),
+                dv.to(v.dtype).transpose(2, 3), None, None, None)
+
+
+def zigzag_ring_attention(q, k, v, *, scaling=None, cu_seqlens=None, timer=None):
+    """q/k/v: [P, b, H, L, d] — rank r's zigzag-sharded interface tensors stacked on dim 0
+    (L = two chunks, early then late). Returns [P, b, L, H, d]; ``cu_seqlens`` set =>
+    packed (document-masked) blocks. Counterpart of ring/zigzag.py:257-260. ``timer``
+    (a :class:`KernelTimer`) records HIP events around every kernel launch."""
+    abi.require_device(q, k, v)
+    if q.dim() != 5 or k.dim() != 5 or v.dim() != 5:
+        raise ValueError("q/k/v must be [world, b, H, L, d]")
+    if q.shape[2] % k.shape[2]:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if q.shape[3] % 2:
+        raise ValueError("local length must hold two equal zigzag chunks")
+    if q.dtype != torch.bfloat16:
+        raise NotImplementedError("the MI355X ring computes in bf16")
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
+    doc = None
+    if cu_seqlens is not None:
+        doc = doc_ids_from_cu(cu_seqlens, q.device)
+        if doc.numel() != q.shape[0] * q.shape[3]:
+            raise ValueError("cu_seqlens must cover the full (padded) sequence")
+    return EmulatedZigzagRing.apply(q, k, v, float(scale), doc, timer)

@@ -1,0 +1,44 @@
+"""Helpers shared by the GPU parity tests (seeded inputs, tolerance checks)."""
+
+import torch
+
+# bf16 outputs vs an fp32 reference, fp32 LSE / states
+BF16_MAX_ABS = 2e-2
+BF16_REL_L2 = 1e-2
+F32_REL = 1e-4
+
+
+def seeded(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float32) * scale
+
+
+def bf16_pair(shape, seed, scale=1.0):
+    """(fp32 CPU tensor holding bf16-representable values, bf16 device tensor)."""
+    x = seeded(shape, seed, scale).to(torch.bfloat16)
+    return x.float(), x.cuda()
+
+
+def rel_l2(got, ref):
+    got, ref = got.double(), ref.double()
+    return ((got - ref).norm() / ref.norm().clamp_min(1e-30)).item()
+
+
+def assert_bf16_close(got, ref, what=""):
+    got = got.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    assert got.shape == ref.shape, f"{what}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
+    assert torch.isfinite(got).all(), f"{what}: non-finite values"
+    err = (got - ref).abs().max().item()
+    rl = rel_l2(got, ref)
+    assert err < BF16_MAX_ABS and rl < BF16_REL_L2, f"{what}: max-abs {err:.3e} rel-L2 {rl:.3e}"
+
+
+def assert_f32_rel(got, ref, what="", tol=F32_REL):
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(got)), f"{what}: finiteness differs"
+    err = ((got[fin] - ref[fin]).abs() / ref[fin].abs().clamp_min(1.0)).max().item() \
+        if fin.any() else 0.0
+    assert err < tol, f"{what}: rel err {err:.3e}"

@@ -1,0 +1,104 @@
+"""The C-ABI library loads without a GPU, exports every symbol include/*.h declares, and
+rejects bad arguments on the host (before any launch) with the reference's exception
+classes."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from ringmaster_amd import abi
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "ringmaster_amd.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(rmx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = abi.lib()
+    names = declared_symbols()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), f"missing export {name}"
+    assert set(names) == set(abi.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_abi_version_and_error_string():
+    lib = abi.lib()
+    assert lib.rmx_abi_version() == 1
+    assert isinstance(lib.rmx_last_error(), bytes)
+
+
+def _layout(**kw):
+    lay = abi.AttnLayout()
+    lay.batch, lay.hq, lay.hkv, lay.head_dim = 1, 4, 2, 128
+    lay.scale, lay.mask = 0.125, abi.MASK_FULL
+    for k, v in kw.items():
+        setattr(lay, k, v)
+    return lay
+
+
+def _fwd(lay, n=0):
+    arr = (abi.FwdProblem * max(n, 1))()
+    return abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, n, None)
+
+
+def test_host_validation_gqa_divisibility():
+    rc = _fwd(_layout(hq=3, hkv=2))
+    assert rc == abi.RMX_EINVAL
+    with pytest.raises(ValueError, match="divisible"):
+        abi.check(rc)
+
+
+def test_host_validation_head_dim_and_mask():
+    assert _fwd(_layout(head_dim=96)) == abi.RMX_EUNSUPPORTED
+    with pytest.raises(NotImplementedError):
+        abi.check(abi.RMX_EUNSUPPORTED)
+    assert _fwd(_layout(mask=7)) == abi.RMX_EINVAL
+    assert _fwd(_layout(scale=float("nan"))) == abi.RMX_EINVAL
+    assert _fwd(_layout(q_ss=12)) == abi.RMX_EINVAL  # not a multiple of 8 elements
+
+
+def test_host_validation_problem_fields():
+    lay = _layout()
+    arr = (abi.FwdProblem * 1)()
+    arr[0].sq, arr[0].sk, arr[0].mode = 4, 4, abi.FWD_WRITE
+    assert abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, 1, None) == abi.RMX_EINVAL  # q NULL
+    assert b"NULL" in abi.lib().rmx_last_error()
+    arr[0].q = arr[0].k = arr[0].v = arr[0].out = 16
+    arr[0].mode = 9
+    assert abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, 1, None) == abi.RMX_EINVAL
+    assert b"mode" in abi.lib().rmx_last_error()
+
+
+def test_empty_calls_are_noops():
+    assert _fwd(_layout(), 0) == abi.RMX_OK
+    lib = abi.lib()
+    assert lib.rmx_zigzag_gather(None, None, 0, 0, 2, -1, 16, 0, None, None) == abi.RMX_OK
+    assert lib.rmx_linear_scan_fwd(None, None, None, None, 0, 8, 4, 4, 2, None) == abi.RMX_OK
+
+
+def test_host_validation_shard_and_scan():
+    lib = abi.lib()
+    assert lib.rmx_zigzag_gather(16, 16, 1, 8, 0, -1, 16, 128, None, None) == abi.RMX_EINVAL
+    assert lib.rmx_zigzag_gather(16, 16, 1, 8, 2, 2, 16, 128, None, None) == abi.RMX_EINVAL
+    assert lib.rmx_linear_scan_fwd(16, 16, 16, None, 1, 9, 4, 4, 2, None) == abi.RMX_EINVAL
+    assert lib.rmx_linear_scan_fwd(16, 16, 16, None, 1, 8, 6, 4, 2, None) == abi.RMX_EINVAL
+
+
+def test_product_refuses_cpu_tensors():
+    import torch
+
+    from ringmaster_amd.ring.kernels import mi355x_hip_block
+    from ringmaster_amd.ring.zigzag import zigzag_ring_attention
+
+    q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        mi355x_hip_block(q, q, q, causal=True, scaling=None)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        zigzag_ring_attention(q[None].transpose(2, 3), q[None].transpose(2, 3),
+                              q[None].transpose(2, 3))

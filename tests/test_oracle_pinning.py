@@ -1,0 +1,241 @@
+"""Pin the CPU oracle before trusting it: fp64 brute force, torch SDPA, closed forms
+and invariants (ring == full attention, merge associativity, scan == recurrence).
+Each check is chosen so that a plausible mistake (dropped term, wrong sign or
+index, transposed operand, wrong ring direction) fails it; test_oracle_mutants.py
+plants such mistakes and asserts these checks catch them."""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import ring_math as rm
+from oracle import state_passing as sp
+
+TOL32 = 2e-5
+
+
+def rnd(*shape, seed, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=dtype)
+
+
+def brute_block(q, k, v, causal, scale):
+    """Pure-Python loops over (b, h, i): softmax by its definition, fp64."""
+    b, sq, hq, d = q.shape
+    sk, hkv = k.shape[1], k.shape[2]
+    out = torch.zeros(b, sq, hq, d, dtype=torch.float64)
+    lse = torch.zeros(b, hq, sq, dtype=torch.float64)
+    for bi in range(b):
+        for h in range(hq):
+            kh = h // (hq // hkv)
+            for i in range(sq):
+                js = [j for j in range(sk) if (not causal) or j <= i + (sk - sq)]
+                s = [float((q[bi, i, h] * k[bi, j, kh]).sum()) * scale for j in js]
+                m = max(s)
+                w = [math.exp(x - m) for x in s]
+                z = sum(w)
+                lse[bi, h, i] = m + math.log(z)
+                for wj, j in zip(w, js):
+                    out[bi, i, h] += (wj / z) * v[bi, j, kh]
+    return out, lse
+
+
+def check_block(block_fn, causal, hq, hkv, sq, sk, d=8):
+    q, k, v = rnd(1, sq, hq, d, seed=1), rnd(1, sk, hkv, d, seed=2), rnd(1, sk, hkv, d, seed=3)
+    out, lse = block_fn(q, k, v, causal=causal, scaling=None)
+    ref_out, ref_lse = brute_block(q, k, v, causal, 1.0 / math.sqrt(d))
+    assert torch.allclose(out.double(), ref_out, atol=TOL32, rtol=TOL32)
+    assert torch.allclose(lse.double(), ref_lse, atol=TOL32, rtol=TOL32)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("hq,hkv,sq,sk", [(2, 2, 5, 5), (4, 2, 3, 7), (4, 1, 6, 6)])
+def test_math_block_vs_brute_force(causal, hq, hkv, sq, sk):
+    check_block(rm.math_block, causal, hq, hkv, sq, sk)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_math_block_vs_sdpa(causal):
+    # library routine: SDPA with GQA; square blocks so top-left == bottom-right causal
+    q, k, v = rnd(2, 16, 8, 32, seed=4), rnd(2, 16, 2, 32, seed=5), rnd(2, 16, 2, 32, seed=6)
+    out, _ = rm.math_block(q, k, v, causal=causal, scaling=0.3)
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                         is_causal=causal, scale=0.3, enable_gqa=True)
+    assert torch.allclose(out.double(), ref.transpose(1, 2), atol=TOL32)
+
+
+def check_merge(merge_fn):
+    """merge(attn(Q, K1), attn(Q, K2)) == attn(Q, [K1; K2]) in out and lse."""
+    q = rnd(1, 6, 2, 8, seed=7)
+    k1, v1 = rnd(1, 5, 2, 8, seed=8), rnd(1, 5, 2, 8, seed=9)
+    k2, v2 = rnd(1, 4, 2, 8, seed=10) + 1.5, rnd(1, 4, 2, 8, seed=11)
+    o1, l1 = rm.math_block(q, k1, v1, causal=False, scaling=None)
+    o2, l2 = rm.math_block(q, k2, v2, causal=False, scaling=None)
+    out, lse = merge_fn(None, None, o1, l1)
+    out, lse = merge_fn(out, lse, o2, l2)
+    ref_o, ref_l = rm.math_block(q, torch.cat([k1, k2], 1), torch.cat([v1, v2], 1), causal=False,
+                                 scaling=None)
+    assert torch.allclose(out.double(), ref_o.double(), atol=TOL32)
+    assert torch.allclose(lse.squeeze(-1).transpose(1, 2).double(), ref_l.double(), atol=TOL32)
+
+
+def test_merge_equals_concatenated_attention():
+    check_merge(rm.update_out_and_lse)
+
+
+def test_merge_neg_inf_block_is_noop_and_commutes():
+    q = rnd(1, 3, 1, 4, seed=12)
+    o1, l1 = rm.math_block(q, rnd(1, 3, 1, 4, seed=13), rnd(1, 3, 1, 4, seed=14), causal=False,
+                           scaling=None)
+    o2, l2 = rm.math_block(q, rnd(1, 2, 1, 4, seed=15), rnd(1, 2, 1, 4, seed=16), causal=False,
+                           scaling=None)
+    a, la = rm.update_out_and_lse(*rm.update_out_and_lse(None, None, o1, l1), o2, l2)
+    b, lb = rm.update_out_and_lse(*rm.update_out_and_lse(None, None, o2, l2), o1, l1)
+    assert torch.allclose(a, b, atol=1e-6) and torch.allclose(la, lb, atol=1e-6)
+    c, lc = rm.update_out_and_lse(a, la, torch.zeros_like(o1), torch.full_like(l1, -math.inf))
+    assert torch.equal(c, a) and torch.equal(lc, la)
+
+
+def zigzag_case(world, half, hq=4, hkv=4, d=8, seed=0, cu=None):
+    S = 2 * world * half
+    q, k, v = rnd(1, S, hq, d, seed=seed + 1), rnd(1, S, hkv, d, seed=seed + 2), \
+        rnd(1, S, hkv, d, seed=seed + 3)
+    dout = rnd(1, S, hq, d, seed=seed + 4)
+    return q, k, v, dout
+
+
+def check_ring(world, half, hq=4, hkv=4, cu=None, fwd=rm.zigzag_ring_forward,
+               bwd=rm.zigzag_ring_backward, tol=1e-5):
+    """The emulated zigzag ring equals full (doc-)causal attention, values and grads."""
+    q, k, v, dout = zigzag_case(world, half, hq, hkv)
+    idx = [rm.zigzag_gidx(r, half, world) for r in range(world)]
+    shard = lambda t: [t[:, i].transpose(1, 2).contiguous() for i in idx]  # noqa: E731
+    outs, lses = fwd(shard(q), shard(k), shard(v), cu_seqlens=cu)
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    ref, ref_lse = rm.full_attention(qr, kr, vr, causal=True, cu_seqlens=cu)
+    ref.backward(dout)
+    err = 0.0
+    for r in range(world):
+        err = max(err, (outs[r].double() - ref.detach()[:, idx[r]]).abs().max().item())
+        err = max(err, (lses[r].double() - ref_lse.detach()[:, :, idx[r]]).abs().max().item())
+    dqs, dks, dvs = bwd([dout[:, i] for i in idx], shard(q), shard(k), shard(v), outs, lses,
+                        cu_seqlens=cu)
+    for r in range(world):
+        err = max(err, (dqs[r].double() - qr.grad[:, idx[r]].transpose(1, 2)).abs().max().item())
+        err = max(err, (dks[r].double() - kr.grad[:, idx[r]].transpose(1, 2)).abs().max().item())
+        err = max(err, (dvs[r].double() - vr.grad[:, idx[r]].transpose(1, 2)).abs().max().item())
+    assert err < tol, f"ring vs full attention err {err}"
+
+
+@pytest.mark.parametrize("world", [1, 2, 4, 8])
+def test_zigzag_ring_equals_full_causal(world):
+    check_ring(world, half=3)
+
+
+def test_zigzag_ring_gqa():
+    check_ring(4, half=2, hq=4, hkv=2)
+
+
+@pytest.mark.parametrize("seq_len,docs,world", [(16, [6, 10], 2), (16, [5, 7, 4], 2),
+                                                (32, [10, 9, 13], 4), (24, [3, 3, 6, 4, 8], 4)])
+def test_zigzag_varlen_equals_per_document(seq_len, docs, world):
+    cu = torch.tensor([0, *torch.tensor(docs).cumsum(0).tolist()], dtype=torch.int32)
+    half = seq_len // (2 * world)
+    check_ring(world, half, cu=cu)
+
+
+def test_full_attention_per_doc_equals_sdpa_per_doc():
+    docs = [5, 7, 4]
+    cu = torch.tensor([0, 5, 12, 16])
+    q, k, v = rnd(1, 16, 2, 8, seed=20), rnd(1, 16, 2, 8, seed=21), rnd(1, 16, 2, 8, seed=22)
+    out, _ = rm.full_attention(q, k, v, causal=True, cu_seqlens=cu)
+    parts = []
+    for a, b in zip(cu[:-1].tolist(), cu[1:].tolist()):
+        parts.append(F.scaled_dot_product_attention(
+            q[:, a:b].transpose(1, 2), k[:, a:b].transpose(1, 2), v[:, a:b].transpose(1, 2),
+            is_causal=True).transpose(1, 2))
+    assert sum(docs) == 16
+    assert torch.allclose(out, torch.cat(parts, 1), atol=1e-10)
+
+
+def test_attention_rows_matches_full():
+    q, k, v = rnd(1, 24, 4, 8, seed=30), rnd(1, 24, 2, 8, seed=31), rnd(1, 24, 2, 8, seed=32)
+    ref, ref_lse = rm.full_attention(q, k, v, causal=True)
+    pos = torch.tensor([0, 5, 23])
+    out, lse = rm.attention_rows(q[:, pos], k, v, pos)
+    assert torch.allclose(out, ref[:, pos], atol=1e-10)
+    assert torch.allclose(lse, ref_lse[:, :, pos], atol=1e-10)
+
+
+# ---------------------------------------------------------------- scan
+def check_scan(scan_fn, world=2, T=8, d=3, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    a = (torch.rand(1, T, d, generator=g, dtype=torch.float64) * 0.9 + 0.05).requires_grad_(True)
+    b = torch.randn(1, T, d, generator=g, dtype=torch.float64).requires_grad_(True)
+    ref = sp.local_linear_scan(a, b)
+    got = scan_fn(a, b, world)
+    assert torch.allclose(got, ref, atol=1e-10)
+    ga = torch.autograd.grad(ref.square().sum(), (a, b))
+    gb = torch.autograd.grad(got.square().sum(), (a, b))
+    for x, y in zip(ga, gb):
+        assert torch.allclose(x, y, atol=1e-10)
+
+
+@pytest.mark.parametrize("world", [1, 2, 4, 8])
+def test_cp_linear_scan_equals_global(world):
+    check_scan(sp.cp_linear_scan_emulated, world=world, T=16)
+
+
+def test_local_scan_closed_forms():
+    b = rnd(2, 10, 3, seed=40)
+    assert torch.allclose(sp.local_linear_scan(torch.ones_like(b), b), b.cumsum(1), atol=1e-12)
+    a = torch.rand(2, 10, 3, dtype=torch.float64) + 0.5
+    b0 = torch.zeros_like(b)
+    b0[:, 0] = 1.0
+    assert torch.allclose(sp.local_linear_scan(a, b0), a.cumprod(1) / a[:, :1], atol=1e-12)
+    assert torch.allclose(sp.local_linear_scan_vec(a, b), sp.local_linear_scan(a, b), atol=1e-12)
+
+
+def test_gated_linear_attention_cast():
+    """S_t = g_t S_{t-1} + k_t v_t^T, o_t = q_t S_t via the scan (tests/test_state_passing.py:61-115)."""
+    g = torch.Generator().manual_seed(1)
+    T, dk, dv = 8, 4, 5
+    q, k, v = (torch.randn(T, n, generator=g, dtype=torch.float64) for n in (dk, dk, dv))
+    gate = torch.rand(T, generator=g, dtype=torch.float64) * 0.9 + 0.05
+    S = torch.zeros(dk, dv, dtype=torch.float64)
+    ref = []
+    for t in range(T):
+        S = gate[t] * S + torch.outer(k[t], v[t])
+        ref.append(q[t] @ S)
+    ref = torch.stack(ref)
+    kv = torch.einsum("ti,tj->tij", k, v).reshape(1, T, dk * dv)
+    a = gate.reshape(1, T, 1).expand(1, T, dk * dv)
+    states = sp.cp_linear_scan_emulated(a, kv, 2).reshape(T, dk, dv)
+    assert torch.allclose(torch.einsum("ti,tij->tj", q, states), ref, atol=1e-10)
+
+
+@pytest.mark.parametrize("world", [2, 4, 8])
+def test_mamba2_prefix_equals_global_ssd(world):
+    torch.manual_seed(0)
+    b, T, H, d, G, n = 1, 16, 2, 3, 1, 4
+    x = torch.randn(b, T, H, d, dtype=torch.float64)
+    dt = torch.rand(b, T, H, dtype=torch.float64) * 0.1
+    A = -torch.rand(H, dtype=torch.float64)
+    B = torch.randn(b, T, G, n, dtype=torch.float64)
+    C = torch.randn(b, T, G, n, dtype=torch.float64)
+    ref_out, _ = sp.ssd_reference(x, dt, A, B, C)
+    n_loc = T // world
+    finals, decays, parts = [], [], []
+    for r in range(world):
+        sl = slice(r * n_loc, (r + 1) * n_loc)
+        out_c, h_final = sp.ssd_reference(x[:, sl], dt[:, sl], A, B[:, sl], C[:, sl])
+        cum_A = torch.cumsum(A[None, None, :] * dt[:, sl], dim=1)
+        finals.append(h_final)
+        decays.append(torch.exp(cum_A[:, -1]))
+        parts.append((out_c, h_final, sl, cum_A))
+    prefixes = sp.cp_state_prefix_emulated(finals, decays)
+    for r, (out_c, h_final, sl, cum_A) in enumerate(parts):
+        corrected, _ = sp.mamba2_cp_correction(out_c, h_final, C[:, sl], cum_A, prefixes[r], H, d)
+        assert (corrected - ref_out[:, sl]).abs().max().item() < 1e-6
