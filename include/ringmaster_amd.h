@@ -40,10 +40,12 @@ extern "C" {
 #define RMX_MASK_DOC 2    /* doc[qg] == doc[kg] && kg <= qg on global indices */
 
 /* forward epilogue modes (online-softmax merge, ring/merge.py:20-31) */
-#define RMX_FWD_WRITE 0       /* out/lse := this block's (out, lse) */
+#define RMX_FWD_WRITE 0       /* out/lse := this block's (out, lse); acc_out (nullable)
+                                 := the same out in fp32 */
 #define RMX_FWD_ACC_INIT 1    /* acc_out/acc_lse := this block (first ring step) */
 #define RMX_FWD_ACC_MERGE 2   /* acc := merge(acc, block) */
-#define RMX_FWD_ACC_FINAL 3   /* out(bf16)/lse := merge(acc, block); acc untouched */
+#define RMX_FWD_ACC_FINAL 3   /* out(bf16)/lse := merge(acc, block); acc_out := the merged
+                                 out in fp32; acc_lse untouched */
 
 /* backward gradient output modes */
 #define RMX_GRAD_WRITE_BF16 0 /* grad_bf16 := this block's gradient */
@@ -125,10 +127,14 @@ int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* probl
                      int32_t nproblems, void* stream);
 
 /*
- * delta[b, h, s] = sum_d dout * out for each problem (FlashAttention-2 backward
- * preprocess). `out` uses the o_* strides.
+ * delta[b, h, s] = sum_d dout * out (FlashAttention-2 backward preprocess;
+ * the rowsum(dO * O) of ring/p2p_attn.py:243-281). `out` is bf16 with the o_*
+ * strides (out_is_f32 == 0, what a Dao-style bwd receives) or the fp32 final
+ * out left in acc_out by the forward, with the a_* strides (out_is_f32 != 0):
+ * the fp32 form matches the reference `math` provider, whose autograd never
+ * rounds out to bf16. dout uses the o_* strides.
  */
-int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const uint16_t* out,
+int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const void* out, int32_t out_is_f32,
                            const uint16_t* dout, float* delta, int32_t sq, void* stream);
 
 /*

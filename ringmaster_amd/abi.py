@@ -83,7 +83,7 @@ SIGNATURES = {
     "rmx_abi_version": (_i32, []),
     "rmx_last_error": (ctypes.c_char_p, []),
     "rmx_attn_fwd": (_i32, [ctypes.POINTER(AttnLayout), ctypes.POINTER(FwdProblem), _i32, _vp]),
-    "rmx_attn_bwd_delta": (_i32, [ctypes.POINTER(AttnLayout), _vp, _vp, _vp, _i32, _vp]),
+    "rmx_attn_bwd_delta": (_i32, [ctypes.POINTER(AttnLayout), _vp, _i32, _vp, _vp, _i32, _vp]),
     "rmx_attn_bwd": (_i32, [ctypes.POINTER(AttnLayout), ctypes.POINTER(BwdProblem), _i32, _vp]),
     "rmx_lse_merge": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32,
                              ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),

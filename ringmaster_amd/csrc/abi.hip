@@ -123,7 +123,7 @@ int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* probl
   return RMX_OK;
 }
 
-int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const uint16_t* out,
+int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const void* out, int32_t out_is_f32,
                            const uint16_t* dout, float* delta, int32_t sq, void* stream) {
   int rc = check_layout(layout);
   if (rc) return rc;
@@ -132,7 +132,8 @@ int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const uint16_t* out,
   if ((rc = check_bf16(out, "out"))) return rc;
   if ((rc = check_bf16(dout, "dout"))) return rc;
   if (!delta) return fail(RMX_EINVAL, "delta is NULL");
-  return dev_status(rmx::launch_attn_bwd_delta(*layout, out, dout, delta, sq, (hipStream_t)stream),
+  return dev_status(rmx::launch_attn_bwd_delta(*layout, out, out_is_f32 != 0, dout, delta, sq,
+                                               (hipStream_t)stream),
                     "rmx_attn_bwd_delta launch");
 }
 

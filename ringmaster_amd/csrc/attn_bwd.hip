@@ -29,9 +29,12 @@ struct BwdParams {
 };
 
 // ---------------------------------------------------------------- delta
-template <int HD>
+// delta = rowsum(dout * out). `out` is the bf16 output (o_* strides) or, when
+// OUT_F32, the fp32 merged output (a_* strides): the fp32 form keeps the bf16
+// rounding of out (up to |dout|*|out|*2^-9 per element) out of dS = P (dP - delta).
+template <int HD, bool OUT_F32>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layout L,
-                                                             const uint16_t* __restrict__ out,
+                                                             const void* __restrict__ out,
                                                              const uint16_t* __restrict__ dout,
                                                              float* __restrict__ delta, int sq) {
   constexpr int TPR = HD / 8;  // threads per row
@@ -45,11 +48,30 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layo
     q = (row / L.hq) % sq;
     bb = row / (L.hq * sq);
     const int64_t off = bb * L.o_sb + (int64_t)q * L.o_ss + h * L.o_sh + 8 * part;
-    const u32x4 a = ld16(out + off), b = ld16(dout + off);
+    const u32x4 b = ld16(dout + off);
+    float o[8];
+    if (OUT_F32) {
+      const float* op = reinterpret_cast<const float*>(out) + bb * L.a_sb + (int64_t)q * L.a_ss +
+                        h * L.a_sh + 8 * part;
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(op);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(op + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[i] = x0[i];
+        o[4 + i] = x1[i];
+      }
+    } else {
+      const u32x4 a = ld16(reinterpret_cast<const uint16_t*>(out) + off);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[2 * i] = __uint_as_float(a[i] << 16);
+        o[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      acc += __uint_as_float(a[i] << 16) * __uint_as_float(b[i] << 16);
-      acc += __uint_as_float(a[i] & 0xffff0000u) * __uint_as_float(b[i] & 0xffff0000u);
+      acc += o[2 * i] * __uint_as_float(b[i] << 16);
+      acc += o[2 * i + 1] * __uint_as_float(b[i] & 0xffff0000u);
     }
   }
 #pragma unroll
@@ -57,19 +79,28 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layo
   if (row < rows && part == 0) delta[bb * L.l_sb + h * L.l_sh + q] = acc;
 }
 
-hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const uint16_t* out,
+template <int HD>
+static void launch_delta_t(const rmx_attn_layout& L, const void* out, int out_f32,
+                           const uint16_t* dout, float* delta, int sq, int64_t rows,
+                           hipStream_t stream) {
+  constexpr int RPB = 256 / (HD / 8);  // rows per block
+  const int grid = (int)((rows + RPB - 1) / RPB);
+  if (out_f32)
+    hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, true>), dim3(grid), dim3(256), 0, stream, L, out,
+                       dout, delta, sq);
+  else
+    hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, false>), dim3(grid), dim3(256), 0, stream, L,
+                       out, dout, delta, sq);
+}
+
+hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int out_f32,
                                  const uint16_t* dout, float* delta, int sq, hipStream_t stream) {
   const int64_t rows = (int64_t)L.batch * sq * L.hq;
   if (rows == 0) return hipSuccess;
-  if (L.head_dim == 128) {
-    const int grid = (int)((rows + 15) / 16);
-    hipLaunchKernelGGL(attn_bwd_delta_kernel<128>, dim3(grid), dim3(256), 0, stream, L, out, dout,
-                       delta, sq);
-  } else {
-    const int grid = (int)((rows + 31) / 32);
-    hipLaunchKernelGGL(attn_bwd_delta_kernel<64>, dim3(grid), dim3(256), 0, stream, L, out, dout,
-                       delta, sq);
-  }
+  if (L.head_dim == 128)
+    launch_delta_t<128>(L, out, out_f32, dout, delta, sq, rows, stream);
+  else
+    launch_delta_t<64>(L, out, out_f32, dout, delta, sq, rows, stream);
   return hipGetLastError();
 }
 

@@ -310,9 +310,10 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(const FwdParams pr
           const f32x4 a = *reinterpret_cast<const f32x4*>(accrow + d0);
           v += a * wa;
         }
-        if (P.mode == RMX_FWD_ACC_INIT || P.mode == RMX_FWD_ACC_MERGE) {
-          *reinterpret_cast<f32x4*>(accrow + d0) = v;
-        } else {
+        // every mode leaves the fp32 result in acc_out when it is given (WRITE and
+        // ACC_FINAL: the final out in fp32, which the backward's delta reads)
+        if (accrow) *reinterpret_cast<f32x4*>(accrow + d0) = v;
+        if (P.mode == RMX_FWD_WRITE || P.mode == RMX_FWD_ACC_FINAL) {
           u32x2 w;
           w[0] = pack_bf2(v[0], v[1]);
           w[1] = pack_bf2(v[2], v[3]);

@@ -10,7 +10,7 @@ namespace rmx {
 
 hipError_t launch_attn_fwd(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                            hipStream_t stream);
-hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const uint16_t* out,
+hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int out_f32,
                                  const uint16_t* dout, float* delta, int sq, hipStream_t stream);
 hipError_t launch_attn_bwd(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                            hipStream_t stream);

@@ -51,25 +51,31 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
-def block_forward(q, k, v, scale: float, causal: bool):
-    """(out bf16 [b, sq, hq, d], lse fp32 [b, hq, sq]) of one block."""
+def block_forward(q, k, v, scale: float, causal: bool, keep_f32: bool = False):
+    """(out bf16 [b, sq, hq, d], lse fp32 [b, hq, sq]) of one block; with ``keep_f32`` also
+    the fp32 out (what the backward's delta is computed from)."""
     b, sq, hq, d = q.shape
     out = torch.empty((b, sq, hq, d), dtype=torch.bfloat16, device=q.device)
     lse = torch.empty((b, hq, sq), dtype=torch.float32, device=q.device)
-    ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_WRITE, out=out, lse=lse)],
+    out32 = torch.empty((b, sq, hq, d), dtype=torch.float32, device=q.device) if keep_f32 else None
+    ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_WRITE, out=out, lse=lse,
+                             acc_out=out32)],
                  scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL)
-    return out, lse
+    return (out, lse, out32) if keep_f32 else (out, lse)
 
 
-def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None, dk=None, dv=None):
-    """dq, dk, dv (bf16) of one block using the given (global) out/lse; returns delta too."""
+def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None, dk=None, dv=None,
+                   out_f32=None):
+    """dq, dk, dv (bf16) of one block using the given (global) out/lse; returns delta too.
+    ``out_f32`` (the forward's fp32 out), when given, is what delta = rowsum(dout * out) reads;
+    otherwise the bf16 ``out`` is used, as a Dao-style backward does."""
     b, sq, hq, d = q.shape
     hkv = k.shape[2]
     if dout.stride() != out.stride():
-        # the delta kernel reads out and dout with one set of strides
+        # the delta kernel reads a bf16 out and dout with one set of strides
         dout = torch.empty_like(out).copy_(dout)
     delta = torch.empty((b, hq, sq), dtype=torch.float32, device=q.device)
-    ops.attn_bwd_delta(out, dout, delta, hkv)
+    ops.attn_bwd_delta(out if out_f32 is None else out_f32, dout, delta, hkv)
     dq_t = dq if (dq is not None and dq.stride() == dout.stride()) else torch.empty_like(dout)
     dk_t = dk if (dk is not None and dk.is_contiguous()) else torch.empty(
         k.shape, dtype=torch.bfloat16, device=k.device)
@@ -89,17 +95,17 @@ class _HipBlockAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, causal, scale):
         q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-        out, lse = block_forward(q, k, v, scale, causal)
-        ctx.save_for_backward(q, k, v, out, lse)
+        out, lse, out32 = block_forward(q, k, v, scale, causal, keep_f32=True)
+        ctx.save_for_backward(q, k, v, out, lse, out32)
         ctx.causal, ctx.scale = causal, scale
         ctx.mark_non_differentiable(lse)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, _dlse):
-        q, k, v, out, lse = ctx.saved_tensors
+        q, k, v, out, lse, out32 = ctx.saved_tensors
         dq, dk, dv, _ = block_backward(_kernel_ready(dout), q, k, v, out, lse, ctx.scale,
-                                       ctx.causal)
+                                       ctx.causal, out_f32=out32)
         return dq, dk, dv, None, None
 
 

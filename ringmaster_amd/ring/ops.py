@@ -144,14 +144,20 @@ def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int) -> None:
 
 
 def attn_bwd_delta(out: torch.Tensor, dout: torch.Tensor, delta: torch.Tensor, hkv: int) -> None:
-    """delta[b, h, s] = sum_d dout * out (fp32). out/dout: [b, s, h, d] bf16 with equal strides."""
-    batch, sq, hq, d = out.shape
-    if dout.shape != out.shape or dout.stride() != out.stride():
-        raise ValueError("out and dout must share shape and strides")
-    job = FwdJob(q=out, k=out[:, :0, :hkv], v=out[:, :0, :hkv], out=out, lse=delta)
+    """delta[b, h, s] = sum_d dout * out (fp32). dout: [b, s, h, d] bf16; out: bf16 with the
+    strides of dout, or the fp32 final out (any strides with a contiguous dim)."""
+    batch, sq, hq, d = dout.shape
+    if out.shape != dout.shape:
+        raise ValueError("out and dout must share their shape")
+    f32 = out.dtype == torch.float32
+    if not f32 and out.stride() != dout.stride():
+        raise ValueError("bf16 out and dout must share strides")
+    job = FwdJob(q=dout, k=dout[:, :0, :hkv], v=dout[:, :0, :hkv], out=dout, lse=delta,
+                 acc_out=out if f32 else None)
     lay = _fill_layout([job], batch, hq, hkv, d, 1.0, abi.MASK_FULL)
-    abi.check(abi.lib().rmx_attn_bwd_delta(ctypes.byref(lay), out.data_ptr(), dout.data_ptr(),
-                                           delta.data_ptr(), sq, abi.stream_of(out)))
+    abi.check(abi.lib().rmx_attn_bwd_delta(ctypes.byref(lay), out.data_ptr(), int(f32),
+                                           dout.data_ptr(), delta.data_ptr(), sq,
+                                           abi.stream_of(dout)))
 
 
 def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int) -> None:

@@ -127,16 +127,18 @@ _NO_TIMER = _NoTimer()
 
 def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=None):
     """Emulated zigzag ring forward. q/k/v: [P, b, H, L, d] bf16 (interface layout per rank).
-    Returns (out [P, b, L, H, d] bf16, lse [P, b, H, L] fp32)."""
+    Returns (out [P, b, L, H, d] bf16, lse [P, b, H, L] fp32, out32 [P, b, L, H, d] fp32):
+    ``out32`` is the running fp32 accumulator, which the last touch of every row leaves
+    holding the final merged out (the backward's delta is computed from it)."""
     timer = timer or _NO_TIMER
     c = _Ctx(q, k, scale, doc)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)  # [P, b, L, H, d] views
     dev = q.device
     out = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.bfloat16, device=dev)
     lse = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
-    acc = acc_lse = None
+    acc = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.float32, device=dev)
+    acc_lse = None
     if c.P > 1:
-        acc = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.float32, device=dev)
         acc_lse = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
     for s, blocks in enumerate(zigzag_schedule(c.P, c.L, split_final=True)):
         jobs = []
@@ -147,26 +149,29 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
                 q=qd[r][:, qs], k=kd[kr][:, ks], v=vd[kr][:, ks],
                 mode=_fwd_mode(bl.first, bl.last),
                 out=out[r][:, qs], lse=lse[r][:, :, qs],
-                acc_out=None if acc is None else acc[r][:, qs],
+                acc_out=acc[r][:, qs],
                 acc_lse=None if acc_lse is None else acc_lse[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
                 doc=c.doc))
         with timer("attn_fwd"):
             ops.attn_fwd(jobs, scale=scale, mask=c.mask(s))
-    return out, lse
+    return out, lse, acc
 
 
 def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | None = None,
                   timer=None):
-    """Reverse-ring backward with the global out/lse. dout/out: [P, b, L, H, d] bf16.
+    """Reverse-ring backward with the global out/lse. dout: [P, b, L, H, d] bf16; out: the
+    global out, fp32 (the forward's ``out32``) or bf16, [P, b, L, H, d].
     Returns fp32 (dq [P, b, L, Hq, d], dk, dv [P, b, L, Hkv, d]). Each step launches the
     KV-major dK/dV kernel and the Q-major dQ kernel over all ranks."""
     timer = timer or _NO_TIMER
     c = _Ctx(q, k, scale, doc)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)
     dev = q.device
-    if dout.stride() != out.stride():
-        dout = torch.empty_like(out).copy_(dout)
+    if not dout.is_contiguous():
+        dout = dout.contiguous()
+    if not out.is_contiguous():
+        out = out.contiguous()
     delta = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
     flat = (c.P * c.b, c.L, c.hq, c.d)
     with timer("attn_bwd_delta"):
@@ -200,15 +205,15 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
 class EmulatedZigzagRing(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, scale, doc, timer):
-        out, lse = ring_forward(q, k, v, scale, doc, timer)
-        ctx.save_for_backward(q, k, v, out, lse)
+        out, lse, out32 = ring_forward(q, k, v, scale, doc, timer)
+        ctx.save_for_backward(q, k, v, out32, lse)
         ctx.scale, ctx.doc, ctx.timer = scale, doc, timer
         return out
 
     @staticmethod
     def backward(ctx, d_out):
-        q, k, v, out, lse = ctx.saved_tensors
-        dq, dk, dv = ring_backward(d_out, q, k, v, out, lse, ctx.scale, ctx.doc, ctx.timer)
+        q, k, v, out32, lse = ctx.saved_tensors
+        dq, dk, dv = ring_backward(d_out, q, k, v, out32, lse, ctx.scale, ctx.doc, ctx.timer)
         # fp32 accumulators -> q.dtype, returned in the interface layout [P, b, H, L, d]
         return (dq.to(q.dtype).transpose(2, 3), dk.to(k.dtype).transpose(2, 3),
                 dv.to(v.dtype).transpose(2, 3), None, None, None)

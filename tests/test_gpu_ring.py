@@ -84,8 +84,11 @@ def test_ring_lse_matches_oracle():
     qs, qd, _ = _stack_interface(qf, world, half)
     ks, kd, _ = _stack_interface(kf, world, half)
     vs, vd, _ = _stack_interface(vf, world, half)
-    out, lse = ring_forward(qd, kd, vd, d ** -0.5)
+    out, lse, out32 = ring_forward(qd, kd, vd, d ** -0.5)
     torch.cuda.synchronize()
-    _, ref_lse = rm.zigzag_ring_forward(qs, ks, vs)
+    ref_out, ref_lse = rm.zigzag_ring_forward(qs, ks, vs)
     for r in range(world):
         assert_f32_rel(lse[r], ref_lse[r], f"lse rank {r}")
+        # the fp32 out the backward's delta reads is the merged out before bf16 rounding
+        assert_bf16_close(out32[r], ref_out[r], f"fp32 out rank {r}")
+        assert torch.equal(out32[r].to(torch.bfloat16), out[r]), f"bf16(out32) != out rank {r}"
