@@ -66,6 +66,16 @@ int check_bf16(const void* p, const char* name) {
   return RMX_OK;
 }
 
+// The attention kernels address one (batch, head) slice of a tensor with 32-bit
+// byte offsets (buffer loads), up to one tile past the last row.
+int check_span(int64_t rows, int64_t stride_elems, const char* name) {
+  const int64_t bytes = (rows + 512) * stride_elems * 2;
+  if (bytes >= ((int64_t)1 << 31))
+    return fail(RMX_EINVAL, "%s: a (batch, head) slice spans %lld bytes (limit 2 GiB)", name,
+                (long long)bytes);
+  return RMX_OK;
+}
+
 int check_doc(const rmx_attn_layout* L, const int32_t* qg, const int32_t* kg, const int32_t* doc) {
   if (L->mask != RMX_MASK_DOC) return RMX_OK;
   if (!qg || !kg || !doc) return fail(RMX_EINVAL, "RMX_MASK_DOC needs q_gidx, k_gidx and doc");
@@ -91,9 +101,12 @@ int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* probl
     if (p.sq < 0 || p.sk < 0) return fail(RMX_EINVAL, "problem %d: negative length", i);
     if (p.sq == 0) continue;
     if ((rc = check_bf16(p.q, "q"))) return rc;
+    if ((rc = check_span(p.sq, layout->q_ss, "q"))) return rc;
     if (p.sk > 0) {
       if ((rc = check_bf16(p.k, "k"))) return rc;
       if ((rc = check_bf16(p.v, "v"))) return rc;
+      if ((rc = check_span(p.sk, layout->k_ss, "k"))) return rc;
+      if ((rc = check_span(p.sk, layout->v_ss, "v"))) return rc;
     }
     if ((rc = check_doc(layout, p.q_gidx, p.k_gidx, p.doc))) return rc;
     switch (p.mode) {
@@ -151,6 +164,10 @@ int32_t rmx_attn_bwd(const rmx_attn_layout* layout, const rmx_bwd_problem* probl
     if ((rc = check_bf16(p.k, "k"))) return rc;
     if ((rc = check_bf16(p.v, "v"))) return rc;
     if ((rc = check_bf16(p.dout, "dout"))) return rc;
+    if ((rc = check_span(p.sq, layout->q_ss, "q"))) return rc;
+    if ((rc = check_span(p.sq, layout->o_ss, "dout"))) return rc;
+    if ((rc = check_span(p.sk, layout->k_ss, "k"))) return rc;
+    if ((rc = check_span(p.sk, layout->v_ss, "v"))) return rc;
     if (!p.lse || !p.delta) return fail(RMX_EINVAL, "problem %d: lse and delta are required", i);
     if ((rc = check_doc(layout, p.q_gidx, p.k_gidx, p.doc))) return rc;
     const int modes[2] = {p.dq_mode, p.dkv_mode};

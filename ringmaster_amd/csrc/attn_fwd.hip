@@ -7,15 +7,23 @@
 // merge `update_out_and_lse` / `_merge_full` / `_merge_slice`
 // (ring/merge.py:20-31, ring/zigzag.py:49-67).
 //
-// Formulation (per wave, 32*NB queries):
-//   S^T = K Q^T   (A = K rows from LDS, sigma-permuted; B = Q held in VGPRs)
-//   online softmax per lane (each lane owns one query column, the two lane
-//   halves split the keys; one cross-half max per tile)
-//   O^T += V^T P^T  (A = V^T from a transposed LDS tile, B = P straight from
-//   the S^T accumulator registers, converted to bf16)
-// so every row statistic is lane-local and P never touches LDS.
+// Work decomposition: one workgroup = 8 waves = 256 queries of one
+// (problem, batch, head); each wave owns 32 queries and walks the key tiles
+// (64 keys) that the mask leaves, two waves per SIMD so one wave's softmax
+// overlaps the other's MFMAs.
+//
+// Per key tile and wave (v_mfma_f32_32x32x16_bf16):
+//   S^T = K Q^T    A = K rows from LDS (rows sigma-permuted, see rmx_common.h),
+//                  B = Q held in VGPRs for the whole loop       (16 MFMAs)
+//   online softmax per lane (a lane owns one query; the two lane halves split
+//   the keys, one cross-half max per tile); the running max is only moved when
+//   a tile raises it by more than 2^8, so the O rescale is rare
+//   O^T += V^T P^T A = V^T read with ds_read_b64_tr_b16 from the row-major V
+//                  tile, B = P straight from the S^T registers     (16 MFMAs)
+// K/V tiles: buffer loads (rows past the end read as zeros) staged through
+// registers into double-buffered LDS tiles whose row padding makes both the
+// 16-byte row reads and the transposed reads bank-conflict free.
 #include "rmx_kernels.h"
-#include "tile_io.h"
 
 namespace rmx {
 
@@ -29,17 +37,31 @@ struct FwdParams {
   float scale_log2;
 };
 
-template <int HD, int NW, int NB>
-__global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(const FwdParams prm) {
-  constexpr int BK = 64;
-  constexpr int QW = 32 * NB;
-  constexpr int BQ = QW * NW;
-  constexpr int NKB = HD / 16;
-  constexpr int NDB = HD / 32;
-  constexpr int NT = NW * 64;
+template <int HD>
+struct FwdCfg {
+  static constexpr int NW = 8;                // waves per workgroup
+  static constexpr int NT = NW * 64;
+  static constexpr int BQ = 32 * NW;          // queries per workgroup
+  static constexpr int BK = 64;               // keys per tile
+  static constexpr int CH = HD / 8;           // 16-byte chunks per row
+  static constexpr int RSK = HD * 2 + 16;     // LDS row stride (bytes) of the K tile
+  static constexpr int RSV = HD * 2 + 64;     // LDS row stride (bytes) of the V tile
+  static constexpr int KT = BK * RSK;
+  static constexpr int VT = BK * RSV;
+  static constexpr int LPT = BK * CH / NT;    // 16-byte chunks per thread per tile
+  static constexpr int NKB = HD / 16;         // k-steps of S^T
+  static constexpr int NDB = HD / 32;         // 32-row blocks of O^T
+  static_assert(LPT >= 1 && BK * CH % NT == 0, "tile split");
+};
 
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][BK * HD];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][HD * BK];
+constexpr float kRescaleSlack = 8.0f;  // log2 units: P <= 2^8 between rescales
+
+template <int HD>
+__global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
+  using C = FwdCfg<HD>;
+  constexpr int BK = C::BK, NKB = C::NKB, NDB = C::NDB, CH = C::CH, LPT = C::LPT;
+
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * (C::KT + C::VT)];
   __shared__ int sKg[2][BK];
   __shared__ int sKd[2][BK];
   __shared__ int sRange[2];
@@ -58,32 +80,31 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(const FwdParams pr
   const int kvh = head / (L.hq / L.hkv);
   const int sq = P.sq, sk = P.sk;
   const int mask = L.mask;
-  const int q0 = qt * BQ;
+  const int q0 = qt * C::BQ;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int qw0 = q0 + 32 * wave;  // first query of this wave
+  const int q = qw0 + l32;         // this lane's query
 
   // ---- Q operand (B of S^T = K Q^T): lane holds Q[q][16kb + 8hl .. +7]
-  bf16x8 qreg[NB][NKB];
-  int qg[NB], qd[NB];
+  bf16x8 qreg[NKB];
+  {
+    const uint16_t* qb = P.q + bb * L.q_sb + head * L.q_sh;
+    const i32x4 rs = make_rsrc(qb, span_bytes(sq, 2 * L.q_ss, HD * 2));
+    const int off = q * (int)(2 * L.q_ss) + 16 * hl;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int q = q0 + wave * QW + nb * 32 + l32;
-    const uint16_t* qp = P.q + bb * L.q_sb + (int64_t)(q < sq ? q : 0) * L.q_ss + head * L.q_sh + 8 * hl;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-      qreg[nb][kb] = q < sq ? __builtin_bit_cast(bf16x8, ld16(qp + 16 * kb)) : zero_bf16x8();
-    qg[nb] = -2147483647;
-    qd[nb] = -1;
-    if (mask == RMX_MASK_DOC && q < sq) {
-      qg[nb] = P.q_gidx[q];
-      qd[nb] = P.doc[qg[nb]];
-    }
+    for (int kb = 0; kb < NKB; ++kb) qreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(rs, off + 32 * kb));
+  }
+  int qg = -2147483647, qd = -1;
+  if (mask == RMX_MASK_DOC && q < sq) {
+    qg = P.q_gidx[q];
+    qd = P.doc[qg];
   }
 
-  // ---- key tile range
+  // ---- key tile range of the workgroup
   const int off = sk - sq;
-  const int qlast = (q0 + BQ < sq ? q0 + BQ : sq) - 1;
+  const int qlast = (q0 + C::BQ < sq ? q0 + C::BQ : sq) - 1;
   const int nkt = (sk + BK - 1) / BK;
   int kt_begin = 0, kt_end = nkt;
   int qg_first = 0, qg_last = 0, qd_first = 0, qd_last = 0;
@@ -101,11 +122,11 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(const FwdParams pr
     }
     __syncthreads();
     int lo = nkt, hi = -1;
-    for (int t = tid; t < nkt; t += NT) {
-      const int ka = t * BK, kb = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
-      const int kga = P.k_gidx[ka], kgb = P.k_gidx[kb];
-      const int kda = P.doc[kga], kdb = P.doc[kgb];
-      if (kga <= qg_last && kdb >= qd_first && kda <= qd_last) {
+    for (int t = tid; t < nkt; t += C::NT) {
+      const int ka = t * BK, kz = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
+      const int kga = P.k_gidx[ka], kgz = P.k_gidx[kz];
+      const int kda = P.doc[kga], kdz = P.doc[kgz];
+      if (kga <= qg_last && kdz >= qd_first && kda <= qd_last) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
       }
@@ -117,35 +138,66 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(const FwdParams pr
     kt_end = sRange[1] + 1;
     if (kt_end < kt_begin) kt_end = kt_begin;
   }
+  // last key this wave can attend (causal): tiles past it are skipped by the wave
+  const int wave_qlast = (qw0 + 31 < sq ? qw0 + 31 : sq - 1);
+  const int wave_kmax = mask == RMX_MASK_CAUSAL ? wave_qlast + off : 2147483647;
 
-  const uint16_t* kbase = P.k + bb * L.k_sb + kvh * L.k_sh;
-  const uint16_t* vbase = P.v + bb * L.v_sb + kvh * L.v_sh;
-
-  f32x16 o[NB][NDB];
+  // ---- K/V staging: buffer resources over this (batch, kv head)
+  const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
+  const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, HD * 2));
+  const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, HD * 2));
+  u32x4 kst[LPT], vst[LPT];
+  auto stage_load = [&](int k0) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
+    for (int i = 0; i < LPT; ++i) {
+      const int cid = tid + i * C::NT, row = cid / CH, c = cid % CH;
+      kst[i] = buf_load16(krs, (k0 + row) * kss + 16 * c);
+      vst[i] = buf_load16(vrs, (k0 + row) * vss + 16 * c);
+    }
+  };
+  auto stage_store = [&](int buf) {
+    uint8_t* kt = smem + buf * (C::KT + C::VT);
+    uint8_t* vt = kt + C::KT;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) o[nb][db] = zero16();
-  float m_run[NB], l_run[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    m_run[nb] = kNegInf;
-    l_run[nb] = 0.f;
-  }
-
-  TileIO<HD, NT> tk, tv;
-  if (kt_begin < kt_end) {
-    const int k0 = kt_begin * BK;
-    tk.load(kbase + (int64_t)k0 * L.k_ss, L.k_ss, sk - k0, tid);
-    tv.load(vbase + (int64_t)k0 * L.v_ss, L.v_ss, sk - k0, tid);
-    tk.store_rows(sK[0], tid);
-    tv.store_t(sV[0], tid);
+    for (int i = 0; i < LPT; ++i) {
+      const int cid = tid + i * C::NT, row = cid / CH, c = cid % CH;
+      *reinterpret_cast<u32x4*>(kt + row * C::RSK + 16 * c) = kst[i];
+      *reinterpret_cast<u32x4*>(vt + row * C::RSV + 16 * c) = vst[i];
+    }
+  };
+  int nkg = 0, nkd = 0;
+  auto doc_load = [&](int k0) {
     if (mask == RMX_MASK_DOC && tid < BK) {
       const int kk = k0 + tid < sk ? k0 + tid : sk - 1;
-      const int g = P.k_gidx[kk];
-      sKg[0][tid] = g;
-      sKd[0][tid] = P.doc[g];
+      nkg = P.k_gidx[kk];
+      nkd = P.doc[nkg];
     }
+  };
+  auto doc_store = [&](int buf) {
+    if (mask == RMX_MASK_DOC && tid < BK) {
+      sKg[buf][tid] = nkg;
+      sKd[buf][tid] = nkd;
+    }
+  };
+
+  // per-lane LDS byte offsets of the operand reads
+  // K rows (A of S^T): row 32mb + sigma(l32), chunk 2kb + hl
+  const int k_lane = sigma(l32) * C::RSK + 16 * hl;
+  // V^T via transposed reads: key row 16kb2 + 8hl + 4t + (m >> 2),
+  // column 32db + 16x + 4(m & 3), m = lane & 15, x = (lane >> 4) & 1
+  const int m16 = lane & 15, x16 = (lane >> 4) & 1;
+  const int v_lane = (8 * hl + (m16 >> 2)) * C::RSV + 2 * (16 * x16 + 4 * (m16 & 3));
+
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = zero16();
+  float m_run = kNegInf, l_run = 0.f;
+
+  if (kt_begin < kt_end) {
+    stage_load(kt_begin * BK);
+    doc_load(kt_begin * BK);
+    stage_store(0);
+    doc_store(0);
   }
   __syncthreads();
 
@@ -154,49 +206,37 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(const FwdParams pr
     const int buf = (kt - kt_begin) & 1;
     const int k0 = kt * BK;
     const bool has_next = kt + 1 < kt_end;
-    int nkg = 0, nkd = 0;
     if (has_next) {
-      const int k1 = k0 + BK;
-      tk.load(kbase + (int64_t)k1 * L.k_ss, L.k_ss, sk - k1, tid);
-      tv.load(vbase + (int64_t)k1 * L.v_ss, L.v_ss, sk - k1, tid);
-      if (mask == RMX_MASK_DOC && tid < BK) {
-        const int kk = k1 + tid < sk ? k1 + tid : sk - 1;
-        nkg = P.k_gidx[kk];
-        nkd = P.doc[nkg];
-      }
+      stage_load(k0 + BK);
+      doc_load(k0 + BK);
     }
+    const uint8_t* kt_lds = smem + buf * (C::KT + C::VT);
+    const uint8_t* vt_lds = kt_lds + C::KT;
 
-    // ---- S^T = K Q^T
-    f32x16 s[NB][2];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      s[nb][0] = zero16();
-      s[nb][1] = zero16();
-    }
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const int row = sigma(l32) + 32 * mb;
+    if (k0 <= wave_kmax) {
+      bool need_mask = (k0 + BK > sk);
+      if (mask == RMX_MASK_CAUSAL) need_mask |= (k0 + BK - 1 > qw0 + off);
+      if (mask == RMX_MASK_DOC) {
+        const int kgz = sKg[buf][BK - 1];
+        const int kda = sKd[buf][0], kdz = sKd[buf][BK - 1];
+        need_mask |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first);
+      }
+
+      // ---- S^T = K Q^T
+      f32x16 s[2];
+      s[0] = zero16();
+      s[1] = zero16();
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
-        const bf16x8 a = lds_row_operand(sK[buf], HD, row, 2 * kb + hl);
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) s[nb][mb] = mfma32(a, qreg[nb][kb], s[nb][mb]);
+        for (int mb = 0; mb < 2; ++mb) {
+          const bf16x8 a = __builtin_bit_cast(
+              bf16x8, *reinterpret_cast<const u32x4*>(kt_lds + k_lane + mb * 32 * C::RSK + 32 * kb));
+          s[mb] = mfma32(a, qreg[kb], s[mb]);
+        }
       }
-    }
 
-    // ---- masking (only on tiles that need it)
-    bool need_mask = (k0 + BK > sk);
-    if (mask == RMX_MASK_CAUSAL) need_mask |= (k0 + BK - 1 > q0 + off);
-    if (mask == RMX_MASK_DOC) {
-      const int kga = sKg[buf][0], kgb = sKg[buf][BK - 1];
-      const int kda = sKd[buf][0], kdb = sKd[buf][BK - 1];
-      need_mask |= !(kda == kdb && kda == qd_first && qd_first == qd_last && kgb <= qg_first);
-      (void)kga;
-    }
-    if (need_mask) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int q = q0 + wave * QW + nb * 32 + l32;
+      if (need_mask) {
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -204,136 +244,129 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(const FwdParams pr
             const int kl = 32 * mb + sig_row(hl, r);
             const int key = k0 + kl;
             bool ok = key < sk;
-            if (mask == RMX_MASK_CAUSAL) ok = ok && (key <= q + off);
-            if (mask == RMX_MASK_DOC) ok = ok && (sKd[buf][kl] == qd[nb]) && (sKg[buf][kl] <= qg[nb]);
-            if (!ok) s[nb][mb][r] = kNegInf;
+            if (mask == RMX_MASK_CAUSAL) ok &= key <= q + off;
+            if (mask == RMX_MASK_DOC) {
+              const int kd = sKd[buf][kl], kg = sKg[buf][kl];
+              ok &= (kd == qd) & (kg <= qg);
+            }
+            s[mb][r] = ok ? s[mb][r] : kNegInf;
           }
       }
-    }
 
-    // ---- online softmax (log2 domain, scale folded into the exponent FMA)
-    bf16x8 pb[NB][4];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
+      // ---- online softmax (log2 domain, scale folded into the exponent FMA)
       float mx = kNegInf;
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[nb][mb][r]);
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[mb][r]);
       mx = fmaxf(mx, xhalf(mx)) * c;
-      const float mnew = fmaxf(m_run[nb], mx);
-      const float mbase = (mnew == kNegInf) ? 0.f : mnew;
-      const float alpha = fast_exp2(m_run[nb] - mbase);
-      float rs = 0.f;
+      // move the running max only when this tile raises it by more than the
+      // slack (or on the first finite tile); otherwise keep the stale max
+      const bool raise = mx > m_run + kRescaleSlack;
+      if (__any(raise)) {
+        const float mnew = fmaxf(m_run, mx);
+        const float alpha = (m_run == kNegInf) ? 0.f : fast_exp2(m_run - mnew);
+        l_run *= alpha;
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = fast_exp2(fmaf(s[nb][mb][r], c, -mbase));
-          s[nb][mb][r] = pv;
-          rs += pv;
-        }
-      l_run[nb] = l_run[nb] * alpha + rs;
-      m_run[nb] = mnew;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) o[nb][db] *= alpha;
-#pragma unroll
-      for (int kb2 = 0; kb2 < 4; ++kb2) {
-        const f32x16& t = s[nb][kb2 >> 1];
-        const int b8 = 8 * (kb2 & 1);
-        pb[nb][kb2] = pack8(t[b8 + 0], t[b8 + 1], t[b8 + 2], t[b8 + 3], t[b8 + 4], t[b8 + 5],
-                            t[b8 + 6], t[b8 + 7]);
+        for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+        m_run = mnew;
       }
-    }
-
-    // ---- O^T += V^T P^T
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int d = 32 * db + l32;
+      const float mbase = (m_run == kNegInf) ? 0.f : m_run;
+      float rs = 0.f;
+      bf16x8 pb[4];
 #pragma unroll
       for (int kb2 = 0; kb2 < 4; ++kb2) {
-        const bf16x8 a = lds_t_operand(sV[buf], d, 2 * kb2 + hl);
+        float pv[8];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) o[nb][db] = mfma32(a, pb[nb][kb2], o[nb][db]);
+        for (int i = 0; i < 8; ++i) {
+          pv[i] = fast_exp2(fmaf(s[kb2 >> 1][8 * (kb2 & 1) + i], c, -mbase));
+          rs += pv[i];
+        }
+        pb[kb2] = pack8_hw(pv);
+      }
+      l_run += rs;
+
+      // ---- O^T += V^T P^T
+#pragma unroll
+      for (int kb2 = 0; kb2 < 4; ++kb2) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const uint16_t* vp = reinterpret_cast<const uint16_t*>(
+              vt_lds + v_lane + 16 * kb2 * C::RSV + 64 * db);
+          const bf16x8 a = join_bf16x8(lds_read_tr(vp), lds_read_tr(vp + 2 * C::RSV));
+          o[db] = mfma32(a, pb[kb2], o[db]);
+        }
       }
     }
 
     if (has_next) {
-      tk.store_rows(sK[buf ^ 1], tid);
-      tv.store_t(sV[buf ^ 1], tid);
-      if (mask == RMX_MASK_DOC && tid < BK) {
-        sKg[buf ^ 1][tid] = nkg;
-        sKd[buf ^ 1][tid] = nkd;
-      }
+      stage_store(buf ^ 1);
+      doc_store(buf ^ 1);
     }
     __syncthreads();
   }
 
   // ---- epilogue: normalise, lse, merge
+  const float lt = l_run + xhalf(l_run);
+  if (q >= sq) return;
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  const float lse_b = lt > 0.f ? (m_run + fast_log2(lt)) * kLn2 : kNegInf;
+  const int64_t lrow = bb * L.l_sb + head * L.l_sh + q;
+  float wa = 0.f, wb = 1.f, lnew = lse_b;
+  if (P.mode == RMX_FWD_ACC_MERGE || P.mode == RMX_FWD_ACC_FINAL) {
+    const float la = P.acc_lse[lrow];
+    const float mxl = fmaxf(la, lse_b);
+    if (mxl == kNegInf) {
+      lnew = kNegInf;
+      wa = 0.f;
+      wb = 0.f;
+    } else {
+      const float mnl = fminf(la, lse_b);
+      lnew = mxl + fast_log2(1.f + fast_exp2((mnl - mxl) * kLog2e)) * kLn2;
+      wa = fast_exp2((la - lnew) * kLog2e);
+      wb = fast_exp2((lse_b - lnew) * kLog2e);
+    }
+  }
+  wb *= inv;
+  float* accrow = P.acc_out ? P.acc_out + bb * L.a_sb + (int64_t)q * L.a_ss + head * L.a_sh : nullptr;
+  uint16_t* orow = P.out ? P.out + bb * L.o_sb + (int64_t)q * L.o_ss + head * L.o_sh : nullptr;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const float lt = l_run[nb] + xhalf(l_run[nb]);
-    const int q = q0 + wave * QW + nb * 32 + l32;
-    if (q >= sq) continue;
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    const float lse_b = lt > 0.f ? (m_run[nb] + fast_log2(lt)) * kLn2 : kNegInf;
-    const int64_t lrow = bb * L.l_sb + head * L.l_sh + q;
-    float wa = 0.f, wb = 1.f, lnew = lse_b;
-    if (P.mode == RMX_FWD_ACC_MERGE || P.mode == RMX_FWD_ACC_FINAL) {
-      const float la = P.acc_lse[lrow];
-      const float mx = fmaxf(la, lse_b);
-      if (mx == kNegInf) {
-        lnew = kNegInf;
-        wa = 0.f;
-        wb = 0.f;
-      } else {
-        const float mn = fminf(la, lse_b);
-        lnew = mx + fast_log2(1.f + fast_exp2((mn - mx) * kLog2e)) * kLn2;
-        wa = fast_exp2((la - lnew) * kLog2e);
-        wb = fast_exp2((lse_b - lnew) * kLog2e);
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d0 = 32 * db + 8 * j + 4 * hl;
+      f32x4 v;
+      v[0] = o[db][4 * j + 0] * wb;
+      v[1] = o[db][4 * j + 1] * wb;
+      v[2] = o[db][4 * j + 2] * wb;
+      v[3] = o[db][4 * j + 3] * wb;
+      if (P.mode == RMX_FWD_ACC_MERGE || P.mode == RMX_FWD_ACC_FINAL) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(accrow + d0);
+        v += a * wa;
+      }
+      // every mode leaves the fp32 result in acc_out when it is given (WRITE and
+      // ACC_FINAL: the final out in fp32, which the backward's delta reads)
+      if (accrow) *reinterpret_cast<f32x4*>(accrow + d0) = v;
+      if (P.mode == RMX_FWD_WRITE || P.mode == RMX_FWD_ACC_FINAL) {
+        u32x2 w;
+        w[0] = cvt_pk_bf16(v[0], v[1]);
+        w[1] = cvt_pk_bf16(v[2], v[3]);
+        *reinterpret_cast<u32x2*>(orow + d0) = w;
       }
     }
-    wb *= inv;
-    float* accrow = P.acc_out ? P.acc_out + bb * L.a_sb + (int64_t)q * L.a_ss + head * L.a_sh : nullptr;
-    uint16_t* orow = P.out ? P.out + bb * L.o_sb + (int64_t)q * L.o_ss + head * L.o_sh : nullptr;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = 32 * db + 8 * j + 4 * hl;
-        f32x4 v;
-        v[0] = o[nb][db][4 * j + 0] * wb;
-        v[1] = o[nb][db][4 * j + 1] * wb;
-        v[2] = o[nb][db][4 * j + 2] * wb;
-        v[3] = o[nb][db][4 * j + 3] * wb;
-        if (P.mode == RMX_FWD_ACC_MERGE || P.mode == RMX_FWD_ACC_FINAL) {
-          const f32x4 a = *reinterpret_cast<const f32x4*>(accrow + d0);
-          v += a * wa;
-        }
-        // every mode leaves the fp32 result in acc_out when it is given (WRITE and
-        // ACC_FINAL: the final out in fp32, which the backward's delta reads)
-        if (accrow) *reinterpret_cast<f32x4*>(accrow + d0) = v;
-        if (P.mode == RMX_FWD_WRITE || P.mode == RMX_FWD_ACC_FINAL) {
-          u32x2 w;
-          w[0] = pack_bf2(v[0], v[1]);
-          w[1] = pack_bf2(v[2], v[3]);
-          *reinterpret_cast<u32x2*>(orow + d0) = w;
-        }
-      }
-    if (hl == 0) {
-      if (P.mode == RMX_FWD_ACC_INIT || P.mode == RMX_FWD_ACC_MERGE) {
-        P.acc_lse[lrow] = lnew;
-      } else if (P.lse) {
-        P.lse[lrow] = lnew;
-      }
+  if (hl == 0) {
+    if (P.mode == RMX_FWD_ACC_INIT || P.mode == RMX_FWD_ACC_MERGE) {
+      P.acc_lse[lrow] = lnew;
+    } else if (P.lse) {
+      P.lse[lrow] = lnew;
     }
   }
 }
 
-template <int HD, int NW, int NB>
+template <int HD>
 static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                                hipStream_t stream) {
-  constexpr int BQ = 32 * NB * NW;
+  constexpr int BQ = FwdCfg<HD>::BQ;
   FwdParams prm;
   prm.L = L;
   prm.nprob = n;
@@ -349,14 +382,14 @@ static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* 
   prm.total = tot;
   if (tot == 0) return hipSuccess;
   const int grid = (tot + 7) / 8 * 8;
-  hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, NB>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+  hipLaunchKernelGGL((attn_fwd_kernel<HD>), dim3(grid), dim3(FwdCfg<HD>::NT), 0, stream, prm);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_fwd(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                            hipStream_t stream) {
-  if (L.head_dim == 128) return launch_fwd_t<128, 4, 1>(L, probs, n, stream);
-  return launch_fwd_t<64, 4, 1>(L, probs, n, stream);
+  if (L.head_dim == 128) return launch_fwd_t<128>(L, probs, n, stream);
+  return launch_fwd_t<64>(L, probs, n, stream);
 }
 
 }  // namespace rmx

@@ -107,3 +107,76 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
 }
 
 }  // namespace rmx
+
+namespace rmx {
+
+// ---------------------------------------------------------------------------
+// Buffer-resource loads. A raw buffer (stride 0) returns zeros for any 16-byte
+// access whose offset lies at or past num_records, so tiles that run over the
+// end of a sequence need no branches and can never read out of bounds.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ u32x4 llvm_raw_buffer_load_v4(i32x4 rsrc, int voffset, int soffset,
+                                         int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+
+// Word 3 = 0x00020000: 32-bit data format, no swizzle/stride (gfx9 family).
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t num_bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = (int32_t)(uint32_t)a;
+  r[1] = (int32_t)((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = (int32_t)num_bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+
+__device__ __forceinline__ u32x4 buf_load16(const i32x4& rsrc, int byte_off) {
+  return llvm_raw_buffer_load_v4(rsrc, byte_off, 0, 0);
+}
+
+// Bytes a buffer over `rows` rows of `row_bytes` at stride `stride_bytes` must cover.
+__device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride_bytes, int row_bytes) {
+  return rows <= 0 ? 0u : (uint32_t)((int64_t)(rows - 1) * stride_bytes + row_bytes);
+}
+
+// ---------------------------------------------------------------------------
+// ds_read_b64_tr_b16 (gfx950): inside each 16-lane group, lane j receives, as
+// element i (0..3), the 16-bit element (j % 4) of the 8-byte chunk addressed by
+// lane 4*i + j/4. With lane 4*i + q pointing at row (r0 + i), columns
+// (c0 + 4q .. c0 + 4q + 3) of a row-major tile, lane j gets column c0 + j of
+// rows r0 .. r0 + 3: a 4 x 16 -> 16 x 4 transpose.
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
+  const bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (__attribute__((address_space(3))) bf16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+__device__ __forceinline__ bf16x8 join_bf16x8(const u32x2& lo, const u32x2& hi) {
+  u32x4 u;
+  u[0] = lo[0];
+  u[1] = lo[1];
+  u[2] = hi[0];
+  u[3] = hi[1];
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// Hardware round-to-nearest-even packing of two floats (v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  const f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+
+__device__ __forceinline__ bf16x8 pack8_hw(const float* v) {
+  u32x4 u;
+  u[0] = cvt_pk_bf16(v[0], v[1]);
+  u[1] = cvt_pk_bf16(v[2], v[3]);
+  u[2] = cvt_pk_bf16(v[4], v[5]);
+  u[3] = cvt_pk_bf16(v[6], v[7]);
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+}  // namespace rmx
