@@ -14,7 +14,6 @@
 //     dK += dS^T Q; the workgroup owns its keys and loops over every q-head
 //     of the GQA group, so the fold needs no cross-workgroup reduction.
 #include "rmx_kernels.h"
-#include "tile_io.h"
 
 namespace rmx {
 
@@ -127,18 +126,58 @@ __device__ __forceinline__ void grad_store4(int mode, float* acc, uint16_t* bf, 
   }
 }
 
-// ---------------------------------------------------------------- dQ (Q-major)
-template <int HD, int NW>
-__global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dq_kernel(const BwdParams prm) {
-  constexpr int BK = 64;
-  constexpr int BQ = 32 * NW;
-  constexpr int NKB = HD / 16;
-  constexpr int NDB = HD / 32;
-  constexpr int NT = NW * 64;
+// ---------------------------------------------------------------- tiles
+// Q-side tiles of the dK/dV kernel (Q, dO) and the K tile of the dQ kernel are
+// read both as 16-byte rows (MFMA A operands) and with ds_read_b64_tr_b16
+// (transposed B / A operands). A row pad of 48 bytes keeps the row reads of 16
+// consecutive rows conflict free and limits the transposed reads of 4
+// consecutive rows to a partial 2-way conflict; tiles only read by rows use a
+// 16-byte pad.
+template <int HD>
+struct BwdTiles {
+  static constexpr int CH = HD / 8;
+  static constexpr int RS_RT = HD * 2 + 48;  // rows + transposed reads
+  static constexpr int RS_R = HD * 2 + 16;   // rows only
+  static constexpr int NKB = HD / 16;
+  static constexpr int NDB = HD / 32;
+};
 
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][BK * HD];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][BK * HD];
-  __shared__ __attribute__((aligned(16))) uint16_t sKt[2][HD * BK];
+// LDS byte offset, relative to a tile with row stride RS, of this lane's
+// transposed 4x16 read that yields element (row 16*kb2 + 8*hl + 4*t + i,
+// column 32*db + l32), i = 0..3; add (16*kb2 + 4*t)*RS + 64*db.
+template <int RS>
+__device__ __forceinline__ int tr_lane_off(int lane) {
+  const int hl = lane >> 5, m = lane & 15, x = (lane >> 4) & 1;
+  return (8 * hl + (m >> 2)) * RS + 2 * (16 * x + 4 * (m & 3));
+}
+
+// bf16x8 operand (k = 8*hl .. 8*hl+7 <-> tile rows 16*kb2 + 8*hl + 0..7, column
+// 32*db + l32) from two transposed reads.
+template <int RS>
+__device__ __forceinline__ bf16x8 tr_operand(const uint8_t* tile, int lane_off, int kb2, int db) {
+  const uint16_t* p = reinterpret_cast<const uint16_t*>(tile + lane_off + 16 * kb2 * RS + 64 * db);
+  return join_bf16x8(lds_read_tr(p), lds_read_tr(p + 2 * RS));
+}
+
+// ---------------------------------------------------------------- dQ (Q-major)
+// One workgroup = 8 waves x 32 queries of one (problem, batch, head). Per key
+// tile (64 keys) and wave:
+//   S^T  = K Q^T    A = K rows (LDS), B = Q (VGPRs)        16 MFMAs
+//   dP^T = V dO^T   A = V rows (LDS), B = dO (VGPRs)       16 MFMAs
+//   P = exp2(S c - lse2), dS = P (dP - delta)  (lane = query: lse/delta per lane)
+//   dQ^T += K^T dS^T  A = K^T by transposed reads of the K tile, B = dS^T
+//                                                            16 MFMAs
+template <int HD>
+__global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm) {
+  using T = BwdTiles<HD>;
+  constexpr int NW = 8, NT = NW * 64, BQ = 32 * NW, BK = 64;
+  constexpr int CH = T::CH, NKB = T::NKB, NDB = T::NDB;
+  constexpr int RSK = T::RS_RT, RSV = T::RS_R;
+  constexpr int KT = BK * RSK, VT = BK * RSV;
+  constexpr int LPT = BK * CH / NT;
+  static_assert(LPT >= 1 && BK * CH % NT == 0, "tile split");
+
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * (KT + VT)];
   __shared__ int sKg[2][BK];
   __shared__ int sKd[2][BK];
   __shared__ int sRange[2];
@@ -159,19 +198,23 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dq_kernel(const BwdParams
   const int q0 = qt * BQ;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int q = q0 + wave * 32 + l32;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int qw0 = q0 + 32 * wave;
+  const int q = qw0 + l32;
   const bool qvalid = q < sq;
 
   bf16x8 qreg[NKB], doreg[NKB];
   {
-    const int qq = qvalid ? q : 0;
-    const uint16_t* qp = P.q + bb * L.q_sb + (int64_t)qq * L.q_ss + head * L.q_sh + 8 * hl;
-    const uint16_t* dp = P.dout + bb * L.o_sb + (int64_t)qq * L.o_ss + head * L.o_sh + 8 * hl;
+    const i32x4 qrs = make_rsrc(P.q + bb * L.q_sb + head * L.q_sh,
+                                span_bytes(sq, 2 * L.q_ss, HD * 2));
+    const i32x4 ors = make_rsrc(P.dout + bb * L.o_sb + head * L.o_sh,
+                                span_bytes(sq, 2 * L.o_ss, HD * 2));
+    const int qo = q * (int)(2 * L.q_ss) + 16 * hl, oo = q * (int)(2 * L.o_ss) + 16 * hl;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      qreg[kb] = qvalid ? __builtin_bit_cast(bf16x8, ld16(qp + 16 * kb)) : zero_bf16x8();
-      doreg[kb] = qvalid ? __builtin_bit_cast(bf16x8, ld16(dp + 16 * kb)) : zero_bf16x8();
+      qreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(qrs, qo + 32 * kb));
+      doreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(ors, oo + 32 * kb));
     }
   }
   const int64_t lrow = bb * L.l_sb + head * L.l_sh + (qvalid ? q : 0);
@@ -204,10 +247,10 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dq_kernel(const BwdParams
     __syncthreads();
     int lo = nkt, hi = -1;
     for (int t = tid; t < nkt; t += NT) {
-      const int ka = t * BK, kb = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
-      const int kga = P.k_gidx[ka], kgb = P.k_gidx[kb];
-      const int kda = P.doc[kga], kdb = P.doc[kgb];
-      if (kga <= qg_last && kdb >= qd_first && kda <= qd_last) {
+      const int ka = t * BK, kz = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
+      const int kga = P.k_gidx[ka], kgz = P.k_gidx[kz];
+      const int kda = P.doc[kga], kdz = P.doc[kgz];
+      if (kga <= qg_last && kdz >= qd_first && kda <= qd_last) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
       }
@@ -219,28 +262,59 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dq_kernel(const BwdParams
     kt_end = sRange[1] + 1;
     if (kt_end < kt_begin) kt_end = kt_begin;
   }
+  const int wave_qlast = (qw0 + 31 < sq ? qw0 + 31 : sq - 1);
+  const int wave_kmax = mask == RMX_MASK_CAUSAL ? wave_qlast + off : 2147483647;
 
-  const uint16_t* kbase = P.k + bb * L.k_sb + kvh * L.k_sh;
-  const uint16_t* vbase = P.v + bb * L.v_sb + kvh * L.v_sh;
+  const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
+  const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, HD * 2));
+  const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, HD * 2));
+  u32x4 kst[LPT], vst[LPT];
+  auto stage_load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int cid = tid + i * NT, row = cid / CH, c = cid % CH;
+      kst[i] = buf_load16(krs, (k0 + row) * kss + 16 * c);
+      vst[i] = buf_load16(vrs, (k0 + row) * vss + 16 * c);
+    }
+  };
+  auto stage_store = [&](int buf) {
+    uint8_t* kt = smem + buf * (KT + VT);
+    uint8_t* vt = kt + KT;
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int cid = tid + i * NT, row = cid / CH, c = cid % CH;
+      *reinterpret_cast<u32x4*>(kt + row * RSK + 16 * c) = kst[i];
+      *reinterpret_cast<u32x4*>(vt + row * RSV + 16 * c) = vst[i];
+    }
+  };
+  int nkg = 0, nkd = 0;
+  auto doc_load = [&](int k0) {
+    if (mask == RMX_MASK_DOC && tid < BK) {
+      const int kk = k0 + tid < sk ? k0 + tid : sk - 1;
+      nkg = P.k_gidx[kk];
+      nkd = P.doc[nkg];
+    }
+  };
+  auto doc_store = [&](int buf) {
+    if (mask == RMX_MASK_DOC && tid < BK) {
+      sKg[buf][tid] = nkg;
+      sKd[buf][tid] = nkd;
+    }
+  };
+
+  const int k_lane = sigma(l32) * RSK + 16 * hl;  // K rows (A of S^T)
+  const int v_lane = sigma(l32) * RSV + 16 * hl;  // V rows (A of dP^T)
+  const int t_lane = tr_lane_off<RSK>(lane);      // K^T (A of dQ^T)
 
   f32x16 acc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) acc[db] = zero16();
 
-  TileIO<HD, NT> tk, tv;
   if (kt_begin < kt_end) {
-    const int k0 = kt_begin * BK;
-    tk.load(kbase + (int64_t)k0 * L.k_ss, L.k_ss, sk - k0, tid);
-    tv.load(vbase + (int64_t)k0 * L.v_ss, L.v_ss, sk - k0, tid);
-    tk.store_rows(sK[0], tid);
-    tk.store_t(sKt[0], tid);
-    tv.store_rows(sV[0], tid);
-    if (mask == RMX_MASK_DOC && tid < BK) {
-      const int kk = k0 + tid < sk ? k0 + tid : sk - 1;
-      const int g = P.k_gidx[kk];
-      sKg[0][tid] = g;
-      sKd[0][tid] = P.doc[g];
-    }
+    stage_load(kt_begin * BK);
+    doc_load(kt_begin * BK);
+    stage_store(0);
+    doc_store(0);
   }
   __syncthreads();
 
@@ -249,87 +323,76 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dq_kernel(const BwdParams
     const int buf = (kt - kt_begin) & 1;
     const int k0 = kt * BK;
     const bool has_next = kt + 1 < kt_end;
-    int nkg = 0, nkd = 0;
     if (has_next) {
-      const int k1 = k0 + BK;
-      tk.load(kbase + (int64_t)k1 * L.k_ss, L.k_ss, sk - k1, tid);
-      tv.load(vbase + (int64_t)k1 * L.v_ss, L.v_ss, sk - k1, tid);
-      if (mask == RMX_MASK_DOC && tid < BK) {
-        const int kk = k1 + tid < sk ? k1 + tid : sk - 1;
-        nkg = P.k_gidx[kk];
-        nkd = P.doc[nkg];
-      }
+      stage_load(k0 + BK);
+      doc_load(k0 + BK);
     }
+    const uint8_t* kt_lds = smem + buf * (KT + VT);
+    const uint8_t* vt_lds = kt_lds + KT;
 
-    f32x16 s[2], dp[2];
-    s[0] = zero16();
-    s[1] = zero16();
-    dp[0] = zero16();
-    dp[1] = zero16();
+    if (k0 <= wave_kmax) {
+      bool need_mask = (k0 + BK > sk);
+      if (mask == RMX_MASK_CAUSAL) need_mask |= (k0 + BK - 1 > qw0 + off);
+      if (mask == RMX_MASK_DOC) {
+        const int kgz = sKg[buf][BK - 1];
+        const int kda = sKd[buf][0], kdz = sKd[buf][BK - 1];
+        need_mask |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first);
+      }
+
+      f32x16 s[2], dp[2];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const int row = sigma(l32) + 32 * mb;
+      for (int mb = 0; mb < 2; ++mb) {
+        s[mb] = zero16();
+        dp[mb] = zero16();
+      }
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
-        const bf16x8 a = lds_row_operand(sK[buf], HD, row, 2 * kb + hl);
-        s[mb] = mfma32(a, qreg[kb], s[mb]);
-        const bf16x8 b = lds_row_operand(sV[buf], HD, row, 2 * kb + hl);
-        dp[mb] = mfma32(b, doreg[kb], dp[mb]);
-      }
-    }
-
-    bool need_mask = (k0 + BK > sk);
-    if (mask == RMX_MASK_CAUSAL) need_mask |= (k0 + BK - 1 > q0 + off);
-    if (mask == RMX_MASK_DOC) {
-      const int kgb = sKg[buf][BK - 1];
-      const int kda = sKd[buf][0], kdb = sKd[buf][BK - 1];
-      need_mask |= !(kda == kdb && kda == qd_first && qd_first == qd_last && kgb <= qg_first);
-    }
-
-    bf16x8 dsb[4];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = fast_exp2(fmaf(s[mb][r], c, -lse2));
-        if (need_mask) {
-          const int kl = 32 * mb + sig_row(hl, r);
-          const int key = k0 + kl;
-          bool ok = key < sk;
-          if (mask == RMX_MASK_CAUSAL) ok = ok && (key <= q + off);
-          if (mask == RMX_MASK_DOC) ok = ok && (sKd[buf][kl] == qd) && (sKg[buf][kl] <= qg);
-          if (!ok) pv = 0.f;
+        for (int mb = 0; mb < 2; ++mb) {
+          const bf16x8 a = __builtin_bit_cast(
+              bf16x8, *reinterpret_cast<const u32x4*>(kt_lds + k_lane + mb * 32 * RSK + 32 * kb));
+          s[mb] = mfma32(a, qreg[kb], s[mb]);
+          const bf16x8 b = __builtin_bit_cast(
+              bf16x8, *reinterpret_cast<const u32x4*>(vt_lds + v_lane + mb * 32 * RSV + 32 * kb));
+          dp[mb] = mfma32(b, doreg[kb], dp[mb]);
         }
-        s[mb][r] = pv * (dp[mb][r] - dlt);
       }
-    }
-#pragma unroll
-    for (int kb2 = 0; kb2 < 4; ++kb2) {
-      const f32x16& t = s[kb2 >> 1];
-      const int b8 = 8 * (kb2 & 1);
-      dsb[kb2] = pack8(t[b8 + 0], t[b8 + 1], t[b8 + 2], t[b8 + 3], t[b8 + 4], t[b8 + 5], t[b8 + 6],
-                       t[b8 + 7]);
-    }
 
-    // dQ^T += K^T dS^T
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int d = 32 * db + l32;
+      bf16x8 dsb[4];
 #pragma unroll
       for (int kb2 = 0; kb2 < 4; ++kb2) {
-        const bf16x8 a = lds_t_operand(sKt[buf], d, 2 * kb2 + hl);
-        acc[db] = mfma32(a, dsb[kb2], acc[db]);
+        const int mb = kb2 >> 1, b8 = 8 * (kb2 & 1);
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float pv = fast_exp2(fmaf(s[mb][b8 + i], c, -lse2));
+          if (need_mask) {
+            const int kl = 32 * mb + sig_row(hl, b8 + i);
+            const int key = k0 + kl;
+            bool ok = key < sk;
+            if (mask == RMX_MASK_CAUSAL) ok &= key <= q + off;
+            if (mask == RMX_MASK_DOC) {
+              const int kd = sKd[buf][kl], kg = sKg[buf][kl];
+              ok &= (kd == qd) & (kg <= qg);
+            }
+            pv = ok ? pv : 0.f;
+          }
+          v[i] = pv * (dp[mb][b8 + i] - dlt);
+        }
+        dsb[kb2] = pack8_hw(v);
       }
+
+      // dQ^T += K^T dS^T
+#pragma unroll
+      for (int kb2 = 0; kb2 < 4; ++kb2)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          acc[db] = mfma32(tr_operand<RSK>(kt_lds, t_lane, kb2, db), dsb[kb2], acc[db]);
     }
 
     if (has_next) {
-      tk.store_rows(sK[buf ^ 1], tid);
-      tk.store_t(sKt[buf ^ 1], tid);
-      tv.store_rows(sV[buf ^ 1], tid);
-      if (mask == RMX_MASK_DOC && tid < BK) {
-        sKg[buf ^ 1][tid] = nkg;
-        sKd[buf ^ 1][tid] = nkd;
-      }
+      stage_store(buf ^ 1);
+      doc_store(buf ^ 1);
     }
     __syncthreads();
   }
@@ -353,18 +416,26 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dq_kernel(const BwdParams
 }
 
 // ---------------------------------------------------------------- dK, dV (KV-major)
-template <int HD, int NW>
-__global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdParams prm) {
-  constexpr int BQ = 64;          // queries per q-tile
-  constexpr int BKV = 32 * NW;    // keys per workgroup
-  constexpr int NKB = HD / 16;
-  constexpr int NDB = HD / 32;
-  constexpr int NT = NW * 64;
+// One workgroup = 4 waves x 32 keys of one (problem, batch, kv head); it walks
+// every q-head of the GQA group and every query tile (64 queries) the mask
+// leaves, so the group fold needs no cross-workgroup reduction. Per query tile
+// and wave:
+//   S  = Q K^T     A = Q rows (LDS), B = K (VGPRs)            16 MFMAs
+//   dP = dO V^T    A = dO rows (LDS), B = V (VGPRs)           16 MFMAs
+//   P = exp2(S c - lse2[q]), dS = P (dP - delta[q])  (lse/delta from LDS)
+//   dV += P^T dO   A = P^T (registers), B = dO^T transposed reads  16 MFMAs
+//   dK += dS^T Q   A = dS^T (registers), B = Q^T transposed reads  16 MFMAs
+template <int HD>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams prm) {
+  using T = BwdTiles<HD>;
+  constexpr int NW = 4, NT = NW * 64, BKV = 32 * NW, BQ = 64;
+  constexpr int CH = T::CH, NKB = T::NKB, NDB = T::NDB;
+  constexpr int RS = T::RS_RT;
+  constexpr int QT = BQ * RS;  // bytes of one Q (or dO) tile
+  constexpr int LPT = BQ * CH / NT;
+  static_assert(LPT >= 1 && BQ * CH % NT == 0, "tile split");
 
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][BQ * HD];
-  __shared__ __attribute__((aligned(16))) uint16_t sDO[2][BQ * HD];
-  __shared__ __attribute__((aligned(16))) uint16_t sQt[2][HD * BQ];
-  __shared__ __attribute__((aligned(16))) uint16_t sDOt[2][HD * BQ];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * QT];
   __shared__ __attribute__((aligned(16))) float sL[2][BQ];
   __shared__ __attribute__((aligned(16))) float sD[2][BQ];
   __shared__ int sQg[2][BQ];
@@ -387,19 +458,23 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
   const int k0 = kt * BKV;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int key = k0 + wave * 32 + l32;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int kw0 = k0 + 32 * wave;  // first key of this wave
+  const int key = kw0 + l32;
   const bool kvalid = key < sk;
 
   bf16x8 kreg[NKB], vreg[NKB];
   {
-    const int kk = kvalid ? key : 0;
-    const uint16_t* kp = P.k + bb * L.k_sb + (int64_t)kk * L.k_ss + kvh * L.k_sh + 8 * hl;
-    const uint16_t* vp = P.v + bb * L.v_sb + (int64_t)kk * L.v_ss + kvh * L.v_sh + 8 * hl;
+    const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh,
+                                span_bytes(sk, 2 * L.k_ss, HD * 2));
+    const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh,
+                                span_bytes(sk, 2 * L.v_ss, HD * 2));
+    const int ko = key * (int)(2 * L.k_ss) + 16 * hl, vo = key * (int)(2 * L.v_ss) + 16 * hl;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      kreg[kb] = kvalid ? __builtin_bit_cast(bf16x8, ld16(kp + 16 * kb)) : zero_bf16x8();
-      vreg[kb] = kvalid ? __builtin_bit_cast(bf16x8, ld16(vp + 16 * kb)) : zero_bf16x8();
+      kreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(krs, ko + 32 * kb));
+      vreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(vrs, vo + 32 * kb));
     }
   }
   int kg = 2147483647, kd = -2;
@@ -408,7 +483,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
     kd = P.doc[kg];
   }
 
-  // ---- q-tile range
+  // ---- query-tile range of the workgroup
   const int off = sk - sq;
   const int klast = (k0 + BKV < sk ? k0 + BKV : sk) - 1;
   const int nqt = (sq + BQ - 1) / BQ;
@@ -430,10 +505,10 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
     __syncthreads();
     int lo = nqt, hi = -1;
     for (int t = tid; t < nqt; t += NT) {
-      const int qa = t * BQ, qb = (t * BQ + BQ < sq ? t * BQ + BQ : sq) - 1;
-      const int qga = P.q_gidx[qa], qgb = P.q_gidx[qb];
-      const int qda = P.doc[qga], qdb = P.doc[qgb];
-      if (qgb >= kg_first && qdb >= kd_first && qda <= kd_last) {
+      const int qa = t * BQ, qz = (t * BQ + BQ < sq ? t * BQ + BQ : sq) - 1;
+      const int qga = P.q_gidx[qa], qgz = P.q_gidx[qz];
+      const int qda = P.doc[qga], qdz = P.doc[qgz];
+      if (qgz >= kg_first && qdz >= kd_first && qda <= kd_last) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
       }
@@ -447,24 +522,25 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
   }
   const int nq_iter = qt_end - qt_begin;
   const int total_iter = nq_iter * G;
+  const int wave_klast = (kw0 + 31 < sk ? kw0 + 31 : sk - 1);
 
-  f32x16 dk[NDB], dv[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    dk[db] = zero16();
-    dv[db] = zero16();
-  }
-
-  TileIO<HD, NT> tq, tdo;
+  // ---- Q / dO staging
+  const int qss = (int)(2 * L.q_ss), oss = (int)(2 * L.o_ss);
+  u32x4 qst[LPT], ost[LPT];
   float nl = 0.f, nd = 0.f;
   int nqg = 0, nqd = 0;
   auto issue_load = [&](int it) {
     const int g = it / nq_iter;
-    const int qtile = qt_begin + it % nq_iter;
+    const int qa = (qt_begin + it % nq_iter) * BQ;
     const int qh = kvh * G + g;
-    const int qa = qtile * BQ;
-    tq.load(P.q + bb * L.q_sb + qh * L.q_sh + (int64_t)qa * L.q_ss, L.q_ss, sq - qa, tid);
-    tdo.load(P.dout + bb * L.o_sb + qh * L.o_sh + (int64_t)qa * L.o_ss, L.o_ss, sq - qa, tid);
+    const i32x4 qrs = make_rsrc(P.q + bb * L.q_sb + qh * L.q_sh, span_bytes(sq, qss, HD * 2));
+    const i32x4 ors = make_rsrc(P.dout + bb * L.o_sb + qh * L.o_sh, span_bytes(sq, oss, HD * 2));
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int cid = tid + i * NT, row = cid / CH, c = cid % CH;
+      qst[i] = buf_load16(qrs, (qa + row) * qss + 16 * c);
+      ost[i] = buf_load16(ors, (qa + row) * oss + 16 * c);
+    }
     if (tid < BQ) {
       const int qq = qa + tid;
       if (qq < sq) {
@@ -477,7 +553,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
           nqd = P.doc[nqg];
         }
       } else {
-        nl = __builtin_inff();
+        nl = __builtin_inff();  // rows past the end: P == 0
         nd = 0.f;
         nqg = -2147483647;
         nqd = -1;
@@ -485,10 +561,14 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
     }
   };
   auto commit = [&](int buf) {
-    tq.store_rows(sQ[buf], tid);
-    tq.store_t(sQt[buf], tid);
-    tdo.store_rows(sDO[buf], tid);
-    tdo.store_t(sDOt[buf], tid);
+    uint8_t* qt_l = smem + buf * 2 * QT;
+    uint8_t* ot_l = qt_l + QT;
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int cid = tid + i * NT, row = cid / CH, c = cid % CH;
+      *reinterpret_cast<u32x4*>(qt_l + row * RS + 16 * c) = qst[i];
+      *reinterpret_cast<u32x4*>(ot_l + row * RS + 16 * c) = ost[i];
+    }
     if (tid < BQ) {
       sL[buf][tid] = nl;
       sD[buf][tid] = nd;
@@ -496,6 +576,16 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
       sQd[buf][tid] = nqd;
     }
   };
+
+  const int r_lane = sigma(l32) * RS + 16 * hl;  // Q / dO rows (A of S, dP)
+  const int t_lane = tr_lane_off<RS>(lane);      // Q^T / dO^T (B of dK, dV)
+
+  f32x16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    dk[db] = zero16();
+    dv[db] = zero16();
+  }
 
   if (total_iter > 0) {
     issue_load(0);
@@ -509,85 +599,76 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
     const int qa = (qt_begin + it % nq_iter) * BQ;
     const bool has_next = it + 1 < total_iter;
     if (has_next) issue_load(it + 1);
+    const uint8_t* qt_l = smem + buf * 2 * QT;
+    const uint8_t* ot_l = qt_l + QT;
 
-    // S = Q K^T, dP = dO V^T  (rows = queries sigma-permuted, cols = this wave's keys)
-    f32x16 s[2], dp[2];
-    s[0] = zero16();
-    s[1] = zero16();
-    dp[0] = zero16();
-    dp[1] = zero16();
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const int row = sigma(l32) + 32 * mb;
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        const bf16x8 a = lds_row_operand(sQ[buf], HD, row, 2 * kb + hl);
-        s[mb] = mfma32(a, kreg[kb], s[mb]);
-        const bf16x8 b = lds_row_operand(sDO[buf], HD, row, 2 * kb + hl);
-        dp[mb] = mfma32(b, vreg[kb], dp[mb]);
+    // causal: this wave's keys are all after the tile's last query
+    const bool active = mask != RMX_MASK_CAUSAL || kw0 <= qa + BQ - 1 + off;
+    if (active) {
+      bool need_mask = (kw0 + 32 > sk);
+      if (mask == RMX_MASK_CAUSAL) need_mask |= (wave_klast > qa + off);
+      if (mask == RMX_MASK_DOC) {
+        const int qga = sQg[buf][0];
+        const int qda = sQd[buf][0];
+        const int qz = (qa + BQ < sq ? BQ : sq - qa) - 1;
+        const int qdz = sQd[buf][qz];
+        need_mask |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga);
       }
-    }
 
-    bool need_mask = (qa + BQ > sq) || (k0 + BKV > sk);
-    if (mask == RMX_MASK_CAUSAL) need_mask |= (klast > qa + off);
-    if (mask == RMX_MASK_DOC) {
-      const int qga = sQg[buf][0];
-      const int qda = sQd[buf][0];
-      const int qlast_row = (qa + BQ < sq ? BQ : sq - qa) - 1;
-      const int qdb = sQd[buf][qlast_row];
-      need_mask |= !(qda == qdb && qda == kd_first && kd_first == kd_last && kg_last <= qga);
-    }
-
-    bf16x8 pt[4], dst[4];
+      // two halves of 32 queries (mb): S = Q K^T and dP = dO V^T for the half
+      // (rows: queries sigma-permuted; lane: this wave's keys), P and dS, then
+      // dV += P^T dO and dK += dS^T Q (rows: this wave's keys; cols: head dim)
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      f32x4 lv[4], dv4[4];
+      for (int mb = 0; mb < 2; ++mb) {
+        f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-      for (int h8 = 0; h8 < 2; ++h8) {
-        const int qb = 32 * mb + 16 * h8 + 8 * hl;
-        lv[2 * h8] = *reinterpret_cast<const f32x4*>(&sL[buf][qb]);
-        lv[2 * h8 + 1] = *reinterpret_cast<const f32x4*>(&sL[buf][qb + 4]);
-        dv4[2 * h8] = *reinterpret_cast<const f32x4*>(&sD[buf][qb]);
-        dv4[2 * h8 + 1] = *reinterpret_cast<const f32x4*>(&sD[buf][qb + 4]);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float l2 = lv[r >> 2][r & 3];
-        const float dl = dv4[r >> 2][r & 3];
-        float pv = fast_exp2(fmaf(s[mb][r], c, -l2));
-        if (need_mask) {
-          const int ql = 32 * mb + sig_row(hl, r);
-          const int qq = qa + ql;
-          bool ok = kvalid && qq < sq;
-          if (mask == RMX_MASK_CAUSAL) ok = ok && (key <= qq + off);
-          if (mask == RMX_MASK_DOC) ok = ok && (sQd[buf][ql] == kd) && (kg <= sQg[buf][ql]);
-          if (!ok) pv = 0.f;
+        for (int kb = 0; kb < NKB; ++kb) {
+          const int o = r_lane + mb * 32 * RS + 32 * kb;
+          const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qt_l + o));
+          s = mfma32(a, kreg[kb], s);
+          const bf16x8 b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ot_l + o));
+          dp = mfma32(b, vreg[kb], dp);
         }
-        s[mb][r] = pv;
-        dp[mb][r] = pv * (dp[mb][r] - dl);
-      }
-    }
+        bf16x8 pt[2], dst[2];
 #pragma unroll
-    for (int kb2 = 0; kb2 < 4; ++kb2) {
-      const int mb = kb2 >> 1, b8 = 8 * (kb2 & 1);
-      const f32x16& t = s[mb];
-      pt[kb2] = pack8(t[b8 + 0], t[b8 + 1], t[b8 + 2], t[b8 + 3], t[b8 + 4], t[b8 + 5], t[b8 + 6],
-                      t[b8 + 7]);
-      const f32x16& u = dp[mb];
-      dst[kb2] = pack8(u[b8 + 0], u[b8 + 1], u[b8 + 2], u[b8 + 3], u[b8 + 4], u[b8 + 5], u[b8 + 6],
-                       u[b8 + 7]);
-    }
-
-    // dV += P^T dO, dK += dS^T Q  (rows = this wave's keys, cols = head dim)
+        for (int h8 = 0; h8 < 2; ++h8) {
+          float pv[8], dsv[8];
+          const int qb = 32 * mb + 16 * h8 + 8 * hl;  // queries of regs 8*h8 .. 8*h8+7
+          const f32x4 l0 = *reinterpret_cast<const f32x4*>(&sL[buf][qb]);
+          const f32x4 l1 = *reinterpret_cast<const f32x4*>(&sL[buf][qb + 4]);
+          const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sD[buf][qb]);
+          const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sD[buf][qb + 4]);
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int d = 32 * db + l32;
+          for (int i = 0; i < 8; ++i) {
+            const int r = 8 * h8 + i;
+            const float l2 = i < 4 ? l0[i & 3] : l1[i & 3];
+            const float dl = i < 4 ? d0[i & 3] : d1[i & 3];
+            float pv1 = fast_exp2(fmaf(s[r], c, -l2));
+            if (need_mask) {
+              const int ql = qb + i;
+              const int qq = qa + ql;
+              bool ok = kvalid;
+              if (mask == RMX_MASK_CAUSAL) ok &= key <= qq + off;
+              if (mask == RMX_MASK_DOC) {
+                const int qd = sQd[buf][ql], qg = sQg[buf][ql];
+                ok &= (qd == kd) & (kg <= qg);
+              }
+              pv1 = ok ? pv1 : 0.f;
+            }
+            pv[i] = pv1;
+            dsv[i] = pv1 * (dp[r] - dl);
+          }
+          pt[h8] = pack8_hw(pv);
+          dst[h8] = pack8_hw(dsv);
+        }
 #pragma unroll
-      for (int kb2 = 0; kb2 < 4; ++kb2) {
-        const bf16x8 bo = lds_t_operand(sDOt[buf], d, 2 * kb2 + hl);
-        dv[db] = mfma32(pt[kb2], bo, dv[db]);
-        const bf16x8 bq = lds_t_operand(sQt[buf], d, 2 * kb2 + hl);
-        dk[db] = mfma32(dst[kb2], bq, dk[db]);
+        for (int h8 = 0; h8 < 2; ++h8)
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+            const int kb2 = 2 * mb + h8;
+            dv[db] = mfma32(pt[h8], tr_operand<RS>(ot_l, t_lane, kb2, db), dv[db]);
+            dk[db] = mfma32(dst[h8], tr_operand<RS>(qt_l, t_lane, kb2, db), dk[db]);
+          }
       }
     }
 
@@ -595,14 +676,14 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
     __syncthreads();
   }
 
-  // ---- epilogue: lane (hl, d) holds rows key = k0 + 32*wave + c_row(hl, r)
+  // ---- epilogue: lane (hl, d) holds rows key = kw0 + c_row(hl, r)
   const float scale = L.scale;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
     const int d = 32 * db + l32;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int kk = k0 + wave * 32 + c_row(hl, r);
+      const int kk = kw0 + c_row(hl, r);
       if (kk >= sk) continue;
       const float gk = dk[db][r] * scale, gv = dv[db][r];
       const int64_t ao = bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + d;
@@ -628,7 +709,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_bwd_dkdv_kernel(const BwdPara
 template <int HD>
 static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                                hipStream_t stream) {
-  constexpr int NW_DQ = 4, NW_KV = 4;
+  constexpr int BQ_DQ = 256, BKV = 128;
   BwdParams pq, pk;
   pq.L = L;
   pk.L = L;
@@ -639,14 +720,14 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
     const bool empty = probs[i].sq == 0 || probs[i].sk == 0;
     if (!empty && probs[i].dq_mode != RMX_GRAD_NONE) {
       pq.P[nq] = probs[i];
-      pq.tiles[nq] = (probs[i].sq + 32 * NW_DQ - 1) / (32 * NW_DQ);
+      pq.tiles[nq] = (probs[i].sq + BQ_DQ - 1) / BQ_DQ;
       pq.tile_start[nq] = tq;
       tq += L.batch * L.hq * pq.tiles[nq];
       ++nq;
     }
     if (!empty && probs[i].dkv_mode != RMX_GRAD_NONE) {
       pk.P[nk] = probs[i];
-      pk.tiles[nk] = (probs[i].sk + 32 * NW_KV - 1) / (32 * NW_KV);
+      pk.tiles[nk] = (probs[i].sk + BKV - 1) / BKV;
       pk.tile_start[nk] = tk;
       tk += L.batch * L.hkv * pk.tiles[nk];
       ++nk;
@@ -659,14 +740,14 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
   pq.total = tq;
   pk.total = tk;
   if (tk > 0) {
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, NW_KV>), dim3((tk + 7) / 8 * 8), dim3(NW_KV * 64),
-                       0, stream, pk);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD>), dim3((tk + 7) / 8 * 8), dim3(256), 0, stream,
+                       pk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (tq > 0) {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, NW_DQ>), dim3((tq + 7) / 8 * 8), dim3(NW_DQ * 64), 0,
-                       stream, pq);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD>), dim3((tq + 7) / 8 * 8), dim3(512), 0, stream,
+                       pq);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -83,7 +83,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   const int q0 = qt * C::BQ;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int qw0 = q0 + 32 * wave;  // first query of this wave
   const int q = qw0 + l32;         // this lane's query
 
