@@ -167,7 +167,7 @@ __device__ __forceinline__ bf16x8 tr_operand(const uint8_t* tile, int lane_off, 
 //   P = exp2(S c - lse2), dS = P (dP - delta)  (lane = query: lse/delta per lane)
 //   dQ^T += K^T dS^T  A = K^T by transposed reads of the K tile, B = dS^T
 //                                                            16 MFMAs
-template <int HD>
+template <int HD, int MASK>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm) {
   using T = BwdTiles<HD>;
   constexpr int NW = 8, NT = NW * 64, BQ = 32 * NW, BK = 64;
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   const int bb = local / (nqt * L.hq);
   const int kvh = head / (L.hq / L.hkv);
   const int sq = P.sq, sk = P.sk;
-  const int mask = L.mask;
+  constexpr int mask = MASK;
   const int q0 = qt * BQ;
 
   const int tid = threadIdx.x;
@@ -364,9 +364,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
         const int mb = kb2 >> 1, b8 = 8 * (kb2 & 1);
         float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float pv = fast_exp2(fmaf(s[mb][b8 + i], c, -lse2));
-          if (need_mask) {
+        for (int i = 0; i < 8; ++i) v[i] = fast_exp2(fmaf(s[mb][b8 + i], c, -lse2));
+        if (need_mask) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
             const int kl = 32 * mb + sig_row(hl, b8 + i);
             const int key = k0 + kl;
             bool ok = key < sk;
@@ -375,10 +376,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
               const int kd = sKd[buf][kl], kg = sKg[buf][kl];
               ok &= (kd == qd) & (kg <= qg);
             }
-            pv = ok ? pv : 0.f;
+            v[i] = ok ? v[i] : 0.f;
           }
-          v[i] = pv * (dp[mb][b8 + i] - dlt);
         }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] *= dp[mb][b8 + i] - dlt;
         dsb[kb2] = pack8_hw(v);
       }
 
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
 //   P = exp2(S c - lse2[q]), dS = P (dP - delta[q])  (lse/delta from LDS)
 //   dV += P^T dO   A = P^T (registers), B = dO^T transposed reads  16 MFMAs
 //   dK += dS^T Q   A = dS^T (registers), B = Q^T transposed reads  16 MFMAs
-template <int HD>
+template <int HD, int MASK>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams prm) {
   using T = BwdTiles<HD>;
   constexpr int NW = 4, NT = NW * 64, BKV = 32 * NW, BQ = 64;
@@ -454,7 +456,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   const int bb = local / (nkt * L.hkv);
   const int G = L.hq / L.hkv;
   const int sq = P.sq, sk = P.sk;
-  const int mask = L.mask;
+  constexpr int mask = MASK;
   const int k0 = kt * BKV;
 
   const int tid = threadIdx.x;
@@ -602,9 +604,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     const uint8_t* qt_l = smem + buf * 2 * QT;
     const uint8_t* ot_l = qt_l + QT;
 
-    // causal: this wave's keys are all after the tile's last query
-    const bool active = mask != RMX_MASK_CAUSAL || kw0 <= qa + BQ - 1 + off;
-    if (active) {
+    // Every wave computes every tile of the workgroup's range (masked P is
+    // zero): a branch around the MFMAs would make the loop-carried dK/dV
+    // accumulators change register class at the merge.
+    {
       bool need_mask = (kw0 + 32 > sk);
       if (mask == RMX_MASK_CAUSAL) need_mask |= (wave_klast > qa + off);
       if (mask == RMX_MASK_DOC) {
@@ -640,11 +643,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
           const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sD[buf][qb + 4]);
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const int r = 8 * h8 + i;
             const float l2 = i < 4 ? l0[i & 3] : l1[i & 3];
-            const float dl = i < 4 ? d0[i & 3] : d1[i & 3];
-            float pv1 = fast_exp2(fmaf(s[r], c, -l2));
-            if (need_mask) {
+            pv[i] = fast_exp2(fmaf(s[8 * h8 + i], c, -l2));
+          }
+          if (need_mask) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
               const int ql = qb + i;
               const int qq = qa + ql;
               bool ok = kvalid;
@@ -653,10 +657,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
                 const int qd = sQd[buf][ql], qg = sQg[buf][ql];
                 ok &= (qd == kd) & (kg <= qg);
               }
-              pv1 = ok ? pv1 : 0.f;
+              pv[i] = ok ? pv[i] : 0.f;
             }
-            pv[i] = pv1;
-            dsv[i] = pv1 * (dp[r] - dl);
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float dl = i < 4 ? d0[i & 3] : d1[i & 3];
+            dsv[i] = pv[i] * (dp[8 * h8 + i] - dl);
           }
           pt[h8] = pack8_hw(pv);
           dst[h8] = pack8_hw(dsv);
@@ -740,14 +747,24 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
   pq.total = tq;
   pk.total = tk;
   if (tk > 0) {
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD>), dim3((tk + 7) / 8 * 8), dim3(256), 0, stream,
-                       pk);
+    const dim3 grid((tk + 7) / 8 * 8);
+    if (L.mask == RMX_MASK_CAUSAL)
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL>), grid, dim3(256), 0, stream, pk);
+    else if (L.mask == RMX_MASK_DOC)
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_DOC>), grid, dim3(256), 0, stream, pk);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_FULL>), grid, dim3(256), 0, stream, pk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (tq > 0) {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<HD>), dim3((tq + 7) / 8 * 8), dim3(512), 0, stream,
-                       pq);
+    const dim3 grid((tq + 7) / 8 * 8);
+    if (L.mask == RMX_MASK_CAUSAL)
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_CAUSAL>), grid, dim3(512), 0, stream, pq);
+    else if (L.mask == RMX_MASK_DOC)
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_DOC>), grid, dim3(512), 0, stream, pq);
+    else
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_FULL>), grid, dim3(512), 0, stream, pq);
     return hipGetLastError();
   }
   return hipSuccess;

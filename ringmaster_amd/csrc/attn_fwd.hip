@@ -56,7 +56,7 @@ struct FwdCfg {
 
 constexpr float kRescaleSlack = 8.0f;  // log2 units: P <= 2^8 between rescales
 
-template <int HD>
+template <int HD, int MASK>
 __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   using C = FwdCfg<HD>;
   constexpr int BK = C::BK, NKB = C::NKB, NDB = C::NDB, CH = C::CH, LPT = C::LPT;
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   const int bb = local / (nqt * L.hq);
   const int kvh = head / (L.hq / L.hkv);
   const int sq = P.sq, sk = P.sk;
-  const int mask = L.mask;
+  constexpr int mask = MASK;
   const int q0 = qt * C::BQ;
 
   const int tid = threadIdx.x;
@@ -383,7 +383,15 @@ static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* 
   prm.total = tot;
   if (tot == 0) return hipSuccess;
   const int grid = (tot + 7) / 8 * 8;
-  hipLaunchKernelGGL((attn_fwd_kernel<HD>), dim3(grid), dim3(FwdCfg<HD>::NT), 0, stream, prm);
+  if (L.mask == RMX_MASK_CAUSAL)
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_CAUSAL>), dim3(grid), dim3(FwdCfg<HD>::NT), 0,
+                       stream, prm);
+  else if (L.mask == RMX_MASK_DOC)
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_DOC>), dim3(grid), dim3(FwdCfg<HD>::NT), 0,
+                       stream, prm);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_FULL>), dim3(grid), dim3(FwdCfg<HD>::NT), 0,
+                       stream, prm);
   return hipGetLastError();
 }
 
