@@ -317,6 +317,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
     doc_store(0);
   }
   __syncthreads();
+  wait_all_loads();
 
   const float c = prm.scale_log2;
   for (int kt = kt_begin; kt < kt_end; ++kt) {
@@ -366,6 +367,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = fast_exp2(fmaf(s[mb][b8 + i], c, -lse2));
         if (need_mask) {
+        keep_branch();
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             const int kl = 32 * mb + sig_row(hl, b8 + i);
@@ -547,15 +549,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       const int qq = qa + tid;
       if (qq < sq) {
         const int64_t lr = bb * L.l_sb + qh * L.l_sh + qq;
-        nl = P.lse[lr] * kLog2e;
-        if (nl == kNegInf) nl = __builtin_inff();
+        nl = P.lse[lr];  // converted at commit, so the load is not waited for here
         nd = P.delta[lr];
         if (mask == RMX_MASK_DOC) {
           nqg = P.q_gidx[qq];
           nqd = P.doc[nqg];
         }
       } else {
-        nl = __builtin_inff();  // rows past the end: P == 0
+        nl = kNegInf;  // rows past the end: P == 0
         nd = 0.f;
         nqg = -2147483647;
         nqd = -1;
@@ -572,7 +573,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       *reinterpret_cast<u32x4*>(ot_l + row * RS + 16 * c) = ost[i];
     }
     if (tid < BQ) {
-      sL[buf][tid] = nl;
+      // lse in log2 units; rows without any attended key (lse = -inf) get +inf
+      // so that every P of the row is exactly 0
+      sL[buf][tid] = nl == kNegInf ? __builtin_inff() : nl * kLog2e;
       sD[buf][tid] = nd;
       sQg[buf][tid] = nqg;
       sQd[buf][tid] = nqd;
@@ -594,6 +597,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     commit(0);
   }
   __syncthreads();
+  wait_all_loads();
 
   const float c = prm.scale_log2;
   for (int it = 0; it < total_iter; ++it) {
@@ -647,6 +651,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
             pv[i] = fast_exp2(fmaf(s[8 * h8 + i], c, -l2));
           }
           if (need_mask) {
+        keep_branch();
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
               const int ql = qb + i;

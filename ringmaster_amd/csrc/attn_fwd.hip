@@ -201,6 +201,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     doc_store(0);
   }
   __syncthreads();
+  wait_all_loads();
 
   const float c = prm.scale_log2;
   for (int kt = kt_begin; kt < kt_end; ++kt) {
@@ -238,6 +239,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
       }
 
       if (need_mask) {
+        keep_branch();
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll

@@ -95,6 +95,17 @@ __device__ __forceinline__ int swz_t(int row) { return row & 7; }
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// An empty volatile asm statement: a block containing it cannot be speculated,
+// so the compiler keeps a rarely taken branch (the masked-tile path) a branch
+// instead of if-converting it into per-element selects on every tile.
+__device__ __forceinline__ void keep_branch() { asm volatile(""); }
+
+// Wait for every outstanding memory operation of the wave. Issued once before a
+// main loop whose body reads registers filled by loads issued before it: the
+// waitcnt pass cannot tell those loads from the loop's own prefetches, and
+// would otherwise wait for the prefetches at the first use in every iteration.
+__device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0); }
+
 // Cross-half exchange: value held by lane l ^ 32.
 __device__ __forceinline__ float xhalf(float v) { return __shfl_xor(v, 32, 64); }
 
