@@ -196,29 +196,81 @@ def block_workload(steps, warmup):
 
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline(heads=1):
-    """Oracle (torch CPU fp32 restatement of the reference math path): rank 0's complete
-    ring fwd+bwd at configs[2] (P=8, L=16384, D=128) for ``heads`` head(s). Zigzag gives
-    every rank the same pairs, so the rate extrapolates to the whole job."""
+    """Oracle (torch CPU fp32 restatement of the reference ``math`` block path) on a
+    bounded sample of configs[2]: rank 0's ring-step-0 block (its 16384 queries x its
+    own 16384 keys, causal) and one remote ring-step block (its late 8192 queries x a
+    remote rank's 16384 keys), forward + backward, ``heads`` head(s). Those are the two
+    block shapes every rank's ring is made of (1 + 7 blocks), so the per-pair rate is
+    the job's rate."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import ring_math as rm
-    from ringmaster_amd.ring.schedule import ring_pairs_per_rank
 
-    P, L, D = 8, 16384, 128
+    L, D = 16384, 128
+    h = L // 2
+    scale = 1.0 / math.sqrt(D)
     g = torch.Generator().manual_seed(1)
-    mk = lambda: [torch.randn(1, heads, L, D, generator=g) for _ in range(P)]  # noqa: E731
-    qs, ks, vs = mk(), mk(), mk()
-    dos = [torch.randn(1, L, heads, D, generator=g) for _ in range(P)]
+    mk = lambda n: torch.randn(1, n, heads, D, generator=g)  # noqa: E731
+    q, k, v, dout = mk(L), mk(L), mk(L), mk(L)
+    kr, vr = mk(L), mk(L)
     t0 = time.perf_counter()
-    outs, lses = rm.zigzag_ring_forward(qs, ks, vs, ranks=[0])
-    rm.zigzag_ring_backward(dos, qs, ks, vs, outs, lses, ranks=[0])
+    # ring step 0: the local 2h x 2h block, bottom-right causal
+    m = rm.causal_mask(L, L)
+    out, lse = rm.masked_block_fwd(q, k, v, m, scale)
+    rm.masked_block_bwd(dout, q, k, v, out, lse, m, scale)
+    del m
+    # a ring step s > r: late query half x the visiting rank's whole KV block
+    out1, lse1 = rm.masked_block_fwd(q[:, h:], kr, vr, 0.0, scale)
+    rm.masked_block_bwd(dout[:, h:], q[:, h:], kr, vr, out1, lse1, 0.0, scale)
     sec = time.perf_counter() - t0
-    flops = 14 * D * heads * ring_pairs_per_rank(P, L)
+    pairs = L * (L + 1) // 2 + h * L
+    flops = 14 * D * heads * pairs
     return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s",
             "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle rank 0 of 8, {heads} head(s), full zigzag ring fwd+bwd at "
-                      f"L=16384, D=128, fp32 torch CPU ({sec:.1f} s; os.cpu_count()="
-                      f"{os.cpu_count()})",
+            "sample": f"oracle (torch CPU fp32) fwd+bwd of rank 0's ring-step-0 block (16384x16384 "
+                      f"causal) and one remote step block (8192x16384), {heads} head(s), D=128: "
+                      f"{pairs} pairs = 2 of the 8 blocks of one rank of configs[2] "
+                      f"({sec:.1f} s; os.cpu_count()={os.cpu_count()})",
             "seconds": round(sec, 2)}
+
+
+# ---------------------------------------------------------------- profiling mode
+def profile_workload():
+    """One warm-up and one configs[2] ring fwd+bwd step, then a 1 GiB device-to-device
+    copy (3 times): the calibration kernel for the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes (bytes counted for a copy of known size give the counter's scale)."""
+    from ringmaster_amd.ring.zigzag import zigzag_ring_attention
+
+    P, S, H, D = 8, 131072, 16, 128
+    L = S // P
+    q = _gen((P, 1, H, L, D), 1).requires_grad_(True)
+    k = _gen((P, 1, H, L, D), 2).requires_grad_(True)
+    v = _gen((P, 1, H, L, D), 3).requires_grad_(True)
+    dout = _gen((P, 1, L, H, D), 4)
+    for i in range(2):
+        out = zigzag_ring_attention(q, k, v)
+        torch.autograd.grad(out, (q, k, v), dout)
+        _sync()
+        print(f"profile: ring step {i} done", flush=True)
+    del q, k, v, dout, out
+    torch.cuda.empty_cache()
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    _sync()
+    print("profile: calibration copies of 1073741824 bytes done", flush=True)
+
+
+def _traffic(kernel):
+    """HBM bytes per launch of ``kernel`` measured by rocprofv3 (profiles/traffic.json), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = data.get("kernels", {}).get(kernel)
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
 def _clocks():
@@ -238,6 +290,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip the HBM-bound kernels")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=1)
+    ap.add_argument("--profile", action="store_true",
+                    help="one ring step + copy calibration, for rocprofv3 counter passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -248,7 +302,12 @@ def main():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         sys.exit(1)
 
+    if args.profile:
+        profile_workload()
+        return
+
     ring = ring_workload(args.steps, args.warmup)
+    ring["roofline"]["traffic"] = _traffic(ring["roofline"]["kernel"])
     torch.cuda.empty_cache()
     extras = {}
     if not args.no_extras:

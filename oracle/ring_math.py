@@ -147,6 +147,13 @@ def zigzag_gidx(rank, half, world):
                       torch.arange((2 * world - 1 - rank) * half, (2 * world - rank) * half)])
 
 
+def kv_source(rank, step, world):
+    """Rank whose KV block ``rank`` holds at ring step ``step``: the KV moves to
+    rank + 1 each hop, so step s sees rank - s (ring/zigzag.py:93,
+    direction ring/p2p_attn.py:65-69)."""
+    return (rank - step) % world
+
+
 def _block_fwd(qd, k, v, scale, mask):
     return masked_block_fwd(qd, k, v, mask, scale)
 
@@ -173,7 +180,7 @@ def zigzag_ring_forward(qs, ks, vs, scaling=None, cu_seqlens=None, ranks=None):
         g = zigzag_gidx(rank, half, world)
         out = lse = None
         for s in range(world):
-            rem = (rank - s) % world
+            rem = kv_source(rank, s, world)
             ck, cv = kd[rem], vd[rem]
             if s == 0:
                 m = (additive_doc_mask(g, g, doc, True) if doc is not None
@@ -221,7 +228,7 @@ def zigzag_ring_backward(d_outs, qs, ks, vs, outs, lses, scaling=None, cu_seqlen
     active = range(world) if ranks is None else ranks
     for s in range(world):
         for rank in active:
-            rem = (rank - s) % world
+            rem = kv_source(rank, s, world)
             g = zigzag_gidx(rank, half, world)
             dod, out, lse = d_outs[rank].float(), outs[rank].float(), lses[rank]
             ck, cv = kd[rem], vd[rem]

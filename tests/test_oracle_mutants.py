@@ -1,0 +1,136 @@
+"""Plant plausible mistakes in (copies of) the CPU oracle and check that the pinning
+checks of test_oracle_pinning.py reject every one of them. A pinning check that a
+mutant passes would pin nothing; these tests keep the checks honest. All on the CPU."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import ring_math as rm
+from oracle import state_passing as sp
+from tests import test_oracle_pinning as pin
+
+
+def _math_block_variant(q, k, v, *, causal, scaling, top_left=False, tile_gqa=False,
+                        scale_mult=1.0):
+    qt, kt, vt = (t.transpose(1, 2).double() for t in (q, k, v))
+    rep = qt.shape[1] // kt.shape[1]
+    if rep > 1:
+        if tile_gqa:  # kv_head = q_head % hkv instead of q_head // (hq / hkv)
+            kt, vt = kt.repeat(1, rep, 1, 1), vt.repeat(1, rep, 1, 1)
+        else:
+            kt, vt = (t.repeat_interleave(rep, dim=1) for t in (kt, vt))
+    scale = (scaling if scaling is not None else 1.0 / math.sqrt(qt.shape[-1])) * scale_mult
+    s = (qt @ kt.transpose(-1, -2)) * scale
+    sq, sk = s.shape[-2:]
+    if causal:
+        keep = torch.ones(sq, sk, dtype=torch.bool).tril(0 if top_left else sk - sq)
+        s = s.masked_fill(~keep, float("-inf"))
+    lse = torch.logsumexp(s, -1)
+    out = torch.softmax(s, -1) @ vt
+    return out.transpose(1, 2), lse
+
+
+@pytest.mark.parametrize("mutation", ["top_left_causal", "tiled_gqa", "scale"])
+def test_block_mutants_are_caught(mutation):
+    kw = {"top_left_causal": dict(top_left=True), "tiled_gqa": dict(tile_gqa=True),
+          "scale": dict(scale_mult=1.01)}[mutation]
+    fn = lambda q, k, v, causal, scaling: _math_block_variant(  # noqa: E731
+        q, k, v, causal=causal, scaling=scaling, **kw)
+    # the unmutated variant passes the same check
+    pin.check_block(lambda q, k, v, causal, scaling: _math_block_variant(
+        q, k, v, causal=causal, scaling=scaling), True, 4, 2, 3, 7)
+    with pytest.raises(AssertionError):
+        pin.check_block(fn, True, 4, 2, 3, 7)
+
+
+def test_merge_mutants_are_caught():
+    def flipped(out, lse, block_out, block_lse):  # exp(new - blk) instead of exp(blk - new)
+        block_lse = rm.lse_to_bshd(block_lse, block_out)
+        if out is None:
+            return block_out.float(), block_lse
+        new = torch.logaddexp(lse, block_lse)
+        return torch.exp(lse - new) * out + torch.exp(new - block_lse) * block_out, new
+
+    def no_renorm(out, lse, block_out, block_lse):  # drops the running-out weight
+        block_lse = rm.lse_to_bshd(block_lse, block_out)
+        if out is None:
+            return block_out.float(), block_lse
+        new = torch.logaddexp(lse, block_lse)
+        return out + torch.exp(block_lse - new) * block_out, new
+
+    for mutant in (flipped, no_renorm):
+        with pytest.raises(AssertionError):
+            pin.check_merge(mutant)
+
+
+def test_ring_direction_mutant_is_caught(monkeypatch):
+    monkeypatch.setattr(rm, "kv_source", lambda rank, step, world: (rank + step) % world)
+    with pytest.raises(AssertionError):
+        pin.check_ring(4, half=2)
+
+
+def test_ring_merge_slice_mutant_is_caught(monkeypatch):
+    orig = rm.merge_slice
+
+    def wrong_rows(out, lse, block_out, block_lse, sl):  # merges into the early rows
+        return orig(out, lse, block_out, block_lse, slice(0, block_out.shape[1]))
+
+    monkeypatch.setattr(rm, "merge_slice", wrong_rows)
+    with pytest.raises(AssertionError):
+        pin.check_ring(2, half=3)
+
+
+def test_ring_backward_delta_mutant_is_caught(monkeypatch):
+    def no_delta(d_out, q, k, v, out, lse, add_mask, scale):  # dS = P dP (delta dropped)
+        nq = q.shape[2]
+        qf, kf, vf = (rm._repeat_kv(t, nq).transpose(1, 2).double() for t in (q, k, v))
+        dof = d_out.transpose(1, 2).double()
+        p = torch.exp((qf @ kf.transpose(-1, -2)) * scale + add_mask - lse.unsqueeze(-1))
+        dv = p.transpose(-1, -2) @ dof
+        ds = p * (dof @ vf.transpose(-1, -2))
+        dq, dk = (ds @ kf) * scale, (ds.transpose(-1, -2) @ qf) * scale
+        hkv = k.shape[2]
+        if hkv != nq:
+            dk = dk.unflatten(1, (hkv, nq // hkv)).sum(2)
+            dv = dv.unflatten(1, (hkv, nq // hkv)).sum(2)
+        return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2)
+
+    monkeypatch.setattr(rm, "masked_block_bwd", no_delta)
+    with pytest.raises(AssertionError):
+        pin.check_ring(2, half=3)
+
+
+def test_zigzag_gidx_mutant_is_caught(monkeypatch):
+    # late chunk first: the document masks then use the wrong global indices
+    monkeypatch.setattr(rm, "zigzag_gidx", lambda r, h, w: torch.cat(
+        [torch.arange((2 * w - 1 - r) * h, (2 * w - r) * h), torch.arange(r * h, (r + 1) * h)]))
+    cu = torch.tensor([0, 6, 16], dtype=torch.int32)
+    with pytest.raises(AssertionError):
+        pin.check_ring(2, half=4, cu=cu)
+
+
+def test_scan_mutants_are_caught():
+    def no_correction(a, b, world):
+        n = a.shape[1] // world
+        return torch.cat([sp.local_linear_scan(a[:, r * n:(r + 1) * n], b[:, r * n:(r + 1) * n])
+                          for r in range(world)], 1)
+
+    def reversed_prefix(a, b, world):  # folds the ranks' pairs in the wrong order
+        n = a.shape[1] // world
+        outs, pairs = [], []
+        for r in range(world):
+            sa, sb = a[:, r * n:(r + 1) * n], b[:, r * n:(r + 1) * n]
+            h = sp.local_linear_scan(sa, sb)
+            pairs.append((torch.cumprod(sa, 1), h))
+        for r in range(world):
+            h_in = torch.zeros_like(b[:, 0])
+            for j in reversed(range(r)):
+                h_in = pairs[j][0][:, -1] * h_in + pairs[j][1][:, -1]
+            outs.append(pairs[r][1] + pairs[r][0] * h_in.unsqueeze(1))
+        return torch.cat(outs, 1)
+
+    for mutant in (no_correction, reversed_prefix):
+        with pytest.raises(AssertionError):
+            pin.check_scan(mutant, world=4, T=16)
