@@ -19,11 +19,8 @@ namespace rmx {
 
 struct BwdParams {
   rmx_attn_layout L;
-  rmx_bwd_problem P[RMX_MAX_BATCHED];
-  int tile_start[RMX_MAX_BATCHED + 1];
-  int tiles[RMX_MAX_BATCHED];
-  int nprob;
-  int total;
+  rmx_bwd_problem P[RMX_MAX_BATCHED];  // in launch order (longest workgroups first)
+  WgMapParams map;  // dQ: groups (batch, q head) x query tiles; dK/dV: (batch, kv head) x key tiles
   float scale_log2;
 };
 
@@ -104,13 +101,6 @@ hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int 
 }
 
 // ---------------------------------------------------------------- shared helpers
-// Per-problem decode of the linear workgroup index.
-__device__ __forceinline__ int find_problem(const BwdParams& prm, int id) {
-  int p = 0;
-  while (p + 1 < prm.nprob && id >= prm.tile_start[p + 1]) ++p;
-  return p;
-}
-
 // Write a 4-float run of a gradient row according to the output mode.
 __device__ __forceinline__ void grad_store4(int mode, float* acc, uint16_t* bf, f32x4 v) {
   if (mode == RMX_GRAD_WRITE_F32) {
@@ -182,16 +172,14 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   __shared__ int sKd[2][BK];
   __shared__ int sRange[2];
 
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  if (id >= prm.total) return;
-  const int p = find_problem(prm, id);
+  const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
+  if (!wc.valid) return;
   const rmx_attn_layout& L = prm.L;
-  const rmx_bwd_problem& P = prm.P[p];
-  const int local = id - prm.tile_start[p];
-  const int nqt = prm.tiles[p];
-  const int qt = nqt - 1 - (local % nqt);
-  const int head = (local / nqt) % L.hq;
-  const int bb = local / (nqt * L.hq);
+  const rmx_bwd_problem& P = prm.P[wc.p];
+  const int nqt = prm.map.ntile[wc.p];
+  const int qt = nqt - 1 - wc.tile;  // heaviest causal tiles first
+  const int head = wc.group % L.hq;
+  const int bb = wc.group / L.hq;
   const int kvh = head / (L.hq / L.hkv);
   const int sq = P.sq, sk = P.sk;
   constexpr int mask = MASK;
@@ -446,16 +434,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   __shared__ int sQd[2][BQ];
   __shared__ int sRange[2];
 
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  if (id >= prm.total) return;
-  const int p = find_problem(prm, id);
+  const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
+  if (!wc.valid) return;
   const rmx_attn_layout& L = prm.L;
-  const rmx_bwd_problem& P = prm.P[p];
-  const int local = id - prm.tile_start[p];
-  const int nkt = prm.tiles[p];
-  const int kt = local % nkt;
-  const int kvh = (local / nkt) % L.hkv;
-  const int bb = local / (nkt * L.hkv);
+  const rmx_bwd_problem& P = prm.P[wc.p];
+  const int kt = wc.tile;
+  const int kvh = wc.group % L.hkv;
+  const int bb = wc.group / L.hkv;
   const int G = L.hq / L.hkv;
   const int sq = P.sq, sk = P.sk;
   constexpr int mask = MASK;
@@ -726,33 +711,39 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
   pq.L = L;
   pk.L = L;
   pq.scale_log2 = pk.scale_log2 = L.scale * kLog2e;
-  // problems with an empty side or a skipped gradient get no workgroups there
-  int tq = 0, tk = 0, nq = 0, nk = 0;
+  // problems with an empty side or a skipped gradient get no workgroups there;
+  // the others run longest workgroups first (dQ: key tiles, dK/dV: query tiles x group)
+  const int G = L.hq / L.hkv;
+  long long cq[RMX_MAX_BATCHED], ck[RMX_MAX_BATCHED];
+  int iq[RMX_MAX_BATCHED], ik[RMX_MAX_BATCHED], nq = 0, nk = 0;
   for (int i = 0; i < n; ++i) {
     const bool empty = probs[i].sq == 0 || probs[i].sk == 0;
     if (!empty && probs[i].dq_mode != RMX_GRAD_NONE) {
-      pq.P[nq] = probs[i];
-      pq.tiles[nq] = (probs[i].sq + BQ_DQ - 1) / BQ_DQ;
-      pq.tile_start[nq] = tq;
-      tq += L.batch * L.hq * pq.tiles[nq];
-      ++nq;
+      cq[nq] = probs[i].sk;
+      iq[nq++] = i;
     }
     if (!empty && probs[i].dkv_mode != RMX_GRAD_NONE) {
-      pk.P[nk] = probs[i];
-      pk.tiles[nk] = (probs[i].sk + BKV - 1) / BKV;
-      pk.tile_start[nk] = tk;
-      tk += L.batch * L.hkv * pk.tiles[nk];
-      ++nk;
+      ck[nk] = (long long)probs[i].sq * G;
+      ik[nk++] = i;
     }
   }
-  for (int i = nq; i <= RMX_MAX_BATCHED; ++i) pq.tile_start[i] = tq;
-  for (int i = nk; i <= RMX_MAX_BATCHED; ++i) pk.tile_start[i] = tk;
-  pq.nprob = nq;
-  pk.nprob = nk;
-  pq.total = tq;
-  pk.total = tk;
+  int oq[RMX_MAX_BATCHED], ok[RMX_MAX_BATCHED], groups[RMX_MAX_BATCHED], ntile[RMX_MAX_BATCHED];
+  order_by_cost(nq, cq, oq);
+  order_by_cost(nk, ck, ok);
+  for (int i = 0; i < nq; ++i) {
+    pq.P[i] = probs[iq[oq[i]]];
+    groups[i] = L.batch * L.hq;
+    ntile[i] = (pq.P[i].sq + BQ_DQ - 1) / BQ_DQ;
+  }
+  const int tq = plan_workgroups(pq.map, nq, groups, ntile);
+  for (int i = 0; i < nk; ++i) {
+    pk.P[i] = probs[ik[ok[i]]];
+    groups[i] = L.batch * L.hkv;
+    ntile[i] = (pk.P[i].sk + BKV - 1) / BKV;
+  }
+  const int tk = plan_workgroups(pk.map, nk, groups, ntile);
   if (tk > 0) {
-    const dim3 grid((tk + 7) / 8 * 8);
+    const dim3 grid(tk);
     if (L.mask == RMX_MASK_CAUSAL)
       hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL>), grid, dim3(256), 0, stream, pk);
     else if (L.mask == RMX_MASK_DOC)
@@ -763,7 +754,7 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
     if (e != hipSuccess) return e;
   }
   if (tq > 0) {
-    const dim3 grid((tq + 7) / 8 * 8);
+    const dim3 grid(tq);
     if (L.mask == RMX_MASK_CAUSAL)
       hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_CAUSAL>), grid, dim3(512), 0, stream, pq);
     else if (L.mask == RMX_MASK_DOC)

@@ -20,20 +20,22 @@
 //   a tile raises it by more than 2^8, so the O rescale is rare
 //   O^T += V^T P^T A = V^T read with ds_read_b64_tr_b16 from the row-major V
 //                  tile, B = P straight from the S^T registers     (16 MFMAs)
-// K/V tiles: buffer loads (rows past the end read as zeros) staged through
-// registers into double-buffered LDS tiles whose row padding makes both the
-// 16-byte row reads and the transposed reads bank-conflict free.
+// K/V tiles: direct global->LDS loads (buffer_load ... lds; rows past the end
+// read as zeros) into three LDS buffers, issued two tiles ahead so L2/HBM
+// latency stays hidden; each tile is published by a barrier that only waits for
+// its own loads. The 16-byte chunks of the unpadded LDS rows are XOR-swizzled
+// (swz_rows for K, swz_tr for V) so both the row reads and the transposed reads
+// are bank-conflict free.
+#include <type_traits>
+
 #include "rmx_kernels.h"
 
 namespace rmx {
 
 struct FwdParams {
   rmx_attn_layout L;
-  rmx_fwd_problem P[RMX_MAX_BATCHED];
-  int tile_start[RMX_MAX_BATCHED + 1];
-  int qtiles[RMX_MAX_BATCHED];
-  int nprob;
-  int total;
+  rmx_fwd_problem P[RMX_MAX_BATCHED];  // in launch order (longest workgroups first)
+  WgMapParams map;                     // groups = (batch, q head), tiles = query tiles
   float scale_log2;
 };
 
@@ -43,15 +45,15 @@ struct FwdCfg {
   static constexpr int NT = NW * 64;
   static constexpr int BQ = 32 * NW;          // queries per workgroup
   static constexpr int BK = 64;               // keys per tile
+  static constexpr int MB = BK / 32;          // 32-key blocks of S^T per tile
   static constexpr int CH = HD / 8;           // 16-byte chunks per row
-  static constexpr int RSK = HD * 2 + 16;     // LDS row stride (bytes) of the K tile
-  static constexpr int RSV = HD * 2 + 64;     // LDS row stride (bytes) of the V tile
-  static constexpr int KT = BK * RSK;
-  static constexpr int VT = BK * RSV;
-  static constexpr int LPT = BK * CH / NT;    // 16-byte chunks per thread per tile
+  static constexpr int RB = HD * 2;           // LDS row bytes (unpadded, swizzled)
+  static constexpr int KT = BK * RB;          // bytes of one K (or V) tile
+  static constexpr int RPK = 1024 / RB;       // rows per 1 KiB DMA instruction
+  static constexpr int NDMA = KT / 1024 / NW; // DMA instructions per wave per tile (K; same for V)
   static constexpr int NKB = HD / 16;         // k-steps of S^T
   static constexpr int NDB = HD / 32;         // 32-row blocks of O^T
-  static_assert(LPT >= 1 && BK * CH % NT == 0, "tile split");
+  static_assert(NDMA >= 1 && KT % (1024 * NW) == 0, "tile split");
 };
 
 constexpr float kRescaleSlack = 8.0f;  // log2 units: P <= 2^8 between rescales
@@ -59,24 +61,28 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units: P <= 2^8 between rescales
 template <int HD, int MASK>
 __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   using C = FwdCfg<HD>;
-  constexpr int BK = C::BK, NKB = C::NKB, NDB = C::NDB, CH = C::CH, LPT = C::LPT;
+  constexpr int BK = C::BK, MB = C::MB, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB;
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * (C::KT + C::VT)];
-  __shared__ int sKg[2][BK];
-  __shared__ int sKd[2][BK];
+  // three K and three V tile buffers (separate objects, so the compiler can tell
+  // the buffer being read from the ones the DMA is filling)
+  __shared__ __attribute__((aligned(1024))) uint8_t sK0[C::KT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sK1[C::KT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sK2[C::KT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sV0[C::KT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sV1[C::KT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sV2[C::KT];
+  __shared__ int sKg[3][BK];
+  __shared__ int sKd[3][BK];
   __shared__ int sRange[2];
 
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  if (id >= prm.total) return;
-  int p = 0;
-  while (p + 1 < prm.nprob && id >= prm.tile_start[p + 1]) ++p;
+  const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
+  if (!wc.valid) return;
   const rmx_attn_layout& L = prm.L;
-  const rmx_fwd_problem& P = prm.P[p];
-  const int local = id - prm.tile_start[p];
-  const int nqt = prm.qtiles[p];
-  const int qt = nqt - 1 - (local % nqt);  // heaviest causal tiles first
-  const int head = (local / nqt) % L.hq;
-  const int bb = local / (nqt * L.hq);
+  const rmx_fwd_problem& P = prm.P[wc.p];
+  const int nqt = prm.map.ntile[wc.p];
+  const int qt = nqt - 1 - wc.tile;  // heaviest causal tiles first
+  const int head = wc.group % L.hq;
+  const int bb = wc.group / L.hq;
   const int kvh = head / (L.hq / L.hkv);
   const int sq = P.sq, sk = P.sk;
   constexpr int mask = MASK;
@@ -139,6 +145,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     kt_end = sRange[1] + 1;
     if (kt_end < kt_begin) kt_end = kt_begin;
   }
+
   // last key this wave can attend (causal): tiles past it are skipped by the wave
   const int wave_qlast = (qw0 + 31 < sq ? qw0 + 31 : sq - 1);
   const int wave_kmax = mask == RMX_MASK_CAUSAL ? wave_qlast + off : 2147483647;
@@ -147,23 +154,29 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
   const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, HD * 2));
   const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, HD * 2));
-  u32x4 kst[LPT], vst[LPT];
-  auto stage_load = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int cid = tid + i * C::NT, row = cid / CH, c = cid % CH;
-      kst[i] = buf_load16(krs, (k0 + row) * kss + 16 * c);
-      vst[i] = buf_load16(vrs, (k0 + row) * vss + 16 * c);
-    }
+  auto kbuf = [&](auto b) -> uint8_t* {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return sK0;
+    else if constexpr (B == 1) return sK1;
+    else return sK2;
   };
-  auto stage_store = [&](int buf) {
-    uint8_t* kt = smem + buf * (C::KT + C::VT);
-    uint8_t* vt = kt + C::KT;
+  auto vbuf = [&](auto b) -> uint8_t* {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return sV0;
+    else if constexpr (B == 1) return sV1;
+    else return sV2;
+  };
+  // DMA of the K/V tile at key k0 into buffer b: instruction n of the tile fills
+  // LDS bytes [1024 n, 1024 n + 1024), lane L row n*RPK + L/CH, swizzled chunk L%CH
+  auto dma_tile = [&](auto b, int k0) {
+    uint8_t* kd = kbuf(b);
+    uint8_t* vd = vbuf(b);
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int cid = tid + i * C::NT, row = cid / CH, c = cid % CH;
-      *reinterpret_cast<u32x4*>(kt + row * C::RSK + 16 * c) = kst[i];
-      *reinterpret_cast<u32x4*>(vt + row * C::RSV + 16 * c) = vst[i];
+    for (int i = 0; i < C::NDMA; ++i) {
+      const int n = wave * C::NDMA + i;
+      const int r = n * C::RPK + lane / CH, p = lane % CH;
+      dma16(krs, kd + 1024 * n, (k0 + r) * kss + 16 * (p ^ swz_rows<HD>(r)));
+      dma16(vrs, vd + 1024 * n, (k0 + r) * vss + 16 * (p ^ swz_tr<HD>(r)));
     }
   };
   int nkg = 0, nkd = 0;
@@ -174,66 +187,82 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
       nkd = P.doc[nkg];
     }
   };
-  auto doc_store = [&](int buf) {
+  auto doc_store = [&](int slot) {
     if (mask == RMX_MASK_DOC && tid < BK) {
-      sKg[buf][tid] = nkg;
-      sKd[buf][tid] = nkd;
+      sKg[slot][tid] = nkg;
+      sKd[slot][tid] = nkd;
     }
   };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  using B2 = std::integral_constant<int, 2>;
 
-  // per-lane LDS byte offsets of the operand reads
-  // K rows (A of S^T): row 32mb + sigma(l32), chunk 2kb + hl
-  const int k_lane = sigma(l32) * C::RSK + 16 * hl;
-  // V^T via transposed reads: key row 16kb2 + 8hl + 4t + (m >> 2),
-  // column 32db + 16x + 4(m & 3), m = lane & 15, x = (lane >> 4) & 1
-  const int m16 = lane & 15, x16 = (lane >> 4) & 1;
-  const int v_lane = (8 * hl + (m16 >> 2)) * C::RSV + 2 * (16 * x16 + 4 * (m16 & 3));
+  // per-lane LDS byte offsets of the operand reads (swizzle folded in; see
+  // swz_rows / swz_tr): K rows (A of S^T) row 32mb + sigma(l32), chunk 2kb + hl
+  int kaddr[NKB];
+  {
+    const int g = hl ^ swz_rows<HD>(sigma(l32));
+    const int base = sigma(l32) * RB + 16 * g;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) kaddr[kb] = base ^ (32 * kb);
+  }
+  // V^T by transposed reads: key row 16kb2 + 8hl + 4t + (m >> 2), column
+  // 32db + 16x + 4(m & 3), m = lane & 15, x = (lane >> 4) & 1
+  int vaddr[NDB];
+  {
+    const int m16 = lane & 15, x16 = (lane >> 4) & 1;
+    const int base = (8 * hl + (m16 >> 2)) * RB + 16 * swz_tr<HD>(m16 >> 2) + 32 * x16 +
+                     16 * ((m16 & 3) >> 1) + 8 * (m16 & 1);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) vaddr[db] = base ^ (64 * db);
+  }
 
   f32x16 o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = zero16();
   float m_run = kNegInf, l_run = 0.f;
-
-  if (kt_begin < kt_end) {
-    stage_load(kt_begin * BK);
-    doc_load(kt_begin * BK);
-    stage_store(0);
-    doc_store(0);
-  }
-  __syncthreads();
-  wait_all_loads();
-
   const float c = prm.scale_log2;
-  for (int kt = kt_begin; kt < kt_end; ++kt) {
-    const int buf = (kt - kt_begin) & 1;
-    const int k0 = kt * BK;
-    const bool has_next = kt + 1 < kt_end;
-    if (has_next) {
-      stage_load(k0 + BK);
-      doc_load(k0 + BK);
-    }
-    const uint8_t* kt_lds = smem + buf * (C::KT + C::VT);
-    const uint8_t* vt_lds = kt_lds + C::KT;
+
+  // tile j (relative to kt_begin) lives in buffer j % 3; its DMA is issued at
+  // the start of tile j - 2 (tiles 0 and 1 in the prologue)
+  const int ntile = kt_end - kt_begin;
+  if (ntile > 0) {
+    dma_tile(B0{}, kt_begin * BK);
+    doc_load(kt_begin * BK);
+    doc_store(0);
+    if (ntile > 1) dma_tile(B1{}, (kt_begin + 1) * BK);
+  }
+  wait_all_loads();
+  __syncthreads();
+
+  auto tile = [&](auto b, int j) {
+    constexpr int B = decltype(b)::value;  // == j % 3
+    const int k0 = (kt_begin + j) * BK;
+    if (j + 1 < ntile) doc_load(k0 + BK);  // key documents of the next tile
+    // buffer (j + 2) % 3 held tile j - 1, released by the last barrier
+    if (j + 2 < ntile) dma_tile(std::integral_constant<int, (B + 2) % 3>{}, k0 + 2 * BK);
+    const uint8_t* kt_lds = kbuf(b);
+    const uint8_t* vt_lds = vbuf(b);
 
     if (k0 <= wave_kmax) {
       bool need_mask = (k0 + BK > sk);
       if (mask == RMX_MASK_CAUSAL) need_mask |= (k0 + BK - 1 > qw0 + off);
       if (mask == RMX_MASK_DOC) {
-        const int kgz = sKg[buf][BK - 1];
-        const int kda = sKd[buf][0], kdz = sKd[buf][BK - 1];
+        const int kgz = sKg[B][BK - 1];
+        const int kda = sKd[B][0], kdz = sKd[B][BK - 1];
         need_mask |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first);
       }
 
-      // ---- S^T = K Q^T
-      f32x16 s[2];
-      s[0] = zero16();
-      s[1] = zero16();
+      // ---- S^T = K Q^T (A = K rows, B = Q in VGPRs); MB blocks of 32 keys
+      f32x16 s[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) s[mb] = zero16();
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
+        for (int mb = 0; mb < MB; ++mb) {
           const bf16x8 a = __builtin_bit_cast(
-              bf16x8, *reinterpret_cast<const u32x4*>(kt_lds + k_lane + mb * 32 * C::RSK + 32 * kb));
+              bf16x8, *reinterpret_cast<const u32x4*>(kt_lds + kaddr[kb] + mb * 32 * RB));
           s[mb] = mfma32(a, qreg[kb], s[mb]);
         }
       }
@@ -241,7 +270,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
       if (need_mask) {
         keep_branch();
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int kl = 32 * mb + sig_row(hl, r);
@@ -249,7 +278,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
             bool ok = key < sk;
             if (mask == RMX_MASK_CAUSAL) ok &= key <= q + off;
             if (mask == RMX_MASK_DOC) {
-              const int kd = sKd[buf][kl], kg = sKg[buf][kl];
+              const int kd = sKd[B][kl], kg = sKg[B][kl];
               ok &= (kd == qd) & (kg <= qg);
             }
             s[mb][r] = ok ? s[mb][r] : kNegInf;
@@ -257,12 +286,19 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
       }
 
       // ---- online softmax (log2 domain, scale folded into the exponent FMA)
-      float mx = kNegInf;
+      // row max as a tree over the scores (short dependency chains)
+      float mxp[2 * MB];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+      for (int t = 0; t < 2 * MB; ++t) {
+        mxp[t] = kNegInf;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[mb][r]);
-      mx = fmaxf(mx, xhalf(mx)) * c;
+        for (int r = 0; r < 8; ++r) mxp[t] = fmaxf(mxp[t], s[t >> 1][8 * (t & 1) + r]);
+      }
+#pragma unroll
+      for (int w = MB; w >= 1; w >>= 1)
+#pragma unroll
+        for (int t = 0; t < w; ++t) mxp[t] = fmaxf(mxp[t], mxp[t + w]);
+      float mx = fmaxf(mxp[0], xhalf(mxp[0])) * c;
       // move the running max only when this tile raises it by more than the
       // slack (or on the first finite tile); otherwise keep the stale max
       const bool raise = mx > m_run + kRescaleSlack;
@@ -275,38 +311,45 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
         m_run = mnew;
       }
       const float mbase = (m_run == kNegInf) ? 0.f : m_run;
-      float rs = 0.f;
-      bf16x8 pb[4];
+      float rsp[2 * MB];  // partial row sums (short dependency chains)
+      bf16x8 pb[2 * MB];
 #pragma unroll
-      for (int kb2 = 0; kb2 < 4; ++kb2) {
+      for (int kb2 = 0; kb2 < 2 * MB; ++kb2) {
         float pv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pv[i] = fast_exp2(fmaf(s[kb2 >> 1][8 * (kb2 & 1) + i], c, -mbase));
-          rs += pv[i];
-        }
+        for (int i = 0; i < 8; ++i) pv[i] = fast_exp2(fmaf(s[kb2 >> 1][8 * (kb2 & 1) + i], c, -mbase));
+        rsp[kb2] = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
         pb[kb2] = pack8_hw(pv);
       }
-      l_run += rs;
+#pragma unroll
+      for (int w = MB; w >= 1; w >>= 1)
+#pragma unroll
+        for (int t = 0; t < w; ++t) rsp[t] += rsp[t + w];
+      l_run += rsp[0];
 
       // ---- O^T += V^T P^T
 #pragma unroll
-      for (int kb2 = 0; kb2 < 4; ++kb2) {
+      for (int kb2 = 0; kb2 < 2 * MB; ++kb2) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          const uint16_t* vp = reinterpret_cast<const uint16_t*>(
-              vt_lds + v_lane + 16 * kb2 * C::RSV + 64 * db);
-          const bf16x8 a = join_bf16x8(lds_read_tr(vp), lds_read_tr(vp + 2 * C::RSV));
+          const uint16_t* vp = reinterpret_cast<const uint16_t*>(vt_lds + vaddr[db] + 16 * kb2 * RB);
+          const bf16x8 a = join_bf16x8(lds_read_tr(vp), lds_read_tr(vp + 2 * RB));
           o[db] = mfma32(a, pb[kb2], o[db]);
         }
       }
     }
 
-    if (has_next) {
-      stage_store(buf ^ 1);
-      doc_store(buf ^ 1);
-    }
-    __syncthreads();
+    // publish tile j + 1 (its DMA was issued a tile ago); tile j + 2's stays in flight
+    if (j + 1 < ntile) doc_store((B + 1) % 3);
+    if (j + 2 < ntile)
+      wait_vm_barrier<2 * C::NDMA>();
+    else
+      wait_vm_barrier<0>();
+  };
+  for (int j = 0; j < ntile; j += 3) {
+    tile(B0{}, j);
+    if (j + 1 < ntile) tile(B1{}, j + 1);
+    if (j + 2 < ntile) tile(B2{}, j + 2);
   }
 
   // ---- epilogue: normalise, lse, merge
@@ -372,19 +415,19 @@ static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* 
   constexpr int BQ = FwdCfg<HD>::BQ;
   FwdParams prm;
   prm.L = L;
-  prm.nprob = n;
   prm.scale_log2 = L.scale * kLog2e;
-  int tot = 0;
+  // longest workgroups (most key tiles) first
+  long long cost[RMX_MAX_BATCHED];
+  int order[RMX_MAX_BATCHED], groups[RMX_MAX_BATCHED], ntile[RMX_MAX_BATCHED];
+  for (int i = 0; i < n; ++i) cost[i] = probs[i].sk;
+  order_by_cost(n, cost, order);
   for (int i = 0; i < n; ++i) {
-    prm.P[i] = probs[i];
-    prm.qtiles[i] = (probs[i].sq + BQ - 1) / BQ;
-    prm.tile_start[i] = tot;
-    tot += L.batch * L.hq * prm.qtiles[i];
+    prm.P[i] = probs[order[i]];
+    groups[i] = L.batch * L.hq;
+    ntile[i] = (prm.P[i].sq + BQ - 1) / BQ;
   }
-  for (int i = n; i <= RMX_MAX_BATCHED; ++i) prm.tile_start[i] = tot;
-  prm.total = tot;
-  if (tot == 0) return hipSuccess;
-  const int grid = (tot + 7) / 8 * 8;
+  const int grid = plan_workgroups(prm.map, n, groups, ntile);
+  if (grid == 0) return hipSuccess;
   if (L.mask == RMX_MASK_CAUSAL)
     hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_CAUSAL>), dim3(grid), dim3(FwdCfg<HD>::NT), 0,
                        stream, prm);

@@ -109,13 +109,6 @@ __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0)
 // Cross-half exchange: value held by lane l ^ 32.
 __device__ __forceinline__ float xhalf(float v) { return __shfl_xor(v, 32, 64); }
 
-// Map a linear workgroup index so that consecutive logical tiles land on the
-// same XCD (the dispatcher deals workgroups round-robin over the 8 XCDs).
-// Requires gridDim.x % 8 == 0.
-__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
-  const int per = nblocks >> 3;
-  return (bid & 7) * per + (bid >> 3);
-}
 
 }  // namespace rmx
 
@@ -188,6 +181,52 @@ __device__ __forceinline__ bf16x8 pack8_hw(const float* v) {
   u[2] = cvt_pk_bf16(v[4], v[5]);
   u[3] = cvt_pk_bf16(v[6], v[7]);
   return __builtin_bit_cast(bf16x8, u);
+}
+
+}  // namespace rmx
+
+namespace rmx {
+
+// ---------------------------------------------------------------------------
+// Direct global -> LDS loads (buffer_load_dwordx4 ... lds). Lane L of the wave
+// writes the 16 bytes at voffset of the buffer to LDS address lds + 16*L
+// (lds must be wave-uniform); offsets at or past num_records write zeros.
+// Completion is counted by vmcnt.
+__device__ void llvm_raw_buffer_load_lds(i32x4 rsrc, __attribute__((address_space(3))) uint32_t* lds,
+                                         int size, int voffset, int soffset, int offset,
+                                         int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+__device__ __forceinline__ void dma16(const i32x4& rsrc, void* lds, int byte_off) {
+  llvm_raw_buffer_load_lds(rsrc, (__attribute__((address_space(3))) uint32_t*)lds, 16, byte_off, 0,
+                           0, 0);
+}
+
+// Workgroup barrier that first waits until at most VM vector-memory operations
+// (LDS DMA included) of this wave are outstanding and all its LDS operations are
+// done. Unlike __syncthreads() it does not wait for every outstanding load, so
+// LDS DMA issued for later tiles stays in flight across it. The memory clobber
+// keeps the compiler from moving memory accesses across it.
+template <int VM>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(VM >= 0 && VM < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(VM) : "memory");
+}
+
+// XOR swizzles of the 16-byte chunks of unpadded LDS rows (HD bf16 per row).
+// Row reads (16 bytes of 16 consecutive rows, rows permuted by sigma):
+template <int HD>
+__device__ __forceinline__ int swz_rows(int r) {
+  return HD == 128 ? sigma(r & 15) : ((r >> 1) & 7);
+}
+// Transposed reads (ds_read_b64_tr_b16 over 4 consecutive rows, 64 bytes each):
+template <int HD>
+__device__ __forceinline__ int swz_tr(int r) {
+  return HD == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+}
+// Both kinds of read on the same tile:
+template <int HD>
+__device__ __forceinline__ int swz_both(int r) {
+  return HD == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
 }
 
 }  // namespace rmx

@@ -29,3 +29,73 @@ hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* d
                                   hipStream_t stream);
 
 }  // namespace rmx
+
+namespace rmx {
+
+// ---------------------------------------------------------------------------
+// Workgroup -> (problem, group, tile) mapping shared by the attention kernels.
+// A "group" is one (batch, head) of a problem (its tiles share K/V or Q/dO) and
+// every group has ntile[p] workgroups. Problems are ordered longest-workgroup
+// first by the launcher. Balanced mode (every problem's group count divisible
+// by 8): the dispatcher deals workgroup ids round-robin over the 8 XCDs, so
+// XCD x = bid % 8 runs ids bid = 8 i + x in order of i; groups g of every
+// problem with g % 8 == x are placed on XCD x (one XCD's L2 serves a group's
+// shared operand, every XCD gets the same share of every problem).
+struct WgMapParams {
+  int nprob;
+  int balanced;
+  int ntile[RMX_MAX_BATCHED];
+  int start[RMX_MAX_BATCHED + 1];  // balanced: per-XCD prefix; else: global prefix
+  int total;                       // workgroups doing work (grid may be larger)
+};
+
+struct WgCoord {
+  int p, group, tile;
+  bool valid;
+};
+
+__device__ __forceinline__ WgCoord map_workgroup(const WgMapParams& m, int bid) {
+  WgCoord c;
+  const int i = m.balanced ? (bid >> 3) : bid;
+  c.valid = m.balanced ? (i < m.start[m.nprob]) : (bid < m.total);
+  int p = 0;
+  while (p + 1 < m.nprob && i >= m.start[p + 1]) ++p;
+  const int local = i - m.start[p];
+  c.p = p;
+  c.tile = local % m.ntile[p];
+  c.group = m.balanced ? (local / m.ntile[p]) * 8 + (bid & 7) : local / m.ntile[p];
+  return c;
+}
+
+// Host side: fill the mapping for problems already in launch order; groups[p] =
+// groups of problem p, ntile[p] = workgroups per group. Returns the grid size.
+inline int plan_workgroups(WgMapParams& m, int n, const int* groups, const int* ntile) {
+  m.nprob = n;
+  m.balanced = n > 0;
+  for (int i = 0; i < n; ++i) m.balanced = m.balanced && groups[i] % 8 == 0;
+  int acc = 0;
+  for (int i = 0; i < n; ++i) {
+    m.ntile[i] = ntile[i] > 0 ? ntile[i] : 1;
+    m.start[i] = acc;
+    acc += (m.balanced ? groups[i] / 8 : groups[i]) * (ntile[i] > 0 ? ntile[i] : 0);
+  }
+  for (int i = n; i <= RMX_MAX_BATCHED; ++i) m.start[i] = acc;
+  m.total = acc;
+  return m.balanced ? 8 * acc : acc;
+}
+
+// Host side: order[] = problem indices sorted by cost[] descending (stable).
+inline void order_by_cost(int n, const long long* cost, int* order) {
+  for (int i = 0; i < n; ++i) order[i] = i;
+  for (int i = 1; i < n; ++i) {
+    const int o = order[i];
+    int j = i - 1;
+    while (j >= 0 && cost[order[j]] < cost[o]) {
+      order[j + 1] = order[j];
+      --j;
+    }
+    order[j + 1] = o;
+  }
+}
+
+}  // namespace rmx
