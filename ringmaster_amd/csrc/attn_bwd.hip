@@ -408,73 +408,87 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
 }
 
 // ---------------------------------------------------------------- dK, dV (KV-major)
-// One workgroup = 4 waves x 32 keys of one (problem, batch, kv head); it walks
-// every q-head of the GQA group and every query tile (64 queries) the mask
-// leaves, so the group fold needs no cross-workgroup reduction. Per query tile
-// and wave:
-//   S  = Q K^T     A = Q rows (LDS), B = K (VGPRs)            16 MFMAs
-//   dP = dO V^T    A = dO rows (LDS), B = V (VGPRs)           16 MFMAs
-//   P = exp2(S c - lse2[q]), dS = P (dP - delta[q])  (lse/delta from LDS)
-//   dV += P^T dO   A = P^T (registers), B = dO^T transposed reads  16 MFMAs
-//   dK += dS^T Q   A = dS^T (registers), B = Q^T transposed reads  16 MFMAs
-template <int HD, int MASK>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams prm) {
-  using T = BwdTiles<HD>;
-  constexpr int NW = 4, NT = NW * 64, BKV = 32 * NW, BQ = 64;
-  constexpr int CH = T::CH, NKB = T::NKB, NDB = T::NDB;
-  constexpr int RS = T::RS_RT;
-  constexpr int QT = BQ * RS;  // bytes of one Q (or dO) tile
-  constexpr int LPT = BQ * CH / NT;
-  static_assert(LPT >= 1 && BQ * CH % NT == 0, "tile split");
+// One workgroup = 128 keys of one (problem, batch, kv head), 8 waves in 4
+// pairs: waves w and w + 4 (which the dispatcher places on the same SIMD) own
+// keys k0 + 32w .. k0 + 32w + 31. The workgroup walks every q-head of the GQA
+// group and every query tile (64 queries) the mask leaves, so the group fold
+// needs no cross-workgroup reduction. Per query tile, in two phases separated
+// by a workgroup barrier:
+//   wave w     (P wave)   phase 1: S = Q K^T (A = Q rows, B = K in VGPRs)
+//                                  P = exp2(S c - lse2[q]) (masked), P -> LDS
+//                         phase 2: dV += P^T dO (A = P^T from registers,
+//                                  B = dO^T by transposed reads)
+//   wave w + 4 (dS wave)  phase 1: dP = dO V^T (A = dO rows, B = V in VGPRs)
+//                         phase 2: dS = P (dP - delta[q]) with P from LDS,
+//                                  dK += dS^T Q (B = Q^T by transposed reads)
+// 16 MFMAs per wave and phase. Each wave holds one 32 x HD accumulator and one
+// of K / V, which leaves room for two waves per SIMD: the P wave's exponentials
+// overlap the dS wave's MFMAs in phase 1, and the other way round in phase 2.
+// Q/dO tiles: direct global->LDS loads into three buffers, issued two tiles
+// ahead; both tiles are read as rows and transposed, so their 16-byte chunks
+// are XOR-swizzled with swz_both.
+template <int HD>
+struct DkdvCfg {
+  static constexpr int NP = 4;                // wave pairs
+  static constexpr int NW = 2 * NP;           // waves per workgroup
+  static constexpr int NT = 64 * NW;
+  static constexpr int BKV = 32 * NP;         // keys per workgroup
+  static constexpr int BQ = 64;               // queries per tile
+  static constexpr int CH = HD / 8;           // 16-byte chunks per row
+  static constexpr int RB = HD * 2;           // LDS row bytes (unpadded, swizzled)
+  static constexpr int QT = BQ * RB;          // bytes of one Q (or dO) tile
+  static constexpr int RPK = 1024 / RB;       // rows per 1 KiB DMA instruction
+  static constexpr int NDMA = QT / 1024 / NW; // DMA instructions per wave per tile and operand
+  static constexpr int NKB = HD / 16;
+  static constexpr int NDB = HD / 32;
+  static_assert(NDMA >= 1 && QT % (1024 * NW) == 0, "tile split");
+};
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * QT];
-  __shared__ __attribute__((aligned(16))) float sL[2][BQ];
-  __shared__ __attribute__((aligned(16))) float sD[2][BQ];
-  __shared__ int sQg[2][BQ];
-  __shared__ int sQd[2][BQ];
+template <int HD, int MASK>
+__global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams prm) {
+  using C = DkdvCfg<HD>;
+  constexpr int BQ = C::BQ, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB, NP = C::NP;
+
+  // three Q and three dO tile buffers (separate objects, so the compiler can
+  // tell the buffer being read from the ones the DMA is filling)
+  __shared__ __attribute__((aligned(1024))) uint8_t sQ0[C::QT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sQ1[C::QT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sQ2[C::QT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sO0[C::QT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sO1[C::QT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sO2[C::QT];
+  // lse (log2 units after the in-place conversion) and delta of each tile
+  __shared__ __attribute__((aligned(512))) float sM0[2 * BQ];
+  __shared__ __attribute__((aligned(512))) float sM1[2 * BQ];
+  __shared__ __attribute__((aligned(512))) float sM2[2 * BQ];
+  // P of each pair in the C-register layout: [pair][32-query half][reg quad][lane]
+  __shared__ __attribute__((aligned(16))) f32x4 sP[NP][2][4][64];
+  __shared__ int sQg[3][BQ];
+  __shared__ int sQd[3][BQ];
   __shared__ int sRange[2];
 
   const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
   if (!wc.valid) return;
   const rmx_attn_layout& L = prm.L;
   const rmx_bwd_problem& P = prm.P[wc.p];
-  const int kt = wc.tile;
   const int kvh = wc.group % L.hkv;
   const int bb = wc.group / L.hkv;
   const int G = L.hq / L.hkv;
   const int sq = P.sq, sk = P.sk;
   constexpr int mask = MASK;
-  const int k0 = kt * BKV;
+  const int k0 = wc.tile * C::BKV;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int pair = wave % NP;
   const int lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int kw0 = k0 + 32 * wave;  // first key of this wave
+  const int kw0 = k0 + 32 * pair;  // first key of this wave pair
   const int key = kw0 + l32;
   const bool kvalid = key < sk;
 
-  bf16x8 kreg[NKB], vreg[NKB];
-  {
-    const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh,
-                                span_bytes(sk, 2 * L.k_ss, HD * 2));
-    const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh,
-                                span_bytes(sk, 2 * L.v_ss, HD * 2));
-    const int ko = key * (int)(2 * L.k_ss) + 16 * hl, vo = key * (int)(2 * L.v_ss) + 16 * hl;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      kreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(krs, ko + 32 * kb));
-      vreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(vrs, vo + 32 * kb));
-    }
-  }
-  int kg = 2147483647, kd = -2;
-  if (mask == RMX_MASK_DOC && kvalid) {
-    kg = P.k_gidx[key];
-    kd = P.doc[kg];
-  }
-
   // ---- query-tile range of the workgroup
   const int off = sk - sq;
-  const int klast = (k0 + BKV < sk ? k0 + BKV : sk) - 1;
+  const int klast = (k0 + C::BKV < sk ? k0 + C::BKV : sk) - 1;
   const int nqt = (sq + BQ - 1) / BQ;
   int qt_begin = 0, qt_end = nqt;
   int kg_first = 0, kg_last = 0, kd_first = 0, kd_last = 0;
@@ -493,7 +507,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     }
     __syncthreads();
     int lo = nqt, hi = -1;
-    for (int t = tid; t < nqt; t += NT) {
+    for (int t = tid; t < nqt; t += C::NT) {
       const int qa = t * BQ, qz = (t * BQ + BQ < sq ? t * BQ + BQ : sq) - 1;
       const int qga = P.q_gidx[qa], qgz = P.q_gidx[qz];
       const int qda = P.doc[qga], qdz = P.doc[qgz];
@@ -510,203 +524,305 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     if (qt_end < qt_begin) qt_end = qt_begin;
   }
   const int nq_iter = qt_end - qt_begin;
-  const int total_iter = nq_iter * G;
+  const int ntile = nq_iter * G;  // (q head, query tile) pairs, q head major
   const int wave_klast = (kw0 + 31 < sk ? kw0 + 31 : sk - 1);
 
-  // ---- Q / dO staging
+  // ---- Q / dO tiles, lse and delta by DMA; query documents (DOC) by wave 0
   const int qss = (int)(2 * L.q_ss), oss = (int)(2 * L.o_ss);
-  u32x4 qst[LPT], ost[LPT];
-  float nl = 0.f, nd = 0.f;
-  int nqg = 0, nqd = 0;
-  auto issue_load = [&](int it) {
-    const int g = it / nq_iter;
+  auto qbuf = [&](auto b) -> uint8_t* {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return sQ0;
+    else if constexpr (B == 1) return sQ1;
+    else return sQ2;
+  };
+  auto obuf = [&](auto b) -> uint8_t* {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return sO0;
+    else if constexpr (B == 1) return sO1;
+    else return sO2;
+  };
+  auto lbuf = [&](auto b) -> float* {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return sM0;
+    else if constexpr (B == 1) return sM1;
+    else return sM2;
+  };
+  auto dbuf = [&](auto b) -> float* { return lbuf(b) + BQ; };
+  // Wave 0 first loads the tile's lse and delta (one dword per lane; rows past
+  // the end read 0, where Q and dO rows are 0 as well, so they add nothing),
+  // then every wave its share of the Q and dO rows: instruction n of a tile
+  // fills LDS bytes [1024 n, 1024 n + 1024), lane L row n*RPK + L/CH, swizzled
+  // chunk L%CH. Wave 0's metadata precedes its tile loads, so a wait that
+  // leaves a later tile's 2*NDMA loads in flight covers it. The loads are the
+  // asm form (dma16_async): the kernel orders every LDS read after them itself.
+  auto dma_tile = [&](auto b, int it) {
     const int qa = (qt_begin + it % nq_iter) * BQ;
-    const int qh = kvh * G + g;
+    const int qh = kvh * G + it / nq_iter;
+    if (wave == 0) {
+      const int64_t lb = bb * L.l_sb + qh * L.l_sh;
+      const uint32_t m = lds_addr(lbuf(b));
+      dma4_async(make_rsrc(P.lse + lb, 4u * sq), m, 4 * (qa + lane));
+      dma4_async(make_rsrc(P.delta + lb, 4u * sq), m + 4 * BQ, 4 * (qa + lane));
+    }
     const i32x4 qrs = make_rsrc(P.q + bb * L.q_sb + qh * L.q_sh, span_bytes(sq, qss, HD * 2));
     const i32x4 ors = make_rsrc(P.dout + bb * L.o_sb + qh * L.o_sh, span_bytes(sq, oss, HD * 2));
+    const uint32_t qd = lds_addr(qbuf(b)), od = lds_addr(obuf(b));
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int cid = tid + i * NT, row = cid / CH, c = cid % CH;
-      qst[i] = buf_load16(qrs, (qa + row) * qss + 16 * c);
-      ost[i] = buf_load16(ors, (qa + row) * oss + 16 * c);
+    for (int i = 0; i < C::NDMA; ++i) {
+      const int n = wave * C::NDMA + i;
+      const int r = n * C::RPK + lane / CH, p = lane % CH;
+      const int ch = 16 * (p ^ swz_both<HD>(r));
+      dma16_async(qrs, qd + 1024 * n, (qa + r) * qss + ch);
+      dma16_async(ors, od + 1024 * n, (qa + r) * oss + ch);
     }
-    if (tid < BQ) {
-      const int qq = qa + tid;
+  };
+  // lse -> log2 units in place, once per tile, by the first dS wave. A row with
+  // lse = -inf attends no key, so every tile holding it takes the masked path,
+  // which discards the +inf exponent.
+  auto lse_to_log2 = [&](auto b) {
+    if (wave == NP) {
+      float* l = lbuf(b);
+      l[lane] = l[lane] * kLog2e;
+    }
+  };
+  int nqg = 0, nqd = 0;
+  auto doc_load = [&](int it) {
+    if (mask == RMX_MASK_DOC && tid < BQ) {
+      const int qq = (qt_begin + it % nq_iter) * BQ + tid;
       if (qq < sq) {
-        const int64_t lr = bb * L.l_sb + qh * L.l_sh + qq;
-        nl = P.lse[lr];  // converted at commit, so the load is not waited for here
-        nd = P.delta[lr];
-        if (mask == RMX_MASK_DOC) {
-          nqg = P.q_gidx[qq];
-          nqd = P.doc[nqg];
-        }
+        nqg = P.q_gidx[qq];
+        nqd = P.doc[nqg];
       } else {
-        nl = kNegInf;  // rows past the end: P == 0
-        nd = 0.f;
-        nqg = -2147483647;
+        nqg = -2147483647;  // rows past the end: masked
         nqd = -1;
       }
     }
   };
-  auto commit = [&](int buf) {
-    uint8_t* qt_l = smem + buf * 2 * QT;
-    uint8_t* ot_l = qt_l + QT;
-#pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int cid = tid + i * NT, row = cid / CH, c = cid % CH;
-      *reinterpret_cast<u32x4*>(qt_l + row * RS + 16 * c) = qst[i];
-      *reinterpret_cast<u32x4*>(ot_l + row * RS + 16 * c) = ost[i];
-    }
-    if (tid < BQ) {
-      // lse in log2 units; rows without any attended key (lse = -inf) get +inf
-      // so that every P of the row is exactly 0
-      sL[buf][tid] = nl == kNegInf ? __builtin_inff() : nl * kLog2e;
-      sD[buf][tid] = nd;
-      sQg[buf][tid] = nqg;
-      sQd[buf][tid] = nqd;
+  auto doc_store = [&](int slot) {
+    if (mask == RMX_MASK_DOC && tid < BQ) {
+      sQg[slot][tid] = nqg;
+      sQd[slot][tid] = nqd;
     }
   };
 
-  const int r_lane = sigma(l32) * RS + 16 * hl;  // Q / dO rows (A of S, dP)
-  const int t_lane = tr_lane_off<RS>(lane);      // Q^T / dO^T (B of dK, dV)
-
-  f32x16 dk[NDB], dv[NDB];
+  // per-lane LDS byte offsets (swizzle folded in): rows (A of S, dP): query row
+  // 32 mb + sigma(l32), chunk 2 kb + hl
+  int raddr[NKB];
+  {
+    const int sr = sigma(l32);
+    const int base = sr * RB + 16 * (hl ^ swz_both<HD>(sr));
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    dk[db] = zero16();
-    dv[db] = zero16();
+    for (int kb = 0; kb < NKB; ++kb) raddr[kb] = base ^ (32 * kb);
   }
+  // transposed reads (B of dV, dK): query rows 16 kb2 + 8 hl + 4 t + (m >> 2),
+  // columns 32 db + 16 x + 4 (m & 3) .. + 3, m = lane & 15, x = (lane >> 4) & 1
+  int taddr[2][NDB];
+  {
+    const int m16 = lane & 15, x16 = (lane >> 4) & 1;
+    const int cc = 2 * x16 + ((m16 & 3) >> 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = 8 * hl + 4 * t + (m16 >> 2);
+      const int base = r * RB + 16 * (cc ^ swz_both<HD>(r)) + 8 * (m16 & 1);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) taddr[t][db] = base ^ (64 * db);
+    }
+  }
+  auto tr_op = [&](const uint8_t* tile, int kb2, int db) -> bf16x8 {
+    const uint8_t* p = tile + 16 * kb2 * RB;
+    return join_bf16x8(lds_read_tr(reinterpret_cast<const uint16_t*>(p + taddr[0][db])),
+                       lds_read_tr(reinterpret_cast<const uint16_t*>(p + taddr[1][db])));
+  };
 
-  if (total_iter > 0) {
-    issue_load(0);
-    commit(0);
+  // ---- prologue: tiles 0 and 1 in flight, documents of tile 0 in LDS
+  if (ntile > 0) {
+    dma_tile(std::integral_constant<int, 0>{}, 0);
+    doc_load(0);
+    doc_store(0);
+    if (ntile > 1) dma_tile(std::integral_constant<int, 1>{}, 1);
   }
-  __syncthreads();
-  wait_all_loads();
 
   const float c = prm.scale_log2;
-  for (int it = 0; it < total_iter; ++it) {
-    const int buf = it & 1;
-    const int qa = (qt_begin + it % nq_iter) * BQ;
-    const bool has_next = it + 1 < total_iter;
-    if (has_next) issue_load(it + 1);
-    const uint8_t* qt_l = smem + buf * 2 * QT;
-    const uint8_t* ot_l = qt_l + QT;
-
-    // Every wave computes every tile of the workgroup's range (masked P is
-    // zero): a branch around the MFMAs would make the loop-carried dK/dV
-    // accumulators change register class at the merge.
+  auto run = [&](auto role) {
+    constexpr bool PW = decltype(role)::value == 0;  // P wave (S, P, dV) or dS wave (dP, dS, dK)
+    bf16x8 kv[NKB];  // K (P wave) or V (dS wave): lane holds row `key`, dims 16 kb + 8 hl ..
     {
-      bool need_mask = (kw0 + 32 > sk);
-      if (mask == RMX_MASK_CAUSAL) need_mask |= (wave_klast > qa + off);
-      if (mask == RMX_MASK_DOC) {
-        const int qga = sQg[buf][0];
-        const int qda = sQd[buf][0];
-        const int qz = (qa + BQ < sq ? BQ : sq - qa) - 1;
-        const int qdz = sQd[buf][qz];
-        need_mask |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga);
-      }
+      const uint16_t* src = PW ? P.k + bb * L.k_sb + kvh * L.k_sh : P.v + bb * L.v_sb + kvh * L.v_sh;
+      const int ss = PW ? (int)(2 * L.k_ss) : (int)(2 * L.v_ss);
+      const i32x4 rs = make_rsrc(src, span_bytes(sk, ss, HD * 2));
+      const int o = key * ss + 16 * hl;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) kv[kb] = __builtin_bit_cast(bf16x8, buf_load16(rs, o + 32 * kb));
+    }
+    int kg = 2147483647, kd = -2;
+    if (PW && mask == RMX_MASK_DOC && kvalid) {
+      kg = P.k_gidx[key];
+      kd = P.doc[kg];
+    }
+    f32x16 acc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[db] = zero16();
+    wait_all_loads();
+    lds_barrier();
+    if (ntile > 0) lse_to_log2(std::integral_constant<int, 0>{});
+    lds_barrier();
 
-      // two halves of 32 queries (mb): S = Q K^T and dP = dO V^T for the half
-      // (rows: queries sigma-permuted; lane: this wave's keys), P and dS, then
-      // dV += P^T dO and dK += dS^T Q (rows: this wave's keys; cols: head dim)
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-          const int o = r_lane + mb * 32 * RS + 32 * kb;
-          const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qt_l + o));
-          s = mfma32(a, kreg[kb], s);
-          const bf16x8 b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ot_l + o));
-          dp = mfma32(b, vreg[kb], dp);
+    auto tile = [&](auto b, int j) {
+      constexpr int B = decltype(b)::value;  // == j % 3
+      using NEXT = std::integral_constant<int, (B + 1) % 3>;
+      const int qa = (qt_begin + j % nq_iter) * BQ;
+      if (j + 1 < ntile) doc_load(j + 1);
+      // buffer (j + 2) % 3 held tile j - 1, released by the last barrier
+      if (j + 2 < ntile) dma_tile(std::integral_constant<int, (B + 2) % 3>{}, j + 2);
+      const uint8_t* qt_l = qbuf(b);
+      const uint8_t* ot_l = obuf(b);
+
+      if constexpr (PW) {
+        // ---- phase 1: S = Q K^T, P
+        bool need_mask = (kw0 + 32 > sk);
+        if (mask == RMX_MASK_CAUSAL) need_mask |= (wave_klast > qa + off);
+        if (mask == RMX_MASK_DOC) {
+          const int qga = sQg[B][0];
+          const int qda = sQd[B][0];
+          const int qz = (qa + BQ < sq ? BQ : sq - qa) - 1;
+          const int qdz = sQd[B][qz];
+          need_mask |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga);
         }
-        bf16x8 pt[2], dst[2];
+        f32x16 s[2];
+        s[0] = zero16();
+        s[1] = zero16();
 #pragma unroll
-        for (int h8 = 0; h8 < 2; ++h8) {
-          float pv[8], dsv[8];
-          const int qb = 32 * mb + 16 * h8 + 8 * hl;  // queries of regs 8*h8 .. 8*h8+7
-          const f32x4 l0 = *reinterpret_cast<const f32x4*>(&sL[buf][qb]);
-          const f32x4 l1 = *reinterpret_cast<const f32x4*>(&sL[buf][qb + 4]);
-          const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sD[buf][qb]);
-          const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sD[buf][qb + 4]);
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float l2 = i < 4 ? l0[i & 3] : l1[i & 3];
-            pv[i] = fast_exp2(fmaf(s[8 * h8 + i], c, -l2));
+          for (int mb = 0; mb < 2; ++mb) {
+            const bf16x8 a =
+                __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qt_l + raddr[kb] + mb * 32 * RB));
+            s[mb] = mfma32(a, kv[kb], s[mb]);
           }
+        bf16x8 pt[4];
+#pragma unroll
+        for (int kb2 = 0; kb2 < 4; ++kb2) {
+          const int mb = kb2 >> 1, h8 = kb2 & 1;
+          const int qb = 16 * kb2 + 8 * hl;  // queries of regs 8 h8 .. 8 h8 + 7
+          const f32x4 l0 = *reinterpret_cast<const f32x4*>(lbuf(b) + qb);
+          const f32x4 l1 = *reinterpret_cast<const f32x4*>(lbuf(b) + qb + 4);
+          float pv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) pv[i] = fast_exp2(fmaf(s[mb][8 * h8 + i], c, -(i < 4 ? l0[i] : l1[i - 4])));
           if (need_mask) {
-        keep_branch();
+            keep_branch();
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
               const int ql = qb + i;
-              const int qq = qa + ql;
               bool ok = kvalid;
-              if (mask == RMX_MASK_CAUSAL) ok &= key <= qq + off;
-              if (mask == RMX_MASK_DOC) {
-                const int qd = sQd[buf][ql], qg = sQg[buf][ql];
-                ok &= (qd == kd) & (kg <= qg);
-              }
+              if (mask == RMX_MASK_CAUSAL) ok &= key <= qa + ql + off;
+              if (mask == RMX_MASK_DOC) ok &= (sQd[B][ql] == kd) & (kg <= sQg[B][ql]);
               pv[i] = ok ? pv[i] : 0.f;
             }
           }
+          f32x4 w0, w1;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float dl = i < 4 ? d0[i & 3] : d1[i & 3];
-            dsv[i] = pv[i] * (dp[8 * h8 + i] - dl);
+          for (int i = 0; i < 4; ++i) {
+            w0[i] = pv[i];
+            w1[i] = pv[4 + i];
           }
-          pt[h8] = pack8_hw(pv);
-          dst[h8] = pack8_hw(dsv);
+          sP[pair][mb][2 * h8][lane] = w0;
+          sP[pair][mb][2 * h8 + 1][lane] = w1;
+          pt[kb2] = pack8_hw(pv);
         }
+        lds_barrier();
+        // ---- phase 2: dV += P^T dO
 #pragma unroll
-        for (int h8 = 0; h8 < 2; ++h8)
+        for (int kb2 = 0; kb2 < 4; ++kb2)
 #pragma unroll
-          for (int db = 0; db < NDB; ++db) {
-            const int kb2 = 2 * mb + h8;
-            dv[db] = mfma32(pt[h8], tr_operand<RS>(ot_l, t_lane, kb2, db), dv[db]);
-            dk[db] = mfma32(dst[h8], tr_operand<RS>(qt_l, t_lane, kb2, db), dk[db]);
-          }
-      }
-    }
-
-    if (has_next) commit(buf ^ 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: lane (hl, d) holds rows key = kw0 + c_row(hl, r)
-  const float scale = L.scale;
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    const int d = 32 * db + l32;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kk = kw0 + c_row(hl, r);
-      if (kk >= sk) continue;
-      const float gk = dk[db][r] * scale, gv = dv[db][r];
-      const int64_t ao = bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + d;
-      const int64_t bo = bb * L.dk_sb + (int64_t)kk * L.dk_ss + kvh * L.dk_sh + d;
-      const int mode = P.dkv_mode;
-      if (mode == RMX_GRAD_WRITE_F32) {
-        P.dk_acc[ao] = gk;
-        P.dv_acc[ao] = gv;
-      } else if (mode == RMX_GRAD_ACC_F32) {
-        P.dk_acc[ao] += gk;
-        P.dv_acc[ao] += gv;
-      } else if (mode == RMX_GRAD_ACC_FINAL) {
-        P.dk[bo] = f2bf(P.dk_acc[ao] + gk);
-        P.dv[bo] = f2bf(P.dv_acc[ao] + gv);
+          for (int db = 0; db < NDB; ++db) acc[db] = mfma32(pt[kb2], tr_op(ot_l, kb2, db), acc[db]);
       } else {
-        P.dk[bo] = f2bf(gk);
-        P.dv[bo] = f2bf(gv);
+        // ---- phase 1: dP = dO V^T
+        f32x16 dp[2];
+        dp[0] = zero16();
+        dp[1] = zero16();
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb) {
+            const bf16x8 a =
+                __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ot_l + raddr[kb] + mb * 32 * RB));
+            dp[mb] = mfma32(a, kv[kb], dp[mb]);
+          }
+        // tile j + 1's lse landed before the last barrier
+        if (j + 1 < ntile) lse_to_log2(NEXT{});
+        lds_barrier();
+        // ---- phase 2: dS = P (dP - delta), dK += dS^T Q
+#pragma unroll
+        for (int kb2 = 0; kb2 < 4; ++kb2) {
+          const int mb = kb2 >> 1, h8 = kb2 & 1;
+          const int qb = 16 * kb2 + 8 * hl;
+          const f32x4 d0 = *reinterpret_cast<const f32x4*>(dbuf(b) + qb);
+          const f32x4 d1 = *reinterpret_cast<const f32x4*>(dbuf(b) + qb + 4);
+          const f32x4 p0 = sP[pair][mb][2 * h8][lane];
+          const f32x4 p1 = sP[pair][mb][2 * h8 + 1][lane];
+          float dsv[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dsv[i] = p0[i] * (dp[mb][8 * h8 + i] - d0[i]);
+            dsv[4 + i] = p1[i] * (dp[mb][8 * h8 + 4 + i] - d1[i]);
+          }
+          const bf16x8 dst = pack8_hw(dsv);
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) acc[db] = mfma32(dst, tr_op(qt_l, kb2, db), acc[db]);
+        }
+      }
+
+      // publish tile j + 1 (its DMA was issued a tile ago); tile j + 2's stays in flight
+      if (j + 1 < ntile) doc_store((B + 1) % 3);
+      if (j + 2 < ntile)
+        wait_vm_barrier<2 * C::NDMA>();
+      else
+        wait_vm_barrier<0>();
+    };
+    for (int j = 0; j < ntile; j += 3) {
+      tile(std::integral_constant<int, 0>{}, j);
+      if (j + 1 < ntile) tile(std::integral_constant<int, 1>{}, j + 1);
+      if (j + 2 < ntile) tile(std::integral_constant<int, 2>{}, j + 2);
+    }
+
+    // ---- epilogue: lane (hl, d) holds rows key = kw0 + c_row(hl, r)
+    const float sc = PW ? 1.f : L.scale;
+    float* gacc = PW ? P.dv_acc : P.dk_acc;
+    uint16_t* gbf = PW ? P.dv : P.dk;
+    const int mode = P.dkv_mode;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int d = 32 * db + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk = kw0 + c_row(hl, r);
+        if (kk >= sk) continue;
+        const float g = acc[db][r] * sc;
+        const int64_t ao = bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + d;
+        const int64_t bo = bb * L.dk_sb + (int64_t)kk * L.dk_ss + kvh * L.dk_sh + d;
+        if (mode == RMX_GRAD_WRITE_F32) {
+          gacc[ao] = g;
+        } else if (mode == RMX_GRAD_ACC_F32) {
+          gacc[ao] += g;
+        } else if (mode == RMX_GRAD_ACC_FINAL) {
+          gbf[bo] = f2bf(gacc[ao] + g);
+        } else {
+          gbf[bo] = f2bf(g);
+        }
       }
     }
-  }
+  };
+  if (wave < NP)
+    run(std::integral_constant<int, 0>{});
+  else
+    run(std::integral_constant<int, 1>{});
 }
 
 template <int HD>
 static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                                hipStream_t stream) {
-  constexpr int BQ_DQ = 256, BKV = 128;
+  constexpr int BQ_DQ = 256, BKV = DkdvCfg<HD>::BKV;
   BwdParams pq, pk;
   pq.L = L;
   pk.L = L;
@@ -745,11 +861,11 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
   if (tk > 0) {
     const dim3 grid(tk);
     if (L.mask == RMX_MASK_CAUSAL)
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL>), grid, dim3(256), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     else if (L.mask == RMX_MASK_DOC)
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_DOC>), grid, dim3(256), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_DOC>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     else
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_FULL>), grid, dim3(256), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_FULL>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -200,16 +200,52 @@ __device__ __forceinline__ void dma16(const i32x4& rsrc, void* lds, int byte_off
   llvm_raw_buffer_load_lds(rsrc, (__attribute__((address_space(3))) uint32_t*)lds, 16, byte_off, 0,
                            0, 0);
 }
+// The same loads written as inline asm (LDS byte address in M0, set by the
+// compiler through the {m0} operand). The compiler does not see these as LDS
+// writes, so it inserts no waits for them at later LDS reads (its alias
+// tracking of LDS DMA falls back to waiting for every outstanding DMA when a
+// kernel has more DMA targets than it can tell apart); the kernel orders them
+// itself with wait_vm_barrier. Loads the compiler cannot see only make its own
+// vmcnt waits stricter, never weaker. The s_nop covers the M0 -> LDS DMA hazard.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void dma16_async(const i32x4& rsrc, uint32_t lds, int byte_off) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(rsrc),
+               "{m0}"(lds)
+               : "memory");
+}
+// One dword per lane: lane L writes LDS address lds + 4*L.
+__device__ __forceinline__ void dma4_async(const i32x4& rsrc, uint32_t lds, int byte_off) {
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(byte_off), "s"(rsrc),
+               "{m0}"(lds)
+               : "memory");
+}
 
 // Workgroup barrier that first waits until at most VM vector-memory operations
 // (LDS DMA included) of this wave are outstanding and all its LDS operations are
 // done. Unlike __syncthreads() it does not wait for every outstanding load, so
-// LDS DMA issued for later tiles stays in flight across it. The memory clobber
-// keeps the compiler from moving memory accesses across it.
+// LDS DMA issued for later tiles stays in flight across it. The wait is the
+// s_waitcnt builtin, not inline asm, so that the compiler's own wait insertion
+// knows which loads it has retired (it would otherwise wait for LDS DMA again
+// before the next reads); the empty asm statements keep memory accesses from
+// moving across the barrier. Encoding (gfx9): vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8], vmcnt[15:14].
 template <int VM>
 __device__ __forceinline__ void wait_vm_barrier() {
-  static_assert(VM >= 0 && VM < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(VM) : "memory");
+  static_assert(VM >= 0 && VM < 16, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(VM | (7 << 4));  // vmcnt(VM) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// Workgroup barrier after this wave's LDS operations only (vector-memory loads,
+// LDS DMA included, stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // XOR swizzles of the 16-byte chunks of unpadded LDS rows (HD bf16 per row).
