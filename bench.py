@@ -311,11 +311,12 @@ def main():
     torch.cuda.empty_cache()
     extras = {}
     if not args.no_extras:
-        extras["shard_qkv_configs2"] = shard_workload(10, 2)
+        # sub-millisecond kernels: enough timed repetitions for a stable average
+        extras["shard_qkv_configs2"] = shard_workload(30, 3)
         torch.cuda.empty_cache()
-        extras["lse_merge_configs1"] = merge_workload(20, 3)
+        extras["lse_merge_configs1"] = merge_workload(50, 5)
         torch.cuda.empty_cache()
-        extras["cp_linear_scan_configs4"] = scan_workload(10, 2)
+        extras["cp_linear_scan_configs4"] = scan_workload(30, 3)
         torch.cuda.empty_cache()
         extras["block_configs1"] = block_workload(3, 1)
         torch.cuda.empty_cache()

@@ -13,22 +13,86 @@
 // The backward is the exact gradient of the same map (what autograd through
 // the reference's loop, cumprod and AllGatherCP computes):
 //   g_t = dh_t + a_{t+1} g_{t+1};  db_t = g_t;  da_t = sum_group g_t h_{t-1}.
+// When a wave's channels share one decay, da is reduced across the wave for 16
+// steps at a time (and, when the workgroup shares one decay, summed per step in
+// LDS and added to da once per workgroup at the end).
+#include <type_traits>
+
 #include "rmx_kernels.h"
 
 namespace rmx {
 
-// AMODE 0: V=4 channels share one decay per step (group size % 4 == 0)
-// AMODE 1: V=4 channels, elementwise decay (groups == d)
-// AMODE 2: V=1, any grouping
-template <int AMODE>
+// V consecutive fp32 channels (V = 1, 2, 4) as one load / store. Every
+// channel row is read once per pass, so the loads are non-temporal too.
+template <int V>
+__device__ __forceinline__ void ldv(const float* p, float* o) {
+  if constexpr (V == 4) {
+    const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+#pragma unroll
+    for (int v = 0; v < 4; ++v) o[v] = x[v];
+  } else if constexpr (V == 2) {
+    const f32x2 x = __builtin_nontemporal_load(reinterpret_cast<const f32x2*>(p));
+    o[0] = x[0];
+    o[1] = x[1];
+  } else {
+    o[0] = __builtin_nontemporal_load(p);
+  }
+}
+// Stores are non-temporal: the scan outputs stream past the caches (h is read
+// back only by the backward, long after).
+template <int V>
+__device__ __forceinline__ void stv(float* p, const float* o) {
+  if constexpr (V == 4) {
+    __builtin_nontemporal_store(f32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<f32x4*>(p));
+  } else if constexpr (V == 2) {
+    __builtin_nontemporal_store(f32x2{o[0], o[1]}, reinterpret_cast<f32x2*>(p));
+  } else {
+    __builtin_nontemporal_store(o[0], p);
+  }
+}
+
+// Sum over the 64 lanes of a wave of 16 per-lane values (one per step): a
+// transposing butterfly in which, at the stage with mask M, each lane keeps the
+// half of its partial sums selected by lane bit M and adds the partner's copy
+// of that half (17 exchanges for 16 steps). Returns the wave sum of step
+// u = 8 b5 + 4 b4 + 2 b3 + b2 of the lane (b = lane bits, so the lanes with
+// b1 = b0 = 0 hold all 16 steps between them) and sets `u`.
+__device__ __forceinline__ float wave_sum16(float (&part)[16], int lane, int& u) {
+  auto stage = [&](auto mask, auto halfc) {
+    constexpr int M = decltype(mask)::value, H = decltype(halfc)::value;
+    const bool hi = (lane & M) != 0;
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const float keep = hi ? part[H + i] : part[i];
+      const float send = hi ? part[i] : part[H + i];
+      part[i] = keep + __shfl_xor(send, M, 64);
+    }
+  };
+  stage(std::integral_constant<int, 32>{}, std::integral_constant<int, 8>{});
+  stage(std::integral_constant<int, 16>{}, std::integral_constant<int, 4>{});
+  stage(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
+  stage(std::integral_constant<int, 4>{}, std::integral_constant<int, 1>{});
+  float x = part[0];
+  x += __shfl_xor(x, 2, 64);
+  x += __shfl_xor(x, 1, 64);
+  u = ((lane >> 2) & 1) | (((lane >> 3) & 1) << 1) | (((lane >> 4) & 1) << 2) |
+      (((lane >> 5) & 1) << 3);
+  return x;
+}
+
+// AMODE 0: the V channels of a thread share one decay per step (group size % V == 0)
+// AMODE 1: elementwise decay (groups == d)
+// AMODE 2: V = 1, any grouping
+// V channels per thread: fewer channels per thread means more waves in flight
+// (each wave waits for its block of U steps before computing it).
+template <int AMODE, int V>
 __global__ __launch_bounds__(256) void linear_scan_fwd_kernel(const float* __restrict__ a,
                                                               const float* __restrict__ b,
                                                               float* __restrict__ h,
                                                               float* __restrict__ cs, int batch,
                                                               int L, int d, int groups,
                                                               int world) {
-  constexpr int V = AMODE == 2 ? 1 : 4;
-  constexpr int U = 8;  // steps in flight per thread
+  constexpr int U = 16;  // steps in flight per thread (enough bytes in flight for HBM)
   const int per_b = d / V;
   const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (t >= (int64_t)batch * per_b) return;
@@ -58,17 +122,9 @@ __global__ __launch_bounds__(256) void linear_scan_fwd_kernel(const float* __res
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t ts = t0 + tt + u;
-        if (V == 4) {
-          const f32x4 x = *reinterpret_cast<const f32x4*>(bp + ts * d);
-#pragma unroll
-          for (int v = 0; v < V; ++v) bv[u][v] = x[v];
-        } else {
-          bv[u][0] = bp[ts * d];
-        }
+        ldv<V>(bp + ts * d, bv[u]);
         if (AMODE == 1) {
-          const f32x4 y = *reinterpret_cast<const f32x4*>(ap + ts * groups + c);
-#pragma unroll
-          for (int v = 0; v < V; ++v) av[u][v] = y[v];
+          ldv<V>(ap + ts * groups + c, av[u]);
         } else {
           const float s = ap[ts * groups + g];
 #pragma unroll
@@ -85,12 +141,7 @@ __global__ __launch_bounds__(256) void linear_scan_fwd_kernel(const float* __res
           cum[v] = cum[v] * av[u][v];
           o[v] = loc[v] + cum[v] * H[v];
         }
-        if (V == 4) {
-          *reinterpret_cast<f32x4*>(hp + ts * d) = f32x4{o[0], o[V > 1 ? 1 : 0], o[V > 2 ? 2 : 0],
-                                                          o[V > 3 ? 3 : 0]};
-        } else {
-          hp[ts * d] = o[0];
-        }
+        stv<V>(hp + ts * d, o);
       }
     }
     for (; tt < Ls; ++tt) {
@@ -116,15 +167,19 @@ __global__ __launch_bounds__(256) void linear_scan_fwd_kernel(const float* __res
   }
 }
 
-template <int AMODE, bool WAVE_REDUCE>
+// WAVE_REDUCE: a wave's 64 V channels share one decay; da is reduced across
+// the wave. LDS_DA (with WAVE_REDUCE): the whole workgroup's 256 V channels
+// share one decay; the wave sums are accumulated per step in LDS (dynamic, L floats)
+// and added to da once per workgroup at the end, so no global atomic is in
+// flight during the main loop.
+template <int AMODE, int V, bool WAVE_REDUCE, bool LDS_DA>
 __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __restrict__ a,
                                                               const float* __restrict__ h,
                                                               const float* __restrict__ dh,
                                                               float* __restrict__ da,
                                                               float* __restrict__ db, int batch,
                                                               int L, int d, int groups) {
-  constexpr int V = AMODE == 2 ? 1 : 4;
-  constexpr int U = 8;
+  constexpr int U = 16;
   const int per_b = d / V;
   const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const bool valid = t < (int64_t)batch * per_b;
@@ -139,6 +194,11 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
   float* dbp = db + (int64_t)bb * L * d + c;
   float* dap = da + (int64_t)bb * L * groups;
 
+  extern __shared__ float sDa[];  // [L] when LDS_DA
+  if (LDS_DA) {
+    for (int i = threadIdx.x; i < L; i += 256) sDa[i] = 0.f;
+    __syncthreads();
+  }
   float gacc[V], anext[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
@@ -148,10 +208,11 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
   auto emit = [&](int64_t ts, const float* gv, const float* hprev) {
     if (AMODE == 1) {
       if (valid) {
-        f32x4 cur = *reinterpret_cast<const f32x4*>(dap + ts * groups + c);
+        float cur[V];
+        ldv<V>(dap + ts * groups + c, cur);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) cur[v] += gv[v] * hprev[v];
-        *reinterpret_cast<f32x4*>(dap + ts * groups + c) = cur;
+        for (int v = 0; v < V; ++v) cur[v] += gv[v] * hprev[v];
+        stv<V>(dap + ts * groups + c, cur);
       }
     } else if (AMODE == 2 && gs == 1) {
       if (valid) dap[ts * groups + c] += gv[0] * hprev[0];
@@ -162,7 +223,12 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
       if (WAVE_REDUCE) {
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
-        if ((threadIdx.x & 63) == 0 && valid) atomicAdd(dap + ts * groups + g, part);
+        if ((threadIdx.x & 63) == 0 && valid) {
+          if (LDS_DA)
+            atomicAdd(&sDa[ts], part);
+          else
+            atomicAdd(dap + ts * groups + g, part);
+        }
       } else {
         atomicAdd(dap + ts * groups + g, part);
       }
@@ -176,23 +242,15 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
     for (int u = 0; u < U; ++u) {
       const int64_t ts = ts_hi - u;
       if (valid) {
-        if (V == 4) {
-          const f32x4 x = *reinterpret_cast<const f32x4*>(gp + ts * d);
-          const f32x4 y = ts > 0 ? *reinterpret_cast<const f32x4*>(hp + (ts - 1) * d)
-                                 : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            gv[u][v] = x[v];
-            hv[u][v] = y[v];
-          }
+        ldv<V>(gp + ts * d, gv[u]);
+        if (ts > 0) {
+          ldv<V>(hp + (ts - 1) * d, hv[u]);
         } else {
-          gv[u][0] = gp[ts * d];
-          hv[u][0] = ts > 0 ? hp[(ts - 1) * d] : 0.f;
+#pragma unroll
+          for (int v = 0; v < V; ++v) hv[u][v] = 0.f;
         }
         if (AMODE == 1) {
-          const f32x4 z = *reinterpret_cast<const f32x4*>(ap + ts * groups + c);
-#pragma unroll
-          for (int v = 0; v < V; ++v) av[u][v] = z[v];
+          ldv<V>(ap + ts * groups + c, av[u]);
         } else {
           const float s = ap[ts * groups + g];
 #pragma unroll
@@ -207,6 +265,7 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
         }
       }
     }
+    float part[U];  // this lane's share of da at step ts_hi - u (wave-reduced path)
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t ts = ts_hi - u;
@@ -217,15 +276,26 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
         o[v] = gacc[v];
         anext[v] = av[u][v];
       }
-      if (valid) {
-        if (V == 4) {
-          *reinterpret_cast<f32x4*>(dbp + ts * d) =
-              f32x4{o[0], o[V > 1 ? 1 : 0], o[V > 2 ? 2 : 0], o[V > 3 ? 3 : 0]};
-        } else {
-          dbp[ts * d] = o[0];
-        }
+      if (valid) stv<V>(dbp + ts * d, o);
+      if (WAVE_REDUCE) {
+        float pp = 0.f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) pp += o[v] * hv[u][v];
+        part[u] = pp;
+      } else {
+        emit(ts, o, hv[u]);
       }
-      emit(ts, o, hv[u]);
+    }
+    if constexpr (WAVE_REDUCE) {
+      static_assert(U == 16, "butterfly over 16 steps");
+      int u;
+      const float sum = wave_sum16(part, threadIdx.x & 63, u);
+      if ((threadIdx.x & 3) == 0 && valid) {
+        if (LDS_DA)
+          atomicAdd(&sDa[ts_hi - u], sum);
+        else
+          atomicAdd(dap + (int64_t)(ts_hi - u) * groups + g, sum);
+      }
     }
   }
   for (; ts_hi >= 0; --ts_hi) {
@@ -243,12 +313,21 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
     }
     emit(ts, o, hv);
   }
+  if (LDS_DA) {
+    __syncthreads();
+    if (valid)
+      for (int i = threadIdx.x; i < L; i += 256) atomicAdd(dap + (int64_t)i * groups + g, sDa[i]);
+  }
 }
+
+// Channels per thread V and decay mode; WAVE_REDUCE needs a wave's 64 V
+// channels in one group, LDS_DA a workgroup's 256 V channels.
+static constexpr int kScanV = 2;
 
 static int scan_amode(int d, int groups) {
   const int gs = d / groups;
-  if (d % 4 == 0 && gs % 4 == 0) return 0;
-  if (d % 4 == 0 && gs == 1) return 1;
+  if (d % kScanV == 0 && gs % kScanV == 0) return 0;
+  if (d % kScanV == 0 && gs == 1) return 1;
   return 2;
 }
 
@@ -256,18 +335,18 @@ hipError_t launch_linear_scan_fwd(const float* a, const float* b, float* h, floa
                                   int L, int d, int groups, int world, hipStream_t stream) {
   if ((int64_t)batch * L * d == 0) return hipSuccess;
   const int mode = scan_amode(d, groups);
-  const int V = mode == 2 ? 1 : 4;
+  const int V = mode == 2 ? 1 : kScanV;
   const int64_t n = (int64_t)batch * (d / V);
   const unsigned grid = (unsigned)((n + 255) / 256);
   if (mode == 0)
-    hipLaunchKernelGGL(linear_scan_fwd_kernel<0>, dim3(grid), dim3(256), 0, stream, a, b, h, cs,
-                       batch, L, d, groups, world);
+    hipLaunchKernelGGL((linear_scan_fwd_kernel<0, kScanV>), dim3(grid), dim3(256), 0, stream, a, b,
+                       h, cs, batch, L, d, groups, world);
   else if (mode == 1)
-    hipLaunchKernelGGL(linear_scan_fwd_kernel<1>, dim3(grid), dim3(256), 0, stream, a, b, h, cs,
-                       batch, L, d, groups, world);
+    hipLaunchKernelGGL((linear_scan_fwd_kernel<1, kScanV>), dim3(grid), dim3(256), 0, stream, a, b,
+                       h, cs, batch, L, d, groups, world);
   else
-    hipLaunchKernelGGL(linear_scan_fwd_kernel<2>, dim3(grid), dim3(256), 0, stream, a, b, h, cs,
-                       batch, L, d, groups, world);
+    hipLaunchKernelGGL((linear_scan_fwd_kernel<2, 1>), dim3(grid), dim3(256), 0, stream, a, b, h,
+                       cs, batch, L, d, groups, world);
   return hipGetLastError();
 }
 
@@ -277,25 +356,26 @@ hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* d
   (void)world;
   if ((int64_t)batch * L * d == 0) return hipSuccess;
   const int mode = scan_amode(d, groups);
-  const int V = mode == 2 ? 1 : 4;
+  const int V = mode == 2 ? 1 : kScanV;
   const int gs = d / groups;
   const int64_t n = (int64_t)batch * (d / V);
   const unsigned grid = (unsigned)((n + 255) / 256);
   if (mode == 0) {
-    // a 64-lane wave covers 256 consecutive channels; reduce in-wave when they
-    // all belong to one group
-    if (gs % 256 == 0)
-      hipLaunchKernelGGL((linear_scan_bwd_kernel<0, true>), dim3(grid), dim3(256), 0, stream, a, h,
-                         dh, da, db, batch, L, d, groups);
+    if (gs % (256 * kScanV) == 0 && L <= 16384)
+      hipLaunchKernelGGL((linear_scan_bwd_kernel<0, kScanV, true, true>), dim3(grid), dim3(256),
+                         (size_t)L * sizeof(float), stream, a, h, dh, da, db, batch, L, d, groups);
+    else if (gs % (64 * kScanV) == 0)
+      hipLaunchKernelGGL((linear_scan_bwd_kernel<0, kScanV, true, false>), dim3(grid), dim3(256), 0,
+                         stream, a, h, dh, da, db, batch, L, d, groups);
     else
-      hipLaunchKernelGGL((linear_scan_bwd_kernel<0, false>), dim3(grid), dim3(256), 0, stream, a,
-                         h, dh, da, db, batch, L, d, groups);
+      hipLaunchKernelGGL((linear_scan_bwd_kernel<0, kScanV, false, false>), dim3(grid), dim3(256),
+                         0, stream, a, h, dh, da, db, batch, L, d, groups);
   } else if (mode == 1) {
-    hipLaunchKernelGGL((linear_scan_bwd_kernel<1, false>), dim3(grid), dim3(256), 0, stream, a, h,
-                       dh, da, db, batch, L, d, groups);
+    hipLaunchKernelGGL((linear_scan_bwd_kernel<1, kScanV, false, false>), dim3(grid), dim3(256), 0,
+                       stream, a, h, dh, da, db, batch, L, d, groups);
   } else {
-    hipLaunchKernelGGL((linear_scan_bwd_kernel<2, false>), dim3(grid), dim3(256), 0, stream, a, h,
-                       dh, da, db, batch, L, d, groups);
+    hipLaunchKernelGGL((linear_scan_bwd_kernel<2, 1, false, false>), dim3(grid), dim3(256), 0,
+                       stream, a, h, dh, da, db, batch, L, d, groups);
   }
   return hipGetLastError();
 }

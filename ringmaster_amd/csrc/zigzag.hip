@@ -8,12 +8,52 @@
 //
 // A token is an opaque row of row_bytes bytes; the kernel moves rows in the
 // widest unit (16/8/4/1 bytes) that divides row_bytes and every base address,
-// one unit per thread per grid-stride step, so consecutive lanes touch
-// consecutive bytes of a row (full 64-byte HBM bursts). Padding rows are
-// copied from a caller-provided pad row (zeros when it is NULL).
+// so consecutive lanes touch consecutive bytes of a row (full 64-byte HBM
+// bursts). Up to 2^31 units, one unit per thread with 32-bit index arithmetic
+// (multiply-high division); beyond, a grid-stride loop with 64-bit indices.
+// Padding rows are copied from a caller-provided pad row (zeros when NULL).
+#include "rmx_fastdiv.h"
 #include "rmx_kernels.h"
 
 namespace rmx {
+
+template <typename U>
+__global__ __launch_bounds__(256) void zigzag_kernel32(const char* __restrict__ src,
+                                                       char* __restrict__ dst, int seq, int world,
+                                                       int rank, uint32_t nunits, uint32_t half,
+                                                       FastDiv f_upr, FastDiv f_local,
+                                                       FastDiv f_batch, int64_t row_bytes,
+                                                       int64_t bstride,
+                                                       const char* __restrict__ pad_row,
+                                                       int scatter) {
+  const uint32_t u = blockIdx.x * 256u + threadIdx.x;
+  if (u >= nunits) return;
+  const uint32_t row = fdiv(u, f_upr);  // shard row (rank-major over all ranks when rank < 0)
+  const uint32_t col = u - row * f_upr.d;
+  const uint32_t rb = fdiv(row, f_local);
+  const uint32_t i = row - rb * f_local.d;  // position inside the rank's shard
+  const uint32_t rr = fdiv(rb, f_batch);
+  const uint32_t b = rb - rr * f_batch.d;
+  const int64_t r = rank < 0 ? (int64_t)rr : rank;
+  const int64_t g = i < half ? r * half + i : (2 * world - 1 - r) * half + (i - half);
+  const int64_t shard_off = (int64_t)row * row_bytes;
+  const int64_t full_off = (int64_t)b * bstride + g * row_bytes;
+  // the destination streams past the caches (non-temporal stores)
+  if (scatter) {
+    if (g < seq)
+      __builtin_nontemporal_store(reinterpret_cast<const U*>(src + shard_off)[col],
+                                  reinterpret_cast<U*>(dst + full_off) + col);
+  } else {
+    U v;
+    __builtin_memset(&v, 0, sizeof(U));
+    if (g < seq) {
+      v = reinterpret_cast<const U*>(src + full_off)[col];
+    } else if (pad_row) {
+      v = reinterpret_cast<const U*>(pad_row)[col];
+    }
+    __builtin_nontemporal_store(v, reinterpret_cast<U*>(dst + shard_off) + col);
+  }
+}
 
 template <typename U>
 __global__ __launch_bounds__(256) void zigzag_kernel(const char* __restrict__ src,
@@ -55,12 +95,8 @@ __global__ __launch_bounds__(256) void zigzag_kernel(const char* __restrict__ sr
   }
 }
 
-struct alignas(16) U16 {
-  uint32_t w[4];
-};
-struct alignas(8) U8 {
-  uint32_t w[2];
-};
+typedef u32x4 U16;  // 16- and 8-byte units (vector types, so stores can be non-temporal)
+typedef u32x2 U8;
 
 hipError_t launch_zigzag(const void* src, void* dst, int batch, int seq, int world, int rank,
                          int64_t row_bytes, int64_t bstride, const void* pad_row, int scatter,
@@ -73,6 +109,35 @@ hipError_t launch_zigzag(const void* src, void* dst, int batch, int seq, int wor
   const int unit = (al % 16 == 0) ? 16 : (al % 8 == 0) ? 8 : (al % 4 == 0) ? 4 : 1;
   const int64_t upr = row_bytes / unit;
   const int64_t nunits = nrows * upr;
+  if (nunits < (int64_t(1) << 31)) {
+    const int64_t half = total_padded / (2 * world);
+    const FastDiv fu = make_fastdiv((uint32_t)upr), fl = make_fastdiv((uint32_t)(2 * half)),
+                  fb = make_fastdiv((uint32_t)batch);
+    const dim3 grid((unsigned)((nunits + 255) / 256));
+    const char* s = reinterpret_cast<const char*>(src);
+    const char* pr = reinterpret_cast<const char*>(pad_row);
+    char* d = reinterpret_cast<char*>(dst);
+    const uint32_t nu = (uint32_t)nunits, hf = (uint32_t)half;
+    switch (unit) {
+      case 16:
+        hipLaunchKernelGGL(zigzag_kernel32<U16>, grid, dim3(256), 0, stream, s, d, seq, world, rank,
+                           nu, hf, fu, fl, fb, row_bytes, bstride, pr, scatter);
+        break;
+      case 8:
+        hipLaunchKernelGGL(zigzag_kernel32<U8>, grid, dim3(256), 0, stream, s, d, seq, world, rank,
+                           nu, hf, fu, fl, fb, row_bytes, bstride, pr, scatter);
+        break;
+      case 4:
+        hipLaunchKernelGGL(zigzag_kernel32<uint32_t>, grid, dim3(256), 0, stream, s, d, seq, world,
+                           rank, nu, hf, fu, fl, fb, row_bytes, bstride, pr, scatter);
+        break;
+      default:
+        hipLaunchKernelGGL(zigzag_kernel32<uint8_t>, grid, dim3(256), 0, stream, s, d, seq, world,
+                           rank, nu, hf, fu, fl, fb, row_bytes, bstride, pr, scatter);
+        break;
+    }
+    return hipGetLastError();
+  }
   int64_t blocks = (nunits + 255) / 256;
   if (blocks > 256 * 128) blocks = 256 * 128;
   const char* s = reinterpret_cast<const char*>(src);
