@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 1
+#define RMX_ABI_VERSION 2
 
 /* error codes */
 #define RMX_OK 0
@@ -37,7 +37,7 @@ extern "C" {
 /* block mask kinds (ring/kernels.py:64-67, ring/varlen_blocks.py:51-58) */
 #define RMX_MASK_FULL 0   /* every (q, k) pair attends */
 #define RMX_MASK_CAUSAL 1 /* bottom-right aligned causal: k <= q + (sk - sq) */
-#define RMX_MASK_DOC 2    /* doc[qg] == doc[kg] && kg <= qg on global indices */
+#define RMX_MASK_DOC 2    /* q_doc[q] == k_doc[k] && k_gidx[k] <= q_gidx[q] */
 
 /* forward epilogue modes (online-softmax merge, ring/merge.py:20-31) */
 #define RMX_FWD_WRITE 0       /* out/lse := this block's (out, lse); acc_out (nullable)
@@ -84,7 +84,9 @@ typedef struct rmx_fwd_problem {
   float* acc_lse;       /* fp32 running lse (ACC_* modes) */
   const int32_t* q_gidx; /* RMX_MASK_DOC: global token index of each q row (strictly increasing) */
   const int32_t* k_gidx; /* RMX_MASK_DOC: global token index of each k row (strictly increasing) */
-  const int32_t* doc;    /* RMX_MASK_DOC: document id per global token (non-decreasing) */
+  const int32_t* q_doc;  /* RMX_MASK_DOC: document id of each q row (non-decreasing), i.e.
+                            doc_ids_from_cu(cu_seqlens)[q_gidx] (ring/varlen_blocks.py:45-48) */
+  const int32_t* k_doc;  /* RMX_MASK_DOC: document id of each k row (non-decreasing) */
   int32_t sq, sk;
   int32_t mode;          /* RMX_FWD_* */
 } rmx_fwd_problem;
@@ -103,9 +105,10 @@ typedef struct rmx_bwd_problem {
   float* dv_acc;
   uint16_t* dk;          /* bf16, dk_* strides */
   uint16_t* dv;
-  const int32_t* q_gidx;
+  const int32_t* q_gidx; /* RMX_MASK_DOC: as in rmx_fwd_problem */
   const int32_t* k_gidx;
-  const int32_t* doc;
+  const int32_t* q_doc;
+  const int32_t* k_doc;
   int32_t sq, sk;
   int32_t dq_mode;       /* RMX_GRAD_* */
   int32_t dkv_mode;      /* RMX_GRAD_* */

@@ -17,6 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
+ABI_VERSION = 2  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
@@ -64,7 +65,7 @@ class FwdProblem(ctypes.Structure):
     _fields_ = [
         ("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp), ("lse", _vp),
         ("acc_out", _vp), ("acc_lse", _vp),
-        ("q_gidx", _vp), ("k_gidx", _vp), ("doc", _vp),
+        ("q_gidx", _vp), ("k_gidx", _vp), ("q_doc", _vp), ("k_doc", _vp),
         ("sq", _i32), ("sk", _i32), ("mode", _i32),
     ]
 
@@ -73,7 +74,7 @@ class BwdProblem(ctypes.Structure):
     _fields_ = [
         ("q", _vp), ("k", _vp), ("v", _vp), ("dout", _vp), ("lse", _vp), ("delta", _vp),
         ("dq_acc", _vp), ("dq", _vp), ("dk_acc", _vp), ("dv_acc", _vp), ("dk", _vp), ("dv", _vp),
-        ("q_gidx", _vp), ("k_gidx", _vp), ("doc", _vp),
+        ("q_gidx", _vp), ("k_gidx", _vp), ("q_doc", _vp), ("k_doc", _vp),
         ("sq", _i32), ("sk", _i32), ("dq_mode", _i32), ("dkv_mode", _i32),
     ]
 
@@ -113,7 +114,7 @@ def lib() -> ctypes.CDLL:
                     fn = getattr(handle, name)
                     fn.restype = res
                     fn.argtypes = args
-                if handle.rmx_abi_version() != 1:
+                if handle.rmx_abi_version() != ABI_VERSION:
                     raise RuntimeError("ringmaster_amd ABI version mismatch")
                 _lib = handle
     return _lib

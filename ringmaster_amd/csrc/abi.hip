@@ -76,9 +76,13 @@ int check_span(int64_t rows, int64_t stride_elems, const char* name) {
   return RMX_OK;
 }
 
-int check_doc(const rmx_attn_layout* L, const int32_t* qg, const int32_t* kg, const int32_t* doc) {
+int check_doc(const rmx_attn_layout* L, const int32_t* qg, const int32_t* kg, const int32_t* qd,
+              const int32_t* kd) {
   if (L->mask != RMX_MASK_DOC) return RMX_OK;
-  if (!qg || !kg || !doc) return fail(RMX_EINVAL, "RMX_MASK_DOC needs q_gidx, k_gidx and doc");
+  if (!qg || !kg || !qd || !kd)
+    return fail(RMX_EINVAL, "RMX_MASK_DOC needs q_gidx, k_gidx, q_doc and k_doc");
+  if (!aligned(qg, 4) || !aligned(kg, 4) || !aligned(qd, 4) || !aligned(kd, 4))
+    return fail(RMX_EINVAL, "RMX_MASK_DOC index arrays must be 4-byte aligned");
   return RMX_OK;
 }
 
@@ -108,7 +112,7 @@ int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* probl
       if ((rc = check_span(p.sk, layout->k_ss, "k"))) return rc;
       if ((rc = check_span(p.sk, layout->v_ss, "v"))) return rc;
     }
-    if ((rc = check_doc(layout, p.q_gidx, p.k_gidx, p.doc))) return rc;
+    if ((rc = check_doc(layout, p.q_gidx, p.k_gidx, p.q_doc, p.k_doc))) return rc;
     switch (p.mode) {
       case RMX_FWD_WRITE:
       case RMX_FWD_ACC_FINAL:
@@ -169,7 +173,7 @@ int32_t rmx_attn_bwd(const rmx_attn_layout* layout, const rmx_bwd_problem* probl
     if ((rc = check_span(p.sk, layout->k_ss, "k"))) return rc;
     if ((rc = check_span(p.sk, layout->v_ss, "v"))) return rc;
     if (!p.lse || !p.delta) return fail(RMX_EINVAL, "problem %d: lse and delta are required", i);
-    if ((rc = check_doc(layout, p.q_gidx, p.k_gidx, p.doc))) return rc;
+    if ((rc = check_doc(layout, p.q_gidx, p.k_gidx, p.q_doc, p.k_doc))) return rc;
     const int modes[2] = {p.dq_mode, p.dkv_mode};
     for (int m = 0; m < 2; ++m) {
       const int mode = modes[m];

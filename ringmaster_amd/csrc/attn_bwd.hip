@@ -212,7 +212,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   int qg = -2147483647, qd = -1;
   if (mask == RMX_MASK_DOC && qvalid) {
     qg = P.q_gidx[q];
-    qd = P.doc[qg];
+    qd = P.q_doc[q];
   }
 
   const int off = sk - sq;
@@ -226,8 +226,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   } else if (mask == RMX_MASK_DOC) {
     qg_first = P.q_gidx[q0];
     qg_last = P.q_gidx[qlast];
-    qd_first = P.doc[qg_first];
-    qd_last = P.doc[qg_last];
+    qd_first = P.q_doc[q0];
+    qd_last = P.q_doc[qlast];
     if (tid == 0) {
       sRange[0] = nkt;
       sRange[1] = -1;
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
     for (int t = tid; t < nkt; t += NT) {
       const int ka = t * BK, kz = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
       const int kga = P.k_gidx[ka], kgz = P.k_gidx[kz];
-      const int kda = P.doc[kga], kdz = P.doc[kgz];
+      const int kda = P.k_doc[ka], kdz = P.k_doc[kz];
       if (kga <= qg_last && kdz >= qd_first && kda <= qd_last) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
     if (mask == RMX_MASK_DOC && tid < BK) {
       const int kk = k0 + tid < sk ? k0 + tid : sk - 1;
       nkg = P.k_gidx[kk];
-      nkd = P.doc[nkg];
+      nkd = P.k_doc[kk];
     }
   };
   auto doc_store = [&](int buf) {
@@ -499,8 +499,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   } else if (mask == RMX_MASK_DOC) {
     kg_first = P.k_gidx[k0];
     kg_last = P.k_gidx[klast];
-    kd_first = P.doc[kg_first];
-    kd_last = P.doc[kg_last];
+    kd_first = P.k_doc[k0];
+    kd_last = P.k_doc[klast];
     if (tid == 0) {
       sRange[0] = nqt;
       sRange[1] = -1;
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     for (int t = tid; t < nqt; t += C::NT) {
       const int qa = t * BQ, qz = (t * BQ + BQ < sq ? t * BQ + BQ : sq) - 1;
       const int qga = P.q_gidx[qa], qgz = P.q_gidx[qz];
-      const int qda = P.doc[qga], qdz = P.doc[qgz];
+      const int qda = P.q_doc[qa], qdz = P.q_doc[qz];
       if (qgz >= kg_first && qdz >= kd_first && qda <= kd_last) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
@@ -555,9 +555,21 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   // chunk L%CH. Wave 0's metadata precedes its tile loads, so a wait that
   // leaves a later tile's 2*NDMA loads in flight covers it. The loads are the
   // asm form (dma16_async): the kernel orders every LDS read after them itself.
-  auto dma_tile = [&](auto b, int it) {
-    const int qa = (qt_begin + it % nq_iter) * BQ;
-    const int qh = kvh * G + it / nq_iter;
+  // Tiles run q head major: tile (qt, hi) is query tile qt of q head kvh * G + hi.
+  // Cursors over that order advance by one tile at a time (no divisions).
+  struct Cursor {
+    int qt, hi;
+  };
+  auto advance = [&](Cursor c) -> Cursor {
+    if (++c.qt == qt_end) {
+      c.qt = qt_begin;
+      ++c.hi;
+    }
+    return c;
+  };
+  auto dma_tile = [&](auto b, Cursor cu) {
+    const int qa = cu.qt * BQ;
+    const int qh = kvh * G + cu.hi;
     if (wave == 0) {
       const int64_t lb = bb * L.l_sb + qh * L.l_sh;
       const uint32_t m = lds_addr(lbuf(b));
@@ -586,12 +598,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     }
   };
   int nqg = 0, nqd = 0;
-  auto doc_load = [&](int it) {
+  auto doc_load = [&](Cursor cu) {
     if (mask == RMX_MASK_DOC && tid < BQ) {
-      const int qq = (qt_begin + it % nq_iter) * BQ + tid;
+      const int qq = cu.qt * BQ + tid;
       if (qq < sq) {
         nqg = P.q_gidx[qq];
-        nqd = P.doc[nqg];
+        nqd = P.q_doc[qq];
       } else {
         nqg = -2147483647;  // rows past the end: masked
         nqd = -1;
@@ -635,11 +647,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   };
 
   // ---- prologue: tiles 0 and 1 in flight, documents of tile 0 in LDS
+  const Cursor c_first = {qt_begin, 0};
   if (ntile > 0) {
-    dma_tile(std::integral_constant<int, 0>{}, 0);
-    doc_load(0);
+    dma_tile(std::integral_constant<int, 0>{}, c_first);
+    doc_load(c_first);
     doc_store(0);
-    if (ntile > 1) dma_tile(std::integral_constant<int, 1>{}, 1);
+    if (ntile > 1) dma_tile(std::integral_constant<int, 1>{}, advance(c_first));
   }
 
   const float c = prm.scale_log2;
@@ -657,7 +670,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     int kg = 2147483647, kd = -2;
     if (PW && mask == RMX_MASK_DOC && kvalid) {
       kg = P.k_gidx[key];
-      kd = P.doc[kg];
+      kd = P.k_doc[key];
     }
     f32x16 acc[NDB];
 #pragma unroll
@@ -667,13 +680,18 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     if (ntile > 0) lse_to_log2(std::integral_constant<int, 0>{});
     lds_barrier();
 
+    // cursors of tiles j, j + 1 and j + 2
+    Cursor cur = c_first, nx1 = advance(c_first), nx2 = advance(advance(c_first));
     auto tile = [&](auto b, int j) {
       constexpr int B = decltype(b)::value;  // == j % 3
       using NEXT = std::integral_constant<int, (B + 1) % 3>;
-      const int qa = (qt_begin + j % nq_iter) * BQ;
-      if (j + 1 < ntile) doc_load(j + 1);
+      const int qa = cur.qt * BQ;
+      if (j + 1 < ntile) doc_load(nx1);
       // buffer (j + 2) % 3 held tile j - 1, released by the last barrier
-      if (j + 2 < ntile) dma_tile(std::integral_constant<int, (B + 2) % 3>{}, j + 2);
+      if (j + 2 < ntile) dma_tile(std::integral_constant<int, (B + 2) % 3>{}, nx2);
+      cur = nx1;
+      nx1 = nx2;
+      nx2 = advance(nx2);
       const uint8_t* qt_l = qbuf(b);
       const uint8_t* ot_l = obuf(b);
 

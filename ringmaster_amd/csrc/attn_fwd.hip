@@ -9,24 +9,32 @@
 //
 // Work decomposition: one workgroup = 8 waves = 256 queries of one
 // (problem, batch, head); each wave owns 32 queries and walks the key tiles
-// (64 keys) that the mask leaves, two waves per SIMD so one wave's softmax
-// overlaps the other's MFMAs.
+// (64 keys) that the mask leaves.
 //
-// Per key tile and wave (v_mfma_f32_32x32x16_bf16):
-//   S^T = K Q^T    A = K rows from LDS (rows sigma-permuted, see rmx_common.h),
-//                  B = Q held in VGPRs for the whole loop       (16 MFMAs)
-//   online softmax per lane (a lane owns one query; the two lane halves split
-//   the keys, one cross-half max per tile); the running max is only moved when
-//   a tile raises it by more than 2^8, so the O rescale is rare
-//   O^T += V^T P^T A = V^T read with ds_read_b64_tr_b16 from the row-major V
-//                  tile, B = P straight from the S^T registers     (16 MFMAs)
+// Per key tile j a wave runs two "slots" (v_mfma_f32_32x32x16_bf16):
+//   M_j  O^T += V_{j-1}^T P_{j-1}^T   A = V^T by ds_read_b64_tr_b16 from the
+//                                     row-major V tile, B = P from registers
+//        S_j^T = K_j Q^T              A = K rows from LDS (rows sigma-permuted,
+//                                     see rmx_common.h), B = Q in VGPRs
+//        (32 MFMAs, two independent chains)
+//   X_j  mask, online softmax of S_j -> P_j (one lane owns one query, the two
+//        lane halves split the keys; the running max only moves when a tile
+//        raises it by more than 2^8, so the O rescale is rare)
+// Ping-pong: waves 0-3 (group A) and 4-7 (group B) -- the dispatcher places
+// waves w and w + 4 on the same SIMD -- run this program one slot apart, with a
+// workgroup barrier between slots: while group A is in M_j, group B is in
+// X_{j-1}, then A in X_j while B is in M_j. Every SIMD thus has one wave issuing
+// MFMAs and one doing the softmax in every slot.
 // K/V tiles: direct global->LDS loads (buffer_load ... lds; rows past the end
-// read as zeros) into three LDS buffers, issued two tiles ahead so L2/HBM
-// latency stays hidden; each tile is published by a barrier that only waits for
-// its own loads. The 16-byte chunks of the unpadded LDS rows are XOR-swizzled
-// (swz_rows for K, swz_tr for V) so both the row reads and the transposed reads
-// are bank-conflict free.
+// read as zeros) into three K and three V buffers. The loads issued at slot 2i
+// (K_{i+2}, V_{i+1}) are first read at slot 2i+4, and each odd slot's barrier
+// waits only for the loads of the even slot two before it. The 16-byte chunks
+// of the unpadded LDS rows are XOR-swizzled (swz_rows for K, swz_tr for V) so
+// both the row reads and the transposed reads are bank-conflict free. The loads
+// are the asm form (dma16_async, dma4_async): the kernel orders every LDS read
+// after them itself.
 #include <type_traits>
+#include <utility>
 
 #include "rmx_kernels.h"
 
@@ -62,17 +70,13 @@ template <int HD, int MASK>
 __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   using C = FwdCfg<HD>;
   constexpr int BK = C::BK, MB = C::MB, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB;
+  constexpr int NDMA = C::NDMA;
 
-  // three K and three V tile buffers (separate objects, so the compiler can tell
-  // the buffer being read from the ones the DMA is filling)
-  __shared__ __attribute__((aligned(1024))) uint8_t sK0[C::KT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sK1[C::KT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sK2[C::KT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sV0[C::KT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sV1[C::KT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sV2[C::KT];
-  __shared__ int sKg[3][BK];
-  __shared__ int sKd[3][BK];
+  __shared__ __attribute__((aligned(1024))) uint8_t sK[4][C::KT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sV[3][C::KT];
+  // RMX_MASK_DOC: global index and document of the keys of tile t, in slot t % 4
+  __shared__ __attribute__((aligned(256))) int sKg[4][BK];
+  __shared__ __attribute__((aligned(256))) int sKd[4][BK];
   __shared__ int sRange[2];
 
   const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
@@ -90,6 +94,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int grp = wave >> 2;                                  // ping-pong group
   const int lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int qw0 = q0 + 32 * wave;  // first query of this wave
   const int q = qw0 + l32;         // this lane's query
@@ -106,7 +111,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   int qg = -2147483647, qd = -1;
   if (mask == RMX_MASK_DOC && q < sq) {
     qg = P.q_gidx[q];
-    qd = P.doc[qg];
+    qd = P.q_doc[q];
   }
 
   // ---- key tile range of the workgroup
@@ -121,8 +126,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   } else if (mask == RMX_MASK_DOC) {
     qg_first = P.q_gidx[q0];
     qg_last = P.q_gidx[qlast];
-    qd_first = P.doc[qg_first];
-    qd_last = P.doc[qg_last];
+    qd_first = P.q_doc[q0];
+    qd_last = P.q_doc[qlast];
     if (tid == 0) {
       sRange[0] = nkt;
       sRange[1] = -1;
@@ -131,8 +136,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     int lo = nkt, hi = -1;
     for (int t = tid; t < nkt; t += C::NT) {
       const int ka = t * BK, kz = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
-      const int kga = P.k_gidx[ka], kgz = P.k_gidx[kz];
-      const int kda = P.doc[kga], kdz = P.doc[kgz];
+      const int kga = P.k_gidx[ka];
+      const int kda = P.k_doc[ka], kdz = P.k_doc[kz];
       if (kga <= qg_last && kdz >= qd_first && kda <= qd_last) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
@@ -145,57 +150,46 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     kt_end = sRange[1] + 1;
     if (kt_end < kt_begin) kt_end = kt_begin;
   }
-
-  // last key this wave can attend (causal): tiles past it are skipped by the wave
-  const int wave_qlast = (qw0 + 31 < sq ? qw0 + 31 : sq - 1);
-  const int wave_kmax = mask == RMX_MASK_CAUSAL ? wave_qlast + off : 2147483647;
+  const int ntile = kt_end - kt_begin;
 
   // ---- K/V staging: buffer resources over this (batch, kv head)
   const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
   const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, HD * 2));
   const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, HD * 2));
-  auto kbuf = [&](auto b) -> uint8_t* {
-    constexpr int B = decltype(b)::value;
-    if constexpr (B == 0) return sK0;
-    else if constexpr (B == 1) return sK1;
-    else return sK2;
-  };
-  auto vbuf = [&](auto b) -> uint8_t* {
-    constexpr int B = decltype(b)::value;
-    if constexpr (B == 0) return sV0;
-    else if constexpr (B == 1) return sV1;
-    else return sV2;
-  };
-  // DMA of the K/V tile at key k0 into buffer b: instruction n of the tile fills
+  // DMA of a K (V) tile at key k0 into buffer b: instruction n of the tile fills
   // LDS bytes [1024 n, 1024 n + 1024), lane L row n*RPK + L/CH, swizzled chunk L%CH
-  auto dma_tile = [&](auto b, int k0) {
-    uint8_t* kd = kbuf(b);
-    uint8_t* vd = vbuf(b);
+  auto dma_k = [&](int b, int k0) __attribute__((always_inline)) {
+    const uint32_t d = lds_addr(&sK[b][0]);
 #pragma unroll
-    for (int i = 0; i < C::NDMA; ++i) {
-      const int n = wave * C::NDMA + i;
+    for (int i = 0; i < NDMA; ++i) {
+      const int n = wave * NDMA + i;
       const int r = n * C::RPK + lane / CH, p = lane % CH;
-      dma16(krs, kd + 1024 * n, (k0 + r) * kss + 16 * (p ^ swz_rows<HD>(r)));
-      dma16(vrs, vd + 1024 * n, (k0 + r) * vss + 16 * (p ^ swz_tr<HD>(r)));
+      dma16_async(krs, d + 1024 * n, (k0 + r) * kss + 16 * (p ^ swz_rows<HD>(r)));
     }
   };
-  int nkg = 0, nkd = 0;
-  auto doc_load = [&](int k0) {
-    if (mask == RMX_MASK_DOC && tid < BK) {
-      const int kk = k0 + tid < sk ? k0 + tid : sk - 1;
-      nkg = P.k_gidx[kk];
-      nkd = P.doc[nkg];
+  auto dma_v = [&](int b, int k0) __attribute__((always_inline)) {
+    const uint32_t d = lds_addr(&sV[b][0]);
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      const int n = wave * NDMA + i;
+      const int r = n * C::RPK + lane / CH, p = lane % CH;
+      dma16_async(vrs, d + 1024 * n, (k0 + r) * vss + 16 * (p ^ swz_tr<HD>(r)));
     }
   };
-  auto doc_store = [&](int slot) {
-    if (mask == RMX_MASK_DOC && tid < BK) {
-      sKg[slot][tid] = nkg;
-      sKd[slot][tid] = nkd;
+  // key metadata of tile t (RMX_MASK_DOC), one dword per lane, by wave 0
+  constexpr bool DOCDMA = mask == RMX_MASK_DOC;
+  i32x4 kgrs = {0, 0, 0, 0}, kdrs = {0, 0, 0, 0};
+  if (DOCDMA) {
+    kgrs = make_rsrc(P.k_gidx, 4u * (uint32_t)sk);
+    kdrs = make_rsrc(P.k_doc, 4u * (uint32_t)sk);
+  }
+  auto dma_doc = [&](int t) __attribute__((always_inline)) {
+    if (DOCDMA && wave == 0) {
+      const int k0 = (kt_begin + t) * BK;
+      dma4_async(kgrs, lds_addr(&sKg[t & 3][0]), 4 * (k0 + lane));
+      dma4_async(kdrs, lds_addr(&sKd[t & 3][0]), 4 * (k0 + lane));
     }
   };
-  using B0 = std::integral_constant<int, 0>;
-  using B1 = std::integral_constant<int, 1>;
-  using B2 = std::integral_constant<int, 2>;
 
   // per-lane LDS byte offsets of the operand reads (swizzle folded in; see
   // swz_rows / swz_tr): K rows (A of S^T) row 32mb + sigma(l32), chunk 2kb + hl
@@ -220,136 +214,260 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   f32x16 o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = zero16();
+  f32x16 sA[MB], sB[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    sA[mb] = zero16();
+    sB[mb] = zero16();
+  }
   float m_run = kNegInf, l_run = 0.f;
   const float c = prm.scale_log2;
 
-  // tile j (relative to kt_begin) lives in buffer j % 3; its DMA is issued at
-  // the start of tile j - 2 (tiles 0 and 1 in the prologue)
-  const int ntile = kt_end - kt_begin;
+  // ---- LDS operand reads
+  auto k_op = [&](int kbi, int t, int mb) __attribute__((always_inline)) -> bf16x8 {
+    return __builtin_bit_cast(
+        bf16x8, *reinterpret_cast<const u32x4*>(&sK[kbi][0] + kaddr[t] + mb * 32 * RB));
+  };
+  auto v_op = [&](int vbi, int kb2, int db) __attribute__((always_inline)) -> bf16x8 {
+    const uint16_t* vp = reinterpret_cast<const uint16_t*>(&sV[vbi][0] + vaddr[db] + 16 * kb2 * RB);
+    return join_bf16x8(lds_read_tr(vp), lds_read_tr(vp + 2 * RB));
+  };
+
+  // ---- masking of a score tile (keys of tile t): out-of-range keys, the causal
+  // diagonal and document boundaries -> -inf. A causal tile past the wave's
+  // diagonal is masked whole and yields P = 0.
+  auto need_mask = [&](int t) __attribute__((always_inline)) -> bool {
+    const int k0 = (kt_begin + t) * BK;
+    bool nm = (k0 + BK > sk);
+    if (mask == RMX_MASK_CAUSAL) nm |= (k0 + BK - 1 > qw0 + off);
+    if (mask == RMX_MASK_DOC) {
+      const int ds = t & 3;
+      const int kgz = sKg[ds][BK - 1];
+      const int kda = sKd[ds][0], kdz = sKd[ds][BK - 1];
+      nm |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first);
+    }
+    return nm;
+  };
+  auto apply_mask = [&](int t, f32x16* sd) __attribute__((always_inline)) {
+    const int k0 = (kt_begin + t) * BK;
+    const int ds = t & 3;
+    // key of (mb, r) = k0 + 8 hl + kc with the constant kc = 32 mb + 16 (r >> 3) + (r & 7):
+    // compare the constants against per-lane limits (no per-element registers)
+    const int kbase = k0 + 8 * hl;
+    const int lim_sk = sk - kbase;      // kc < lim_sk  <=>  key < sk
+    const int lim_c = q + off - kbase;  // kc <= lim_c  <=>  key <= q + off
+    const int* kgrow = &sKg[ds][8 * hl];
+    const int* kdrow = &sKd[ds][8 * hl];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kc = 32 * mb + 16 * (r >> 3) + (r & 7);
+        bool ok = kc < lim_sk;
+        if (mask == RMX_MASK_CAUSAL) ok &= kc <= lim_c;
+        if (mask == RMX_MASK_DOC) ok &= (kdrow[kc] == qd) & (kgrow[kc] <= qg);
+        sd[mb][r] = ok ? sd[mb][r] : kNegInf;
+      }
+  };
+  // row max of a score tile (log2 units, both lane halves)
+  auto tile_max_part = [&](const f32x16* sd, int lo, int hi) __attribute__((always_inline)) -> float {
+    float m = kNegInf;
+    for (int e = lo; e < hi; ++e) m = fmaxf(m, sd[e >> 4][e & 15]);
+    return m;
+  };
+  // online-softmax bookkeeping for a new tile whose row max (log2 units) is mx:
+  // the running max only moves when the tile raises it by more than the slack
+  auto rescale = [&](float mx, bool live) __attribute__((always_inline)) {
+    const bool raise = live && mx > m_run + kRescaleSlack;
+    if (__any(raise)) {
+      const float mnew = raise ? fmaxf(m_run, mx) : m_run;
+      const float alpha = (m_run == kNegInf) ? 0.f : fast_exp2(m_run - mnew);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+      m_run = mnew;
+    }
+  };
+
+  // ---- prologue: K_0, K_1, V_0 (and the metadata of tiles 0, 1) resident;
+  // K_2, V_1 in flight; S_0 computed, masked and its max folded in
   if (ntile > 0) {
-    dma_tile(B0{}, kt_begin * BK);
-    doc_load(kt_begin * BK);
-    doc_store(0);
-    if (ntile > 1) dma_tile(B1{}, (kt_begin + 1) * BK);
+    dma_k(0, kt_begin * BK);
+    dma_v(0, kt_begin * BK);
+    dma_doc(0);
+    if (ntile > 1) {
+      dma_k(1, (kt_begin + 1) * BK);
+      dma_doc(1);
+    }
   }
   wait_all_loads();
   __syncthreads();
+  // loads issued at iteration j (j = -1: here): K_{j+3} into K buffer (j+3) % 4,
+  // V_{j+2} into V buffer (j+2) % 3; iteration j + 2 is the first to read them
+  auto issue = [&](int j, int vb2) __attribute__((always_inline)) {
+    if (j + 3 < ntile) {
+      dma_k((j + 3) & 3, (kt_begin + j + 3) * BK);
+      dma_doc(j + 3);
+    }
+    if (j + 2 < ntile) dma_v(vb2, (kt_begin + j + 2) * BK);
+  };
+  // end of iteration j: everything but the loads issued at iteration j has landed
+  auto barrier_wait = [&](int j) __attribute__((always_inline)) {
+    if (j + 3 < ntile) {
+      if (DOCDMA && wave == 0)
+        wait_vm_barrier<2 * NDMA + 2>();
+      else
+        wait_vm_barrier<2 * NDMA>();
+    } else if (j + 2 < ntile) {
+      wait_vm_barrier<NDMA>();
+    } else {
+      wait_vm_barrier<0>();
+    }
+  };
+  issue(-1, 1);
+  if (ntile > 0) {
+#pragma unroll
+    for (int t = 0; t < NKB; ++t)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) sA[mb] = mfma32(k_op(0, t, mb), qreg[t], sA[mb]);
+    if (need_mask(0)) {
+      keep_branch();
+      apply_mask(0, sA);
+    }
+    float mx = tile_max_part(sA, 0, 32);
+    mx = fmaxf(mx, xhalf(mx)) * c;
+    rescale(mx, true);
+  }
 
-  auto tile = [&](auto b, int j) {
-    constexpr int B = decltype(b)::value;  // == j % 3
-    const int k0 = (kt_begin + j) * BK;
-    if (j + 1 < ntile) doc_load(k0 + BK);  // key documents of the next tile
-    // buffer (j + 2) % 3 held tile j - 1, released by the last barrier
-    if (j + 2 < ntile) dma_tile(std::integral_constant<int, (B + 2) % 3>{}, k0 + 2 * BK);
-    const uint8_t* kt_lds = kbuf(b);
-    const uint8_t* vt_lds = vbuf(b);
-
-    if (k0 <= wave_kmax) {
-      bool need_mask = (k0 + BK > sk);
-      if (mask == RMX_MASK_CAUSAL) need_mask |= (k0 + BK - 1 > qw0 + off);
-      if (mask == RMX_MASK_DOC) {
-        const int kgz = sKg[B][BK - 1];
-        const int kda = sKd[B][0], kdz = sKd[B][BK - 1];
-        need_mask |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first);
-      }
-
-      // ---- S^T = K Q^T (A = K rows, B = Q in VGPRs); MB blocks of 32 keys
-      f32x16 s[MB];
+  // ---- iteration j: S_j (masked, its max folded into m_run) is in sc.
+  //   region 1: S_{j+1} = K_{j+1} Q^T into sn (NKB steps of MB MFMAs), with the
+  //             exponentials of the first 3/4 of S_j (pairs of elements ->
+  //             v_cvt_pk_bf16_f32 -> P_j);
+  //   region 2: O += V_j^T P_j (PVS steps of two MFMAs), with the last quarter
+  //             of the exponentials (ahead of the PV MFMAs that use them) and
+  //             the row max of S_{j+1};
+  //   then the rescale decision for tile j + 1 and the barrier.
+  // Operands are read one step ahead; scheduling fences keep the steps in order
+  // so each step's VALU work issues under its MFMAs.
+  constexpr int PVS = (2 * MB * NDB) / 2;  // PV steps (two MFMAs each)
+  constexpr int NPAIR = MB * 8;            // element pairs per lane (32 scores)
+  constexpr int P1 = NPAIR * 3 / 4;        // pairs done in region 1
+  constexpr int PV3 = PVS * 3 / 4;         // first PV step that needs pb[3]
+  constexpr int KD = 3, VD = 3;            // operand prefetch depth (steps) of regions 1 and 2
+  static_assert(VD <= NKB && VD < PVS && 2 * MB * KD <= 15 && 4 * VD <= 15, "lgkmcnt range");
+  auto pv_idx = [](int u, int v) { return 2 * u + v; };  // PV MFMA: kb2 = idx / NDB, db = idx % NDB
+  auto iter = [&](int j, int vbj, f32x16* sc, f32x16* sn) __attribute__((always_inline)) {
+    const int vb2 = vbj == 0 ? 2 : vbj - 1;  // (j + 2) % 3
+    issue(j, vb2);
+    const int kbi = (j + 1) & 3;
+    const bool live = j + 1 < ntile;
+    const float mbase = (m_run == kNegInf) ? 0.f : m_run;
+    u32x4 pw[2 * MB];   // P_j packed to bf16, one u32x4 per 16-key block
+    float rsp[2 * MB];  // partial row sums per 16-key block
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) s[mb] = zero16();
+    for (int i = 0; i < 2 * MB; ++i) rsp[i] = 0.f;
+    auto pair = [&](auto pp) __attribute__((always_inline)) {
+      constexpr int pi = decltype(pp)::value;  // pair index: elements 2 pi, 2 pi + 1
+      constexpr int kb2 = pi / 4, w = pi % 4;
+      const float x0 = fast_exp2(fmaf(sc[kb2 >> 1][8 * (kb2 & 1) + 2 * w], c, -mbase));
+      const float x1 = fast_exp2(fmaf(sc[kb2 >> 1][8 * (kb2 & 1) + 2 * w + 1], c, -mbase));
+      float rs = rsp[kb2] + (x0 + x1);
+      uint32_t pk = cvt_pk_bf16(x0, x1);
+      // pin the results here: otherwise the compiler sinks the exponentials to
+      // their first use (after the region) and the step has no VALU work
+      asm volatile("" : "+v"(rs), "+v"(pk));
+      rsp[kb2] = rs;
+      pw[kb2][w] = pk;
+    };
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
+    for (int mb = 0; mb < MB; ++mb) sn[mb] = zero16();
+    bf16x8 va[VD + 1][2];
+    // region 1
+    bf16x8 ka[KD + 1][MB];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const bf16x8 a = __builtin_bit_cast(
-              bf16x8, *reinterpret_cast<const u32x4*>(kt_lds + kaddr[kb] + mb * 32 * RB));
-          s[mb] = mfma32(a, qreg[kb], s[mb]);
-        }
-      }
-
-      if (need_mask) {
-        keep_branch();
+    for (int t = 0; t < KD; ++t)
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+      for (int mb = 0; mb < MB; ++mb) ka[t][mb] = k_op(kbi, t, mb);
+    [&]<int... T>(std::integer_sequence<int, T...>) __attribute__((always_inline)) {
+      (
+          [&] {
+            constexpr int t = T;
+            if constexpr (t + KD < NKB) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kl = 32 * mb + sig_row(hl, r);
-            const int key = k0 + kl;
-            bool ok = key < sk;
-            if (mask == RMX_MASK_CAUSAL) ok &= key <= q + off;
-            if (mask == RMX_MASK_DOC) {
-              const int kd = sKd[B][kl], kg = sKg[B][kl];
-              ok &= (kd == qd) & (kg <= qg);
+              for (int mb = 0; mb < MB; ++mb) ka[(t + KD) % (KD + 1)][mb] = k_op(kbi, t + KD, mb);
             }
-            s[mb][r] = ok ? s[mb][r] : kNegInf;
-          }
-      }
+            if constexpr (t + VD >= NKB) {  // the first V operands of region 2
+              constexpr int u = t + VD - NKB;
+#pragma unroll
+              for (int v = 0; v < 2; ++v) va[u][v] = v_op(vbj, pv_idx(u, v) / NDB, pv_idx(u, v) % NDB);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) sn[mb] = mfma32(ka[t % (KD + 1)][mb], qreg[t], sn[mb]);
+            [&]<int... Q>(std::integer_sequence<int, Q...>) __attribute__((always_inline)) {
+              (pair(std::integral_constant<int, P1 * t / NKB + Q>{}), ...);
+            }(std::make_integer_sequence<int, P1 * (t + 1) / NKB - P1 * t / NKB>{});
+            __builtin_amdgcn_sched_barrier(0);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, NKB>{});
 
-      // ---- online softmax (log2 domain, scale folded into the exponent FMA)
-      // row max as a tree over the scores (short dependency chains)
-      float mxp[2 * MB];
-#pragma unroll
-      for (int t = 0; t < 2 * MB; ++t) {
-        mxp[t] = kNegInf;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) mxp[t] = fmaxf(mxp[t], s[t >> 1][8 * (t & 1) + r]);
-      }
-#pragma unroll
-      for (int w = MB; w >= 1; w >>= 1)
-#pragma unroll
-        for (int t = 0; t < w; ++t) mxp[t] = fmaxf(mxp[t], mxp[t + w]);
-      float mx = fmaxf(mxp[0], xhalf(mxp[0])) * c;
-      // move the running max only when this tile raises it by more than the
-      // slack (or on the first finite tile); otherwise keep the stale max
-      const bool raise = mx > m_run + kRescaleSlack;
-      if (__any(raise)) {
-        const float mnew = fmaxf(m_run, mx);
-        const float alpha = (m_run == kNegInf) ? 0.f : fast_exp2(m_run - mnew);
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-        m_run = mnew;
-      }
-      const float mbase = (m_run == kNegInf) ? 0.f : m_run;
-      float rsp[2 * MB];  // partial row sums (short dependency chains)
-      bf16x8 pb[2 * MB];
-#pragma unroll
-      for (int kb2 = 0; kb2 < 2 * MB; ++kb2) {
-        float pv[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pv[i] = fast_exp2(fmaf(s[kb2 >> 1][8 * (kb2 & 1) + i], c, -mbase));
-        rsp[kb2] = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-        pb[kb2] = pack8_hw(pv);
-      }
-#pragma unroll
-      for (int w = MB; w >= 1; w >>= 1)
-#pragma unroll
-        for (int t = 0; t < w; ++t) rsp[t] += rsp[t + w];
-      l_run += rsp[0];
-
-      // ---- O^T += V^T P^T
-#pragma unroll
-      for (int kb2 = 0; kb2 < 2 * MB; ++kb2) {
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const uint16_t* vp = reinterpret_cast<const uint16_t*>(vt_lds + vaddr[db] + 16 * kb2 * RB);
-          const bf16x8 a = join_bf16x8(lds_read_tr(vp), lds_read_tr(vp + 2 * RB));
-          o[db] = mfma32(a, pb[kb2], o[db]);
-        }
-      }
+    // mask S_{j+1} (rare: sequence end, causal diagonal, document boundaries)
+    if (live && need_mask(j + 1)) {
+      keep_branch();
+      apply_mask(j + 1, sn);
     }
 
-    // publish tile j + 1 (its DMA was issued a tile ago); tile j + 2's stays in flight
-    if (j + 1 < ntile) doc_store((B + 1) % 3);
-    if (j + 2 < ntile)
-      wait_vm_barrier<2 * C::NDMA>();
-    else
-      wait_vm_barrier<0>();
+    // region 2
+    float mpart[PVS];
+    [&]<int... U>(std::integer_sequence<int, U...>) __attribute__((always_inline)) {
+      (
+          [&] {
+            constexpr int u = U;
+            if constexpr (u + VD < PVS) {
+#pragma unroll
+              for (int v = 0; v < 2; ++v)
+                va[(u + VD) % (VD + 1)][v] = v_op(vbj, pv_idx(u + VD, v) / NDB, pv_idx(u + VD, v) % NDB);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+              const int idx = pv_idx(u, v);
+              o[idx % NDB] = mfma32(va[u % (VD + 1)][v], __builtin_bit_cast(bf16x8, pw[idx / NDB]), o[idx % NDB]);
+            }
+            // the remaining pairs, all before step PV3 (which starts on pb[3])
+            if constexpr (u < PV3) {
+              [&]<int... Q>(std::integer_sequence<int, Q...>) __attribute__((always_inline)) {
+                (pair(std::integral_constant<int, P1 + (NPAIR - P1) * u / PV3 + Q>{}), ...);
+              }(std::make_integer_sequence<int, (NPAIR - P1) * (u + 1) / PV3 - (NPAIR - P1) * u / PV3>{});
+            }
+            // row max of S_{j+1}, 32 / PVS scores per step
+            mpart[u] = tile_max_part(sn, 32 * u / PVS, 32 * (u + 1) / PVS);
+            asm volatile("" : "+v"(mpart[u]));
+            __builtin_amdgcn_sched_barrier(0);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, PVS>{});
+
+    float rs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2 * MB; ++i) rs += rsp[i];
+    l_run += rs;
+    float mx = kNegInf;
+#pragma unroll
+    for (int u = 0; u < PVS; ++u) mx = fmaxf(mx, mpart[u]);
+    mx = fmaxf(mx, xhalf(mx)) * c;
+    rescale(mx, live);
+    barrier_wait(j);
   };
-  for (int j = 0; j < ntile; j += 3) {
-    tile(B0{}, j);
-    if (j + 1 < ntile) tile(B1{}, j + 1);
-    if (j + 2 < ntile) tile(B2{}, j + 2);
+
+  int vbj = 0;  // j % 3
+  for (int j = 0; j < ntile; j += 2) {
+    iter(j, vbj, sA, sB);
+    vbj = vbj == 2 ? 0 : vbj + 1;
+    if (j + 1 >= ntile) break;
+    iter(j + 1, vbj, sB, sA);
+    vbj = vbj == 2 ? 0 : vbj + 1;
   }
 
   // ---- epilogue: normalise, lse, merge

@@ -30,7 +30,8 @@ class FwdJob:
     acc_lse: torch.Tensor | None = None
     q_gidx: torch.Tensor | None = None
     k_gidx: torch.Tensor | None = None
-    doc: torch.Tensor | None = None
+    q_doc: torch.Tensor | None = None
+    k_doc: torch.Tensor | None = None
 
 
 @dataclasses.dataclass
@@ -51,7 +52,8 @@ class BwdJob:
     dv: torch.Tensor | None = None
     q_gidx: torch.Tensor | None = None
     k_gidx: torch.Tensor | None = None
-    doc: torch.Tensor | None = None
+    q_doc: torch.Tensor | None = None
+    k_doc: torch.Tensor | None = None
 
 
 _ROLES = {
@@ -138,7 +140,8 @@ def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int) -> None:
         p.q, p.k, p.v = j.q.data_ptr(), j.k.data_ptr(), j.v.data_ptr()
         p.out, p.lse = abi.ptr(j.out), abi.ptr(j.lse)
         p.acc_out, p.acc_lse = abi.ptr(j.acc_out), abi.ptr(j.acc_lse)
-        p.q_gidx, p.k_gidx, p.doc = _int32(j.q_gidx), _int32(j.k_gidx), _int32(j.doc)
+        p.q_gidx, p.k_gidx = _int32(j.q_gidx), _int32(j.k_gidx)
+        p.q_doc, p.k_doc = _int32(j.q_doc), _int32(j.k_doc)
         p.sq, p.sk, p.mode = j.q.shape[1], j.k.shape[1], j.mode
     abi.check(abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, len(jobs), abi.stream_of(q0)))
 
@@ -177,7 +180,8 @@ def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int) -> None:
         p.dq_acc, p.dq = abi.ptr(j.dq_acc), abi.ptr(j.dq)
         p.dk_acc, p.dv_acc = abi.ptr(j.dk_acc), abi.ptr(j.dv_acc)
         p.dk, p.dv = abi.ptr(j.dk), abi.ptr(j.dv)
-        p.q_gidx, p.k_gidx, p.doc = _int32(j.q_gidx), _int32(j.k_gidx), _int32(j.doc)
+        p.q_gidx, p.k_gidx = _int32(j.q_gidx), _int32(j.k_gidx)
+        p.q_doc, p.k_doc = _int32(j.q_doc), _int32(j.k_doc)
         p.sq, p.sk = j.q.shape[1], j.k.shape[1]
         p.dq_mode, p.dkv_mode = j.dq_mode, j.dkv_mode
     abi.check(abi.lib().rmx_attn_bwd(ctypes.byref(lay), arr, len(jobs), abi.stream_of(q0)))

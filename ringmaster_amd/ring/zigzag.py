@@ -60,10 +60,12 @@ class _Ctx:
         self.half = self.L // 2
         self.scale = scale
         self.doc = doc
-        self.gidx = None
+        self.gidx = self.rdoc = None
         if doc is not None:
             rows = [zigzag_gidx(r, self.half, self.P) for r in range(self.P)]
             self.gidx = torch.tensor(rows, dtype=torch.int32).to(q.device)
+            # document id of every local row of every rank: [P, L]
+            self.rdoc = doc[self.gidx.long()].to(torch.int32).contiguous()
 
     def mask(self, step: int) -> int:
         if self.doc is not None:
@@ -72,6 +74,9 @@ class _Ctx:
 
     def idx(self, rank, lo, hi):
         return None if self.gidx is None else self.gidx[rank, lo:hi]
+
+    def docs(self, rank, lo, hi):
+        return None if self.rdoc is None else self.rdoc[rank, lo:hi]
 
 
 class KernelTimer:
@@ -152,7 +157,7 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
                 acc_out=acc[r][:, qs],
                 acc_lse=None if acc_lse is None else acc_lse[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
-                doc=c.doc))
+                q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi)))
         with timer("attn_fwd"):
             ops.attn_fwd(jobs, scale=scale, mask=c.mask(s))
     return out, lse, acc
@@ -190,7 +195,7 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
                 q=qd[r][:, qs], k=kd[kr][:, ks], v=vd[kr][:, ks], dout=dout[r][:, qs],
                 lse=lse[r][:, :, qs], delta=delta[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
-                doc=c.doc)
+                q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi))
             kv_jobs.append(ops.BwdJob(dq_mode=abi.GRAD_NONE, dkv_mode=mode,
                                       dk_acc=dk[kr][:, ks], dv_acc=dv[kr][:, ks], **common))
             q_jobs.append(ops.BwdJob(dq_mode=mode, dkv_mode=abi.GRAD_NONE,

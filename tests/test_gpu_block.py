@@ -106,7 +106,8 @@ def test_doc_mask_block():
     lse = torch.empty(1, H, 256, device="cuda")
     dev_i32 = lambda t: t.to(torch.int32).cuda()  # noqa: E731
     ops.attn_fwd([ops.FwdJob(q=qd, k=kd, v=vd, mode=abi.FWD_WRITE, out=out, lse=lse,
-                             q_gidx=dev_i32(qg), k_gidx=dev_i32(kg), doc=dev_i32(doc))],
+                             q_gidx=dev_i32(qg), k_gidx=dev_i32(kg),
+                             q_doc=dev_i32(doc[qg]), k_doc=dev_i32(doc[kg]))],
                  scale=d ** -0.5, mask=abi.MASK_DOC)
     torch.cuda.synchronize()
     assert_bf16_close(out, ref, "doc out")
