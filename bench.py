@@ -108,6 +108,61 @@ def ring_workload(steps, warmup):
             "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2)}
 
 
+def varlen_docs(total, seed=5, median=2048, sigma=1.0, lo=128, hi=16384):
+    """configs[3] document lengths: clip(round(exp(ln median + sigma z)), lo, hi), z ~ N(0, 1)
+    from ``seed``, drawn until they cover ``total``; the last one is cut to the remainder."""
+    g = torch.Generator().manual_seed(seed)
+    lens, acc = [], 0
+    while acc < total:
+        z = torch.randn(1, generator=g).item()
+        n = int(min(max(round(math.exp(math.log(median) + sigma * z)), lo), hi))
+        n = min(n, total - acc)
+        lens.append(n)
+        acc += n
+    return lens
+
+
+def varlen_workload(steps, warmup):
+    """packed lognormal documents under P=4 zigzag CP, S=65536, Hq=32/Hkv=8,
+    D=128, bf16, fwd+bwd (document-masked blocks)."""
+    from ringmaster_amd.ring.zigzag import KernelTimer, zigzag_ring_attention
+
+    P, S, Hq, Hkv, D = 4, 65536, 32, 8, 128
+    L = S // P
+    lens = varlen_docs(S)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32)
+    pairs = sum(n * (n + 1) // 2 for n in lens)
+    q = _gen((P, 1, Hq, L, D), 1).requires_grad_(True)
+    k = _gen((P, 1, Hkv, L, D), 2).requires_grad_(True)
+    v = _gen((P, 1, Hkv, L, D), 3).requires_grad_(True)
+    dout = _gen((P, 1, L, Hq, D), 4)
+    cu_dev = cu.cuda()
+    timer = KernelTimer()
+
+    def step(t=None):
+        out = zigzag_ring_attention(q, k, v, cu_seqlens=cu_dev, timer=t)
+        torch.autograd.grad(out, (q, k, v), dout)
+
+    for _ in range(warmup):
+        step()
+    _sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(timer)
+    _sync()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    flops = 14 * D * Hq * pairs
+    tf = flops / (ms * 1e-3) / 1e12
+    kern = {}
+    for name in ("attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq"):
+        m = timer.mean_ms(name)
+        if m is not None:
+            kern[name] = {"mean_ms": round(m, 4), "launches_per_step": timer.count(name) // steps}
+    return {"ms": round(ms, 3), "docs": len(lens), "attended_pairs": pairs, "flops": flops,
+            "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "kernels": kern}
+
+
 # ---------------------------------------------------------------- HBM-bound kernels
 def shard_workload(steps, warmup):
     from ringmaster_amd.shard import zigzag_shard
@@ -157,6 +212,28 @@ def scan_workload(steps, warmup):
             "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "fwd_GB/s": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
             "bwd_GB/s": round(bb / (bwd_ms * 1e-3) / 1e9, 1)}
+
+
+def mamba_workload(steps, warmup):
+    """configs[4] Mamba2 CP output correction: 8 shards of 8192 tokens stacked on the
+    batch axis, nheads=64, headdim=64, d_state=128, strong decay; one launch."""
+    from ringmaster_amd.strategies.mamba import mamba2_cp_correction
+
+    P, T, H, D, N = 8, 8192, 64, 64, 128
+    g = torch.Generator(device="cuda").manual_seed(5)
+    out = _gen((P, T, H * D), 10)
+    C = _gen((P, T, 1, N), 11)
+    A = -torch.exp(torch.rand(H, generator=g, device="cuda") * math.log(16.0))
+    dt = torch.nn.functional.softplus(torch.randn(P, T, H, generator=g, device="cuda"))
+    cum_A = torch.cumsum(A * dt, dim=1)
+    h_prev = _gen((P, H, D, N), 12, torch.float32)
+    h_final = _gen((P, H, D, N), 13, torch.float32)
+    ms = _time(lambda: mamba2_cp_correction(out, h_final, C, cum_A, h_prev, H, D), steps, warmup)
+    # read out + write y (bf16), read C, cum_A, h_prev, read + write h_final
+    nbytes = 2 * out.numel() * 2 + C.numel() * 2 + cum_A.numel() * 4 + 3 * h_prev.numel() * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "bytes": nbytes, "GB/s": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def block_workload(steps, warmup):
@@ -318,7 +395,11 @@ def main():
         torch.cuda.empty_cache()
         extras["cp_linear_scan_configs4"] = scan_workload(30, 3)
         torch.cuda.empty_cache()
+        extras["mamba2_correction_configs4"] = mamba_workload(30, 3)
+        torch.cuda.empty_cache()
         extras["block_configs1"] = block_workload(3, 1)
+        torch.cuda.empty_cache()
+        extras["varlen_configs3"] = varlen_workload(3, 1)
         torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_heads)
 

@@ -209,6 +209,26 @@ int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* dh, flo
                             float* db, int32_t batch, int32_t L, int32_t d, int32_t groups,
                             int32_t world, void* stream);
 
+/*
+ * Mamba2 context-parallel output correction (strategies/mamba.py:101-139):
+ *   y[b,t,h,:] = out[b,t,h,:] + bf16(e^{cum_A[b,t,h]} sum_n C[b,t,g(h),n] h_prev[b,h,:,n])
+ *   h_final_out[b,h] = h_final[b,h] + e^{cum_A[b,T-1,h]} h_prev[b,h]
+ * with g(h) = h / (nheads / ngroups). seq_idx (nullable, int32 [batch, T]): tokens
+ * with seq_idx != 0 get no correction, and no state is updated when the last
+ * token of any batch row has seq_idx != 0 (h_final_out := h_final; the reference
+ * tests seq_idx[:, -1].any() over the batch). Layouts (contiguous):
+ * out, y: bf16 [batch, T, nheads * head_dim] (y may alias out); C: bf16
+ * [batch, T, ngroups, d_state]; cum_A: fp32 [batch, T, nheads]; h_prev, h_final,
+ * h_final_out: fp32 [batch, nheads, head_dim, d_state] (h_final_out may alias
+ * h_final). head_dim in {32, 64, 128}; d_state in {16, 32, 64, 128, 256} with
+ * head_dim * d_state <= 32768.
+ */
+int32_t rmx_mamba2_cp_correction(const uint16_t* out, uint16_t* y, const float* h_final,
+                                 float* h_final_out, const uint16_t* C, const float* cum_A,
+                                 const float* h_prev, const int32_t* seq_idx, int32_t batch,
+                                 int32_t T, int32_t nheads, int32_t head_dim, int32_t ngroups,
+                                 int32_t d_state, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,8 +87,11 @@ def cp_state_prefix_emulated(finals, decays):
     return prefixes
 
 
-def mamba2_cp_correction(out, h_final, C, cum_A, h_prev, num_heads, head_dim):
-    """y_t += C_t . (exp(cumA_t) H_in); state += exp(cumA_last) H_in (strategies/mamba.py:101-139)."""
+def mamba2_cp_correction(out, h_final, C, cum_A, h_prev, num_heads, head_dim, seq_idx=None):
+    """y_t += C_t . (exp(cumA_t) H_in); state += exp(cumA_last) H_in (strategies/mamba.py:101-139).
+    seq_idx [b, T]: tokens with seq_idx != 0 start a fresh packed sequence on this rank and
+    get no correction (:124-126); no state is updated when the last token of any batch
+    row is such a token (seq_idx[:, -1].any(), :131-135)."""
     if not h_prev.any():
         return out, h_final
     B, T, _ = out.shape
@@ -96,7 +99,11 @@ def mamba2_cp_correction(out, h_final, C, cum_A, h_prev, num_heads, head_dim):
     decay = torch.exp(cum_A).float()
     prop = decay[:, :, :, None, None] * h_prev[:, None].float()
     Cx = C.float().repeat_interleave(hpg, dim=2)
-    dy = torch.einsum("bthn,bthdn->bthd", Cx, prop).reshape(B, T, num_heads * head_dim)
-    corrected = out + dy.to(out.dtype)
+    dy = torch.einsum("bthn,bthdn->bthd", Cx, prop)
+    if seq_idx is not None:
+        dy = dy * (seq_idx == 0).to(dy.dtype)[:, :, None, None]
+    corrected = out + dy.reshape(B, T, num_heads * head_dim).to(out.dtype)
+    if seq_idx is not None and seq_idx[:, -1].any():
+        return corrected, h_final
     h = h_final + (decay[:, -1, :, None, None] * h_prev.float()).to(h_final.dtype)
     return corrected, h

@@ -93,6 +93,8 @@ SIGNATURES = {
     "rmx_zigzag_scatter": (_i32, [_vp, _vp, _i32, _i32, _i32, _i64, _i64, _vp]),
     "rmx_linear_scan_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "rmx_linear_scan_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "rmx_mamba2_cp_correction": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
+                                        _i32, _i32, _i32, _vp]),
 }
 
 _lock = threading.Lock()

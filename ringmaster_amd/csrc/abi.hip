@@ -294,4 +294,31 @@ int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* dh, flo
                     "rmx_linear_scan_bwd launch");
 }
 
+int32_t rmx_mamba2_cp_correction(const uint16_t* out, uint16_t* y, const float* h_final,
+                                 float* h_final_out, const uint16_t* C, const float* cum_A,
+                                 const float* h_prev, const int32_t* seq_idx, int32_t batch,
+                                 int32_t T, int32_t nheads, int32_t head_dim, int32_t ngroups,
+                                 int32_t d_state, void* stream) {
+  if (batch < 0 || T < 0 || nheads < 0) return fail(RMX_EINVAL, "negative shape");
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return fail(RMX_EUNSUPPORTED, "head_dim must be 32, 64 or 128 (got %d)", head_dim);
+  if (d_state != 16 && d_state != 32 && d_state != 64 && d_state != 128 && d_state != 256)
+    return fail(RMX_EUNSUPPORTED, "d_state must be 16, 32, 64, 128 or 256 (got %d)", d_state);
+  if ((int64_t)head_dim * d_state > 32768)
+    return fail(RMX_EUNSUPPORTED, "head_dim * d_state must be at most 32768 (got %d x %d)",
+                head_dim, d_state);
+  if (ngroups <= 0 || nheads % ngroups)
+    return fail(RMX_EINVAL, "ngroups (%d) must divide nheads (%d)", ngroups, nheads);
+  if ((int64_t)batch * nheads == 0) return RMX_OK;
+  if (T == 0) return fail(RMX_EINVAL, "the shard has no tokens (T == 0)");
+  if (!out || !y || !h_final || !h_final_out || !C || !cum_A || !h_prev)
+    return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!aligned(C, 16) || !aligned(h_prev, 16) || !aligned(h_final, 16) || !aligned(h_final_out, 16))
+    return fail(RMX_EINVAL, "C, h_prev, h_final and h_final_out must be 16-byte aligned");
+  return dev_status(rmx::launch_mamba2_correction(out, y, h_final, h_final_out, C, cum_A, h_prev,
+                                                  seq_idx, batch, T, nheads, head_dim, ngroups,
+                                                  d_state, (hipStream_t)stream),
+                    "rmx_mamba2_cp_correction launch");
+}
+
 }  // extern "C"

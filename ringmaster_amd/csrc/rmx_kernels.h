@@ -28,6 +28,12 @@ hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* d
                                   float* db, int batch, int L, int d, int groups, int world,
                                   hipStream_t stream);
 
+hipError_t launch_mamba2_correction(const uint16_t* out, uint16_t* y, const float* h_final,
+                                    float* h_final_out, const uint16_t* C, const float* cum_A,
+                                    const float* h_prev, const int32_t* seq_idx, int batch, int T,
+                                    int nheads, int head_dim, int ngroups, int d_state,
+                                    hipStream_t stream);
+
 }  // namespace rmx
 
 namespace rmx {

@@ -239,3 +239,47 @@ def test_mamba2_prefix_equals_global_ssd(world):
     for r, (out_c, h_final, sl, cum_A) in enumerate(parts):
         corrected, _ = sp.mamba2_cp_correction(out_c, h_final, C[:, sl], cum_A, prefixes[r], H, d)
         assert (corrected - ref_out[:, sl]).abs().max().item() < 1e-6
+
+
+def _ssd_segments(x, dt, A, B, C, seg):
+    """SSD with the state reset at every segment start (packed sequences): per-segment
+    ssd_reference runs, concatenated; returns (out, final state of the last segment)."""
+    outs, h = [], None
+    bounds = [0] + [t for t in range(1, seg.numel()) if seg[t] != seg[t - 1]] + [seg.numel()]
+    for lo, hi in zip(bounds, bounds[1:]):
+        o, h = sp.ssd_reference(x[:, lo:hi], dt[:, lo:hi], A, B[:, lo:hi], C[:, lo:hi])
+        outs.append(o)
+    return torch.cat(outs, 1), h
+
+
+@pytest.mark.parametrize("cut", [5, 11])
+def test_mamba2_correction_packed_sequences(cut):
+    """Two packed documents over two ranks: per-rank SSD with resets at the document
+    boundary, the single-hop prefix and the seq_idx-masked correction equal the
+    per-document SSD (strategies/mamba.py:68-98,101-139)."""
+    torch.manual_seed(1)
+    b, T, H, d, G, n = 1, 16, 2, 3, 1, 4
+    x = torch.randn(b, T, H, d, dtype=torch.float64)
+    dt = torch.rand(b, T, H, dtype=torch.float64) * 0.1
+    A = -torch.rand(H, dtype=torch.float64)
+    B = torch.randn(b, T, G, n, dtype=torch.float64)
+    C = torch.randn(b, T, G, n, dtype=torch.float64)
+    doc = (torch.arange(T) >= cut).long()                 # document id per token
+    ref_out, _ = _ssd_segments(x, dt, A, B, C, doc)
+    world, n_loc = 2, T // 2
+    shards = [slice(r * n_loc, (r + 1) * n_loc) for r in range(world)]
+    finals, decays, parts = [], [], []
+    for sl in shards:
+        seg = doc[sl]
+        out_c, h_final = _ssd_segments(x[:, sl], dt[:, sl], A, B[:, sl], C[:, sl], seg)
+        cum_A = torch.cumsum(A[None, None, :] * dt[:, sl], dim=1)
+        finals.append(h_final)
+        decays.append(torch.exp(cum_A[:, -1]))
+        seq_idx = (seg - seg[0]).reshape(1, -1)             # 0 = continues the incoming document
+        parts.append((out_c, h_final, sl, cum_A, seq_idx))
+    # single hop: rank 1 receives rank 0's final state
+    prefixes = [torch.zeros_like(finals[0]), finals[0]]
+    for r, (out_c, h_final, sl, cum_A, seq_idx) in enumerate(parts):
+        corrected, _ = sp.mamba2_cp_correction(out_c, h_final, C[:, sl], cum_A, prefixes[r], H, d,
+                                               seq_idx=seq_idx)
+        assert (corrected - ref_out[:, sl]).abs().max().item() < 1e-6
