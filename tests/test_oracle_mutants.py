@@ -134,3 +134,16 @@ def test_scan_mutants_are_caught():
     for mutant in (no_correction, reversed_prefix):
         with pytest.raises(AssertionError):
             pin.check_scan(mutant, world=4, T=16)
+
+
+def test_correction_seq_idx_mutant_is_caught(monkeypatch):
+    """A correction that ignores seq_idx (adds the carried state to a packed sequence
+    that starts fresh on the rank) fails the packed-sequence pinning check."""
+    real = sp.mamba2_cp_correction
+
+    def ignore_seq_idx(out, h_final, C, cum_A, h_prev, num_heads, head_dim, seq_idx=None):
+        return real(out, h_final, C, cum_A, h_prev, num_heads, head_dim, seq_idx=None)
+
+    monkeypatch.setattr(sp, "mamba2_cp_correction", ignore_seq_idx)
+    with pytest.raises(AssertionError):
+        pin.test_mamba2_correction_packed_sequences(11)
