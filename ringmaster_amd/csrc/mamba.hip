@@ -22,6 +22,7 @@
 // seq_idx are one value per lane. One workgroup = 4 waves walks 1024 tokens of
 // one (batch, head), 32 tokens per wave and step. The kernel is HBM-bound on
 // reading `out` and writing `y` (4 bytes per element).
+#include <algorithm>
 #include <type_traits>
 
 #include "rmx_kernels.h"
@@ -37,7 +38,7 @@ struct MambaCorrArgs {
   const float* cum_A;
   const float* h_prev;
   const int32_t* seq_idx;
-  int T, nheads, head_dim, ngroups, d_state;
+  int batch, T, nheads, head_dim, ngroups, d_state;
 };
 
 constexpr int kMambaTokensPerWg = 1024;
@@ -176,13 +177,245 @@ __global__ __launch_bounds__(256) void mamba2_correction_kernel(const MambaCorrA
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming variant for d_state <= 128 (the production Mamba2 shapes). A
+// "unit" is SL = min(head_dim, 64) channels of one head; a workgroup holds 4
+// units of heads that share one C group and walks kMambaTokensPerWg tokens,
+// 32 per step. Per wave:
+//  * H_in of its unit lives in registers for the whole walk, as the MFMA A
+//    operands (bf16 hi + lo, 2 * NDB * NS * 4 VGPRs), loaded once;
+//  * the step's C rows (shared by the 4 waves), its out rows and its cum_A /
+//    seq_idx values arrive by LDS DMA two steps ahead, in 3-stage rings; every
+//    global access is a 16-byte lane of a full 128-byte line (out, y, C) except
+//    cum_A, whose per-token value sits at a head stride;
+//  * dY^T = H_in C^T runs on MFMA with sigma-permuted A rows, so a lane holds
+//    runs of 8 consecutive channels of one token; out + dY is formed in place in
+//    the out stage (same 16-byte slots), then re-read row-wise and stored as
+//    full lines through a buffer resource that drops rows past the range end.
+// Workgroups are renumbered so that consecutive logical ids (the token blocks
+// of one unit group, then the unit groups of one batch row) land on the same
+// XCD: H_in and C are then fetched from HBM about once per XCD and re-read from
+// its L2.
+constexpr int kMambaFastTokensPerWg = 1024;
+
+// 16-byte chunk swizzle for LDS rows of CH chunks: the chunk XOR that makes 16
+// consecutive rows' reads of one logical chunk hit 16 distinct bank groups.
+template <int CH>
+__device__ __forceinline__ int swz_chunks(int row) {
+  constexpr int RP = CH >= 16 ? 1 : 16 / CH;  // rows per 256-byte bank line
+  return (row / RP) & (CH - 1);
+}
+
+template <int SL, int N>
+struct MambaFastCfg {
+  static constexpr int NDB = SL / 32;              // 32-channel blocks per unit
+  static constexpr int NS = N / 16;                // MFMA k-steps over d_state
+  static constexpr int CHC = N / 8;                // 16-byte chunks per C row
+  static constexpr int CHO = SL / 8;               // 16-byte chunks per out row of a unit
+  static constexpr int NI = SL / 16;               // out DMA / y store instructions per step
+  static constexpr int ND = N >= 64 ? N / 64 : 1;  // C DMA instructions per wave and step
+  static constexpr int CS = ND * 4 * 1024;         // C stage bytes (rows past 32 are padding)
+  static constexpr int OS = 32 * SL * 2;           // out stage bytes per wave
+  static constexpr int AS = 512;                   // cum_A (256 B) + seq_idx (256 B) per wave
+  static constexpr int NDMA = ND + NI + 2;         // DMA instructions per wave and step
+};
+
+template <int SL, int N>
+__global__ __launch_bounds__(256, 2) void mamba2_correction_stream_kernel(const MambaCorrArgs a,
+                                                                          const int ntb,
+                                                                          const int nug) {
+  using F = MambaFastCfg<SL, N>;
+  constexpr int NDB = F::NDB, NS = F::NS, CHC = F::CHC, CHO = F::CHO, NI = F::NI, ND = F::ND;
+  constexpr int CS = F::CS, OS = F::OS, AS = F::AS;
+  __shared__ __attribute__((aligned(16))) uint8_t sC[3 * CS];
+  __shared__ __attribute__((aligned(16))) uint8_t sO[4][3 * OS];
+  __shared__ __attribute__((aligned(16))) uint8_t sA[4][3 * AS];
+
+  int id = blockIdx.x;
+  const int nwg = gridDim.x;
+  if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
+  const int tb = id % ntb, rest = id / ntb;
+  const int ug = rest % nug, bb = rest / nug;
+  const int T = a.T, H = a.nheads, HD = a.head_dim, G = a.ngroups;
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: resources stay in SGPRs
+  const int uph = HD / SL;  // units per head
+  const int unit = 4 * ug + wave, h = unit / uph, sl = unit % uph;
+  const int g = (4 * ug / uph) / (H / G);  // one C group for the whole workgroup
+  const int tbeg = tb * kMambaFastTokensPerWg;
+  const int tend = tbeg + kMambaFastTokensPerWg < T ? tbeg + kMambaFastTokensPerWg : T;
+  const int nstep = (tend - tbeg + 31) / 32;
+  const int64_t HHD = (int64_t)H * HD;
+  const int64_t hbase = (((int64_t)bb * H + h) * HD + (int64_t)sl * SL) * N;  // unit's rows of [HD][N]
+
+  // ---- the state update (first token block): coalesced over the unit's SL x N block
+  if (tb == 0) {
+    bool fresh_last = false;  // seq_idx[:, -1].any() over the whole batch (:131)
+    if (a.seq_idx)
+      for (int b2 = 0; b2 < a.batch; ++b2) fresh_last |= a.seq_idx[(int64_t)b2 * T + T - 1] != 0;
+    const float e = fresh_last ? 0.f : expf(a.cum_A[((int64_t)bb * T + T - 1) * H + h]);
+    for (int i = 4 * lane; i < SL * N; i += 4 * 64) {
+      const f32x4 hf = *reinterpret_cast<const f32x4*>(a.h_final + hbase + i);
+      const f32x4 hp = *reinterpret_cast<const f32x4*>(a.h_prev + hbase + i);
+      *reinterpret_cast<f32x4*>(a.h_final_out + hbase + i) = hf + hp * e;
+    }
+  }
+
+  // ---- H_in -> registers: A operand (db, ks) = rows 32 db + sigma(l32), k = 16 ks + 8 hl ..
+  bf16x8 ahi[NDB][NS], alo[NDB][NS];
+  {
+    const float* hrow = a.h_prev + hbase + (int64_t)sigma(l32) * N + 8 * hl;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int ks = 0; ks < NS; ++ks) {
+        const float* src = hrow + (int64_t)32 * db * N + 16 * ks;
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
+        const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        u32x4 hi, lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // hardware round-to-nearest-even; lo = the exact remainder, rounded
+          hi[i] = cvt_pk_bf16(xv[2 * i], xv[2 * i + 1]);
+          lo[i] = cvt_pk_bf16(xv[2 * i] - __uint_as_float(hi[i] << 16),
+                              xv[2 * i + 1] - __uint_as_float(hi[i] & 0xffff0000u));
+        }
+        ahi[db][ks] = __builtin_bit_cast(bf16x8, hi);
+        alo[db][ks] = __builtin_bit_cast(bf16x8, lo);
+      }
+  }
+
+  // ---- buffer resources (offsets at or past num_records read zeros / drop stores)
+  const int cstride = G * N * 2, ostride = (int)(HHD * 2);
+  const i32x4 rC = make_rsrc(a.C + ((int64_t)bb * T * G + g) * N, span_bytes(T, cstride, N * 2));
+  const i32x4 rO = make_rsrc(a.out + (int64_t)bb * T * HHD + (int64_t)h * HD + sl * SL,
+                             span_bytes(T, ostride, SL * 2));
+  const i32x4 rY = make_rsrc(a.y + ((int64_t)bb * T + tbeg) * HHD + (int64_t)h * HD + sl * SL,
+                             span_bytes(tend - tbeg, ostride, SL * 2));
+  const i32x4 rA = make_rsrc(a.cum_A + (int64_t)bb * T * H + h, span_bytes(T, H * 4, 4));
+  const i32x4 rS = a.seq_idx ? make_rsrc(a.seq_idx + (int64_t)bb * T, (uint32_t)T * 4u)
+                             : make_rsrc(a.cum_A, 0u);
+  const uint32_t ldsC = lds_addr(sC), ldsO = lds_addr(sO[wave]), ldsA = lds_addr(sA[wave]);
+
+  auto issue = [&](int st, int t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const int p = (i * 4 + wave) * 64 + lane, row = p / CHC, pc = p % CHC;
+      const int off = row < 32 ? (t0 + row) * cstride + 16 * (pc ^ swz_chunks<CHC>(row))
+                               : (int)span_bytes(T, cstride, N * 2);
+      dma16_async(rC, ldsC + st * CS + (i * 4 + wave) * 1024, off);
+    }
+#pragma unroll
+    for (int k = 0; k < NI; ++k) {
+      const int p = 64 * k + lane, row = p / CHO, pc = p % CHO;
+      dma16_async(rO, ldsO + st * OS + 1024 * k,
+                  (t0 + row) * ostride + 16 * (pc ^ swz_chunks<CHO>(row)));
+    }
+    dma4_async(rA, ldsA + st * AS, (t0 + l32) * (H * 4));
+    dma4_async(rS, ldsA + st * AS + 256, (t0 + l32) * 4);
+  };
+
+  issue(0, tbeg);
+  if (nstep > 1) issue(1, tbeg + 32);
+  // vmcnt budget at the top of step s: everything issued after step s's DMA may
+  // stay in flight (the y stores of steps s-2 and s-1, the DMA of step s+1)
+  constexpr int K0 = F::NDMA, K1 = F::NDMA + NI, KS = F::NDMA + 2 * NI;
+  for (int s = 0; s < nstep; ++s) {
+    if (s >= 2 && s + 1 < nstep)
+      wait_vm_barrier<KS>();
+    else if (s == 1 && nstep > 2)
+      wait_vm_barrier<K1>();
+    else if (s == 0 && nstep > 1)
+      wait_vm_barrier<K0>();
+    else
+      wait_vm_barrier<0>();
+    if (s + 2 < nstep) issue((s + 2) % 3, tbeg + 32 * (s + 2));
+    const int st = s % 3;
+
+    const uint8_t* cst = sC + st * CS + l32 * (CHC * 16);
+    f32x16 acc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[db] = zero16();
+#pragma unroll
+    for (int ks = 0; ks < NS; ++ks) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(cst + 16 * ((2 * ks + hl) ^ swz_chunks<CHC>(l32)));
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) acc[db] = mfma32(ahi[db][ks], b, acc[db]);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) acc[db] = mfma32(alo[db][ks], b, acc[db]);
+    }
+    const uint8_t* ast = sA[wave] + st * AS;
+    const float ca = reinterpret_cast<const float*>(ast)[l32];
+    const int sq = reinterpret_cast<const int32_t*>(ast + 256)[l32];
+    const float e = sq != 0 ? 0.f : expf(ca);
+
+    // out + bf16(dY) in place: lane (hl, l32), reg r of block db holds channel
+    // 32 db + 16 (r / 8) + 8 hl + r % 8 of token l32 = logical chunk 4 db + 2 (r / 8) + hl
+    uint8_t* ost = sO[wave] + st * OS;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int c = 4 * db + 2 * half + hl;
+        u32x4* slot = reinterpret_cast<u32x4*>(ost + 16 * (l32 * CHO + (c ^ swz_chunks<CHO>(l32))));
+        const u32x4 ov = *slot;
+        u32x4 yv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // bf16(out + bf16(dy)), both roundings to nearest even
+          const uint32_t dy = cvt_pk_bf16(acc[db][8 * half + 2 * i] * e, acc[db][8 * half + 2 * i + 1] * e);
+          yv[i] = cvt_pk_bf16(__uint_as_float(ov[i] << 16) + __uint_as_float(dy << 16),
+                              __uint_as_float(ov[i] & 0xffff0000u) + __uint_as_float(dy & 0xffff0000u));
+        }
+        *slot = yv;
+      }
+    // y rows back out as full 128-byte lines (rows past the range end are dropped)
+#pragma unroll
+    for (int k = 0; k < NI; ++k) {
+      const int p = 64 * k + lane, row = p / CHO, pc = p % CHO;
+      const u32x4 yv = *reinterpret_cast<const u32x4*>(ost + 16 * p);
+      buf_store16(rY, (32 * s + row) * ostride + 16 * (pc ^ swz_chunks<CHO>(row)), yv);
+    }
+  }
+}
+
 hipError_t launch_mamba2_correction(const uint16_t* out, uint16_t* y, const float* h_final,
                                     float* h_final_out, const uint16_t* C, const float* cum_A,
                                     const float* h_prev, const int32_t* seq_idx, int batch, int T,
                                     int nheads, int head_dim, int ngroups, int d_state,
                                     hipStream_t stream) {
   MambaCorrArgs a{out, y, h_final, h_final_out, C, cum_A, h_prev, seq_idx,
-                  T, nheads, head_dim, ngroups, d_state};
+                  batch, T, nheads, head_dim, ngroups, d_state};
+  // streaming kernel: 4 units (SL channels of a head) per workgroup, all in one C group,
+  // and every buffer offset (up to two 32-token steps past T) within int32
+  const int SL = head_dim == 32 ? 32 : 64, uph = head_dim / SL;
+  const int units = nheads * uph, heads_per_wg = 4 / uph;
+  const int64_t row_bytes = std::max<int64_t>({(int64_t)nheads * head_dim * 2,
+                                              (int64_t)ngroups * d_state * 2, (int64_t)nheads * 4});
+  if (d_state <= 128 && units % 4 == 0 && (nheads / ngroups) % heads_per_wg == 0 &&
+      ((int64_t)T + 64) * row_bytes < ((int64_t)1 << 31)) {
+    const int ntb = (T + kMambaFastTokensPerWg - 1) / kMambaFastTokensPerWg, nug = units / 4;
+    const dim3 sgrid((unsigned)((int64_t)nug * ntb * batch));
+    auto go = [&](auto sl, auto n) {
+      constexpr int S = decltype(sl)::value, NN = decltype(n)::value;
+      hipLaunchKernelGGL((mamba2_correction_stream_kernel<S, NN>), sgrid, dim3(256), 0, stream, a, ntb,
+                         nug);
+    };
+    auto by_n = [&](auto sl) {
+      switch (d_state) {
+        case 16: go(sl, std::integral_constant<int, 16>{}); break;
+        case 32: go(sl, std::integral_constant<int, 32>{}); break;
+        case 64: go(sl, std::integral_constant<int, 64>{}); break;
+        default: go(sl, std::integral_constant<int, 128>{}); break;
+      }
+    };
+    if (SL == 32)
+      by_n(std::integral_constant<int, 32>{});
+    else
+      by_n(std::integral_constant<int, 64>{});
+    return hipGetLastError();
+  }
   const dim3 grid(nheads, (T + kMambaTokensPerWg - 1) / kMambaTokensPerWg, batch);
   auto go = [&](auto hd, auto n) {
     constexpr int HD = decltype(hd)::value, N = decltype(n)::value;

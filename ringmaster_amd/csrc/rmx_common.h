@@ -139,6 +139,15 @@ __device__ __forceinline__ u32x4 buf_load16(const i32x4& rsrc, int byte_off) {
   return llvm_raw_buffer_load_v4(rsrc, byte_off, 0, 0);
 }
 
+// Stores at or past num_records are dropped by the hardware, so a tile's rows
+// past the end of its range need no branch (and every wave issues the same
+// number of stores, which keeps vmcnt accounting static).
+__device__ void llvm_raw_buffer_store_v4(u32x4 data, i32x4 rsrc, int voffset, int soffset,
+                                         int aux) __asm("llvm.amdgcn.raw.buffer.store.v4i32");
+__device__ __forceinline__ void buf_store16(const i32x4& rsrc, int byte_off, const u32x4& v) {
+  llvm_raw_buffer_store_v4(v, rsrc, byte_off, 0, 0);
+}
+
 // Bytes a buffer over `rows` rows of `row_bytes` at stride `stride_bytes` must cover.
 __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride_bytes, int row_bytes) {
   return rows <= 0 ? 0u : (uint32_t)((int64_t)(rows - 1) * stride_bytes + row_bytes);
@@ -233,9 +242,9 @@ __device__ __forceinline__ void dma4_async(const i32x4& rsrc, uint32_t lds, int 
 // lgkmcnt[11:8], vmcnt[15:14].
 template <int VM>
 __device__ __forceinline__ void wait_vm_barrier() {
-  static_assert(VM >= 0 && VM < 16, "vmcnt range");
+  static_assert(VM >= 0 && VM < 64, "vmcnt range");
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(VM | (7 << 4));  // vmcnt(VM) lgkmcnt(0)
+  __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | ((VM >> 4) << 14));  // vmcnt(VM) lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }

@@ -55,15 +55,24 @@ def _check(args, H, d, seq_idx=None):
     assert_f32_rel(hf, ref_h, "h_final")
 
 
-@pytest.mark.parametrize("T,H,d,G,n", [(200, 4, 64, 1, 128), (96, 6, 32, 2, 16),
-                                       (130, 2, 128, 2, 64), (1, 3, 64, 3, 32)])
+# Streaming kernel (d_state <= 128, 4 units of min(d, 64) channels per workgroup in one
+# C group): (200,4,64,1,128), (70,8,32,2,32), (300,4,128,2,64) (two units per head),
+# (2100,4,64,1,16) (three 1024-token blocks, ragged last step), (64,4,64,1,64) (two
+# steps), (1,4,64,1,128) (one token). General kernel: (96,6,32,2,16), (130,2,128,2,64)
+# (one head per group), (1,3,64,3,32), (40,2,64,1,256) (d_state 256).
+@pytest.mark.parametrize("T,H,d,G,n", [(200, 4, 64, 1, 128), (70, 8, 32, 2, 32),
+                                       (300, 4, 128, 2, 64), (2100, 4, 64, 1, 16),
+                                       (64, 4, 64, 1, 64), (1, 4, 64, 1, 128),
+                                       (96, 6, 32, 2, 16), (130, 2, 128, 2, 64),
+                                       (1, 3, 64, 3, 32), (40, 2, 64, 1, 256)])
 def test_correction_matches_oracle(T, H, d, G, n):
     _check(_inputs(2, T, H, d, G, n, seed=10), H, d)
 
 
+@pytest.mark.parametrize("H,G", [(4, 1), (2, 2)])   # streaming kernel, general kernel
 @pytest.mark.parametrize("fresh_last", [False, True])
-def test_correction_seq_idx(fresh_last):
-    Bsz, T, H, d, G, n = 2, 160, 4, 64, 1, 32
+def test_correction_seq_idx(fresh_last, H, G):
+    Bsz, T, d, n = 2, 160, 64, 32
     args = _inputs(Bsz, T, H, d, G, n, seed=20)
     seq_idx = torch.zeros(Bsz, T, dtype=torch.int32)
     seq_idx[0, 70:] = 1                    # a new packed sequence starts at token 70
