@@ -180,29 +180,38 @@ __global__ __launch_bounds__(256) void mamba2_correction_kernel(const MambaCorrA
 // ---------------------------------------------------------------------------
 // Streaming variant for d_state <= 128 (the production Mamba2 shapes). A
 // "unit" is SL = min(head_dim, 64) channels of one head; a workgroup holds 4
-// units of heads that share one C group and walks kMambaTokensPerWg tokens,
+// units of heads that share one C group and walks kMambaFastTokensPerWg tokens,
 // 32 per step. Per wave:
 //  * H_in of its unit lives in registers for the whole walk, as the MFMA A
-//    operands (bf16 hi + lo, 2 * NDB * NS * 4 VGPRs), loaded once;
-//  * the step's C rows (shared by the 4 waves), its out rows and its cum_A /
-//    seq_idx values arrive by LDS DMA two steps ahead, in 3-stage rings; every
-//    global access is a 16-byte lane of a full 128-byte line (out, y, C) except
-//    cum_A, whose per-token value sits at a head stride;
+//    operands (bf16 hi + lo, 2 * NDB * NS * 4 VGPRs). It is read once with
+//    coalesced 16-byte loads, split into hi + lo and transposed through LDS into
+//    the operand layout (a direct operand-layout load would touch 32 cache lines
+//    per instruction);
+//  * the step's C rows, cum_A values (of the workgroup's heads) and seq_idx
+//    values are shared by the 4 waves, its out rows are its own; all arrive by
+//    LDS DMA two steps ahead, in 3-stage rings, and every wave issues the same
+//    number of DMA instructions per step, so the vmcnt budget is static;
 //  * dY^T = H_in C^T runs on MFMA with sigma-permuted A rows, so a lane holds
 //    runs of 8 consecutive channels of one token; out + dY is formed in place in
 //    the out stage (same 16-byte slots), then re-read row-wise and stored as
-//    full lines through a buffer resource that drops rows past the range end.
-// Workgroups are renumbered so that consecutive logical ids (the token blocks
-// of one unit group, then the unit groups of one batch row) land on the same
-// XCD: H_in and C are then fetched from HBM about once per XCD and re-read from
-// its L2.
-constexpr int kMambaFastTokensPerWg = 1024;
+//    full 128-byte lines through a buffer resource that drops rows past the
+//    range end.
+// Workgroups are renumbered so that consecutive logical ids land on the same
+// XCD, unit groups fastest: the workgroups running together on an XCD cover
+// whole token rows of out / y (every head) for a few token blocks of one batch
+// row, so their HBM traffic spreads over all channels, each C tile is fetched
+// once and re-read from that XCD's L2, and so is each unit's H_in. 2048 tokens
+// per workgroup amortise the H_in prologue (and at configs[4] give exactly two
+// resident workgroups per CU).
+constexpr int kMambaFastTokensPerWg = 2048;
 
-// 16-byte chunk swizzle for LDS rows of CH chunks: the chunk XOR that makes 16
-// consecutive rows' reads of one logical chunk hit 16 distinct bank groups.
+// 16-byte chunk swizzle for LDS rows of CH chunks. A ds_read/write_b128 is
+// served 8 lanes at a time from one 128-byte bank window, so the 8 rows that 8
+// consecutive lanes touch (one logical chunk each) must land in 8 distinct
+// 16-byte bank slots: (row * CH + (c ^ swz(row))) mod 8 distinct over 8 rows.
 template <int CH>
 __device__ __forceinline__ int swz_chunks(int row) {
-  constexpr int RP = CH >= 16 ? 1 : 16 / CH;  // rows per 256-byte bank line
+  constexpr int RP = CH >= 8 ? 1 : 8 / CH;  // rows sharing one 128-byte window
   return (row / RP) & (CH - 1);
 }
 
@@ -210,14 +219,17 @@ template <int SL, int N>
 struct MambaFastCfg {
   static constexpr int NDB = SL / 32;              // 32-channel blocks per unit
   static constexpr int NS = N / 16;                // MFMA k-steps over d_state
-  static constexpr int CHC = N / 8;                // 16-byte chunks per C row
+  static constexpr int CHC = N / 8;                // 16-byte chunks per C row (and per H row in bf16)
   static constexpr int CHO = SL / 8;               // 16-byte chunks per out row of a unit
   static constexpr int NI = SL / 16;               // out DMA / y store instructions per step
   static constexpr int ND = N >= 64 ? N / 64 : 1;  // C DMA instructions per wave and step
   static constexpr int CS = ND * 4 * 1024;         // C stage bytes (rows past 32 are padding)
   static constexpr int OS = 32 * SL * 2;           // out stage bytes per wave
-  static constexpr int AS = 512;                   // cum_A (256 B) + seq_idx (256 B) per wave
+  static constexpr int XS = 2 * 4 * 256;           // cum_A + seq_idx stage: one 256-byte DMA per wave each
   static constexpr int NDMA = ND + NI + 2;         // DMA instructions per wave and step
+  static constexpr int RING = 3 * CS + 4 * 3 * OS + 3 * XS;
+  static constexpr int HSCR = 4 * 32 * N * 4;      // H_in transpose: 32 rows x N (bf16 hi + lo) per wave
+  static constexpr int LDS = RING > HSCR ? RING : HSCR;
 };
 
 template <int SL, int N>
@@ -226,84 +238,113 @@ __global__ __launch_bounds__(256, 2) void mamba2_correction_stream_kernel(const 
                                                                           const int nug) {
   using F = MambaFastCfg<SL, N>;
   constexpr int NDB = F::NDB, NS = F::NS, CHC = F::CHC, CHO = F::CHO, NI = F::NI, ND = F::ND;
-  constexpr int CS = F::CS, OS = F::OS, AS = F::AS;
-  __shared__ __attribute__((aligned(16))) uint8_t sC[3 * CS];
-  __shared__ __attribute__((aligned(16))) uint8_t sO[4][3 * OS];
-  __shared__ __attribute__((aligned(16))) uint8_t sA[4][3 * AS];
+  constexpr int CS = F::CS, OS = F::OS, XS = F::XS;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F::LDS];
+  uint8_t* const sC = smem;                       // [3][CS]
+  uint8_t* const sO = smem + 3 * CS;              // [4 waves][3][OS]
+  uint8_t* const sX = sO + 4 * 3 * OS;            // [3][XS]: cum_A [4][256 B], seq_idx [4][256 B]
 
   int id = blockIdx.x;
   const int nwg = gridDim.x;
   if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
-  const int tb = id % ntb, rest = id / ntb;
-  const int ug = rest % nug, bb = rest / nug;
+  const int ug = id % nug, rest = id / nug;
+  const int tb = rest % ntb, bb = rest / ntb;
   const int T = a.T, H = a.nheads, HD = a.head_dim, G = a.ngroups;
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: resources stay in SGPRs
-  const int uph = HD / SL;  // units per head
+  const int uph = HD / SL;             // units per head
+  const int hpw = 4 / uph;             // heads per workgroup
+  const int h0 = 4 * ug / uph;         // first head of the workgroup
   const int unit = 4 * ug + wave, h = unit / uph, sl = unit % uph;
-  const int g = (4 * ug / uph) / (H / G);  // one C group for the whole workgroup
+  const int g = h0 / (H / G);          // one C group for the whole workgroup
   const int tbeg = tb * kMambaFastTokensPerWg;
   const int tend = tbeg + kMambaFastTokensPerWg < T ? tbeg + kMambaFastTokensPerWg : T;
   const int nstep = (tend - tbeg + 31) / 32;
   const int64_t HHD = (int64_t)H * HD;
   const int64_t hbase = (((int64_t)bb * H + h) * HD + (int64_t)sl * SL) * N;  // unit's rows of [HD][N]
 
-  // ---- the state update (first token block): coalesced over the unit's SL x N block
+  // ---- H_in -> registers (and, in the first token block, the state update).
+  // Per 32-row block: coalesced fp32 loads -> bf16 hi/lo rows in this wave's LDS
+  // scratch ([32][N] each, 16-byte chunks swizzled) -> A operands (db, ks) =
+  // rows 32 db + sigma(l32), k = 16 ks + 8 hl .. + 7.
+  float e_last = 0.f;
   if (tb == 0) {
     bool fresh_last = false;  // seq_idx[:, -1].any() over the whole batch (:131)
     if (a.seq_idx)
       for (int b2 = 0; b2 < a.batch; ++b2) fresh_last |= a.seq_idx[(int64_t)b2 * T + T - 1] != 0;
-    const float e = fresh_last ? 0.f : expf(a.cum_A[((int64_t)bb * T + T - 1) * H + h]);
-    for (int i = 4 * lane; i < SL * N; i += 4 * 64) {
-      const f32x4 hf = *reinterpret_cast<const f32x4*>(a.h_final + hbase + i);
-      const f32x4 hp = *reinterpret_cast<const f32x4*>(a.h_prev + hbase + i);
-      *reinterpret_cast<f32x4*>(a.h_final_out + hbase + i) = hf + hp * e;
-    }
+    e_last = fresh_last ? 0.f : expf(a.cum_A[((int64_t)bb * T + T - 1) * H + h]);
   }
-
-  // ---- H_in -> registers: A operand (db, ks) = rows 32 db + sigma(l32), k = 16 ks + 8 hl ..
   bf16x8 ahi[NDB][NS], alo[NDB][NS];
   {
-    const float* hrow = a.h_prev + hbase + (int64_t)sigma(l32) * N + 8 * hl;
+    uint16_t* const shi = reinterpret_cast<uint16_t*>(smem + wave * (32 * N * 4));
+    uint16_t* const slo = shi + 32 * N;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+    for (int db = 0; db < NDB; ++db) {
+      const int64_t blk = hbase + (int64_t)32 * db * N;
+      // 32 rows x N fp32 = N/8 loads of 1 KB per wave, all issued before any use
+      f32x4 xs[N / 8];
+#pragma unroll
+      for (int q = 0; q < N / 8; ++q)
+        xs[q] = *reinterpret_cast<const f32x4*>(a.h_prev + blk + 4 * (64 * q + lane));
+      if (tb == 0) {
+        f32x4 hf[N / 8];
+#pragma unroll
+        for (int q = 0; q < N / 8; ++q)
+          hf[q] = *reinterpret_cast<const f32x4*>(a.h_final + blk + 4 * (64 * q + lane));
+#pragma unroll
+        for (int q = 0; q < N / 8; ++q)
+          *reinterpret_cast<f32x4*>(a.h_final_out + blk + 4 * (64 * q + lane)) = hf[q] + xs[q] * e_last;
+      }
+#pragma unroll
+      for (int q = 0; q < N / 8; ++q) {
+        const int p = 64 * q + lane, row = p / (N / 4), n0 = 4 * (p % (N / 4));
+        const f32x4 x = xs[q];
+        u32x2 hi, lo;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          // hardware round-to-nearest-even; lo = the exact remainder, rounded
+          hi[i] = cvt_pk_bf16(x[2 * i], x[2 * i + 1]);
+          lo[i] = cvt_pk_bf16(x[2 * i] - __uint_as_float(hi[i] << 16),
+                              x[2 * i + 1] - __uint_as_float(hi[i] & 0xffff0000u));
+        }
+        const int off = row * N + 8 * ((n0 >> 3) ^ (swz_row(row) & (CHC - 1))) + (n0 & 4);
+        *reinterpret_cast<u32x2*>(shi + off) = hi;
+        *reinterpret_cast<u32x2*>(slo + off) = lo;
+      }
+      const int arow = sigma(l32);
 #pragma unroll
       for (int ks = 0; ks < NS; ++ks) {
-        const float* src = hrow + (int64_t)32 * db * N + 16 * ks;
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
-        const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
-        const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        u32x4 hi, lo;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // hardware round-to-nearest-even; lo = the exact remainder, rounded
-          hi[i] = cvt_pk_bf16(xv[2 * i], xv[2 * i + 1]);
-          lo[i] = cvt_pk_bf16(xv[2 * i] - __uint_as_float(hi[i] << 16),
-                              xv[2 * i + 1] - __uint_as_float(hi[i] & 0xffff0000u));
-        }
-        ahi[db][ks] = __builtin_bit_cast(bf16x8, hi);
-        alo[db][ks] = __builtin_bit_cast(bf16x8, lo);
+        const int off = arow * N + 8 * ((2 * ks + hl) ^ (swz_row(arow) & (CHC - 1)));
+        ahi[db][ks] = *reinterpret_cast<const bf16x8*>(shi + off);
+        alo[db][ks] = *reinterpret_cast<const bf16x8*>(slo + off);
       }
+    }
   }
+  lds_barrier();  // every wave's scratch reads are done before the rings' DMA lands there
 
   // ---- buffer resources (offsets at or past num_records read zeros / drop stores)
   const int cstride = G * N * 2, ostride = (int)(HHD * 2);
-  const i32x4 rC = make_rsrc(a.C + ((int64_t)bb * T * G + g) * N, span_bytes(T, cstride, N * 2));
+  const uint32_t cspan = span_bytes(T, cstride, N * 2), aspan = (uint32_t)T * (uint32_t)H * 4u;
+  const i32x4 rC = make_rsrc(a.C + ((int64_t)bb * T * G + g) * N, cspan);
   const i32x4 rO = make_rsrc(a.out + (int64_t)bb * T * HHD + (int64_t)h * HD + sl * SL,
                              span_bytes(T, ostride, SL * 2));
   const i32x4 rY = make_rsrc(a.y + ((int64_t)bb * T + tbeg) * HHD + (int64_t)h * HD + sl * SL,
                              span_bytes(tend - tbeg, ostride, SL * 2));
-  const i32x4 rA = make_rsrc(a.cum_A + (int64_t)bb * T * H + h, span_bytes(T, H * 4, 4));
-  const i32x4 rS = a.seq_idx ? make_rsrc(a.seq_idx + (int64_t)bb * T, (uint32_t)T * 4u)
-                             : make_rsrc(a.cum_A, 0u);
-  const uint32_t ldsC = lds_addr(sC), ldsO = lds_addr(sO[wave]), ldsA = lds_addr(sA[wave]);
+  const i32x4 rA = make_rsrc(a.cum_A + (int64_t)bb * T * H, aspan);
+  const uint32_t sspan = a.seq_idx ? (uint32_t)T * 4u : 0u;
+  const i32x4 rS = make_rsrc(a.seq_idx ? (const void*)(a.seq_idx + (int64_t)bb * T) : (const void*)a.cum_A,
+                             sspan);
+  const uint32_t ldsC = lds_addr(sC), ldsO = lds_addr(sO + wave * 3 * OS), ldsX = lds_addr(sX);
+  // cum_A / seq_idx: wave w fetches tokens 8 w .. 8 w + 7 of the step; lane L
+  // of the cum_A DMA holds (token 8 w + L / hpw, head h0 + L % hpw)
+  const int xa_tok = 8 * wave + lane / hpw, xa_head = h0 + lane % hpw;
+  const bool xa_live = lane < 8 * hpw;
 
   auto issue = [&](int st, int t0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
       const int p = (i * 4 + wave) * 64 + lane, row = p / CHC, pc = p % CHC;
-      const int off = row < 32 ? (t0 + row) * cstride + 16 * (pc ^ swz_chunks<CHC>(row))
-                               : (int)span_bytes(T, cstride, N * 2);
+      const int off = row < 32 ? (t0 + row) * cstride + 16 * (pc ^ swz_chunks<CHC>(row)) : (int)cspan;
       dma16_async(rC, ldsC + st * CS + (i * 4 + wave) * 1024, off);
     }
 #pragma unroll
@@ -312,8 +353,9 @@ __global__ __launch_bounds__(256, 2) void mamba2_correction_stream_kernel(const 
       dma16_async(rO, ldsO + st * OS + 1024 * k,
                   (t0 + row) * ostride + 16 * (pc ^ swz_chunks<CHO>(row)));
     }
-    dma4_async(rA, ldsA + st * AS, (t0 + l32) * (H * 4));
-    dma4_async(rS, ldsA + st * AS + 256, (t0 + l32) * 4);
+    dma4_async(rA, ldsX + st * XS + 256 * wave,
+               xa_live ? (t0 + xa_tok) * (H * 4) + 4 * xa_head : (int)aspan);
+    dma4_async(rS, ldsX + st * XS + 1024 + 256 * wave, lane < 8 ? (t0 + 8 * wave + lane) * 4 : (int)sspan);
   };
 
   issue(0, tbeg);
@@ -321,6 +363,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_correction_stream_kernel(const 
   // vmcnt budget at the top of step s: everything issued after step s's DMA may
   // stay in flight (the y stores of steps s-2 and s-1, the DMA of step s+1)
   constexpr int K0 = F::NDMA, K1 = F::NDMA + NI, KS = F::NDMA + 2 * NI;
+  const int hw = wave / uph;  // this unit's head within the workgroup
   for (int s = 0; s < nstep; ++s) {
     if (s >= 2 && s + 1 < nstep)
       wait_vm_barrier<KS>();
@@ -345,14 +388,14 @@ __global__ __launch_bounds__(256, 2) void mamba2_correction_stream_kernel(const 
 #pragma unroll
       for (int db = 0; db < NDB; ++db) acc[db] = mfma32(alo[db][ks], b, acc[db]);
     }
-    const uint8_t* ast = sA[wave] + st * AS;
-    const float ca = reinterpret_cast<const float*>(ast)[l32];
-    const int sq = reinterpret_cast<const int32_t*>(ast + 256)[l32];
+    const uint8_t* xst = sX + st * XS;
+    const float ca = reinterpret_cast<const float*>(xst)[64 * (l32 >> 3) + (l32 & 7) * hpw + hw];
+    const int sq = reinterpret_cast<const int32_t*>(xst + 1024)[64 * (l32 >> 3) + (l32 & 7)];
     const float e = sq != 0 ? 0.f : expf(ca);
 
     // out + bf16(dY) in place: lane (hl, l32), reg r of block db holds channel
     // 32 db + 16 (r / 8) + 8 hl + r % 8 of token l32 = logical chunk 4 db + 2 (r / 8) + hl
-    uint8_t* ost = sO[wave] + st * OS;
+    uint8_t* ost = sO + (wave * 3 + st) * OS;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
