@@ -57,7 +57,7 @@ def _check(args, H, d, seq_idx=None):
 
 # Streaming kernel (d_state <= 128, 4 units of min(d, 64) channels per workgroup in one
 # C group): (200,4,64,1,128), (70,8,32,2,32), (300,4,128,2,64) (two units per head),
-# (2100,4,64,1,16) (three 1024-token blocks, ragged last step), (64,4,64,1,64) (two
+# (2100,4,64,1,16) (two 2048-token blocks, the second a ragged 52 tokens), (64,4,64,1,64) (two
 # steps), (1,4,64,1,128) (one token). General kernel: (96,6,32,2,16), (130,2,128,2,64)
 # (one head per group), (1,3,64,3,32), (40,2,64,1,256) (d_state 256).
 @pytest.mark.parametrize("T,H,d,G,n", [(200, 4, 64, 1, 128), (70, 8, 32, 2, 32),
