@@ -236,6 +236,42 @@ def mamba_workload(steps, warmup):
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def mamba_bwd_workload(steps, warmup):
+    """configs[4] Mamba2 CP correction backward (dC, dcumA, dh_prev from dL/dy and
+    dL/dh_final_out) through the C ABI with a preallocated workspace; one launch
+    sequence. Algorithmic bytes: read dy, C, cum_A, h_prev, dh_final; write dC, dcumA,
+    dh_prev. MFMA work: S recomputed with a three-part H_in (3 x 2 T H d n), the dh_prev
+    product with a two-part G e (2 x 2 T H d n) and dC with a two-part H_in (2 x 2 T H d n)."""
+    from ringmaster_amd import abi
+
+    P, T, H, D, N = 8, 8192, 64, 64, 128
+    g = torch.Generator(device="cuda").manual_seed(5)
+    gy = _gen((P, T, H * D), 14)
+    C = _gen((P, T, 1, N), 11)
+    A = -torch.exp(torch.rand(H, generator=g, device="cuda") * math.log(16.0))
+    dt = torch.nn.functional.softplus(torch.randn(P, T, H, generator=g, device="cuda"))
+    cum_A = torch.cumsum(A * dt, dim=1)
+    h_prev = _gen((P, H, D, N), 12, torch.float32)
+    ghf = _gen((P, H, D, N), 15, torch.float32)
+    gC, gA, gH = torch.empty_like(C), torch.empty_like(cum_A), torch.empty_like(h_prev)
+    lib = abi.lib()
+    ws_bytes = lib.rmx_mamba2_cp_correction_bwd_workspace(P, T, H, D, 1, N)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    stream = abi.stream_of(gy)
+
+    def run():
+        abi.check(lib.rmx_mamba2_cp_correction_bwd(
+            gy.data_ptr(), ghf.data_ptr(), C.data_ptr(), cum_A.data_ptr(), h_prev.data_ptr(),
+            None, gC.data_ptr(), gA.data_ptr(), gH.data_ptr(), ws.data_ptr(), ws_bytes,
+            P, T, H, D, 1, N, stream))
+
+    ms = _time(run, steps, warmup)
+    nbytes = gy.numel() * 2 + 2 * C.numel() * 2 + 2 * cum_A.numel() * 4 + 3 * h_prev.numel() * 4
+    flops = 7 * 2 * P * T * H * D * N
+    return {"ms": round(ms, 4), "bytes": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+
+
 def block_workload(steps, warmup):
     """one non-causal ring step, Hq=32/Hkv=8, 16384^2, D=128, fwd+bwd, merged
     into a running fp32 (out, lse) from a prior step."""
@@ -396,6 +432,8 @@ def main():
         extras["cp_linear_scan_configs4"] = scan_workload(30, 3)
         torch.cuda.empty_cache()
         extras["mamba2_correction_configs4"] = mamba_workload(30, 3)
+        torch.cuda.empty_cache()
+        extras["mamba2_correction_bwd_configs4"] = mamba_bwd_workload(20, 3)
         torch.cuda.empty_cache()
         extras["block_configs1"] = block_workload(3, 1)
         torch.cuda.empty_cache()

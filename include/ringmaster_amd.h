@@ -20,13 +20,14 @@
 #ifndef RINGMASTER_AMD_H
 #define RINGMASTER_AMD_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 2
+#define RMX_ABI_VERSION 3  /* 3: Mamba2 correction backward entry points */
 
 /* error codes */
 #define RMX_OK 0
@@ -228,6 +229,29 @@ int32_t rmx_mamba2_cp_correction(const uint16_t* out, uint16_t* y, const float* 
                                  const float* h_prev, const int32_t* seq_idx, int32_t batch,
                                  int32_t T, int32_t nheads, int32_t head_dim, int32_t ngroups,
                                  int32_t d_state, void* stream);
+
+/*
+ * Backward of rmx_mamba2_cp_correction: the gradients autograd takes through the
+ * reference's torch ops (strategies/mamba.py:116-137) for C, cum_A and h_prev.
+ * (The gradients of out and h_final are the upstream ones, unchanged.) Inputs:
+ * gy bf16 [batch, T, nheads * head_dim] (dL/dy); ghf fp32 like h_prev
+ * (dL/dh_final_out, nullable: no gradient reaches it); C, cum_A, h_prev, seq_idx
+ * as in the forward. Outputs: gC bf16 like C, g_cumA fp32 like cum_A, g_hprev
+ * fp32 like h_prev. workspace: device memory of at least
+ * rmx_mamba2_cp_correction_bwd_workspace(...) bytes (block partials of dL/dh_prev,
+ * h_prev^T split into bf16 hi/lo, e^{cum_A} transposed); its contents on entry
+ * do not matter. head_dim in {64, 128}; d_state in {64, 128}; the head slices
+ * of 64 channels come in fours from one C group ((nheads / ngroups) divisible by
+ * 4 at head_dim 64, by 2 at head_dim 128); otherwise RMX_EUNSUPPORTED.
+ */
+size_t rmx_mamba2_cp_correction_bwd_workspace(int32_t batch, int32_t T, int32_t nheads,
+                                              int32_t head_dim, int32_t ngroups, int32_t d_state);
+int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const uint16_t* C,
+                                     const float* cum_A, const float* h_prev,
+                                     const int32_t* seq_idx, uint16_t* gC, float* g_cumA,
+                                     float* g_hprev, void* workspace, size_t workspace_bytes,
+                                     int32_t batch, int32_t T, int32_t nheads, int32_t head_dim,
+                                     int32_t ngroups, int32_t d_state, void* stream);
 
 #ifdef __cplusplus
 }

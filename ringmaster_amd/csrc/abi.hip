@@ -2,6 +2,7 @@
 // include/ringmaster_amd.h). Every argument is validated here, on the host,
 // before anything is launched; errors are reported as negative codes with a
 // per-thread message and nothing ever throws across the ABI.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -313,12 +314,65 @@ int32_t rmx_mamba2_cp_correction(const uint16_t* out, uint16_t* y, const float* 
   if (T == 0) return fail(RMX_EINVAL, "the shard has no tokens (T == 0)");
   if (!out || !y || !h_final || !h_final_out || !C || !cum_A || !h_prev)
     return fail(RMX_EINVAL, "NULL tensor pointer");
-  if (!aligned(C, 16) || !aligned(h_prev, 16) || !aligned(h_final, 16) || !aligned(h_final_out, 16))
-    return fail(RMX_EINVAL, "C, h_prev, h_final and h_final_out must be 16-byte aligned");
+  if (!aligned(C, 16) || !aligned(h_prev, 16) || !aligned(h_final, 16) || !aligned(h_final_out, 16) ||
+      !aligned(out, 16) || !aligned(y, 16))
+    return fail(RMX_EINVAL, "out, y, C, h_prev, h_final and h_final_out must be 16-byte aligned");
   return dev_status(rmx::launch_mamba2_correction(out, y, h_final, h_final_out, C, cum_A, h_prev,
                                                   seq_idx, batch, T, nheads, head_dim, ngroups,
                                                   d_state, (hipStream_t)stream),
                     "rmx_mamba2_cp_correction launch");
+}
+
+static int check_mamba_bwd(int32_t batch, int32_t T, int32_t nheads, int32_t head_dim,
+                           int32_t ngroups, int32_t d_state) {
+  if (batch < 0 || T < 0 || nheads < 0) return fail(RMX_EINVAL, "negative shape");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(RMX_EUNSUPPORTED, "the correction backward takes head_dim 64 or 128 (got %d)", head_dim);
+  if (d_state != 64 && d_state != 128)
+    return fail(RMX_EUNSUPPORTED, "the correction backward takes d_state 64 or 128 (got %d)", d_state);
+  if (ngroups <= 0 || nheads % ngroups)
+    return fail(RMX_EINVAL, "ngroups (%d) must divide nheads (%d)", ngroups, nheads);
+  const int heads_per_wg = head_dim == 64 ? 4 : 2;
+  if ((nheads / ngroups) % heads_per_wg)
+    return fail(RMX_EUNSUPPORTED,
+                "the correction backward needs nheads / ngroups divisible by %d at head_dim %d",
+                heads_per_wg, head_dim);
+  const int64_t row = std::max<int64_t>({(int64_t)nheads * head_dim * 2,
+                                         (int64_t)ngroups * d_state * 2, (int64_t)nheads * 4});
+  if (((int64_t)T + 256) * row >= ((int64_t)1 << 31))
+    return fail(RMX_EUNSUPPORTED, "a batch row of the shard exceeds 2 GiB");
+  return RMX_OK;
+}
+
+size_t rmx_mamba2_cp_correction_bwd_workspace(int32_t batch, int32_t T, int32_t nheads,
+                                              int32_t head_dim, int32_t ngroups, int32_t d_state) {
+  if (check_mamba_bwd(batch, T, nheads, head_dim, ngroups, d_state)) return 0;
+  return rmx::mamba2_bwd_workspace(batch, T, nheads, head_dim, d_state);
+}
+
+int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const uint16_t* C,
+                                     const float* cum_A, const float* h_prev,
+                                     const int32_t* seq_idx, uint16_t* gC, float* g_cumA,
+                                     float* g_hprev, void* workspace, size_t workspace_bytes,
+                                     int32_t batch, int32_t T, int32_t nheads, int32_t head_dim,
+                                     int32_t ngroups, int32_t d_state, void* stream) {
+  int rc = check_mamba_bwd(batch, T, nheads, head_dim, ngroups, d_state);
+  if (rc) return rc;
+  if ((int64_t)batch * nheads == 0) return RMX_OK;
+  if (T == 0) return fail(RMX_EINVAL, "the shard has no tokens (T == 0)");
+  if (!gy || !C || !cum_A || !h_prev || !gC || !g_cumA || !g_hprev || !workspace)
+    return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!aligned(gy, 16) || !aligned(C, 16) || !aligned(h_prev, 16) || !aligned(gC, 16) ||
+      !aligned(g_hprev, 16) || (ghf && !aligned(ghf, 16)))
+    return fail(RMX_EINVAL, "gy, C, h_prev, ghf, gC and g_hprev must be 16-byte aligned");
+  const size_t need = rmx::mamba2_bwd_workspace(batch, T, nheads, head_dim, d_state);
+  if (workspace_bytes < need)
+    return fail(RMX_EINVAL, "workspace of %zu bytes is below the %zu required", workspace_bytes, need);
+  return dev_status(rmx::launch_mamba2_correction_bwd(gy, ghf, C, cum_A, h_prev, seq_idx, gC, g_cumA,
+                                                      g_hprev, workspace, batch, T, nheads,
+                                                      head_dim, ngroups, d_state,
+                                                      (hipStream_t)stream),
+                    "rmx_mamba2_cp_correction_bwd launch");
 }
 
 }  // extern "C"

@@ -1,0 +1,595 @@
+// Mamba2 context-parallel output correction, backward, for gfx950.
+//
+// Reference: the autograd of `mamba2_cp_correction` (strategies/mamba.py:101-139),
+// plain torch ops there. With e[t,h] = mask[t] * exp(cumA[t,h]) (mask = seq_idx == 0),
+// S[t,h,d] = sum_n C[t,g(h),n] H_in[h,d,n] and the upstream gradients G = dL/dy
+// (bf16, [B,T,H*d]) and Gs = dL/dh_final_out (fp32, may be absent):
+//   dC[t,g,n]    = sum_{h in g} e[t,h] sum_d G[t,h,d] H_in[h,d,n]
+//   dcumA[t,h]   = e[t,h] sum_d G[t,h,d] S[t,h,d]
+//                  + [t = T-1, state updated] exp(cumA[T-1,h]) sum_{d,n} Gs H_in
+//   dH_in[h,d,n] = sum_t e[t,h] G[t,h,d] C[t,g(h),n]
+//                  + [state updated] exp(cumA[T-1,h]) Gs[h,d,n]
+// (dout = G and dh_final = Gs pass through; the state is updated unless a batch
+// row's last token starts a fresh sequence, :131). Four launches:
+//  1. prep: H_in^T split into bf16 hi + lo ([B,H,n,d]) and e transposed to [B,H,T];
+//  2. unit kernel: per head slice of 64 channels walking a token block, S on MFMA
+//     (H_in hi/lo from registers, as in the forward), dcumA, and the block's
+//     dH_in partial (G e split into bf16 hi + lo, times C) on MFMA;
+//  3. reduce: dH_in = sum of the block partials + the state term, and the state
+//     term of dcumA;
+//  4. dC kernel: per 256-token tile of one group, all heads' G H_in^T products
+//     on MFMA (H_in^T hi/lo staged per 64-channel chunk in LDS), scaled by e.
+// Every fp32 result is formed from exact bf16 x bf16 products with fp32
+// accumulation (the hi/lo splits carry ~16 mantissa bits of the fp32 factors).
+#include <type_traits>
+
+#include "rmx_kernels.h"
+
+namespace rmx {
+
+struct MambaBwdArgs {
+  const uint16_t* gy;
+  const float* ghf;  // may be null: no gradient reaches h_final_out
+  const uint16_t* C;
+  const float* cum_A;
+  const float* h_prev;
+  const int32_t* seq_idx;
+  uint16_t* gC;
+  float* g_cumA;
+  float* g_hprev;
+  float* part;      // [ntb][B][H][d][n] dH_in partials of the unit kernel's token blocks
+  uint16_t* ht_hi;  // [B][H][n][d]
+  uint16_t* ht_lo;
+  float* eT;        // [B][H][T]
+  int batch, T, nheads, head_dim, ngroups, d_state, ntb;
+};
+
+constexpr int kMambaBwdTokensPerWg = 4096;  // unit kernel token block
+constexpr int kMambaBwdCTokens = 256;       // dC kernel token tile (4 waves x 64)
+
+// Chunk swizzle for LDS tiles read both row-wise (8 consecutive rows, one
+// 16-byte chunk each) and by ds_read_b64_tr_b16 (4 consecutive rows, one
+// 32-byte chunk pair each): f(row) mod 8 differs over any 8 rows and f(row) / 2
+// differs over any 4 aligned rows, so both reads hit 8 distinct 16-byte bank
+// slots of a 128-byte window (rows of 128 or 256 bytes).
+__device__ __forceinline__ int swz_pair(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+
+// Transposed operand read (k = 8*hl .. 8*hl+7 <-> tile rows r0 + 8*hl + 0..7,
+// column c0 + l32) from a tile with 16-byte chunks swizzled by swz_pair and
+// RB-byte rows. Lane (x = (lane >> 4) & 1, m = lane & 15) addresses row
+// r0 + 8*hl + 4*t + (m >> 2), columns c0 + 16x + 4(m & 3) .. + 3.
+template <int RB>
+__device__ __forceinline__ bf16x8 tr_read(const uint8_t* tile, int r0, int c0, int lane) {
+  const int hl = lane >> 5, m = lane & 15, x = (lane >> 4) & 1;
+  u32x2 part[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int r = r0 + 8 * hl + 4 * t + (m >> 2);
+    const int col = c0 + 16 * x + 4 * (m & 3);  // element column, 8-byte aligned
+    const int chunk = col >> 3;
+    const uint8_t* p = tile + r * RB + 16 * (chunk ^ swz_pair(r)) + 2 * (col & 7);
+    part[t] = lds_read_tr(reinterpret_cast<const uint16_t*>(p));
+  }
+  return join_bf16x8(part[0], part[1]);
+}
+
+__device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
+  u32x4 h, l;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = cvt_pk_bf16(v[2 * i], v[2 * i + 1]);
+    l[i] = cvt_pk_bf16(v[2 * i] - __uint_as_float(h[i] << 16),
+                       v[2 * i + 1] - __uint_as_float(h[i] & 0xffff0000u));
+  }
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
+}
+
+// ---------------------------------------------------------------------------
+// 1. prep: grid (H, B), 256 threads. H_in[b,h] ([d][n] fp32) -> [n][d] bf16 hi/lo
+// through LDS, and eT[b,h,:] = mask * exp(cumA[b,:,h]).
+template <int HD, int N>
+__global__ __launch_bounds__(256) void mamba2_bwd_prep_kernel(const MambaBwdArgs a) {
+  __shared__ float st[HD][N + 1];
+  const int h = blockIdx.x, bb = blockIdx.y, tid = threadIdx.x;
+  const int H = a.nheads, T = a.T;
+  const int64_t hb = ((int64_t)bb * H + h) * HD * N;
+  for (int i = tid; i < HD * N; i += 256) st[i / N][i % N] = a.h_prev[hb + i];
+  __syncthreads();
+  // thread -> (n, 8 consecutive d): 16-byte hi and lo stores
+  for (int i = tid; i < N * (HD / 8); i += 256) {
+    const int n = i / (HD / 8), d0 = 8 * (i % (HD / 8));
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = st[d0 + k][n];
+    bf16x8 hi, lo;
+    split8(v, hi, lo);
+    *reinterpret_cast<bf16x8*>(a.ht_hi + hb + (int64_t)n * HD + d0) = hi;
+    *reinterpret_cast<bf16x8*>(a.ht_lo + hb + (int64_t)n * HD + d0) = lo;
+  }
+  float* et = a.eT + ((int64_t)bb * H + h) * T;
+  for (int t = tid; t < T; t += 256) {
+    const int64_t tok = (int64_t)bb * T + t;
+    const bool live = !a.seq_idx || a.seq_idx[tok] == 0;
+    et[t] = live ? expf(a.cum_A[tok * H + h]) : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. unit kernel. A unit is 64 channels of one head (head_dim 64: one head,
+// 128: half a head); a workgroup holds 4 units of heads in one C group and
+// walks kMambaBwdTokensPerWg tokens, 32 per step, with the forward's DMA rings
+// (C and aux shared, G per wave, two steps ahead). Per wave and step:
+//   S^T (64 ch x 32 tok) = H_in C^T        48 MFMAs: H_in = hi + mid + lo, three
+//       bf16 parts (residual ~2^-27: dcumA contracts S against G once more, so the
+//       forward's two-part split would leave ~2^-18 x a cancellation factor);
+//       hi and mid in registers, lo re-read from this wave's LDS every step
+//   dcumA[t] = e[t] sum_d G[t,d] S[t,d]    (lane = token; one cross-half add)
+//   dH^T partial (64 ch x N) += (G e)^T C  4 N/32 MFMAs per 16 tokens: A = G^T e
+//       split into hi/lo (transposed reads of the G stage), B = C (transposed
+//       reads of the C stage)
+// The dH partial (128 fp32 per lane at N = 128) stays in registers for the
+// whole walk: one wave per SIMD, accumulators in AGPRs.
+template <int N>
+struct MambaBwdUnitCfg {
+  static constexpr int SL = 64, NDB = 2, NS = N / 16, CHC = N / 8, CHO = 8, NI = 4, NB = N / 32;
+  static constexpr int ND = N / 64;            // C DMA instructions per wave and step
+  static constexpr int CS = 32 * N * 2;        // C stage bytes (= ND * 4 KB)
+  static constexpr int OS = 32 * SL * 2;       // G stage bytes per wave
+  static constexpr int XS = 2 * 4 * 256;       // cum_A + seq_idx stage
+  static constexpr int NDMA = ND + NI + 2;
+  static constexpr int EW = 4 * 32 * 4;        // e of the step's tokens, per wave
+  static constexpr int RING = 3 * CS + 4 * 3 * OS + 3 * XS + EW;
+  static constexpr int HSCR = 4 * 32 * N * 4;  // H_in transpose scratch
+  static constexpr int H3 = 64 * N * 2;        // third bf16 part of H_in, per wave
+  static constexpr int LDS = (RING > HSCR ? RING : HSCR) + 4 * H3;
+};
+
+template <int N>
+__global__ __launch_bounds__(256, 1) void mamba2_bwd_unit_kernel(const MambaBwdArgs a, const int nug) {
+  using F = MambaBwdUnitCfg<N>;
+  constexpr int SL = F::SL, NDB = F::NDB, NS = F::NS, CHC = F::CHC, CHO = F::CHO, NI = F::NI;
+  constexpr int NB = F::NB, ND = F::ND, CS = F::CS, OS = F::OS, XS = F::XS;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F::LDS];
+  uint8_t* const sC = smem;
+  uint8_t* const sO = smem + 3 * CS;
+  uint8_t* const sX = sO + 4 * 3 * OS;
+  float* const sE = reinterpret_cast<float*>(sX + 3 * XS);  // [4 waves][32]
+  constexpr int RS = F::RING > F::HSCR ? F::RING : F::HSCR;
+  // third part of H_in: [64 rows][N] bf16 per wave, 16-byte chunks swizzled by swz_row
+  uint16_t* const sH3 = reinterpret_cast<uint16_t*>(smem + RS);
+
+  const int ntb = a.ntb;
+  int id = blockIdx.x;
+  const int nwg = gridDim.x;
+  if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
+  const int ug = id % nug, rest = id / nug;
+  const int tb = rest % ntb, bb = rest / ntb;
+  const int T = a.T, H = a.nheads, HD = a.head_dim, G = a.ngroups;
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int uph = HD / SL, hpw = 4 / uph, h0 = 4 * ug / uph;
+  const int unit = 4 * ug + wave, h = unit / uph, sl = unit % uph, hw = wave / uph;
+  const int g = h0 / (H / G);
+  const int tbeg = tb * kMambaBwdTokensPerWg;
+  const int tend = tbeg + kMambaBwdTokensPerWg < T ? tbeg + kMambaBwdTokensPerWg : T;
+  const int nstep = (tend - tbeg + 31) / 32;
+  const int64_t HHD = (int64_t)H * HD;
+  const int64_t hbase = (((int64_t)bb * H + h) * HD + (int64_t)sl * SL) * N;
+
+  // ---- H_in -> registers (hi, mid; coalesced loads, LDS transpose as in the
+  // forward) and this wave's LDS (lo)
+  bf16x8 ahi[NDB][NS], alo[NDB][NS];
+  uint16_t* const h3w = sH3 + wave * (64 * N);
+  {
+    uint16_t* const shi = reinterpret_cast<uint16_t*>(smem + wave * (32 * N * 4));
+    uint16_t* const slo = shi + 32 * N;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int64_t blk = hbase + (int64_t)32 * db * N;
+      f32x4 xs[N / 8];
+#pragma unroll
+      for (int q = 0; q < N / 8; ++q)
+        xs[q] = *reinterpret_cast<const f32x4*>(a.h_prev + blk + 4 * (64 * q + lane));
+#pragma unroll
+      for (int q = 0; q < N / 8; ++q) {
+        const int p = 64 * q + lane, row = p / (N / 4), n0 = 4 * (p % (N / 4));
+        u32x2 hi, lo, l3;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const float x0 = xs[q][2 * i], x1 = xs[q][2 * i + 1];
+          hi[i] = cvt_pk_bf16(x0, x1);
+          const float r0 = x0 - __uint_as_float(hi[i] << 16), r1 = x1 - __uint_as_float(hi[i] & 0xffff0000u);
+          lo[i] = cvt_pk_bf16(r0, r1);
+          l3[i] = cvt_pk_bf16(r0 - __uint_as_float(lo[i] << 16), r1 - __uint_as_float(lo[i] & 0xffff0000u));
+        }
+        const int off = row * N + 8 * ((n0 >> 3) ^ (swz_row(row) & (CHC - 1))) + (n0 & 4);
+        *reinterpret_cast<u32x2*>(shi + off) = hi;
+        *reinterpret_cast<u32x2*>(slo + off) = lo;
+        *reinterpret_cast<u32x2*>(h3w + 32 * db * N + off) = l3;
+      }
+      const int arow = sigma(l32);
+#pragma unroll
+      for (int ks = 0; ks < NS; ++ks) {
+        const int off = arow * N + 8 * ((2 * ks + hl) ^ (swz_row(arow) & (CHC - 1)));
+        ahi[db][ks] = *reinterpret_cast<const bf16x8*>(shi + off);
+        alo[db][ks] = *reinterpret_cast<const bf16x8*>(slo + off);
+      }
+    }
+  }
+  lds_barrier();
+
+  const int cstride = G * N * 2, ostride = (int)(HHD * 2);
+  const uint32_t cspan = span_bytes(T, cstride, N * 2), aspan = (uint32_t)T * (uint32_t)H * 4u;
+  const i32x4 rC = make_rsrc(a.C + ((int64_t)bb * T * G + g) * N, cspan);
+  const i32x4 rO = make_rsrc(a.gy + (int64_t)bb * T * HHD + (int64_t)h * HD + sl * SL,
+                             span_bytes(T, ostride, SL * 2));
+  const i32x4 rA = make_rsrc(a.cum_A + (int64_t)bb * T * H, aspan);
+  const uint32_t sspan = a.seq_idx ? (uint32_t)T * 4u : 0u;
+  const i32x4 rS = make_rsrc(a.seq_idx ? (const void*)(a.seq_idx + (int64_t)bb * T) : (const void*)a.cum_A,
+                             sspan);
+  const uint32_t ldsC = lds_addr(sC), ldsO = lds_addr(sO + wave * 3 * OS), ldsX = lds_addr(sX);
+  const int xa_tok = 8 * wave + lane / hpw, xa_head = h0 + lane % hpw;
+  const bool xa_live = lane < 8 * hpw;
+
+  auto issue = [&](int st, int t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const int p = (i * 4 + wave) * 64 + lane, row = p / CHC, pc = p % CHC;
+      dma16_async(rC, ldsC + st * CS + (i * 4 + wave) * 1024,
+                  (t0 + row) * cstride + 16 * (pc ^ swz_pair(row)));
+    }
+#pragma unroll
+    for (int k = 0; k < NI; ++k) {
+      const int p = 64 * k + lane, row = p / CHO, pc = p % CHO;
+      dma16_async(rO, ldsO + st * OS + 1024 * k, (t0 + row) * ostride + 16 * (pc ^ swz_pair(row)));
+    }
+    dma4_async(rA, ldsX + st * XS + 256 * wave,
+               xa_live ? (t0 + xa_tok) * (H * 4) + 4 * xa_head : (int)aspan);
+    dma4_async(rS, ldsX + st * XS + 1024 + 256 * wave, lane < 8 ? (t0 + 8 * wave + lane) * 4 : (int)sspan);
+  };
+
+  f32x16 gh[NDB][NB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) gh[db][nb] = zero16();
+
+  issue(0, tbeg);
+  if (nstep > 1) issue(1, tbeg + 32);
+  // vmcnt budget at the top of step s: what was issued after step s's DMA (the
+  // dcumA stores of steps s-2 and s-1, one per wave and step, and step s+1's DMA)
+  constexpr int K0 = F::NDMA, K1 = F::NDMA + 1, KS = F::NDMA + 2;
+  float* const gca_row = a.g_cumA + (int64_t)bb * T * H + h;
+  float* const ew = sE + 32 * wave;
+  for (int s = 0; s < nstep; ++s) {
+    if (s >= 2 && s + 1 < nstep)
+      wait_vm_barrier<KS>();
+    else if (s == 1 && nstep > 2)
+      wait_vm_barrier<K1>();
+    else if (s == 0 && nstep > 1)
+      wait_vm_barrier<K0>();
+    else
+      wait_vm_barrier<0>();
+    if (s + 2 < nstep) issue((s + 2) % 3, tbeg + 32 * (s + 2));
+    const int st = s % 3, t0 = tbeg + 32 * s;
+    const uint8_t* cst = sC + st * CS;
+    const uint8_t* ost = sO + (wave * 3 + st) * OS;
+
+    // S^T = H_in C^T
+    f32x16 acc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[db] = zero16();
+    const int arow = sigma(l32);
+#pragma unroll
+    for (int ks = 0; ks < NS; ++ks) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(cst + l32 * (CHC * 16) +
+                                                        16 * ((2 * ks + hl) ^ swz_pair(l32)));
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) acc[db] = mfma32(ahi[db][ks], b, acc[db]);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) acc[db] = mfma32(alo[db][ks], b, acc[db]);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(
+            h3w + (32 * db + arow) * N + 8 * ((2 * ks + hl) ^ (swz_row(arow) & (CHC - 1))));
+        acc[db] = mfma32(a3, b, acc[db]);
+      }
+    }
+    // e of token l32 (0 past the block end: those rows belong to the next block)
+    const uint8_t* xst = sX + st * XS;
+    const float ca = reinterpret_cast<const float*>(xst)[64 * (l32 >> 3) + (l32 & 7) * hpw + hw];
+    const int sq = reinterpret_cast<const int32_t*>(xst + 1024)[64 * (l32 >> 3) + (l32 & 7)];
+    const bool live = t0 + l32 < tend;
+    const float e = (sq != 0 || !live) ? 0.f : expf(ca);
+    if (hl == 0) ew[l32] = e;
+
+    // dcumA: lane (hl, l32) reg r of block db = channel 32 db + 16 (r / 8) + 8 hl + r % 8
+    float dot = 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int c = 4 * db + 2 * half + hl;
+        const u32x4 gv = *reinterpret_cast<const u32x4*>(ost + 16 * (l32 * CHO + (c ^ swz_pair(l32))));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dot += __uint_as_float(gv[i] << 16) * acc[db][8 * half + 2 * i];
+          dot += __uint_as_float(gv[i] & 0xffff0000u) * acc[db][8 * half + 2 * i + 1];
+        }
+      }
+    dot += xhalf(dot);
+    if (hl == 0 && live) {
+      float* dst = gca_row + (int64_t)(t0 + l32) * H;
+      if (uph == 1)
+        *dst = e * dot;
+      else
+        unsafeAtomicAdd(dst, e * dot);  // hardware fp32 add; two addends per element: order-free
+    }
+
+    // dH^T += (G e)^T C over the step's 32 tokens (two k-steps of 16)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const f32x4 e0 = *reinterpret_cast<const f32x4*>(ew + 16 * kk + 8 * hl);
+      const f32x4 e1 = *reinterpret_cast<const f32x4*>(ew + 16 * kk + 8 * hl + 4);
+      const float e8[8] = {e0[0], e0[1], e0[2], e0[3], e1[0], e1[1], e1[2], e1[3]};
+      bf16x8 gah[NDB], gal[NDB];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const u32x4 gt = __builtin_bit_cast(u32x4, tr_read<CHO * 16>(ost, 16 * kk, 32 * db, lane));
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = __uint_as_float(gt[i] << 16) * e8[2 * i];
+          v[2 * i + 1] = __uint_as_float(gt[i] & 0xffff0000u) * e8[2 * i + 1];
+        }
+        split8(v, gah[db], gal[db]);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const bf16x8 cb = tr_read<CHC * 16>(cst, 16 * kk, 32 * nb, lane);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          gh[db][nb] = mfma32(gah[db], cb, gh[db][nb]);
+          gh[db][nb] = mfma32(gal[db], cb, gh[db][nb]);
+        }
+      }
+    }
+  }
+
+  // ---- the block's dH_in partial: lane (hl, l32) reg r of (db, nb) holds
+  // channel 32 db + 8 (r / 4) + 4 hl + r % 4 (A rows unpermuted), state n = 32 nb + l32
+  float* dst = a.part + ((((int64_t)tb * a.batch + bb) * H + h) * HD + (int64_t)sl * SL) * N;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        dst[(int64_t)(32 * db + c_row(hl, r)) * N + 32 * nb + l32] = gh[db][nb][r];
+}
+
+// ---------------------------------------------------------------------------
+// 3. reduce: grid (H, B), 256 threads. dH_in = sum of the block partials
+// (+ exp(cumA[T-1]) Gs when the state is updated), and the state's term of
+// dcumA[T-1] = exp(cumA[T-1]) sum Gs H_in (added after the unit kernel).
+template <int HD, int N>
+__global__ __launch_bounds__(256) void mamba2_bwd_reduce_kernel(const MambaBwdArgs a) {
+  __shared__ float red[4];
+  const int h = blockIdx.x, bb = blockIdx.y, tid = threadIdx.x;
+  const int H = a.nheads, T = a.T;
+  bool fresh_last = false;
+  if (a.seq_idx)
+    for (int b2 = 0; b2 < a.batch; ++b2) fresh_last |= a.seq_idx[(int64_t)b2 * T + T - 1] != 0;
+  const bool upd = a.ghf && !fresh_last;
+  const float el = upd ? expf(a.cum_A[((int64_t)bb * T + T - 1) * H + h]) : 0.f;
+  const int64_t hb = ((int64_t)bb * H + h) * HD * N;
+  const int64_t pstride = (int64_t)a.batch * H * HD * N;
+  float dot = 0.f;
+  for (int i = 4 * tid; i < HD * N; i += 4 * 256) {
+    f32x4 s = *reinterpret_cast<const f32x4*>(a.part + hb + i);
+    for (int k = 1; k < a.ntb; ++k) s += *reinterpret_cast<const f32x4*>(a.part + k * pstride + hb + i);
+    if (upd) {
+      const f32x4 gs = *reinterpret_cast<const f32x4*>(a.ghf + hb + i);
+      const f32x4 hp = *reinterpret_cast<const f32x4*>(a.h_prev + hb + i);
+      s += el * gs;
+      dot += gs[0] * hp[0] + gs[1] * hp[1] + gs[2] * hp[2] + gs[3] * hp[3];
+    }
+    *reinterpret_cast<f32x4*>(a.g_hprev + hb + i) = s;
+  }
+  if (upd) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = dot;
+    __syncthreads();
+    if (tid == 0) a.g_cumA[((int64_t)bb * T + T - 1) * H + h] += el * (red[0] + red[1] + red[2] + red[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. dC kernel: one workgroup = 4 waves x 64 tokens of one (batch, group); the
+// contraction runs over the group's (head, channel) pairs in chunks of 64
+// channels (one head at head_dim 64, half a head at 128). Per chunk and wave:
+//   P^T (N x 64 tok) = H_in^T G^T   A = H_in^T rows (hi and lo, LDS, sigma-
+//                                    permuted), B = G rows (LDS)   4 N/32 MFMAs
+//   dC^T += e P^T                   (lane = token: one e per lane and chunk)
+// The next chunk's H_in^T (shared) and G (per wave) tiles load by DMA during
+// the current one; e comes from the transposed eT rows.
+template <int N>
+struct MambaBwdCCfg {
+  static constexpr int NB = N / 32, CH = 8;    // 64 channels = 8 chunks per row
+  static constexpr int HS = 2 * N * 128;       // H_in^T chunk stage: hi + lo, N rows x 128 B
+  static constexpr int GS = 64 * 128;          // G chunk stage per wave: 64 tokens x 128 B
+  static constexpr int ES = 4 * 256;           // e of the 256 tokens
+  static constexpr int NDH = HS / 4096;        // H DMA instructions per wave (4 waves x 1 KB)
+  static constexpr int NDMA = NDH + 8 + 1;     // + G (8 KB per wave) + e
+  static constexpr int LDS = 2 * HS + 4 * 2 * GS + 2 * ES;
+};
+
+template <int N>
+__global__ __launch_bounds__(256, 1) void mamba2_bwd_c_kernel(const MambaBwdArgs a, const int ntt) {
+  using F = MambaBwdCCfg<N>;
+  constexpr int NB = F::NB, CH = F::CH, HS = F::HS, GS = F::GS, ES = F::ES, NDH = F::NDH;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F::LDS];
+  uint8_t* const sH = smem;                 // [2][HS]: hi [N][64] then lo [N][64]
+  uint8_t* const sG = smem + 2 * HS;        // [4 waves][2][GS]
+  uint8_t* const sEt = sG + 4 * 2 * GS;     // [2][ES]
+
+  int id = blockIdx.x;
+  const int nwg = gridDim.x;
+  if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
+  const int tt = id % ntt, rest = id / ntt;
+  const int g = rest % a.ngroups, bb = rest / a.ngroups;
+  const int T = a.T, H = a.nheads, HD = a.head_dim;
+  const int hpg = H / a.ngroups, cph = HD / 64, nchunk = hpg * cph;
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t0 = tt * kMambaBwdCTokens;
+  const int64_t HHD = (int64_t)H * HD;
+  const int ostride = (int)(HHD * 2);
+
+  const i32x4 rG = make_rsrc(a.gy + (int64_t)bb * T * HHD, span_bytes(T, ostride, (int)(HHD * 2)));
+  const uint32_t ldsH = lds_addr(sH), ldsG = lds_addr(sG + wave * 2 * GS), ldsE = lds_addr(sEt);
+  // chunk j: head hg = g * hpg + j / cph, channels 64 (j % cph) .. + 63
+  auto issue = [&](int st, int j) __attribute__((always_inline)) {
+    const int hg = g * hpg + j / cph, c0 = 64 * (j % cph);
+    const uint16_t* hhi = a.ht_hi + ((int64_t)bb * H + hg) * N * HD + c0;
+    const uint16_t* hlo = a.ht_lo + ((int64_t)bb * H + hg) * N * HD + c0;
+    const i32x4 rh = make_rsrc(hhi, span_bytes(N, HD * 2, 128));
+    const i32x4 rl = make_rsrc(hlo, span_bytes(N, HD * 2, 128));
+#pragma unroll
+    for (int i = 0; i < NDH; ++i) {
+      const int p = (i * 4 + wave) * 64 + lane;      // 16-byte slot of the stage
+      const bool lo = (i * 4 + wave) * 64 >= N * CH;  // second half of the stage: lo plane
+      const int q = lo ? p - N * CH : p, row = q / CH, pc = q % CH;
+      const int off = row * (HD * 2) + 16 * (pc ^ swz_row(row));
+      // one resource per instruction: the planes split at an instruction boundary
+      dma16_async(lo ? rl : rh, ldsH + st * HS + (i * 4 + wave) * 1024, off);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int p = 64 * k + lane, row = p / CH, pc = p % CH;
+      dma16_async(rG, ldsG + st * GS + 1024 * k,
+                  (t0 + 64 * wave + row) * ostride + 2 * (hg * HD + c0) + 16 * (pc ^ (row & 7)));
+    }
+    const i32x4 re = make_rsrc(a.eT + ((int64_t)bb * H + hg) * T, (uint32_t)T * 4u);
+    dma4_async(re, ldsE + st * ES + 256 * wave, (t0 + 64 * wave + lane) * 4);
+  };
+
+  f32x16 acc[2][NB];  // dC^T: [token block][n block]
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[cb][nb] = zero16();
+
+  issue(0, 0);
+  const int arow = sigma(l32);
+  for (int j = 0; j < nchunk; ++j) {
+    wait_vm_barrier<0>();
+    if (j + 1 < nchunk) issue((j + 1) & 1, j + 1);
+    const uint8_t* hst = sH + (j & 1) * HS;
+    const uint8_t* gst = sG + (wave * 2 + (j & 1)) * GS;
+    const float* est = reinterpret_cast<const float*>(sEt + (j & 1) * ES) + 64 * wave;
+    f32x16 p[2][NB];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) p[cb][nb] = zero16();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8 gb[2];
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        const int row = 32 * cb + l32;
+        gb[cb] = *reinterpret_cast<const bf16x8*>(gst + row * 128 + 16 * ((2 * ks + hl) ^ (row & 7)));
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int row = 32 * nb + arow;
+        const int off = row * 128 + 16 * ((2 * ks + hl) ^ swz_row(row));
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(hst + off);
+        const bf16x8 al = *reinterpret_cast<const bf16x8*>(hst + N * 128 + off);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          p[cb][nb] = mfma32(ah, gb[cb], p[cb][nb]);
+          p[cb][nb] = mfma32(al, gb[cb], p[cb][nb]);
+        }
+      }
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const float e = est[32 * cb + l32];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[cb][nb] += e * p[cb][nb];
+    }
+  }
+
+  // dC[b, t, g, n]: lane (hl, l32) reg r of (cb, nb) = token 64 wave + 32 cb + l32,
+  // n = 32 nb + 16 (r / 8) + 8 hl + r % 8 (sigma-permuted A rows)
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int t = t0 + 64 * wave + 32 * cb + l32;
+    if (t >= T) continue;
+    uint16_t* dst = a.gC + (((int64_t)bb * T + t) * a.ngroups + g) * N + 8 * hl;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = acc[cb][nb][8 * half + i];
+        *reinterpret_cast<bf16x8*>(dst + 32 * nb + 16 * half) = pack8_hw(v);
+      }
+  }
+}
+
+__global__ void mamba2_bwd_zero_kernel(float* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0.f;
+}
+
+// ---------------------------------------------------------------------------
+size_t mamba2_bwd_workspace(int batch, int T, int nheads, int head_dim, int d_state) {
+  const size_t state = (size_t)batch * nheads * head_dim * d_state;
+  const size_t ntb = (size_t)((T + kMambaBwdTokensPerWg - 1) / kMambaBwdTokensPerWg);
+  return ntb * state * 4 + 2 * state * 2 + (size_t)batch * nheads * T * 4 + 256;
+}
+
+hipError_t launch_mamba2_correction_bwd(const uint16_t* gy, const float* ghf, const uint16_t* C,
+                                        const float* cum_A, const float* h_prev,
+                                        const int32_t* seq_idx, uint16_t* gC, float* g_cumA,
+                                        float* g_hprev, void* workspace, int batch, int T,
+                                        int nheads, int head_dim, int ngroups, int d_state,
+                                        hipStream_t stream) {
+  const size_t state = (size_t)batch * nheads * head_dim * d_state;
+  const int ntb = (T + kMambaBwdTokensPerWg - 1) / kMambaBwdTokensPerWg;
+  uint8_t* ws = reinterpret_cast<uint8_t*>(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  MambaBwdArgs a{gy, ghf, C, cum_A, h_prev, seq_idx, gC, g_cumA, g_hprev,
+                 reinterpret_cast<float*>(ws),
+                 reinterpret_cast<uint16_t*>(ws + ntb * state * 4),
+                 reinterpret_cast<uint16_t*>(ws + ntb * state * 4 + state * 2),
+                 reinterpret_cast<float*>(ws + ntb * state * 4 + state * 4),
+                 batch, T, nheads, head_dim, ngroups, d_state, ntb};
+  const int uph = head_dim / 64, nug = nheads * uph / 4;
+  const int ntt = (T + kMambaBwdCTokens - 1) / kMambaBwdCTokens;
+  auto run = [&](auto hd, auto n) {
+    constexpr int HDc = decltype(hd)::value, Nc = decltype(n)::value;
+    hipLaunchKernelGGL((mamba2_bwd_prep_kernel<HDc, Nc>), dim3(nheads, batch), dim3(256), 0, stream, a);
+    if (uph == 2)  // two units per head add into dcumA (a fill kernel, not a memset node)
+      hipLaunchKernelGGL(mamba2_bwd_zero_kernel, dim3(1024), dim3(256), 0, stream, g_cumA,
+                         (int64_t)batch * T * nheads);
+    hipLaunchKernelGGL((mamba2_bwd_unit_kernel<Nc>), dim3((unsigned)(nug * ntb * batch)), dim3(256), 0,
+                       stream, a, nug);
+    hipLaunchKernelGGL((mamba2_bwd_reduce_kernel<HDc, Nc>), dim3(nheads, batch), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((mamba2_bwd_c_kernel<Nc>), dim3((unsigned)(ntt * ngroups * batch)), dim3(256), 0,
+                       stream, a, ntt);
+    return hipGetLastError();
+  };
+  if (head_dim == 64)
+    return d_state == 64 ? run(std::integral_constant<int, 64>{}, std::integral_constant<int, 64>{})
+                         : run(std::integral_constant<int, 64>{}, std::integral_constant<int, 128>{});
+  return d_state == 64 ? run(std::integral_constant<int, 128>{}, std::integral_constant<int, 64>{})
+                       : run(std::integral_constant<int, 128>{}, std::integral_constant<int, 128>{});
+}
+
+}  // namespace rmx

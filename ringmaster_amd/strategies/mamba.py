@@ -52,21 +52,8 @@ def cp_state_prefix(ssm_states: torch.Tensor, chunk_decays: torch.Tensor, *,
     return h_prev
 
 
-def mamba2_cp_correction(out: torch.Tensor, h_final: torch.Tensor, C: torch.Tensor,
-                         cum_A: torch.Tensor, h_prev: torch.Tensor, num_heads: int,
-                         head_dim: int, seq_idx: torch.Tensor | None = None):
-    """Add the carried-in state's contribution to a shard's SSM output and final state.
-
-    Same arguments and result as the reference (strategies/mamba.py:101-139):
-    ``out`` bf16 ``[B, T, H*head_dim]``, ``h_final`` fp32 ``[B, H, head_dim, d_state]``,
-    ``C`` bf16 ``[B, T, ngroups, d_state]``, ``cum_A`` fp32 ``[B, T, H]``, ``h_prev``
-    fp32 like ``h_final``, ``seq_idx`` optional int ``[B, T]``. Returns
-    ``(corrected_out, corrected_h_final)`` as new tensors. Emulated ranks can be
-    stacked on the batch axis (each batch row carries its own ``h_prev``). Forward
-    only: the autograd of the correction is not implemented here."""
+def _validate_correction(out, h_final, C, cum_A, h_prev, num_heads, head_dim, seq_idx):
     abi.require_device(out, h_final, C, cum_A, h_prev)
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (out, h_final, C, cum_A, h_prev)):
-        raise NotImplementedError("the MI355X Mamba2 correction is forward-only")
     if out.dtype != torch.bfloat16 or C.dtype != torch.bfloat16:
         raise NotImplementedError("the MI355X Mamba2 correction takes bf16 out and C")
     if h_final.dtype != torch.float32 or h_prev.dtype != torch.float32 or \
@@ -82,18 +69,90 @@ def mamba2_cp_correction(out: torch.Tensor, h_final: torch.Tensor, C: torch.Tens
         raise ValueError("shapes of out/C/cum_A/h_prev/h_final do not agree")
     if num_heads % G:
         raise ValueError(f"ngroups {G} must divide num_heads {num_heads}")
-    sid = None
-    if seq_idx is not None:
-        if seq_idx.shape != (Bsz, T):
-            raise ValueError("seq_idx must be [B, T]")
-        abi.require_device(seq_idx)
-        sid = seq_idx.to(torch.int32).contiguous()
-    out_c, C_c, cum_c = out.contiguous(), C.contiguous(), cum_A.contiguous()
-    hp_c, hf_c = h_prev.contiguous(), h_final.contiguous()
-    y = torch.empty_like(out_c)
-    hf_out = torch.empty_like(hf_c)
-    abi.check(abi.lib().rmx_mamba2_cp_correction(
-        out_c.data_ptr(), y.data_ptr(), hf_c.data_ptr(), hf_out.data_ptr(), C_c.data_ptr(),
-        cum_c.data_ptr(), hp_c.data_ptr(), abi.ptr(sid), Bsz, T, num_heads, head_dim, G, n,
-        abi.stream_of(out)))
-    return y, hf_out
+    if seq_idx is None:
+        return None
+    if seq_idx.shape != (Bsz, T):
+        raise ValueError("seq_idx must be [B, T]")
+    abi.require_device(seq_idx)
+    return seq_idx.to(torch.int32).contiguous()
+
+
+def _bwd_workspace_bytes(Bsz, T, H, d, G, n) -> int:
+    nbytes = abi.lib().rmx_mamba2_cp_correction_bwd_workspace(Bsz, T, H, d, G, n)
+    if nbytes == 0:
+        raise NotImplementedError(
+            "the MI355X Mamba2 correction backward does not take this shape: "
+            + (abi.lib().rmx_last_error() or b"").decode(errors="replace"))
+    return nbytes
+
+
+class _Correction(torch.autograd.Function):
+    """y = out + bf16(e C.H_in), h_final_out = h_final + e_last H_in, with the gradients
+    autograd takes through the reference's torch ops (strategies/mamba.py:116-137):
+    dout = dy and dh_final = dh_final_out unchanged; dC, dcumA and dh_prev from the
+    backward kernels."""
+
+    @staticmethod
+    def forward(ctx, out, h_final, C, cum_A, h_prev, num_heads, head_dim, sid):
+        Bsz, T, _ = out.shape
+        G, n = C.shape[2], C.shape[3]
+        out_c, C_c, cum_c = out.contiguous(), C.contiguous(), cum_A.contiguous()
+        hp_c, hf_c = h_prev.contiguous(), h_final.contiguous()
+        y = torch.empty_like(out_c)
+        hf_out = torch.empty_like(hf_c)
+        abi.check(abi.lib().rmx_mamba2_cp_correction(
+            out_c.data_ptr(), y.data_ptr(), hf_c.data_ptr(), hf_out.data_ptr(), C_c.data_ptr(),
+            cum_c.data_ptr(), hp_c.data_ptr(), abi.ptr(sid), Bsz, T, num_heads, head_dim, G, n,
+            abi.stream_of(out)))
+        ctx.save_for_backward(C_c, cum_c, hp_c, sid)
+        ctx.meta = (num_heads, head_dim)
+        return y, hf_out
+
+    @staticmethod
+    def backward(ctx, gy, ghf):
+        C, cum_A, h_prev, sid = ctx.saved_tensors
+        num_heads, head_dim = ctx.meta
+        need = ctx.needs_input_grad
+        gC = g_cumA = g_hprev = None
+        if need[2] or need[3] or need[4]:
+            Bsz, T = C.shape[:2]
+            G, n = C.shape[2], C.shape[3]
+            if gy is None:
+                gy = torch.zeros((Bsz, T, num_heads * head_dim), dtype=torch.bfloat16,
+                                 device=C.device)
+            gy_c = gy.to(torch.bfloat16).contiguous()
+            ghf_c = None if ghf is None else ghf.to(torch.float32).contiguous()
+            nbytes = _bwd_workspace_bytes(Bsz, T, num_heads, head_dim, G, n)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=C.device)
+            gC = torch.empty_like(C)
+            g_cumA = torch.empty_like(cum_A)
+            g_hprev = torch.empty_like(h_prev)
+            abi.check(abi.lib().rmx_mamba2_cp_correction_bwd(
+                gy_c.data_ptr(), abi.ptr(ghf_c), C.data_ptr(), cum_A.data_ptr(), h_prev.data_ptr(),
+                abi.ptr(sid), gC.data_ptr(), g_cumA.data_ptr(), g_hprev.data_ptr(), ws.data_ptr(),
+                nbytes, Bsz, T, num_heads, head_dim, G, n, abi.stream_of(C)))
+        return gy, ghf, gC, g_cumA, g_hprev, None, None, None
+
+
+def mamba2_cp_correction(out: torch.Tensor, h_final: torch.Tensor, C: torch.Tensor,
+                         cum_A: torch.Tensor, h_prev: torch.Tensor, num_heads: int,
+                         head_dim: int, seq_idx: torch.Tensor | None = None):
+    """Add the carried-in state's contribution to a shard's SSM output and final state.
+
+    Same arguments, result and autograd as the reference (strategies/mamba.py:101-139):
+    ``out`` bf16 ``[B, T, H*head_dim]``, ``h_final`` fp32 ``[B, H, head_dim, d_state]``,
+    ``C`` bf16 ``[B, T, ngroups, d_state]``, ``cum_A`` fp32 ``[B, T, H]``, ``h_prev``
+    fp32 like ``h_final``, ``seq_idx`` optional int ``[B, T]``. Returns
+    ``(corrected_out, corrected_h_final)``; like the reference, an all-zero ``h_prev``
+    returns ``(out, h_final)`` themselves (no graph to ``C``, ``cum_A``, ``h_prev``).
+    Emulated ranks can be stacked on the batch axis (each batch row carries its own
+    ``h_prev``). The backward takes head_dim 64 or 128 and d_state 64 or 128 (the
+    forward any of the kernel's shapes); a graph that needs an unsupported backward
+    fails here, at the forward, with NotImplementedError."""
+    sid = _validate_correction(out, h_final, C, cum_A, h_prev, num_heads, head_dim, seq_idx)
+    if not h_prev.any():
+        return out, h_final
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (out, h_final, C, cum_A, h_prev)):
+        Bsz, T, _ = out.shape
+        _bwd_workspace_bytes(Bsz, T, num_heads, head_dim, C.shape[2], C.shape[3])
+    return _Correction.apply(out, h_final, C, cum_A, h_prev, num_heads, head_dim, sid)

@@ -125,3 +125,119 @@ def test_state_prefix_matches_oracle(world):
     assert torch.equal(hop[0], torch.zeros_like(hop[0]))
     for r in range(1, world):
         assert torch.equal(hop[r], finals[r - 1])
+
+
+# ---- backward: gradients of C, cum_A and h_prev against autograd through the oracle
+# (the reference's torch ops, run in fp32 on the CPU). dC is bf16: rel-L2 within the
+# bf16 bar and max error within 2^-7 of the largest |dC|; dcumA and dh_prev are fp32:
+# the north-star 1e-4 relative bound (absolute below magnitude 1).
+
+def _oracle_grads(args, H, d, gy, ghf, seq_idx=None):
+    out, h_final, C, cum_A, h_prev = args
+    Cf = C.float().requires_grad_(True)          # bf16 values held in fp32: unrounded dC
+    ca = cum_A.clone().requires_grad_(True)
+    hp = h_prev.clone().requires_grad_(True)
+    y, hf = sp.mamba2_cp_correction(out, h_final, Cf, ca, hp, H, d, seq_idx=seq_idx)
+    outs, gouts = [y], [gy]
+    if ghf is not None and hf.requires_grad:
+        outs.append(hf)
+        gouts.append(ghf)
+    return torch.autograd.grad(outs, (Cf, ca, hp), gouts, allow_unused=True)
+
+
+def _check_bwd(args, H, d, seq_idx=None, with_ghf=True, seed=90):
+    from ringmaster_amd.strategies.mamba import mamba2_cp_correction
+
+    out, h_final, C, cum_A, h_prev = args
+    Bsz, T, _ = out.shape
+    gy = seeded((Bsz, T, H * d), seed).to(torch.bfloat16)
+    ghf = seeded(h_prev.shape, seed + 1) if with_ghf else None
+    rC, rA, rH = _oracle_grads(args, H, d, gy, ghf, seq_idx)
+    dC, dA, dH = (t.cuda().requires_grad_(True) for t in (C, cum_A, h_prev))
+    y, hf = mamba2_cp_correction(out.cuda(), h_final.cuda(), dC, dA, dH, H, d,
+                                 seq_idx=None if seq_idx is None else seq_idx.cuda())
+    outs, gouts = [y], [gy.cuda()]
+    if with_ghf:
+        outs.append(hf)
+        gouts.append(ghf.cuda())
+    gC, gA, gH = torch.autograd.grad(outs, (dC, dA, dH), gouts)
+    torch.cuda.synchronize()
+    assert gC.dtype == torch.bfloat16 and gA.dtype == torch.float32 and gH.dtype == torch.float32
+    gC = gC.float().cpu()
+    assert torch.isfinite(gC).all()
+    rl = rel_l2(gC, rC)
+    worst = (gC - rC).abs().max().item() / rC.abs().max().clamp_min(1e-30).item()
+    assert rl < BF16_REL_L2 and worst <= 2.0 ** -7, f"dC: rel-L2 {rl:.3e}, max err {worst:.3e}"
+    assert_f32_rel(gA, rA, "dcumA")
+    assert_f32_rel(gH, rH, "dh_prev")
+
+
+@pytest.mark.parametrize("T,H,d,G,n", [(200, 4, 64, 1, 128), (300, 4, 128, 2, 64),
+                                       (4500, 4, 64, 1, 64), (70, 8, 64, 2, 128),
+                                       (33, 4, 128, 1, 128)])
+def test_correction_backward_matches_oracle(T, H, d, G, n):
+    _check_bwd(_inputs(2, T, H, d, G, n, seed=60), H, d)
+
+
+@pytest.mark.parametrize("fresh_last", [False, True])
+def test_correction_backward_seq_idx(fresh_last):
+    Bsz, T, H, d, G, n = 2, 160, 4, 64, 1, 64
+    seq_idx = torch.zeros(Bsz, T, dtype=torch.int32)
+    seq_idx[0, 70:] = 1
+    if fresh_last:
+        seq_idx[1, 150:] = 2
+    _check_bwd(_inputs(Bsz, T, H, d, G, n, seed=70), H, d, seq_idx=seq_idx)
+
+
+def test_correction_backward_without_state_gradient():
+    """Only y reaches the loss: no dL/dh_final_out (the kernels take a null pointer)."""
+    _check_bwd(_inputs(2, 96, 4, 64, 1, 128, seed=80), 4, 64, with_ghf=False)
+
+
+def test_correction_backward_zero_prefix_has_no_graph():
+    """As in the reference, an all-zero h_prev returns (out, h_final) themselves."""
+    from ringmaster_amd.strategies.mamba import mamba2_cp_correction
+
+    out, h_final, C, cum_A, h_prev = (t.cuda() for t in _inputs(1, 64, 4, 64, 1, 64, seed=85))
+    C.requires_grad_(True)
+    y, hf = mamba2_cp_correction(out, h_final, C, cum_A, torch.zeros_like(h_prev), 4, 64)
+    assert y is out and hf is h_final
+
+
+def test_correction_backward_unsupported_shape_raises_at_forward():
+    from ringmaster_amd.strategies.mamba import mamba2_cp_correction
+
+    out, h_final, C, cum_A, h_prev = (t.cuda() for t in _inputs(1, 64, 4, 64, 1, 32, seed=86))
+    C.requires_grad_(True)
+    with pytest.raises(NotImplementedError, match="d_state"):
+        mamba2_cp_correction(out, h_final, C, cum_A, h_prev, 4, 64)
+
+
+def test_correction_backward_configs4_full_size():
+    """configs[4] shapes against fp32 torch GPU formulas of the same gradients:
+    dC = sum_{h,d} e G H_in, dcumA = e sum_d G S (+ the state term at T-1),
+    dh_prev = sum_t e G C + e_last dh_final_out."""
+    from ringmaster_amd.strategies.mamba import mamba2_cp_correction
+
+    Bsz, T, H, d, G, n = 8, 8192, 64, 64, 1, 128
+    out, h_final, C, cum_A, h_prev = (t.cuda() for t in _inputs(Bsz, T, H, d, G, n, seed=95,
+                                                                strong_decay=True))
+    gy = seeded((Bsz, T, H * d), 96).to(torch.bfloat16).cuda()
+    ghf = seeded(h_prev.shape, 97).cuda()
+    dC, dA, dH = (t.clone().requires_grad_(True) for t in (C, cum_A, h_prev))
+    y, hf = mamba2_cp_correction(out, h_final, dC, dA, dH, H, d)
+    gC, gA, gH = torch.autograd.grad((y, hf), (dC, dA, dH), (gy, ghf))
+    C0 = C[:, :, 0].float()
+    e = torch.exp(cum_A)
+    Gy = gy.float().reshape(Bsz, T, H, d)
+    Ge = Gy * e[..., None]
+    S = torch.einsum("btn,bhdn->bthd", C0, h_prev)
+    rA = (Ge * S).sum(-1)
+    rA[:, -1] += e[:, -1] * (ghf * h_prev).sum((-1, -2))
+    rH = torch.einsum("bthd,btn->bhdn", Ge, C0) + e[:, -1, :, None, None] * ghf
+    rC = torch.einsum("bthd,bhdn->btn", Ge, h_prev)
+    torch.cuda.synchronize()
+    rl = rel_l2(gC[:, :, 0].float(), rC)
+    assert rl < BF16_REL_L2, f"dC rel-L2 {rl:.3e}"
+    assert_f32_rel(gA, rA, "dcumA")
+    assert_f32_rel(gH, rH, "dh_prev")

@@ -283,3 +283,79 @@ def test_mamba2_correction_packed_sequences(cut):
         corrected, _ = sp.mamba2_cp_correction(out_c, h_final, C[:, sl], cum_A, prefixes[r], H, d,
                                                seq_idx=seq_idx)
         assert (corrected - ref_out[:, sl]).abs().max().item() < 1e-6
+
+
+def _correction_case(seed, seq_kind):
+    g = torch.Generator().manual_seed(seed)
+    b, T, H, d, G, n = 2, 12, 4, 3, 2, 5
+    out = torch.randn(b, T, H * d, generator=g, dtype=torch.float64)   # fp64: no output rounding
+    h_final = torch.randn(b, H, d, n, generator=g, dtype=torch.float64)
+    C = torch.randn(b, T, G, n, generator=g, dtype=torch.float64)
+    cum_A = torch.cumsum(-torch.rand(b, T, H, generator=g, dtype=torch.float64) * 0.3, dim=1)
+    h_prev = torch.randn(b, H, d, n, generator=g, dtype=torch.float64)
+    seq_idx = None
+    if seq_kind != "none":
+        seq_idx = torch.zeros(b, T, dtype=torch.long)
+        seq_idx[0, 7:] = 1
+        if seq_kind == "fresh_last":
+            seq_idx[1, 10:] = 3
+    gy = torch.randn(b, T, H * d, generator=g, dtype=torch.float64)
+    ghf = torch.randn(b, H, d, n, generator=g, dtype=torch.float64)
+    return (out, h_final, C, cum_A, h_prev, H, d), seq_idx, gy, ghf
+
+
+def _correction_loss(args, seq_idx, gy, ghf, C, cum_A, h_prev):
+    out, h_final, _, _, _, H, d = args
+    y, hf = sp.mamba2_cp_correction(out, h_final, C, cum_A, h_prev, H, d, seq_idx=seq_idx)
+    return (y.double() * gy).sum() + (hf.double() * ghf).sum()
+
+
+@pytest.mark.parametrize("seq_kind", ["none", "packed", "fresh_last"])
+def test_mamba2_correction_backward_pinned(seq_kind):
+    """The gradients the correction's backward kernels produce (dC, dcumA, dh_prev) are
+    autograd through the oracle's restatement of strategies/mamba.py:101-139; pin them
+    (a) against central finite differences of the same loss and (b) against the closed
+    forms the kernels implement: with e = mask exp(cumA), S = C.H_in,
+    dC = sum_{h in g} e G H_in, dcumA = e sum_d G S (+ e_last sum Gs H_in at T-1 when the
+    state is updated), dh_prev = sum_t e G C (+ e_last Gs)."""
+    args, seq_idx, gy, ghf = _correction_case(5, seq_kind)
+    out, h_final, C, cum_A, h_prev, H, d = args
+    leaves = [t.clone().requires_grad_(True) for t in (C, cum_A, h_prev)]
+    grads = torch.autograd.grad(_correction_loss(args, seq_idx, gy, ghf, *leaves), leaves)
+
+    # (a) finite differences (the oracle computes in fp32 inside: eps 1e-3, loose bound)
+    g = torch.Generator().manual_seed(6)
+    for which, base in enumerate((C, cum_A, h_prev)):
+        for _ in range(6):
+            idx = tuple(int(torch.randint(s, (1,), generator=g)) for s in base.shape)
+            vals = []
+            for sgn in (1.0, -1.0):
+                pert = [C, cum_A, h_prev]
+                t = base.clone()
+                t[idx] += sgn * 1e-3
+                pert[which] = t
+                vals.append(_correction_loss(args, seq_idx, gy, ghf, *pert).item())
+            fd = (vals[0] - vals[1]) / 2e-3
+            an = grads[which][idx].item()
+            assert abs(fd - an) <= 2e-3 * max(1.0, abs(an)), (which, idx, fd, an)
+
+    # (b) closed forms
+    b, T = C.shape[:2]
+    G, n = C.shape[2], C.shape[3]
+    hpg = H // G
+    mask = torch.ones(b, T, dtype=torch.float64) if seq_idx is None else (seq_idx == 0).double()
+    e = mask[..., None] * torch.exp(cum_A)                              # [b, T, H]
+    Cx = C.repeat_interleave(hpg, dim=2)                                # [b, T, H, n]
+    Gy = gy.reshape(b, T, H, d)
+    S = torch.einsum("bthn,bhdn->bthd", Cx, h_prev)
+    dA = e * (Gy * S).sum(-1)
+    dH = torch.einsum("bthd,bthn->bhdn", Gy * e[..., None], Cx)
+    dCx = torch.einsum("bthd,bhdn->bthn", Gy * e[..., None], h_prev)
+    dC = dCx.reshape(b, T, G, hpg, n).sum(3)
+    upd = seq_idx is None or not bool(seq_idx[:, -1].any())
+    if upd:
+        el = torch.exp(cum_A[:, -1])
+        dA[:, -1] += el * (ghf * h_prev).sum((-1, -2))
+        dH = dH + el[..., None, None] * ghf
+    for got, ref in zip(grads, (dC, dA, dH)):
+        assert (got - ref).abs().max().item() <= 1e-4 * max(1.0, ref.abs().max().item())
