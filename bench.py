@@ -288,6 +288,7 @@ def block_workload(steps, warmup):
     out = torch.empty((1, S, Hq, D), dtype=torch.bfloat16, device="cuda")
     lse = torch.empty((1, Hq, S), device="cuda")
     delta = torch.empty((1, Hq, S), device="cuda")
+    nlse = torch.empty((1, Hq, S), device="cuda")
     dq = torch.empty((1, S, Hq, D), device="cuda")
     dk = torch.empty((1, S, Hkv, D), device="cuda")
     dv = torch.empty_like(dk)
@@ -295,8 +296,9 @@ def block_workload(steps, warmup):
     def step():
         ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_ACC_FINAL, out=out, lse=lse,
                                  acc_out=acc, acc_lse=acc_lse)], scale=sc, mask=abi.MASK_FULL)
-        ops.attn_bwd_delta(acc, dout, delta, Hkv)  # fp32 final out left in acc by ACC_FINAL
-        ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta,
+        # fp32 final out left in acc by ACC_FINAL
+        ops.attn_bwd_delta(acc, dout, delta, Hkv, lse=lse, nlse=nlse)
+        ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta, nlse=nlse,
                                  dq_mode=abi.GRAD_WRITE_F32, dkv_mode=abi.GRAD_WRITE_F32,
                                  dq_acc=dq, dk_acc=dk, dv_acc=dv)], scale=sc, mask=abi.MASK_FULL)
 

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 3  /* 3: Mamba2 correction backward entry points */
+#define RMX_ABI_VERSION 4  /* 3: Mamba2 correction backward entry points; 4: nlse */
 
 /* error codes */
 #define RMX_OK 0
@@ -100,6 +100,8 @@ typedef struct rmx_bwd_problem {
   const uint16_t* dout;  /* bf16, o_* strides */
   const float* lse;      /* fp32 [b, hq, sq] global lse */
   const float* delta;    /* fp32 [b, hq, sq] rowsum(dout * out_global) */
+  const float* nlse;     /* fp32 [b, hq, sq] -lse * log2(e), written by rmx_attn_bwd_delta;
+                            required when dkv_mode != RMX_GRAD_NONE */
   float* dq_acc;         /* fp32, a_* strides (F32 modes) */
   uint16_t* dq;          /* bf16, o_* strides (WRITE_BF16 / ACC_FINAL) */
   float* dk_acc;         /* fp32, ka_* strides */
@@ -137,9 +139,13 @@ int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* probl
  * out left in acc_out by the forward, with the a_* strides (out_is_f32 != 0):
  * the fp32 form matches the reference `math` provider, whose autograd never
  * rounds out to bf16. dout uses the o_* strides.
+ * When nlse is not NULL, the same pass also writes nlse[b, h, s] = -lse * log2(e)
+ * from the global lse (the exponent offset the dK/dV kernel adds per query);
+ * lse, delta and nlse share the l_* strides.
  */
 int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const void* out, int32_t out_is_f32,
-                           const uint16_t* dout, float* delta, int32_t sq, void* stream);
+                           const uint16_t* dout, float* delta, const float* lse, float* nlse,
+                           int32_t sq, void* stream);
 
 /*
  * Batched block-attention backward with the global out/lse (ring identity,

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
-ABI_VERSION = 3  # RMX_ABI_VERSION of include/ringmaster_amd.h
+ABI_VERSION = 4  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
@@ -73,7 +73,7 @@ class FwdProblem(ctypes.Structure):
 class BwdProblem(ctypes.Structure):
     _fields_ = [
         ("q", _vp), ("k", _vp), ("v", _vp), ("dout", _vp), ("lse", _vp), ("delta", _vp),
-        ("dq_acc", _vp), ("dq", _vp), ("dk_acc", _vp), ("dv_acc", _vp), ("dk", _vp), ("dv", _vp),
+        ("nlse", _vp), ("dq_acc", _vp), ("dq", _vp), ("dk_acc", _vp), ("dv_acc", _vp), ("dk", _vp), ("dv", _vp),
         ("q_gidx", _vp), ("k_gidx", _vp), ("q_doc", _vp), ("k_doc", _vp),
         ("sq", _i32), ("sk", _i32), ("dq_mode", _i32), ("dkv_mode", _i32),
     ]
@@ -84,7 +84,8 @@ SIGNATURES = {
     "rmx_abi_version": (_i32, []),
     "rmx_last_error": (ctypes.c_char_p, []),
     "rmx_attn_fwd": (_i32, [ctypes.POINTER(AttnLayout), ctypes.POINTER(FwdProblem), _i32, _vp]),
-    "rmx_attn_bwd_delta": (_i32, [ctypes.POINTER(AttnLayout), _vp, _i32, _vp, _vp, _i32, _vp]),
+    "rmx_attn_bwd_delta": (_i32, [ctypes.POINTER(AttnLayout), _vp, _i32, _vp, _vp, _vp, _vp, _i32,
+                                  _vp]),
     "rmx_attn_bwd": (_i32, [ctypes.POINTER(AttnLayout), ctypes.POINTER(BwdProblem), _i32, _vp]),
     "rmx_lse_merge": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32,
                              ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),

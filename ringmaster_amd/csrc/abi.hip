@@ -142,7 +142,8 @@ int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* probl
 }
 
 int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const void* out, int32_t out_is_f32,
-                           const uint16_t* dout, float* delta, int32_t sq, void* stream) {
+                           const uint16_t* dout, float* delta, const float* lse, float* nlse,
+                           int32_t sq, void* stream) {
   int rc = check_layout(layout);
   if (rc) return rc;
   if (sq < 0) return fail(RMX_EINVAL, "negative sequence length");
@@ -150,8 +151,9 @@ int32_t rmx_attn_bwd_delta(const rmx_attn_layout* layout, const void* out, int32
   if ((rc = check_bf16(out, "out"))) return rc;
   if ((rc = check_bf16(dout, "dout"))) return rc;
   if (!delta) return fail(RMX_EINVAL, "delta is NULL");
-  return dev_status(rmx::launch_attn_bwd_delta(*layout, out, out_is_f32 != 0, dout, delta, sq,
-                                               (hipStream_t)stream),
+  if (nlse && !lse) return fail(RMX_EINVAL, "nlse requires lse");
+  return dev_status(rmx::launch_attn_bwd_delta(*layout, out, out_is_f32 != 0, dout, delta, lse,
+                                               nlse, sq, (hipStream_t)stream),
                     "rmx_attn_bwd_delta launch");
 }
 
@@ -174,6 +176,8 @@ int32_t rmx_attn_bwd(const rmx_attn_layout* layout, const rmx_bwd_problem* probl
     if ((rc = check_span(p.sk, layout->k_ss, "k"))) return rc;
     if ((rc = check_span(p.sk, layout->v_ss, "v"))) return rc;
     if (!p.lse || !p.delta) return fail(RMX_EINVAL, "problem %d: lse and delta are required", i);
+    if (p.dkv_mode != RMX_GRAD_NONE && !p.nlse)
+      return fail(RMX_EINVAL, "problem %d: nlse (from rmx_attn_bwd_delta) is required for dk/dv", i);
     if ((rc = check_doc(layout, p.q_gidx, p.k_gidx, p.q_doc, p.k_doc))) return rc;
     const int modes[2] = {p.dq_mode, p.dkv_mode};
     for (int m = 0; m < 2; ++m) {

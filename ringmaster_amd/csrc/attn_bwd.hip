@@ -28,11 +28,15 @@ struct BwdParams {
 // delta = rowsum(dout * out). `out` is the bf16 output (o_* strides) or, when
 // OUT_F32, the fp32 merged output (a_* strides): the fp32 form keeps the bf16
 // rounding of out (up to |dout|*|out|*2^-9 per element) out of dS = P (dP - delta).
+// With nlse, the same pass writes nlse = -lse log2(e) (the per-query exponent
+// offset of the dK/dV kernel) at the same [b, h, s] position.
 template <int HD, bool OUT_F32>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layout L,
                                                              const void* __restrict__ out,
                                                              const uint16_t* __restrict__ dout,
-                                                             float* __restrict__ delta, int sq) {
+                                                             float* __restrict__ delta,
+                                                             const float* __restrict__ lse,
+                                                             float* __restrict__ nlse, int sq) {
   constexpr int TPR = HD / 8;  // threads per row
   const int rows = L.batch * sq * L.hq;
   const int row = blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
@@ -72,31 +76,36 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layo
   }
 #pragma unroll
   for (int m = TPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
-  if (row < rows && part == 0) delta[bb * L.l_sb + h * L.l_sh + q] = acc;
+  if (row < rows && part == 0) {
+    const int64_t lo = bb * L.l_sb + h * L.l_sh + q;
+    delta[lo] = acc;
+    if (nlse) nlse[lo] = lse[lo] * -kLog2e;
+  }
 }
 
 template <int HD>
 static void launch_delta_t(const rmx_attn_layout& L, const void* out, int out_f32,
-                           const uint16_t* dout, float* delta, int sq, int64_t rows,
-                           hipStream_t stream) {
+                           const uint16_t* dout, float* delta, const float* lse, float* nlse,
+                           int sq, int64_t rows, hipStream_t stream) {
   constexpr int RPB = 256 / (HD / 8);  // rows per block
   const int grid = (int)((rows + RPB - 1) / RPB);
   if (out_f32)
     hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, true>), dim3(grid), dim3(256), 0, stream, L, out,
-                       dout, delta, sq);
+                       dout, delta, lse, nlse, sq);
   else
     hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, false>), dim3(grid), dim3(256), 0, stream, L,
-                       out, dout, delta, sq);
+                       out, dout, delta, lse, nlse, sq);
 }
 
 hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int out_f32,
-                                 const uint16_t* dout, float* delta, int sq, hipStream_t stream) {
+                                 const uint16_t* dout, float* delta, const float* lse, float* nlse,
+                                 int sq, hipStream_t stream) {
   const int64_t rows = (int64_t)L.batch * sq * L.hq;
   if (rows == 0) return hipSuccess;
   if (L.head_dim == 128)
-    launch_delta_t<128>(L, out, out_f32, dout, delta, sq, rows, stream);
+    launch_delta_t<128>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
   else
-    launch_delta_t<64>(L, out, out_f32, dout, delta, sq, rows, stream);
+    launch_delta_t<64>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
   return hipGetLastError();
 }
 
@@ -407,33 +416,43 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
     }
 }
 
-// ---------------------------------------------------------------- dK, dV (KV-major)
-// One workgroup = 128 keys of one (problem, batch, kv head), 8 waves in 4
-// pairs: waves w and w + 4 (which the dispatcher places on the same SIMD) own
-// keys k0 + 32w .. k0 + 32w + 31. The workgroup walks every q-head of the GQA
-// group and every query tile (64 queries) the mask leaves, so the group fold
-// needs no cross-workgroup reduction. Per query tile, in two phases separated
-// by a workgroup barrier:
-//   wave w     (P wave)   phase 1: S = Q K^T (A = Q rows, B = K in VGPRs)
-//                                  P = exp2(S c - lse2[q]) (masked), P -> LDS
-//                         phase 2: dV += P^T dO (A = P^T from registers,
-//                                  B = dO^T by transposed reads)
-//   wave w + 4 (dS wave)  phase 1: dP = dO V^T (A = dO rows, B = V in VGPRs)
-//                         phase 2: dS = P (dP - delta[q]) with P from LDS,
-//                                  dK += dS^T Q (B = Q^T by transposed reads)
-// 16 MFMAs per wave and phase. Each wave holds one 32 x HD accumulator and one
-// of K / V, which leaves room for two waves per SIMD: the P wave's exponentials
-// overlap the dS wave's MFMAs in phase 1, and the other way round in phase 2.
-// Q/dO tiles: direct global->LDS loads into three buffers, issued two tiles
-// ahead; both tiles are read as rows and transposed, so their 16-byte chunks
-// are XOR-swizzled with swz_both.
+// ---------------------------------------------------------------- dK, dV (KV-major, one wave per SIMD)
+// One workgroup = 128 keys of one (problem, batch, kv head), 4 waves (one per
+// SIMD, up to 512 registers each). Wave w owns keys k0 + 32w .. k0 + 32w + 31
+// and runs all four GEMMs of a query tile (64 queries) itself, so P and dS never
+// leave its registers:
+//   S   = Q K^T             A = Q rows (LDS), B = K (VGPRs)
+//   P   = exp2(S c + nl)    nl = -lse log2(e) per query (from the delta pass),
+//                           in place in S (fp32)
+//   dP' = delta - dO V^T    A = dO rows (LDS), B = -V (VGPRs); the accumulator
+//                           starts at delta, read from LDS straight into it
+//   dV += P^T dO            A = P^T (registers), B = dO^T (transposed LDS reads)
+//   dK -= (P dP')^T Q       A = (P dP')^T, B = Q^T (transposed LDS reads)
+// (dS = P (dP - delta) = -P dP'; the sign goes into the final scale of dK.)
+// A tile is a software pipeline of four phases of NS = HD/8 steps, one MFMA per
+// step, each step's VALU work issued under its MFMA and its LDS operand read
+// three steps ahead (across phase and tile boundaries):
+//   phase 0: dP'_j           | exponentials of S_j rows 0..31, P^T block 0
+//   phase 1: dV_j            | exponentials of rows 32..63, P^T blocks 1..3,
+//                              (P dP')^T block 0
+//   -- barrier: tile j + 1 landed; tile j - 3's buffer takes tile j + 3
+//   phase 2: dK_j            | (P dP')^T blocks 1..3
+//   phase 3: S_{j+1}         | (reads of nl and delta of tile j + 1)
+// S_{j+1} reuses the registers of P_j (dead after phase 2). Masked tiles (rare)
+// get S := -inf on their masked pairs before their exponentials, with nl clamped
+// to a finite value so that a row with lse = -inf (it attends nothing) gives 0,
+// not NaN.
+// Q/dO tiles (with lse, delta) arrive by LDS DMA into four buffers; a tile is
+// issued three barriers before it is read. Tiles past the end are issued as
+// zero-length loads (they write zeros to a free buffer and touch no memory),
+// which keeps every wait count static.
 template <int HD>
 struct DkdvCfg {
-  static constexpr int NP = 4;                // wave pairs
-  static constexpr int NW = 2 * NP;           // waves per workgroup
+  static constexpr int NW = 4;                // waves per workgroup (one per SIMD)
   static constexpr int NT = 64 * NW;
-  static constexpr int BKV = 32 * NP;         // keys per workgroup
+  static constexpr int BKV = 32 * NW;         // keys per workgroup
   static constexpr int BQ = 64;               // queries per tile
+  static constexpr int NBUF = 4;              // Q/dO tile buffers
   static constexpr int CH = HD / 8;           // 16-byte chunks per row
   static constexpr int RB = HD * 2;           // LDS row bytes (unpadded, swizzled)
   static constexpr int QT = BQ * RB;          // bytes of one Q (or dO) tile
@@ -441,30 +460,23 @@ struct DkdvCfg {
   static constexpr int NDMA = QT / 1024 / NW; // DMA instructions per wave per tile and operand
   static constexpr int NKB = HD / 16;
   static constexpr int NDB = HD / 32;
+  static constexpr int NS = HD / 8;           // steps (MFMAs) per phase
   static_assert(NDMA >= 1 && QT % (1024 * NW) == 0, "tile split");
+  static_assert(NS == 2 * NKB && NS == 4 * NDB, "phase shapes");
 };
 
 template <int HD, int MASK>
-__global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams prm) {
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams prm) {
   using C = DkdvCfg<HD>;
-  constexpr int BQ = C::BQ, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB, NP = C::NP;
+  constexpr int BQ = C::BQ, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB, NS = C::NS;
+  constexpr int NB = C::NBUF;
 
-  // three Q and three dO tile buffers (separate objects, so the compiler can
-  // tell the buffer being read from the ones the DMA is filling)
-  __shared__ __attribute__((aligned(1024))) uint8_t sQ0[C::QT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sQ1[C::QT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sQ2[C::QT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sO0[C::QT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sO1[C::QT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sO2[C::QT];
-  // lse (log2 units after the in-place conversion) and delta of each tile
-  __shared__ __attribute__((aligned(512))) float sM0[2 * BQ];
-  __shared__ __attribute__((aligned(512))) float sM1[2 * BQ];
-  __shared__ __attribute__((aligned(512))) float sM2[2 * BQ];
-  // P of each pair in the C-register layout: [pair][32-query half][reg quad][lane]
-  __shared__ __attribute__((aligned(16))) f32x4 sP[NP][2][4][64];
-  __shared__ int sQg[3][BQ];
-  __shared__ int sQd[3][BQ];
+  __shared__ __attribute__((aligned(1024))) uint8_t sQ[NB][C::QT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sO[NB][C::QT];
+  // nl = -lse log2(e) and delta of each tile
+  __shared__ __attribute__((aligned(512))) float sM[NB][2 * BQ];
+  __shared__ int sQg[NB][BQ];
+  __shared__ int sQd[NB][BQ];
   __shared__ int sRange[2];
 
   const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
@@ -480,9 +492,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int pair = wave % NP;
   const int lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int kw0 = k0 + 32 * pair;  // first key of this wave pair
+  const int kw0 = k0 + 32 * wave;  // first key of this wave
   const int key = kw0 + l32;
   const bool kvalid = key < sk;
 
@@ -509,7 +520,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     int lo = nqt, hi = -1;
     for (int t = tid; t < nqt; t += C::NT) {
       const int qa = t * BQ, qz = (t * BQ + BQ < sq ? t * BQ + BQ : sq) - 1;
-      const int qga = P.q_gidx[qa], qgz = P.q_gidx[qz];
+      const int qgz = P.q_gidx[qz];
       const int qda = P.q_doc[qa], qdz = P.q_doc[qz];
       if (qgz >= kg_first && qdz >= kd_first && qda <= kd_last) {
         lo = t < lo ? t : lo;
@@ -523,40 +534,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     qt_end = sRange[1] + 1;
     if (qt_end < qt_begin) qt_end = qt_begin;
   }
-  const int nq_iter = qt_end - qt_begin;
-  const int ntile = nq_iter * G;  // (q head, query tile) pairs, q head major
+  const int ntile = (qt_end - qt_begin) * G;  // (q head, query tile) pairs, q head major
   const int wave_klast = (kw0 + 31 < sk ? kw0 + 31 : sk - 1);
 
-  // ---- Q / dO tiles, lse and delta by DMA; query documents (DOC) by wave 0
-  const int qss = (int)(2 * L.q_ss), oss = (int)(2 * L.o_ss);
-  auto qbuf = [&](auto b) -> uint8_t* {
-    constexpr int B = decltype(b)::value;
-    if constexpr (B == 0) return sQ0;
-    else if constexpr (B == 1) return sQ1;
-    else return sQ2;
-  };
-  auto obuf = [&](auto b) -> uint8_t* {
-    constexpr int B = decltype(b)::value;
-    if constexpr (B == 0) return sO0;
-    else if constexpr (B == 1) return sO1;
-    else return sO2;
-  };
-  auto lbuf = [&](auto b) -> float* {
-    constexpr int B = decltype(b)::value;
-    if constexpr (B == 0) return sM0;
-    else if constexpr (B == 1) return sM1;
-    else return sM2;
-  };
-  auto dbuf = [&](auto b) -> float* { return lbuf(b) + BQ; };
-  // Wave 0 first loads the tile's lse and delta (one dword per lane; rows past
-  // the end read 0, where Q and dO rows are 0 as well, so they add nothing),
-  // then every wave its share of the Q and dO rows: instruction n of a tile
+  // ---- tile loads. Wave 0 first loads the tile's lse and delta (one dword per
+  // lane; rows past the end read 0, where Q and dO rows are 0 as well, so they
+  // add nothing), then every wave its share of the Q and dO rows (instruction n
   // fills LDS bytes [1024 n, 1024 n + 1024), lane L row n*RPK + L/CH, swizzled
-  // chunk L%CH. Wave 0's metadata precedes its tile loads, so a wait that
-  // leaves a later tile's 2*NDMA loads in flight covers it. The loads are the
-  // asm form (dma16_async): the kernel orders every LDS read after them itself.
-  // Tiles run q head major: tile (qt, hi) is query tile qt of q head kvh * G + hi.
-  // Cursors over that order advance by one tile at a time (no divisions).
+  // chunk L%CH). Every wave issues 2*NDMA loads per tile after its metadata, so
+  // a wait that leaves the last 2*NDMA loads in flight covers every earlier tile.
   struct Cursor {
     int qt, hi;
   };
@@ -567,18 +553,20 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     }
     return c;
   };
-  auto dma_tile = [&](auto b, Cursor cu) {
+  const int qss = (int)(2 * L.q_ss), oss = (int)(2 * L.o_ss);
+  auto dma_tile = [&](int b, Cursor cu, bool live) {
     const int qa = cu.qt * BQ;
-    const int qh = kvh * G + cu.hi;
+    const int qh = live ? kvh * G + cu.hi : kvh * G;
     if (wave == 0) {
       const int64_t lb = bb * L.l_sb + qh * L.l_sh;
-      const uint32_t m = lds_addr(lbuf(b));
-      dma4_async(make_rsrc(P.lse + lb, 4u * sq), m, 4 * (qa + lane));
-      dma4_async(make_rsrc(P.delta + lb, 4u * sq), m + 4 * BQ, 4 * (qa + lane));
+      const uint32_t m = lds_addr(sM[b]);
+      const uint32_t n = live ? 4u * sq : 0u;
+      dma4_async(make_rsrc(P.nlse + lb, n), m, 4 * (qa + lane));
+      dma4_async(make_rsrc(P.delta + lb, n), m + 4 * BQ, 4 * (qa + lane));
     }
-    const i32x4 qrs = make_rsrc(P.q + bb * L.q_sb + qh * L.q_sh, span_bytes(sq, qss, HD * 2));
-    const i32x4 ors = make_rsrc(P.dout + bb * L.o_sb + qh * L.o_sh, span_bytes(sq, oss, HD * 2));
-    const uint32_t qd = lds_addr(qbuf(b)), od = lds_addr(obuf(b));
+    const i32x4 qrs = make_rsrc(P.q + bb * L.q_sb + qh * L.q_sh, live ? span_bytes(sq, qss, HD * 2) : 0u);
+    const i32x4 ors = make_rsrc(P.dout + bb * L.o_sb + qh * L.o_sh, live ? span_bytes(sq, oss, HD * 2) : 0u);
+    const uint32_t qd = lds_addr(sQ[b]), od = lds_addr(sO[b]);
 #pragma unroll
     for (int i = 0; i < C::NDMA; ++i) {
       const int n = wave * C::NDMA + i;
@@ -586,15 +574,6 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       const int ch = 16 * (p ^ swz_both<HD>(r));
       dma16_async(qrs, qd + 1024 * n, (qa + r) * qss + ch);
       dma16_async(ors, od + 1024 * n, (qa + r) * oss + ch);
-    }
-  };
-  // lse -> log2 units in place, once per tile, by the first dS wave. A row with
-  // lse = -inf attends no key, so every tile holding it takes the masked path,
-  // which discards the +inf exponent.
-  auto lse_to_log2 = [&](auto b) {
-    if (wave == NP) {
-      float* l = lbuf(b);
-      l[lane] = l[lane] * kLog2e;
     }
   };
   int nqg = 0, nqd = 0;
@@ -617,7 +596,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     }
   };
 
-  // per-lane LDS byte offsets (swizzle folded in): rows (A of S, dP): query row
+  // per-lane LDS byte offsets (swizzle folded in): rows (A of S, dP'): query row
   // 32 mb + sigma(l32), chunk 2 kb + hl
   int raddr[NKB];
   {
@@ -645,170 +624,282 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     return join_bf16x8(lds_read_tr(reinterpret_cast<const uint16_t*>(p + taddr[0][db])),
                        lds_read_tr(reinterpret_cast<const uint16_t*>(p + taddr[1][db])));
   };
+  auto row_op = [&](const uint8_t* tile, int kb, int mb) -> bf16x8 {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(tile + raddr[kb] + mb * 32 * RB));
+  };
 
-  // ---- prologue: tiles 0 and 1 in flight, documents of tile 0 in LDS
-  const Cursor c_first = {qt_begin, 0};
-  if (ntile > 0) {
-    dma_tile(std::integral_constant<int, 0>{}, c_first);
-    doc_load(c_first);
-    doc_store(0);
-    if (ntile > 1) dma_tile(std::integral_constant<int, 1>{}, advance(c_first));
+  // ---- K and -V of this wave's keys in registers (lane: key row, dims 16 kb + 8 hl ..)
+  bf16x8 kreg[NKB], vreg[NKB];
+  {
+    const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
+    const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, HD * 2));
+    const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, HD * 2));
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      kreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(krs, key * kss + 16 * hl + 32 * kb));
+      vreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(vrs, key * vss + 16 * hl + 32 * kb) ^ 0x80008000u);
+    }
+    // MFMA reads its A/B operands from AGPRs as well: K and -V live there, which
+    // leaves the VGPRs to the fp32 tiles the VALU works on
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) asm volatile("" : "+a"(kreg[kb]), "+a"(vreg[kb]));
+  }
+  int kg = 2147483647, kd = -2;
+  if (mask == RMX_MASK_DOC && kvalid) {
+    kg = P.k_gidx[key];
+    kd = P.k_doc[key];
   }
 
-  const float c = prm.scale_log2;
-  auto run = [&](auto role) {
-    constexpr bool PW = decltype(role)::value == 0;  // P wave (S, P, dV) or dS wave (dP, dS, dK)
-    bf16x8 kv[NKB];  // K (P wave) or V (dS wave): lane holds row `key`, dims 16 kb + 8 hl ..
-    {
-      const uint16_t* src = PW ? P.k + bb * L.k_sb + kvh * L.k_sh : P.v + bb * L.v_sb + kvh * L.v_sh;
-      const int ss = PW ? (int)(2 * L.k_ss) : (int)(2 * L.v_ss);
-      const i32x4 rs = make_rsrc(src, span_bytes(sk, ss, HD * 2));
-      const int o = key * ss + 16 * hl;
+  // per-tile metadata in the accumulator / exponent layout: element r of half mb
+  // belongs to query 32 mb + sig_row(hl, r), i.e. two runs of 8 queries
+  auto load_rows = [&](const float* m, f32x16* dst) {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) kv[kb] = __builtin_bit_cast(bf16x8, buf_load16(rs, o + 32 * kb));
-    }
-    int kg = 2147483647, kd = -2;
-    if (PW && mask == RMX_MASK_DOC && kvalid) {
-      kg = P.k_gidx[key];
-      kd = P.k_doc[key];
-    }
-    f32x16 acc[NDB];
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) acc[db] = zero16();
-    wait_all_loads();
-    lds_barrier();
-    if (ntile > 0) lse_to_log2(std::integral_constant<int, 0>{});
-    lds_barrier();
-
-    // cursors of tiles j, j + 1 and j + 2
-    Cursor cur = c_first, nx1 = advance(c_first), nx2 = advance(advance(c_first));
-    auto tile = [&](auto b, int j) {
-      constexpr int B = decltype(b)::value;  // == j % 3
-      using NEXT = std::integral_constant<int, (B + 1) % 3>;
-      const int qa = cur.qt * BQ;
-      if (j + 1 < ntile) doc_load(nx1);
-      // buffer (j + 2) % 3 held tile j - 1, released by the last barrier
-      if (j + 2 < ntile) dma_tile(std::integral_constant<int, (B + 2) % 3>{}, nx2);
-      cur = nx1;
-      nx1 = nx2;
-      nx2 = advance(nx2);
-      const uint8_t* qt_l = qbuf(b);
-      const uint8_t* ot_l = obuf(b);
-
-      if constexpr (PW) {
-        // ---- phase 1: S = Q K^T, P
-        bool need_mask = (kw0 + 32 > sk);
-        if (mask == RMX_MASK_CAUSAL) need_mask |= (wave_klast > qa + off);
-        if (mask == RMX_MASK_DOC) {
-          const int qga = sQg[B][0];
-          const int qda = sQd[B][0];
-          const int qz = (qa + BQ < sq ? BQ : sq - qa) - 1;
-          const int qdz = sQd[B][qz];
-          need_mask |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga);
-        }
-        f32x16 s[2];
-        s[0] = zero16();
-        s[1] = zero16();
+      for (int h8 = 0; h8 < 2; ++h8) {
+        const float* p = m + 32 * mb + 16 * h8 + 8 * hl;
+        const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-          for (int mb = 0; mb < 2; ++mb) {
-            const bf16x8 a =
-                __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qt_l + raddr[kb] + mb * 32 * RB));
-            s[mb] = mfma32(a, kv[kb], s[mb]);
-          }
-        bf16x8 pt[4];
-#pragma unroll
-        for (int kb2 = 0; kb2 < 4; ++kb2) {
-          const int mb = kb2 >> 1, h8 = kb2 & 1;
-          const int qb = 16 * kb2 + 8 * hl;  // queries of regs 8 h8 .. 8 h8 + 7
-          const f32x4 l0 = *reinterpret_cast<const f32x4*>(lbuf(b) + qb);
-          const f32x4 l1 = *reinterpret_cast<const f32x4*>(lbuf(b) + qb + 4);
-          float pv[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) pv[i] = fast_exp2(fmaf(s[mb][8 * h8 + i], c, -(i < 4 ? l0[i] : l1[i - 4])));
-          if (need_mask) {
-            keep_branch();
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const int ql = qb + i;
-              bool ok = kvalid;
-              if (mask == RMX_MASK_CAUSAL) ok &= key <= qa + ql + off;
-              if (mask == RMX_MASK_DOC) ok &= (sQd[B][ql] == kd) & (kg <= sQg[B][ql]);
-              pv[i] = ok ? pv[i] : 0.f;
-            }
-          }
-          f32x4 w0, w1;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            w0[i] = pv[i];
-            w1[i] = pv[4 + i];
-          }
-          sP[pair][mb][2 * h8][lane] = w0;
-          sP[pair][mb][2 * h8 + 1][lane] = w1;
-          pt[kb2] = pack8_hw(pv);
-        }
-        lds_barrier();
-        // ---- phase 2: dV += P^T dO
-#pragma unroll
-        for (int kb2 = 0; kb2 < 4; ++kb2)
-#pragma unroll
-          for (int db = 0; db < NDB; ++db) acc[db] = mfma32(pt[kb2], tr_op(ot_l, kb2, db), acc[db]);
-      } else {
-        // ---- phase 1: dP = dO V^T
-        f32x16 dp[2];
-        dp[0] = zero16();
-        dp[1] = zero16();
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-          for (int mb = 0; mb < 2; ++mb) {
-            const bf16x8 a =
-                __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ot_l + raddr[kb] + mb * 32 * RB));
-            dp[mb] = mfma32(a, kv[kb], dp[mb]);
-          }
-        // tile j + 1's lse landed before the last barrier
-        if (j + 1 < ntile) lse_to_log2(NEXT{});
-        lds_barrier();
-        // ---- phase 2: dS = P (dP - delta), dK += dS^T Q
-#pragma unroll
-        for (int kb2 = 0; kb2 < 4; ++kb2) {
-          const int mb = kb2 >> 1, h8 = kb2 & 1;
-          const int qb = 16 * kb2 + 8 * hl;
-          const f32x4 d0 = *reinterpret_cast<const f32x4*>(dbuf(b) + qb);
-          const f32x4 d1 = *reinterpret_cast<const f32x4*>(dbuf(b) + qb + 4);
-          const f32x4 p0 = sP[pair][mb][2 * h8][lane];
-          const f32x4 p1 = sP[pair][mb][2 * h8 + 1][lane];
-          float dsv[8];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            dsv[i] = p0[i] * (dp[mb][8 * h8 + i] - d0[i]);
-            dsv[4 + i] = p1[i] * (dp[mb][8 * h8 + 4 + i] - d1[i]);
-          }
-          const bf16x8 dst = pack8_hw(dsv);
-#pragma unroll
-          for (int db = 0; db < NDB; ++db) acc[db] = mfma32(dst, tr_op(qt_l, kb2, db), acc[db]);
+        for (int i = 0; i < 4; ++i) {
+          dst[mb][8 * h8 + i] = a[i];
+          dst[mb][8 * h8 + 4 + i] = b[i];
         }
       }
+  };
 
-      // publish tile j + 1 (its DMA was issued a tile ago); tile j + 2's stays in flight
-      if (j + 1 < ntile) doc_store((B + 1) % 3);
-      if (j + 2 < ntile)
-        wait_vm_barrier<2 * C::NDMA>();
-      else
-        wait_vm_barrier<0>();
-    };
-    for (int j = 0; j < ntile; j += 3) {
-      tile(std::integral_constant<int, 0>{}, j);
-      if (j + 1 < ntile) tile(std::integral_constant<int, 1>{}, j + 1);
-      if (j + 2 < ntile) tile(std::integral_constant<int, 2>{}, j + 2);
+  // ---- masking (rare tiles: sequence end, causal diagonal, document boundaries)
+  auto need_mask_of = [&](int qa, int slot) -> bool {
+    bool m = (kw0 + 32 > sk);
+    if (mask == RMX_MASK_CAUSAL) m |= (wave_klast > qa + off);
+    if (mask == RMX_MASK_DOC) {
+      const int qga = sQg[slot][0];
+      const int qda = sQd[slot][0];
+      const int qz = (qa + BQ < sq ? BQ : sq - qa) - 1;
+      const int qdz = sQd[slot][qz];
+      m |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga);
     }
+    return m;
+  };
+  // S := -inf on masked pairs, nl finite (see above). The 32 elements are
+  // expanded at compile time: a runtime element index would put S in scratch.
+  auto apply_mask = [&](int qa, int slot, f32x16* s, f32x16* nl) __attribute__((always_inline)) {
+    [&]<int... E>(std::integer_sequence<int, E...>) __attribute__((always_inline)) {
+      (
+          [&] {
+            constexpr int mb = E >> 4, r = E & 15;
+            const int ql = 32 * mb + sig_row(hl, r);
+            bool ok = kvalid;
+            if (mask == RMX_MASK_CAUSAL) ok &= key <= qa + ql + off;
+            if (mask == RMX_MASK_DOC) ok &= (sQd[slot][ql] == kd) & (kg <= sQg[slot][ql]);
+            s[mb][r] = ok ? s[mb][r] : kNegInf;
+            nl[mb][r] = fminf(nl[mb][r], 3.0e38f);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, 32>{});
+  };
 
-    // ---- epilogue: lane (hl, d) holds rows key = kw0 + c_row(hl, r)
-    const float sc = PW ? 1.f : L.scale;
-    float* gacc = PW ? P.dv_acc : P.dk_acc;
-    uint16_t* gbf = PW ? P.dv : P.dk;
-    const int mode = P.dkv_mode;
+  // read i (0..7) of load_rows: rows 32 (i / 4) + 16 ((i / 2) % 2) + 8 hl + 4 (i % 2) .. + 3
+  auto load_rows_part = [&](const float* m, f32x16* dst, int i) {
+    const int mb = i >> 2, h8 = (i >> 1) & 1, hf = i & 1;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(m + 32 * mb + 16 * h8 + 8 * hl + 4 * hf);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[mb][8 * h8 + 4 * hf + e] = a[e];
+  };
+
+  // ---- prologue: tiles 0, 1 and 2 issued, documents of tile 0 in LDS
+  Cursor cur = {qt_begin, 0};
+  Cursor nx1 = advance(cur), nx2 = advance(nx1), nx3 = advance(nx2);
+  dma_tile(0, cur, ntile > 0);
+  dma_tile(1, nx1, ntile > 1);
+  dma_tile(2, nx2, ntile > 2);
+  doc_load(cur);
+  doc_store(0);
+
+  f32x16 dv[NDB], dk[NDB], s[2], dp[2], nl[2];
+  // register classes: the dV/dK accumulators (MFMA only) in AGPRs; S, P and dP'
+  // (read by the VALU) in VGPRs
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    dv[db] = zero16();
+    dk[db] = zero16();
+    asm volatile("" : "+a"(dv[db]), "+a"(dk[db]));
+  }
+  auto pin_v = [](f32x16* x) __attribute__((always_inline)) {
+    asm volatile("" : "+v"(x[0]), "+v"(x[1]));
+  };
+  wait_all_loads();
+  lds_barrier();
+  const float c = prm.scale_log2;
+
+  constexpr int KD = 7;  // operand read-ahead (steps)
+  // the ring's slots line up across tiles: a tile is 4 NS steps
+  static_assert((4 * NS) % (KD + 1) == 0, "operand ring size must divide the tile's steps");
+  bf16x8 ops[KD + 1];
+  // LDS operand of step T of the tile in buffer b (T >= 4 NS: the next tile's)
+  auto operand = [&](int b, int T) -> bf16x8 {
+    const int ph = T / NS, t = T % NS;
+    const int bn = (b + 1) % NB;
+    if (ph == 0) return row_op(sO[b], t >> 1, t & 1);
+    if (ph == 1) return tr_op(sO[b], t / NDB, t % NDB);
+    if (ph == 2) return tr_op(sQ[b], t / NDB, t % NDB);
+    if (ph == 3) return row_op(sQ[bn], t >> 1, t & 1);
+    return row_op(sO[bn], t >> 1, t & 1);
+  };
+
+  if (ntile > 0) {
+    // S_0, nl_0 and delta_0, the first operands of tile 0
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) s[mb] = zero16();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32(row_op(sQ[0], kb, mb), kreg[kb], s[mb]);
+    pin_v(s);
+    load_rows(sM[0], nl);
+    load_rows(sM[0] + BQ, dp);
+    pin_v(dp);
+    if (need_mask_of(cur.qt * BQ, 0)) {
+      keep_branch();
+      apply_mask(cur.qt * BQ, 0, s, nl);
+    }
+#pragma unroll
+    for (int T = 0; T < KD; ++T) ops[T] = operand(0, T);
+  }
+
+  // pack elements 2w, 2w + 1 of 8-row block blk (rows 32 (blk / 2) + sig_row(hl,
+  // 8 (blk % 2) + ..)) of x (times y when given) into word w of op
+  auto pack_pair = [&](bf16x8& op, const f32x16* x, const f32x16* y, int blk, int w) {
+    const int mb = blk >> 1, r = 8 * (blk & 1) + 2 * w;
+    float v0 = x[mb][r], v1 = x[mb][r + 1];
+    if (y) {
+      v0 *= y[mb][r];
+      v1 *= y[mb][r + 1];
+    }
+    u32x4 u = __builtin_bit_cast(u32x4, op);
+    uint32_t pk = cvt_pk_bf16(v0, v1);
+    asm volatile("" : "+v"(pk));
+    u[w] = pk;
+    op = __builtin_bit_cast(bf16x8, u);
+  };
+
+  auto tile = [&](auto bc, int j) {
+    constexpr int B = decltype(bc)::value;  // == j % NB
+    constexpr int BN = (B + 1) % NB;
+    if (j + 1 < ntile) doc_load(nx1);
+    bf16x8 pt[4], dst[4];
+    auto step = [&](auto Tc) __attribute__((always_inline)) {
+      constexpr int T = decltype(Tc)::value;
+      constexpr int ph = T / NS, t = T % NS;
+      constexpr int NP = 4 / NDB;  // packs per step when a block is packed over NDB steps
+      ops[(T + KD) % (KD + 1)] = operand(B, T + KD);
+      if constexpr (ph == 3) {
+        // metadata of tile j + 1 (landed at this tile's barrier): the 8 reads of
+        // nl, then the 8 of delta, spread over the phase
+        constexpr int RPS = 16 / NS;  // reads per step
+#pragma unroll
+        for (int q = 0; q < RPS; ++q) {
+          const int i = RPS * t + q;
+          if (i < 8)
+            load_rows_part(sM[BN], nl, i);
+          else
+            load_rows_part(sM[BN] + BQ, dp, i - 8);
+        }
+        if constexpr (t == NS - 1) pin_v(dp);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const bf16x8 a = ops[T % (KD + 1)];
+      if constexpr (ph == 0) {
+        dp[t & 1] = mfma32(a, vreg[t >> 1], dp[t & 1]);
+      } else if constexpr (ph == 1) {
+        dv[t % NDB] = mfma32(pt[t / NDB], a, dv[t % NDB]);
+      } else if constexpr (ph == 2) {
+        dk[t % NDB] = mfma32(dst[t / NDB], a, dk[t % NDB]);
+      } else {
+        if constexpr (t < 2) s[t] = zero16();
+        s[t & 1] = mfma32(a, kreg[t >> 1], s[t & 1]);
+        if constexpr (t == NS - 1) pin_v(s);
+      }
+      if constexpr (ph == 0) {
+        // exponentials of rows 0..31; P^T block 0 once its rows are done
+        constexpr int e0 = 16 * t / NS, e1 = 16 * (t + 1) / NS;
+#pragma unroll
+        for (int e = e0; e < e1; ++e) {
+          float x = fast_exp2(fmaf(s[0][e], c, nl[0][e]));
+          asm volatile("" : "+v"(x));
+          s[0][e] = x;
+        }
+        if constexpr (t >= NS / 2 && t < NS / 2 + 4) pack_pair(pt[0], s, nullptr, 0, t - NS / 2);
+      } else if constexpr (ph == 1) {
+        // exponentials of rows 32..63 in the first half of the phase
+        if constexpr (t < NS / 2) {
+          constexpr int e0 = 32 * t / NS, e1 = 32 * (t + 1) / NS;
+#pragma unroll
+          for (int e = e0; e < e1; ++e) {
+            float x = fast_exp2(fmaf(s[1][e], c, nl[1][e]));
+            asm volatile("" : "+v"(x));
+            s[1][e] = x;
+          }
+        }
+        // P^T block k + 1 in steps [k NDB, (k + 1) NDB); (P dP')^T block 0 last
+        constexpr int k = t / NDB;
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+          const int w = NP * (t % NDB) + q;
+          if constexpr (k < 3)
+            pack_pair(pt[k + 1], s, nullptr, k + 1, w);
+          else
+            pack_pair(dst[0], s, dp, 0, w);
+        }
+      } else if constexpr (ph == 2) {
+        // (P dP')^T block k + 1 in steps [k NDB, (k + 1) NDB)
+        constexpr int k = t / NDB;
+        if constexpr (k < 3) {
+#pragma unroll
+          for (int q = 0; q < NP; ++q) pack_pair(dst[k + 1], s, dp, k + 1, NP * (t % NDB) + q);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    [&]<int... T>(std::integer_sequence<int, T...>) __attribute__((always_inline)) {
+      (step(std::integral_constant<int, T>{}), ...);
+    }(std::make_integer_sequence<int, 2 * NS>{});  // phases 0, 1
+
+    // hand-over: tile j + 1 landed (tile j + 2 may stay in flight); tile j - 3's
+    // buffer (last read in phase 2 of tile j - 3) takes tile j + 3
+    if (j + 1 < ntile) doc_store(BN);
+    wait_vm_barrier<2 * C::NDMA>();
+    dma_tile((B + 3) % NB, nx3, j + 3 < ntile);
+    const int qa_next = nx1.qt * BQ;
+    cur = nx1;
+    nx1 = nx2;
+    nx2 = nx3;
+    nx3 = advance(nx3);
+
+    [&]<int... T>(std::integer_sequence<int, T...>) __attribute__((always_inline)) {
+      (step(std::integral_constant<int, 2 * NS + T>{}), ...);
+    }(std::make_integer_sequence<int, 2 * NS>{});  // phases 2, 3
+
+    if (j + 1 < ntile && need_mask_of(qa_next, BN)) {
+      keep_branch();
+      apply_mask(qa_next, BN, s, nl);
+    }
+  };
+  for (int j = 0; j < ntile; j += NB) {
+    tile(std::integral_constant<int, 0>{}, j);
+    if (j + 1 < ntile) tile(std::integral_constant<int, 1>{}, j + 1);
+    if (j + 2 < ntile) tile(std::integral_constant<int, 2>{}, j + 2);
+    if (j + 3 < ntile) tile(std::integral_constant<int, 3>{}, j + 3);
+  }
+  wait_all_loads();  // zero-length loads issued past the end
+
+  // ---- epilogue: lane (hl, l32) holds column d = 32 db + l32 of keys kw0 + c_row(hl, r)
+  const int mode = P.dkv_mode;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const float sc = g == 0 ? 1.f : -L.scale;
+    float* gacc = g == 0 ? P.dv_acc : P.dk_acc;
+    uint16_t* gbf = g == 0 ? P.dv : P.dk;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       const int d = 32 * db + l32;
@@ -816,25 +907,21 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       for (int r = 0; r < 16; ++r) {
         const int kk = kw0 + c_row(hl, r);
         if (kk >= sk) continue;
-        const float g = acc[db][r] * sc;
+        const float gv = (g == 0 ? dv[db][r] : dk[db][r]) * sc;
         const int64_t ao = bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + d;
         const int64_t bo = bb * L.dk_sb + (int64_t)kk * L.dk_ss + kvh * L.dk_sh + d;
         if (mode == RMX_GRAD_WRITE_F32) {
-          gacc[ao] = g;
+          gacc[ao] = gv;
         } else if (mode == RMX_GRAD_ACC_F32) {
-          gacc[ao] += g;
+          gacc[ao] += gv;
         } else if (mode == RMX_GRAD_ACC_FINAL) {
-          gbf[bo] = f2bf(gacc[ao] + g);
+          gbf[bo] = f2bf(gacc[ao] + gv);
         } else {
-          gbf[bo] = f2bf(g);
+          gbf[bo] = f2bf(gv);
         }
       }
     }
-  };
-  if (wave < NP)
-    run(std::integral_constant<int, 0>{});
-  else
-    run(std::integral_constant<int, 1>{});
+  }
 }
 
 template <int HD>

@@ -11,7 +11,8 @@ namespace rmx {
 hipError_t launch_attn_fwd(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                            hipStream_t stream);
 hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int out_f32,
-                                 const uint16_t* dout, float* delta, int sq, hipStream_t stream);
+                                 const uint16_t* dout, float* delta, const float* lse, float* nlse,
+                                 int sq, hipStream_t stream);
 hipError_t launch_attn_bwd(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                            hipStream_t stream);
 hipError_t launch_lse_merge(float* out, float* lse, const void* blk_out, int blk_is_f32,

@@ -75,12 +75,15 @@ def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None,
         # the delta kernel reads a bf16 out and dout with one set of strides
         dout = torch.empty_like(out).copy_(dout)
     delta = torch.empty((b, hq, sq), dtype=torch.float32, device=q.device)
-    ops.attn_bwd_delta(out if out_f32 is None else out_f32, dout, delta, hkv)
+    nlse = torch.empty_like(delta)
+    if not lse.is_contiguous():
+        lse = lse.contiguous()
+    ops.attn_bwd_delta(out if out_f32 is None else out_f32, dout, delta, hkv, lse=lse, nlse=nlse)
     dq_t = dq if (dq is not None and dq.stride() == dout.stride()) else torch.empty_like(dout)
     dk_t = dk if (dk is not None and dk.is_contiguous()) else torch.empty(
         k.shape, dtype=torch.bfloat16, device=k.device)
     dv_t = dv if (dv is not None and dv.stride() == dk_t.stride()) else torch.empty_like(dk_t)
-    ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta,
+    ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta, nlse=nlse,
                              dq_mode=abi.GRAD_WRITE_BF16, dkv_mode=abi.GRAD_WRITE_BF16,
                              dq=dq_t, dk=dk_t, dv=dv_t)],
                  scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL)

@@ -44,6 +44,7 @@ class BwdJob:
     delta: torch.Tensor
     dq_mode: int
     dkv_mode: int
+    nlse: torch.Tensor | None = None
     dq_acc: torch.Tensor | None = None
     dq: torch.Tensor | None = None
     dk_acc: torch.Tensor | None = None
@@ -69,6 +70,7 @@ _ROLES = {
     "lse": ("l", 2, torch.float32),
     "acc_lse": ("l", 2, torch.float32),
     "delta": ("l", 2, torch.float32),
+    "nlse": ("l", 2, torch.float32),
     "dk": ("dk", 3, torch.bfloat16),
     "dv": ("dk", 3, torch.bfloat16),
     "dk_acc": ("ka", 3, torch.float32),
@@ -146,21 +148,31 @@ def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int) -> None:
     abi.check(abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, len(jobs), abi.stream_of(q0)))
 
 
-def attn_bwd_delta(out: torch.Tensor, dout: torch.Tensor, delta: torch.Tensor, hkv: int) -> None:
+def attn_bwd_delta(out: torch.Tensor, dout: torch.Tensor, delta: torch.Tensor, hkv: int,
+                   lse: torch.Tensor | None = None, nlse: torch.Tensor | None = None) -> None:
     """delta[b, h, s] = sum_d dout * out (fp32). dout: [b, s, h, d] bf16; out: bf16 with the
-    strides of dout, or the fp32 final out (any strides with a contiguous dim)."""
+    strides of dout, or the fp32 final out (any strides with a contiguous dim). With ``nlse``
+    (and the global ``lse``), also nlse = -lse * log2(e), which the dK/dV kernel reads; lse,
+    delta and nlse must share their strides."""
     batch, sq, hq, d = dout.shape
     if out.shape != dout.shape:
         raise ValueError("out and dout must share their shape")
     f32 = out.dtype == torch.float32
     if not f32 and out.stride() != dout.stride():
         raise ValueError("bf16 out and dout must share strides")
+    if (nlse is None) != (lse is None):
+        raise ValueError("lse and nlse go together")
     job = FwdJob(q=dout, k=dout[:, :0, :hkv], v=dout[:, :0, :hkv], out=dout, lse=delta,
                  acc_out=out if f32 else None)
-    lay = _fill_layout([job], batch, hq, hkv, d, 1.0, abi.MASK_FULL)
+    jobs = [job]
+    if nlse is not None:
+        if lse.shape != delta.shape or nlse.shape != delta.shape:
+            raise ValueError("lse, delta and nlse must share their shape")
+        jobs += [FwdJob(q=dout, k=job.k, v=job.v, lse=lse), FwdJob(q=dout, k=job.k, v=job.v, lse=nlse)]
+    lay = _fill_layout(jobs, batch, hq, hkv, d, 1.0, abi.MASK_FULL)
     abi.check(abi.lib().rmx_attn_bwd_delta(ctypes.byref(lay), out.data_ptr(), int(f32),
-                                           dout.data_ptr(), delta.data_ptr(), sq,
-                                           abi.stream_of(dout)))
+                                           dout.data_ptr(), delta.data_ptr(), abi.ptr(lse),
+                                           abi.ptr(nlse), sq, abi.stream_of(dout)))
 
 
 def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int) -> None:
@@ -176,7 +188,7 @@ def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int) -> None:
     for i, j in enumerate(jobs):
         p = arr[i]
         p.q, p.k, p.v, p.dout = j.q.data_ptr(), j.k.data_ptr(), j.v.data_ptr(), j.dout.data_ptr()
-        p.lse, p.delta = j.lse.data_ptr(), j.delta.data_ptr()
+        p.lse, p.delta, p.nlse = j.lse.data_ptr(), j.delta.data_ptr(), abi.ptr(j.nlse)
         p.dq_acc, p.dq = abi.ptr(j.dq_acc), abi.ptr(j.dq)
         p.dk_acc, p.dv_acc = abi.ptr(j.dk_acc), abi.ptr(j.dv_acc)
         p.dk, p.dv = abi.ptr(j.dk), abi.ptr(j.dv)

@@ -178,10 +178,14 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
     if not out.is_contiguous():
         out = out.contiguous()
     delta = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
+    nlse = torch.empty_like(delta)
+    if not lse.is_contiguous():
+        lse = lse.contiguous()
     flat = (c.P * c.b, c.L, c.hq, c.d)
+    lflat = (c.P * c.b, c.hq, c.L)
     with timer("attn_bwd_delta"):
-        ops.attn_bwd_delta(out.reshape(flat), dout.reshape(flat),
-                           delta.reshape(c.P * c.b, c.hq, c.L), c.hkv)
+        ops.attn_bwd_delta(out.reshape(flat), dout.reshape(flat), delta.reshape(lflat), c.hkv,
+                           lse=lse.reshape(lflat), nlse=nlse.reshape(lflat))
     dq = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.float32, device=dev)
     dk = torch.empty((c.P, c.b, c.L, c.hkv, c.d), dtype=torch.float32, device=dev)
     dv = torch.empty_like(dk)
@@ -193,7 +197,7 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
             qs, ks = slice(bl.q_lo, bl.q_hi), slice(bl.k_lo, bl.k_hi)
             common = dict(
                 q=qd[r][:, qs], k=kd[kr][:, ks], v=vd[kr][:, ks], dout=dout[r][:, qs],
-                lse=lse[r][:, :, qs], delta=delta[r][:, :, qs],
+                lse=lse[r][:, :, qs], delta=delta[r][:, :, qs], nlse=nlse[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
                 q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi))
             kv_jobs.append(ops.BwdJob(dq_mode=abi.GRAD_NONE, dkv_mode=mode,

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 3
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 4
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -73,6 +73,22 @@ def test_host_validation_problem_fields():
     arr[0].mode = 9
     assert abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, 1, None) == abi.RMX_EINVAL
     assert b"mode" in abi.lib().rmx_last_error()
+
+
+def test_host_validation_backward_nlse():
+    lay = _layout()
+    arr = (abi.BwdProblem * 1)()
+    p = arr[0]
+    p.q = p.k = p.v = p.dout = p.lse = p.delta = 16
+    p.dk_acc = p.dv_acc = 256
+    p.sq, p.sk = 4, 4
+    p.dq_mode, p.dkv_mode = abi.GRAD_NONE, abi.GRAD_WRITE_F32
+    lib = abi.lib()
+    assert lib.rmx_attn_bwd(ctypes.byref(lay), arr, 1, None) == abi.RMX_EINVAL
+    assert b"nlse" in lib.rmx_last_error()
+    # the delta pass writes nlse only from a given lse
+    assert lib.rmx_attn_bwd_delta(ctypes.byref(lay), 16, 0, 16, 16, None, 16, 4, None) == abi.RMX_EINVAL
+    assert b"lse" in lib.rmx_last_error()
 
 
 def test_empty_calls_are_noops():
