@@ -262,6 +262,148 @@ def zigzag_ring_backward(d_outs, qs, ks, vs, outs, lses, scaling=None, cu_seqlen
             [t.transpose(1, 2) for t in cur_dv])
 
 
+# ---------------------------------------------------------------- contiguous rings
+def contiguous_gidx(rank, local_len):
+    """Global token indices of rank's contiguous chunk."""
+    return torch.arange(rank * local_len, (rank + 1) * local_len)
+
+
+def _contig_mask(rank, rem, L, step, causal, doc):
+    """Mask of rank's block against rank rem's KV: document-masked on global indices for
+    packed inputs (ring/varlen_blocks.py:51-58), else bottom-right causal on the step-0
+    diagonal of a causal ring (ring/p2p_attn.py:168, :112-118) and nothing elsewhere."""
+    if doc is not None:
+        return additive_doc_mask(contiguous_gidx(rank, L), contiguous_gidx(rem, L), doc, causal)
+    return causal_mask(L, L) if (causal and step == 0) else 0.0
+
+
+def _prep(qs, ks, vs, scaling):
+    d = qs[0].shape[-1]
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(d)
+    return ([q.transpose(1, 2).float() for q in qs], [k.transpose(1, 2).float() for k in ks],
+            [v.transpose(1, 2).float() for v in vs], scale)
+
+
+def contiguous_ring_forward(qs, ks, vs, *, causal=True, scaling=None, cu_seqlens=None):
+    """Contiguous p2p ring forward, the explicit path of RingP2PAttention.forward
+    (ring/p2p_attn.py:161-185): rank r merges, in step order, its block against the KV
+    rank (r - s) mod P holds at step s (kv_source), skipping s > r when causal; only
+    the step-0 block is causal. qs/ks/vs: per-rank [b, H, L, d]; returns per-rank out
+    [b, L, H, d] (q dtype) and lse [b, H, L] fp32."""
+    world = len(qs)
+    qd, kd, vd, scale = _prep(qs, ks, vs, scaling)
+    L = qd[0].shape[1]
+    doc = doc_ids_from_cu(cu_seqlens) if cu_seqlens is not None else None
+    outs, lses = [], []
+    for rank in range(world):
+        out = lse = None
+        for s in range(world):
+            if causal and s > rank:
+                continue
+            rem = kv_source(rank, s, world)
+            bo, bl = _block_fwd(qd[rank], kd[rem], vd[rem], scale,
+                                _contig_mask(rank, rem, L, s, causal, doc))
+            out, lse = update_out_and_lse(out, lse, bo, bl)
+        outs.append(out.to(qs[0].dtype))
+        lses.append(lse.squeeze(-1).transpose(1, 2).contiguous())
+    return outs, lses
+
+
+def contiguous_ring_backward(d_outs, qs, ks, vs, outs, lses, *, causal=True, scaling=None,
+                             cu_seqlens=None):
+    """Reverse contiguous ring with the global out/lse (ring/p2p_attn.py:243-281): after
+    every step the dK/dV accumulator a rank holds moves on with its KV block (:266-275),
+    so after P hops each block's gradient is back at its owner. d_outs/outs: per-rank
+    [b, L, H, d]; returns per-rank (dq, dk, dv) [b, H, L, d] fp32."""
+    world = len(qs)
+    qd, kd, vd, scale = _prep(qs, ks, vs, scaling)
+    L = qd[0].shape[1]
+    doc = doc_ids_from_cu(cu_seqlens) if cu_seqlens is not None else None
+    dq = [torch.zeros_like(q) for q in qd]
+    cur_dk = [torch.zeros_like(k) for k in kd]
+    cur_dv = [torch.zeros_like(v) for v in vd]
+    for s in range(world):
+        for rank in range(world):
+            if causal and s > rank:
+                continue
+            rem = kv_source(rank, s, world)
+            dqb, dkb, dvb = masked_block_bwd(d_outs[rank].float(), qd[rank], kd[rem], vd[rem],
+                                             outs[rank].float(), lses[rank],
+                                             _contig_mask(rank, rem, L, s, causal, doc), scale)
+            dq[rank] += dqb
+            cur_dk[rank] += dkb
+            cur_dv[rank] += dvb
+        cur_dk = [cur_dk[(r - 1) % world] for r in range(world)]
+        cur_dv = [cur_dv[(r - 1) % world] for r in range(world)]
+    return ([t.transpose(1, 2) for t in dq], [t.transpose(1, 2) for t in cur_dk],
+            [t.transpose(1, 2) for t in cur_dv])
+
+
+def distflash_forward(qs, ks, vs, *, scaling=None, cu_seqlens=None):
+    """DistFlashAttention.forward (ring/distflash.py:98-152), in its merge order: the
+    causal diagonal; the owner-local blocks (r, r - d) for d > P // 2 in increasing d
+    (phase 2, :125-131); then the partials of the blocks (r, r - d), d = 1 .. P // 2,
+    that helper r - d computed and routed back (phase 1, :133-142)."""
+    world = len(qs)
+    qd, kd, vd, scale = _prep(qs, ks, vs, scaling)
+    L = qd[0].shape[1]
+    half = world // 2
+    doc = doc_ids_from_cu(cu_seqlens) if cu_seqlens is not None else None
+    outs, lses = [], []
+    for r in range(world):
+        out, lse = update_out_and_lse(None, None, *_block_fwd(
+            qd[r], kd[r], vd[r], scale, _contig_mask(r, r, L, 0, True, doc)))
+        order = [d for d in range(half + 1, world)] + [d for d in range(1, half + 1)]
+        for d in order:
+            if r - d < 0:
+                continue
+            bo, bl = _block_fwd(qd[r], kd[r - d], vd[r - d], scale,
+                                _contig_mask(r, r - d, L, d, True, doc))
+            out, lse = update_out_and_lse(out, lse, bo, bl)
+        outs.append(out.to(qs[0].dtype))
+        lses.append(lse.squeeze(-1).transpose(1, 2).contiguous())
+    return outs, lses
+
+
+def distflash_backward(d_outs, qs, ks, vs, outs, lses, *, scaling=None, cu_seqlens=None):
+    """DistFlashAttention.backward (ring/distflash.py:154-226): the diagonal seeds dq,
+    dk, dv; phase 2 (d > P // 2): the owner r computes (r, r - d), keeps dq and sends the
+    dK/dV with the KV back to owner r - d; phase 1 (d <= P // 2): helper r - d computes
+    the block from the owner's (dout, q, out, lse), keeps dK/dV and returns dq."""
+    world = len(qs)
+    qd, kd, vd, scale = _prep(qs, ks, vs, scaling)
+    L = qd[0].shape[1]
+    half = world // 2
+    doc = doc_ids_from_cu(cu_seqlens) if cu_seqlens is not None else None
+    dq = [torch.zeros_like(q) for q in qd]
+    dk = [torch.zeros_like(k) for k in kd]
+    dv = [torch.zeros_like(v) for v in vd]
+
+    def block(i, j, d):
+        return masked_block_bwd(d_outs[i].float(), qd[i], kd[j], vd[j], outs[i].float(),
+                                lses[i], _contig_mask(i, j, L, d, True, doc), scale)
+
+    for r in range(world):
+        a, b_, c = block(r, r, 0)
+        dq[r] += a
+        dk[r] += b_
+        dv[r] += c
+    for d in range(half + 1, world):  # phase 2: owner r, KV owner r - d
+        for r in range(d, world):
+            a, b_, c = block(r, r - d, d)
+            dq[r] += a
+            dk[r - d] += b_
+            dv[r - d] += c
+    for d in range(1, half + 1):  # phase 1: helper h computes for owner h + d
+        for h in range(world - d):
+            a, b_, c = block(h + d, h, d)
+            dk[h] += b_
+            dv[h] += c
+            dq[h + d] += a
+    return ([t.transpose(1, 2) for t in dq], [t.transpose(1, 2) for t in dk],
+            [t.transpose(1, 2) for t in dv])
+
+
 def full_attention(q, k, v, *, causal=True, scaling=None, cu_seqlens=None):
     """Brute-force attention over the whole sequence in the caller's dtype (use
     fp64 to pin). q/k/v [b, S, H, d] -> out [b, S, H, d], lse [b, H, S]."""

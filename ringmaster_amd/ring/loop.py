@@ -1,0 +1,71 @@
+"""The ring attention entry points of ring/loop.py, P ranks emulated on one MI355X.
+
+``ring_attention`` dispatches like the reference (ring/loop.py:20-61): one rank is a
+single block call, ``rotate_method="allgather"`` is the gather-then-attend ring
+(:201-228), anything else (the reference's ``alltoall``) is the p2p ring with its
+preconditions (FA2-class implementation, zero dropout, no window: :52-57).
+``varlen_ring_attention`` attends within each packed document over the gathered K/V
+(:102-198). Inputs are the per-rank interface tensors ``[b, H, L, d]`` stacked on a
+leading rank axis; outputs are ``[P, b, L, H, d]``.
+
+Gathering K/V and attending once per rank computes the same blocks as the p2p ring
+(a bottom-right causal mask over ``K[0 : (r + 1) L]`` is the ring's diagonal-causal
+plus full earlier blocks), so both methods run the emulated contiguous ring: on one
+GPU every rank already reads every KV block in place from HBM.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ringmaster_amd.ring.kernels import PROVIDERS
+from ringmaster_amd.ring.p2p_attn import contiguous_ring
+from ringmaster_amd.ring.zigzag import doc_for
+
+
+def _method(rotate_method) -> str:
+    return str(getattr(rotate_method, "value", rotate_method)).lower()
+
+
+def ring_attention(q, k, v, *, group=None, causal: bool, scaling=None, dropout: float = 0.0,
+                   provider: str = "mi355x_hip", rotate_method="alltoall",
+                   attn_implementation: str = "flash_attention_2", window=None, timer=None):
+    """q/k/v: [P, b, H, L, d]; returns [P, b, L, H, d]."""
+    if group is not None:
+        raise ValueError("the emulated ring takes the ranks on the leading axis, not a group")
+    if provider not in PROVIDERS:
+        raise KeyError(provider)
+    if provider != "mi355x_hip":
+        raise NotImplementedError(f"provider {provider!r} has no MI355X ring in this build")
+    if q.dim() != 5:
+        raise ValueError("q/k/v must be [world, b, H, L, d]")
+    if q.shape[0] == 1:
+        block = PROVIDERS[provider]
+        out, _ = block(q[0].transpose(1, 2), k[0].transpose(1, 2), v[0].transpose(1, 2),
+                       causal=causal, scaling=scaling, dropout=dropout,
+                       attn_implementation=attn_implementation, window=window)
+        return out.unsqueeze(0)
+    if _method(rotate_method) == "allgather":
+        if dropout or window is not None:
+            raise NotImplementedError("dropout and sliding windows are not supported")
+        return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer)
+    if dropout or window is not None or attn_implementation not in ("flash_attention_2", "math"):
+        raise ValueError("P2P Ring requires FA2, zero dropout, and no sliding window")
+    return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer)
+
+
+def varlen_ring_attention(q, k, v, *, group=None, scaling, cu_seqlens, causal=True,
+                          dropout=0.0, window=None, attn_implementation="math", timer=None):
+    """Packed documents over contiguous shards: each query attends the earlier keys of
+    its own document (global positions ``r * L + i``). q/k/v: [P, b, H, L, d]; returns
+    [P, b, L, H, d]."""
+    if group is not None:
+        raise ValueError("the emulated ring takes the ranks on the leading axis, not a group")
+    if dropout or window is not None:
+        raise NotImplementedError("dropout and sliding windows are not supported")
+    if not causal:
+        raise NotImplementedError("packed (document-masked) blocks are causal in this build")
+    if not isinstance(cu_seqlens, torch.Tensor):
+        cu_seqlens = torch.as_tensor(cu_seqlens)
+    return contiguous_ring(q, k, v, causal=True, scaling=scaling, doc=doc_for(cu_seqlens, q),
+                           timer=timer)

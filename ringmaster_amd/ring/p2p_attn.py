@@ -1,0 +1,37 @@
+"""Contiguous p2p ring attention, P ranks emulated on one MI355X.
+
+Counterpart of ``RingP2PAttention`` / ``ring_p2p_attention`` (ring/p2p_attn.py:121-291):
+rank ``r`` holds the contiguous chunk ``r`` of the sequence; at step ``s`` it attends
+the KV block of rank ``(r - s) mod P`` (hop direction ring/p2p_attn.py:65-69), causal
+rings skipping ``s > r`` and masking only the step-0 diagonal; the online-softmax merge
+runs in the forward epilogue and the backward uses the global out/lse, the dK/dV
+accumulators of a block updated in place at its owner (what the reference's dk/dv
+rotation achieves after P hops, :243-281). One batched launch per ring step covers
+every rank, as for the zigzag ring.
+"""
+
+from __future__ import annotations
+
+import math
+
+from ringmaster_amd.ring.zigzag import EmulatedRing, check_ring_inputs
+
+
+def contiguous_ring(q, k, v, *, causal: bool, scaling=None, doc=None, timer=None):
+    """q/k/v: [P, b, H, L, d] bf16, rank r's contiguous interface tensors stacked on
+    dim 0. Returns out [P, b, L, H, d]. ``doc``: per-token document ids of the packed
+    sequence (document-masked blocks, causal only)."""
+    check_ring_inputs(q, k, v)
+    if doc is not None and not causal:
+        raise NotImplementedError("packed (document-masked) blocks are causal in this build")
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
+    return EmulatedRing.apply(q, k, v, float(scale), doc, timer, "contiguous", bool(causal))
+
+
+def ring_p2p_attention(q, k, v, *, group=None, causal, scaling, timer=None):
+    """q/k/v: [P, b, H, L, d]; returns [P, b, L, H, d] (each rank's interface output
+    layout, ring/p2p_attn.py:284-291). ``group`` must be None: the ranks are the
+    leading axis. GQA is native (no KV repetition)."""
+    if group is not None:
+        raise ValueError("the emulated ring takes the ranks on the leading axis, not a group")
+    return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer)

@@ -89,3 +89,52 @@ def ring_pairs_per_rank(world: int, local_len: int) -> int:
     """Pairs each rank attends: L(L+1)/2 + (P-1) * 2h^2, equal on every rank."""
     h = local_len // 2
     return local_len * (local_len + 1) // 2 + (world - 1) * 2 * h * h
+
+
+# ---------------------------------------------------------------- contiguous layouts
+def contiguous_schedule(world: int, local_len: int, *, causal: bool) -> list[list[Block]]:
+    """Blocks of every step of the contiguous ring (rank ``r`` owns tokens
+    ``[r L, (r + 1) L)``): at step ``s`` rank ``r`` attends the KV block of rank
+    ``(r - s) mod P`` (ring/p2p_attn.py:161-185, hop direction :65-69), all of it;
+    causal rings skip ``s > r`` (the KV lies in the future) and make only the
+    step-0 diagonal block causal. A rank's rows are first touched at step 0 and last
+    at step ``r`` (causal) or ``P - 1``.
+
+    The same per-step block sets are DistFlash's (ring/distflash.py:1-20): its
+    step ``d`` computes exactly the blocks ``(i, i - d)``, ``i >= d``, whether a
+    helper (``d <= P // 2``, partial routed to the owner) or the owner itself
+    (``d > P // 2``) runs them; only the rank doing the work differs."""
+    if world < 1:
+        raise ValueError("world must be positive")
+    if local_len < 1:
+        raise ValueError("local length must be positive")
+    steps: list[list[Block]] = []
+    for s in range(world):
+        blocks = []
+        for r in range(world):
+            if causal and s > r:
+                continue
+            last = s == (r if causal else world - 1)
+            blocks.append(Block(r, 0, local_len, (r - s) % world, 0, local_len,
+                                causal and s == 0, s == 0, last))
+        steps.append(blocks)
+    return steps
+
+
+def contiguous_gidx(rank: int, local_len: int) -> list[int]:
+    """Global token indices of ``rank``'s contiguous chunk."""
+    return list(range(rank * local_len, (rank + 1) * local_len))
+
+
+def distflash_work(world: int) -> list[int]:
+    """Causal blocks each rank computes under the DistFlash schedule
+    (ring/distflash.py:98-152): its diagonal, the owner-local blocks
+    ``(r, r - d)`` with ``d > P // 2`` (phase 2) and the helper blocks
+    ``(r + d, r)`` with ``1 <= d <= P // 2`` (phase 1). P=4 gives 3, 3, 2, 2
+    against the plain ring's 1, 2, 3, 4 (ring/distflash.py:15)."""
+    half = world // 2
+    work = [1] * world
+    for r in range(world):
+        work[r] += sum(1 for d in range(half + 1, world) if r - d >= 0)
+        work[r] += sum(1 for d in range(1, half + 1) if r + d < world)
+    return work

@@ -31,7 +31,8 @@ import torch
 
 from ringmaster_amd import abi
 from ringmaster_amd.ring import ops
-from ringmaster_amd.ring.schedule import zigzag_gidx, zigzag_schedule
+from ringmaster_amd.ring.schedule import (contiguous_gidx, contiguous_schedule, zigzag_gidx,
+                                          zigzag_schedule)
 
 
 def doc_ids_from_cu(cu_seqlens: torch.Tensor, device) -> torch.Tensor:
@@ -52,25 +53,34 @@ def _fwd_mode(first: bool, last: bool) -> int:
 
 
 class _Ctx:
-    """Per-call tensors shared by the forward and backward passes."""
+    """Per-call tensors shared by the forward and backward passes. ``layout`` is
+    "zigzag" (rank r holds chunks r and 2P-1-r) or "contiguous" (rank r holds
+    chunk r); the zigzag ring is causal only."""
 
-    def __init__(self, q, k, scale, doc):
+    def __init__(self, q, k, scale, doc, layout="zigzag", causal=True):
         self.P, self.b, self.hq, self.L, self.d = q.shape
         self.hkv = k.shape[2]
         self.half = self.L // 2
         self.scale = scale
         self.doc = doc
+        self.layout, self.causal = layout, causal
         self.gidx = self.rdoc = None
         if doc is not None:
-            rows = [zigzag_gidx(r, self.half, self.P) for r in range(self.P)]
+            rows = [zigzag_gidx(r, self.half, self.P) if layout == "zigzag"
+                    else contiguous_gidx(r, self.L) for r in range(self.P)]
             self.gidx = torch.tensor(rows, dtype=torch.int32).to(q.device)
             # document id of every local row of every rank: [P, L]
             self.rdoc = doc[self.gidx.long()].to(torch.int32).contiguous()
 
+    def schedule(self, split_final: bool):
+        if self.layout == "zigzag":
+            return zigzag_schedule(self.P, self.L, split_final=split_final)
+        return contiguous_schedule(self.P, self.L, causal=self.causal)
+
     def mask(self, step: int) -> int:
         if self.doc is not None:
             return abi.MASK_DOC
-        return abi.MASK_CAUSAL if step == 0 else abi.MASK_FULL
+        return abi.MASK_CAUSAL if (self.causal and step == 0) else abi.MASK_FULL
 
     def idx(self, rank, lo, hi):
         return None if self.gidx is None else self.gidx[rank, lo:hi]
@@ -130,13 +140,15 @@ class _NoTimer:
 _NO_TIMER = _NoTimer()
 
 
-def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=None):
-    """Emulated zigzag ring forward. q/k/v: [P, b, H, L, d] bf16 (interface layout per rank).
+def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=None,
+                 layout: str = "zigzag", causal: bool = True):
+    """Emulated ring forward (zigzag or contiguous layout). q/k/v: [P, b, H, L, d] bf16
+    (interface layout per rank).
     Returns (out [P, b, L, H, d] bf16, lse [P, b, H, L] fp32, out32 [P, b, L, H, d] fp32):
     ``out32`` is the running fp32 accumulator, which the last touch of every row leaves
     holding the final merged out (the backward's delta is computed from it)."""
     timer = timer or _NO_TIMER
-    c = _Ctx(q, k, scale, doc)
+    c = _Ctx(q, k, scale, doc, layout, causal)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)  # [P, b, L, H, d] views
     dev = q.device
     out = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.bfloat16, device=dev)
@@ -145,7 +157,7 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
     acc_lse = None
     if c.P > 1:
         acc_lse = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
-    for s, blocks in enumerate(zigzag_schedule(c.P, c.L, split_final=True)):
+    for s, blocks in enumerate(c.schedule(split_final=True)):
         jobs = []
         for bl in blocks:
             r, kr = bl.rank, bl.kv_rank
@@ -164,13 +176,13 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
 
 
 def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | None = None,
-                  timer=None):
+                  timer=None, layout: str = "zigzag", causal: bool = True):
     """Reverse-ring backward with the global out/lse. dout: [P, b, L, H, d] bf16; out: the
     global out, fp32 (the forward's ``out32``) or bf16, [P, b, L, H, d].
     Returns fp32 (dq [P, b, L, Hq, d], dk, dv [P, b, L, Hkv, d]). Each step launches the
     KV-major dK/dV kernel and the Q-major dQ kernel over all ranks."""
     timer = timer or _NO_TIMER
-    c = _Ctx(q, k, scale, doc)
+    c = _Ctx(q, k, scale, doc, layout, causal)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)
     dev = q.device
     if not dout.is_contiguous():
@@ -189,7 +201,7 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
     dq = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.float32, device=dev)
     dk = torch.empty((c.P, c.b, c.L, c.hkv, c.d), dtype=torch.float32, device=dev)
     dv = torch.empty_like(dk)
-    for s, blocks in enumerate(zigzag_schedule(c.P, c.L, split_final=False)):
+    for s, blocks in enumerate(c.schedule(split_final=False)):
         mode = abi.GRAD_WRITE_F32 if s == 0 else abi.GRAD_ACC_F32
         kv_jobs, q_jobs = [], []
         for bl in blocks:
@@ -211,21 +223,46 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
     return dq, dk, dv
 
 
-class EmulatedZigzagRing(torch.autograd.Function):
+class EmulatedRing(torch.autograd.Function):
+    """The emulated ring (zigzag or contiguous layout) with its reverse-ring backward."""
+
     @staticmethod
-    def forward(ctx, q, k, v, scale, doc, timer):
-        out, lse, out32 = ring_forward(q, k, v, scale, doc, timer)
+    def forward(ctx, q, k, v, scale, doc, timer, layout, causal):
+        out, lse, out32 = ring_forward(q, k, v, scale, doc, timer, layout, causal)
         ctx.save_for_backward(q, k, v, out32, lse)
         ctx.scale, ctx.doc, ctx.timer = scale, doc, timer
+        ctx.layout, ctx.causal = layout, causal
         return out
 
     @staticmethod
     def backward(ctx, d_out):
         q, k, v, out32, lse = ctx.saved_tensors
-        dq, dk, dv = ring_backward(d_out, q, k, v, out32, lse, ctx.scale, ctx.doc, ctx.timer)
+        dq, dk, dv = ring_backward(d_out, q, k, v, out32, lse, ctx.scale, ctx.doc, ctx.timer,
+                                   ctx.layout, ctx.causal)
         # fp32 accumulators -> q.dtype, returned in the interface layout [P, b, H, L, d]
         return (dq.to(q.dtype).transpose(2, 3), dk.to(k.dtype).transpose(2, 3),
-                dv.to(v.dtype).transpose(2, 3), None, None, None)
+                dv.to(v.dtype).transpose(2, 3), None, None, None, None, None)
+
+
+def check_ring_inputs(q, k, v):
+    """Validation shared by the emulated rings (q/k/v: [world, b, H, L, d])."""
+    abi.require_device(q, k, v)
+    if q.dim() != 5 or k.dim() != 5 or v.dim() != 5:
+        raise ValueError("q/k/v must be [world, b, H, L, d]")
+    if q.shape[2] % k.shape[2]:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if q.dtype != torch.bfloat16:
+        raise NotImplementedError("the MI355X ring computes in bf16")
+
+
+def doc_for(cu_seqlens, q):
+    """Per-token document ids of the packed sequence (None when not packed)."""
+    if cu_seqlens is None:
+        return None
+    doc = doc_ids_from_cu(cu_seqlens, q.device)
+    if doc.numel() != q.shape[0] * q.shape[3]:
+        raise ValueError("cu_seqlens must cover the full (padded) sequence")
+    return doc
 
 
 def zigzag_ring_attention(q, k, v, *, scaling=None, cu_seqlens=None, timer=None):
@@ -233,19 +270,8 @@ def zigzag_ring_attention(q, k, v, *, scaling=None, cu_seqlens=None, timer=None)
     (L = two chunks, early then late). Returns [P, b, L, H, d]; ``cu_seqlens`` set =>
     packed (document-masked) blocks. Counterpart of ring/zigzag.py:257-260. ``timer``
     (a :class:`KernelTimer`) records HIP events around every kernel launch."""
-    abi.require_device(q, k, v)
-    if q.dim() != 5 or k.dim() != 5 or v.dim() != 5:
-        raise ValueError("q/k/v must be [world, b, H, L, d]")
-    if q.shape[2] % k.shape[2]:
-        raise ValueError("Query heads must be divisible by KV heads")
+    check_ring_inputs(q, k, v)
     if q.shape[3] % 2:
         raise ValueError("local length must hold two equal zigzag chunks")
-    if q.dtype != torch.bfloat16:
-        raise NotImplementedError("the MI355X ring computes in bf16")
     scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
-    doc = None
-    if cu_seqlens is not None:
-        doc = doc_ids_from_cu(cu_seqlens, q.device)
-        if doc.numel() != q.shape[0] * q.shape[3]:
-            raise ValueError("cu_seqlens must cover the full (padded) sequence")
-    return EmulatedZigzagRing.apply(q, k, v, float(scale), doc, timer)
+    return EmulatedRing.apply(q, k, v, float(scale), doc_for(cu_seqlens, q), timer, "zigzag", True)

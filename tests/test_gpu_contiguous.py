@@ -1,0 +1,107 @@
+"""Emulated contiguous rings on the MI355X (p2p / allgather ``ring_attention``,
+``ring_p2p_attention``, DistFlash, packed ``varlen_ring_attention``) vs the CPU oracle
+rings (fp32), values and gradients."""
+
+import pytest
+import torch
+
+from oracle import ring_math as rm
+from tests.gpu_util import assert_bf16_close, bf16_pair
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(world, L, hq, hkv, d=128, seed=0):
+    S = world * L
+    full = [bf16_pair((1, S, h, d), seed + i)[0] for i, h in enumerate((hq, hkv, hkv, hq), 1)]
+    idx = [rm.contiguous_gidx(r, L) for r in range(world)]
+    per = [[t[:, i].transpose(1, 2).contiguous() for i in idx] for t in full[:3]]
+    dev = [torch.stack(p).to(torch.bfloat16).cuda().requires_grad_(True) for p in per]
+    dos = [full[3][:, i] for i in idx]
+    dod = torch.stack(dos).to(torch.bfloat16).cuda()
+    return per, dev, dos, dod
+
+
+def _check(fn, ref_fwd, ref_bwd, world, L, hq=2, hkv=2, cu=None, seed=0):
+    per, (qd, kd, vd), dos, dod = _inputs(world, L, hq, hkv, seed=seed)
+    print(f"case world={world} L={L} hq={hq} hkv={hkv} docs={cu}", flush=True)
+    out = fn(qd, kd, vd)
+    out.backward(dod)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = ref_fwd(*per, cu_seqlens=cu)
+    rdq, rdk, rdv = ref_bwd(dos, *per, ref_out, ref_lse, cu_seqlens=cu)
+    for r in range(world):
+        assert_bf16_close(out[r], ref_out[r], f"out rank {r}")
+        assert_bf16_close(qd.grad[r], rdq[r], f"dq rank {r}")
+        assert_bf16_close(kd.grad[r], rdk[r], f"dk rank {r}")
+        assert_bf16_close(vd.grad[r], rdv[r], f"dv rank {r}")
+
+
+def _contig(causal):
+    return (lambda *a, **kw: rm.contiguous_ring_forward(*a, causal=causal, **kw),
+            lambda *a, **kw: rm.contiguous_ring_backward(*a, causal=causal, **kw))
+
+
+@pytest.mark.parametrize("world", [1, 2, 4, 8])
+@pytest.mark.parametrize("causal", [True, False])
+def test_p2p_ring(world, causal):
+    from ringmaster_amd.ring import ring_p2p_attention
+
+    _check(lambda q, k, v: ring_p2p_attention(q, k, v, causal=causal, scaling=None),
+           *_contig(causal), world, 128)
+
+
+@pytest.mark.parametrize("method", ["allgather", "alltoall"])
+def test_ring_attention_methods_gqa_ragged(method):
+    from ringmaster_amd.ring import ring_attention
+
+    _check(lambda q, k, v: ring_attention(q, k, v, causal=True, rotate_method=method,
+                                          attn_implementation="math"),
+           *_contig(True), 4, 100, hq=4, hkv=2)
+
+
+def test_ring_attention_single_rank_is_one_block():
+    from ringmaster_amd.ring import ring_attention
+
+    _check(lambda q, k, v: ring_attention(q, k, v, causal=True), *_contig(True), 1, 192)
+
+
+@pytest.mark.parametrize("world", [2, 4, 8])
+def test_distflash(world):
+    from ringmaster_amd.ring import distflash_attention
+
+    # MHA: with GQA the first rank's dV sums two heads over every rank and reaches |dV| ~ 4,
+    # where one bf16 rounding of the output (half an ulp, 2^-7 * 4) nearly fills the 2e-2
+    # bound by itself; the GQA fold is covered by the ring_attention and varlen cases
+    _check(lambda q, k, v: distflash_attention(q, k, v, scaling=None),
+           rm.distflash_forward, rm.distflash_backward, world, 96, hq=2, hkv=2)
+
+
+@pytest.mark.parametrize("docs", [[300, 212], [100, 50, 250, 112]])
+def test_distflash_varlen(docs):
+    from ringmaster_amd.ring import distflash_attention
+
+    cu = torch.tensor([0, *torch.tensor(docs).cumsum(0).tolist()], dtype=torch.int32)
+    world = 4
+    _check(lambda q, k, v: distflash_attention(q, k, v, scaling=None, cu_seqlens=cu.cuda()),
+           rm.distflash_forward, rm.distflash_backward, world, 128, hq=2, hkv=1, cu=cu)
+
+
+def test_varlen_ring_attention():
+    from ringmaster_amd.ring import varlen_ring_attention
+
+    cu = torch.tensor([0, 37, 200, 201, 390, 512], dtype=torch.int32)
+    _check(lambda q, k, v: varlen_ring_attention(q, k, v, scaling=None, cu_seqlens=cu.cuda()),
+           *_contig(True), 4, 128, cu=cu)
+
+
+def test_p2p_preconditions():
+    from ringmaster_amd.ring import ring_attention
+
+    q = torch.zeros(2, 1, 2, 64, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="P2P Ring requires"):
+        ring_attention(q, q, q, causal=True, dropout=0.1)
+    with pytest.raises(ValueError, match="P2P Ring requires"):
+        ring_attention(q, q, q, causal=True, attn_implementation="sdpa")
+    with pytest.raises(NotImplementedError):
+        ring_attention(q, q, q, causal=True, rotate_method="allgather", window=(4, 0))

@@ -147,3 +147,18 @@ def test_correction_seq_idx_mutant_is_caught(monkeypatch):
     monkeypatch.setattr(sp, "mamba2_cp_correction", ignore_seq_idx)
     with pytest.raises(AssertionError):
         pin.test_mamba2_correction_packed_sequences(11)
+
+
+@pytest.mark.parametrize("mutation", ["direction", "skip_past"])
+def test_contiguous_ring_mutants_are_caught(monkeypatch, mutation):
+    pin.check_contiguous(4, 3)  # the unmutated oracle passes
+    if mutation == "direction":  # KV hops the other way round the ring
+        monkeypatch.setattr(rm, "kv_source", lambda rank, step, world: (rank + step) % world)
+    else:  # attends the block of step s > r instead of skipping it: future tokens leak in
+        real = rm.contiguous_ring_forward
+
+        def leaky(qs, ks, vs, *, causal=True, **kw):
+            return real(qs, ks, vs, causal=False, **kw)
+        monkeypatch.setattr(rm, "contiguous_ring_forward", leaky)
+    with pytest.raises(AssertionError):
+        pin.check_contiguous(4, 3)

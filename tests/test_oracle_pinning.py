@@ -146,6 +146,61 @@ def test_zigzag_varlen_equals_per_document(seq_len, docs, world):
     check_ring(world, half, cu=cu)
 
 
+def check_contiguous(world, L, *, causal=True, hq=4, hkv=4, cu=None, fwd=None, bwd=None,
+                     tol=1e-5):
+    """An emulated contiguous ring (p2p or DistFlash restatement) equals full (doc-)causal
+    or full non-causal attention, values and grads."""
+    fwd = fwd or (lambda *a, **kw: rm.contiguous_ring_forward(*a, causal=causal, **kw))
+    bwd = bwd or (lambda *a, **kw: rm.contiguous_ring_backward(*a, causal=causal, **kw))
+    S = world * L
+    q, k, v = rnd(1, S, hq, 8, seed=1), rnd(1, S, hkv, 8, seed=2), rnd(1, S, hkv, 8, seed=3)
+    dout = rnd(1, S, hq, 8, seed=4)
+    idx = [rm.contiguous_gidx(r, L) for r in range(world)]
+    shard = lambda t: [t[:, i].transpose(1, 2).contiguous() for i in idx]  # noqa: E731
+    outs, lses = fwd(shard(q), shard(k), shard(v), cu_seqlens=cu)
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    ref, ref_lse = rm.full_attention(qr, kr, vr, causal=causal, cu_seqlens=cu)
+    ref.backward(dout)
+    err = 0.0
+    for r in range(world):
+        err = max(err, (outs[r].double() - ref.detach()[:, idx[r]]).abs().max().item())
+        err = max(err, (lses[r].double() - ref_lse.detach()[:, :, idx[r]]).abs().max().item())
+    dqs, dks, dvs = bwd([dout[:, i] for i in idx], shard(q), shard(k), shard(v), outs, lses,
+                        cu_seqlens=cu)
+    for r in range(world):
+        err = max(err, (dqs[r].double() - qr.grad[:, idx[r]].transpose(1, 2)).abs().max().item())
+        err = max(err, (dks[r].double() - kr.grad[:, idx[r]].transpose(1, 2)).abs().max().item())
+        err = max(err, (dvs[r].double() - vr.grad[:, idx[r]].transpose(1, 2)).abs().max().item())
+    assert err < tol, f"contiguous ring vs full attention err {err}"
+
+
+@pytest.mark.parametrize("world", [1, 2, 3, 4])
+@pytest.mark.parametrize("causal", [True, False])
+def test_contiguous_ring_equals_full(world, causal):
+    check_contiguous(world, 5, causal=causal)
+
+
+def test_contiguous_ring_gqa():
+    check_contiguous(4, 4, hq=4, hkv=2)
+
+
+@pytest.mark.parametrize("docs,world", [([6, 10], 2), ([10, 9, 13], 4), ([3, 3, 6, 4, 8], 4)])
+def test_contiguous_varlen_equals_per_document(docs, world):
+    cu = torch.tensor([0, *torch.tensor(docs).cumsum(0).tolist()], dtype=torch.int32)
+    check_contiguous(world, sum(docs) // world, cu=cu)
+
+
+@pytest.mark.parametrize("world", [1, 2, 3, 4, 5])
+def test_distflash_equals_full_causal(world):
+    check_contiguous(world, 4, fwd=rm.distflash_forward, bwd=rm.distflash_backward)
+
+
+def test_distflash_varlen_and_gqa():
+    cu = torch.tensor([0, 7, 9, 20, 24], dtype=torch.int32)
+    check_contiguous(4, 6, hq=4, hkv=2, cu=cu, fwd=rm.distflash_forward,
+                     bwd=rm.distflash_backward)
+
+
 def test_full_attention_per_doc_equals_sdpa_per_doc():
     docs = [5, 7, 4]
     cu = torch.tensor([0, 5, 12, 16])

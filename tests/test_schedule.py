@@ -5,7 +5,8 @@ import pytest
 import torch
 
 from ringmaster_amd.balancers import contiguous_indices, head_tail_indices
-from ringmaster_amd.ring.schedule import ring_pairs_per_rank, zigzag_gidx, zigzag_schedule
+from ringmaster_amd.ring.schedule import (contiguous_gidx, contiguous_schedule, distflash_work,
+                                          ring_pairs_per_rank, zigzag_gidx, zigzag_schedule)
 
 
 def coverage(world, L, split_final):
@@ -80,3 +81,41 @@ def test_balancer_literals(golden):
     g = golden["head_tail_global_positions"]
     half = g["local_len"] // 2
     assert zigzag_gidx(g["cp_rank"], half, g["cp_size"]) == g["expected"]
+
+
+@pytest.mark.parametrize("world,L", [(1, 5), (2, 4), (4, 3), (8, 2), (5, 3)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_contiguous_schedule_covers_each_pair_once(world, L, causal):
+    S = world * L
+    cnt = torch.zeros(S, S, dtype=torch.int32)
+    last = {}
+    for s, blocks in enumerate(contiguous_schedule(world, L, causal=causal)):
+        assert sorted(b.kv_rank for b in blocks) == sorted({b.kv_rank for b in blocks})
+        for bl in blocks:
+            assert bl.kv_rank == (bl.rank - s) % world and bl.first == (s == 0)
+            qg = torch.tensor(contiguous_gidx(bl.rank, L))
+            kg = torch.tensor(contiguous_gidx(bl.kv_rank, L))
+            allow = torch.ones(L, L, dtype=torch.bool)
+            if bl.causal:
+                allow = allow.tril()
+            if causal:
+                assert bool((kg.unsqueeze(0) <= qg.unsqueeze(1))[allow].all())
+            cnt[qg.unsqueeze(1).expand(L, L)[allow], kg.unsqueeze(0).expand(L, L)[allow]] += 1
+            if bl.last:
+                assert bl.rank not in last
+                last[bl.rank] = s
+    full = torch.ones(S, S, dtype=torch.int32)
+    assert torch.equal(cnt, full.tril() if causal else full)
+    assert last == {r: (r if causal else world - 1) for r in range(world)}
+
+
+def test_distflash_balance_literals():
+    # ring/distflash.py:15: "P=4 -> 3,3,2,2 vs ring's 1,2,3,4"
+    assert distflash_work(4) == [3, 3, 2, 2]
+    ring = [sum(1 for blocks in contiguous_schedule(4, 1, causal=True) for b in blocks
+                if b.rank == r) for r in range(4)]
+    assert ring == [1, 2, 3, 4]
+    for world in range(1, 10):
+        work = distflash_work(world)
+        assert sum(work) == world * (world + 1) // 2  # every causal block exactly once
+        assert max(work) - min(work) <= 1
