@@ -108,6 +108,30 @@ def ring_workload(steps, warmup):
             "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2)}
 
 
+def distflash_workload(steps, warmup):
+    """The DistFlash (contiguous, load-balanced causal) ring at the configs[2] shape: P=8,
+    S=131072 (16384 contiguous tokens per rank), H=16, D=128, bf16, fwd+bwd. Same attended
+    pairs as the zigzag ring; on one GPU step d runs the blocks (i, i - d), i >= d."""
+    from ringmaster_amd.ring import distflash_attention
+
+    P, S, H, D = 8, 131072, 16, 128
+    L = S // P
+    q = _gen((P, 1, H, L, D), 1).requires_grad_(True)
+    k = _gen((P, 1, H, L, D), 2).requires_grad_(True)
+    v = _gen((P, 1, H, L, D), 3).requires_grad_(True)
+    dout = _gen((P, 1, L, H, D), 4)
+    flops = 14 * D * H * (S * (S + 1) // 2)
+
+    def step():
+        out = distflash_attention(q, k, v, scaling=None)
+        torch.autograd.grad(out, (q, k, v), dout)
+
+    ms = _time(step, steps, warmup)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 3), "flops": flops, "TFLOP/s": round(tf, 1),
+            "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
 def varlen_docs(total, seed=5, median=2048, sigma=1.0, lo=128, hi=16384):
     """configs[3] document lengths: clip(round(exp(ln median + sigma z)), lo, hi), z ~ N(0, 1)
     from ``seed``, drawn until they cover ``total``; the last one is cut to the remainder."""
@@ -234,6 +258,33 @@ def mamba_workload(steps, warmup):
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"ms": round(ms, 4), "bytes": nbytes, "GB/s": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def conv_workload(steps, warmup):
+    """configs[4] Mamba2 CP causal conv1d with the halo, fwd and bwd: 8 shards of 8192
+    tokens, conv channels = nheads * headdim + 2 * ngroups * d_state = 4352, width 4,
+    silu, bias. Algorithmic bytes: fwd reads x and writes y (bf16); bwd reads x and dy
+    and writes dx (the weight / bias gradients are 4352 x 5 floats)."""
+    from ringmaster_amd.strategies.mamba import causal_conv1d_cp
+
+    P, T, C, W = 8, 8192, 64 * 64 + 2 * 128, 4
+    x = _gen((P, 1, C, T), 14).requires_grad_(True)
+    w = _gen((C, W), 15, scale=0.5).requires_grad_(True)
+    b = _gen((C,), 16).requires_grad_(True)
+    dy = _gen((P, 1, C, T), 17)
+    fwd_ms = _time(lambda: causal_conv1d_cp(x, w, b, "silu"), steps, warmup)
+    y = causal_conv1d_cp(x, w, b, "silu")
+    tot_ms = _time(lambda: torch.autograd.grad(causal_conv1d_cp(x, w, b, "silu"), (x, w, b), dy),
+                   steps, warmup)
+    bwd_ms = tot_ms - fwd_ms
+    n = x.numel() * 2
+    fwd_bytes, bwd_bytes = 2 * n, 3 * n
+    return {"fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+            "bytes": fwd_bytes + bwd_bytes,
+            "GB/s": round((fwd_bytes + bwd_bytes) / (tot_ms * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round((fwd_bytes + bwd_bytes) / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "fwd_GB/s": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9, 1),
+            "bwd_GB/s": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1)}
 
 
 def mamba_bwd_workload(steps, warmup):
@@ -437,9 +488,13 @@ def main():
         torch.cuda.empty_cache()
         extras["mamba2_correction_bwd_configs4"] = mamba_bwd_workload(20, 3)
         torch.cuda.empty_cache()
+        extras["mamba2_conv_cp_configs4"] = conv_workload(20, 3)
+        torch.cuda.empty_cache()
         extras["block_configs1"] = block_workload(3, 1)
         torch.cuda.empty_cache()
         extras["varlen_configs3"] = varlen_workload(3, 1)
+        torch.cuda.empty_cache()
+        extras["distflash_configs2_shape"] = distflash_workload(2, 1)
         torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_heads)
 

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 4  /* 3: Mamba2 correction backward entry points; 4: nlse */
+#define RMX_ABI_VERSION 5  /* 3: Mamba2 correction backward; 4: nlse; 5: CP causal conv1d */
 
 /* error codes */
 #define RMX_OK 0
@@ -258,6 +258,38 @@ int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const
                                      float* g_hprev, void* workspace, size_t workspace_bytes,
                                      int32_t batch, int32_t T, int32_t nheads, int32_t head_dim,
                                      int32_t ngroups, int32_t d_state, void* stream);
+
+/*
+ * Mamba2 context-parallel causal conv1d with the halo (mamba.py:46-101, the conv
+ * hook of the reference's Mamba2 adapter): the depthwise causal conv of every
+ * rank's shard, where shard r's first width-1 outputs read the last width-1
+ * tokens of shard r-1 (the all-gathered halo; zeros for r = 0). doc (nullable,
+ * int32 [batch, world * local_len], doc_ids_from_cu(cu_seqlens)): taps from
+ * another document contribute zero (the reference's per-document segments and
+ * halo mask). y[g] = act(bias + sum_i w[i] x[g - (width-1) + i]) with
+ * causal_conv1d_fn's semantics; activation 0 = none, 1 = silu.
+ * x, y: bf16 [world, batch, channels, local_len] (each shard channels-first, the
+ * layout causal_conv1d_fn takes), contiguous, 16-byte aligned; weight bf16
+ * [channels, width]; bias bf16 [channels] (nullable). local_len % 8 == 0,
+ * 1 <= width <= 9.
+ */
+int32_t rmx_causal_conv1d_cp(const uint16_t* x, const uint16_t* weight, const uint16_t* bias,
+                             const int32_t* doc, uint16_t* y, int32_t world, int32_t batch,
+                             int32_t channels, int32_t local_len, int32_t width,
+                             int32_t activation, void* stream);
+
+/*
+ * Backward of rmx_causal_conv1d_cp (what autograd through the reference's halo
+ * all-gather and per-shard convolutions computes): writes dx (bf16, like x; the
+ * halo's gradient lands on the previous shard's last tokens) and ADDS the fp32
+ * dweight [channels, width] and dbias [channels] (nullable) sums (caller
+ * zero-fills them).
+ */
+int32_t rmx_causal_conv1d_cp_bwd(const uint16_t* x, const uint16_t* weight, const uint16_t* bias,
+                                 const int32_t* doc, const uint16_t* dy, uint16_t* dx,
+                                 float* dweight, float* dbias, int32_t world, int32_t batch,
+                                 int32_t channels, int32_t local_len, int32_t width,
+                                 int32_t activation, void* stream);
 
 #ifdef __cplusplus
 }

@@ -379,4 +379,52 @@ int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const
                     "rmx_mamba2_cp_correction_bwd launch");
 }
 
+static int check_conv(const uint16_t* x, const uint16_t* weight, const uint16_t* bias,
+                      const void* y, int32_t world, int32_t batch, int32_t channels,
+                      int32_t local_len, int32_t width, int32_t activation) {
+  if (world < 1) return fail(RMX_EINVAL, "world must be positive (got %d)", world);
+  if (batch < 0 || channels < 0 || local_len < 0)
+    return fail(RMX_EINVAL, "negative batch, channels or length");
+  if (width < 1 || width > 9)
+    return fail(RMX_EUNSUPPORTED, "convolution width %d outside 1..9", width);
+  if (local_len % 8)
+    return fail(RMX_EUNSUPPORTED, "local length %d is not a multiple of 8", local_len);
+  if (activation != 0 && activation != 1)
+    return fail(RMX_EINVAL, "unknown activation %d (0 none, 1 silu)", activation);
+  if ((int64_t)batch * channels * local_len == 0) return RMX_OK;
+  if (!x || !weight || !y) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!aligned(x, 16) || !aligned(y, 16)) return fail(RMX_EINVAL, "x and outputs must be 16-byte aligned");
+  if (!aligned(weight, 2) || (bias && !aligned(bias, 2)))
+    return fail(RMX_EINVAL, "weight and bias must be 2-byte aligned");
+  return RMX_OK;
+}
+
+int32_t rmx_causal_conv1d_cp(const uint16_t* x, const uint16_t* weight, const uint16_t* bias,
+                             const int32_t* doc, uint16_t* y, int32_t world, int32_t batch,
+                             int32_t channels, int32_t local_len, int32_t width,
+                             int32_t activation, void* stream) {
+  int rc = check_conv(x, weight, bias, y, world, batch, channels, local_len, width, activation);
+  if (rc) return rc;
+  if ((int64_t)batch * channels * local_len == 0) return RMX_OK;
+  return dev_status(rmx::launch_causal_conv1d_cp(x, weight, bias, doc, y, world, batch, channels,
+                                                 local_len, width, activation, (hipStream_t)stream),
+                    "rmx_causal_conv1d_cp launch");
+}
+
+int32_t rmx_causal_conv1d_cp_bwd(const uint16_t* x, const uint16_t* weight, const uint16_t* bias,
+                                 const int32_t* doc, const uint16_t* dy, uint16_t* dx,
+                                 float* dweight, float* dbias, int32_t world, int32_t batch,
+                                 int32_t channels, int32_t local_len, int32_t width,
+                                 int32_t activation, void* stream) {
+  int rc = check_conv(x, weight, bias, dx, world, batch, channels, local_len, width, activation);
+  if (rc) return rc;
+  if ((int64_t)batch * channels * local_len == 0) return RMX_OK;
+  if (!dy || !dweight) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!aligned(dy, 16)) return fail(RMX_EINVAL, "dy must be 16-byte aligned");
+  return dev_status(rmx::launch_causal_conv1d_cp_bwd(x, weight, bias, doc, dy, dx, dweight, dbias,
+                                                     world, batch, channels, local_len, width,
+                                                     activation, (hipStream_t)stream),
+                    "rmx_causal_conv1d_cp_bwd launch");
+}
+
 }  // extern "C"

@@ -1,0 +1,254 @@
+// Depthwise causal conv1d over the P contiguous shards of one sequence, with the
+// context-parallel halo of the reference's Mamba2 conv adapter (mamba.py:46-101):
+// shard r's first W-1 outputs read the last W-1 tokens of shard r-1 (the
+// all-gathered halo; zeros for r = 0), and for packed sequences a tap from
+// another document contributes nothing (the reference splits each shard at
+// document boundaries and masks the halo by document). On the global sequence:
+//   z[g] = bias + sum_{i<W} w[i] x[g - (W-1) + i] [doc(g - (W-1) + i) == doc(g)]
+//   y[g] = act(z[g]),  act = identity or silu
+// (causal_conv1d_fn's published semantics: a depthwise conv1d with W-1 zeros of
+// left padding). HBM-bound: one thread owns 8 consecutive tokens of one
+// (shard, batch, channel) row and reads them and the 8 before as 16-byte loads.
+#include "rmx_kernels.h"
+
+namespace rmx {
+
+struct ConvArgs {
+  const uint16_t* x;
+  const uint16_t* w;
+  const uint16_t* bias;  // nullable
+  const int32_t* doc;    // nullable, [batch, world * L]
+  const uint16_t* dy;    // backward
+  uint16_t* y;           // forward output / backward dx
+  float* dw;             // backward: += dL/dw  [C, W]
+  float* db;             // backward: += dL/dbias [C] (nullable)
+  int world, batch, C, L, W, act;
+};
+
+__device__ __forceinline__ void load8(const uint16_t* p, float* o) {
+  const u32x4 u = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __uint_as_float(u[i] << 16);
+    o[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ float silu(float z) { return z / (1.f + __expf(-z)); }
+// d silu / dz = s (1 + z (1 - s)), s = sigmoid(z)
+__device__ __forceinline__ float dsilu(float z) {
+  const float s = 1.f / (1.f + __expf(-z));
+  return s * (1.f + z * (1.f - s));
+}
+
+// Row `row` = (p * batch + b) * C + c; run j covers local tokens [8j, 8j + 8).
+struct ConvRun {
+  int p, b, c, t0;
+  int64_t rowoff;  // element offset of the row
+};
+
+__device__ __forceinline__ ConvRun conv_run(const ConvArgs& a, int64_t idx) {
+  const int nr = a.L / 8;
+  ConvRun r;
+  const int64_t row = idx / nr;
+  r.t0 = (int)(idx - row * nr) * 8;
+  r.c = (int)(row % a.C);
+  const int64_t pb = row / a.C;
+  r.b = (int)(pb % a.batch);
+  r.p = (int)(pb / a.batch);
+  r.rowoff = row * a.L;
+  return r;
+}
+
+// 8 tokens at local offset t of the chunk `dir` chunks away from the run (dir = -1
+// previous, 0 current, +1 next), crossing into the neighbouring shard when needed;
+// zeros outside the sequence. Also their global positions' document ids.
+__device__ __forceinline__ void chunk(const ConvArgs& a, const uint16_t* base, const ConvRun& r,
+                                      int dir, float* v, int* d) {
+  int t = r.t0 + 8 * dir, p = r.p;
+  if (t < 0) {
+    t += a.L;
+    --p;
+  } else if (t >= a.L) {
+    t -= a.L;
+    ++p;
+  }
+  const bool in = p >= 0 && p < a.world;
+  if (in) {
+    // the same (batch, channel) row of shard p starts (p - r.p) * batch * C rows away
+    load8(base + r.rowoff + (int64_t)(p - r.p) * a.batch * a.C * a.L + t, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  }
+  if (a.doc) {
+    const int64_t g = (int64_t)p * a.L + t;
+    const int32_t* dp = a.doc + (int64_t)r.b * a.world * a.L + g;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d[i] = in ? dp[i] : -1 - i;  // outside: matches nothing
+  }
+}
+
+template <int W>
+__global__ __launch_bounds__(256) void causal_conv1d_fwd_kernel(const ConvArgs a) {
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)a.world * a.batch * a.C * (a.L / 8)) return;
+  const ConvRun r = conv_run(a, idx);
+  float xv[16];
+  int dv[16];
+  chunk(a, a.x, r, -1, xv, dv);
+  chunk(a, a.x, r, 0, xv + 8, dv + 8);
+  float w[W];
+#pragma unroll
+  for (int i = 0; i < W; ++i) w[i] = bf2f(a.w[r.c * W + i]);
+  const float bias = a.bias ? bf2f(a.bias[r.c]) : 0.f;
+  float y[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float z = bias;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      const int s = 8 + k - (W - 1) + i;  // tap position in xv
+      const bool ok = !a.doc || dv[s] == dv[8 + k];
+      z += ok ? w[i] * xv[s] : 0.f;
+    }
+    y[k] = a.act ? silu(z) : z;
+  }
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = pack_bf2(y[2 * i], y[2 * i + 1]);
+  *reinterpret_cast<u32x4*>(a.y + r.rowoff + r.t0) = o;
+}
+
+// dz[g] = dy[g] act'(z[g]);  dx[g'] = sum_i w[i] dz[g' + W-1 - i] [same doc];
+// dw[i] += sum_g dz[g] x[g - (W-1) + i] [same doc];  db += sum_g dz[g].
+// A thread owns dx and the dw/db terms of its 8 tokens; dz of the next W-1
+// tokens (next chunk, possibly the next shard's) is recomputed.
+template <int W>
+__global__ __launch_bounds__(256) void causal_conv1d_bwd_kernel(const ConvArgs a) {
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)a.world * a.batch * a.C * (a.L / 8);
+  const bool valid = idx < total;
+  const ConvRun r = conv_run(a, valid ? idx : 0);
+  float w[W];
+#pragma unroll
+  for (int i = 0; i < W; ++i) w[i] = bf2f(a.w[r.c * W + i]);
+  const float bias = a.bias ? bf2f(a.bias[r.c]) : 0.f;
+  float pw[W], pb = 0.f;
+#pragma unroll
+  for (int i = 0; i < W; ++i) pw[i] = 0.f;
+  if (valid) {
+    float xv[24], gv[16];
+    int dv[24];
+    chunk(a, a.x, r, -1, xv, dv);
+    chunk(a, a.x, r, 0, xv + 8, dv + 8);
+    chunk(a, a.x, r, 1, xv + 16, dv + 16);
+    chunk(a, a.dy, r, 0, gv, dv + 8);
+    chunk(a, a.dy, r, 1, gv + 8, dv + 16);
+    // dz of the run's 8 tokens and of the next W-1
+    float dz[8 + W - 1];
+#pragma unroll
+    for (int k = 0; k < 8 + W - 1; ++k) {
+      float z = bias;
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        const int s = 8 + k - (W - 1) + i;
+        const bool ok = !a.doc || dv[s] == dv[8 + k];
+        z += ok ? w[i] * xv[s] : 0.f;
+      }
+      dz[k] = gv[k] * (a.act ? dsilu(z) : 1.f);
+    }
+    float dx[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        const int o = k + (W - 1) - i;  // output that reads token k through tap i
+        const bool ok = !a.doc || dv[8 + o] == dv[8 + k];
+        acc += ok ? w[i] * dz[o] : 0.f;
+      }
+      dx[k] = acc;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      pb += dz[k];
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        const int s = 8 + k - (W - 1) + i;
+        const bool ok = !a.doc || dv[s] == dv[8 + k];
+        pw[i] += ok ? dz[k] * xv[s] : 0.f;
+      }
+    }
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pack_bf2(dx[2 * i], dx[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(a.y + r.rowoff + r.t0) = o;
+  }
+  // dw / db: one atomic per wave when the whole wave works on one channel
+  const int lane = threadIdx.x & 63;
+  const int c0 = __shfl(valid ? r.c : -1, 0, 64);
+  const bool uniform = __all(valid && r.c == c0);
+  if (uniform) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      pb += __shfl_xor(pb, m, 64);
+#pragma unroll
+      for (int i = 0; i < W; ++i) pw[i] += __shfl_xor(pw[i], m, 64);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < W; ++i) atomicAdd(a.dw + c0 * W + i, pw[i]);
+      if (a.db) atomicAdd(a.db + c0, pb);
+    }
+  } else if (valid) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) atomicAdd(a.dw + r.c * W + i, pw[i]);
+    if (a.db) atomicAdd(a.db + r.c, pb);
+  }
+}
+
+static hipError_t launch_conv(const ConvArgs& a, hipStream_t stream, bool bwd) {
+  const int64_t n = (int64_t)a.world * a.batch * a.C * (a.L / 8);
+  if (n == 0) return hipSuccess;
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  switch (a.W) {
+#define RMX_CONV_CASE(w)                                                            \
+  case w:                                                                          \
+    if (bwd)                                                                       \
+      hipLaunchKernelGGL(causal_conv1d_bwd_kernel<w>, grid, block, 0, stream, a); \
+    else                                                                           \
+      hipLaunchKernelGGL(causal_conv1d_fwd_kernel<w>, grid, block, 0, stream, a); \
+    break;
+    RMX_CONV_CASE(1)
+    RMX_CONV_CASE(2)
+    RMX_CONV_CASE(3)
+    RMX_CONV_CASE(4)
+    RMX_CONV_CASE(5)
+    RMX_CONV_CASE(6)
+    RMX_CONV_CASE(7)
+    RMX_CONV_CASE(8)
+    RMX_CONV_CASE(9)
+#undef RMX_CONV_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_causal_conv1d_cp(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                   const int32_t* doc, uint16_t* y, int world, int batch, int C,
+                                   int L, int W, int act, hipStream_t stream) {
+  const ConvArgs a{x, w, bias, doc, nullptr, y, nullptr, nullptr, world, batch, C, L, W, act};
+  return launch_conv(a, stream, false);
+}
+
+hipError_t launch_causal_conv1d_cp_bwd(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                       const int32_t* doc, const uint16_t* dy, uint16_t* dx,
+                                       float* dw, float* db, int world, int batch, int C, int L,
+                                       int W, int act, hipStream_t stream) {
+  const ConvArgs a{x, w, bias, doc, dy, dx, dw, db, world, batch, C, L, W, act};
+  return launch_conv(a, stream, true);
+}
+
+}  // namespace rmx

@@ -41,6 +41,13 @@ hipError_t launch_mamba2_correction_bwd(const uint16_t* gy, const float* ghf, co
                                         float* g_hprev, void* workspace, int batch, int T,
                                         int nheads, int head_dim, int ngroups, int d_state,
                                         hipStream_t stream);
+hipError_t launch_causal_conv1d_cp(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                   const int32_t* doc, uint16_t* y, int world, int batch, int C,
+                                   int L, int W, int act, hipStream_t stream);
+hipError_t launch_causal_conv1d_cp_bwd(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                       const int32_t* doc, const uint16_t* dy, uint16_t* dx,
+                                       float* dw, float* db, int world, int batch, int C, int L,
+                                       int W, int act, hipStream_t stream);
 
 }  // namespace rmx
 

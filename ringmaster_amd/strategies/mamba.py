@@ -156,3 +156,79 @@ def mamba2_cp_correction(out: torch.Tensor, h_final: torch.Tensor, C: torch.Tens
         Bsz, T, _ = out.shape
         _bwd_workspace_bytes(Bsz, T, num_heads, head_dim, C.shape[2], C.shape[3])
     return _Correction.apply(out, h_final, C, cum_A, h_prev, num_heads, head_dim, sid)
+
+
+# ---------------------------------------------------------------- CP causal conv1d
+_ACTIVATIONS = {None: 0, "silu": 1, "swish": 1}
+
+
+class _CausalConv1dCP(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias, doc, act):
+        y = torch.empty_like(x)
+        P, B, C, L = x.shape
+        abi.check(abi.lib().rmx_causal_conv1d_cp(
+            x.data_ptr(), weight.data_ptr(), abi.ptr(bias), abi.ptr(doc), y.data_ptr(),
+            P, B, C, L, weight.shape[1], act, abi.stream_of(x)))
+        ctx.save_for_backward(x, weight, bias, doc)
+        ctx.act = act
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight, bias, doc = ctx.saved_tensors
+        P, B, C, L = x.shape
+        dy = dy.contiguous()
+        dx = torch.empty_like(x)
+        dw = torch.zeros(weight.shape, dtype=torch.float32, device=x.device)
+        db = torch.zeros(C, dtype=torch.float32, device=x.device) if bias is not None else None
+        abi.check(abi.lib().rmx_causal_conv1d_cp_bwd(
+            x.data_ptr(), weight.data_ptr(), abi.ptr(bias), abi.ptr(doc), dy.data_ptr(),
+            dx.data_ptr(), dw.data_ptr(), abi.ptr(db), P, B, C, L, weight.shape[1], ctx.act,
+            abi.stream_of(x)))
+        return (dx, dw.to(weight.dtype), None if db is None else db.to(bias.dtype), None, None)
+
+
+def causal_conv1d_cp(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                     activation: str | None = None, cu_seqlens: torch.Tensor | None = None):
+    """The Mamba2 CP convolution of the reference adapter (mamba.py:46-101) for every
+    rank at once: ``x`` bf16 ``[world, batch, channels, local_len]`` (each rank's
+    channels-first shard, as ``causal_conv1d_fn`` takes it), ``weight`` ``[channels,
+    width]`` (or ``[channels, 1, width]``), ``bias`` ``[channels]`` or None, ``activation``
+    None / "silu" / "swish". Shard r's first width-1 outputs read shard r-1's last tokens
+    (the halo; zeros for rank 0); with ``cu_seqlens`` taps never cross a document
+    boundary. Differentiable in x, weight and bias. Returns ``[world, batch, channels,
+    local_len]``."""
+    abi.require_device(x, weight)
+    if weight.dim() == 3 and weight.shape[1] == 1:
+        weight = weight[:, 0]
+    if x.dim() != 4 or weight.dim() != 2 or weight.shape[0] != x.shape[2]:
+        raise ValueError("x must be [world, batch, channels, len] and weight [channels, width]")
+    if bias is not None and bias.shape != (x.shape[2],):
+        raise ValueError("bias must be [channels]")
+    if activation not in _ACTIVATIONS:
+        raise NotImplementedError(f"activation {activation!r}")
+    width = weight.shape[1] - 1
+    if x.shape[3] < width:
+        raise ValueError("Mamba CP shards must be at least convolution width - 1 tokens")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or (
+            bias is not None and bias.dtype != torch.bfloat16):
+        raise NotImplementedError("the MI355X conv computes bf16 tensors")
+    doc = None
+    if cu_seqlens is not None:
+        from ringmaster_amd.ring.zigzag import doc_ids_from_cu
+
+        # the reference reshapes the ids of the packed batch to [batch, world * len]
+        doc = doc_ids_from_cu(cu_seqlens, x.device)
+        n = x.shape[0] * x.shape[3]
+        if doc.numel() == x.shape[1] * n:
+            doc = doc.reshape(x.shape[1], n)
+        elif doc.numel() == n:
+            doc = doc.reshape(1, n).expand(x.shape[1], n)
+        else:
+            raise ValueError("cu_seqlens must cover the full (padded) sequence")
+        doc = doc.contiguous()
+    x = x.contiguous()
+    weight = weight.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    return _CausalConv1dCP.apply(x, weight, bias, doc, _ACTIVATIONS[activation])
