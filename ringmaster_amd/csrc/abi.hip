@@ -392,6 +392,8 @@ static int check_conv(const uint16_t* x, const uint16_t* weight, const uint16_t*
   if (activation != 0 && activation != 1)
     return fail(RMX_EINVAL, "unknown activation %d (0 none, 1 silu)", activation);
   if ((int64_t)batch * channels * local_len == 0) return RMX_OK;
+  if ((int64_t)world * batch * channels * ((local_len / 8 + 255) / 256) > 2147483647LL)
+    return fail(RMX_EUNSUPPORTED, "conv grid of more than 2^31 workgroups");
   if (!x || !weight || !y) return fail(RMX_EINVAL, "NULL tensor pointer");
   if (!aligned(x, 16) || !aligned(y, 16)) return fail(RMX_EINVAL, "x and outputs must be 16-byte aligned");
   if (!aligned(weight, 2) || (bias && !aligned(bias, 2)))

@@ -8,7 +8,9 @@
 //   y[g] = act(z[g]),  act = identity or silu
 // (causal_conv1d_fn's published semantics: a depthwise conv1d with W-1 zeros of
 // left padding). HBM-bound: one thread owns 8 consecutive tokens of one
-// (shard, batch, channel) row and reads them and the 8 before as 16-byte loads.
+// (shard, batch, channel) row and reads them and the 8 before as 16-byte loads;
+// a workgroup covers 256 runs of one row, so the row's coordinates, weights and
+// bias are scalar.
 #include "rmx_kernels.h"
 
 namespace rmx {
@@ -34,70 +36,79 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* o) {
   }
 }
 
-__device__ __forceinline__ float silu(float z) { return z / (1.f + __expf(-z)); }
+// sigmoid with the hardware reciprocal (1 ulp): the outputs are bf16
+__device__ __forceinline__ float sigm(float z) {
+  return __builtin_amdgcn_rcpf(1.f + fast_exp2(-z * kLog2e));
+}
+__device__ __forceinline__ float silu(float z) { return z * sigm(z); }
 // d silu / dz = s (1 + z (1 - s)), s = sigmoid(z)
 __device__ __forceinline__ float dsilu(float z) {
-  const float s = 1.f / (1.f + __expf(-z));
+  const float s = sigm(z);
   return s * (1.f + z * (1.f - s));
 }
 
 // Row `row` = (p * batch + b) * C + c; run j covers local tokens [8j, 8j + 8).
+// Workgroup w covers runs [256 (w % bpr), 256 (w % bpr) + 256) of row w / bpr,
+// bpr = ceil(L / 8 / 256): row, p, b and c are workgroup-uniform.
 struct ConvRun {
   int p, b, c, t0;
   int64_t rowoff;  // element offset of the row
+  bool valid;
 };
 
-__device__ __forceinline__ ConvRun conv_run(const ConvArgs& a, int64_t idx) {
+__device__ __forceinline__ ConvRun conv_run(const ConvArgs& a) {
   const int nr = a.L / 8;
+  const int bpr = (nr + 255) / 256;
+  const int row = blockIdx.x / bpr;
+  const int j = (blockIdx.x - row * bpr) * 256 + threadIdx.x;
   ConvRun r;
-  const int64_t row = idx / nr;
-  r.t0 = (int)(idx - row * nr) * 8;
-  r.c = (int)(row % a.C);
-  const int64_t pb = row / a.C;
-  r.b = (int)(pb % a.batch);
-  r.p = (int)(pb / a.batch);
-  r.rowoff = row * a.L;
+  r.valid = j < nr;
+  r.t0 = (r.valid ? j : 0) * 8;
+  r.c = row % a.C;
+  const int pb = row / a.C;
+  r.b = pb % a.batch;
+  r.p = pb / a.batch;
+  r.rowoff = (int64_t)row * a.L;
   return r;
 }
 
-// 8 tokens at local offset t of the chunk `dir` chunks away from the run (dir = -1
-// previous, 0 current, +1 next), crossing into the neighbouring shard when needed;
-// zeros outside the sequence. Also their global positions' document ids.
+// 8 tokens of the chunk `dir` chunks away from the run (dir = -1 previous, 0
+// current, +1 next), crossing into the neighbouring shard when needed; zeros
+// outside the sequence. Also the document ids of those positions (outside: ids
+// that match nothing). Branch-free: an outside read is redirected to the run's
+// own chunk and its values are replaced by zeros.
+template <bool DOC>
 __device__ __forceinline__ void chunk(const ConvArgs& a, const uint16_t* base, const ConvRun& r,
                                       int dir, float* v, int* d) {
   int t = r.t0 + 8 * dir, p = r.p;
-  if (t < 0) {
-    t += a.L;
-    --p;
-  } else if (t >= a.L) {
-    t -= a.L;
-    ++p;
-  }
+  t = t < 0 ? t + a.L : (t >= a.L ? t - a.L : t);
+  p = r.t0 + 8 * dir < 0 ? p - 1 : (r.t0 + 8 * dir >= a.L ? p + 1 : p);
   const bool in = p >= 0 && p < a.world;
-  if (in) {
-    // the same (batch, channel) row of shard p starts (p - r.p) * batch * C rows away
-    load8(base + r.rowoff + (int64_t)(p - r.p) * a.batch * a.C * a.L + t, v);
-  } else {
+  const int pc = in ? p : r.p, tc = in ? t : r.t0;
+  // the same (batch, channel) row of shard pc starts (pc - r.p) * batch * C rows away
+  load8(base + r.rowoff + (int64_t)(pc - r.p) * a.batch * a.C * a.L + tc, v);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.f;
-  }
-  if (a.doc) {
-    const int64_t g = (int64_t)p * a.L + t;
-    const int32_t* dp = a.doc + (int64_t)r.b * a.world * a.L + g;
+  for (int i = 0; i < 8; ++i) v[i] = in ? v[i] : 0.f;
+  if (DOC) {
+    const int32_t* dp = a.doc + (int64_t)r.b * a.world * a.L + (int64_t)pc * a.L + tc;
+    const i32x4 d0 = *reinterpret_cast<const i32x4*>(dp);
+    const i32x4 d1 = *reinterpret_cast<const i32x4*>(dp + 4);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) d[i] = in ? dp[i] : -1 - i;  // outside: matches nothing
+    for (int i = 0; i < 4; ++i) {
+      d[i] = in ? d0[i] : -1 - i;
+      d[4 + i] = in ? d1[i] : -5 - i;
+    }
   }
 }
 
-template <int W>
+template <int W, bool DOC>
 __global__ __launch_bounds__(256) void causal_conv1d_fwd_kernel(const ConvArgs a) {
-  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)a.world * a.batch * a.C * (a.L / 8)) return;
-  const ConvRun r = conv_run(a, idx);
+  const ConvRun r = conv_run(a);
+  if (!r.valid) return;
   float xv[16];
   int dv[16];
-  chunk(a, a.x, r, -1, xv, dv);
-  chunk(a, a.x, r, 0, xv + 8, dv + 8);
+  chunk<DOC>(a, a.x, r, -1, xv, dv);
+  chunk<DOC>(a, a.x, r, 0, xv + 8, dv + 8);
   float w[W];
 #pragma unroll
   for (int i = 0; i < W; ++i) w[i] = bf2f(a.w[r.c * W + i]);
@@ -109,7 +120,7 @@ __global__ __launch_bounds__(256) void causal_conv1d_fwd_kernel(const ConvArgs a
 #pragma unroll
     for (int i = 0; i < W; ++i) {
       const int s = 8 + k - (W - 1) + i;  // tap position in xv
-      const bool ok = !a.doc || dv[s] == dv[8 + k];
+      const bool ok = !DOC || dv[s] == dv[8 + k];
       z += ok ? w[i] * xv[s] : 0.f;
     }
     y[k] = a.act ? silu(z) : z;
@@ -124,12 +135,10 @@ __global__ __launch_bounds__(256) void causal_conv1d_fwd_kernel(const ConvArgs a
 // dw[i] += sum_g dz[g] x[g - (W-1) + i] [same doc];  db += sum_g dz[g].
 // A thread owns dx and the dw/db terms of its 8 tokens; dz of the next W-1
 // tokens (next chunk, possibly the next shard's) is recomputed.
-template <int W>
+template <int W, bool DOC>
 __global__ __launch_bounds__(256) void causal_conv1d_bwd_kernel(const ConvArgs a) {
-  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)a.world * a.batch * a.C * (a.L / 8);
-  const bool valid = idx < total;
-  const ConvRun r = conv_run(a, valid ? idx : 0);
+  const ConvRun r = conv_run(a);
+  const bool valid = r.valid;
   float w[W];
 #pragma unroll
   for (int i = 0; i < W; ++i) w[i] = bf2f(a.w[r.c * W + i]);
@@ -140,11 +149,11 @@ __global__ __launch_bounds__(256) void causal_conv1d_bwd_kernel(const ConvArgs a
   if (valid) {
     float xv[24], gv[16];
     int dv[24];
-    chunk(a, a.x, r, -1, xv, dv);
-    chunk(a, a.x, r, 0, xv + 8, dv + 8);
-    chunk(a, a.x, r, 1, xv + 16, dv + 16);
-    chunk(a, a.dy, r, 0, gv, dv + 8);
-    chunk(a, a.dy, r, 1, gv + 8, dv + 16);
+    chunk<DOC>(a, a.x, r, -1, xv, dv);
+    chunk<DOC>(a, a.x, r, 0, xv + 8, dv + 8);
+    chunk<DOC>(a, a.x, r, 1, xv + 16, dv + 16);
+    chunk<false>(a, a.dy, r, 0, gv, dv + 8);
+    chunk<false>(a, a.dy, r, 1, gv + 8, dv + 16);
     // dz of the run's 8 tokens and of the next W-1
     float dz[8 + W - 1];
 #pragma unroll
@@ -153,7 +162,7 @@ __global__ __launch_bounds__(256) void causal_conv1d_bwd_kernel(const ConvArgs a
 #pragma unroll
       for (int i = 0; i < W; ++i) {
         const int s = 8 + k - (W - 1) + i;
-        const bool ok = !a.doc || dv[s] == dv[8 + k];
+        const bool ok = !DOC || dv[s] == dv[8 + k];
         z += ok ? w[i] * xv[s] : 0.f;
       }
       dz[k] = gv[k] * (a.act ? dsilu(z) : 1.f);
@@ -165,7 +174,7 @@ __global__ __launch_bounds__(256) void causal_conv1d_bwd_kernel(const ConvArgs a
 #pragma unroll
       for (int i = 0; i < W; ++i) {
         const int o = k + (W - 1) - i;  // output that reads token k through tap i
-        const bool ok = !a.doc || dv[8 + o] == dv[8 + k];
+        const bool ok = !DOC || dv[8 + o] == dv[8 + k];
         acc += ok ? w[i] * dz[o] : 0.f;
       }
       dx[k] = acc;
@@ -176,7 +185,7 @@ __global__ __launch_bounds__(256) void causal_conv1d_bwd_kernel(const ConvArgs a
 #pragma unroll
       for (int i = 0; i < W; ++i) {
         const int s = 8 + k - (W - 1) + i;
-        const bool ok = !a.doc || dv[s] == dv[8 + k];
+        const bool ok = !DOC || dv[s] == dv[8 + k];
         pw[i] += ok ? dz[k] * xv[s] : 0.f;
       }
     }
@@ -185,23 +194,15 @@ __global__ __launch_bounds__(256) void causal_conv1d_bwd_kernel(const ConvArgs a
     for (int i = 0; i < 4; ++i) o[i] = pack_bf2(dx[2 * i], dx[2 * i + 1]);
     *reinterpret_cast<u32x4*>(a.y + r.rowoff + r.t0) = o;
   }
-  // dw / db: one atomic per wave when the whole wave works on one channel
-  const int lane = threadIdx.x & 63;
-  const int c0 = __shfl(valid ? r.c : -1, 0, 64);
-  const bool uniform = __all(valid && r.c == c0);
-  if (uniform) {
+  // dw / db: the workgroup's runs share one channel; one atomic per wave
+  // (invalid lanes hold zeros)
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      pb += __shfl_xor(pb, m, 64);
+  for (int m = 32; m >= 1; m >>= 1) {
+    pb += __shfl_xor(pb, m, 64);
 #pragma unroll
-      for (int i = 0; i < W; ++i) pw[i] += __shfl_xor(pw[i], m, 64);
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int i = 0; i < W; ++i) atomicAdd(a.dw + c0 * W + i, pw[i]);
-      if (a.db) atomicAdd(a.db + c0, pb);
-    }
-  } else if (valid) {
+    for (int i = 0; i < W; ++i) pw[i] += __shfl_xor(pw[i], m, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
 #pragma unroll
     for (int i = 0; i < W; ++i) atomicAdd(a.dw + r.c * W + i, pw[i]);
     if (a.db) atomicAdd(a.db + r.c, pb);
@@ -209,16 +210,21 @@ __global__ __launch_bounds__(256) void causal_conv1d_bwd_kernel(const ConvArgs a
 }
 
 static hipError_t launch_conv(const ConvArgs& a, hipStream_t stream, bool bwd) {
-  const int64_t n = (int64_t)a.world * a.batch * a.C * (a.L / 8);
-  if (n == 0) return hipSuccess;
-  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  const int64_t rows = (int64_t)a.world * a.batch * a.C;
+  const int64_t bpr = (a.L / 8 + 255) / 256;
+  if (rows * bpr == 0) return hipSuccess;
+  const dim3 grid((unsigned)(rows * bpr)), block(256);
   switch (a.W) {
-#define RMX_CONV_CASE(w)                                                            \
-  case w:                                                                          \
-    if (bwd)                                                                       \
-      hipLaunchKernelGGL(causal_conv1d_bwd_kernel<w>, grid, block, 0, stream, a); \
-    else                                                                           \
-      hipLaunchKernelGGL(causal_conv1d_fwd_kernel<w>, grid, block, 0, stream, a); \
+#define RMX_CONV_CASE(w)                                                                     \
+  case w:                                                                                   \
+    if (bwd && a.doc)                                                                       \
+      hipLaunchKernelGGL((causal_conv1d_bwd_kernel<w, true>), grid, block, 0, stream, a);  \
+    else if (bwd)                                                                           \
+      hipLaunchKernelGGL((causal_conv1d_bwd_kernel<w, false>), grid, block, 0, stream, a); \
+    else if (a.doc)                                                                         \
+      hipLaunchKernelGGL((causal_conv1d_fwd_kernel<w, true>), grid, block, 0, stream, a);  \
+    else                                                                                    \
+      hipLaunchKernelGGL((causal_conv1d_fwd_kernel<w, false>), grid, block, 0, stream, a); \
     break;
     RMX_CONV_CASE(1)
     RMX_CONV_CASE(2)
