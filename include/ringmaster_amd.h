@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 5  /* 3: Mamba2 correction backward; 4: nlse; 5: CP causal conv1d */
+#define RMX_ABI_VERSION 6  /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum */
 
 /* error codes */
 #define RMX_OK 0
@@ -258,6 +258,32 @@ int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const
                                      float* g_hprev, void* workspace, size_t workspace_bytes,
                                      int32_t batch, int32_t T, int32_t nheads, int32_t head_dim,
                                      int32_t ngroups, int32_t d_state, void* stream);
+
+/*
+ * Mamba2 CP chunk decay from dt, the first step of the reference's CP scan
+ * wrapper (strategies/mamba.py:276-283): per row (rank shard x batch) and head,
+ *   e_t = softplus(dt_t + dt_bias) if dt_softplus else dt_t   (torch softplus,
+ *         threshold 20; dt_bias only with dt_softplus, as in the reference)
+ *   cum_A[r,t,h] = sum_{s<=t} A[h] e_s,   decay[r,h] = exp(cum_A[r,T-1,h])
+ * computed in fp32. dt: [rows, T, nheads] bf16 (dt_is_f32 = 0) or fp32;
+ * dt_bias, A: fp32 [nheads] (dt_bias nullable); cum_A fp32 [rows, T, nheads];
+ * decay fp32 [rows, nheads]; all contiguous.
+ */
+int32_t rmx_mamba2_dt_cumsum(const void* dt, int32_t dt_is_f32, const float* dt_bias,
+                             const float* A, int32_t dt_softplus, float* cum_A, float* decay,
+                             int32_t rows, int32_t T, int32_t nheads, void* stream);
+
+/*
+ * Gradient of rmx_mamba2_dt_cumsum: given dL/dcum_A (nullable) and dL/ddecay
+ * (nullable, with the forward's decay), writes dL/ddt (fp32 [rows, T, nheads])
+ * and ADDS dL/dA and dL/ddt_bias (fp32 [nheads]; dt_bias gradient only with
+ * dt_softplus; nullable) (caller zero-fills them).
+ */
+int32_t rmx_mamba2_dt_cumsum_bwd(const void* dt, int32_t dt_is_f32, const float* dt_bias,
+                                 const float* A, int32_t dt_softplus, const float* g_cum_A,
+                                 const float* g_decay, const float* decay, float* g_dt,
+                                 float* g_A, float* g_dt_bias, int32_t rows, int32_t T,
+                                 int32_t nheads, void* stream);
 
 /*
  * Mamba2 context-parallel causal conv1d with the halo (mamba.py:46-101, the conv

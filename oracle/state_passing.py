@@ -107,3 +107,33 @@ def mamba2_cp_correction(out, h_final, C, cum_A, h_prev, num_heads, head_dim, se
         return corrected, h_final
     h = h_final + (decay[:, -1, :, None, None] * h_prev.float()).to(h_final.dtype)
     return corrected, h
+
+
+def chunk_decay(dt, A, dt_bias=None, dt_softplus=False):
+    """cum_A and the chunk decay of the CP scan wrapper (strategies/mamba.py:276-283):
+    dt_eff = softplus(dt + dt_bias) when dt_softplus (dt_bias is then optional), else dt;
+    cum_A = cumsum(A dt_eff) over T; decay = exp(cum_A[:, -1]). dt [b, T, H], A [H]."""
+    if dt_softplus:
+        dt_eff = torch.nn.functional.softplus(dt + (dt_bias if dt_bias is not None else 0))
+    else:
+        dt_eff = dt
+    cum_A = torch.cumsum(A[None, None, :] * dt_eff, dim=1)
+    return cum_A, torch.exp(cum_A[:, -1])
+
+
+def cp_scan_wrapper_emulated(outs, finals, dts, A, Cs, num_heads, head_dim, dt_bias=None,
+                             dt_softplus=False, seq_idxs=None):
+    """The correction of the reference's mamba_chunk_scan_combined wrapper
+    (strategies/mamba.py:250-300) on every rank: chunk decay from dt, the cross-rank
+    entering state (cp_state_prefix, :68-98; single hop for packed sequences, :94-95)
+    and mamba2_cp_correction. outs [b, T, H*d], finals [b, H, d, n], dts [b, T, H],
+    Cs [b, T, G, n] per rank. Returns per-rank (corrected out, corrected state)."""
+    world = len(outs)
+    cums, decays = zip(*[chunk_decay(dt, A, dt_bias, dt_softplus) for dt in dts])
+    if seq_idxs is None:
+        prefixes = cp_state_prefix_emulated(list(finals), list(decays))
+    else:
+        prefixes = [torch.zeros_like(finals[0])] + [finals[r - 1] for r in range(1, world)]
+    return [mamba2_cp_correction(outs[r], finals[r], Cs[r], cums[r], prefixes[r], num_heads,
+                                 head_dim, None if seq_idxs is None else seq_idxs[r])
+            for r in range(world)]

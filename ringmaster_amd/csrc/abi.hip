@@ -379,6 +379,46 @@ int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const
                     "rmx_mamba2_cp_correction_bwd launch");
 }
 
+static int check_dt(const void* dt, int32_t dt_is_f32, const float* A, int32_t softplus,
+                    int32_t rows, int32_t T, int32_t nheads) {
+  if (rows < 0 || T < 0 || nheads < 0) return fail(RMX_EINVAL, "negative rows, T or nheads");
+  if (dt_is_f32 != 0 && dt_is_f32 != 1) return fail(RMX_EINVAL, "dt_is_f32 must be 0 or 1");
+  if (softplus != 0 && softplus != 1) return fail(RMX_EINVAL, "dt_softplus must be 0 or 1");
+  if ((int64_t)rows * T * nheads == 0) return RMX_OK;
+  if (!dt || !A) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if ((int64_t)rows * ((nheads + 63) / 64) > 2147483647LL)
+    return fail(RMX_EUNSUPPORTED, "more than 2^31 workgroups");
+  return RMX_OK;
+}
+
+int32_t rmx_mamba2_dt_cumsum(const void* dt, int32_t dt_is_f32, const float* dt_bias,
+                             const float* A, int32_t dt_softplus, float* cum_A, float* decay,
+                             int32_t rows, int32_t T, int32_t nheads, void* stream) {
+  int rc = check_dt(dt, dt_is_f32, A, dt_softplus, rows, T, nheads);
+  if (rc) return rc;
+  if ((int64_t)rows * T * nheads == 0) return RMX_OK;
+  if (!cum_A || !decay) return fail(RMX_EINVAL, "NULL tensor pointer");
+  return dev_status(rmx::launch_mamba2_dt_cumsum(dt, dt_is_f32, dt_bias, A, dt_softplus, cum_A,
+                                                 decay, rows, T, nheads, (hipStream_t)stream),
+                    "rmx_mamba2_dt_cumsum launch");
+}
+
+int32_t rmx_mamba2_dt_cumsum_bwd(const void* dt, int32_t dt_is_f32, const float* dt_bias,
+                                 const float* A, int32_t dt_softplus, const float* g_cum_A,
+                                 const float* g_decay, const float* decay, float* g_dt,
+                                 float* g_A, float* g_dt_bias, int32_t rows, int32_t T,
+                                 int32_t nheads, void* stream) {
+  int rc = check_dt(dt, dt_is_f32, A, dt_softplus, rows, T, nheads);
+  if (rc) return rc;
+  if ((int64_t)rows * T * nheads == 0) return RMX_OK;
+  if (!g_dt || !g_A || (g_decay && !decay)) return fail(RMX_EINVAL, "NULL tensor pointer");
+  return dev_status(rmx::launch_mamba2_dt_cumsum_bwd(dt, dt_is_f32, dt_bias, A, dt_softplus,
+                                                     g_cum_A, g_decay, decay, g_dt, g_A,
+                                                     g_dt_bias, rows, T, nheads,
+                                                     (hipStream_t)stream),
+                    "rmx_mamba2_dt_cumsum_bwd launch");
+}
+
 static int check_conv(const uint16_t* x, const uint16_t* weight, const uint16_t* bias,
                       const void* y, int32_t world, int32_t batch, int32_t channels,
                       int32_t local_len, int32_t width, int32_t activation) {

@@ -41,6 +41,14 @@ hipError_t launch_mamba2_correction_bwd(const uint16_t* gy, const float* ghf, co
                                         float* g_hprev, void* workspace, int batch, int T,
                                         int nheads, int head_dim, int ngroups, int d_state,
                                         hipStream_t stream);
+hipError_t launch_mamba2_dt_cumsum(const void* dt, int dt_f32, const float* bias, const float* A,
+                                   int softplus, float* cum_A, float* decay, int rows, int T,
+                                   int H, hipStream_t stream);
+hipError_t launch_mamba2_dt_cumsum_bwd(const void* dt, int dt_f32, const float* bias,
+                                       const float* A, int softplus, const float* g_cum,
+                                       const float* g_decay, const float* decay, float* g_dt,
+                                       float* g_A, float* g_bias, int rows, int T, int H,
+                                       hipStream_t stream);
 hipError_t launch_causal_conv1d_cp(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                                    const int32_t* doc, uint16_t* y, int world, int batch, int C,
                                    int L, int W, int act, hipStream_t stream);

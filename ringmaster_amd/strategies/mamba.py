@@ -19,7 +19,52 @@ from __future__ import annotations
 import torch
 
 from ringmaster_amd import abi
-from ringmaster_amd.strategies.state_passing import linear_scan_forward
+from ringmaster_amd.strategies.state_passing import linear_scan_backward, linear_scan_forward
+
+
+def _prefix_forward(ssm_states, chunk_decays, single_hop):
+    world, b, H = ssm_states.shape[:3]
+    h_prev = torch.zeros_like(ssm_states)
+    if world == 1:
+        return h_prev, None, None
+    if single_hop:
+        h_prev[1:] = ssm_states[:-1]
+        return h_prev, None, None
+    # scan h_r = A_r h_{r-1} + B_r over the rank axis (one decay per head): then
+    # H_in_r = h_{r-1}. Only ranks 0..world-2 feed a later rank.
+    a = chunk_decays[:-1].permute(1, 0, 2).contiguous()                       # [b, world-1, H]
+    bst = ssm_states[:-1].permute(1, 0, 2, 3, 4).reshape(b, world - 1, -1).contiguous()
+    h = linear_scan_forward(a, bst, 1)                                         # [b, world-1, H*d*n]
+    h_prev[1:] = h.reshape(b, world - 1, *ssm_states.shape[2:]).transpose(0, 1)
+    return h_prev, a, h
+
+
+class _StatePrefix(torch.autograd.Function):
+    """Differentiable like the reference's all-gather + torch prefix: the gradient of
+    the rank-axis scan comes from the fp32 linear-scan backward kernel."""
+
+    @staticmethod
+    def forward(ctx, ssm_states, chunk_decays, single_hop):
+        h_prev, a, h = _prefix_forward(ssm_states, chunk_decays, single_hop)
+        ctx.single_hop = single_hop
+        ctx.shape = ssm_states.shape
+        ctx.save_for_backward(a, h)
+        return h_prev
+
+    @staticmethod
+    def backward(ctx, g):
+        a, h = ctx.saved_tensors
+        world, b = ctx.shape[:2]
+        g_states = torch.zeros(ctx.shape, dtype=torch.float32, device=g.device)
+        g_decays = torch.zeros(ctx.shape[:3], dtype=torch.float32, device=g.device)
+        if world > 1 and ctx.single_hop:
+            g_states[:-1] = g[1:]
+        elif world > 1:
+            dh = g[1:].transpose(0, 1).reshape(b, world - 1, -1)
+            da, db = linear_scan_backward(a, h, dh, 1)
+            g_states[:-1] = db.reshape(b, world - 1, *ctx.shape[2:]).transpose(0, 1)
+            g_decays[:-1] = da.permute(1, 0, 2)
+        return g_states, g_decays, None
 
 
 def cp_state_prefix(ssm_states: torch.Tensor, chunk_decays: torch.Tensor, *,
@@ -30,26 +75,102 @@ def cp_state_prefix(ssm_states: torch.Tensor, chunk_decays: torch.Tensor, *,
     final state (computed from h0 = 0); ``chunk_decays``: fp32 ``[world, b, nheads]``,
     each rank's chunk decay ``A_r = exp(sum_t A dt_t)``. Returns ``h_prev`` shaped like
     ``ssm_states`` (rank 0 receives zeros). ``single_hop`` keeps only the immediate
-    predecessor (packed sequences), as the reference does."""
+    predecessor (packed sequences), as the reference does. Differentiable in both
+    inputs."""
     abi.require_device(ssm_states, chunk_decays)
     if ssm_states.dim() != 5 or chunk_decays.shape != ssm_states.shape[:3]:
         raise ValueError("ssm_states must be [world, b, H, d, n] and chunk_decays [world, b, H]")
     if ssm_states.dtype != torch.float32 or chunk_decays.dtype != torch.float32:
         raise NotImplementedError("the MI355X state passing carries fp32 states")
-    world, b, H = ssm_states.shape[:3]
-    h_prev = torch.zeros_like(ssm_states)
-    if world == 1:
-        return h_prev
-    if single_hop:
-        h_prev[1:] = ssm_states[:-1]
-        return h_prev
-    # scan h_r = A_r h_{r-1} + B_r over the rank axis (one decay per head): then
-    # H_in_r = h_{r-1}. Only ranks 0..world-2 feed a later rank.
-    a = chunk_decays[:-1].permute(1, 0, 2).contiguous()                       # [b, world-1, H]
-    bst = ssm_states[:-1].permute(1, 0, 2, 3, 4).reshape(b, world - 1, -1).contiguous()
-    h = linear_scan_forward(a, bst, 1)                                         # [b, world-1, H*d*n]
-    h_prev[1:] = h.reshape(b, world - 1, *ssm_states.shape[2:]).transpose(0, 1)
-    return h_prev
+    return _StatePrefix.apply(ssm_states, chunk_decays, bool(single_hop))
+
+
+class _DtCumsum(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, dt, A, dt_bias, softplus):
+        rows, T, H = dt.shape
+        cum = torch.empty((rows, T, H), dtype=torch.float32, device=dt.device)
+        decay = torch.empty((rows, H), dtype=torch.float32, device=dt.device)
+        abi.check(abi.lib().rmx_mamba2_dt_cumsum(
+            dt.data_ptr(), int(dt.dtype == torch.float32), abi.ptr(dt_bias), A.data_ptr(),
+            int(softplus), cum.data_ptr(), decay.data_ptr(), rows, T, H, abi.stream_of(dt)))
+        ctx.save_for_backward(dt, A, dt_bias, decay)
+        ctx.softplus = softplus
+        return cum, decay
+
+    @staticmethod
+    def backward(ctx, g_cum, g_decay):
+        dt, A, dt_bias, decay = ctx.saved_tensors
+        rows, T, H = dt.shape
+        g_cum = None if g_cum is None else g_cum.contiguous().float()
+        g_decay = None if g_decay is None else g_decay.contiguous().float()
+        g_dt = torch.empty((rows, T, H), dtype=torch.float32, device=dt.device)
+        g_A = torch.zeros(H, dtype=torch.float32, device=dt.device)
+        g_b = torch.zeros(H, dtype=torch.float32, device=dt.device) if dt_bias is not None else None
+        abi.check(abi.lib().rmx_mamba2_dt_cumsum_bwd(
+            dt.data_ptr(), int(dt.dtype == torch.float32), abi.ptr(dt_bias), A.data_ptr(),
+            int(ctx.softplus), abi.ptr(g_cum), abi.ptr(g_decay), decay.data_ptr(),
+            g_dt.data_ptr(), g_A.data_ptr(), abi.ptr(g_b), rows, T, H, abi.stream_of(dt)))
+        return g_dt.to(dt.dtype), g_A, g_b, None
+
+
+def mamba2_chunk_decay(dt: torch.Tensor, A: torch.Tensor, dt_bias: torch.Tensor | None = None,
+                       dt_softplus: bool = False):
+    """``cum_A = cumsum(A * dt_eff, dim=T)`` and the chunk decay ``exp(cum_A[:, -1])`` of
+    the reference's CP scan wrapper (strategies/mamba.py:276-283), with
+    ``dt_eff = softplus(dt + dt_bias)`` when ``dt_softplus`` (else ``dt``). ``dt``:
+    ``[..., T, nheads]`` bf16 or fp32; ``A``, ``dt_bias``: ``[nheads]``. Returns fp32
+    ``cum_A`` shaped like ``dt`` and ``decay`` ``[..., nheads]``; differentiable in dt, A
+    and dt_bias. Computed in fp32 (the reference's arithmetic when dt_bias or dt is fp32,
+    as HF's fp32 dt_bias parameter makes it)."""
+    abi.require_device(dt, A)
+    if dt.dim() < 2 or A.dim() != 1 or A.shape[0] != dt.shape[-1]:
+        raise ValueError("dt must be [..., T, nheads] and A [nheads]")
+    if dt.dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError("dt must be bf16 or fp32")
+    lead, (T, H) = dt.shape[:-2], dt.shape[-2:]
+    d3 = dt.reshape(-1, T, H).contiguous()
+    A32 = A.float().contiguous()
+    b32 = None
+    if dt_softplus and dt_bias is not None:
+        b32 = dt_bias.float().contiguous()
+    cum, decay = _DtCumsum.apply(d3, A32, b32, bool(dt_softplus))
+    return cum.reshape(*lead, T, H), decay.reshape(*lead, H)
+
+
+def mamba2_cp_apply(scan_output: torch.Tensor, ssm_state: torch.Tensor, dt: torch.Tensor,
+                    A: torch.Tensor, C: torch.Tensor, *, dt_bias: torch.Tensor | None = None,
+                    dt_softplus: bool = False, seq_idx: torch.Tensor | None = None):
+    """The CP correction the reference's ``mamba_chunk_scan_combined`` wrapper applies
+    (strategies/mamba.py:250-300) for every rank at once: chunk decay from dt, the exact
+    cross-rank entering state (single hop for packed sequences) and the output / state
+    correction. Ranks stacked on a leading axis: ``scan_output`` bf16 ``[P, B, T, H, d]``
+    (or ``[P, B, T, H*d]``), ``ssm_state`` fp32 ``[P, B, H, d, n]`` (each shard's scan
+    from a zero state), ``dt`` ``[P, B, T, H]``, ``A`` ``[H]``, ``C`` bf16
+    ``[P, B, T, G, n]``, ``seq_idx`` int32 ``[P, B, T]`` or None. Returns the corrected
+    ``(scan_output, ssm_state)``; differentiable like the reference's torch ops."""
+    P, B = ssm_state.shape[:2]
+    H, d, n = ssm_state.shape[2:]
+    T = dt.shape[2]
+    cum_A, decay = mamba2_chunk_decay(dt, A, dt_bias, dt_softplus)          # [P,B,T,H], [P,B,H]
+    h_prev = cp_state_prefix(ssm_state, decay, single_hop=seq_idx is not None)
+    if seq_idx is None:
+        # every rank's rows in one launch, stacked on the batch axis
+        y, h_final = mamba2_cp_correction(
+            scan_output.reshape(P * B, T, H * d), ssm_state.reshape(P * B, H, d, n),
+            C.reshape(P * B, T, *C.shape[3:]), cum_A.reshape(P * B, T, H),
+            h_prev.reshape(P * B, H, d, n), H, d)
+        return y.reshape(scan_output.shape), h_final.reshape(ssm_state.shape)
+    # packed: the state update is skipped when the last token of any of a rank's batch
+    # rows starts a fresh sequence (seq_idx[:, -1].any() per rank, strategies/mamba.py:131),
+    # so each rank gets its own launch
+    ys, hs = [], []
+    for r in range(P):
+        y, h = mamba2_cp_correction(scan_output[r].reshape(B, T, H * d), ssm_state[r], C[r],
+                                    cum_A[r], h_prev[r], H, d, seq_idx=seq_idx[r])
+        ys.append(y)
+        hs.append(h)
+    return torch.stack(ys).reshape(scan_output.shape), torch.stack(hs)
 
 
 def _validate_correction(out, h_final, C, cum_A, h_prev, num_heads, head_dim, seq_idx):

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 5
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 6
     assert isinstance(lib.rmx_last_error(), bytes)
 
 

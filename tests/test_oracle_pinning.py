@@ -296,6 +296,47 @@ def test_mamba2_prefix_equals_global_ssd(world):
         assert (corrected - ref_out[:, sl]).abs().max().item() < 1e-6
 
 
+@pytest.mark.parametrize("world", [1, 2, 4])
+@pytest.mark.parametrize("softplus", [False, True])
+def test_cp_scan_wrapper_equals_global_ssd_values_and_grads(world, softplus):
+    """The CP wrapper (chunk decay from dt, prefix, correction) applied to each shard's
+    zero-state SSD equals the global SSD, in values and in the gradients w.r.t. dt, A,
+    dt_bias, x and C (the shards' SSD runs inside the same graph)."""
+    torch.manual_seed(1)
+    b, T, H, d, G, n = 1, 16, 2, 3, 1, 4
+    x = torch.randn(b, T, H, d, dtype=torch.float64, requires_grad=True)
+    dt_raw = (torch.randn(b, T, H, dtype=torch.float64) * 0.5 - 2.0).requires_grad_(True)
+    bias = (torch.randn(H, dtype=torch.float64) * 0.1).requires_grad_(True)
+    A = (-torch.rand(H, dtype=torch.float64) - 0.1).requires_grad_(True)
+    B = torch.randn(b, T, G, n, dtype=torch.float64)
+    C = torch.randn(b, T, G, n, dtype=torch.float64, requires_grad=True)
+    dt_eff = torch.nn.functional.softplus(dt_raw + bias) if softplus else dt_raw.abs() * 0.1
+    ref_out, ref_state = sp.ssd_reference(x, dt_eff, A, B, C)
+    n_loc = T // world
+    outs, finals, dts, Cs = [], [], [], []
+    for r in range(world):
+        sl = slice(r * n_loc, (r + 1) * n_loc)
+        o, h = sp.ssd_reference(x[:, sl], dt_eff[:, sl], A, B[:, sl], C[:, sl])
+        outs.append(o)
+        finals.append(h)
+        dts.append(dt_raw[:, sl] if softplus else dt_eff[:, sl])
+        Cs.append(C[:, sl])
+    res = sp.cp_scan_wrapper_emulated(outs, finals, dts, A, Cs, H, d,
+                                      dt_bias=bias if softplus else None, dt_softplus=softplus)
+    got = torch.cat([o for o, _ in res], dim=1)
+    assert (got - ref_out).abs().max().item() < 1e-6
+    assert (res[-1][1] - ref_state).abs().max().item() < 1e-6
+    w = torch.randn_like(ref_out)
+    gs = torch.autograd.grad((got * w).sum() + res[-1][1].sum(), (x, dt_raw, A, C, bias),
+                             allow_unused=True, retain_graph=True)
+    rs = torch.autograd.grad((ref_out * w).sum() + ref_state.sum(), (x, dt_raw, A, C, bias),
+                             allow_unused=True)
+    for g, r in zip(gs, rs):
+        if r is None:
+            continue
+        assert (g - r).abs().max().item() < 1e-5, (g - r).abs().max().item()
+
+
 def _ssd_segments(x, dt, A, B, C, seg):
     """SSD with the state reset at every segment start (packed sequences): per-segment
     ssd_reference runs, concatenated; returns (out, final state of the last segment)."""
