@@ -201,23 +201,6 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   const int q = qw0 + l32;
   const bool qvalid = q < sq;
 
-  bf16x8 qreg[NKB], doreg[NKB];
-  {
-    const i32x4 qrs = make_rsrc(P.q + bb * L.q_sb + head * L.q_sh,
-                                span_bytes(sq, 2 * L.q_ss, HD * 2));
-    const i32x4 ors = make_rsrc(P.dout + bb * L.o_sb + head * L.o_sh,
-                                span_bytes(sq, 2 * L.o_ss, HD * 2));
-    const int qo = q * (int)(2 * L.q_ss) + 16 * hl, oo = q * (int)(2 * L.o_ss) + 16 * hl;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      qreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(qrs, qo + 32 * kb));
-      doreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(ors, oo + 32 * kb));
-    }
-  }
-  const int64_t lrow = bb * L.l_sb + head * L.l_sh + (qvalid ? q : 0);
-  float lse2 = qvalid ? P.lse[lrow] * kLog2e : kNegInf;
-  if (lse2 == kNegInf) lse2 = __builtin_inff();  // no key attended: P == 0 everywhere
-  const float dlt = qvalid ? P.delta[lrow] : 0.f;
   int qg = -2147483647, qd = -1;
   if (mask == RMX_MASK_DOC && qvalid) {
     qg = P.q_gidx[q];
@@ -259,6 +242,25 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
     kt_end = sRange[1] + 1;
     if (kt_end < kt_begin) kt_end = kt_begin;
   }
+  // no key tile: an accumulated dQ keeps its value
+  if (kt_end == kt_begin && P.dq_mode == RMX_GRAD_ACC_F32) return;
+  bf16x8 qreg[NKB], doreg[NKB];
+  {
+    const i32x4 qrs = make_rsrc(P.q + bb * L.q_sb + head * L.q_sh,
+                                span_bytes(sq, 2 * L.q_ss, HD * 2));
+    const i32x4 ors = make_rsrc(P.dout + bb * L.o_sb + head * L.o_sh,
+                                span_bytes(sq, 2 * L.o_ss, HD * 2));
+    const int qo = q * (int)(2 * L.q_ss) + 16 * hl, oo = q * (int)(2 * L.o_ss) + 16 * hl;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      qreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(qrs, qo + 32 * kb));
+      doreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(ors, oo + 32 * kb));
+    }
+  }
+  const int64_t lrow = bb * L.l_sb + head * L.l_sh + (qvalid ? q : 0);
+  float lse2 = qvalid ? P.lse[lrow] * kLog2e : kNegInf;
+  if (lse2 == kNegInf) lse2 = __builtin_inff();  // no key attended: P == 0 everywhere
+  const float dlt = qvalid ? P.delta[lrow] : 0.f;
   const int wave_qlast = (qw0 + 31 < sq ? qw0 + 31 : sq - 1);
   const int wave_kmax = mask == RMX_MASK_CAUSAL ? wave_qlast + off : 2147483647;
 
@@ -535,6 +537,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     if (qt_end < qt_begin) qt_end = qt_begin;
   }
   const int ntile = (qt_end - qt_begin) * G;  // (q head, query tile) pairs, q head major
+  // no query tile: accumulated dK and dV keep their values
+  if (ntile == 0 && P.dkv_mode == RMX_GRAD_ACC_F32) return;
   const int wave_klast = (kw0 + 31 < sk ? kw0 + 31 : sk - 1);
 
   // ---- tile loads. Wave 0 first loads the tile's lse and delta (one dword per

@@ -99,15 +99,6 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   const int qw0 = q0 + 32 * wave;  // first query of this wave
   const int q = qw0 + l32;         // this lane's query
 
-  // ---- Q operand (B of S^T = K Q^T): lane holds Q[q][16kb + 8hl .. +7]
-  bf16x8 qreg[NKB];
-  {
-    const uint16_t* qb = P.q + bb * L.q_sb + head * L.q_sh;
-    const i32x4 rs = make_rsrc(qb, span_bytes(sq, 2 * L.q_ss, HD * 2));
-    const int off = q * (int)(2 * L.q_ss) + 16 * hl;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) qreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(rs, off + 32 * kb));
-  }
   int qg = -2147483647, qd = -1;
   if (mask == RMX_MASK_DOC && q < sq) {
     qg = P.q_gidx[q];
@@ -151,6 +142,18 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     if (kt_end < kt_begin) kt_end = kt_begin;
   }
   const int ntile = kt_end - kt_begin;
+  // no key tile: a merge into the running (out, lse) leaves it as it is
+  if (ntile == 0 && P.mode == RMX_FWD_ACC_MERGE) return;
+
+  // ---- Q operand (B of S^T = K Q^T): lane holds Q[q][16kb + 8hl .. +7]
+  bf16x8 qreg[NKB];
+  if (ntile > 0) {
+    const uint16_t* qb = P.q + bb * L.q_sb + head * L.q_sh;
+    const i32x4 rs = make_rsrc(qb, span_bytes(sq, 2 * L.q_ss, HD * 2));
+    const int qo = q * (int)(2 * L.q_ss) + 16 * hl;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) qreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(rs, qo + 32 * kb));
+  }
 
   // ---- K/V staging: buffer resources over this (batch, kv head)
   const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);

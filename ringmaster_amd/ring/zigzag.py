@@ -31,15 +31,22 @@ import torch
 
 from ringmaster_amd import abi
 from ringmaster_amd.ring import ops
-from ringmaster_amd.ring.schedule import (contiguous_gidx, contiguous_schedule, zigzag_gidx,
-                                          zigzag_schedule)
+from ringmaster_amd.ring.schedule import contiguous_schedule, zigzag_schedule
 
 
-def doc_ids_from_cu(cu_seqlens: torch.Tensor, device) -> torch.Tensor:
-    """Per-token document id over the full sequence (ring/varlen_blocks.py:45-48)."""
-    seg = cu_seqlens.to(device=device, dtype=torch.int64).diff()
-    return torch.repeat_interleave(
-        torch.arange(seg.numel(), device=device, dtype=torch.int32), seg).contiguous()
+def doc_ids_from_cu(cu_seqlens: torch.Tensor, device, total: int | None = None) -> torch.Tensor:
+    """Per-token document id over the full sequence (ring/varlen_blocks.py:45-48).
+
+    With ``total`` (the sequence length) the ids come from a search of the document
+    starts over ``arange(total)`` on the device: the same ids for a consistent
+    ``cu_seqlens`` (0 first, ``total`` last) and no device-to-host synchronization."""
+    cu = cu_seqlens.to(device=device, dtype=torch.int64)
+    if total is None:
+        seg = cu.diff()
+        return torch.repeat_interleave(
+            torch.arange(seg.numel(), device=device, dtype=torch.int32), seg).contiguous()
+    pos = torch.arange(total, device=device, dtype=torch.int64)
+    return torch.searchsorted(cu[1:], pos, right=True).to(torch.int32).contiguous()
 
 
 def _fwd_mode(first: bool, last: bool) -> int:
@@ -50,6 +57,27 @@ def _fwd_mode(first: bool, last: bool) -> int:
     if last:
         return abi.FWD_ACC_FINAL
     return abi.FWD_ACC_MERGE
+
+
+_ROWS_CACHE: dict = {}
+
+
+def _global_rows(layout: str, P: int, L: int, device) -> torch.Tensor:
+    """Global token index of every local row of every rank, int32 [P, L], built on the
+    device (zigzag: chunks r and 2P-1-r of length L/2, early first; contiguous: chunk r)
+    and cached per (layout, P, L, device)."""
+    key = (layout, P, L, str(device))
+    rows = _ROWS_CACHE.get(key)
+    if rows is None:
+        r = torch.arange(P, device=device, dtype=torch.int32)[:, None]
+        if layout == "zigzag":
+            h = L // 2
+            i = torch.arange(h, device=device, dtype=torch.int32)[None, :]
+            rows = torch.cat([r * h + i, (2 * P - 1 - r) * h + i], dim=1).contiguous()
+        else:
+            rows = (r * L + torch.arange(L, device=device, dtype=torch.int32)[None, :]).contiguous()
+        _ROWS_CACHE[key] = rows
+    return rows
 
 
 class _Ctx:
@@ -66,9 +94,7 @@ class _Ctx:
         self.layout, self.causal = layout, causal
         self.gidx = self.rdoc = None
         if doc is not None:
-            rows = [zigzag_gidx(r, self.half, self.P) if layout == "zigzag"
-                    else contiguous_gidx(r, self.L) for r in range(self.P)]
-            self.gidx = torch.tensor(rows, dtype=torch.int32).to(q.device)
+            self.gidx = _global_rows(layout, self.P, self.L, q.device)
             # document id of every local row of every rank: [P, L]
             self.rdoc = doc[self.gidx.long()].to(torch.int32).contiguous()
 
@@ -256,13 +282,15 @@ def check_ring_inputs(q, k, v):
 
 
 def doc_for(cu_seqlens, q):
-    """Per-token document ids of the packed sequence (None when not packed)."""
+    """Per-token document ids of the packed sequence (None when not packed). A host
+    ``cu_seqlens`` is checked to cover the sequence; a device one is read without a
+    synchronization and must end at the sequence length."""
     if cu_seqlens is None:
         return None
-    doc = doc_ids_from_cu(cu_seqlens, q.device)
-    if doc.numel() != q.shape[0] * q.shape[3]:
+    total = q.shape[0] * q.shape[3]
+    if cu_seqlens.device.type == "cpu" and int(cu_seqlens[-1]) != total:
         raise ValueError("cu_seqlens must cover the full (padded) sequence")
-    return doc
+    return doc_ids_from_cu(cu_seqlens, q.device, total)
 
 
 def zigzag_ring_attention(q, k, v, *, scaling=None, cu_seqlens=None, timer=None):

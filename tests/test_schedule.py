@@ -119,3 +119,28 @@ def test_distflash_balance_literals():
         work = distflash_work(world)
         assert sum(work) == world * (world + 1) // 2  # every causal block exactly once
         assert max(work) - min(work) <= 1
+
+
+@pytest.mark.parametrize("world,L", [(1, 8), (2, 8), (4, 6), (3, 10)])
+def test_device_row_tables_match_host_lists(world, L):
+    from ringmaster_amd.ring.zigzag import _global_rows
+
+    zz = _global_rows("zigzag", world, L, "cpu")
+    assert zz.dtype == torch.int32 and zz.shape == (world, L)
+    assert zz.tolist() == [zigzag_gidx(r, L // 2, world) for r in range(world)]
+    ct = _global_rows("contiguous", world, L, "cpu")
+    assert ct.tolist() == [contiguous_gidx(r, L) for r in range(world)]
+    assert _global_rows("zigzag", world, L, "cpu") is zz  # cached
+
+
+@pytest.mark.parametrize("lens", [[16], [1, 15], [5, 0, 7, 4], [3, 3, 3, 3, 4], [0, 16]])
+def test_sync_free_doc_ids_match_repeat_interleave(lens):
+    # ring/varlen_blocks.py:45-48 builds the ids with repeat_interleave; zero-length
+    # documents (repeated offsets) must be skipped the same way
+    from ringmaster_amd.ring.zigzag import doc_ids_from_cu
+
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    ref = doc_ids_from_cu(cu, "cpu")
+    fast = doc_ids_from_cu(cu, "cpu", sum(lens))
+    assert fast.dtype == ref.dtype == torch.int32
+    assert torch.equal(fast, ref)
