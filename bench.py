@@ -260,6 +260,52 @@ def mamba_workload(steps, warmup):
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def chunk_state_workload(steps, warmup):
+    """configs[4] Mamba2 shard final state (rmx_mamba2_chunk_state and its backward): 8
+    shards of 8192 tokens, nheads=64, headdim=64, ngroups=1, d_state=128. Algorithmic
+    bytes: fwd reads x, B, e, cum_A and writes the fp32 state; bwd reads x, B, e, cum_A
+    and the state gradient and writes g_x, g_B (bf16), g_e, g_cum_A (fp32)."""
+    from ringmaster_amd import abi
+
+    P, T, H, D, G, N = 8, 8192, 64, 64, 1, 128
+    g = torch.Generator(device="cuda").manual_seed(7)
+    x = _gen((P, T, H, D), 30)
+    B = _gen((P, T, G, N), 31)
+    A = -torch.exp(torch.rand(H, generator=g, device="cuda") * math.log(16.0))
+    e = torch.nn.functional.softplus(torch.randn(P, T, H, generator=g, device="cuda") - 2.0)
+    cum = torch.cumsum(A * e, dim=1)
+    state = torch.empty((P, H, D, N), dtype=torch.float32, device="cuda")
+    gst = _gen((P, H, D, N), 32, torch.float32)
+    g_x, g_B = torch.empty_like(x), torch.empty_like(B)
+    g_e, g_cum = torch.empty_like(e), torch.empty_like(e)
+    lib, st = abi.lib(), abi.stream_of(x)
+
+    def fwd():
+        abi.check(lib.rmx_mamba2_chunk_state(x.data_ptr(), B.data_ptr(), e.data_ptr(),
+                                             cum.data_ptr(), None, state.data_ptr(), P, T, H,
+                                             D, G, N, st))
+
+    def bwd():
+        abi.check(lib.rmx_mamba2_chunk_state_bwd(
+            x.data_ptr(), B.data_ptr(), e.data_ptr(), cum.data_ptr(), None, gst.data_ptr(),
+            g_x.data_ptr(), g_B.data_ptr(), g_e.data_ptr(), g_cum.data_ptr(), P, T, H, D, G, N,
+            st))
+
+    fwd_ms = _time(fwd, steps, warmup)
+    bwd_ms = _time(bwd, steps, warmup)
+    small = e.numel() * 4
+    fwd_bytes = x.numel() * 2 + B.numel() * 2 + 2 * small + state.numel() * 4
+    bwd_bytes = 2 * x.numel() * 2 + 2 * B.numel() * 2 + 4 * small + gst.numel() * 4
+    flops = 2 * P * T * H * D * N
+    out = {}
+    for name, ms, nb, fl in (("fwd", fwd_ms, fwd_bytes, flops), ("bwd", bwd_ms, bwd_bytes, 2 * flops)):
+        gbs = nb / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "bytes": nb, "GB/s": round(gbs, 1),
+                     "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                     "TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 1)}
+    return out
+
+
 def conv_workload(steps, warmup):
     """configs[4] Mamba2 CP causal conv1d with the halo, fwd and bwd: 8 shards of 8192
     tokens, conv channels = nheads * headdim + 2 * ngroups * d_state = 4352, width 4,
@@ -489,6 +535,8 @@ def main():
         extras["mamba2_correction_bwd_configs4"] = mamba_bwd_workload(20, 3)
         torch.cuda.empty_cache()
         extras["mamba2_conv_cp_configs4"] = conv_workload(20, 3)
+        torch.cuda.empty_cache()
+        extras["mamba2_chunk_state_configs4"] = chunk_state_workload(20, 3)
         torch.cuda.empty_cache()
         extras["block_configs1"] = block_workload(3, 1)
         torch.cuda.empty_cache()

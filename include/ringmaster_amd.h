@@ -27,7 +27,8 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 6  /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum */
+#define RMX_ABI_VERSION 7  /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+                              7: effective dt in/out of the dt cumsum, shard final state */
 
 /* error codes */
 #define RMX_OK 0
@@ -267,23 +268,58 @@ int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const
  *   cum_A[r,t,h] = sum_{s<=t} A[h] e_s,   decay[r,h] = exp(cum_A[r,T-1,h])
  * computed in fp32. dt: [rows, T, nheads] bf16 (dt_is_f32 = 0) or fp32;
  * dt_bias, A: fp32 [nheads] (dt_bias nullable); cum_A fp32 [rows, T, nheads];
- * decay fp32 [rows, nheads]; all contiguous.
+ * e (nullable): the effective dt e_t, fp32 [rows, T, nheads] (what the shard
+ * state below weighs tokens with); decay fp32 [rows, nheads]; all contiguous.
  */
 int32_t rmx_mamba2_dt_cumsum(const void* dt, int32_t dt_is_f32, const float* dt_bias,
-                             const float* A, int32_t dt_softplus, float* cum_A, float* decay,
-                             int32_t rows, int32_t T, int32_t nheads, void* stream);
+                             const float* A, int32_t dt_softplus, float* cum_A, float* e,
+                             float* decay, int32_t rows, int32_t T, int32_t nheads, void* stream);
 
 /*
- * Gradient of rmx_mamba2_dt_cumsum: given dL/dcum_A (nullable) and dL/ddecay
- * (nullable, with the forward's decay), writes dL/ddt (fp32 [rows, T, nheads])
- * and ADDS dL/dA and dL/ddt_bias (fp32 [nheads]; dt_bias gradient only with
- * dt_softplus; nullable) (caller zero-fills them).
+ * Gradient of rmx_mamba2_dt_cumsum: given dL/dcum_A (nullable), dL/de (nullable,
+ * a direct gradient of the effective dt) and dL/ddecay (nullable, with the
+ * forward's decay), writes dL/ddt (fp32 [rows, T, nheads]) and ADDS dL/dA and
+ * dL/ddt_bias (fp32 [nheads]; dt_bias gradient only with dt_softplus; nullable)
+ * (caller zero-fills them).
  */
 int32_t rmx_mamba2_dt_cumsum_bwd(const void* dt, int32_t dt_is_f32, const float* dt_bias,
                                  const float* A, int32_t dt_softplus, const float* g_cum_A,
-                                 const float* g_decay, const float* decay, float* g_dt,
-                                 float* g_A, float* g_dt_bias, int32_t rows, int32_t T,
-                                 int32_t nheads, void* stream);
+                                 const float* g_e, const float* g_decay, const float* decay,
+                                 float* g_dt, float* g_A, float* g_dt_bias, int32_t rows,
+                                 int32_t T, int32_t nheads, void* stream);
+
+/*
+ * Mamba2 shard final state from x, B and dt: the final_states of mamba-ssm's
+ * mamba_chunk_scan_combined(..., return_final_states=True) from a zero state,
+ * which the reference's CP scan wrapper gathers across ranks (mamba.py:113-141,
+ * 160-172: `final` of each shard, the last document's state when packed;
+ * strategies/mamba.py:250-300). Per row and head h of group g = h / (H / G):
+ *   state[r,h] = sum_{t0[r] <= t < T} exp(cum_A[r,T-1,h] - cum_A[r,t,h]) e[r,t,h]
+ *                x[r,t,h,:] (x) B[r,t,g,:]
+ * (the SSD recurrence h_t = exp(A e_t) h_{t-1} + e_t x_t (x) B_t unrolled; the
+ * weighted B is rounded to bf16 like mamba-ssm's chunk-state kernel, sums fp32).
+ * x bf16 [rows, T, H, head_dim]; B bf16 [rows, T, G, d_state]; e, cum_A fp32
+ * [rows, T, H] (from rmx_mamba2_dt_cumsum); t0 int32 [rows] (nullable: 0), the
+ * first token of each row's last document; state fp32 [rows, H, head_dim,
+ * d_state]. head_dim and d_state in {64, 128}; contiguous, 16-byte aligned.
+ */
+int32_t rmx_mamba2_chunk_state(const uint16_t* x, const uint16_t* B, const float* e,
+                               const float* cum_A, const int32_t* t0, float* state, int32_t rows,
+                               int32_t T, int32_t nheads, int32_t head_dim, int32_t ngroups,
+                               int32_t d_state, void* stream);
+
+/*
+ * Gradient of rmx_mamba2_chunk_state given g_state = dL/dstate (fp32, like
+ * state): writes g_x (bf16, like x), g_B (bf16, like B), g_e and g_cum_A (fp32
+ * [rows, T, H]). g_cum_A[r, T-1, h] is left as -g_w w of that token; the full
+ * entry is sum_{t<T-1} g_w w = -sum_{t<T-1} g_cum_A[r, t, h], which the caller
+ * writes (every weight depends on cum_A at T-1).
+ */
+int32_t rmx_mamba2_chunk_state_bwd(const uint16_t* x, const uint16_t* B, const float* e,
+                                   const float* cum_A, const int32_t* t0, const float* g_state,
+                                   uint16_t* g_x, uint16_t* g_B, float* g_e, float* g_cum_A,
+                                   int32_t rows, int32_t T, int32_t nheads, int32_t head_dim,
+                                   int32_t ngroups, int32_t d_state, void* stream);
 
 /*
  * Mamba2 context-parallel causal conv1d with the halo (mamba.py:46-101, the conv

@@ -3,7 +3,10 @@
 Follows strategies/state_passing.py:19-59 (local scan, ``cp_linear_scan`` with the
 all-gather of (A_r, B_r) emulated as a list over ranks), the Mamba2 SSD reference
 of tests/test_mamba_cp.py:16-32, and ``cp_state_prefix`` / ``mamba2_cp_correction``
-(strategies/mamba.py:68-139). Autograd-capable (torch ops only).
+(strategies/mamba.py:68-139), and the shard final state the CP scan wrapper gathers
+(``final`` of mamba.py:113-141,160-172, computed there by mamba-ssm's
+``mamba_chunk_scan_combined``, a dependency absent from the reference tree).
+Autograd-capable (torch ops only).
 """
 
 from __future__ import annotations
@@ -107,6 +110,23 @@ def mamba2_cp_correction(out, h_final, C, cum_A, h_prev, num_heads, head_dim, se
         return corrected, h_final
     h = h_final + (decay[:, -1, :, None, None] * h_prev.float()).to(h_final.dtype)
     return corrected, h
+
+
+def chunk_state(x, B, e, cum_A, t0=None):
+    """Final SSM state of a shard's scan from a zero state (``final`` of mamba.py:113-141;
+    per document the state of the last segment, :120-141): the SSD recurrence of
+    ``ssd_reference`` unrolled,
+    ``S[b,h] = sum_{t >= t0[b]} exp(cum_A[b,T-1,h] - cum_A[b,t,h]) e[b,t,h] x[b,t,h] (x) B[b,t,g]``
+    with ``cum_A = cumsum(A e)``. x [b,T,H,d], B [b,T,G,n], e / cum_A [b,T,H], t0 [b]
+    (first token of each row's last document) or None. Returns [b,H,d,n]."""
+    bsz, T, H, _ = x.shape
+    G = B.shape[2]
+    w = torch.exp(cum_A[:, -1:, :] - cum_A) * e
+    if t0 is not None:
+        keep = torch.arange(T)[None, :] >= torch.as_tensor(t0).reshape(bsz, 1)
+        w = w * keep[:, :, None].to(w.dtype)
+    Bx = B.repeat_interleave(H // G, dim=2)
+    return torch.einsum("bth,bthd,bthn->bhdn", w, x, Bx)
 
 
 def chunk_decay(dt, A, dt_bias=None, dt_softplus=False):

@@ -392,31 +392,79 @@ static int check_dt(const void* dt, int32_t dt_is_f32, const float* A, int32_t s
 }
 
 int32_t rmx_mamba2_dt_cumsum(const void* dt, int32_t dt_is_f32, const float* dt_bias,
-                             const float* A, int32_t dt_softplus, float* cum_A, float* decay,
-                             int32_t rows, int32_t T, int32_t nheads, void* stream) {
+                             const float* A, int32_t dt_softplus, float* cum_A, float* e,
+                             float* decay, int32_t rows, int32_t T, int32_t nheads, void* stream) {
   int rc = check_dt(dt, dt_is_f32, A, dt_softplus, rows, T, nheads);
   if (rc) return rc;
   if ((int64_t)rows * T * nheads == 0) return RMX_OK;
   if (!cum_A || !decay) return fail(RMX_EINVAL, "NULL tensor pointer");
   return dev_status(rmx::launch_mamba2_dt_cumsum(dt, dt_is_f32, dt_bias, A, dt_softplus, cum_A,
-                                                 decay, rows, T, nheads, (hipStream_t)stream),
+                                                 e, decay, rows, T, nheads, (hipStream_t)stream),
                     "rmx_mamba2_dt_cumsum launch");
 }
 
 int32_t rmx_mamba2_dt_cumsum_bwd(const void* dt, int32_t dt_is_f32, const float* dt_bias,
                                  const float* A, int32_t dt_softplus, const float* g_cum_A,
-                                 const float* g_decay, const float* decay, float* g_dt,
-                                 float* g_A, float* g_dt_bias, int32_t rows, int32_t T,
-                                 int32_t nheads, void* stream) {
+                                 const float* g_e, const float* g_decay, const float* decay,
+                                 float* g_dt, float* g_A, float* g_dt_bias, int32_t rows,
+                                 int32_t T, int32_t nheads, void* stream) {
   int rc = check_dt(dt, dt_is_f32, A, dt_softplus, rows, T, nheads);
   if (rc) return rc;
   if ((int64_t)rows * T * nheads == 0) return RMX_OK;
   if (!g_dt || !g_A || (g_decay && !decay)) return fail(RMX_EINVAL, "NULL tensor pointer");
   return dev_status(rmx::launch_mamba2_dt_cumsum_bwd(dt, dt_is_f32, dt_bias, A, dt_softplus,
-                                                     g_cum_A, g_decay, decay, g_dt, g_A,
+                                                     g_cum_A, g_e, g_decay, decay, g_dt, g_A,
                                                      g_dt_bias, rows, T, nheads,
                                                      (hipStream_t)stream),
                     "rmx_mamba2_dt_cumsum_bwd launch");
+}
+
+static int check_state(const uint16_t* x, const uint16_t* B, const float* e, const float* cum_A,
+                       int32_t rows, int32_t T, int32_t H, int32_t D, int32_t G, int32_t N) {
+  if (rows < 0 || T < 0 || H < 0 || G < 1) return fail(RMX_EINVAL, "bad rows, T, nheads or ngroups");
+  if ((D != 64 && D != 128) || (N != 64 && N != 128))
+    return fail(RMX_EUNSUPPORTED, "head_dim %d / d_state %d outside {64, 128}", D, N);
+  if (H % G) return fail(RMX_EINVAL, "nheads %d not a multiple of ngroups %d", H, G);
+  if ((int64_t)rows * T * H == 0) return RMX_OK;
+  // 32-bit byte offsets per row, with a tile of slack past the end
+  if ((int64_t)(T + 256) * H * D * 2 >= 2147483647LL || (int64_t)(T + 256) * G * N * 2 >= 2147483647LL)
+    return fail(RMX_EUNSUPPORTED, "more than 2^31 bytes of x or B per row");
+  if ((int64_t)rows * H * 2 > 2147483647LL || (int64_t)rows * G * ((T + 255) / 256) > 2147483647LL)
+    return fail(RMX_EUNSUPPORTED, "more than 2^31 workgroups");
+  if (!x || !B || !e || !cum_A) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!aligned(x, 16) || !aligned(B, 16)) return fail(RMX_EINVAL, "x and B must be 16-byte aligned");
+  return RMX_OK;
+}
+
+int32_t rmx_mamba2_chunk_state(const uint16_t* x, const uint16_t* B, const float* e,
+                               const float* cum_A, const int32_t* t0, float* state, int32_t rows,
+                               int32_t T, int32_t nheads, int32_t head_dim, int32_t ngroups,
+                               int32_t d_state, void* stream) {
+  int rc = check_state(x, B, e, cum_A, rows, T, nheads, head_dim, ngroups, d_state);
+  if (rc) return rc;
+  if ((int64_t)rows * nheads == 0) return RMX_OK;
+  if (!state) return fail(RMX_EINVAL, "NULL tensor pointer");
+  return dev_status(rmx::launch_mamba2_chunk_state(x, B, e, cum_A, t0, state, rows, T, nheads,
+                                                   head_dim, ngroups, d_state,
+                                                   (hipStream_t)stream),
+                    "rmx_mamba2_chunk_state launch");
+}
+
+int32_t rmx_mamba2_chunk_state_bwd(const uint16_t* x, const uint16_t* B, const float* e,
+                                   const float* cum_A, const int32_t* t0, const float* g_state,
+                                   uint16_t* g_x, uint16_t* g_B, float* g_e, float* g_cum_A,
+                                   int32_t rows, int32_t T, int32_t nheads, int32_t head_dim,
+                                   int32_t ngroups, int32_t d_state, void* stream) {
+  int rc = check_state(x, B, e, cum_A, rows, T, nheads, head_dim, ngroups, d_state);
+  if (rc) return rc;
+  if ((int64_t)rows * T * nheads == 0) return RMX_OK;
+  if (!g_state || !g_x || !g_B || !g_e || !g_cum_A) return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!aligned(g_state, 16) || !aligned(g_x, 8) || !aligned(g_B, 8))
+    return fail(RMX_EINVAL, "g_state must be 16-byte and g_x, g_B 8-byte aligned");
+  return dev_status(rmx::launch_mamba2_chunk_state_bwd(x, B, e, cum_A, t0, g_state, g_x, g_B,
+                                                       g_e, g_cum_A, rows, T, nheads, head_dim,
+                                                       ngroups, d_state, (hipStream_t)stream),
+                    "rmx_mamba2_chunk_state_bwd launch");
 }
 
 static int check_conv(const uint16_t* x, const uint16_t* weight, const uint16_t* bias,

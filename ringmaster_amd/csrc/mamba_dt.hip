@@ -18,6 +18,8 @@ struct DtArgs {
   const float* A;        // [H]
   int softplus;
   float* cum_A;          // fwd out [rows, T, H]
+  float* e_out;          // fwd out [rows, T, H] (effective dt) or null
+  const float* g_e;      // bwd in [rows, T, H] (direct gradient of e) or null
   float* decay;          // fwd out / bwd in [rows, H]
   const float* g_cum;    // bwd in [rows, T, H] or null
   const float* g_decay;  // bwd in [rows, H] or null
@@ -72,15 +74,17 @@ __global__ __launch_bounds__(256) void mamba2_dt_cumsum_kernel(const DtArgs a) {
   if (hv) {
 #pragma unroll 8
     for (int t = lo; t < hi; ++t) {
-      run += Ah * e_of(t);
+      const float e = e_of(t);
+      run += Ah * e;
       a.cum_A[base + (int64_t)t * a.H] = run;
+      if (a.e_out) a.e_out[base + (int64_t)t * a.H] = e;
     }
     if (w == 3) a.decay[(int64_t)r * a.H + h] = expf(run);
   }
 }
 
 // G_t = g_cum_t (+ g_decay decay at t = T-1);  R_s = sum_{t>=s} G_t;
-// g_e_s = A R_s;  g_A += sum_s R_s e_s;  g_dt_s = g_e_s softplus'(dt_s + bias)
+// g_e_s = A R_s (+ the direct g_e_s);  g_A += sum_s R_s e_s;  g_dt_s = g_e_s softplus'(dt_s + bias)
 // (or g_e_s);  g_bias += sum_s g_dt_s (softplus only).
 __global__ __launch_bounds__(256) void mamba2_dt_cumsum_bwd_kernel(const DtArgs a) {
   __shared__ float part[4][64];
@@ -119,7 +123,7 @@ __global__ __launch_bounds__(256) void mamba2_dt_cumsum_bwd_kernel(const DtArgs 
       const float x = dt_at(a, base + (int64_t)t * a.H);
       const float e = a.softplus ? softplus_t(x + bh) : x;
       pa += run * e;
-      const float ge = Ah * run;
+      const float ge = Ah * run + (a.g_e ? a.g_e[base + (int64_t)t * a.H] : 0.f);
       const float gdt = a.softplus ? ge * softplus_grad(x + bh) : ge;
       pb += gdt;
       a.g_dt[base + (int64_t)t * a.H] = gdt;
@@ -137,10 +141,10 @@ __global__ __launch_bounds__(256) void mamba2_dt_cumsum_bwd_kernel(const DtArgs 
 }
 
 hipError_t launch_mamba2_dt_cumsum(const void* dt, int dt_f32, const float* bias, const float* A,
-                                   int softplus, float* cum_A, float* decay, int rows, int T,
-                                   int H, hipStream_t stream) {
-  DtArgs a{dt, dt_f32, bias, A, softplus, cum_A, decay, nullptr, nullptr, nullptr, nullptr,
-           nullptr, rows, T, H};
+                                   int softplus, float* cum_A, float* e, float* decay, int rows,
+                                   int T, int H, hipStream_t stream) {
+  DtArgs a{dt, dt_f32, bias, A, softplus, cum_A, e, nullptr, decay, nullptr, nullptr, nullptr,
+           nullptr, nullptr, rows, T, H};
   const int64_t grid = (int64_t)rows * ((H + 63) / 64);
   if (grid == 0) return hipSuccess;
   hipLaunchKernelGGL(mamba2_dt_cumsum_kernel, dim3((unsigned)grid), dim3(256), 0, stream, a);
@@ -149,11 +153,11 @@ hipError_t launch_mamba2_dt_cumsum(const void* dt, int dt_f32, const float* bias
 
 hipError_t launch_mamba2_dt_cumsum_bwd(const void* dt, int dt_f32, const float* bias,
                                        const float* A, int softplus, const float* g_cum,
-                                       const float* g_decay, const float* decay, float* g_dt,
-                                       float* g_A, float* g_bias, int rows, int T, int H,
-                                       hipStream_t stream) {
-  DtArgs a{dt, dt_f32, bias, A, softplus, nullptr, const_cast<float*>(decay), g_cum, g_decay,
-           g_dt, g_A, g_bias, rows, T, H};
+                                       const float* g_e, const float* g_decay, const float* decay,
+                                       float* g_dt, float* g_A, float* g_bias, int rows, int T,
+                                       int H, hipStream_t stream) {
+  DtArgs a{dt, dt_f32, bias, A, softplus, nullptr, nullptr, g_e, const_cast<float*>(decay),
+           g_cum, g_decay, g_dt, g_A, g_bias, rows, T, H};
   const int64_t grid = (int64_t)rows * ((H + 63) / 64);
   if (grid == 0) return hipSuccess;
   hipLaunchKernelGGL(mamba2_dt_cumsum_bwd_kernel, dim3((unsigned)grid), dim3(256), 0, stream, a);

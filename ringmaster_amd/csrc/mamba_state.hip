@@ -1,0 +1,391 @@
+// Mamba2 per-shard final SSM state from x, B and dt: the final_states that
+// mamba-ssm's mamba_chunk_scan_combined returns for a zero initial state, which
+// the reference's CP scan wrapper all-gathers and carries across ranks
+// (mamba.py:113-141,160-172; strategies/mamba.py:250-300). Per row (rank shard x
+// batch) and head h of group g,
+//   S[h] = sum_{t0 <= t < T} w_t x_t (x) B_t,   w_t = exp(cum_A_{T-1} - cum_A_t) e_t
+// with e the effective dt (after bias and softplus) and cum_A = cumsum(A e), both
+// from rmx_mamba2_dt_cumsum; t0 is the first token of the row's last document (0
+// when unpacked), since the scan restarts its state at every document start. The
+// closed form is the SSD recurrence h_t = exp(A e_t) h_{t-1} + e_t x_t (x) B_t
+// unrolled. Like mamba-ssm's chunk-state kernel, the weight scales B in fp32 and
+// the product is rounded to bf16 before the MFMA; sums are fp32.
+//
+// Forward: a workgroup = 4 waves over one (row, head, token half). Each stage
+// stages 64 tokens of x and of w*B in LDS (rows padded so the transposed reads
+// are free of bank conflicts); both MFMA operands are token-major, so they come
+// from ds_read_b64_tr_b16 (S = X^T (wB): M = head dim, N = state, K = tokens).
+// Each wave owns D*N/4096 of the 32x32 output tiles, all in one row block.
+//
+// Backward (given G = dL/dS fp32): a workgroup = 8 waves x 32 tokens of one
+// (row, group); it loops over the group's heads, staging G_h in LDS as bf16:
+//   U   = B G_h^T            (MFMA M = head dim, N = tokens, K = state)
+//   g_x = w U,  g_w = <x, U>,  g_e = g_w exp(cum_A_{T-1} - cum_A_t),
+//   g_cum_A_t = -g_w w_t  (the t = T-1 entry is replaced by the caller with
+//   sum_{t<T-1} g_w w, the dependence of every weight on cum_A_{T-1})
+//   g_B += G_h^T (w x)       (MFMA M = state, N = tokens, K = head dim), summed
+//   over the group's heads in registers and written once.
+#include "rmx_kernels.h"
+
+namespace rmx {
+
+struct StateArgs {
+  const uint16_t* x;      // [rows, T, H, D] bf16
+  const uint16_t* B;      // [rows, T, G, N] bf16
+  const float* e;         // [rows, T, H]
+  const float* cum_A;     // [rows, T, H]
+  const int32_t* t0;      // [rows] or null
+  float* state;           // fwd out [rows, H, D, N]
+  const float* g_state;   // bwd in [rows, H, D, N]
+  uint16_t* g_x;          // bwd out [rows, T, H, D] bf16
+  uint16_t* g_B;          // bwd out [rows, T, G, N] bf16
+  float* g_e;             // bwd out [rows, T, H]
+  float* g_cum;           // bwd out [rows, T, H]
+  int rows, T, H, G;
+  int split;              // fwd: workgroups per (row, head) over the tokens
+};
+
+// LDS row stride (bytes) of a tile of `row_bytes` rows: every 4 consecutive rows
+// of a transposed read land on disjoint banks.
+template <int ROW_BYTES>
+constexpr int padded_stride() {
+  static_assert(ROW_BYTES == 128 || ROW_BYTES == 256, "rows of 64 or 128 bf16");
+  return ROW_BYTES == 128 ? ROW_BYTES + 16 : ROW_BYTES + 32;
+}
+
+// Transposed operand (8 tokens x column l32 of a 32-column block) of a row-major
+// bf16 LDS tile whose rows are tokens: rows r0 .. r0+7, columns c0 .. c0+31.
+template <int STRIDE>
+__device__ __forceinline__ bf16x8 tr_tokens(const uint8_t* tile, int r0, int c0, int lane) {
+  const int j = lane & 15, half = (lane >> 4) & 1;
+  const int row = r0 + 8 * (lane >> 5) + (j >> 2);
+  const uint8_t* p = tile + row * STRIDE + 2 * (c0 + 16 * half + 4 * (j & 3));
+  return join_bf16x8(lds_read_tr(reinterpret_cast<const uint16_t*>(p)),
+                     lds_read_tr(reinterpret_cast<const uint16_t*>(p + 4 * STRIDE)));
+}
+
+__device__ __forceinline__ u32x4 scale_bf16x8(const u32x4& v, float w) {
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = cvt_pk_bf16(__uint_as_float(v[i] << 16) * w, __uint_as_float(v[i] & 0xffff0000u) * w);
+  return o;
+}
+
+// ---------------------------------------------------------------- forward
+template <int D, int N>
+__global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs a) {
+  constexpr int TK = 64;                                // tokens per stage
+  constexpr int XS = padded_stride<2 * D>(), BS = padded_stride<2 * N>();
+  constexpr int NBN = N / 32;                           // 32-wide state blocks
+  constexpr int TPW = (D / 32) * NBN / 4;               // output tiles per wave
+  constexpr int XCH = TK * D / 8 / 256, BCH = TK * N / 8 / 256;  // 16-B chunks per thread
+  static_assert(TPW >= 1 && NBN % TPW == 0 && XCH >= 1 && BCH >= 1, "tile split");
+  __shared__ __attribute__((aligned(16))) uint8_t sX[TK * XS];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[TK * BS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int split = blockIdx.x % a.split;
+  const int rh = blockIdx.x / a.split;
+  const int h = rh % a.H, row = rh / a.H;
+  const int g = h / (a.H / a.G);
+  const int T = a.T;
+  // tokens of this workgroup: whole stages, the last split takes the remainder
+  const int nst = (T + TK - 1) / TK;
+  const int st_lo = (int)((int64_t)nst * split / a.split);
+  const int st_hi = (int)((int64_t)nst * (split + 1) / a.split);
+  const int t0 = a.t0 ? a.t0[row] : 0;
+  const int st_begin = st_lo > t0 / TK ? st_lo : t0 / TK;
+
+  const int64_t th = (int64_t)row * T * a.H + h;  // (row, t = 0, h) in [rows, T, H]
+  const float cl = a.cum_A[th + (int64_t)(T - 1) * a.H];
+  const i32x4 xrs = make_rsrc(a.x + (int64_t)row * T * a.H * D, (uint32_t)T * a.H * D * 2);
+  const i32x4 brs = make_rsrc(a.B + (int64_t)row * T * a.G * N, (uint32_t)T * a.G * N * 2);
+
+  u32x4 xr[XCH], br[BCH];
+  float wr[BCH];
+  auto load = [&](int st) {
+    const int tb = st * TK;
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = tid + 256 * i, t = tb + c / (D / 8);
+      xr[i] = buf_load16(xrs, ((t * a.H + h) * D + 8 * (c % (D / 8))) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i, t = tb + c / (N / 8);
+      br[i] = buf_load16(brs, ((t * a.G + g) * N + 8 * (c % (N / 8))) * 2);
+      const bool live = t >= t0 && t < T;
+      const int64_t o = th + (int64_t)(live ? t : 0) * a.H;
+      wr[i] = live ? a.e[o] : 0.f;
+      if (live) wr[i] *= expf(cl - a.cum_A[o]);
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = tid + 256 * i;
+      st16(sX + (c / (D / 8)) * XS + 16 * (c % (D / 8)), xr[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i;
+      st16(sB + (c / (N / 8)) * BS + 16 * (c % (N / 8)), scale_bf16x8(br[i], wr[i]));
+    }
+  };
+
+  const int mb = (wave * TPW) / NBN, nb0 = (wave * TPW) % NBN;
+  f32x16 acc[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) acc[i] = zero16();
+
+  if (st_begin < st_hi) load(st_begin);
+  for (int st = st_begin; st < st_hi; ++st) {
+    __syncthreads();  // the previous stage's reads are done
+    store();
+    __syncthreads();
+    if (st + 1 < st_hi) load(st + 1);
+#pragma unroll
+    for (int ks = 0; ks < TK / 16; ++ks) {
+      const bf16x8 av = tr_tokens<XS>(sX, 16 * ks, 32 * mb, lane);
+#pragma unroll
+      for (int i = 0; i < TPW; ++i)
+        acc[i] = mfma32(av, tr_tokens<BS>(sB, 16 * ks, 32 * (nb0 + i), lane), acc[i]);
+    }
+  }
+
+  // lane (hl, l32), reg r: d = 32 mb + c_row(hl, r), n = 32 nb + l32
+  const int hl = lane >> 5, l32 = lane & 31;
+  float* out = a.state + ((int64_t)row * a.H + h) * D * N;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float* p = out + (32 * mb + c_row(hl, r)) * N + 32 * (nb0 + i) + l32;
+      if (a.split == 1)
+        *p = acc[i][r];
+      else
+        atomicAdd(p, acc[i][r]);  // two splits onto zero: exact in either order
+    }
+}
+
+__global__ void zero_f32_kernel(float* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+// ---------------------------------------------------------------- backward
+template <int D, int N>
+__global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const StateArgs a) {
+  constexpr int NW = 8, NT = 64 * NW, BT = 32 * NW;  // 32 tokens per wave
+  constexpr int GS = 2 * N + 16;                     // LDS row stride of G (bf16)
+  constexpr int NMD = D / 32, NKN = N / 16;          // GEMM 1 (U): M blocks, k-steps
+  constexpr int NMN = N / 32, NKD = D / 16;          // GEMM 2 (g_B): M blocks, k-steps
+  constexpr int GCH = D * N / 8 / NT;                // 8-float chunks of G per thread
+  static_assert(GCH >= 1, "G split");
+  __shared__ __attribute__((aligned(16))) uint8_t sG[2][D * GS];
+
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nbt = (a.T + BT - 1) / BT;
+  const int bt = blockIdx.x % nbt;
+  const int rg = blockIdx.x / nbt;
+  const int g = rg % a.G, row = rg / a.G;
+  const int T = a.T, H = a.H, hpg = H / a.G;
+  const int t = bt * BT + 32 * wave + l32;  // this lane's token
+  const bool tv = t < T;
+  const int t0 = a.t0 ? a.t0[row] : 0;
+  const bool live = tv && t >= t0;
+
+  // B rows of this lane's token as the B operand of U (k = state n = 16 kb + 8 hl ..)
+  bf16x8 bop[NKN];
+  {
+    const i32x4 brs = make_rsrc(a.B + (int64_t)row * T * a.G * N, (uint32_t)T * a.G * N * 2);
+#pragma unroll
+    for (int kb = 0; kb < NKN; ++kb)
+      bop[kb] = __builtin_bit_cast(bf16x8, buf_load16(brs, ((t * a.G + g) * N + 16 * kb + 8 * hl) * 2));
+  }
+  const i32x4 xrs = make_rsrc(a.x + (int64_t)row * T * H * D, (uint32_t)T * H * D * 2);
+
+  f32x16 gb[NMN];
+#pragma unroll
+  for (int i = 0; i < NMN; ++i) gb[i] = zero16();
+
+  // G_h (fp32 [D][N]) -> bf16 LDS rows, through registers one head ahead
+  f32x4 gr[GCH][2];
+  auto load_g = [&](int h) {
+    const float* gp = a.g_state + ((int64_t)row * H + h) * D * N;
+#pragma unroll
+    for (int i = 0; i < GCH; ++i) {
+      const int c = tid + NT * i;
+      gr[i][0] = *reinterpret_cast<const f32x4*>(gp + 8 * c);
+      gr[i][1] = *reinterpret_cast<const f32x4*>(gp + 8 * c + 4);
+    }
+  };
+  auto store_g = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < GCH; ++i) {
+      const int c = tid + NT * i, d = c / (N / 8), n8 = c % (N / 8);
+      u32x4 u;
+      u[0] = cvt_pk_bf16(gr[i][0][0], gr[i][0][1]);
+      u[1] = cvt_pk_bf16(gr[i][0][2], gr[i][0][3]);
+      u[2] = cvt_pk_bf16(gr[i][1][0], gr[i][1][1]);
+      u[3] = cvt_pk_bf16(gr[i][1][2], gr[i][1][3]);
+      st16(sG[buf] + d * GS + 16 * n8, u);
+    }
+  };
+
+  const int h_first = g * hpg;
+  load_g(h_first);
+  for (int hi = 0; hi < hpg; ++hi) {
+    const int h = h_first + hi, buf = hi & 1;
+    store_g(buf);
+    __syncthreads();  // G_h visible; the reads of buffer buf from two heads ago are done
+    if (hi + 1 < hpg) load_g(h + 1);
+    const uint8_t* sg = sG[buf];
+
+    // weight of this lane's token for head h
+    const int64_t th = (int64_t)row * T * H + h;
+    const float cl = a.cum_A[th + (int64_t)(T - 1) * H];
+    const int64_t o = th + (int64_t)(tv ? t : 0) * H;
+    const float dec = live ? expf(cl - a.cum_A[o]) : 0.f;
+    const float w = live ? dec * a.e[o] : 0.f;
+
+    // U^T (d x tokens) = G_h B^T: A = G rows (LDS), B = this lane's B row
+    f32x16 u[NMD];
+#pragma unroll
+    for (int m = 0; m < NMD; ++m) {
+      u[m] = zero16();
+#pragma unroll
+      for (int kb = 0; kb < NKN; ++kb) {
+        const bf16x8 ga = __builtin_bit_cast(
+            bf16x8, ld16(sg + (32 * m + l32) * GS + 2 * (16 * kb + 8 * hl)));
+        u[m] = mfma32(ga, bop[kb], u[m]);
+      }
+    }
+    // lane (hl, l32) holds U[token t][d = 32 m + c_row(hl, r)]: g_x, g_w
+    float gw = 0.f;
+    const int xo = (t * H + h) * D;
+#pragma unroll
+    for (int m = 0; m < NMD; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int d = 32 * m + 8 * q + 4 * hl;  // regs 4q .. 4q+3 = d .. d+3
+        const u32x4 xv4 = buf_load16(xrs, (xo + (d & ~7)) * 2);
+        const uint32_t lo = (d & 4) ? xv4[2] : xv4[0], hi2 = (d & 4) ? xv4[3] : xv4[1];
+        const float x0 = __uint_as_float(lo << 16), x1 = __uint_as_float(lo & 0xffff0000u);
+        const float x2 = __uint_as_float(hi2 << 16), x3 = __uint_as_float(hi2 & 0xffff0000u);
+        gw += x0 * u[m][4 * q] + x1 * u[m][4 * q + 1] + x2 * u[m][4 * q + 2] + x3 * u[m][4 * q + 3];
+        if (tv) {
+          u32x2 s;
+          s[0] = cvt_pk_bf16(w * u[m][4 * q], w * u[m][4 * q + 1]);
+          s[1] = cvt_pk_bf16(w * u[m][4 * q + 2], w * u[m][4 * q + 3]);
+          *reinterpret_cast<u32x2*>(a.g_x + (int64_t)row * T * H * D + xo + d) = s;
+        }
+      }
+    gw += xhalf(gw);
+    if (tv && hl == 0) {
+      a.g_e[o] = gw * dec;
+      a.g_cum[o] = -gw * w;
+    }
+
+    // g_B^T (state x tokens) += G_h^T (w x)^T: A = G^T by transposed reads, B = w x
+    bf16x8 wx[NKD];
+#pragma unroll
+    for (int kb = 0; kb < NKD; ++kb)
+      wx[kb] = __builtin_bit_cast(bf16x8, scale_bf16x8(buf_load16(xrs, (xo + 16 * kb + 8 * hl) * 2), w));
+#pragma unroll
+    for (int m = 0; m < NMN; ++m)
+#pragma unroll
+      for (int kb = 0; kb < NKD; ++kb)
+        gb[m] = mfma32(tr_tokens<GS>(sg, 16 * kb, 32 * m, lane), wx[kb], gb[m]);
+  }
+
+  // lane (hl, l32) holds g_B[token t][n = 32 m + c_row(hl, r)]
+  if (tv) {
+    uint16_t* gbp = a.g_B + ((int64_t)row * T * a.G + (int64_t)t * a.G + g) * N;
+#pragma unroll
+    for (int m = 0; m < NMN; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        u32x2 s;
+        s[0] = cvt_pk_bf16(gb[m][4 * q], gb[m][4 * q + 1]);
+        s[1] = cvt_pk_bf16(gb[m][4 * q + 2], gb[m][4 * q + 3]);
+        *reinterpret_cast<u32x2*>(gbp + 32 * m + 8 * q + 4 * hl) = s;
+      }
+  }
+}
+
+// ---------------------------------------------------------------- launchers
+template <int D, int N>
+static void launch_fwd_dn(const StateArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((mamba2_chunk_state_kernel<D, N>), dim3((unsigned)(a.rows * a.H * a.split)),
+                     dim3(256), 0, stream, a);
+}
+template <int D, int N>
+static void launch_bwd_dn(const StateArgs& a, hipStream_t stream) {
+  const int nbt = (a.T + 255) / 256;
+  hipLaunchKernelGGL((mamba2_chunk_state_bwd_kernel<D, N>), dim3((unsigned)(a.rows * a.G * nbt)),
+                     dim3(512), 0, stream, a);
+}
+
+#define RMX_STATE_DISPATCH(FN, D, N, A, S)         \
+  if ((D) == 64 && (N) == 64) FN<64, 64>(A, S);    \
+  else if ((D) == 64 && (N) == 128) FN<64, 128>(A, S); \
+  else if ((D) == 128 && (N) == 64) FN<128, 64>(A, S); \
+  else FN<128, 128>(A, S);
+
+hipError_t launch_mamba2_chunk_state(const uint16_t* x, const uint16_t* B, const float* e,
+                                     const float* cum_A, const int32_t* t0, float* state,
+                                     int rows, int T, int H, int D, int G, int N,
+                                     hipStream_t stream) {
+  StateArgs a{};
+  a.x = x;
+  a.B = B;
+  a.e = e;
+  a.cum_A = cum_A;
+  a.t0 = t0;
+  a.state = state;
+  a.rows = rows;
+  a.T = T;
+  a.H = H;
+  a.G = G;
+  // a second workgroup per (row, head) when fewer than 4 per CU would run
+  a.split = ((int64_t)rows * H < 1024 && T >= 1024) ? 2 : 1;
+  if (a.split == 2 || T == 0) {  // atomically summed halves / the empty shard's zero state
+    const int64_t n = (int64_t)rows * H * D * N;
+    hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       state, n);
+    if (T == 0) return hipGetLastError();
+  }
+  RMX_STATE_DISPATCH(launch_fwd_dn, D, N, a, stream)
+  return hipGetLastError();
+}
+
+hipError_t launch_mamba2_chunk_state_bwd(const uint16_t* x, const uint16_t* B, const float* e,
+                                         const float* cum_A, const int32_t* t0,
+                                         const float* g_state, uint16_t* g_x, uint16_t* g_B,
+                                         float* g_e, float* g_cum, int rows, int T, int H, int D,
+                                         int G, int N, hipStream_t stream) {
+  StateArgs a{};
+  a.x = x;
+  a.B = B;
+  a.e = e;
+  a.cum_A = cum_A;
+  a.t0 = t0;
+  a.g_state = g_state;
+  a.g_x = g_x;
+  a.g_B = g_B;
+  a.g_e = g_e;
+  a.g_cum = g_cum;
+  a.rows = rows;
+  a.T = T;
+  a.H = H;
+  a.G = G;
+  a.split = 1;
+  RMX_STATE_DISPATCH(launch_bwd_dn, D, N, a, stream)
+  return hipGetLastError();
+}
+
+}  // namespace rmx

@@ -42,13 +42,22 @@ hipError_t launch_mamba2_correction_bwd(const uint16_t* gy, const float* ghf, co
                                         int nheads, int head_dim, int ngroups, int d_state,
                                         hipStream_t stream);
 hipError_t launch_mamba2_dt_cumsum(const void* dt, int dt_f32, const float* bias, const float* A,
-                                   int softplus, float* cum_A, float* decay, int rows, int T,
-                                   int H, hipStream_t stream);
+                                   int softplus, float* cum_A, float* e, float* decay, int rows,
+                                   int T, int H, hipStream_t stream);
 hipError_t launch_mamba2_dt_cumsum_bwd(const void* dt, int dt_f32, const float* bias,
                                        const float* A, int softplus, const float* g_cum,
-                                       const float* g_decay, const float* decay, float* g_dt,
-                                       float* g_A, float* g_bias, int rows, int T, int H,
-                                       hipStream_t stream);
+                                       const float* g_e, const float* g_decay, const float* decay,
+                                       float* g_dt, float* g_A, float* g_bias, int rows, int T,
+                                       int H, hipStream_t stream);
+hipError_t launch_mamba2_chunk_state(const uint16_t* x, const uint16_t* B, const float* e,
+                                     const float* cum_A, const int32_t* t0, float* state,
+                                     int rows, int T, int H, int D, int G, int N,
+                                     hipStream_t stream);
+hipError_t launch_mamba2_chunk_state_bwd(const uint16_t* x, const uint16_t* B, const float* e,
+                                         const float* cum_A, const int32_t* t0,
+                                         const float* g_state, uint16_t* g_x, uint16_t* g_B,
+                                         float* g_e, float* g_cum, int rows, int T, int H, int D,
+                                         int G, int N, hipStream_t stream);
 hipError_t launch_causal_conv1d_cp(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                                    const int32_t* doc, uint16_t* y, int world, int batch, int C,
                                    int L, int W, int act, hipStream_t stream);

@@ -86,32 +86,40 @@ def cp_state_prefix(ssm_states: torch.Tensor, chunk_decays: torch.Tensor, *,
 
 
 class _DtCumsum(torch.autograd.Function):
+    """(cum_A, decay, e) from dt; e (the effective dt) only when ``want_e``."""
+
     @staticmethod
-    def forward(ctx, dt, A, dt_bias, softplus):
+    def forward(ctx, dt, A, dt_bias, softplus, want_e):
         rows, T, H = dt.shape
         cum = torch.empty((rows, T, H), dtype=torch.float32, device=dt.device)
         decay = torch.empty((rows, H), dtype=torch.float32, device=dt.device)
+        e = torch.empty((rows, T, H) if want_e else (0,), dtype=torch.float32, device=dt.device)
         abi.check(abi.lib().rmx_mamba2_dt_cumsum(
             dt.data_ptr(), int(dt.dtype == torch.float32), abi.ptr(dt_bias), A.data_ptr(),
-            int(softplus), cum.data_ptr(), decay.data_ptr(), rows, T, H, abi.stream_of(dt)))
+            int(softplus), cum.data_ptr(), e.data_ptr() if want_e else None, decay.data_ptr(),
+            rows, T, H, abi.stream_of(dt)))
         ctx.save_for_backward(dt, A, dt_bias, decay)
         ctx.softplus = softplus
-        return cum, decay
+        ctx.set_materialize_grads(False)
+        return cum, decay, e
 
     @staticmethod
-    def backward(ctx, g_cum, g_decay):
+    def backward(ctx, g_cum, g_decay, g_e):
         dt, A, dt_bias, decay = ctx.saved_tensors
         rows, T, H = dt.shape
+        if g_cum is None and g_decay is None and g_e is None:
+            return None, None, None, None, None
         g_cum = None if g_cum is None else g_cum.contiguous().float()
         g_decay = None if g_decay is None else g_decay.contiguous().float()
+        g_e = None if g_e is None or g_e.numel() == 0 else g_e.contiguous().float()
         g_dt = torch.empty((rows, T, H), dtype=torch.float32, device=dt.device)
         g_A = torch.zeros(H, dtype=torch.float32, device=dt.device)
         g_b = torch.zeros(H, dtype=torch.float32, device=dt.device) if dt_bias is not None else None
         abi.check(abi.lib().rmx_mamba2_dt_cumsum_bwd(
             dt.data_ptr(), int(dt.dtype == torch.float32), abi.ptr(dt_bias), A.data_ptr(),
-            int(ctx.softplus), abi.ptr(g_cum), abi.ptr(g_decay), decay.data_ptr(),
+            int(ctx.softplus), abi.ptr(g_cum), abi.ptr(g_e), abi.ptr(g_decay), decay.data_ptr(),
             g_dt.data_ptr(), g_A.data_ptr(), abi.ptr(g_b), rows, T, H, abi.stream_of(dt)))
-        return g_dt.to(dt.dtype), g_A, g_b, None
+        return g_dt.to(dt.dtype), g_A, g_b, None, None
 
 
 def mamba2_chunk_decay(dt: torch.Tensor, A: torch.Tensor, dt_bias: torch.Tensor | None = None,
@@ -134,8 +142,88 @@ def mamba2_chunk_decay(dt: torch.Tensor, A: torch.Tensor, dt_bias: torch.Tensor 
     b32 = None
     if dt_softplus and dt_bias is not None:
         b32 = dt_bias.float().contiguous()
-    cum, decay = _DtCumsum.apply(d3, A32, b32, bool(dt_softplus))
+    cum, decay, _ = _DtCumsum.apply(d3, A32, b32, bool(dt_softplus), False)
     return cum.reshape(*lead, T, H), decay.reshape(*lead, H)
+
+
+class _ChunkState(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, B, e, cum_A, t0):
+        rows, T, H, D = x.shape
+        G, N = B.shape[2], B.shape[3]
+        state = torch.empty((rows, H, D, N), dtype=torch.float32, device=x.device)
+        abi.check(abi.lib().rmx_mamba2_chunk_state(
+            x.data_ptr(), B.data_ptr(), e.data_ptr(), cum_A.data_ptr(), abi.ptr(t0),
+            state.data_ptr(), rows, T, H, D, G, N, abi.stream_of(x)))
+        ctx.save_for_backward(x, B, e, cum_A, t0)
+        return state
+
+    @staticmethod
+    def backward(ctx, g):
+        x, B, e, cum_A, t0 = ctx.saved_tensors
+        rows, T, H, D = x.shape
+        G, N = B.shape[2], B.shape[3]
+        g = g.contiguous().float()
+        g_x, g_B = torch.empty_like(x), torch.empty_like(B)
+        g_e = torch.empty((rows, T, H), dtype=torch.float32, device=x.device)
+        g_cum = torch.empty_like(g_e)
+        abi.check(abi.lib().rmx_mamba2_chunk_state_bwd(
+            x.data_ptr(), B.data_ptr(), e.data_ptr(), cum_A.data_ptr(), abi.ptr(t0),
+            g.data_ptr(), g_x.data_ptr(), g_B.data_ptr(), g_e.data_ptr(), g_cum.data_ptr(),
+            rows, T, H, D, G, N, abi.stream_of(x)))
+        if T:
+            # every weight exp(cum_A[T-1] - cum_A[t]) also depends on cum_A[T-1]
+            g_cum[:, T - 1] = -g_cum[:, :T - 1].sum(1)
+        return g_x, g_B, g_e, g_cum, None
+
+
+def last_document_start(seq_idx: torch.Tensor) -> torch.Tensor:
+    """First token of each row's last document (int32 [rows]) from per-token document
+    ids ``[rows, T]``, on the device and without a synchronization."""
+    T = seq_idx.shape[-1]
+    pos = torch.arange(1, T + 1, device=seq_idx.device, dtype=torch.int32)
+    return ((seq_idx != seq_idx[:, -1:]).to(torch.int32) * pos).amax(1).to(torch.int32)
+
+
+def mamba2_chunk_state(x: torch.Tensor, dt: torch.Tensor, A: torch.Tensor, B: torch.Tensor, *,
+                       dt_bias: torch.Tensor | None = None, dt_softplus: bool = False,
+                       seq_idx: torch.Tensor | None = None) -> torch.Tensor:
+    """Final SSM state of each shard's scan from a zero state: the ``final_states`` of
+    mamba-ssm's ``mamba_chunk_scan_combined(..., return_final_states=True)`` that the
+    reference's CP wrapper gathers across ranks (mamba.py:113-141 and :160-172;
+    strategies/mamba.py:250-300). ``state[h] = sum_t exp(cum_A[T-1] - cum_A[t]) e_t
+    x_t (x) B_t`` over the last document's tokens (all tokens when ``seq_idx`` is None),
+    with ``e = softplus(dt + dt_bias)`` when ``dt_softplus`` (else ``dt``) and
+    ``cum_A = cumsum(A e)``. ``x`` bf16 ``[..., T, H, D]``, ``dt`` ``[..., T, H]``,
+    ``A`` ``[H]``, ``B`` bf16 ``[..., T, G, N]``, ``seq_idx`` int ``[..., T]``; returns
+    fp32 ``[..., H, D, N]``, differentiable in x, B, dt, A and dt_bias. D, N in {64, 128}."""
+    abi.require_device(x, dt, A, B)
+    if x.dim() < 3 or B.dim() != x.dim() or dt.dim() != x.dim() - 1:
+        raise ValueError("x must be [..., T, H, D], B [..., T, G, N] and dt [..., T, H]")
+    lead, (T, H, D) = x.shape[:-3], x.shape[-3:]
+    G, N = B.shape[-2:]
+    if tuple(B.shape[:-2]) != (*lead, T) or tuple(dt.shape) != (*lead, T, H):
+        raise ValueError("x, dt and B disagree on the batch or token axes")
+    if A.dim() != 1 or A.shape[0] != H or H % G:
+        raise ValueError("A must be [nheads] and nheads a multiple of ngroups")
+    if x.dtype != torch.bfloat16 or B.dtype != torch.bfloat16:
+        raise NotImplementedError("the MI355X shard state takes bf16 x and B")
+    if dt.dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError("dt must be bf16 or fp32")
+    if D not in (64, 128) or N not in (64, 128):
+        raise NotImplementedError("head_dim and d_state must be 64 or 128")
+    x3 = x.reshape(-1, T, H, D).contiguous()
+    B3 = B.reshape(-1, T, G, N).contiguous()
+    d3 = dt.reshape(-1, T, H).contiguous()
+    b32 = dt_bias.float().contiguous() if (dt_softplus and dt_bias is not None) else None
+    cum, _, e = _DtCumsum.apply(d3, A.float().contiguous(), b32, bool(dt_softplus), True)
+    t0 = None
+    if seq_idx is not None:
+        if tuple(seq_idx.shape) != (*lead, T):
+            raise ValueError("seq_idx must be [..., T]")
+        t0 = last_document_start(seq_idx.reshape(-1, T))
+    state = _ChunkState.apply(x3, B3, e, cum, t0)
+    return state.reshape(*lead, H, D, N)
 
 
 def mamba2_cp_apply(scan_output: torch.Tensor, ssm_state: torch.Tensor, dt: torch.Tensor,

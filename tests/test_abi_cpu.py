@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 6
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 7
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -118,3 +118,26 @@ def test_product_refuses_cpu_tensors():
     with pytest.raises(RuntimeError, match="ROCm device"):
         zigzag_ring_attention(q[None].transpose(2, 3), q[None].transpose(2, 3),
                               q[None].transpose(2, 3))
+
+
+def test_host_validation_chunk_state():
+    lib = abi.lib()
+    p = 16  # any 16-byte aligned non-null value: validation fails before a launch
+    # head_dim / d_state outside {64, 128}, heads not a multiple of groups, bad rows
+    assert lib.rmx_mamba2_chunk_state(p, p, p, p, None, p, 1, 8, 4, 32, 1, 64, None) \
+        == abi.RMX_EUNSUPPORTED
+    assert lib.rmx_mamba2_chunk_state(p, p, p, p, None, p, 1, 8, 4, 64, 1, 96, None) \
+        == abi.RMX_EUNSUPPORTED
+    assert lib.rmx_mamba2_chunk_state(p, p, p, p, None, p, 1, 8, 6, 64, 4, 64, None) \
+        == abi.RMX_EINVAL
+    assert lib.rmx_mamba2_chunk_state(p, p, p, p, None, p, -1, 8, 4, 64, 1, 64, None) \
+        == abi.RMX_EINVAL
+    assert lib.rmx_mamba2_chunk_state(8, p, p, p, None, p, 1, 8, 4, 64, 1, 64, None) \
+        == abi.RMX_EINVAL  # x not 16-byte aligned
+    assert lib.rmx_mamba2_chunk_state_bwd(p, p, p, p, None, None, p, p, p, p, 1, 8, 4, 64, 1, 64,
+                                          None) == abi.RMX_EINVAL  # no g_state
+    # empty problems are no-ops
+    assert lib.rmx_mamba2_chunk_state(None, None, None, None, None, None, 0, 8, 4, 64, 1, 64,
+                                      None) == abi.RMX_OK
+    assert lib.rmx_mamba2_chunk_state_bwd(None, None, None, None, None, None, None, None, None,
+                                          None, 2, 0, 4, 64, 1, 64, None) == abi.RMX_OK

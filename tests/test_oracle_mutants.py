@@ -162,3 +162,30 @@ def test_contiguous_ring_mutants_are_caught(monkeypatch, mutation):
         monkeypatch.setattr(rm, "contiguous_ring_forward", leaky)
     with pytest.raises(AssertionError):
         pin.check_contiguous(4, 3)
+
+
+@pytest.mark.parametrize("mutation", ["decay_sign", "no_dt", "ignore_t0", "decay_from_start"])
+def test_chunk_state_mutants_are_caught(monkeypatch, mutation):
+    """Plausible slips in the shard-state closed form (decay exponent reversed, the dt
+    factor dropped, the document start ignored, decay measured from the shard start)
+    fail its pinning against the SSD recurrence."""
+
+    def mutant(x, B, e, cum_A, t0=None):
+        bsz, T, H, _ = x.shape
+        if mutation == "decay_sign":
+            w = torch.exp(cum_A - cum_A[:, -1:, :]) * e
+        elif mutation == "no_dt":
+            w = torch.exp(cum_A[:, -1:, :] - cum_A)
+        elif mutation == "decay_from_start":
+            w = torch.exp(cum_A) * e
+        else:
+            w = torch.exp(cum_A[:, -1:, :] - cum_A) * e
+        if t0 is not None and mutation != "ignore_t0":
+            keep = torch.arange(T)[None, :] >= torch.as_tensor(t0).reshape(bsz, 1)
+            w = w * keep[:, :, None].to(w.dtype)
+        Bx = B.repeat_interleave(H // B.shape[2], dim=2)
+        return torch.einsum("bth,bthd,bthn->bhdn", w, x, Bx)
+
+    monkeypatch.setattr(sp, "chunk_state", mutant)
+    with pytest.raises(AssertionError):
+        pin.test_chunk_state_equals_ssd_final_state(2)

@@ -455,3 +455,48 @@ def test_mamba2_correction_backward_pinned(seq_kind):
         dH = dH + el[..., None, None] * ghf
     for got, ref in zip(grads, (dC, dA, dH)):
         assert (got - ref).abs().max().item() <= 1e-4 * max(1.0, ref.abs().max().item())
+
+
+@pytest.mark.parametrize("G", [1, 2])
+def test_chunk_state_equals_ssd_final_state(G):
+    """The closed-form shard state equals the SSD recurrence's final state, and with a
+    document start t0 the state of the last document run alone (the scan restarts)."""
+    torch.manual_seed(3)
+    b, T, H, d, n = 2, 24, 4, 3, 5
+    x = torch.randn(b, T, H, d, dtype=torch.float64)
+    e = torch.rand(b, T, H, dtype=torch.float64) * 0.3
+    A = -torch.rand(H, dtype=torch.float64) - 0.2
+    B = torch.randn(b, T, G, n, dtype=torch.float64)
+    C = torch.randn(b, T, G, n, dtype=torch.float64)
+    cum = torch.cumsum(A[None, None, :] * e, dim=1)
+    _, h_ref = sp.ssd_reference(x, e, A, B, C)
+    assert (sp.chunk_state(x, B, e, cum) - h_ref).abs().max().item() < 1e-12
+    t0 = torch.tensor([7, 0])
+    got = sp.chunk_state(x, B, e, cum, t0)
+    for r in range(b):
+        lo = int(t0[r])
+        _, h = sp.ssd_reference(x[r:r + 1, lo:], e[r:r + 1, lo:], A, B[r:r + 1, lo:],
+                                C[r:r + 1, lo:])
+        assert (got[r] - h[0]).abs().max().item() < 1e-12
+
+
+def test_chunk_state_gradients_equal_recurrence_gradients():
+    """Gradients of the closed form (through cum_A = cumsum(A e), e = softplus(dt + bias))
+    equal autograd through the SSD recurrence w.r.t. x, B, dt, A and dt_bias."""
+    torch.manual_seed(4)
+    b, T, H, d, G, n = 1, 12, 2, 3, 1, 4
+    x = torch.randn(b, T, H, d, dtype=torch.float64, requires_grad=True)
+    B = torch.randn(b, T, G, n, dtype=torch.float64, requires_grad=True)
+    C = torch.randn(b, T, G, n, dtype=torch.float64)
+    dt = (torch.randn(b, T, H, dtype=torch.float64) - 1.5).requires_grad_(True)
+    bias = (torch.randn(H, dtype=torch.float64) * 0.1).requires_grad_(True)
+    A = (-torch.rand(H, dtype=torch.float64) - 0.2).requires_grad_(True)
+    cum, _ = sp.chunk_decay(dt, A, bias, True)
+    e = torch.nn.functional.softplus(dt + bias)
+    S = sp.chunk_state(x, B, e, cum)
+    _, h_ref = sp.ssd_reference(x, e, A, B, C)
+    gw = torch.randn_like(S)
+    gs = torch.autograd.grad((S * gw).sum(), (x, B, dt, A, bias), retain_graph=True)
+    rs = torch.autograd.grad((h_ref * gw).sum(), (x, B, dt, A, bias))
+    for g, r in zip(gs, rs):
+        assert (g - r).abs().max().item() < 1e-10
