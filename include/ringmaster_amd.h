@@ -297,7 +297,7 @@ int32_t rmx_mamba2_dt_cumsum_bwd(const void* dt, int32_t dt_is_f32, const float*
  *   state[r,h] = sum_{t0[r] <= t < T} exp(cum_A[r,T-1,h] - cum_A[r,t,h]) e[r,t,h]
  *                x[r,t,h,:] (x) B[r,t,g,:]
  * (the SSD recurrence h_t = exp(A e_t) h_{t-1} + e_t x_t (x) B_t unrolled; the
- * weighted B is rounded to bf16 like mamba-ssm's chunk-state kernel, sums fp32).
+ * weighted x is rounded to bf16 before the MFMA, sums fp32).
  * x bf16 [rows, T, H, head_dim]; B bf16 [rows, T, G, d_state]; e, cum_A fp32
  * [rows, T, H] (from rmx_mamba2_dt_cumsum); t0 int32 [rows] (nullable: 0), the
  * first token of each row's last document; state fp32 [rows, H, head_dim,

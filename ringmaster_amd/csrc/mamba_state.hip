@@ -8,13 +8,14 @@
 // from rmx_mamba2_dt_cumsum; t0 is the first token of the row's last document (0
 // when unpacked), since the scan restarts its state at every document start. The
 // closed form is the SSD recurrence h_t = exp(A e_t) h_{t-1} + e_t x_t (x) B_t
-// unrolled. Like mamba-ssm's chunk-state kernel, the weight scales B in fp32 and
-// the product is rounded to bf16 before the MFMA; sums are fp32.
+// unrolled. The weight scales x in fp32 and the product is rounded to bf16 before
+// the MFMA (mamba-ssm's chunk-state kernel scales B instead: the two differ by the
+// bf16 rounding of one factor of each product); sums are fp32.
 //
 // Forward: a workgroup = 4 waves over one (row, head, token half). Each stage
-// stages 64 tokens of x and of w*B in LDS (rows padded so the transposed reads
+// stages 64 tokens of w*x and of B in LDS (rows padded so the transposed reads
 // are free of bank conflicts); both MFMA operands are token-major, so they come
-// from ds_read_b64_tr_b16 (S = X^T (wB): M = head dim, N = state, K = tokens).
+// from ds_read_b64_tr_b16 (S = (wX)^T B: M = head dim, N = state, K = tokens).
 // Each wave owns D*N/4096 of the 32x32 output tiles, all in one row block.
 //
 // Backward (given G = dL/dS fp32): a workgroup = 8 waves x 32 tokens of one
@@ -45,12 +46,13 @@ struct StateArgs {
   int split;              // fwd: workgroups per (row, head) over the tokens
 };
 
-// LDS row stride (bytes) of a tile of `row_bytes` rows: every 4 consecutive rows
-// of a transposed read land on disjoint banks.
+// LDS row stride (bytes) of a tile of `row_bytes` rows: a stride of 16 banks
+// (mod 64) puts the 8 reads of 8 bytes that 32 lanes of a transposed read make
+// (4 rows x 2 column halves) on disjoint banks.
 template <int ROW_BYTES>
 constexpr int padded_stride() {
   static_assert(ROW_BYTES == 128 || ROW_BYTES == 256, "rows of 64 or 128 bf16");
-  return ROW_BYTES == 128 ? ROW_BYTES + 16 : ROW_BYTES + 32;
+  return ROW_BYTES + 64;
 }
 
 // Transposed operand (8 tokens x column l32 of a 32-column block) of a row-major
@@ -62,6 +64,21 @@ __device__ __forceinline__ bf16x8 tr_tokens(const uint8_t* tile, int r0, int c0,
   const uint8_t* p = tile + row * STRIDE + 2 * (c0 + 16 * half + 4 * (j & 3));
   return join_bf16x8(lds_read_tr(reinterpret_cast<const uint16_t*>(p)),
                      lds_read_tr(reinterpret_cast<const uint16_t*>(p + 4 * STRIDE)));
+}
+
+// The same operand from a tile of unpadded RB-byte rows whose 16-byte chunk p of
+// row r sits at p ^ swz_both<RB / 2>(r), the swizzle that keeps both the 16-byte
+// row reads of 16 consecutive rows and these transposed reads free of conflicts.
+template <int RB>
+__device__ __forceinline__ bf16x8 tr_tokens_swz(const uint8_t* tile, int r0, int c0, int lane) {
+  const int j = lane & 15, half = (lane >> 4) & 1;
+  const int row = r0 + 8 * (lane >> 5) + (j >> 2);
+  const int col = c0 + 16 * half + 4 * (j & 3);
+  const int p = col >> 3, sub = 2 * (col & 7);
+  const uint8_t* p0 = tile + row * RB + 16 * (p ^ swz_both<RB / 2>(row)) + sub;
+  const uint8_t* p1 = tile + (row + 4) * RB + 16 * (p ^ swz_both<RB / 2>(row + 4)) + sub;
+  return join_bf16x8(lds_read_tr(reinterpret_cast<const uint16_t*>(p0)),
+                     lds_read_tr(reinterpret_cast<const uint16_t*>(p1)));
 }
 
 __device__ __forceinline__ u32x4 scale_bf16x8(const u32x4& v, float w) {
@@ -86,9 +103,15 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int split = blockIdx.x % a.split;
-  const int rh = blockIdx.x / a.split;
-  const int h = rh % a.H, row = rh / a.H;
+  // Workgroups go to the 8 XCDs round-robin. Give each XCD a contiguous run of
+  // (row, split, head) ordinals, head fastest, so the heads that read the same B
+  // rows run together on one XCD and find them in its L2.
+  const int nwg = gridDim.x;
+  const int k = (nwg % 8 == 0) ? (int)(blockIdx.x % 8) * (nwg / 8) + (int)(blockIdx.x / 8)
+                               : (int)blockIdx.x;
+  const int h = k % a.H;
+  const int split = (k / a.H) % a.split;
+  const int row = k / (a.H * a.split);
   const int g = h / (a.H / a.G);
   const int T = a.T;
   // tokens of this workgroup: whole stages, the last split takes the remainder
@@ -103,35 +126,40 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
   const i32x4 xrs = make_rsrc(a.x + (int64_t)row * T * a.H * D, (uint32_t)T * a.H * D * 2);
   const i32x4 brs = make_rsrc(a.B + (int64_t)row * T * a.G * N, (uint32_t)T * a.G * N * 2);
 
-  u32x4 xr[XCH], br[BCH];
-  float wr[BCH];
-  auto load = [&](int st) {
+  // Two stages of loads in flight: register sets 0 and 1 hold stages of even and
+  // odd parity. The weights are formed at the store, so issuing loads never waits.
+  struct Regs {
+    u32x4 x[XCH], b[BCH];
+    float e[XCH], c[XCH];
+  };
+  Regs rg[2];
+  auto load = [&](int st, Regs& r) __attribute__((always_inline)) {
     const int tb = st * TK;
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
       const int c = tid + 256 * i, t = tb + c / (D / 8);
-      xr[i] = buf_load16(xrs, ((t * a.H + h) * D + 8 * (c % (D / 8))) * 2);
+      r.x[i] = buf_load16(xrs, ((t * a.H + h) * D + 8 * (c % (D / 8))) * 2);
+      const int64_t o = th + (int64_t)(t < T ? t : T - 1) * a.H;
+      r.e[i] = a.e[o];
+      r.c[i] = a.cum_A[o];
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
       const int c = tid + 256 * i, t = tb + c / (N / 8);
-      br[i] = buf_load16(brs, ((t * a.G + g) * N + 8 * (c % (N / 8))) * 2);
-      const bool live = t >= t0 && t < T;
-      const int64_t o = th + (int64_t)(live ? t : 0) * a.H;
-      wr[i] = live ? a.e[o] : 0.f;
-      if (live) wr[i] *= expf(cl - a.cum_A[o]);
+      r.b[i] = buf_load16(brs, ((t * a.G + g) * N + 8 * (c % (N / 8))) * 2);
     }
   };
-  auto store = [&]() {
+  auto store = [&](int st, const Regs& r) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int c = tid + 256 * i;
-      st16(sX + (c / (D / 8)) * XS + 16 * (c % (D / 8)), xr[i]);
+      const int c = tid + 256 * i, t = st * TK + c / (D / 8);
+      const float w = (t >= t0 && t < T) ? r.e[i] * expf(cl - r.c[i]) : 0.f;
+      st16(sX + (c / (D / 8)) * XS + 16 * (c % (D / 8)), scale_bf16x8(r.x[i], w));
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
       const int c = tid + 256 * i;
-      st16(sB + (c / (N / 8)) * BS + 16 * (c % (N / 8)), scale_bf16x8(br[i], wr[i]));
+      st16(sB + (c / (N / 8)) * BS + 16 * (c % (N / 8)), r.b[i]);
     }
   };
 
@@ -139,13 +167,7 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
   f32x16 acc[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) acc[i] = zero16();
-
-  if (st_begin < st_hi) load(st_begin);
-  for (int st = st_begin; st < st_hi; ++st) {
-    __syncthreads();  // the previous stage's reads are done
-    store();
-    __syncthreads();
-    if (st + 1 < st_hi) load(st + 1);
+  auto compute = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < TK / 16; ++ks) {
       const bf16x8 av = tr_tokens<XS>(sX, 16 * ks, 32 * mb, lane);
@@ -153,6 +175,20 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
       for (int i = 0; i < TPW; ++i)
         acc[i] = mfma32(av, tr_tokens<BS>(sB, 16 * ks, 32 * (nb0 + i), lane), acc[i]);
     }
+  };
+  auto stage = [&](int st, Regs& r) __attribute__((always_inline)) {
+    __syncthreads();  // the previous stage's reads are done
+    store(st, r);
+    __syncthreads();
+    if (st + 2 < st_hi) load(st + 2, r);
+    compute();
+  };
+
+  if (st_begin < st_hi) load(st_begin, rg[0]);
+  if (st_begin + 1 < st_hi) load(st_begin + 1, rg[1]);
+  for (int st = st_begin; st < st_hi; st += 2) {
+    stage(st, rg[0]);
+    if (st + 1 < st_hi) stage(st + 1, rg[1]);
   }
 
   // lane (hl, l32), reg r: d = 32 mb + c_row(hl, r), n = 32 nb + l32
@@ -179,7 +215,7 @@ __global__ void zero_f32_kernel(float* p, int64_t n) {
 template <int D, int N>
 __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const StateArgs a) {
   constexpr int NW = 8, NT = 64 * NW, BT = 32 * NW;  // 32 tokens per wave
-  constexpr int GS = 2 * N + 16;                     // LDS row stride of G (bf16)
+  constexpr int GS = 2 * N;                          // LDS row bytes of G (bf16, swizzled)
   constexpr int NMD = D / 32, NKN = N / 16;          // GEMM 1 (U): M blocks, k-steps
   constexpr int NMN = N / 32, NKD = D / 16;          // GEMM 2 (g_B): M blocks, k-steps
   constexpr int GCH = D * N / 8 / NT;                // 8-float chunks of G per thread
@@ -232,25 +268,38 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
       u[1] = cvt_pk_bf16(gr[i][0][2], gr[i][0][3]);
       u[2] = cvt_pk_bf16(gr[i][1][0], gr[i][1][1]);
       u[3] = cvt_pk_bf16(gr[i][1][2], gr[i][1][3]);
-      st16(sG[buf] + d * GS + 16 * n8, u);
+      st16(sG[buf] + d * GS + 16 * (n8 ^ swz_both<N>(d)), u);
     }
   };
 
-  const int h_first = g * hpg;
-  load_g(h_first);
-  for (int hi = 0; hi < hpg; ++hi) {
-    const int h = h_first + hi, buf = hi & 1;
+  // per-head operands of this lane's token, loaded one head ahead: x[t, h, 16 kb +
+  // 8 hl .. +7] (the B operand layout of g_B), e, cum_A at t and at T-1
+  struct HeadRegs {
+    u32x4 x[NKD];
+    float e, c, cl;
+  };
+  HeadRegs hr[2];
+  auto load_h = [&](int h, HeadRegs& r) __attribute__((always_inline)) {
+    const int xo = (t * H + h) * D;
+#pragma unroll
+    for (int kb = 0; kb < NKD; ++kb) r.x[kb] = buf_load16(xrs, (xo + 16 * kb + 8 * hl) * 2);
+    const int64_t th = (int64_t)row * T * H + h;
+    r.e = a.e[th + (int64_t)(tv ? t : 0) * H];
+    r.c = a.cum_A[th + (int64_t)(tv ? t : 0) * H];
+    r.cl = a.cum_A[th + (int64_t)(T - 1) * H];
+  };
+
+  auto head = [&](int hi, const HeadRegs& cur, HeadRegs& nxt) __attribute__((always_inline)) {
+    const int h = g * hpg + hi, buf = hi & 1;
     store_g(buf);
     __syncthreads();  // G_h visible; the reads of buffer buf from two heads ago are done
-    if (hi + 1 < hpg) load_g(h + 1);
+    if (hi + 1 < hpg) {
+      load_g(h + 1);
+      load_h(h + 1, nxt);
+    }
     const uint8_t* sg = sG[buf];
-
-    // weight of this lane's token for head h
-    const int64_t th = (int64_t)row * T * H + h;
-    const float cl = a.cum_A[th + (int64_t)(T - 1) * H];
-    const int64_t o = th + (int64_t)(tv ? t : 0) * H;
-    const float dec = live ? expf(cl - a.cum_A[o]) : 0.f;
-    const float w = live ? dec * a.e[o] : 0.f;
+    const float dec = live ? expf(cur.cl - cur.c) : 0.f;
+    const float w = live ? dec * cur.e : 0.f;
 
     // U^T (d x tokens) = G_h B^T: A = G rows (LDS), B = this lane's B row
     f32x16 u[NMD];
@@ -259,47 +308,66 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
       u[m] = zero16();
 #pragma unroll
       for (int kb = 0; kb < NKN; ++kb) {
+        const int gr = 32 * m + l32;
         const bf16x8 ga = __builtin_bit_cast(
-            bf16x8, ld16(sg + (32 * m + l32) * GS + 2 * (16 * kb + 8 * hl)));
+            bf16x8, ld16(sg + gr * GS + 16 * ((2 * kb + hl) ^ swz_both<N>(gr))));
         u[m] = mfma32(ga, bop[kb], u[m]);
       }
     }
+    // x in the C layout of U (lane half hl: d = 8 blk + 4 hl .. +3, blk = 4 m + q):
+    // 8-wide block 2 kb + hl is this lane's, the other half-blocks come from the
+    // partner lane (l ^ 32), which holds block 2 kb + (1 - hl)
+    u32x2 xc[D / 8];
+#pragma unroll
+    for (int kb = 0; kb < NKD; ++kb) {
+      const u32x4 own = cur.x[kb];
+      const uint32_t s0 = hl ? own[0] : own[2], s1 = hl ? own[1] : own[3];
+      const uint32_t r0 = (uint32_t)__shfl_xor((int)s0, 32, 64);
+      const uint32_t r1 = (uint32_t)__shfl_xor((int)s1, 32, 64);
+      xc[2 * kb][0] = hl ? r0 : own[0];
+      xc[2 * kb][1] = hl ? r1 : own[1];
+      xc[2 * kb + 1][0] = hl ? own[2] : r0;
+      xc[2 * kb + 1][1] = hl ? own[3] : r1;
+    }
     // lane (hl, l32) holds U[token t][d = 32 m + c_row(hl, r)]: g_x, g_w
     float gw = 0.f;
-    const int xo = (t * H + h) * D;
+    uint16_t* gxp = a.g_x + (int64_t)row * T * H * D + (int64_t)(t * H + h) * D;
 #pragma unroll
     for (int m = 0; m < NMD; ++m)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int d = 32 * m + 8 * q + 4 * hl;  // regs 4q .. 4q+3 = d .. d+3
-        const u32x4 xv4 = buf_load16(xrs, (xo + (d & ~7)) * 2);
-        const uint32_t lo = (d & 4) ? xv4[2] : xv4[0], hi2 = (d & 4) ? xv4[3] : xv4[1];
-        const float x0 = __uint_as_float(lo << 16), x1 = __uint_as_float(lo & 0xffff0000u);
-        const float x2 = __uint_as_float(hi2 << 16), x3 = __uint_as_float(hi2 & 0xffff0000u);
+        const u32x2 xv = xc[4 * m + q];
+        const float x0 = __uint_as_float(xv[0] << 16), x1 = __uint_as_float(xv[0] & 0xffff0000u);
+        const float x2 = __uint_as_float(xv[1] << 16), x3 = __uint_as_float(xv[1] & 0xffff0000u);
         gw += x0 * u[m][4 * q] + x1 * u[m][4 * q + 1] + x2 * u[m][4 * q + 2] + x3 * u[m][4 * q + 3];
         if (tv) {
-          u32x2 s;
-          s[0] = cvt_pk_bf16(w * u[m][4 * q], w * u[m][4 * q + 1]);
-          s[1] = cvt_pk_bf16(w * u[m][4 * q + 2], w * u[m][4 * q + 3]);
-          *reinterpret_cast<u32x2*>(a.g_x + (int64_t)row * T * H * D + xo + d) = s;
+          u32x2 sv;
+          sv[0] = cvt_pk_bf16(w * u[m][4 * q], w * u[m][4 * q + 1]);
+          sv[1] = cvt_pk_bf16(w * u[m][4 * q + 2], w * u[m][4 * q + 3]);
+          *reinterpret_cast<u32x2*>(gxp + 32 * m + 8 * q + 4 * hl) = sv;
         }
       }
     gw += xhalf(gw);
     if (tv && hl == 0) {
+      const int64_t o = (int64_t)row * T * H + h + (int64_t)t * H;
       a.g_e[o] = gw * dec;
       a.g_cum[o] = -gw * w;
     }
 
     // g_B^T (state x tokens) += G_h^T (w x)^T: A = G^T by transposed reads, B = w x
-    bf16x8 wx[NKD];
-#pragma unroll
-    for (int kb = 0; kb < NKD; ++kb)
-      wx[kb] = __builtin_bit_cast(bf16x8, scale_bf16x8(buf_load16(xrs, (xo + 16 * kb + 8 * hl) * 2), w));
 #pragma unroll
     for (int m = 0; m < NMN; ++m)
 #pragma unroll
       for (int kb = 0; kb < NKD; ++kb)
-        gb[m] = mfma32(tr_tokens<GS>(sg, 16 * kb, 32 * m, lane), wx[kb], gb[m]);
+        gb[m] = mfma32(tr_tokens_swz<GS>(sg, 16 * kb, 32 * m, lane),
+                       __builtin_bit_cast(bf16x8, scale_bf16x8(cur.x[kb], w)), gb[m]);
+  };
+
+  load_g(g * hpg);
+  load_h(g * hpg, hr[0]);
+  for (int hi = 0; hi < hpg; hi += 2) {
+    head(hi, hr[0], hr[1]);
+    if (hi + 1 < hpg) head(hi + 1, hr[1], hr[0]);
   }
 
   // lane (hl, l32) holds g_B[token t][n = 32 m + c_row(hl, r)]

@@ -45,16 +45,16 @@ def _raw_forward(x, B, e, cum, t0):
 
 
 def _kernel_rounding_ref(x, B, e, cum, t0):
-    """The closed form with the weighted B rounded to bf16 as the kernel (and mamba-ssm's
-    chunk-state kernel) does, summed in fp64."""
+    """The closed form with the weighted x rounded to bf16 as the kernel does, summed
+    in fp64."""
     R, T, H, _ = x.shape
     G = B.shape[2]
     w = e * torch.exp(cum[:, -1:, :] - cum)
     keep = torch.arange(T)[None, :] >= t0[:, None]
     w = torch.where(keep[:, :, None], w, torch.zeros_like(w))
-    Bx = B.float().repeat_interleave(H // G, dim=2)
-    Bs = (Bx * w[..., None]).to(torch.bfloat16).double()
-    return torch.einsum("bthd,bthn->bhdn", x.double(), Bs)
+    xs = (x.float() * w[..., None]).to(torch.bfloat16).double()
+    Bx = B.double().repeat_interleave(H // G, dim=2)
+    return torch.einsum("bthd,bthn->bhdn", xs, Bx)
 
 
 @pytest.mark.parametrize("docs", [None, (7,)])
