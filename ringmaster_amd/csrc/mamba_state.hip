@@ -221,6 +221,9 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
   constexpr int GCH = D * N / 8 / NT;                // 8-float chunks of G per thread
   static_assert(GCH >= 1, "G split");
   __shared__ __attribute__((aligned(16))) uint8_t sG[2][D * GS];
+  // g_e (lane half 0) and g_cum_A (half 1) of 8 consecutive heads per token, so
+  // that each token's row of those [rows, T, H] arrays is written 32 bytes at a time
+  __shared__ __attribute__((aligned(16))) float sE[2][BT][8];
 
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -348,10 +351,20 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
         }
       }
     gw += xhalf(gw);
-    if (tv && hl == 0) {
-      const int64_t o = (int64_t)row * T * H + h + (int64_t)t * H;
-      a.g_e[o] = gw * dec;
-      a.g_cum[o] = -gw * w;
+    // each wave stages only its own tokens' strip: no barrier, LDS order suffices
+    float* strip = &sE[hl][32 * wave + l32][0];
+    strip[hi & 7] = hl ? -gw * w : gw * dec;
+    if ((hi & 7) == 7 || hi == hpg - 1) {
+      const int h0 = h - (hi & 7), cnt = (hi & 7) + 1;
+      if (tv) {
+        float* dst = (hl ? a.g_cum : a.g_e) + (int64_t)row * T * H + (int64_t)t * H + h0;
+        if (cnt == 8 && ((H | h0) & 3) == 0) {  // 16-byte aligned rows
+          *reinterpret_cast<f32x4*>(dst) = *reinterpret_cast<const f32x4*>(strip);
+          *reinterpret_cast<f32x4*>(dst + 4) = *reinterpret_cast<const f32x4*>(strip + 4);
+        } else {
+          for (int j = 0; j < cnt; ++j) dst[j] = strip[j];
+        }
+      }
     }
 
     // g_B^T (state x tokens) += G_h^T (w x)^T: A = G^T by transposed reads, B = w x

@@ -78,8 +78,15 @@ def test_chunk_state_forward(R, T, H, D, G, N, docs):
     assert rel_l2(got, exact) < BF16_REL_L2, rel_l2(got, exact)
 
 
+# backward extras: groups of 12 heads (32-byte g_e / g_cum_A rows at aligned head
+# offsets, then a partial group), 10 heads (the second group starts unaligned), and
+# the configs[4] layout (64 heads in one group) on a shorter shard
+BWD_CASES = CASES[:4] + [(1, 256, 24, 64, 2, 128), (1, 160, 20, 64, 2, 64),
+                         (2, 512, 64, 64, 1, 128)]
+
+
 @pytest.mark.parametrize("docs", [None, (100,)])
-@pytest.mark.parametrize("R,T,H,D,G,N", CASES[:4])
+@pytest.mark.parametrize("R,T,H,D,G,N", BWD_CASES)
 def test_chunk_state_backward_raw(R, T, H, D, G, N, docs):
     from ringmaster_amd import abi
 
