@@ -126,13 +126,14 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
   const i32x4 xrs = make_rsrc(a.x + (int64_t)row * T * a.H * D, (uint32_t)T * a.H * D * 2);
   const i32x4 brs = make_rsrc(a.B + (int64_t)row * T * a.G * N, (uint32_t)T * a.G * N * 2);
 
-  // Two stages of loads in flight: register sets 0 and 1 hold stages of even and
-  // odd parity. The weights are formed at the store, so issuing loads never waits.
+  // One stage of loads in flight (the next stage's registers fill while this one
+  // computes); the weights are formed at the store, so issuing loads never waits,
+  // and the small register set lets four workgroups share a CU.
   struct Regs {
     u32x4 x[XCH], b[BCH];
     float e[XCH], c[XCH];
   };
-  Regs rg[2];
+  Regs rg;
   auto load = [&](int st, Regs& r) __attribute__((always_inline)) {
     const int tb = st * TK;
 #pragma unroll
@@ -176,19 +177,13 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
         acc[i] = mfma32(av, tr_tokens<BS>(sB, 16 * ks, 32 * (nb0 + i), lane), acc[i]);
     }
   };
-  auto stage = [&](int st, Regs& r) __attribute__((always_inline)) {
+  if (st_begin < st_hi) load(st_begin, rg);
+  for (int st = st_begin; st < st_hi; ++st) {
     __syncthreads();  // the previous stage's reads are done
-    store(st, r);
+    store(st, rg);
     __syncthreads();
-    if (st + 2 < st_hi) load(st + 2, r);
+    if (st + 1 < st_hi) load(st + 1, rg);
     compute();
-  };
-
-  if (st_begin < st_hi) load(st_begin, rg[0]);
-  if (st_begin + 1 < st_hi) load(st_begin + 1, rg[1]);
-  for (int st = st_begin; st < st_hi; st += 2) {
-    stage(st, rg[0]);
-    if (st + 1 < st_hi) stage(st + 1, rg[1]);
   }
 
   // lane (hl, l32), reg r: d = 32 mb + c_row(hl, r), n = 32 nb + l32
