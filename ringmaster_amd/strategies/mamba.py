@@ -131,7 +131,7 @@ def mamba2_chunk_decay(dt: torch.Tensor, A: torch.Tensor, dt_bias: torch.Tensor 
     ``cum_A`` shaped like ``dt`` and ``decay`` ``[..., nheads]``; differentiable in dt, A
     and dt_bias. Computed in fp32 (the reference's arithmetic when dt_bias or dt is fp32,
     as HF's fp32 dt_bias parameter makes it)."""
-    abi.require_device(dt, A)
+    abi.require_device(dt, A, dt_bias)
     if dt.dim() < 2 or A.dim() != 1 or A.shape[0] != dt.shape[-1]:
         raise ValueError("dt must be [..., T, nheads] and A [nheads]")
     if dt.dtype not in (torch.bfloat16, torch.float32):
@@ -197,7 +197,7 @@ def mamba2_chunk_state(x: torch.Tensor, dt: torch.Tensor, A: torch.Tensor, B: to
     ``cum_A = cumsum(A e)``. ``x`` bf16 ``[..., T, H, D]``, ``dt`` ``[..., T, H]``,
     ``A`` ``[H]``, ``B`` bf16 ``[..., T, G, N]``, ``seq_idx`` int ``[..., T]``; returns
     fp32 ``[..., H, D, N]``, differentiable in x, B, dt, A and dt_bias. D, N in {64, 128}."""
-    abi.require_device(x, dt, A, B)
+    abi.require_device(x, dt, A, B, dt_bias, seq_idx)
     if x.dim() < 3 or B.dim() != x.dim() or dt.dim() != x.dim() - 1:
         raise ValueError("x must be [..., T, H, D], B [..., T, G, N] and dt [..., T, H]")
     lead, (T, H, D) = x.shape[:-3], x.shape[-3:]
@@ -408,7 +408,7 @@ def causal_conv1d_cp(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor |
     (the halo; zeros for rank 0); with ``cu_seqlens`` taps never cross a document
     boundary. Differentiable in x, weight and bias. Returns ``[world, batch, channels,
     local_len]``."""
-    abi.require_device(x, weight)
+    abi.require_device(x, weight, bias)
     if weight.dim() == 3 and weight.shape[1] == 1:
         weight = weight[:, 0]
     if x.dim() != 4 or weight.dim() != 2 or weight.shape[0] != x.shape[2]:

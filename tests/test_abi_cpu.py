@@ -141,3 +141,22 @@ def test_host_validation_chunk_state():
                                       None) == abi.RMX_OK
     assert lib.rmx_mamba2_chunk_state_bwd(None, None, None, None, None, None, None, None, None,
                                           None, 2, 0, 4, 64, 1, 64, None) == abi.RMX_OK
+
+
+def test_mamba_entry_points_refuse_cpu_tensors():
+    import torch
+
+    from ringmaster_amd.strategies.mamba import (causal_conv1d_cp, mamba2_chunk_decay,
+                                                 mamba2_chunk_state)
+
+    x = torch.zeros(1, 64, 2, 64, dtype=torch.bfloat16)
+    dt = torch.zeros(1, 64, 2)
+    A = torch.zeros(2)
+    B = torch.zeros(1, 64, 1, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        mamba2_chunk_state(x, dt, A, B)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        mamba2_chunk_decay(dt, A, torch.zeros(2), dt_softplus=True)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        causal_conv1d_cp(torch.zeros(1, 1, 8, 16, dtype=torch.bfloat16),
+                         torch.zeros(8, 4, dtype=torch.bfloat16))

@@ -174,3 +174,17 @@ def test_chunk_state_chain_values_and_grads(softplus, dt_f32, packed):
         assert got.grad is not None, name
         err = rel_l2(got.grad.cpu(), ref.grad)
         assert err < 2e-2, (name, err)
+
+
+def test_host_tensors_next_to_device_ones_are_refused():
+    """A dt_bias or seq_idx left on the host raises instead of reaching a kernel."""
+    from ringmaster_amd.strategies.mamba import mamba2_chunk_state
+
+    x = torch.zeros(1, 64, 2, 64, dtype=torch.bfloat16, device="cuda")
+    dt = torch.zeros(1, 64, 2, device="cuda")
+    A = torch.zeros(2, device="cuda")
+    B = torch.zeros(1, 64, 1, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        mamba2_chunk_state(x, dt, A, B, dt_bias=torch.zeros(2), dt_softplus=True)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        mamba2_chunk_state(x, dt, A, B, seq_idx=torch.zeros(1, 64, dtype=torch.int32))
