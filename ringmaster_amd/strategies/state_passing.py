@@ -46,6 +46,9 @@ def linear_scan_forward(a, b, world: int = 1, return_chunk_state: bool = False):
 
 def linear_scan_backward(a, h, dh, world: int = 1):
     a, h, groups = _prep(a, h, world)
+    abi.require_device(dh)
+    if dh.shape != h.shape:
+        raise ValueError("dh must be shaped like h")
     dh = dh.contiguous().float()
     batch, L, d = h.shape
     da = torch.zeros_like(a)
