@@ -9,7 +9,8 @@
  *     caller;
  *   - launches asynchronously on the caller's HIP stream (a hipStream_t passed
  *     as void*; NULL is the default stream);
- *   - keeps no mutable global state apart from the per-thread error string.
+ *   - keeps no mutable global state apart from the per-thread error string (and the
+ *     per-device address of the one allocation-free entry point's scratch array).
  *
  * Tensor conventions follow the reference ring path: q/k/v/out are
  * [batch, seq, heads, dim] with arbitrary element strides for the first three
@@ -27,8 +28,9 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 7  /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
-                              7: effective dt in/out of the dt cumsum, shard final state */
+#define RMX_ABI_VERSION 8  /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+                              7: effective dt in/out of the dt cumsum, shard final state;
+                              8: allocation-free Mamba2 correction bwd */
 
 /* error codes */
 #define RMX_OK 0
@@ -259,6 +261,29 @@ int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const
                                      float* g_hprev, void* workspace, size_t workspace_bytes,
                                      int32_t batch, int32_t T, int32_t nheads, int32_t head_dim,
                                      int32_t ngroups, int32_t d_state, void* stream);
+
+/*
+ * Allocation-free variant of rmx_mamba2_cp_correction_bwd. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments and
+ * results as rmx_mamba2_cp_correction_bwd without the workspace: the workspace is a
+ * file-scope device array of RMX_MAMBA2_BWD_SCRATCH_MAX bytes (96 MiB), which the library
+ * holds on every GPU it runs on until the process ends. A shape whose
+ * rmx_mamba2_cp_correction_bwd_workspace exceeds that maximum returns RMX_EINVAL before
+ * anything is launched. The call allocates and frees nothing. Every call on one GPU
+ * shares that GPU's array and its contents (none of which needs to start at zero), so
+ * calls that overlap on one GPU (from other streams or threads) race. The array's
+ * device address is looked up once per device, on the first call with that device
+ * current; the stream must belong to the current device.
+ */
+#define RMX_MAMBA2_BWD_SCRATCH_MAX ((size_t)96 << 20)
+int32_t rmx_mamba2_cp_correction_bwd_noalloc(const uint16_t* gy, const float* ghf,
+                                             const uint16_t* C, const float* cum_A,
+                                             const float* h_prev, const int32_t* seq_idx,
+                                             uint16_t* gC, float* g_cumA, float* g_hprev,
+                                             int32_t batch, int32_t T, int32_t nheads,
+                                             int32_t head_dim, int32_t ngroups, int32_t d_state,
+                                             void* stream);
 
 /*
  * Mamba2 CP chunk decay from dt, the first step of the reference's CP scan

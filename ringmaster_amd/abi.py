@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
-ABI_VERSION = 7  # RMX_ABI_VERSION of include/ringmaster_amd.h
+ABI_VERSION = 8  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
@@ -98,6 +98,7 @@ SIGNATURES = {
                                         _i32, _i32, _i32, _vp]),
     "rmx_mamba2_cp_correction_bwd_workspace": (ctypes.c_size_t, [_i32] * 6),
     "rmx_mamba2_cp_correction_bwd": (_i32, [_vp] * 10 + [ctypes.c_size_t] + [_i32] * 6 + [_vp]),
+    "rmx_mamba2_cp_correction_bwd_noalloc": (_i32, [_vp] * 9 + [_i32] * 6 + [_vp]),
     "rmx_mamba2_dt_cumsum": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32,
                                     _vp]),
     "rmx_mamba2_dt_cumsum_bwd": (_i32, [_vp, _i32, _vp, _vp, _i32] + [_vp] * 7

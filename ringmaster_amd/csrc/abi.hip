@@ -354,21 +354,34 @@ size_t rmx_mamba2_cp_correction_bwd_workspace(int32_t batch, int32_t T, int32_t 
   return rmx::mamba2_bwd_workspace(batch, T, nheads, head_dim, d_state);
 }
 
+// Shared argument checks of the two correction-backward entry points (1 = nothing to do).
+static int check_mamba_bwd_args(const uint16_t* gy, const float* ghf, const uint16_t* C,
+                                const float* cum_A, const float* h_prev, uint16_t* gC,
+                                float* g_cumA, float* g_hprev, int32_t batch, int32_t T,
+                                int32_t nheads, int32_t head_dim, int32_t ngroups,
+                                int32_t d_state) {
+  int rc = check_mamba_bwd(batch, T, nheads, head_dim, ngroups, d_state);
+  if (rc) return rc;
+  if ((int64_t)batch * nheads == 0) return 1;
+  if (T == 0) return fail(RMX_EINVAL, "the shard has no tokens (T == 0)");
+  if (!gy || !C || !cum_A || !h_prev || !gC || !g_cumA || !g_hprev)
+    return fail(RMX_EINVAL, "NULL tensor pointer");
+  if (!aligned(gy, 16) || !aligned(C, 16) || !aligned(h_prev, 16) || !aligned(gC, 16) ||
+      !aligned(g_hprev, 16) || (ghf && !aligned(ghf, 16)))
+    return fail(RMX_EINVAL, "gy, C, h_prev, ghf, gC and g_hprev must be 16-byte aligned");
+  return RMX_OK;
+}
+
 int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const uint16_t* C,
                                      const float* cum_A, const float* h_prev,
                                      const int32_t* seq_idx, uint16_t* gC, float* g_cumA,
                                      float* g_hprev, void* workspace, size_t workspace_bytes,
                                      int32_t batch, int32_t T, int32_t nheads, int32_t head_dim,
                                      int32_t ngroups, int32_t d_state, void* stream) {
-  int rc = check_mamba_bwd(batch, T, nheads, head_dim, ngroups, d_state);
-  if (rc) return rc;
-  if ((int64_t)batch * nheads == 0) return RMX_OK;
-  if (T == 0) return fail(RMX_EINVAL, "the shard has no tokens (T == 0)");
-  if (!gy || !C || !cum_A || !h_prev || !gC || !g_cumA || !g_hprev || !workspace)
-    return fail(RMX_EINVAL, "NULL tensor pointer");
-  if (!aligned(gy, 16) || !aligned(C, 16) || !aligned(h_prev, 16) || !aligned(gC, 16) ||
-      !aligned(g_hprev, 16) || (ghf && !aligned(ghf, 16)))
-    return fail(RMX_EINVAL, "gy, C, h_prev, ghf, gC and g_hprev must be 16-byte aligned");
+  int rc = check_mamba_bwd_args(gy, ghf, C, cum_A, h_prev, gC, g_cumA, g_hprev, batch, T, nheads,
+                                head_dim, ngroups, d_state);
+  if (rc) return rc < 0 ? rc : RMX_OK;
+  if (!workspace) return fail(RMX_EINVAL, "NULL workspace");
   const size_t need = rmx::mamba2_bwd_workspace(batch, T, nheads, head_dim, d_state);
   if (workspace_bytes < need)
     return fail(RMX_EINVAL, "workspace of %zu bytes is below the %zu required", workspace_bytes, need);
@@ -377,6 +390,31 @@ int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const
                                                       head_dim, ngroups, d_state,
                                                       (hipStream_t)stream),
                     "rmx_mamba2_cp_correction_bwd launch");
+}
+
+int32_t rmx_mamba2_cp_correction_bwd_noalloc(const uint16_t* gy, const float* ghf,
+                                             const uint16_t* C, const float* cum_A,
+                                             const float* h_prev, const int32_t* seq_idx,
+                                             uint16_t* gC, float* g_cumA, float* g_hprev,
+                                             int32_t batch, int32_t T, int32_t nheads,
+                                             int32_t head_dim, int32_t ngroups, int32_t d_state,
+                                             void* stream) {
+  int rc = check_mamba_bwd_args(gy, ghf, C, cum_A, h_prev, gC, g_cumA, g_hprev, batch, T, nheads,
+                                head_dim, ngroups, d_state);
+  if (rc) return rc < 0 ? rc : RMX_OK;
+  const size_t need = rmx::mamba2_bwd_workspace(batch, T, nheads, head_dim, d_state);
+  if (need > RMX_MAMBA2_BWD_SCRATCH_MAX)
+    return fail(RMX_EINVAL,
+                "the shape needs a %zu-byte workspace, above the %zu bytes of the allocation-free "
+                "entry point's scratch array (use rmx_mamba2_cp_correction_bwd with a workspace)",
+                need, (size_t)RMX_MAMBA2_BWD_SCRATCH_MAX);
+  void* ws = nullptr;
+  rc = dev_status(rmx::mamba2_bwd_scratch(&ws), "scratch array lookup (hipGetSymbolAddress)");
+  if (rc) return rc;
+  return dev_status(rmx::launch_mamba2_correction_bwd(gy, ghf, C, cum_A, h_prev, seq_idx, gC, g_cumA,
+                                                      g_hprev, ws, batch, T, nheads, head_dim,
+                                                      ngroups, d_state, (hipStream_t)stream),
+                    "rmx_mamba2_cp_correction_bwd_noalloc launch");
 }
 
 static int check_dt(const void* dt, int32_t dt_is_f32, const float* A, int32_t softplus,

@@ -21,6 +21,7 @@
 //     on MFMA (H_in^T hi/lo staged per 64-channel chunk in LDS), scaled by e.
 // Every fp32 result is formed from exact bf16 x bf16 products with fp32
 // accumulation (the hi/lo splits carry ~16 mantissa bits of the fp32 factors).
+#include <mutex>
 #include <type_traits>
 
 #include "rmx_kernels.h"
@@ -549,6 +550,37 @@ __global__ void mamba2_bwd_zero_kernel(float* p, int64_t n) {
 }
 
 // ---------------------------------------------------------------------------
+// Workspace of the allocation-free entry point (rmx_mamba2_cp_correction_bwd_noalloc):
+// a file-scope device array, one per GPU the library runs on, held until the process
+// ends. In host code `scratch` names a host-side stand-in, not device memory: host code
+// only ever uses the address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) uint8_t scratch[RMX_MAMBA2_BWD_SCRATCH_MAX];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch` per device
+}  // namespace
+
+// The current device's copy of `scratch`, looked up once per device (with that device
+// current) and kept for the rest of the process.
+hipError_t mamba2_bwd_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
 size_t mamba2_bwd_workspace(int batch, int T, int nheads, int head_dim, int d_state) {
   const size_t state = (size_t)batch * nheads * head_dim * d_state;
   const size_t ntb = (size_t)((T + kMambaBwdTokensPerWg - 1) / kMambaBwdTokensPerWg);

@@ -35,6 +35,7 @@ hipError_t launch_mamba2_correction(const uint16_t* out, uint16_t* y, const floa
                                     int nheads, int head_dim, int ngroups, int d_state,
                                     hipStream_t stream);
 size_t mamba2_bwd_workspace(int batch, int T, int nheads, int head_dim, int d_state);
+hipError_t mamba2_bwd_scratch(void** out);
 hipError_t launch_mamba2_correction_bwd(const uint16_t* gy, const float* ghf, const uint16_t* C,
                                         const float* cum_A, const float* h_prev,
                                         const int32_t* seq_idx, uint16_t* gC, float* g_cumA,

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 7
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 8
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -141,6 +141,27 @@ def test_host_validation_chunk_state():
                                       None) == abi.RMX_OK
     assert lib.rmx_mamba2_chunk_state_bwd(None, None, None, None, None, None, None, None, None,
                                           None, 2, 0, 4, 64, 1, 64, None) == abi.RMX_OK
+
+
+def test_host_validation_correction_bwd_noalloc():
+    """The allocation-free correction backward checks its arguments, and rejects shapes
+    whose workspace exceeds its fixed scratch array, before touching the device."""
+    lib = abi.lib()
+    p = 16  # any 16-byte aligned non-null value: validation fails before a launch
+    need = lib.rmx_mamba2_cp_correction_bwd_workspace(8, 16384, 64, 64, 1, 128)
+    assert need > (96 << 20)
+    assert lib.rmx_mamba2_cp_correction_bwd_noalloc(p, None, p, p, p, None, p, p, p, 8, 16384, 64,
+                                                    64, 1, 128, None) == abi.RMX_EINVAL
+    assert b"scratch" in lib.rmx_last_error()
+    # configs[4] (8 shards x 8192 tokens, 64 heads of 64, d_state 128) fits the array
+    assert lib.rmx_mamba2_cp_correction_bwd_workspace(8, 8192, 64, 64, 1, 128) <= (96 << 20)
+    assert lib.rmx_mamba2_cp_correction_bwd_noalloc(p, None, None, p, p, None, p, p, p, 2, 64, 4,
+                                                    64, 1, 64, None) == abi.RMX_EINVAL  # C NULL
+    assert b"NULL" in lib.rmx_last_error()
+    assert lib.rmx_mamba2_cp_correction_bwd_noalloc(p, None, p, p, p, None, p, p, p, 2, 64, 4, 64,
+                                                    1, 32, None) == abi.RMX_EUNSUPPORTED
+    assert lib.rmx_mamba2_cp_correction_bwd_noalloc(None, None, None, None, None, None, None, None,
+                                                    None, 0, 64, 4, 64, 1, 64, None) == abi.RMX_OK
 
 
 def test_mamba_entry_points_refuse_cpu_tensors():
