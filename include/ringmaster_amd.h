@@ -28,9 +28,10 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 8  /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 9  /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
-                              8: allocation-free Mamba2 correction bwd */
+                              8: allocation-free Mamba2 correction bwd;
+                              9: carried-in state h_in / dh_in of the linear scan */
 
 /* error codes */
 #define RMX_OK 0
@@ -198,26 +199,33 @@ int32_t rmx_zigzag_scatter(const void* src, void* dst, int32_t batch, int32_t se
                            void* stream);
 
 /*
- * Context-parallel linear scan h_t = a_t h_{t-1} + b_t emulated over `world`
- * contiguous shards of length L/world (strategies/state_passing.py:19-59): each
- * shard scans from zero, the shards' (decay, carry) pairs are prefix-combined
- * in rank order and the correction h += cumA * H_in is applied.
+ * Context-parallel linear scan h_t = a_t h_{t-1} + b_t (strategies/state_passing.py:19-59).
+ * Replaces `cp_linear_scan(a, b, group)` (strategies/state_passing.py:29): with world == 1
+ * and h_in it is one rank's call on its local chunk (the local zero-init scan corrected by
+ * cumA * H_in, :59, where H_in is the rank-ordered prefix of the earlier ranks' (A_j, B_j),
+ * :55-57); with world > 1 the sequence is `world` contiguous shards emulated in one launch
+ * (each shard scans from zero, the shards' (decay, carry) pairs are prefix-combined in rank
+ * order and the correction applied), starting from h_in.
  * a: fp32 [batch, L, groups] with `groups` dividing d (a[b,t,g] applies to the
  * d/groups consecutive channels of group g; groups == d is elementwise);
- * b, h: fp32 [batch, L, d] contiguous. chunk_state (nullable): fp32
- * [world, batch, 2, d] receives each shard's (A_r broadcast, B_r).
+ * b, h: fp32 [batch, L, d] contiguous. h_in (nullable: zero): fp32 [batch, d], the state
+ * before token 0. chunk_state (nullable): fp32 [world, batch, 2, d] receives each
+ * shard's (A_r broadcast, B_r), what a rank contributes to the all-gather of :49-52.
  */
-int32_t rmx_linear_scan_fwd(const float* a, const float* b, float* h, float* chunk_state,
-                            int32_t batch, int32_t L, int32_t d, int32_t groups,
-                            int32_t world, void* stream);
+int32_t rmx_linear_scan_fwd(const float* a, const float* b, const float* h_in, float* h,
+                            float* chunk_state, int32_t batch, int32_t L, int32_t d,
+                            int32_t groups, int32_t world, void* stream);
 
 /*
- * Gradient of rmx_linear_scan_fwd: given dh and the forward h, writes
- * db [batch, L, d] and ADDS da [batch, L, groups] (caller zero-fills da).
+ * Gradient of rmx_linear_scan_fwd (what autograd through the reference's loop, cumprod
+ * and the all-gather's all-reduce backward computes): given dh, the forward's h and h_in
+ * (nullable), writes db [batch, L, d], ADDS da [batch, L, groups] (caller zero-fills da)
+ * and, when dh_in is not NULL, writes dh_in [batch, d] = a_0 * g_0, the gradient of h_in
+ * (zero when L == 0), which a rank sends back to the ranks whose states formed its H_in.
  */
-int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* dh, float* da,
-                            float* db, int32_t batch, int32_t L, int32_t d, int32_t groups,
-                            int32_t world, void* stream);
+int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* h_in, const float* dh,
+                            float* da, float* db, float* dh_in, int32_t batch, int32_t L,
+                            int32_t d, int32_t groups, int32_t world, void* stream);
 
 /*
  * Mamba2 context-parallel output correction (strategies/mamba.py:101-139):

@@ -58,6 +58,27 @@ def cp_linear_scan_emulated(a, b, world, scan=local_linear_scan):
     return torch.cat(outs, dim=1)
 
 
+def rank_linear_scan(a, b, h_in):
+    """One rank's ``cp_linear_scan`` on its local chunk given the state entering it
+    (strategies/state_passing.py:38-39,59): the zero-init local scan corrected by
+    ``cumprod(a) * h_in``. a, b: [batch, L_local, d]; h_in: [batch, d]."""
+    return local_linear_scan(a, b) + torch.cumprod(a, dim=1) * h_in.unsqueeze(1)
+
+
+def scan_prefix(a, b, world):
+    """The H_in of every rank (strategies/state_passing.py:49-57): the all-gathered
+    (A_r, B_r) = (cumprod(a)[-1], local_h[-1]) of each chunk folded in rank order.
+    a, b: full [batch, L, d]; returns [world, batch, d]."""
+    n = a.shape[1] // world
+    h_in = torch.zeros_like(b[:, 0])
+    out = []
+    for r in range(world):
+        out.append(h_in)
+        sa, sb = a[:, r * n:(r + 1) * n], b[:, r * n:(r + 1) * n]
+        h_in = torch.cumprod(sa, dim=1)[:, -1] * h_in + local_linear_scan(sa, sb)[:, -1]
+    return torch.stack(out)
+
+
 def ssd_reference(x, dt, A, B, C):
     """Mamba2 SSD: h_t = exp(A dt_t) h_{t-1} + (dt_t B_t) (x) x_t; y_t = C_t . h_t
     (tests/test_mamba_cp.py:16-32). x [b,T,H,d], dt [b,T,H], A [H], B/C [b,T,G,n]."""
@@ -127,6 +148,16 @@ def chunk_state(x, B, e, cum_A, t0=None):
         w = w * keep[:, :, None].to(w.dtype)
     Bx = B.repeat_interleave(H // G, dim=2)
     return torch.einsum("bth,bthd,bthn->bhdn", w, x, Bx)
+
+
+def effective_dt(dt, dt_bias=None, dt_softplus=False, dt_limit=(0.0, float("inf"))):
+    """The per-token step the shard's own scan uses (mamba.py:143-148, mamba-ssm's rule):
+    dt + dt_bias whenever dt_bias is given, then softplus when dt_softplus, then clamped
+    to dt_limit. (The CP wrapper's chunk decay, ``chunk_decay`` below, has its own rule.)"""
+    e = dt if dt_bias is None else dt + dt_bias
+    if dt_softplus:
+        e = torch.nn.functional.softplus(e)
+    return e.clamp(*dt_limit)
 
 
 def chunk_decay(dt, A, dt_bias=None, dt_softplus=False):

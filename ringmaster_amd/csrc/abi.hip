@@ -269,33 +269,41 @@ static int check_scan(int batch, int L, int d, int groups, int world) {
   return RMX_OK;
 }
 
-int32_t rmx_linear_scan_fwd(const float* a, const float* b, float* h, float* chunk_state,
-                            int32_t batch, int32_t L, int32_t d, int32_t groups, int32_t world,
-                            void* stream) {
+int32_t rmx_linear_scan_fwd(const float* a, const float* b, const float* h_in, float* h,
+                            float* chunk_state, int32_t batch, int32_t L, int32_t d, int32_t groups,
+                            int32_t world, void* stream) {
   int rc = check_scan(batch, L, d, groups, world);
   if (rc) return rc;
   if ((int64_t)batch * L * d == 0) return RMX_OK;
   if (!a || !b || !h) return fail(RMX_EINVAL, "NULL tensor pointer");
-  if (!aligned(a, 16) || !aligned(b, 16) || !aligned(h, 16))
-    return fail(RMX_EINVAL, "a, b and h must be 16-byte aligned");
+  if (!aligned(a, 16) || !aligned(b, 16) || !aligned(h, 16) || (h_in && !aligned(h_in, 16)))
+    return fail(RMX_EINVAL, "a, b, h_in and h must be 16-byte aligned");
   return dev_status(
-      rmx::launch_linear_scan_fwd(a, b, h, chunk_state, batch, L, d, groups, world,
+      rmx::launch_linear_scan_fwd(a, b, h_in, h, chunk_state, batch, L, d, groups, world,
                                   (hipStream_t)stream),
       "rmx_linear_scan_fwd launch");
 }
 
-int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* dh, float* da, float* db,
-                            int32_t batch, int32_t L, int32_t d, int32_t groups, int32_t world,
-                            void* stream) {
+int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* h_in, const float* dh,
+                            float* da, float* db, float* dh_in, int32_t batch, int32_t L,
+                            int32_t d, int32_t groups, int32_t world, void* stream) {
   int rc = check_scan(batch, L, d, groups, world);
   if (rc) return rc;
-  if ((int64_t)batch * L * d == 0) return RMX_OK;
+  if ((int64_t)batch * d == 0) return RMX_OK;
+  if (L == 0) {
+    if (dh_in && !aligned(dh_in, 16)) return fail(RMX_EINVAL, "dh_in must be 16-byte aligned");
+    return dev_status(rmx::launch_linear_scan_bwd(a, h, h_in, dh, da, db, dh_in, batch, L, d,
+                                                  groups, world, (hipStream_t)stream),
+                      "rmx_linear_scan_bwd launch");
+  }
   if (!a || !h || !dh || !da || !db) return fail(RMX_EINVAL, "NULL tensor pointer");
   if (!aligned(a, 16) || !aligned(h, 16) || !aligned(dh, 16) || !aligned(da, 16) ||
-      !aligned(db, 16))
+      !aligned(db, 16) || (h_in && !aligned(h_in, 16)) || (dh_in && !aligned(dh_in, 16)))
     return fail(RMX_EINVAL, "scan tensors must be 16-byte aligned");
-  return dev_status(rmx::launch_linear_scan_bwd(a, h, dh, da, db, batch, L, d, groups, world,
-                                                (hipStream_t)stream),
+  if (dh_in && !h_in)
+    return fail(RMX_EINVAL, "dh_in is the gradient of h_in: pass the forward's h_in with it");
+  return dev_status(rmx::launch_linear_scan_bwd(a, h, h_in, dh, da, db, dh_in, batch, L, d,
+                                                groups, world, (hipStream_t)stream),
                     "rmx_linear_scan_bwd launch");
 }
 

@@ -22,12 +22,12 @@ hipError_t launch_lse_merge(float* out, float* lse, const void* blk_out, int blk
 hipError_t launch_zigzag(const void* src, void* dst, int batch, int seq, int world, int rank,
                          int64_t row_bytes, int64_t bstride, const void* pad_row, int scatter,
                          hipStream_t stream);
-hipError_t launch_linear_scan_fwd(const float* a, const float* b, float* h, float* chunk_state,
-                                  int batch, int L, int d, int groups, int world,
-                                  hipStream_t stream);
-hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* dh, float* da,
-                                  float* db, int batch, int L, int d, int groups, int world,
-                                  hipStream_t stream);
+hipError_t launch_linear_scan_fwd(const float* a, const float* b, const float* hin, float* h,
+                                  float* chunk_state, int batch, int L, int d, int groups,
+                                  int world, hipStream_t stream);
+hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* hin,
+                                  const float* dh, float* da, float* db, float* dhin, int batch,
+                                  int L, int d, int groups, int world, hipStream_t stream);
 
 hipError_t launch_mamba2_correction(const uint16_t* out, uint16_t* y, const float* h_final,
                                     float* h_final_out, const uint16_t* C, const float* cum_A,

@@ -10,9 +10,14 @@
 // channels and walks the shards in rank order, so b is read once and h written
 // once (HBM-bound; the decay a is per channel group and mostly cache-resident).
 //
+// A carried-in state h_in (nullable) is the state before token 0: H starts at
+// h_in instead of zero, which is what a real rank's local chunk receives as the
+// prefix of the ranks before it (the H_in of strategies/state_passing.py:55-59).
+//
 // The backward is the exact gradient of the same map (what autograd through
 // the reference's loop, cumprod and AllGatherCP computes):
-//   g_t = dh_t + a_{t+1} g_{t+1};  db_t = g_t;  da_t = sum_group g_t h_{t-1}.
+//   g_t = dh_t + a_{t+1} g_{t+1};  db_t = g_t;  da_t = sum_group g_t h_{t-1}
+// with h_{-1} = h_in, and dh_in = a_0 g_0.
 // When a wave's channels share one decay, da is reduced across the wave for 16
 // steps at a time (and, when the workgroup shares one decay, summed per step in
 // LDS and added to da once per workgroup at the end).
@@ -88,6 +93,7 @@ __device__ __forceinline__ float wave_sum16(float (&part)[16], int lane, int& u)
 template <int AMODE, int V>
 __global__ __launch_bounds__(256) void linear_scan_fwd_kernel(const float* __restrict__ a,
                                                               const float* __restrict__ b,
+                                                              const float* __restrict__ hin,
                                                               float* __restrict__ h,
                                                               float* __restrict__ cs, int batch,
                                                               int L, int d, int groups,
@@ -107,7 +113,7 @@ __global__ __launch_bounds__(256) void linear_scan_fwd_kernel(const float* __res
 
   float H[V];
 #pragma unroll
-  for (int v = 0; v < V; ++v) H[v] = 0.f;
+  for (int v = 0; v < V; ++v) H[v] = hin ? hin[(int64_t)bb * d + c + v] : 0.f;
   for (int r = 0; r < world; ++r) {
     float loc[V], cum[V];
 #pragma unroll
@@ -175,9 +181,11 @@ __global__ __launch_bounds__(256) void linear_scan_fwd_kernel(const float* __res
 template <int AMODE, int V, bool WAVE_REDUCE, bool LDS_DA>
 __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __restrict__ a,
                                                               const float* __restrict__ h,
+                                                              const float* __restrict__ hin,
                                                               const float* __restrict__ dh,
                                                               float* __restrict__ da,
-                                                              float* __restrict__ db, int batch,
+                                                              float* __restrict__ db,
+                                                              float* __restrict__ dhin, int batch,
                                                               int L, int d, int groups) {
   constexpr int U = 16;
   const int per_b = d / V;
@@ -199,11 +207,12 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
     for (int i = threadIdx.x; i < L; i += 256) sDa[i] = 0.f;
     __syncthreads();
   }
-  float gacc[V], anext[V];
+  float gacc[V], anext[V], h0[V];  // h0: the state before token 0 (h_in or zero)
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     gacc[v] = 0.f;
     anext[v] = 0.f;
+    h0[v] = (hin && valid) ? hin[(int64_t)bb * d + c + v] : 0.f;
   }
   auto emit = [&](int64_t ts, const float* gv, const float* hprev) {
     if (AMODE == 1) {
@@ -247,7 +256,7 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
           ldv<V>(hp + (ts - 1) * d, hv[u]);
         } else {
 #pragma unroll
-          for (int v = 0; v < V; ++v) hv[u][v] = 0.f;
+          for (int v = 0; v < V; ++v) hv[u][v] = h0[v];
         }
         if (AMODE == 1) {
           ldv<V>(ap + ts * groups + c, av[u]);
@@ -304,7 +313,7 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       const float gvv = valid ? gp[ts * d + v] : 0.f;
-      hv[v] = (valid && ts > 0) ? hp[(ts - 1) * d + v] : 0.f;
+      hv[v] = (valid && ts > 0) ? hp[(ts - 1) * d + v] : h0[v];
       const float avv = valid ? (AMODE == 1 ? ap[ts * groups + c + v] : ap[ts * groups + g]) : 0.f;
       gacc[v] = gvv + anext[v] * gacc[v];
       o[v] = gacc[v];
@@ -313,11 +322,20 @@ __global__ __launch_bounds__(256) void linear_scan_bwd_kernel(const float* __res
     }
     emit(ts, o, hv);
   }
+  if (dhin && valid) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) dhin[(int64_t)bb * d + c + v] = anext[v] * gacc[v];  // a_0 g_0
+  }
   if (LDS_DA) {
     __syncthreads();
     if (valid)
       for (int i = threadIdx.x; i < L; i += 256) atomicAdd(dap + (int64_t)i * groups + g, sDa[i]);
   }
+}
+
+__global__ void scan_fill_zero_kernel(float* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0.f;
 }
 
 // Channels per thread V and decay mode; WAVE_REDUCE needs a wave's 64 V
@@ -331,8 +349,9 @@ static int scan_amode(int d, int groups) {
   return 2;
 }
 
-hipError_t launch_linear_scan_fwd(const float* a, const float* b, float* h, float* cs, int batch,
-                                  int L, int d, int groups, int world, hipStream_t stream) {
+hipError_t launch_linear_scan_fwd(const float* a, const float* b, const float* hin, float* h,
+                                  float* cs, int batch, int L, int d, int groups, int world,
+                                  hipStream_t stream) {
   if ((int64_t)batch * L * d == 0) return hipSuccess;
   const int mode = scan_amode(d, groups);
   const int V = mode == 2 ? 1 : kScanV;
@@ -340,21 +359,27 @@ hipError_t launch_linear_scan_fwd(const float* a, const float* b, float* h, floa
   const unsigned grid = (unsigned)((n + 255) / 256);
   if (mode == 0)
     hipLaunchKernelGGL((linear_scan_fwd_kernel<0, kScanV>), dim3(grid), dim3(256), 0, stream, a, b,
-                       h, cs, batch, L, d, groups, world);
+                       hin, h, cs, batch, L, d, groups, world);
   else if (mode == 1)
     hipLaunchKernelGGL((linear_scan_fwd_kernel<1, kScanV>), dim3(grid), dim3(256), 0, stream, a, b,
-                       h, cs, batch, L, d, groups, world);
+                       hin, h, cs, batch, L, d, groups, world);
   else
-    hipLaunchKernelGGL((linear_scan_fwd_kernel<2, 1>), dim3(grid), dim3(256), 0, stream, a, b, h,
-                       cs, batch, L, d, groups, world);
+    hipLaunchKernelGGL((linear_scan_fwd_kernel<2, 1>), dim3(grid), dim3(256), 0, stream, a, b, hin,
+                       h, cs, batch, L, d, groups, world);
   return hipGetLastError();
 }
 
-hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* dh, float* da,
-                                  float* db, int batch, int L, int d, int groups, int world,
-                                  hipStream_t stream) {
+hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* hin,
+                                  const float* dh, float* da, float* db, float* dhin, int batch,
+                                  int L, int d, int groups, int world, hipStream_t stream) {
   (void)world;
-  if ((int64_t)batch * L * d == 0) return hipSuccess;
+  if ((int64_t)batch * d == 0) return hipSuccess;
+  if (L == 0) {  // no token: the carried-in state gets no gradient
+    if (dhin)
+      hipLaunchKernelGGL(scan_fill_zero_kernel, dim3(64), dim3(256), 0, stream, dhin,
+                         (int64_t)batch * d);
+    return hipGetLastError();
+  }
   const int mode = scan_amode(d, groups);
   const int V = mode == 2 ? 1 : kScanV;
   const int gs = d / groups;
@@ -363,19 +388,19 @@ hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* d
   if (mode == 0) {
     if (gs % (256 * kScanV) == 0 && L <= 16384)
       hipLaunchKernelGGL((linear_scan_bwd_kernel<0, kScanV, true, true>), dim3(grid), dim3(256),
-                         (size_t)L * sizeof(float), stream, a, h, dh, da, db, batch, L, d, groups);
+                         (size_t)L * sizeof(float), stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
     else if (gs % (64 * kScanV) == 0)
       hipLaunchKernelGGL((linear_scan_bwd_kernel<0, kScanV, true, false>), dim3(grid), dim3(256), 0,
-                         stream, a, h, dh, da, db, batch, L, d, groups);
+                         stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
     else
       hipLaunchKernelGGL((linear_scan_bwd_kernel<0, kScanV, false, false>), dim3(grid), dim3(256),
-                         0, stream, a, h, dh, da, db, batch, L, d, groups);
+                         0, stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
   } else if (mode == 1) {
     hipLaunchKernelGGL((linear_scan_bwd_kernel<1, kScanV, false, false>), dim3(grid), dim3(256), 0,
-                       stream, a, h, dh, da, db, batch, L, d, groups);
+                       stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
   } else {
     hipLaunchKernelGGL((linear_scan_bwd_kernel<2, 1, false, false>), dim3(grid), dim3(256), 0,
-                       stream, a, h, dh, da, db, batch, L, d, groups);
+                       stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
   }
   return hipGetLastError();
 }

@@ -293,11 +293,15 @@ def doc_for(cu_seqlens, q):
     return doc_ids_from_cu(cu_seqlens, q.device, total)
 
 
-def zigzag_ring_attention(q, k, v, *, scaling=None, cu_seqlens=None, timer=None):
+def zigzag_ring_attention(q, k, v, *, group=None, scaling=None, cu_seqlens=None, timer=None):
     """q/k/v: [P, b, H, L, d] — rank r's zigzag-sharded interface tensors stacked on dim 0
     (L = two chunks, early then late). Returns [P, b, L, H, d]; ``cu_seqlens`` set =>
-    packed (document-masked) blocks. Counterpart of ring/zigzag.py:257-260. ``timer``
-    (a :class:`KernelTimer`) records HIP events around every kernel launch."""
+    packed (document-masked) blocks. Counterpart of ``zigzag_ring_attention(q, k, v, *,
+    group, scaling, cu_seqlens)`` (ring/zigzag.py:257-260): ``group`` must be None, the
+    ranks being the leading axis of one process. ``timer`` (a :class:`KernelTimer`)
+    records HIP events around every kernel launch."""
+    if group is not None:
+        raise ValueError("the emulated ring takes the ranks on the leading axis, not a group")
     check_ring_inputs(q, k, v)
     if q.shape[3] % 2:
         raise ValueError("local length must hold two equal zigzag chunks")

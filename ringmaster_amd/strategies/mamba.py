@@ -187,14 +187,16 @@ def last_document_start(seq_idx: torch.Tensor) -> torch.Tensor:
 
 def mamba2_chunk_state(x: torch.Tensor, dt: torch.Tensor, A: torch.Tensor, B: torch.Tensor, *,
                        dt_bias: torch.Tensor | None = None, dt_softplus: bool = False,
+                       dt_limit: tuple = (0.0, float("inf")),
                        seq_idx: torch.Tensor | None = None) -> torch.Tensor:
     """Final SSM state of each shard's scan from a zero state: the ``final_states`` of
     mamba-ssm's ``mamba_chunk_scan_combined(..., return_final_states=True)`` that the
     reference's CP wrapper gathers across ranks (mamba.py:113-141 and :160-172;
     strategies/mamba.py:250-300). ``state[h] = sum_t exp(cum_A[T-1] - cum_A[t]) e_t
     x_t (x) B_t`` over the last document's tokens (all tokens when ``seq_idx`` is None),
-    with ``e = softplus(dt + dt_bias)`` when ``dt_softplus`` (else ``dt``) and
-    ``cum_A = cumsum(A e)``. ``x`` bf16 ``[..., T, H, D]``, ``dt`` ``[..., T, H]``,
+    with the step of the shard's own scan (mamba.py:143-148): ``e = dt + dt_bias`` whenever
+    ``dt_bias`` is given, then softplus when ``dt_softplus``, then clamped to ``dt_limit``;
+    and ``cum_A = cumsum(A e)``. ``x`` bf16 ``[..., T, H, D]``, ``dt`` ``[..., T, H]``,
     ``A`` ``[H]``, ``B`` bf16 ``[..., T, G, N]``, ``seq_idx`` int ``[..., T]``; returns
     fp32 ``[..., H, D, N]``, differentiable in x, B, dt, A and dt_bias. D, N in {64, 128}."""
     abi.require_device(x, dt, A, B, dt_bias, seq_idx)
@@ -215,8 +217,19 @@ def mamba2_chunk_state(x: torch.Tensor, dt: torch.Tensor, A: torch.Tensor, B: to
     x3 = x.reshape(-1, T, H, D).contiguous()
     B3 = B.reshape(-1, T, G, N).contiguous()
     d3 = dt.reshape(-1, T, H).contiguous()
-    b32 = dt_bias.float().contiguous() if (dt_softplus and dt_bias is not None) else None
-    cum, _, e = _DtCumsum.apply(d3, A.float().contiguous(), b32, bool(dt_softplus), True)
+    lo, hi = (float(v) for v in dt_limit)
+    if dt_softplus and lo <= 0.0 and hi == float("inf"):
+        # softplus >= 0, so the clamp is the identity: the dt kernel computes the step
+        b32 = dt_bias.float().contiguous() if dt_bias is not None else None
+        cum, _, e = _DtCumsum.apply(d3, A.float().contiguous(), b32, True, True)
+    else:
+        # a bias without softplus, or a clamp that bites: the step in fp32 elementwise
+        # ops first (mamba.py:143-148), then the kernel's cumsum over it
+        step = d3.float() if dt_bias is None else d3.float() + dt_bias.float()
+        if dt_softplus:
+            step = torch.nn.functional.softplus(step)
+        step = step.clamp(lo, hi).contiguous()
+        cum, _, e = _DtCumsum.apply(step, A.float().contiguous(), None, False, True)
     t0 = None
     if seq_idx is not None:
         if tuple(seq_idx.shape) != (*lead, T):

@@ -32,20 +32,38 @@ def _prep(a, b, world):
     return a.contiguous(), b.contiguous(), groups
 
 
-def linear_scan_forward(a, b, world: int = 1, return_chunk_state: bool = False):
+def _h_in(h_in, b):
+    if h_in is None:
+        return None
+    abi.require_device(h_in)
+    if h_in.shape != (b.shape[0], b.shape[2]):
+        raise ValueError(f"h_in must be [batch, d] = {(b.shape[0], b.shape[2])} "
+                         f"(got {tuple(h_in.shape)})")
+    if h_in.dtype != torch.float32:
+        raise NotImplementedError("the MI355X scan carries fp32 states")
+    return h_in.contiguous()
+
+
+def linear_scan_forward(a, b, world: int = 1, return_chunk_state: bool = False, h_in=None):
+    """h for the whole ``[batch, L, d]`` input split into ``world`` shards, from ``h_in``
+    (``[batch, d]``, zero when None); with ``return_chunk_state`` also every shard's
+    ``(A_r, B_r)`` as ``[world, batch, 2, d]``."""
     a, b, groups = _prep(a, b, world)
+    h_in = _h_in(h_in, b)
     batch, L, d = b.shape
     h = torch.empty_like(b)
     cs = torch.empty((world, batch, 2, d), dtype=torch.float32, device=b.device) \
         if return_chunk_state else None
-    abi.check(abi.lib().rmx_linear_scan_fwd(a.data_ptr(), b.data_ptr(), h.data_ptr(),
-                                            abi.ptr(cs), batch, L, d, groups, world,
-                                            abi.stream_of(b)))
+    abi.check(abi.lib().rmx_linear_scan_fwd(a.data_ptr(), b.data_ptr(), abi.ptr(h_in),
+                                            h.data_ptr(), abi.ptr(cs), batch, L, d, groups,
+                                            world, abi.stream_of(b)))
     return (h, cs) if return_chunk_state else h
 
 
-def linear_scan_backward(a, h, dh, world: int = 1):
+def linear_scan_backward(a, h, dh, world: int = 1, h_in=None):
+    """(da, db) of :func:`linear_scan_forward`, plus dh_in when ``h_in`` is given."""
     a, h, groups = _prep(a, h, world)
+    h_in = _h_in(h_in, h)
     abi.require_device(dh)
     if dh.shape != h.shape:
         raise ValueError("dh must be shaped like h")
@@ -53,33 +71,84 @@ def linear_scan_backward(a, h, dh, world: int = 1):
     batch, L, d = h.shape
     da = torch.zeros_like(a)
     db = torch.empty_like(h)
-    abi.check(abi.lib().rmx_linear_scan_bwd(a.data_ptr(), h.data_ptr(), dh.data_ptr(),
-                                            da.data_ptr(), db.data_ptr(), batch, L, d, groups,
-                                            world, abi.stream_of(h)))
-    return da, db
+    dh_in = torch.empty_like(h_in) if h_in is not None else None
+    abi.check(abi.lib().rmx_linear_scan_bwd(a.data_ptr(), h.data_ptr(), abi.ptr(h_in),
+                                            dh.data_ptr(), da.data_ptr(), db.data_ptr(),
+                                            abi.ptr(dh_in), batch, L, d, groups, world,
+                                            abi.stream_of(h)))
+    return (da, db) if h_in is None else (da, db, dh_in)
 
 
 class _CPLinearScan(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, a, b, world):
-        h = linear_scan_forward(a, b, world)
-        ctx.save_for_backward(a, h)
+    def forward(ctx, a, b, world, h_in):
+        h = linear_scan_forward(a, b, world, h_in=h_in)
+        ctx.save_for_backward(a, h, h_in)
         ctx.world = world
         return h
 
     @staticmethod
     def backward(ctx, dh):
-        a, h = ctx.saved_tensors
-        da, db = linear_scan_backward(a, h, dh, ctx.world)
-        return da, db, None
+        a, h, h_in = ctx.saved_tensors
+        grads = linear_scan_backward(a, h, dh, ctx.world, h_in=h_in)
+        dh_in = grads[2] if h_in is not None else None
+        return grads[0], grads[1], None, dh_in
 
 
 def local_linear_scan(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """h_t = a_t h_{t-1} + b_t from zero (strategies/state_passing.py:19-26)."""
-    return _CPLinearScan.apply(a, b, 1)
+    return _CPLinearScan.apply(a, b, 1, None)
 
 
-def cp_linear_scan(a: torch.Tensor, b: torch.Tensor, world: int) -> torch.Tensor:
-    """Exact CP linear scan of the full ``[batch, L, d]`` sequence split into ``world``
-    contiguous shards; returns every shard's corrected hidden states (rank order)."""
-    return _CPLinearScan.apply(a, b, int(world))
+def _group_size(group) -> int:
+    if group is None:
+        return 1
+    if isinstance(group, int):
+        raise TypeError("cp_linear_scan(a, b, group): the third argument is the process group "
+                        "(strategies/state_passing.py:29); emulate P ranks with world=P")
+    import torch.distributed as dist
+
+    return dist.get_world_size(group)
+
+
+def cp_linear_scan(a: torch.Tensor, b: torch.Tensor, group=None, *, world: int | None = None,
+                   h_in: torch.Tensor | None = None) -> torch.Tensor:
+    """Exact context-parallel linear scan ``h_t = a_t h_{t-1} + b_t``
+    (``cp_linear_scan(a, b, group)``, strategies/state_passing.py:29-59), differentiable.
+
+    * ``group`` as in the reference: ``None`` (or a group of one rank) scans the given
+      chunk from zero, the reference's ``world == 1`` path. This one-GPU build runs no
+      collectives, so a group of several ranks raises ``NotImplementedError``.
+    * ``h_in`` (fp32 ``[batch, d]``): one rank's call on its local chunk ``a, b [batch,
+      L_local, d]`` given the state entering it, i.e. the rank-ordered prefix of the
+      earlier ranks' ``(A_j, B_j)`` (``:55-57``, see :func:`cp_scan_prefix`): returns
+      ``local_h + cum_a * h_in`` (``:59``); ``h_in`` receives its gradient
+      (``a_0 * g_0``), which a multi-process caller returns to the earlier ranks.
+    * ``world=P``: the full ``[batch, L, d]`` sequence split into P contiguous shards,
+      every rank emulated in one launch (rank order, corrected states of every shard).
+    """
+    if _group_size(group) != 1:
+        raise NotImplementedError(
+            "the MI355X build emulates the ranks on one GPU: pass the full sequence with "
+            "world=P, or one rank's chunk with its carried-in h_in")
+    if world is not None and h_in is not None and int(world) != 1:
+        raise ValueError("h_in is the state entering one rank's chunk: use world=1 with it")
+    return _CPLinearScan.apply(a, b, int(world or 1), h_in)
+
+
+def cp_scan_prefix(chunk_states: torch.Tensor) -> torch.Tensor:
+    """The state entering every rank's chunk from the gathered ``(A_r, B_r)`` pairs
+    (``[world, batch, 2, d]``, what :func:`linear_scan_forward` returns as its chunk
+    state): ``H_in_r = A_{r-1} H_in_{r-1} + B_{r-1}``, ``H_in_0 = 0``
+    (strategies/state_passing.py:55-57), as ``[world, batch, d]``, by the scan kernel
+    over the rank axis."""
+    abi.require_device(chunk_states)
+    if chunk_states.dim() != 4 or chunk_states.shape[2] != 2:
+        raise ValueError("chunk_states must be [world, batch, 2, d]")
+    world, batch, _, d = chunk_states.shape
+    out = torch.zeros((world, batch, d), dtype=torch.float32, device=chunk_states.device)
+    if world > 1:
+        a = chunk_states[:-1, :, 0].transpose(0, 1).contiguous().float()   # [batch, world-1, d]
+        b = chunk_states[:-1, :, 1].transpose(0, 1).contiguous().float()
+        out[1:] = linear_scan_forward(a, b, 1).transpose(0, 1)
+    return out

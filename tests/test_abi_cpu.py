@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 8
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 9
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -95,15 +95,20 @@ def test_empty_calls_are_noops():
     assert _fwd(_layout(), 0) == abi.RMX_OK
     lib = abi.lib()
     assert lib.rmx_zigzag_gather(None, None, 0, 0, 2, -1, 16, 0, None, None) == abi.RMX_OK
-    assert lib.rmx_linear_scan_fwd(None, None, None, None, 0, 8, 4, 4, 2, None) == abi.RMX_OK
+    assert lib.rmx_linear_scan_fwd(None, None, None, None, None, 0, 8, 4, 4, 2, None) == abi.RMX_OK
 
 
 def test_host_validation_shard_and_scan():
     lib = abi.lib()
     assert lib.rmx_zigzag_gather(16, 16, 1, 8, 0, -1, 16, 128, None, None) == abi.RMX_EINVAL
     assert lib.rmx_zigzag_gather(16, 16, 1, 8, 2, 2, 16, 128, None, None) == abi.RMX_EINVAL
-    assert lib.rmx_linear_scan_fwd(16, 16, 16, None, 1, 9, 4, 4, 2, None) == abi.RMX_EINVAL
-    assert lib.rmx_linear_scan_fwd(16, 16, 16, None, 1, 8, 6, 4, 2, None) == abi.RMX_EINVAL
+    assert lib.rmx_linear_scan_fwd(16, 16, None, 16, None, 1, 9, 4, 4, 2, None) == abi.RMX_EINVAL
+    assert lib.rmx_linear_scan_fwd(16, 16, None, 16, None, 1, 8, 6, 4, 2, None) == abi.RMX_EINVAL
+    assert lib.rmx_linear_scan_fwd(16, 16, 8, 16, None, 1, 8, 4, 4, 2, None) == abi.RMX_EINVAL
+    assert b"aligned" in lib.rmx_last_error()  # h_in not 16-byte aligned
+    assert lib.rmx_linear_scan_bwd(16, 16, None, 16, 16, 16, 16, 1, 8, 4, 4, 1, None) \
+        == abi.RMX_EINVAL  # dh_in without h_in
+    assert b"h_in" in lib.rmx_last_error()
 
 
 def test_product_refuses_cpu_tensors():
@@ -181,3 +186,33 @@ def test_mamba_entry_points_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match="ROCm device"):
         causal_conv1d_cp(torch.zeros(1, 1, 8, 16, dtype=torch.bfloat16),
                          torch.zeros(8, 4, dtype=torch.bfloat16))
+
+
+def test_cp_linear_scan_group_argument():
+    """cp_linear_scan(a, b, group) takes the reference's process group as its third
+    argument; an integer there (a world size) is refused with a pointer to world=."""
+    import torch
+
+    from ringmaster_amd.strategies.state_passing import cp_linear_scan
+
+    a = torch.ones(1, 4, 2)
+    with pytest.raises(TypeError, match="world="):
+        cp_linear_scan(a, a, 2)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        cp_linear_scan(a, a, None)
+    with pytest.raises(ValueError, match="world=1"):
+        cp_linear_scan(a, a, world=2, h_in=torch.zeros(1, 2))
+
+
+def test_zigzag_ring_attention_group_keyword():
+    """zigzag_ring_attention accepts the reference's ``group`` keyword (ring/zigzag.py:257);
+    the emulated ring takes its ranks on the leading axis, so only None is valid."""
+    import torch
+
+    from ringmaster_amd.ring.zigzag import zigzag_ring_attention
+
+    q = torch.zeros(2, 1, 2, 8, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="leading axis"):
+        zigzag_ring_attention(q, q, q, group=object())
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        zigzag_ring_attention(q, q, q, group=None)

@@ -46,17 +46,36 @@ def test_zigzag_shard_roundtrip_small(world, seq_len):
 
 
 def test_zigzag_shard_batch_matches_oracle():
-    from ringmaster_amd.shard import zigzag_shard_batch
+    """The product's batch shard against the oracle (every key, including a mask, a 3-D
+    feature tensor and a tensor the caller padded already) and through the pinned rules
+    of tests/test_shard_oracle.py (positions, pads, global shift labels, cover, unshard)."""
+    from ringmaster_amd.shard import zigzag_shard, zigzag_shard_batch, zigzag_unshard
+    from tests.test_shard_oracle import check_shard_batch
 
-    for cp, seq in ((2, 16), (4, 22), (8, 48)):
+    for cp, seq in ((2, 16), (4, 22), (8, 48), (8, 37)):
+        total = seq + (-seq) % (2 * cp)
         base = {"input_ids": torch.arange(seq).view(1, seq) + 1000,
-                "labels": torch.arange(seq).view(1, seq) * 3}
+                "labels": torch.arange(seq).view(1, seq) * 3,
+                "attention_mask": torch.ones(1, seq, dtype=torch.long),
+                "features": torch.randn(1, seq, 5, generator=torch.Generator().manual_seed(seq)),
+                "prepadded": torch.arange(total).view(1, total) + 7}
         for r in range(cp):
             ref, (orig, pad) = osh.zigzag_shard_batch({k: v.clone() for k, v in base.items()}, r, cp)
             got, info = zigzag_shard_batch({k: v.cuda() for k, v in base.items()}, r, cp)
             assert info.original_seq_len == orig and info.pad_len == pad
-            for key in ("input_ids", "labels", "shift_labels", "position_ids"):
+            assert set(got) == set(ref)
+            for key in ref:
                 assert torch.equal(got[key].cpu(), ref[key]), (cp, seq, r, key)
+
+    def shard_fn(batch, r, w):
+        out, info = zigzag_shard_batch({k: v.cuda() for k, v in batch.items()}, r, w)
+        return {k: v.cpu() for k, v in out.items()}, (info.original_seq_len, info.pad_len)
+
+    check_shard_batch(
+        shard_fn,
+        unshard_fn=lambda shards, seq: zigzag_unshard(torch.stack(shards).cuda(), seq).cpu(),
+        shard_tensor_fn=lambda x, w, r, pad_value=0: zigzag_shard(
+            x.cuda(), w, rank=r, pad_value=pad_value).cpu())
 
 
 def test_zigzag_shard_full_size_bit_exact():
@@ -92,13 +111,51 @@ def test_linear_scan_small(groups_mode, world):
     ref = sp.cp_linear_scan_emulated(af, bf, world)
     ref.backward(dh.double())
     ad, bd = a.cuda().requires_grad_(True), b.cuda().requires_grad_(True)
-    h = cp_linear_scan(ad, bd, world)
+    h = cp_linear_scan(ad, bd, world=world)
     h.backward(dh.cuda())
     torch.cuda.synchronize()
     assert_f32_rel(h, ref, "h")
     ref_da = af.grad.reshape(2, T, groups, d // groups).sum(-1)
     assert_f32_rel(bd.grad, bf.grad, "db")
     assert_f32_rel(ad.grad, ref_da, "da", tol=1e-3 if groups_mode == "grouped" else 1e-4)
+
+
+@pytest.mark.parametrize("groups_mode", ["elementwise", "grouped"])
+def test_linear_scan_per_rank_with_h_in(groups_mode):
+    """The per-rank boundary of cp_linear_scan(a, b, group) (strategies/state_passing.py:
+    29-59): rank r's local chunk with the carried-in state H_in (the rank-ordered prefix of
+    the earlier ranks' (A_j, B_j)) equals the global scan's slice; its gradients (da, db and
+    dh_in = a_0 g_0) equal autograd through the oracle's per-rank scan; cp_scan_prefix
+    folds the kernel's chunk states into the same H_in."""
+    from ringmaster_amd.strategies.state_passing import (cp_linear_scan, cp_scan_prefix,
+                                                         linear_scan_forward)
+
+    g = torch.Generator().manual_seed(8)
+    world, n = 4, 48
+    d, groups = (12, 12) if groups_mode == "elementwise" else (1024, 4)
+    a = torch.rand(2, world * n, groups, generator=g) * 0.9 + 0.05
+    b = torch.randn(2, world * n, d, generator=g)
+    af = a.repeat_interleave(d // groups, dim=2).double()
+    glob = sp.local_linear_scan(af, b.double())
+    pre = sp.scan_prefix(af, b.double(), world)
+    _, cs = linear_scan_forward(a.cuda(), b.cuda(), world, return_chunk_state=True)
+    assert_f32_rel(cp_scan_prefix(cs), pre, "H_in from the chunk states")
+    for r in range(world):
+        sl = slice(r * n, (r + 1) * n)
+        dh = torch.randn(2, n, d, generator=g)
+        ar, br = a[:, sl].cuda().requires_grad_(True), b[:, sl].cuda().requires_grad_(True)
+        hin = pre[r].float().cuda().requires_grad_(True)
+        h = cp_linear_scan(ar, br, None, h_in=hin)
+        h.backward(dh.cuda())
+        assert_f32_rel(h, glob[:, sl], f"rank {r}: h vs the global scan")
+        ra = af[:, sl].clone().requires_grad_(True)
+        rb = b[:, sl].double().requires_grad_(True)
+        rh = pre[r].clone().requires_grad_(True)
+        sp.rank_linear_scan(ra, rb, rh).backward(dh.double())
+        assert_f32_rel(br.grad, rb.grad, f"rank {r}: db")
+        assert_f32_rel(hin.grad, rh.grad, f"rank {r}: dh_in")
+        ref_da = ra.grad.reshape(2, n, groups, d // groups).sum(-1)
+        assert_f32_rel(ar.grad, ref_da, f"rank {r}: da", tol=1e-3 if groups > 12 else 1e-4)
 
 
 def test_linear_scan_config4_full_size():

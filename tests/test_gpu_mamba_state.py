@@ -122,21 +122,28 @@ def test_chunk_state_backward_raw(R, T, H, D, G, N, docs):
         assert g_e[0, :docs[0]].abs().max().item() == 0.0
 
 
-@pytest.mark.parametrize("softplus,dt_f32", [(True, False), (False, True)])
+@pytest.mark.parametrize("softplus,dt_f32,with_bias,limit", [
+    (True, False, True, None), (False, True, False, None),
+    (False, True, True, None),          # bias without softplus: added, then clamped at 0
+    (True, True, True, (0.05, 0.8)),    # a dt_limit that clamps both ends
+])
 @pytest.mark.parametrize("packed", [False, True])
-def test_chunk_state_chain_values_and_grads(softplus, dt_f32, packed):
+def test_chunk_state_chain_values_and_grads(softplus, dt_f32, with_bias, limit, packed):
     """mamba2_chunk_state from raw dt (dt kernel with its effective-dt output + state)
-    against the oracle chain (chunk_decay, chunk_state) in fp64: values and gradients
-    w.r.t. x, B, dt, A and dt_bias."""
+    against the oracle chain (effective_dt of mamba.py:143-148, cumsum, chunk_state) in
+    fp64: values and gradients w.r.t. x, B, dt, A and dt_bias."""
     from ringmaster_amd.strategies.mamba import mamba2_chunk_state
 
-    print(f"case chain softplus={softplus} dt_f32={dt_f32} packed={packed}", flush=True)
+    print(f"case chain softplus={softplus} dt_f32={dt_f32} bias={with_bias} limit={limit} "
+          f"packed={packed}", flush=True)
     P, Bsz, T, H, D, G, N = 2, 2, 384, 8, 64, 2, 128
     x = seeded((P, Bsz, T, H, D), 21).to(torch.bfloat16)
     B = seeded((P, Bsz, T, G, N), 22).to(torch.bfloat16)
     raw = seeded((P, Bsz, T, H), 23) - 1.0
-    dt = (raw if softplus else torch.nn.functional.softplus(raw)).to(
-        torch.float32 if dt_f32 else torch.bfloat16)
+    if not softplus and not with_bias:
+        raw = torch.nn.functional.softplus(raw)  # positive steps
+    dt = raw.to(torch.float32 if dt_f32 else torch.bfloat16)
+    lim = limit or (0.0, float("inf"))
     A = -0.02 * torch.exp(seeded((H,), 24) * 0.3)
     bias = seeded((H,), 25) * 0.5
     seq = None
@@ -150,8 +157,8 @@ def test_chunk_state_chain_values_and_grads(softplus, dt_f32, packed):
     xr, Br, dtr, Ar, br = (t.double().requires_grad_(True)
                            for t in (x.float(), B.float(), dt.float(), A, bias))
     rows = P * Bsz
-    cum_r, _ = sp.chunk_decay(dtr.reshape(rows, T, H), Ar, br if softplus else None, softplus)
-    e_r = torch.nn.functional.softplus(dtr + br) if softplus else dtr
+    e_r = sp.effective_dt(dtr, br if with_bias else None, softplus, lim)
+    cum_r = torch.cumsum(Ar[None, None, :] * e_r.reshape(rows, T, H), dim=1)
     t0 = None
     if packed:
         s = seq.reshape(rows, T)
@@ -162,13 +169,14 @@ def test_chunk_state_chain_values_and_grads(softplus, dt_f32, packed):
     (S_r * gs.double()).sum().backward()
 
     xd, Bd, dtd, Ad, bd = (t.cuda().requires_grad_(True) for t in (x, B, dt, A, bias))
-    S = mamba2_chunk_state(xd, dtd, Ad, Bd, dt_bias=bd if softplus else None,
-                           dt_softplus=softplus, seq_idx=seq.cuda() if packed else None)
+    S = mamba2_chunk_state(xd, dtd, Ad, Bd, dt_bias=bd if with_bias else None,
+                           dt_softplus=softplus, dt_limit=lim,
+                           seq_idx=seq.cuda() if packed else None)
     S.backward(gs.cuda())
     torch.cuda.synchronize()
     assert rel_l2(S.detach().cpu(), S_r) < BF16_REL_L2
     checks = [("x", xd, xr), ("B", Bd, Br), ("dt", dtd, dtr), ("A", Ad, Ar)]
-    if softplus:
+    if with_bias:
         checks.append(("dt_bias", bd, br))
     for name, got, ref in checks:
         assert got.grad is not None, name
@@ -188,3 +196,20 @@ def test_host_tensors_next_to_device_ones_are_refused():
         mamba2_chunk_state(x, dt, A, B, dt_bias=torch.zeros(2), dt_softplus=True)
     with pytest.raises(RuntimeError, match="ROCm device"):
         mamba2_chunk_state(x, dt, A, B, seq_idx=torch.zeros(1, 64, dtype=torch.int32))
+
+
+def test_host_bias_next_to_device_tensors_is_refused():
+    """Device x / weight / dt / A with a host bias or dt_bias: the check of that one
+    tensor raises (the others alone would pass it)."""
+    from ringmaster_amd.strategies.mamba import causal_conv1d_cp, mamba2_chunk_decay
+
+    x = torch.zeros(1, 1, 8, 16, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(8, 4, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        causal_conv1d_cp(x, w, torch.zeros(8, dtype=torch.bfloat16))
+    dt = torch.zeros(1, 64, 2, device="cuda")
+    A = torch.zeros(2, device="cuda")
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        mamba2_chunk_decay(dt, A, torch.zeros(2), dt_softplus=True)
+    causal_conv1d_cp(x, w, torch.zeros(8, dtype=torch.bfloat16, device="cuda"))  # all on device
+    mamba2_chunk_decay(dt, A, torch.zeros(2, device="cuda"), dt_softplus=True)

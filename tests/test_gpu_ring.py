@@ -59,6 +59,25 @@ def test_dense_ring_gqa():
     _run_ring(4, half=96, hq=4, hkv=2)
 
 
+@pytest.mark.parametrize("world", [2, 4])
+def test_dense_ring_d64(world):
+    """head_dim 64: the forward's merge epilogues (ACC_INIT / MERGE / FINAL) and the fp32
+    gradient accumulation of both backward kernels at D=64 (checked on the fp32 results,
+    see tests/test_gpu_configs.py)."""
+    from tests.test_gpu_configs import _ring_vs_oracle
+
+    _ring_vs_oracle(world, half=96, hq=4, hkv=2, d=64, seed=40)
+
+
+@pytest.mark.parametrize("world", [2, 4])
+def test_varlen_ring_d64(world):
+    from tests.test_gpu_configs import _ring_vs_oracle
+
+    half = 96
+    cu = torch.tensor([0, 70, 130, 131, 300, 2 * world * half], dtype=torch.int32)
+    _ring_vs_oracle(world, half=half, hq=4, hkv=1, d=64, cu=cu, seed=50)
+
+
 @pytest.mark.parametrize("docs", [[300, 212], [100, 50, 250, 112], [512]])
 def test_varlen_ring(docs):
     world, half = 2, 128

@@ -189,3 +189,58 @@ def test_chunk_state_mutants_are_caught(monkeypatch, mutation):
     monkeypatch.setattr(sp, "chunk_state", mutant)
     with pytest.raises(AssertionError):
         pin.test_chunk_state_equals_ssd_final_state(2)
+
+
+def _shard_batch_variant(batch, cp_rank, cp_size, *, zero_pad_pos=False, pad_label_zero=False,
+                         per_shard_shift=False, swap_chunks=False):
+    """oracle/shard.zigzag_shard_batch with one planted mistake."""
+    from oracle import shard as osh
+
+    bsz, seq_len = batch["input_ids"].shape[:2]
+    pad_len = osh.pad_multiple(seq_len, 2 * cp_size)
+    if not per_shard_shift and "labels" in batch:
+        shift = torch.full_like(batch["labels"], -100)
+        shift[:, :-1] = batch["labels"][:, 1:]
+        batch["shift_labels"] = shift
+    batch["position_ids"] = torch.arange(seq_len).unsqueeze(0).expand(bsz, -1)
+    total = seq_len + pad_len
+    for key, val in list(batch.items()):
+        if pad_len and val.dim() > 1 and val.size(1) == seq_len:
+            fill = -100 if key in ("labels", "shift_labels") and not pad_label_zero else 0
+            pad = torch.full((val.size(0), pad_len, *val.shape[2:]), fill, dtype=val.dtype)
+            if key == "position_ids" and not zero_pad_pos:
+                pad = val[:, -1:] + torch.arange(1, pad_len + 1)
+            batch[key] = torch.cat([val, pad], dim=1)
+    half = total // (2 * cp_size)
+    lo, hi = cp_rank, 2 * cp_size - 1 - cp_rank
+    parts = [torch.arange(lo * half, (lo + 1) * half), torch.arange(hi * half, (hi + 1) * half)]
+    idx = torch.cat(parts[::-1] if swap_chunks else parts)
+    for key, val in list(batch.items()):
+        if val.dim() > 1 and val.size(1) == total:
+            batch[key] = val.index_select(1, idx)
+    if per_shard_shift and "labels" in batch:  # shifted after sharding: boundary targets lost
+        shift = torch.full_like(batch["labels"], -100)
+        shift[:, :-1] = batch["labels"][:, 1:]
+        batch["shift_labels"] = shift
+    return batch, (seq_len, pad_len)
+
+
+@pytest.mark.parametrize("mutation", ["zero_pad_pos", "pad_label_zero", "per_shard_shift",
+                                      "swap_chunks"])
+def test_shard_mutants_are_caught(mutation):
+    from tests.test_shard_oracle import check_shard_batch
+
+    check_shard_batch(_shard_batch_variant)  # the unmutated variant passes
+    with pytest.raises(AssertionError):
+        check_shard_batch(lambda b, r, w: _shard_batch_variant(b, r, w, **{mutation: True}))
+
+
+def test_unshard_mutant_is_caught():
+    from oracle import shard as osh
+    from tests.test_shard_oracle import check_shard_batch
+
+    def reversed_ranks(shards, seq):  # scatters rank r's rows to rank (P-1-r)'s positions
+        return osh.zigzag_unshard_tensor(shards[::-1], seq)
+
+    with pytest.raises(AssertionError):
+        check_shard_batch(osh.zigzag_shard_batch, reversed_ranks)

@@ -500,3 +500,49 @@ def test_chunk_state_gradients_equal_recurrence_gradients():
     rs = torch.autograd.grad((h_ref * gw).sum(), (x, B, dt, A, bias))
     for g, r in zip(gs, rs):
         assert (g - r).abs().max().item() < 1e-10
+
+
+def test_rank_linear_scan_is_the_recurrence_from_h_in():
+    """One rank's scan given h_in equals the recurrence started at h_in (fp64), its
+    h_in gradient is a_0 g_0, and the ranks stitched with the folded prefix equal the
+    global scan from zero (strategies/state_passing.py:29-59)."""
+    g = torch.Generator().manual_seed(21)
+    bsz, L, d, world = 2, 24, 5, 4
+    a = (torch.rand(bsz, L, d, generator=g, dtype=torch.float64) * 0.9 + 0.05)
+    b = torch.randn(bsz, L, d, generator=g, dtype=torch.float64)
+    h_in = torch.randn(bsz, d, generator=g, dtype=torch.float64).requires_grad_(True)
+    h = h_in
+    direct = []
+    for t in range(L):
+        h = a[:, t] * h + b[:, t]
+        direct.append(h)
+    got = sp.rank_linear_scan(a, b, h_in)
+    assert torch.allclose(got, torch.stack(direct, 1), atol=1e-12, rtol=1e-12)
+    dh = torch.randn(bsz, L, d, generator=g, dtype=torch.float64)
+    (gin,) = torch.autograd.grad(got, h_in, dh)
+    adj = torch.zeros_like(b[:, 0])
+    for t in reversed(range(L)):  # g_t = dh_t + a_{t+1} g_{t+1}
+        adj = dh[:, t] + (a[:, t + 1] * adj if t + 1 < L else 0)
+    assert torch.allclose(gin, a[:, 0] * adj, atol=1e-12, rtol=1e-12)
+    pre = sp.scan_prefix(a, b, world)
+    n = L // world
+    stitched = torch.cat([sp.rank_linear_scan(a[:, r * n:(r + 1) * n], b[:, r * n:(r + 1) * n],
+                                              pre[r]) for r in range(world)], 1)
+    assert torch.allclose(stitched, sp.local_linear_scan(a, b), atol=1e-12, rtol=1e-12)
+    assert torch.allclose(stitched, sp.cp_linear_scan_emulated(a, b, world), atol=1e-12)
+
+
+def test_effective_dt_rules():
+    """The shard scan's step (mamba.py:143-148) against values fixed by the reference's
+    text: the bias is added with or without softplus, negative steps clamp to the default
+    dt_limit (0, inf), softplus(0) = ln 2, and a finite dt_limit clamps both ends. The CP
+    wrapper's chunk decay (strategies/mamba.py:276-281) instead keeps dt as it is when
+    softplus is off, bias or not."""
+    t = torch.tensor
+    assert sp.effective_dt(t([-1.0, 0.5])).tolist() == [0.0, 0.5]
+    assert sp.effective_dt(t([-1.0]), t([3.0])).tolist() == [2.0]
+    assert torch.allclose(sp.effective_dt(t([-0.5]), t([0.5]), True), t([math.log(2.0)]))
+    assert torch.allclose(sp.effective_dt(t([5.0, -5.0]), None, False, (0.1, 1.0)), t([1.0, 0.1]))
+    dt = t([[[-1.0]]])
+    cum, decay = sp.chunk_decay(dt, t([2.0]), t([3.0]), False)
+    assert cum.item() == -2.0 and torch.allclose(decay, torch.exp(t([[-2.0]])))
