@@ -30,14 +30,20 @@ COMMON_FLAGS = ["-O3", "-std=c++20", "-fPIC", f"--offload-arch={ARCH}", "-Wall",
                 "-Wno-unused-function", "-Wno-unused-variable"]
 
 
+# Per-unit device flags. attn_bwd: MFMAs write VGPRs (the S / dP tiles the VALU reads
+# then need no v_accvgpr_read); the compiler's AGPR-copy rewrite still places the
+# operands pinned to AGPRs there.
+UNIT_FLAGS = {"attn_bwd": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _sources():
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, "-I", str(CSRC), "-I", str(ROOT / "include"),
-           "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, *UNIT_FLAGS.get(src.stem, []), "-I", str(CSRC),
+           "-I", str(ROOT / "include"), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")

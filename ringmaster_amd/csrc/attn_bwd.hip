@@ -432,8 +432,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
 //   dK -= (P dP')^T Q       A = (P dP')^T, B = Q^T (transposed LDS reads)
 // (dS = P (dP - delta) = -P dP'; the sign goes into the final scale of dK.)
 // A tile is a software pipeline of four phases of NS = HD/8 steps, one MFMA per
-// step, each step's VALU work issued under its MFMA and its LDS operand read
-// three steps ahead (across phase and tile boundaries):
+// step, each step's VALU work issued under its MFMA and its LDS operand read six
+// to seven steps ahead, in pairs every other step (across phase and tile
+// boundaries):
 //   phase 0: dP'_j           | exponentials of S_j rows 0..31, P^T block 0
 //   phase 1: dV_j            | exponentials of rows 32..63, P^T blocks 1..3,
 //                              (P dP')^T block 0
@@ -557,27 +558,45 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     }
     return c;
   };
+  // Everything but the tile's row offset and q head is fixed per workgroup: byte bases
+  // of the (batch, first q head of the group) slices, per-head strides and each lane's
+  // offsets inside a tile. A tile only moves the buffer bases (scalar adds) and shrinks
+  // num_records by the same amount, so rows past the end still read as zero.
   const int qss = (int)(2 * L.q_ss), oss = (int)(2 * L.o_ss);
+  const uint8_t* const qb0 = reinterpret_cast<const uint8_t*>(P.q + bb * L.q_sb + (int64_t)kvh * G * L.q_sh);
+  const uint8_t* const ob0 = reinterpret_cast<const uint8_t*>(P.dout + bb * L.o_sb + (int64_t)kvh * G * L.o_sh);
+  const uint8_t* const nb0 = reinterpret_cast<const uint8_t*>(P.nlse + bb * L.l_sb + (int64_t)kvh * G * L.l_sh);
+  const uint8_t* const db0 = reinterpret_cast<const uint8_t*>(P.delta + bb * L.l_sb + (int64_t)kvh * G * L.l_sh);
+  const int qhs = (int)(2 * L.q_sh), ohs = (int)(2 * L.o_sh), lhs = (int)(4 * L.l_sh);
+  const uint32_t qspan = span_bytes(sq, qss, HD * 2), ospan = span_bytes(sq, oss, HD * 2);
+  int vq[C::NDMA], vo[C::NDMA];
+#pragma unroll
+  for (int i = 0; i < C::NDMA; ++i) {
+    const int n = wave * C::NDMA + i;
+    const int r = n * C::RPK + lane / CH, p = lane % CH;
+    const int ch = 16 * (p ^ swz_both<HD>(r));
+    vq[i] = r * qss + ch;
+    vo[i] = r * oss + ch;
+  }
   auto dma_tile = [&](int b, Cursor cu, bool live) {
     const int qa = cu.qt * BQ;
-    const int qh = live ? kvh * G + cu.hi : kvh * G;
+    const int hi = live ? cu.hi : 0;
     if (wave == 0) {
-      const int64_t lb = bb * L.l_sb + qh * L.l_sh;
+      const int lo = hi * lhs + 4 * qa;
+      const uint32_t n = live ? 4u * (uint32_t)(sq - qa) : 0u;
       const uint32_t m = lds_addr(sM[b]);
-      const uint32_t n = live ? 4u * sq : 0u;
-      dma4_async(make_rsrc(P.nlse + lb, n), m, 4 * (qa + lane));
-      dma4_async(make_rsrc(P.delta + lb, n), m + 4 * BQ, 4 * (qa + lane));
+      dma4_async(make_rsrc(nb0 + lo, n), m, 4 * lane);
+      dma4_async(make_rsrc(db0 + lo, n), m + 4 * BQ, 4 * lane);
     }
-    const i32x4 qrs = make_rsrc(P.q + bb * L.q_sb + qh * L.q_sh, live ? span_bytes(sq, qss, HD * 2) : 0u);
-    const i32x4 ors = make_rsrc(P.dout + bb * L.o_sb + qh * L.o_sh, live ? span_bytes(sq, oss, HD * 2) : 0u);
+    const int qo = hi * qhs + qa * qss, oo = hi * ohs + qa * oss;
+    const i32x4 qrs = make_rsrc(qb0 + qo, live ? qspan - (uint32_t)(qa * qss) : 0u);
+    const i32x4 ors = make_rsrc(ob0 + oo, live ? ospan - (uint32_t)(qa * oss) : 0u);
     const uint32_t qd = lds_addr(sQ[b]), od = lds_addr(sO[b]);
 #pragma unroll
     for (int i = 0; i < C::NDMA; ++i) {
       const int n = wave * C::NDMA + i;
-      const int r = n * C::RPK + lane / CH, p = lane % CH;
-      const int ch = 16 * (p ^ swz_both<HD>(r));
-      dma16_async(qrs, qd + 1024 * n, (qa + r) * qss + ch);
-      dma16_async(ors, od + 1024 * n, (qa + r) * oss + ch);
+      dma16_async(qrs, qd + 1024 * n, vq[i]);
+      dma16_async(ors, od + 1024 * n, vo[i]);
     }
   };
   int nqg = 0, nqd = 0;
@@ -721,13 +740,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   doc_store(0);
 
   f32x16 dv[NDB], dk[NDB], s[2], dp[2], nl[2];
-  // register classes: the dV/dK accumulators (MFMA only) in AGPRs; S, P and dP'
-  // (read by the VALU) in VGPRs
+  // register classes: S, P and dP' (read by the VALU) in VGPRs; the unit is built with
+  // VGPR-form MFMAs, and the register allocator places the dV/dK accumulators
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
     dv[db] = zero16();
     dk[db] = zero16();
-    asm volatile("" : "+a"(dv[db]), "+a"(dk[db]));
   }
   auto pin_v = [](f32x16* x) __attribute__((always_inline)) {
     asm volatile("" : "+v"(x[0]), "+v"(x[1]));
@@ -736,10 +754,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   lds_barrier();
   const float c = prm.scale_log2;
 
-  constexpr int KD = 7;  // operand read-ahead (steps)
+  // operand read-ahead (steps). Reads come in pairs every other step, the later step's
+  // operand first: the wait before an even step's MFMA then also covers the next step's
+  // operand, so one s_waitcnt serves two MFMAs.
+  constexpr int KD = 6, RING = 8;
   // the ring's slots line up across tiles: a tile is 4 NS steps
-  static_assert((4 * NS) % (KD + 1) == 0, "operand ring size must divide the tile's steps");
-  bf16x8 ops[KD + 1];
+  static_assert((4 * NS) % RING == 0 && KD + 2 <= RING && KD % 2 == 0,
+                "operand ring size must divide the tile's steps");
+  bf16x8 ops[RING];
   // LDS operand of step T of the tile in buffer b (T >= 4 NS: the next tile's)
   auto operand = [&](int b, int T) -> bf16x8 {
     const int ph = T / NS, t = T % NS;
@@ -796,7 +818,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       constexpr int T = decltype(Tc)::value;
       constexpr int ph = T / NS, t = T % NS;
       constexpr int NP = 4 / NDB;  // packs per step when a block is packed over NDB steps
-      ops[(T + KD) % (KD + 1)] = operand(B, T + KD);
+      if constexpr (T % 2 == 0) {
+        ops[(T + KD + 1) % RING] = operand(B, T + KD + 1);
+        ops[(T + KD) % RING] = operand(B, T + KD);
+      }
       if constexpr (ph == 3) {
         // metadata of tile j + 1 (landed at this tile's barrier): the 8 reads of
         // nl, then the 8 of delta, spread over the phase
@@ -812,7 +837,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
         if constexpr (t == NS - 1) pin_v(dp);
       }
       __builtin_amdgcn_sched_barrier(0);
-      const bf16x8 a = ops[T % (KD + 1)];
+      const bf16x8 a = ops[T % RING];
       if constexpr (ph == 0) {
         dp[t & 1] = mfma32(a, vreg[t >> 1], dp[t & 1]);
       } else if constexpr (ph == 1) {
