@@ -54,6 +54,77 @@ def _time(fn, steps, warmup):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
+class ClockSampler:
+    """Samples the GPU's current shader clock (``rocm-smi --showclocks``, read from sysfs, no
+    GPU work) from a background thread while a timed region runs: the clock under load, which
+    the power limit holds below the 2.4 GHz of the peak figure."""
+
+    def __init__(self, period_s=0.25):
+        self.period, self.mhz = period_s, []
+        self._stop = None
+
+    def _read(self):
+        try:
+            out = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True,
+                                 timeout=10).stdout
+        except Exception:
+            return None
+        for ln in out.splitlines():
+            if "sclk" in ln and "Mhz" in ln:
+                try:
+                    return int(ln.rsplit("(", 1)[1].split("Mhz")[0])
+                except (IndexError, ValueError):
+                    return None
+        return None
+
+    def __enter__(self):
+        import threading
+
+        self._stop = threading.Event()
+
+        def run():
+            while not self._stop.is_set():
+                v = self._read()
+                if v is not None:
+                    self.mhz.append(v)
+                self._stop.wait(self.period)
+
+        self._t = threading.Thread(target=run, daemon=True)
+        self._t.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._t.join(timeout=15)
+        return False
+
+    def summary(self):
+        if not self.mhz:
+            return None
+        v = sorted(self.mhz)
+        return {"samples": len(v), "min_mhz": v[0], "median_mhz": v[len(v) // 2],
+                "max_mhz": v[-1], "source": "rocm-smi --showclocks sampled during the timed steps"}
+
+
+def gemm_ceiling(steps=20, warmup=5):
+    """The library bf16 GEMM rate on this GPU (torch.matmul -> hipBLASLt), the practical MFMA
+    ceiling the attention kernels are compared with, at 8192^3 and 16384^3, and the clock
+    during it."""
+    out = {}
+    for n in (8192, 16384):
+        a = _gen((n, n), 11)
+        b = _gen((n, n), 12)
+        with ClockSampler() as clk:
+            ms = _time(lambda: torch.matmul(a, b), steps, warmup)
+        tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
+        out[f"bf16_{n}^3"] = {"ms": round(ms, 3), "TFLOP/s": round(tf, 1),
+                              "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+                              "sclk_under_load": clk.summary()}
+        del a, b
+        torch.cuda.empty_cache()
+    return out
+
+
 # ---------------------------------------------------------------- configs[2] ring
 def ring_workload(steps, warmup):
     from ringmaster_amd.ring.schedule import ring_pairs_per_rank
@@ -77,11 +148,12 @@ def ring_workload(steps, warmup):
     for _ in range(warmup):
         step()
     _sync()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step(timer)
-    _sync()
-    ms = (time.perf_counter() - t0) / steps * 1e3
+    with ClockSampler() as clk:
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(timer)
+        _sync()
+        ms = (time.perf_counter() - t0) / steps * 1e3
     # per-kernel averages over the timed region; algorithmic FLOPs per launch:
     # each launch is one ring step over all P ranks = pairs / P
     per_launch_pairs = pairs / P
@@ -105,7 +177,8 @@ def ring_workload(steps, warmup):
             "frac": kern[dom]["frac_bf16_peak"], "traffic": None,
             "algorithmic_flop_per_launch": credit[dom] * D * H * per_launch_pairs}
     return {"ms": ms, "flops": flops, "kernels": kern, "roofline": roof,
-            "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2)}
+            "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
+            "sclk_under_load": clk.summary()}
 
 
 def distflash_workload(steps, warmup):
@@ -504,6 +577,8 @@ def main():
     ap.add_argument("--cpu-heads", type=int, default=1)
     ap.add_argument("--profile", action="store_true",
                     help="one ring step + copy calibration, for rocprofv3 counter passes")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="time torch bf16 GEMMs (hipBLASLt) at 8192^3 and 16384^3 and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -516,6 +591,9 @@ def main():
 
     if args.profile:
         profile_workload()
+        return
+    if args.gemm_ceiling:
+        print(json.dumps({"gemm_ceiling": gemm_ceiling()}))
         return
 
     ring = ring_workload(args.steps, args.warmup)
@@ -570,7 +648,8 @@ def main():
         "kernels": ring["kernels"],
         "extras": extras,
         "peak_mem_gib": ring["peak_mem_gib"],
-        "clocks": _clocks(),
+        "sclk_under_load": ring["sclk_under_load"],
+        "clocks_after_run": _clocks(),
     }
     print(json.dumps(line))
 
