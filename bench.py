@@ -181,6 +181,47 @@ def ring_workload(steps, warmup):
             "sclk_under_load": clk.summary()}
 
 
+def per_rank_workload(steps, warmup, ranks=(0, 7)):
+    """One simulated rank of configs[2] at its real grid: rank r's 8 forward and 16 backward
+    launches (dK/dV and dQ per step) without the other ranks' blocks in the same launch,
+    i.e. the per-GPU compute of a real 8-GPU ring, step by step."""
+    from ringmaster_amd.ring.zigzag import KernelTimer, ring_backward, ring_forward
+
+    P, S, H, D = 8, 131072, 16, 128
+    L = S // P
+    q, k, v = _gen((P, 1, H, L, D), 1), _gen((P, 1, H, L, D), 2), _gen((P, 1, H, L, D), 3)
+    dout = _gen((P, 1, L, H, D), 4)
+    scale = 1.0 / math.sqrt(D)
+    _, lse, out32 = ring_forward(q, k, v, scale)  # the global out / lse the backward reads
+    res = {}
+    for r in ranks:
+        only = {r}
+
+        def step(t=None):
+            ring_forward(q, k, v, scale, timer=t, only_ranks=only)
+            ring_backward(dout, q, k, v, out32, lse, scale, timer=t, only_ranks=only)
+
+        for _ in range(warmup):
+            step()
+        _sync()
+        timer = KernelTimer()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(timer)
+        _sync()
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        per = {}
+        for name in ("attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq"):
+            spans = timer.events[name]
+            per_step = [sum(a.elapsed_time(b) for a, b in spans[i::P]) / steps for i in range(P)]
+            per[name] = [round(x, 3) for x in per_step]
+        res[f"rank{r}"] = {"ms_fwd_bwd": round(ms, 3),
+                           "fwd_ms_per_ring_step": per["attn_fwd"],
+                           "dkdv_ms_per_ring_step": per["attn_bwd_dkdv"],
+                           "dq_ms_per_ring_step": per["attn_bwd_dq"]}
+    return res
+
+
 def distflash_workload(steps, warmup):
     """The DistFlash (contiguous, load-balanced causal) ring at the configs[2] shape: P=8,
     S=131072 (16384 contiguous tokens per rank), H=16, D=128, bf16, fwd+bwd. Same attended
@@ -309,6 +350,34 @@ def scan_workload(steps, warmup):
             "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "fwd_GB/s": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
             "bwd_GB/s": round(bb / (bwd_ms * 1e-3) / 1e9, 1)}
+
+
+def scan_long_workload(steps, warmup):
+    """The L-parallel (chained) cp_linear_scan on long sequences: a token-level recurrence
+    over configs[2]'s 131072 tokens with 4096 channels (32 decay groups), and the long-L /
+    small-d shape L=65536, d=256 (8 groups). Algorithmic bytes: fwd reads b, writes h;
+    bwd reads h, dh, writes db (a, da: 1/128 of that or less)."""
+    from ringmaster_amd.strategies.state_passing import linear_scan_backward, linear_scan_forward
+
+    res = {}
+    for (B, L, d, G) in ((1, 131072, 4096, 32), (1, 65536, 256, 8)):
+        g = torch.Generator(device="cuda").manual_seed(5)
+        a = 1.0 - 0.01 * torch.rand(B, L, G, generator=g, device="cuda")
+        b = torch.randn(B, L, d, generator=g, device="cuda")
+        dh = torch.randn(B, L, d, generator=g, device="cuda")
+        h = linear_scan_forward(a, b, algo="chunked")
+        fwd_ms = _time(lambda: linear_scan_forward(a, b, algo="chunked"), steps, warmup)
+        bwd_ms = _time(lambda: linear_scan_backward(a, h, dh, algo="chunked"), steps, warmup)
+        n = B * L * d * 4
+        fb, bb = 2 * n + a.numel() * 4, 3 * n + 2 * a.numel() * 4
+        res[f"B{B}_L{L}_d{d}_G{G}"] = {
+            "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+            "fwd_GB/s": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
+            "bwd_GB/s": round(bb / (bwd_ms * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round((fb + bb) / ((fwd_ms + bwd_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del a, b, dh, h
+        torch.cuda.empty_cache()
+    return res
 
 
 def mamba_workload(steps, warmup):
@@ -579,6 +648,8 @@ def main():
                     help="one ring step + copy calibration, for rocprofv3 counter passes")
     ap.add_argument("--gemm-ceiling", action="store_true",
                     help="time torch bf16 GEMMs (hipBLASLt) at 8192^3 and 16384^3 and exit")
+    ap.add_argument("--per-rank", action="store_true",
+                    help="time one simulated rank of configs[2] (ranks 0 and 7) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -595,6 +666,9 @@ def main():
     if args.gemm_ceiling:
         print(json.dumps({"gemm_ceiling": gemm_ceiling()}))
         return
+    if args.per_rank:
+        print(json.dumps({"per_rank_configs2": per_rank_workload(args.steps, args.warmup)}))
+        return
 
     ring = ring_workload(args.steps, args.warmup)
     ring["roofline"]["traffic"] = _traffic(ring["roofline"]["kernel"])
@@ -607,6 +681,8 @@ def main():
         extras["lse_merge_configs1"] = merge_workload(50, 5)
         torch.cuda.empty_cache()
         extras["cp_linear_scan_configs4"] = scan_workload(30, 3)
+        torch.cuda.empty_cache()
+        extras["cp_linear_scan_long_L"] = scan_long_workload(10, 2)
         torch.cuda.empty_cache()
         extras["mamba2_correction_configs4"] = mamba_workload(30, 3)
         torch.cuda.empty_cache()
@@ -621,6 +697,8 @@ def main():
         extras["varlen_configs3"] = varlen_workload(3, 1)
         torch.cuda.empty_cache()
         extras["distflash_configs2_shape"] = distflash_workload(2, 1)
+        torch.cuda.empty_cache()
+        extras["per_rank_configs2"] = per_rank_workload(3, 1)
         torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_heads)
 

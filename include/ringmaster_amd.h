@@ -28,10 +28,11 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 9  /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 10 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
                               8: allocation-free Mamba2 correction bwd;
-                              9: carried-in state h_in / dh_in of the linear scan */
+                              9: carried-in state h_in / dh_in of the linear scan;
+                              10: L-parallel linear scan (workspace argument) */
 
 /* error codes */
 #define RMX_OK 0
@@ -214,7 +215,20 @@ int32_t rmx_zigzag_scatter(const void* src, void* dst, int32_t batch, int32_t se
  */
 int32_t rmx_linear_scan_fwd(const float* a, const float* b, const float* h_in, float* h,
                             float* chunk_state, int32_t batch, int32_t L, int32_t d,
-                            int32_t groups, int32_t world, void* stream);
+                            int32_t groups, int32_t world, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace of the L-parallel scan path of rmx_linear_scan_fwd / _bwd for this shape (same
+ * value for both directions), and through chunk_tokens (nullable) its chunk length. With
+ * workspace == NULL the scan entry points run a thread per channel along the whole sequence
+ * (the fast form when batch * d fills the GPU); with a workspace of at least this size they
+ * run the chained scan that is parallel over L (long sequences, few channels). Only one call
+ * may use a workspace at a time. With chunk_state, the L-parallel path needs L / world to
+ * be a multiple of the chunk length.
+ */
+size_t rmx_linear_scan_workspace(int32_t batch, int32_t L, int32_t d, int32_t groups,
+                                 int32_t* chunk_tokens);
 
 /*
  * Gradient of rmx_linear_scan_fwd (what autograd through the reference's loop, cumprod
@@ -225,7 +239,8 @@ int32_t rmx_linear_scan_fwd(const float* a, const float* b, const float* h_in, f
  */
 int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* h_in, const float* dh,
                             float* da, float* db, float* dh_in, int32_t batch, int32_t L,
-                            int32_t d, int32_t groups, int32_t world, void* stream);
+                            int32_t d, int32_t groups, int32_t world, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /*
  * Mamba2 context-parallel output correction (strategies/mamba.py:101-139):

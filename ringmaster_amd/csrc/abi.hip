@@ -269,15 +269,52 @@ static int check_scan(int batch, int L, int d, int groups, int world) {
   return RMX_OK;
 }
 
+// The L-parallel path's plan for a validated shape; fails when the caller's workspace is
+// too small or the shape does not fit its 32-bit chunk tickets.
+static int scan_chunk_plan_for(rmx::ScanChunkPlan& p, int batch, int L, int d, int groups,
+                               size_t workspace_bytes) {
+  p = rmx::scan_chunk_plan(batch, L, d, groups);
+  if ((int64_t)batch * p.ntiles * p.nchunks >= ((int64_t)1 << 31))
+    return fail(RMX_EINVAL, "%lld chunks exceed the chained scan's 2^31 tickets",
+                (long long)batch * p.ntiles * p.nchunks);
+  if (workspace_bytes < p.bytes)
+    return fail(RMX_EINVAL, "workspace of %zu bytes is below the %zu the L-parallel scan needs",
+                workspace_bytes, p.bytes);
+  return RMX_OK;
+}
+
+size_t rmx_linear_scan_workspace(int32_t batch, int32_t L, int32_t d, int32_t groups,
+                                 int32_t* chunk_tokens) {
+  if (batch <= 0 || L <= 0 || d <= 0 || groups <= 0 || d % groups) {
+    if (chunk_tokens) *chunk_tokens = 0;
+    return 0;
+  }
+  const rmx::ScanChunkPlan p = rmx::scan_chunk_plan(batch, L, d, groups);
+  if (chunk_tokens) *chunk_tokens = p.TC;
+  return p.bytes;
+}
+
 int32_t rmx_linear_scan_fwd(const float* a, const float* b, const float* h_in, float* h,
                             float* chunk_state, int32_t batch, int32_t L, int32_t d, int32_t groups,
-                            int32_t world, void* stream) {
+                            int32_t world, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_scan(batch, L, d, groups, world);
   if (rc) return rc;
   if ((int64_t)batch * L * d == 0) return RMX_OK;
   if (!a || !b || !h) return fail(RMX_EINVAL, "NULL tensor pointer");
   if (!aligned(a, 16) || !aligned(b, 16) || !aligned(h, 16) || (h_in && !aligned(h_in, 16)))
     return fail(RMX_EINVAL, "a, b, h_in and h must be 16-byte aligned");
+  if (workspace) {
+    rmx::ScanChunkPlan p;
+    if ((rc = scan_chunk_plan_for(p, batch, L, d, groups, workspace_bytes))) return rc;
+    if (chunk_state && (L / world) % p.TC)
+      return fail(RMX_EINVAL,
+                  "chunk_state with the L-parallel scan needs L / world (%d) to be a multiple "
+                  "of its %d-token chunks (run it without a workspace)", L / world, p.TC);
+    return dev_status(rmx::launch_linear_scan_fwd_chunked(p, a, b, h_in, h, chunk_state, workspace,
+                                                          batch, L, d, groups, world,
+                                                          (hipStream_t)stream),
+                      "rmx_linear_scan_fwd launch");
+  }
   return dev_status(
       rmx::launch_linear_scan_fwd(a, b, h_in, h, chunk_state, batch, L, d, groups, world,
                                   (hipStream_t)stream),
@@ -286,7 +323,8 @@ int32_t rmx_linear_scan_fwd(const float* a, const float* b, const float* h_in, f
 
 int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* h_in, const float* dh,
                             float* da, float* db, float* dh_in, int32_t batch, int32_t L,
-                            int32_t d, int32_t groups, int32_t world, void* stream) {
+                            int32_t d, int32_t groups, int32_t world, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   int rc = check_scan(batch, L, d, groups, world);
   if (rc) return rc;
   if ((int64_t)batch * d == 0) return RMX_OK;
@@ -302,6 +340,14 @@ int32_t rmx_linear_scan_bwd(const float* a, const float* h, const float* h_in, c
     return fail(RMX_EINVAL, "scan tensors must be 16-byte aligned");
   if (dh_in && !h_in)
     return fail(RMX_EINVAL, "dh_in is the gradient of h_in: pass the forward's h_in with it");
+  if (workspace) {
+    rmx::ScanChunkPlan p;
+    if ((rc = scan_chunk_plan_for(p, batch, L, d, groups, workspace_bytes))) return rc;
+    return dev_status(rmx::launch_linear_scan_bwd_chunked(p, a, h, h_in, dh, da, db, dh_in,
+                                                          workspace, batch, L, d, groups,
+                                                          (hipStream_t)stream),
+                      "rmx_linear_scan_bwd launch");
+  }
   return dev_status(rmx::launch_linear_scan_bwd(a, h, h_in, dh, da, db, dh_in, batch, L, d,
                                                 groups, world, (hipStream_t)stream),
                     "rmx_linear_scan_bwd launch");

@@ -28,6 +28,20 @@ hipError_t launch_linear_scan_fwd(const float* a, const float* b, const float* h
 hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* hin,
                                   const float* dh, float* da, float* db, float* dhin, int batch,
                                   int L, int d, int groups, int world, hipStream_t stream);
+// L-parallel (chained) scan: channel tiling, chunk length and workspace layout of one shape
+struct ScanChunkPlan {
+  int V, amode, cw_log2, lg_log2, CT, TC, ntiles, nchunks;
+  size_t words_off, bytes;
+};
+ScanChunkPlan scan_chunk_plan(int batch, int L, int d, int groups);
+hipError_t launch_linear_scan_fwd_chunked(const ScanChunkPlan& p, const float* a, const float* b,
+                                          const float* hin, float* h, float* cs, void* ws,
+                                          int batch, int L, int d, int groups, int world,
+                                          hipStream_t stream);
+hipError_t launch_linear_scan_bwd_chunked(const ScanChunkPlan& p, const float* a, const float* h,
+                                          const float* hin, const float* dh, float* da, float* db,
+                                          float* dhin, void* ws, int batch, int L, int d,
+                                          int groups, hipStream_t stream);
 
 hipError_t launch_mamba2_correction(const uint16_t* out, uint16_t* y, const float* h_final,
                                     float* h_final_out, const uint16_t* C, const float* cum_A,

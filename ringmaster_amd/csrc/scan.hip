@@ -21,69 +21,10 @@
 // When a wave's channels share one decay, da is reduced across the wave for 16
 // steps at a time (and, when the workgroup shares one decay, summed per step in
 // LDS and added to da once per workgroup at the end).
-#include <type_traits>
-
 #include "rmx_kernels.h"
+#include "scan_common.h"
 
 namespace rmx {
-
-// V consecutive fp32 channels (V = 1, 2, 4) as one load / store. Every
-// channel row is read once per pass, so the loads are non-temporal too.
-template <int V>
-__device__ __forceinline__ void ldv(const float* p, float* o) {
-  if constexpr (V == 4) {
-    const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
-#pragma unroll
-    for (int v = 0; v < 4; ++v) o[v] = x[v];
-  } else if constexpr (V == 2) {
-    const f32x2 x = __builtin_nontemporal_load(reinterpret_cast<const f32x2*>(p));
-    o[0] = x[0];
-    o[1] = x[1];
-  } else {
-    o[0] = __builtin_nontemporal_load(p);
-  }
-}
-// Stores are non-temporal: the scan outputs stream past the caches (h is read
-// back only by the backward, long after).
-template <int V>
-__device__ __forceinline__ void stv(float* p, const float* o) {
-  if constexpr (V == 4) {
-    __builtin_nontemporal_store(f32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<f32x4*>(p));
-  } else if constexpr (V == 2) {
-    __builtin_nontemporal_store(f32x2{o[0], o[1]}, reinterpret_cast<f32x2*>(p));
-  } else {
-    __builtin_nontemporal_store(o[0], p);
-  }
-}
-
-// Sum over the 64 lanes of a wave of 16 per-lane values (one per step): a
-// transposing butterfly in which, at the stage with mask M, each lane keeps the
-// half of its partial sums selected by lane bit M and adds the partner's copy
-// of that half (17 exchanges for 16 steps). Returns the wave sum of step
-// u = 8 b5 + 4 b4 + 2 b3 + b2 of the lane (b = lane bits, so the lanes with
-// b1 = b0 = 0 hold all 16 steps between them) and sets `u`.
-__device__ __forceinline__ float wave_sum16(float (&part)[16], int lane, int& u) {
-  auto stage = [&](auto mask, auto halfc) {
-    constexpr int M = decltype(mask)::value, H = decltype(halfc)::value;
-    const bool hi = (lane & M) != 0;
-#pragma unroll
-    for (int i = 0; i < H; ++i) {
-      const float keep = hi ? part[H + i] : part[i];
-      const float send = hi ? part[i] : part[H + i];
-      part[i] = keep + __shfl_xor(send, M, 64);
-    }
-  };
-  stage(std::integral_constant<int, 32>{}, std::integral_constant<int, 8>{});
-  stage(std::integral_constant<int, 16>{}, std::integral_constant<int, 4>{});
-  stage(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
-  stage(std::integral_constant<int, 4>{}, std::integral_constant<int, 1>{});
-  float x = part[0];
-  x += __shfl_xor(x, 2, 64);
-  x += __shfl_xor(x, 1, 64);
-  u = ((lane >> 2) & 1) | (((lane >> 3) & 1) << 1) | (((lane >> 4) & 1) << 2) |
-      (((lane >> 5) & 1) << 3);
-  return x;
-}
 
 // AMODE 0: the V channels of a thread share one decay per step (group size % V == 0)
 // AMODE 1: elementwise decay (groups == d)
@@ -338,35 +279,71 @@ __global__ void scan_fill_zero_kernel(float* p, int64_t n) {
     p[i] = 0.f;
 }
 
-// Channels per thread V and decay mode; WAVE_REDUCE needs a wave's 64 V
-// channels in one group, LDS_DA a workgroup's 256 V channels.
-static constexpr int kScanV = 2;
-
-static int scan_amode(int d, int groups) {
+// Decay mode for V channels per thread: 0 when the V channels of a thread share one
+// decay, 1 elementwise, 2 otherwise (then V = 1).
+static int scan_amode(int d, int groups, int V) {
   const int gs = d / groups;
-  if (d % kScanV == 0 && gs % kScanV == 0) return 0;
-  if (d % kScanV == 0 && gs == 1) return 1;
+  if (d % V == 0 && gs % V == 0) return 0;
+  if (d % V == 0 && gs == 1) return 1;
   return 2;
+}
+
+// Four channels per thread (16-byte accesses) where the shape allows, else two, else one.
+static int scan_v(int d, int groups) {
+  for (int V : {4, 2})
+    if (scan_amode(d, groups, V) != 2) return V;
+  return 1;
+}
+
+template <int V>
+static void launch_fwd_v(int mode, unsigned grid, const float* a, const float* b, const float* hin,
+                         float* h, float* cs, int batch, int L, int d, int groups, int world,
+                         hipStream_t stream) {
+  if (mode == 0)
+    hipLaunchKernelGGL((linear_scan_fwd_kernel<0, V>), dim3(grid), dim3(256), 0, stream, a, b, hin,
+                       h, cs, batch, L, d, groups, world);
+  else
+    hipLaunchKernelGGL((linear_scan_fwd_kernel<1, V>), dim3(grid), dim3(256), 0, stream, a, b, hin,
+                       h, cs, batch, L, d, groups, world);
 }
 
 hipError_t launch_linear_scan_fwd(const float* a, const float* b, const float* hin, float* h,
                                   float* cs, int batch, int L, int d, int groups, int world,
                                   hipStream_t stream) {
   if ((int64_t)batch * L * d == 0) return hipSuccess;
-  const int mode = scan_amode(d, groups);
-  const int V = mode == 2 ? 1 : kScanV;
+  const int V = scan_v(d, groups);
+  const int mode = scan_amode(d, groups, V);
   const int64_t n = (int64_t)batch * (d / V);
   const unsigned grid = (unsigned)((n + 255) / 256);
-  if (mode == 0)
-    hipLaunchKernelGGL((linear_scan_fwd_kernel<0, kScanV>), dim3(grid), dim3(256), 0, stream, a, b,
-                       hin, h, cs, batch, L, d, groups, world);
-  else if (mode == 1)
-    hipLaunchKernelGGL((linear_scan_fwd_kernel<1, kScanV>), dim3(grid), dim3(256), 0, stream, a, b,
-                       hin, h, cs, batch, L, d, groups, world);
+  if (V == 4)
+    launch_fwd_v<4>(mode, grid, a, b, hin, h, cs, batch, L, d, groups, world, stream);
+  else if (V == 2)
+    launch_fwd_v<2>(mode, grid, a, b, hin, h, cs, batch, L, d, groups, world, stream);
   else
     hipLaunchKernelGGL((linear_scan_fwd_kernel<2, 1>), dim3(grid), dim3(256), 0, stream, a, b, hin,
                        h, cs, batch, L, d, groups, world);
   return hipGetLastError();
+}
+
+// WAVE_REDUCE needs a wave's 64 V channels in one decay group, LDS_DA a workgroup's 256.
+template <int V>
+static void launch_bwd_v(int mode, unsigned grid, const float* a, const float* h, const float* hin,
+                         const float* dh, float* da, float* db, float* dhin, int batch, int L,
+                         int d, int groups, hipStream_t stream) {
+  const int gs = d / groups;
+  if (mode == 1)
+    hipLaunchKernelGGL((linear_scan_bwd_kernel<1, V, false, false>), dim3(grid), dim3(256), 0,
+                       stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
+  else if (gs % (256 * V) == 0 && L <= 16384)
+    hipLaunchKernelGGL((linear_scan_bwd_kernel<0, V, true, true>), dim3(grid), dim3(256),
+                       (size_t)L * sizeof(float), stream, a, h, hin, dh, da, db, dhin, batch, L, d,
+                       groups);
+  else if (gs % (64 * V) == 0)
+    hipLaunchKernelGGL((linear_scan_bwd_kernel<0, V, true, false>), dim3(grid), dim3(256), 0,
+                       stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
+  else
+    hipLaunchKernelGGL((linear_scan_bwd_kernel<0, V, false, false>), dim3(grid), dim3(256), 0,
+                       stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
 }
 
 hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* hin,
@@ -380,28 +357,17 @@ hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* h
                          (int64_t)batch * d);
     return hipGetLastError();
   }
-  const int mode = scan_amode(d, groups);
-  const int V = mode == 2 ? 1 : kScanV;
-  const int gs = d / groups;
+  const int V = scan_v(d, groups);
+  const int mode = scan_amode(d, groups, V);
   const int64_t n = (int64_t)batch * (d / V);
   const unsigned grid = (unsigned)((n + 255) / 256);
-  if (mode == 0) {
-    if (gs % (256 * kScanV) == 0 && L <= 16384)
-      hipLaunchKernelGGL((linear_scan_bwd_kernel<0, kScanV, true, true>), dim3(grid), dim3(256),
-                         (size_t)L * sizeof(float), stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
-    else if (gs % (64 * kScanV) == 0)
-      hipLaunchKernelGGL((linear_scan_bwd_kernel<0, kScanV, true, false>), dim3(grid), dim3(256), 0,
-                         stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
-    else
-      hipLaunchKernelGGL((linear_scan_bwd_kernel<0, kScanV, false, false>), dim3(grid), dim3(256),
-                         0, stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
-  } else if (mode == 1) {
-    hipLaunchKernelGGL((linear_scan_bwd_kernel<1, kScanV, false, false>), dim3(grid), dim3(256), 0,
-                       stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
-  } else {
+  if (V == 4)
+    launch_bwd_v<4>(mode, grid, a, h, hin, dh, da, db, dhin, batch, L, d, groups, stream);
+  else if (V == 2)
+    launch_bwd_v<2>(mode, grid, a, h, hin, dh, da, db, dhin, batch, L, d, groups, stream);
+  else
     hipLaunchKernelGGL((linear_scan_bwd_kernel<2, 1, false, false>), dim3(grid), dim3(256), 0,
                        stream, a, h, hin, dh, da, db, dhin, batch, L, d, groups);
-  }
   return hipGetLastError();
 }
 

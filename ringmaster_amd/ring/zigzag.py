@@ -166,13 +166,20 @@ class _NoTimer:
 _NO_TIMER = _NoTimer()
 
 
+def _only(blocks, only_ranks):
+    return blocks if only_ranks is None else [bl for bl in blocks if bl.rank in only_ranks]
+
+
 def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=None,
-                 layout: str = "zigzag", causal: bool = True):
+                 layout: str = "zigzag", causal: bool = True, only_ranks=None):
     """Emulated ring forward (zigzag or contiguous layout). q/k/v: [P, b, H, L, d] bf16
     (interface layout per rank).
     Returns (out [P, b, L, H, d] bf16, lse [P, b, H, L] fp32, out32 [P, b, L, H, d] fp32):
     ``out32`` is the running fp32 accumulator, which the last touch of every row leaves
-    holding the final merged out (the backward's delta is computed from it)."""
+    holding the final merged out (the backward's delta is computed from it).
+    ``only_ranks`` (a set of ranks) launches only those ranks' blocks, each ring step at the
+    grid one GPU of a real P-GPU ring runs; the other ranks' outputs are then not computed
+    (per-rank timing)."""
     timer = timer or _NO_TIMER
     c = _Ctx(q, k, scale, doc, layout, causal)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)  # [P, b, L, H, d] views
@@ -185,7 +192,7 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
         acc_lse = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
     for s, blocks in enumerate(c.schedule(split_final=True)):
         jobs = []
-        for bl in blocks:
+        for bl in _only(blocks, only_ranks):
             r, kr = bl.rank, bl.kv_rank
             qs, ks = slice(bl.q_lo, bl.q_hi), slice(bl.k_lo, bl.k_hi)
             jobs.append(ops.FwdJob(
@@ -202,11 +209,12 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
 
 
 def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | None = None,
-                  timer=None, layout: str = "zigzag", causal: bool = True):
+                  timer=None, layout: str = "zigzag", causal: bool = True, only_ranks=None):
     """Reverse-ring backward with the global out/lse. dout: [P, b, L, H, d] bf16; out: the
     global out, fp32 (the forward's ``out32``) or bf16, [P, b, L, H, d].
     Returns fp32 (dq [P, b, L, Hq, d], dk, dv [P, b, L, Hkv, d]). Each step launches the
-    KV-major dK/dV kernel and the Q-major dQ kernel over all ranks."""
+    KV-major dK/dV kernel and the Q-major dQ kernel over all ranks (``only_ranks``: over
+    those ranks only, as in :func:`ring_forward`; the gradients are then partial)."""
     timer = timer or _NO_TIMER
     c = _Ctx(q, k, scale, doc, layout, causal)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)
@@ -230,7 +238,7 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
     for s, blocks in enumerate(c.schedule(split_final=False)):
         mode = abi.GRAD_WRITE_F32 if s == 0 else abi.GRAD_ACC_F32
         kv_jobs, q_jobs = [], []
-        for bl in blocks:
+        for bl in _only(blocks, only_ranks):
             r, kr = bl.rank, bl.kv_rank
             qs, ks = slice(bl.q_lo, bl.q_hi), slice(bl.k_lo, bl.k_hi)
             common = dict(

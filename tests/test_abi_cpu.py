@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 9
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 10
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -95,20 +95,62 @@ def test_empty_calls_are_noops():
     assert _fwd(_layout(), 0) == abi.RMX_OK
     lib = abi.lib()
     assert lib.rmx_zigzag_gather(None, None, 0, 0, 2, -1, 16, 0, None, None) == abi.RMX_OK
-    assert lib.rmx_linear_scan_fwd(None, None, None, None, None, 0, 8, 4, 4, 2, None) == abi.RMX_OK
+    assert lib.rmx_linear_scan_fwd(None, None, None, None, None, 0, 8, 4, 4, 2, None, 0, None) \
+        == abi.RMX_OK
 
 
 def test_host_validation_shard_and_scan():
     lib = abi.lib()
     assert lib.rmx_zigzag_gather(16, 16, 1, 8, 0, -1, 16, 128, None, None) == abi.RMX_EINVAL
     assert lib.rmx_zigzag_gather(16, 16, 1, 8, 2, 2, 16, 128, None, None) == abi.RMX_EINVAL
-    assert lib.rmx_linear_scan_fwd(16, 16, None, 16, None, 1, 9, 4, 4, 2, None) == abi.RMX_EINVAL
-    assert lib.rmx_linear_scan_fwd(16, 16, None, 16, None, 1, 8, 6, 4, 2, None) == abi.RMX_EINVAL
-    assert lib.rmx_linear_scan_fwd(16, 16, 8, 16, None, 1, 8, 4, 4, 2, None) == abi.RMX_EINVAL
+    fwd = lambda *a: lib.rmx_linear_scan_fwd(*a, None, 0, None)  # noqa: E731
+    assert fwd(16, 16, None, 16, None, 1, 9, 4, 4, 2) == abi.RMX_EINVAL
+    assert fwd(16, 16, None, 16, None, 1, 8, 6, 4, 2) == abi.RMX_EINVAL
+    assert fwd(16, 16, 8, 16, None, 1, 8, 4, 4, 2) == abi.RMX_EINVAL
     assert b"aligned" in lib.rmx_last_error()  # h_in not 16-byte aligned
-    assert lib.rmx_linear_scan_bwd(16, 16, None, 16, 16, 16, 16, 1, 8, 4, 4, 1, None) \
+    assert lib.rmx_linear_scan_bwd(16, 16, None, 16, 16, 16, 16, 1, 8, 4, 4, 1, None, 0, None) \
         == abi.RMX_EINVAL  # dh_in without h_in
     assert b"h_in" in lib.rmx_last_error()
+
+
+def test_scan_workspace_plan_and_checks():
+    """The L-parallel scan's workspace query and the checks of its entry points."""
+    lib = abi.lib()
+    tc = ctypes.c_int32(0)
+    need = lib.rmx_linear_scan_workspace(1, 65536, 256, 8, ctypes.byref(tc))
+    # 256 channels: one 64-lane x 4-channel token group per wave, 4 waves x 16 tokens
+    assert tc.value == 64
+    slots = 65536 // 64
+    assert need >= 256 + slots * 4 + slots * 256 * 12
+    assert lib.rmx_linear_scan_workspace(1, 0, 256, 8, None) == 0
+    assert lib.rmx_linear_scan_workspace(1, 4096, 3, 2, None) == 0  # groups must divide d
+    # d = 1: one channel per token group, 64 token groups per wave
+    lib.rmx_linear_scan_workspace(2, 65536, 1, 1, ctypes.byref(tc))
+    assert tc.value == 4 * 64 * 16
+    # a workspace below the plan's size is refused before any launch
+    assert lib.rmx_linear_scan_fwd(16, 16, None, 16, None, 1, 65536, 256, 8, 1, 16, need - 1,
+                                   None) == abi.RMX_EINVAL
+    assert b"workspace" in lib.rmx_last_error()
+    assert lib.rmx_linear_scan_bwd(16, 16, None, 16, 16, 16, None, 1, 65536, 256, 8, 1, 16,
+                                   need - 1, None) == abi.RMX_EINVAL
+    # chunk states need shards aligned to the chunks
+    assert lib.rmx_linear_scan_fwd(16, 16, None, 16, 16, 1, 65536 - 64 * 8 + 8 * 8, 256, 8, 8, 16,
+                                   need, None) == abi.RMX_EINVAL
+    assert b"chunk" in lib.rmx_last_error()
+
+
+def test_scan_algo_selection():
+    from ringmaster_amd.strategies import state_passing as sp
+
+    ws = sp._workspace("auto", 1, 65536, 256, 8, 1, False, "cpu")
+    assert ws is not None and ws.dtype.itemsize == 1          # long L, few channels: chunked
+    assert sp._workspace("auto", 1, 256, 524288, 64, 8, True, "cpu") is None  # configs[4]
+    assert sp._workspace("per_channel", 1, 65536, 256, 8, 1, False, "cpu") is None
+    assert sp._workspace("auto", 1, 65536 - 8, 256, 8, 8, True, "cpu") is None
+    with pytest.raises(ValueError, match="chunk"):
+        sp._workspace("chunked", 1, 65536 - 8, 256, 8, 8, True, "cpu")
+    with pytest.raises(ValueError, match="algo"):
+        sp._workspace("serial", 1, 65536, 256, 8, 1, False, "cpu")
 
 
 def test_product_refuses_cpu_tensors():

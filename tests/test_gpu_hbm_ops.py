@@ -174,3 +174,30 @@ def test_linear_scan_config4_full_size():
     for r in (0, 7):
         cum = a[:, r * n:(r + 1) * n].prod(1).repeat_interleave(d // G, dim=1)
         assert_f32_rel(cs[r, :, 0], cum, f"A_{r}")
+
+
+def test_linear_scan_config4_full_size_backward():
+    """configs[4] backward at full size (256 chunk states x 524288 fp32, 64 decay groups,
+    world 8): db, da (sums over 8192 channels per group) and the forward, against autograd
+    through the oracle's emulated ranks in fp64 (strategies/state_passing.py:19-59)."""
+    from ringmaster_amd.strategies.state_passing import cp_linear_scan
+
+    L, d, G, world = 256, 524288, 64, 8
+    g = torch.Generator().manual_seed(9)
+    a = torch.rand(1, L, G, generator=g) * 0.9 + 0.05
+    b = torch.randn(1, L, d, generator=g)
+    dh = torch.randn(1, L, d, generator=g)
+    ad, bd = a.cuda().requires_grad_(True), b.cuda().requires_grad_(True)
+    h = cp_linear_scan(ad, bd, world=world)
+    h.backward(dh.cuda())
+    torch.cuda.synchronize()
+    h, da, db = h.detach().cpu(), ad.grad.cpu(), bd.grad.cpu()
+    af = a.double().repeat_interleave(d // G, dim=2).requires_grad_(True)
+    bf = b.double().requires_grad_(True)
+    ref = sp.cp_linear_scan_emulated(af, bf, world)
+    ref.backward(dh.double())
+    assert_f32_rel(h, ref.detach(), "h")
+    del ref
+    assert_f32_rel(db, bf.grad, "db")
+    ref_da = af.grad.reshape(1, L, G, d // G).sum(-1)
+    assert_f32_rel(da, ref_da, "da", tol=1e-3)

@@ -111,3 +111,27 @@ def test_ring_lse_matches_oracle():
         # the fp32 out the backward's delta reads is the merged out before bf16 rounding
         assert_bf16_close(out32[r], ref_out[r], f"fp32 out rank {r}")
         assert torch.equal(out32[r].to(torch.bfloat16), out[r]), f"bf16(out32) != out rank {r}"
+
+
+def test_one_rank_alone_matches_the_full_ring():
+    """``only_ranks`` (the per-rank timing mode) launches one rank's blocks at that rank's own
+    grid: its out / lse / fp32 out and its dQ must equal the batched ring's bit for bit."""
+    from ringmaster_amd.ring.zigzag import ring_backward, ring_forward
+
+    world, half, h, d = 4, 160, 2, 128
+    L = 2 * half
+    g = torch.Generator(device="cuda").manual_seed(11)
+    mk = lambda *s: torch.randn(*s, generator=g, device="cuda").to(torch.bfloat16)  # noqa: E731
+    q, k, v = mk(world, 1, h, L, d), mk(world, 1, h, L, d), mk(world, 1, h, L, d)
+    dout = mk(world, 1, L, h, d)
+    scale = d ** -0.5
+    out, lse, out32 = ring_forward(q, k, v, scale)
+    dq, _, _ = ring_backward(dout, q, k, v, out32, lse, scale)
+    for r in range(world):
+        o1, l1, a1 = ring_forward(q, k, v, scale, only_ranks={r})
+        dq1, _, _ = ring_backward(dout, q, k, v, out32, lse, scale, only_ranks={r})
+        torch.cuda.synchronize()
+        assert torch.equal(o1[r], out[r]), f"out rank {r}"
+        assert torch.equal(l1[r], lse[r]), f"lse rank {r}"
+        assert torch.equal(a1[r], out32[r]), f"fp32 out rank {r}"
+        assert torch.equal(dq1[r], dq[r]), f"dq rank {r}"
