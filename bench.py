@@ -181,10 +181,12 @@ def ring_workload(steps, warmup):
             "sclk_under_load": clk.summary()}
 
 
-def per_rank_workload(steps, warmup, ranks=(0, 7)):
-    """One simulated rank of configs[2] at its real grid: rank r's 8 forward and 16 backward
-    launches (dK/dV and dQ per step) without the other ranks' blocks in the same launch,
-    i.e. the per-GPU compute of a real 8-GPU ring, step by step."""
+def per_rank_workload(steps, warmup):
+    """One simulated GPU of configs[2] at its real grid: the blocks one rank computes, step
+    by step (8 forward and 16 backward launches), without the other ranks' blocks in the
+    same launch: the per-GPU compute of a real 8-GPU ring. Zigzag (ranks 0 and 7: equal
+    work) and DistFlash on contiguous chunks (workers 0, 3, 4, 7: 4.5 blocks of 8192^2...
+    16384^2 for workers 0-3, 3.5 for workers 4-7, schedule.distflash_work)."""
     from ringmaster_amd.ring.zigzag import KernelTimer, ring_backward, ring_forward
 
     P, S, H, D = 8, 131072, 16, 128
@@ -192,33 +194,40 @@ def per_rank_workload(steps, warmup, ranks=(0, 7)):
     q, k, v = _gen((P, 1, H, L, D), 1), _gen((P, 1, H, L, D), 2), _gen((P, 1, H, L, D), 3)
     dout = _gen((P, 1, L, H, D), 4)
     scale = 1.0 / math.sqrt(D)
-    _, lse, out32 = ring_forward(q, k, v, scale)  # the global out / lse the backward reads
     res = {}
-    for r in ranks:
-        only = {r}
+    for layout, ranks in (("zigzag", (0, 7)), ("distflash", (0, 3, 4, 7))):
+        # the global out / lse the backward reads
+        _, lse, out32 = ring_forward(q, k, v, scale, layout=layout)
+        per_layout = {}
+        for r in ranks:
+            only = {r}
 
-        def step(t=None):
-            ring_forward(q, k, v, scale, timer=t, only_ranks=only)
-            ring_backward(dout, q, k, v, out32, lse, scale, timer=t, only_ranks=only)
+            def step(t=None):
+                ring_forward(q, k, v, scale, timer=t, layout=layout, only_ranks=only)
+                ring_backward(dout, q, k, v, out32, lse, scale, timer=t, layout=layout,
+                              only_ranks=only)
 
-        for _ in range(warmup):
-            step()
-        _sync()
-        timer = KernelTimer()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            step(timer)
-        _sync()
-        ms = (time.perf_counter() - t0) / steps * 1e3
-        per = {}
-        for name in ("attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq"):
-            spans = timer.events[name]
-            per_step = [sum(a.elapsed_time(b) for a, b in spans[i::P]) / steps for i in range(P)]
-            per[name] = [round(x, 3) for x in per_step]
-        res[f"rank{r}"] = {"ms_fwd_bwd": round(ms, 3),
-                           "fwd_ms_per_ring_step": per["attn_fwd"],
-                           "dkdv_ms_per_ring_step": per["attn_bwd_dkdv"],
-                           "dq_ms_per_ring_step": per["attn_bwd_dq"]}
+            for _ in range(warmup):
+                step()
+            _sync()
+            timer = KernelTimer()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step(timer)
+            _sync()
+            ms = (time.perf_counter() - t0) / steps * 1e3
+            per = {}
+            for name in ("attn_fwd", "attn_bwd_dkdv", "attn_bwd_dq"):
+                spans = timer.events[name]
+                per[name] = [round(sum(a.elapsed_time(b) for a, b in spans[i::P]) / steps, 3)
+                             for i in range(P)]
+            per_layout[f"rank{r}"] = {"ms_fwd_bwd": round(ms, 3),
+                                      "fwd_ms_per_step": per["attn_fwd"],
+                                      "dkdv_ms_per_step": per["attn_bwd_dkdv"],
+                                      "dq_ms_per_step": per["attn_bwd_dq"]}
+        res[layout] = per_layout
+        del lse, out32
+        torch.cuda.empty_cache()
     return res
 
 
@@ -649,7 +658,7 @@ def main():
     ap.add_argument("--gemm-ceiling", action="store_true",
                     help="time torch bf16 GEMMs (hipBLASLt) at 8192^3 and 16384^3 and exit")
     ap.add_argument("--per-rank", action="store_true",
-                    help="time one simulated rank of configs[2] (ranks 0 and 7) and exit")
+                    help="time single simulated GPUs of configs[2] (zigzag, DistFlash) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "

@@ -34,6 +34,11 @@ class Block:
     causal: bool
     first: bool = True
     last: bool = True
+    worker: int | None = None  # the rank whose GPU computes the block (None: ``rank``)
+
+    @property
+    def runs_on(self) -> int:
+        return self.rank if self.worker is None else self.worker
 
     @property
     def pairs(self) -> int:
@@ -124,6 +129,38 @@ def contiguous_schedule(world: int, local_len: int, *, causal: bool) -> list[lis
 def contiguous_gidx(rank: int, local_len: int) -> list[int]:
     """Global token indices of ``rank``'s contiguous chunk."""
     return list(range(rank * local_len, (rank + 1) * local_len))
+
+
+def distflash_schedule(world: int, local_len: int) -> list[list[Block]]:
+    """DistFlash's steps (ring/distflash.py:87-152) in the reference's merge order, every
+    causal block ``(q_i, kv_j)``, ``i >= j``, exactly once:
+
+    * step 0: each rank's diagonal block, causal (:113);
+    * phase 2, ``d = P//2 + 1 .. P-1`` (:115-121): the query owner ``r`` computes
+      ``(q_r, kv_{r-d})`` for ``r >= d`` with the KV block rotated to it;
+    * phase 1, ``d = 1 .. P//2`` (:123-133): the helper ``r`` (the KV owner) computes
+      ``(q_{r+d}, kv_r)`` for ``r + d < P`` and routes the partial (out, lse) to the
+      owner ``r + d``, which merges it after its own blocks.
+
+    ``rank`` is the query owner (whose rows the block merges into), ``kv_rank`` the KV
+    owner, ``worker`` the rank that computes it; ``first`` / ``last`` mark the first
+    and last block merged into the owner's rows in this order."""
+    if world < 1:
+        raise ValueError("world must be positive")
+    if local_len < 1:
+        raise ValueError("local length must be positive")
+    half = world // 2
+    order = [[(r, r, r) for r in range(world)]]  # (query owner, KV owner, worker)
+    for d in range(half + 1, world):
+        order.append([(r, r - d, r) for r in range(d, world)])
+    for d in range(1, half + 1):
+        order.append([(r + d, r, r) for r in range(world - d)])
+    last = {}
+    for s, step in enumerate(order):
+        for qi, _, _ in step:
+            last[qi] = s
+    return [[Block(qi, 0, local_len, kj, 0, local_len, s == 0, s == 0, last[qi] == s, worker=w)
+             for qi, kj, w in step] for s, step in enumerate(order)]
 
 
 def distflash_work(world: int) -> list[int]:

@@ -31,7 +31,7 @@ import torch
 
 from ringmaster_amd import abi
 from ringmaster_amd.ring import ops
-from ringmaster_amd.ring.schedule import contiguous_schedule, zigzag_schedule
+from ringmaster_amd.ring.schedule import contiguous_schedule, distflash_schedule, zigzag_schedule
 
 
 def doc_ids_from_cu(cu_seqlens: torch.Tensor, device, total: int | None = None) -> torch.Tensor:
@@ -82,8 +82,9 @@ def _global_rows(layout: str, P: int, L: int, device) -> torch.Tensor:
 
 class _Ctx:
     """Per-call tensors shared by the forward and backward passes. ``layout`` is
-    "zigzag" (rank r holds chunks r and 2P-1-r) or "contiguous" (rank r holds
-    chunk r); the zigzag ring is causal only."""
+    "zigzag" (rank r holds chunks r and 2P-1-r), "contiguous" (rank r holds chunk r)
+    or "distflash" (contiguous chunks, DistFlash's helper / owner work placement); the
+    zigzag and DistFlash rings are causal only."""
 
     def __init__(self, q, k, scale, doc, layout="zigzag", causal=True):
         self.P, self.b, self.hq, self.L, self.d = q.shape
@@ -101,6 +102,8 @@ class _Ctx:
     def schedule(self, split_final: bool):
         if self.layout == "zigzag":
             return zigzag_schedule(self.P, self.L, split_final=split_final)
+        if self.layout == "distflash":
+            return distflash_schedule(self.P, self.L)
         return contiguous_schedule(self.P, self.L, causal=self.causal)
 
     def mask(self, step: int) -> int:
@@ -167,7 +170,8 @@ _NO_TIMER = _NoTimer()
 
 
 def _only(blocks, only_ranks):
-    return blocks if only_ranks is None else [bl for bl in blocks if bl.rank in only_ranks]
+    """The blocks the ranks in ``only_ranks`` compute (all blocks for None)."""
+    return blocks if only_ranks is None else [bl for bl in blocks if bl.runs_on in only_ranks]
 
 
 def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=None,
@@ -177,9 +181,10 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
     Returns (out [P, b, L, H, d] bf16, lse [P, b, H, L] fp32, out32 [P, b, L, H, d] fp32):
     ``out32`` is the running fp32 accumulator, which the last touch of every row leaves
     holding the final merged out (the backward's delta is computed from it).
-    ``only_ranks`` (a set of ranks) launches only those ranks' blocks, each ring step at the
-    grid one GPU of a real P-GPU ring runs; the other ranks' outputs are then not computed
-    (per-rank timing)."""
+    ``only_ranks`` (a set of ranks) launches only the blocks those ranks compute (for
+    DistFlash the helper computes blocks of other ranks' queries), each step at the grid
+    one GPU of a real P-GPU ring runs; outputs of the blocks left out are then not
+    computed (per-rank timing)."""
     timer = timer or _NO_TIMER
     c = _Ctx(q, k, scale, doc, layout, causal)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)  # [P, b, L, H, d] views

@@ -5,7 +5,8 @@ import pytest
 import torch
 
 from ringmaster_amd.balancers import contiguous_indices, head_tail_indices
-from ringmaster_amd.ring.schedule import (contiguous_gidx, contiguous_schedule, distflash_work,
+from ringmaster_amd.ring.schedule import (contiguous_gidx, contiguous_schedule,
+                                          distflash_schedule, distflash_work,
                                           ring_pairs_per_rank, zigzag_gidx, zigzag_schedule)
 
 
@@ -119,6 +120,61 @@ def test_distflash_balance_literals():
         work = distflash_work(world)
         assert sum(work) == world * (world + 1) // 2  # every causal block exactly once
         assert max(work) - min(work) <= 1
+
+
+def _reference_distflash_blocks(world):
+    """(query owner, KV owner, worker) in the order the reference's forward merges them
+    into the owner's rows, read off its loops (ring/distflash.py:113-133): the diagonal,
+    the phase-2 loop over d = 1..P-1 keeping d > P//2 and r - d >= 0, then the phase-1
+    loop over d = 1..P//2 where helper r computes q_{r+d} for r + d < P."""
+    half = world // 2
+    per_owner = {r: [(r, r, r)] for r in range(world)}
+    for r in range(world):
+        for d in range(1, world):
+            if d > half and r - d >= 0:
+                per_owner[r].append((r, r - d, r))
+    for d in range(1, half + 1):
+        for r in range(world):
+            if r + d < world:
+                per_owner[r + d].append((r + d, r, r))
+    return per_owner
+
+
+@pytest.mark.parametrize("world", [1, 2, 3, 4, 5, 8])
+def test_distflash_schedule_is_the_reference_placement(world):
+    L = 4
+    steps = distflash_schedule(world, L)
+    seen, per_owner, per_worker = set(), {r: [] for r in range(world)}, [0] * world
+    for s, blocks in enumerate(steps):
+        assert blocks, "no empty steps"
+        assert len({b.rank for b in blocks}) == len(blocks)      # one block per owner per step
+        assert len({b.kv_rank for b in blocks}) == len(blocks)   # one dK/dV target per step
+        for b in blocks:
+            i, j, w = b.rank, b.kv_rank, b.runs_on
+            assert i >= j and (i, j) not in seen
+            seen.add((i, j))
+            assert (b.q_lo, b.q_hi, b.k_lo, b.k_hi) == (0, L, 0, L)
+            assert b.causal == (s == 0) == (i == j) == b.first
+            d = i - j
+            assert w == (i if (d == 0 or d > world // 2) else j)  # owner / helper placement
+            per_owner[i].append((i, j, w))
+            per_worker[w] += 1
+    assert len(seen) == world * (world + 1) // 2                 # every causal block once
+    assert per_owner == _reference_distflash_blocks(world)       # the reference's merge order
+    assert per_worker == distflash_work(world)
+    last = {b.rank: s for s, blocks in enumerate(steps) for b in blocks}
+    for s, blocks in enumerate(steps):
+        for b in blocks:
+            assert b.last == (last[b.rank] == s)
+
+
+def test_distflash_balance_at_eight_ranks():
+    assert distflash_work(8) == [5, 5, 5, 5, 4, 4, 4, 4]
+    steps = distflash_schedule(8, 1)
+    # in units of a full block (the diagonal is half of one): 4.5 for ranks 0-3, 3.5 for 4-7
+    units = [sum(0.5 if b.causal else 1.0 for st in steps for b in st if b.runs_on == r)
+             for r in range(8)]
+    assert units == [4.5] * 4 + [3.5] * 4
 
 
 @pytest.mark.parametrize("world,L", [(1, 8), (2, 8), (4, 6), (3, 10)])
