@@ -585,6 +585,13 @@ def cpu_baseline(heads=1):
     out1, lse1 = rm.masked_block_fwd(q[:, h:], kr, vr, 0.0, scale)
     rm.masked_block_bwd(dout[:, h:], q[:, h:], kr, vr, out1, lse1, 0.0, scale)
     sec = time.perf_counter() - t0
+    cpu_model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
+                             None)
+    except OSError:
+        pass
     pairs = L * (L + 1) // 2 + h * L
     flops = 14 * D * heads * pairs
     return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s",
@@ -593,7 +600,7 @@ def cpu_baseline(heads=1):
                       f"causal) and one remote step block (8192x16384), {heads} head(s), D=128: "
                       f"{pairs} pairs = 2 of the 8 blocks of one rank of configs[2] "
                       f"({sec:.1f} s; os.cpu_count()={os.cpu_count()})",
-            "seconds": round(sec, 2)}
+            "seconds": round(sec, 2), "cpu_model": cpu_model}
 
 
 # ---------------------------------------------------------------- profiling mode

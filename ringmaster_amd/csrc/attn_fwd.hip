@@ -11,27 +11,27 @@
 // (problem, batch, head); each wave owns 32 queries and walks the key tiles
 // (64 keys) that the mask leaves.
 //
-// Per key tile j a wave runs two "slots" (v_mfma_f32_32x32x16_bf16):
-//   M_j  O^T += V_{j-1}^T P_{j-1}^T   A = V^T by ds_read_b64_tr_b16 from the
-//                                     row-major V tile, B = P from registers
-//        S_j^T = K_j Q^T              A = K rows from LDS (rows sigma-permuted,
-//                                     see rmx_common.h), B = Q in VGPRs
-//        (32 MFMAs, two independent chains)
-//   X_j  mask, online softmax of S_j -> P_j (one lane owns one query, the two
-//        lane halves split the keys; the running max only moves when a tile
-//        raises it by more than 2^8, so the O rescale is rare)
-// Ping-pong: waves 0-3 (group A) and 4-7 (group B) -- the dispatcher places
-// waves w and w + 4 on the same SIMD -- run this program one slot apart, with a
-// workgroup barrier between slots: while group A is in M_j, group B is in
-// X_{j-1}, then A in X_j while B is in M_j. Every SIMD thus has one wave issuing
-// MFMAs and one doing the softmax in every slot.
+// Each wave runs a software pipeline over the key tiles (v_mfma_f32_32x32x16_bf16);
+// iteration j holds S_j = (K_j Q^T)^T (masked, its row max folded in) and does
+//   region 1: S_{j+1} = K_{j+1} Q^T (A = K rows from LDS, rows sigma-permuted,
+//             see rmx_common.h; B = Q in VGPRs) while the VALU computes the
+//             exponentials of the first 3/4 of S_j and packs them to bf16 (P_j);
+//   region 2: O^T += V_j^T P_j^T (A = V^T by ds_read_b64_tr_b16 from the
+//             row-major V tile, B = P_j from registers) while the VALU finishes
+//             the exponentials of S_j and takes the row max of S_{j+1};
+//   then the online-softmax rescale decision for tile j + 1 (the running max
+//   only moves when a tile raises it by more than 2^8, so the O rescale is
+//   rare) and one workgroup barrier.
+// One lane owns one query; the two lane halves split the keys. Operands are read
+// from LDS three steps ahead of their MFMA, and scheduling fences keep each
+// step's VALU work under its MFMAs.
 // K/V tiles: direct global->LDS loads (buffer_load ... lds; rows past the end
-// read as zeros) into three K and three V buffers. The loads issued at slot 2i
-// (K_{i+2}, V_{i+1}) are first read at slot 2i+4, and each odd slot's barrier
-// waits only for the loads of the even slot two before it. The 16-byte chunks
-// of the unpadded LDS rows are XOR-swizzled (swz_rows for K, swz_tr for V) so
-// both the row reads and the transposed reads are bank-conflict free. The loads
-// are the asm form (dma16_async, dma4_async): the kernel orders every LDS read
+// read as zeros) into four K and three V buffers. Iteration j issues K_{j+3}
+// and V_{j+2}, which iteration j + 2 is the first to read, and its closing
+// barrier waits only for the loads issued before it. The 16-byte chunks of the
+// unpadded LDS rows are XOR-swizzled (swz_rows for K, swz_tr for V) so both
+// the row reads and the transposed reads are bank-conflict free. The loads are
+// the asm form (dma16_async, dma4_async): the kernel orders every LDS read
 // after them itself.
 #include <type_traits>
 #include <utility>
@@ -94,7 +94,6 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int grp = wave >> 2;                                  // ping-pong group
   const int lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int qw0 = q0 + 32 * wave;  // first query of this wave
   const int q = qw0 + l32;         // this lane's query

@@ -26,6 +26,7 @@ block (ring/zigzag.py:86-120,170-209); dense inputs use the causal / full cases.
 from __future__ import annotations
 
 import math
+import os
 
 import torch
 
@@ -294,15 +295,28 @@ def check_ring_inputs(q, k, v):
         raise NotImplementedError("the MI355X ring computes in bf16")
 
 
+def check_cu_seqlens(cu_seqlens, total: int) -> None:
+    """``cu_seqlens`` starts at 0, never decreases and ends at ``total`` (ValueError)."""
+    cu = cu_seqlens.detach().to("cpu", torch.int64)
+    if cu.dim() != 1 or cu.numel() < 2:
+        raise ValueError("cu_seqlens must be 1-D with at least two entries")
+    if int(cu[0]) != 0 or int(cu[-1]) != total:
+        raise ValueError(f"cu_seqlens must run from 0 to the full (padded) sequence {total} "
+                         f"(got {int(cu[0])} .. {int(cu[-1])})")
+    if bool((cu.diff() < 0).any()):
+        raise ValueError("cu_seqlens must not decrease")
+
+
 def doc_for(cu_seqlens, q):
     """Per-token document ids of the packed sequence (None when not packed). A host
     ``cu_seqlens`` is checked to cover the sequence; a device one is read without a
-    synchronization and must end at the sequence length."""
+    synchronization and must end at the sequence length, which the environment variable
+    ``RINGMASTER_AMD_DEBUG=1`` checks too (at the cost of a device-to-host copy)."""
     if cu_seqlens is None:
         return None
     total = q.shape[0] * q.shape[3]
-    if cu_seqlens.device.type == "cpu" and int(cu_seqlens[-1]) != total:
-        raise ValueError("cu_seqlens must cover the full (padded) sequence")
+    if cu_seqlens.device.type == "cpu" or os.environ.get("RINGMASTER_AMD_DEBUG") == "1":
+        check_cu_seqlens(cu_seqlens, total)
     return doc_ids_from_cu(cu_seqlens, q.device, total)
 
 

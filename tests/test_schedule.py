@@ -200,3 +200,17 @@ def test_sync_free_doc_ids_match_repeat_interleave(lens):
     fast = doc_ids_from_cu(cu, "cpu", sum(lens))
     assert fast.dtype == ref.dtype == torch.int32
     assert torch.equal(fast, ref)
+
+
+def test_cu_seqlens_checks():
+    from ringmaster_amd.ring.zigzag import check_cu_seqlens, doc_for
+
+    check_cu_seqlens(torch.tensor([0, 3, 3, 8]), 8)  # empty documents are allowed
+    for bad, match in (([1, 8], "from 0"), ([0, 7], "from 0"), ([0, 5, 4, 8], "decrease"),
+                       ([8], "two entries")):
+        with pytest.raises(ValueError, match=match):
+            check_cu_seqlens(torch.tensor(bad), 8)
+    q = torch.zeros(2, 1, 1, 4, 8)                      # [P, b, H, L, d]: total 8
+    assert doc_for(torch.tensor([0, 5, 8], dtype=torch.int32), q).tolist() == [0] * 5 + [1] * 3
+    with pytest.raises(ValueError):
+        doc_for(torch.tensor([0, 5, 9], dtype=torch.int32), q)
