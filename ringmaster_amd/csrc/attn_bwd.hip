@@ -13,7 +13,13 @@
 //   * attn_bwd_dkdv (KV-major, lane = key): S, dP, dV += P^T dO,
 //     dK += dS^T Q; the workgroup owns its keys and loops over every q-head
 //     of the GQA group, so the fold needs no cross-workgroup reduction.
+#include <utility>
+
 #include "rmx_kernels.h"
+
+#ifndef RMX_DQ_NB
+#define RMX_DQ_NB 2  // K/V tile buffers of the dQ kernel
+#endif
 
 namespace rmx {
 
@@ -126,37 +132,13 @@ __device__ __forceinline__ void grad_store4(int mode, float* acc, uint16_t* bf, 
 }
 
 // ---------------------------------------------------------------- tiles
-// Q-side tiles of the dK/dV kernel (Q, dO) and the K tile of the dQ kernel are
-// read both as 16-byte rows (MFMA A operands) and with ds_read_b64_tr_b16
-// (transposed B / A operands). A row pad of 48 bytes keeps the row reads of 16
-// consecutive rows conflict free and limits the transposed reads of 4
-// consecutive rows to a partial 2-way conflict; tiles only read by rows use a
-// 16-byte pad.
+// Operand shapes shared by the two kernels.
 template <int HD>
 struct BwdTiles {
   static constexpr int CH = HD / 8;
-  static constexpr int RS_RT = HD * 2 + 48;  // rows + transposed reads
-  static constexpr int RS_R = HD * 2 + 16;   // rows only
   static constexpr int NKB = HD / 16;
   static constexpr int NDB = HD / 32;
 };
-
-// LDS byte offset, relative to a tile with row stride RS, of this lane's
-// transposed 4x16 read that yields element (row 16*kb2 + 8*hl + 4*t + i,
-// column 32*db + l32), i = 0..3; add (16*kb2 + 4*t)*RS + 64*db.
-template <int RS>
-__device__ __forceinline__ int tr_lane_off(int lane) {
-  const int hl = lane >> 5, m = lane & 15, x = (lane >> 4) & 1;
-  return (8 * hl + (m >> 2)) * RS + 2 * (16 * x + 4 * (m & 3));
-}
-
-// bf16x8 operand (k = 8*hl .. 8*hl+7 <-> tile rows 16*kb2 + 8*hl + 0..7, column
-// 32*db + l32) from two transposed reads.
-template <int RS>
-__device__ __forceinline__ bf16x8 tr_operand(const uint8_t* tile, int lane_off, int kb2, int db) {
-  const uint16_t* p = reinterpret_cast<const uint16_t*>(tile + lane_off + 16 * kb2 * RS + 64 * db);
-  return join_bf16x8(lds_read_tr(p), lds_read_tr(p + 2 * RS));
-}
 
 // ---------------------------------------------------------------- dQ (Q-major)
 // One workgroup = 8 waves x 32 queries of one (problem, batch, head). Per key
@@ -166,19 +148,32 @@ __device__ __forceinline__ bf16x8 tr_operand(const uint8_t* tile, int lane_off, 
 //   P = exp2(S c - lse2), dS = P (dP - delta)  (lane = query: lse/delta per lane)
 //   dQ^T += K^T dS^T  A = K^T by transposed reads of the K tile, B = dS^T
 //                                                            16 MFMAs
+// K/V tiles (and the key documents) arrive by LDS DMA into NB buffers, tile
+// t + NB - 1 issued while tile t is computed, one barrier per tile. Rows are
+// unpadded with their 16-byte chunks XOR-swizzled by swz_both, so the K row reads,
+// the K transposed reads and the V row reads are all bank-conflict free. The tile
+// loop is unrolled over the buffers: every operand read is then a per-lane VGPR
+// (swizzle folded in) plus a compile-time offset below 64 KiB, with no address
+// arithmetic in the loop. Tiles past the end are issued as zero-length loads,
+// which keeps every wait count static.
 template <int HD, int MASK>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm) {
   using T = BwdTiles<HD>;
   constexpr int NW = 8, NT = NW * 64, BQ = 32 * NW, BK = 64;
   constexpr int CH = T::CH, NKB = T::NKB, NDB = T::NDB;
-  constexpr int RSK = T::RS_RT, RSV = T::RS_R;
-  constexpr int KT = BK * RSK, VT = BK * RSV;
-  constexpr int LPT = BK * CH / NT;
-  static_assert(LPT >= 1 && BK * CH % NT == 0, "tile split");
+  constexpr int RB = HD * 2;              // LDS row bytes (unpadded, swizzled)
+  constexpr int KT = BK * RB;             // bytes of one K (or V) tile
+  constexpr int RPK = 1024 / RB;          // rows per 1 KiB DMA instruction
+  constexpr int NDMA = KT / 1024 / NW;    // DMA instructions per wave, tile and operand
+  constexpr int NB = RMX_DQ_NB;           // tile buffers
+  // K tiles at [0, NB KT), V tiles after them; V rows get their own base register when
+  // the last V tile would sit past the 16-bit LDS instruction offset
+  constexpr bool VBASE = 2 * NB * KT - KT / 2 > 65535;
+  static_assert(NDMA >= 1 && KT % (1024 * NW) == 0, "tile split");
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * (KT + VT)];
-  __shared__ int sKg[2][BK];
-  __shared__ int sKd[2][BK];
+  __shared__ __attribute__((aligned(1024))) uint8_t sT[2 * NB][KT];  // K tiles, then V tiles
+  __shared__ __attribute__((aligned(256))) int sKg[NB][BK];
+  __shared__ __attribute__((aligned(256))) int sKd[NB][BK];
   __shared__ int sRange[2];
 
   const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
@@ -264,71 +259,114 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   const int wave_qlast = (qw0 + 31 < sq ? qw0 + 31 : sq - 1);
   const int wave_kmax = mask == RMX_MASK_CAUSAL ? wave_qlast + off : 2147483647;
 
+  // ---- tile loads: wave w fills 1 KiB pieces w*NDMA .. of the K and V tiles (lane L:
+  // row n*RPK + L/CH, swizzled chunk L%CH); wave 0 also the tile's key documents
+  const int ntile = kt_end - kt_begin;
   const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
-  const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, HD * 2));
-  const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, HD * 2));
-  u32x4 kst[LPT], vst[LPT];
-  auto stage_load = [&](int k0) {
+  const uint8_t* const kb0 = reinterpret_cast<const uint8_t*>(P.k + bb * L.k_sb + kvh * L.k_sh);
+  const uint8_t* const vb0 = reinterpret_cast<const uint8_t*>(P.v + bb * L.v_sb + kvh * L.v_sh);
+  const uint32_t kspan = span_bytes(sk, kss, HD * 2), vspan = span_bytes(sk, vss, HD * 2);
+  int vk[NDMA], vv[NDMA];
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int cid = tid + i * NT, row = cid / CH, c = cid % CH;
-      kst[i] = buf_load16(krs, (k0 + row) * kss + 16 * c);
-      vst[i] = buf_load16(vrs, (k0 + row) * vss + 16 * c);
+  for (int i = 0; i < NDMA; ++i) {
+    const int n = wave * NDMA + i;
+    const int r = n * RPK + lane / CH, ch = 16 * ((lane % CH) ^ swz_both<HD>(r));
+    vk[i] = r * kss + ch;
+    vv[i] = r * vss + ch;
+  }
+  constexpr bool DOCDMA = mask == RMX_MASK_DOC;
+  // loads per tile and wave: what the end-of-tile wait leaves in flight
+  auto dma_tile = [&](int t) __attribute__((always_inline)) {
+    const bool live = t < ntile;
+    const int b = t % NB;
+    const int ka = (kt_begin + (live ? t : 0)) * BK;
+    if (DOCDMA && wave == 0) {
+      const uint32_t n = live ? 4u * (uint32_t)(sk - ka) : 0u;
+      dma4_async(make_rsrc(P.k_gidx + ka, n), lds_addr(&sKg[b][0]), 4 * lane);
+      dma4_async(make_rsrc(P.k_doc + ka, n), lds_addr(&sKd[b][0]), 4 * lane);
     }
-  };
-  auto stage_store = [&](int buf) {
-    uint8_t* kt = smem + buf * (KT + VT);
-    uint8_t* vt = kt + KT;
+    const i32x4 krs = make_rsrc(kb0 + (int64_t)ka * kss, live ? kspan - (uint32_t)(ka * kss) : 0u);
+    const i32x4 vrs = make_rsrc(vb0 + (int64_t)ka * vss, live ? vspan - (uint32_t)(ka * vss) : 0u);
+    const uint32_t kd = lds_addr(&sT[b][0]), vd = lds_addr(&sT[NB + b][0]);
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int cid = tid + i * NT, row = cid / CH, c = cid % CH;
-      *reinterpret_cast<u32x4*>(kt + row * RSK + 16 * c) = kst[i];
-      *reinterpret_cast<u32x4*>(vt + row * RSV + 16 * c) = vst[i];
+    for (int i = 0; i < NDMA; ++i) {
+      const int n = wave * NDMA + i;
+      dma16_async(krs, kd + 1024 * n, vk[i]);
+      dma16_async(vrs, vd + 1024 * n, vv[i]);
     }
   };
-  int nkg = 0, nkd = 0;
-  auto doc_load = [&](int k0) {
-    if (mask == RMX_MASK_DOC && tid < BK) {
-      const int kk = k0 + tid < sk ? k0 + tid : sk - 1;
-      nkg = P.k_gidx[kk];
-      nkd = P.k_doc[kk];
-    }
-  };
-  auto doc_store = [&](int buf) {
-    if (mask == RMX_MASK_DOC && tid < BK) {
-      sKg[buf][tid] = nkg;
-      sKd[buf][tid] = nkd;
-    }
+  // end of tile t: tile t + 1 has landed in every wave, tiles t + 2 .. t + NB - 1 stay
+  // in flight
+  auto tile_barrier = [&]() __attribute__((always_inline)) {
+    if (DOCDMA && wave == 0)
+      wait_vm_barrier<(NB - 2) * (2 * NDMA + 2)>();
+    else
+      wait_vm_barrier<(NB - 2) * 2 * NDMA>();
   };
 
-  const int k_lane = sigma(l32) * RSK + 16 * hl;  // K rows (A of S^T)
-  const int v_lane = sigma(l32) * RSV + 16 * hl;  // V rows (A of dP^T)
-  const int t_lane = tr_lane_off<RSK>(lane);      // K^T (A of dQ^T)
+  // per-lane LDS byte offsets (swizzle folded in): rows (A of S^T, dP^T): key row
+  // 32 mb + sigma(l32), chunk 2 kb + hl
+  int raddr[NKB], vaddr[VBASE ? NKB : 1];
+  {
+    const int sr = sigma(l32);
+    const int base = sr * RB + 16 * (hl ^ swz_both<HD>(sr));
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) raddr[kb] = base ^ (32 * kb);
+    if constexpr (VBASE) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) vaddr[kb] = raddr[kb] + (int)lds_addr(&sT[NB][0]);
+    }
+  }
+  // transposed reads (A of dQ^T = K^T): key rows 16 kb2 + 8 hl + 4 t + (m >> 2),
+  // columns 32 db + 16 x + 4 (m & 3) .. + 3, m = lane & 15, x = (lane >> 4) & 1
+  int taddr[2][NDB];
+  {
+    const int m16 = lane & 15, x16 = (lane >> 4) & 1;
+    const int cc = 2 * x16 + ((m16 & 3) >> 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = 8 * hl + 4 * t + (m16 >> 2);
+      const int base = r * RB + 16 * (cc ^ swz_both<HD>(r)) + 8 * (m16 & 1);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) taddr[t][db] = base ^ (64 * db);
+    }
+  }
+  auto tr_op = [&](const uint8_t* tile, int kb2, int db) -> bf16x8 {
+    const uint8_t* p = tile + 16 * kb2 * RB;
+    return join_bf16x8(lds_read_tr(reinterpret_cast<const uint16_t*>(p + taddr[0][db])),
+                       lds_read_tr(reinterpret_cast<const uint16_t*>(p + taddr[1][db])));
+  };
+  auto row_op = [&](const uint8_t* tile, int kb, int mb) -> bf16x8 {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(tile + raddr[kb] + mb * 32 * RB));
+  };
+  // V rows of buffer b (compile-time): through the V base register when there is one
+  auto vrow_op = [&](int b, int kb, int mb) -> bf16x8 {
+    if constexpr (VBASE) {
+      const auto* base = reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(
+          (uintptr_t)(uint32_t)vaddr[kb]);
+      return __builtin_bit_cast(
+          bf16x8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+                      base + b * KT + mb * 32 * RB));
+    } else {
+      return row_op(&sT[NB + b][0], kb, mb);
+    }
+  };
 
   f32x16 acc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) acc[db] = zero16();
 
-  if (kt_begin < kt_end) {
-    stage_load(kt_begin * BK);
-    doc_load(kt_begin * BK);
-    stage_store(0);
-    doc_store(0);
-  }
-  __syncthreads();
-  wait_all_loads();
+#pragma unroll
+  for (int t = 0; t < NB - 1; ++t) dma_tile(t);
+  tile_barrier();
 
   const float c = prm.scale_log2;
-  for (int kt = kt_begin; kt < kt_end; ++kt) {
-    const int buf = (kt - kt_begin) & 1;
-    const int k0 = kt * BK;
-    const bool has_next = kt + 1 < kt_end;
-    if (has_next) {
-      stage_load(k0 + BK);
-      doc_load(k0 + BK);
-    }
-    const uint8_t* kt_lds = smem + buf * (KT + VT);
-    const uint8_t* vt_lds = kt_lds + KT;
+  // tile t in buffer BUF = t % NB (a compile-time constant in each unrolled copy)
+  auto tile_step = [&](int t, auto bufc) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
+    const int k0 = (kt_begin + t) * BK;
+    dma_tile(t + NB - 1);  // into the buffer tile t - 1 used: every wave is past it
+    const uint8_t* kt_lds = &sT[buf][0];
 
     if (k0 <= wave_kmax) {
       bool need_mask = (k0 + BK > sk);
@@ -349,12 +387,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
-          const bf16x8 a = __builtin_bit_cast(
-              bf16x8, *reinterpret_cast<const u32x4*>(kt_lds + k_lane + mb * 32 * RSK + 32 * kb));
-          s[mb] = mfma32(a, qreg[kb], s[mb]);
-          const bf16x8 b = __builtin_bit_cast(
-              bf16x8, *reinterpret_cast<const u32x4*>(vt_lds + v_lane + mb * 32 * RSV + 32 * kb));
-          dp[mb] = mfma32(b, doreg[kb], dp[mb]);
+          s[mb] = mfma32(row_op(kt_lds, kb, mb), qreg[kb], s[mb]);
+          dp[mb] = mfma32(vrow_op(buf, kb, mb), doreg[kb], dp[mb]);
         }
       }
 
@@ -390,15 +424,16 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
       for (int kb2 = 0; kb2 < 4; ++kb2)
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-          acc[db] = mfma32(tr_operand<RSK>(kt_lds, t_lane, kb2, db), dsb[kb2], acc[db]);
+          acc[db] = mfma32(tr_op(kt_lds, kb2, db), dsb[kb2], acc[db]);
     }
-
-    if (has_next) {
-      stage_store(buf ^ 1);
-      doc_store(buf ^ 1);
-    }
-    __syncthreads();
+    tile_barrier();
+  };
+  for (int t = 0; t < ntile; t += NB) {
+    [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
+      ((t + B < ntile ? tile_step(t + B, std::integral_constant<int, B>{}) : void()), ...);
+    }(std::make_integer_sequence<int, NB>{});
   }
+  wait_all_loads();  // the zero-length loads past the end
 
   if (!qvalid) return;
   const float scale = L.scale;
