@@ -26,6 +26,10 @@
 //   sum_{t<T-1} g_w w, the dependence of every weight on cum_A_{T-1})
 //   g_B += G_h^T (w x)       (MFMA M = state, N = tokens, K = head dim), summed
 //   over the group's heads in registers and written once.
+// Each wave stages its 32 tokens' g_x rows of a head in LDS and writes them as
+// whole rows (a store of 8-byte pieces of 32 rows 8 KiB apart was the kernel's
+// main cost), and reads e / cum_A 32 bytes (8 heads) per token at a time into an
+// LDS table (4-byte reads per head fetched each 128-byte line again and again).
 #include "rmx_kernels.h"
 
 namespace rmx {
@@ -219,6 +223,16 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
   // g_e (lane half 0) and g_cum_A (half 1) of 8 consecutive heads per token, so
   // that each token's row of those [rows, T, H] arrays is written 32 bytes at a time
   __shared__ __attribute__((aligned(16))) float sE[2][BT][8];
+  // each wave's g_x rows of one head (32 tokens x D bf16), staged so that they leave as
+  // whole rows: rows of 2D + 8 bytes keep the 8-byte writes of 32 rows on distinct banks
+  constexpr int XS = 2 * D + 8;
+  __shared__ __attribute__((aligned(16))) uint8_t sX[NW][32 * XS];
+  // e (columns 0..7) and cum_A (8..15) of 8 consecutive heads per token, loaded 32 bytes
+  // per token row instead of 4 bytes per head (a 17-float row keeps 32 tokens' reads of
+  // one column on distinct banks); each wave reads only its own tokens' rows. Shapes whose
+  // tiles leave no room for the table load 4 bytes per head.
+  constexpr bool kEC = 2 * D * GS + 2 * BT * 8 * 4 + NW * 32 * XS + BT * 17 * 4 <= 163840;
+  __shared__ float sEC[kEC ? BT : 1][17];
 
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -277,27 +291,54 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
     float e, c, cl;
   };
   HeadRegs hr[2];
+  // e / cum_A by 8-head groups when the group's heads are 8-aligned rows of 32 bytes
+  const bool ec8 = kEC && ((H | hpg | g * hpg) & 7) == 0;
+  // a group's values (e for lane half 0, cum_A for half 1: 32 bytes of this lane's token
+  // row) go straight to the wave's table, so no registers stay live across heads
+  float* ecrow = sEC[kEC ? 32 * wave + l32 : 0];
+  auto load_ec = [&](int h0) __attribute__((always_inline)) {
+    const float* src = (hl ? a.cum_A : a.e) + ((int64_t)row * T + (tv ? t : 0)) * H + h0;
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
+    const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ecrow[8 * hl + i] = v0[i];
+      ecrow[8 * hl + 4 + i] = v1[i];
+    }
+  };
   auto load_h = [&](int h, HeadRegs& r) __attribute__((always_inline)) {
     const int xo = (t * H + h) * D;
 #pragma unroll
     for (int kb = 0; kb < NKD; ++kb) r.x[kb] = buf_load16(xrs, (xo + 16 * kb + 8 * hl) * 2);
     const int64_t th = (int64_t)row * T * H + h;
-    r.e = a.e[th + (int64_t)(tv ? t : 0) * H];
-    r.c = a.cum_A[th + (int64_t)(tv ? t : 0) * H];
+    if (!ec8) {
+      r.e = a.e[th + (int64_t)(tv ? t : 0) * H];
+      r.c = a.cum_A[th + (int64_t)(tv ? t : 0) * H];
+    }
     r.cl = a.cum_A[th + (int64_t)(T - 1) * H];
   };
 
   auto head = [&](int hi, const HeadRegs& cur, HeadRegs& nxt) __attribute__((always_inline)) {
     const int h = g * hpg + hi, buf = hi & 1;
     store_g(buf);
-    __syncthreads();  // G_h visible; the reads of buffer buf from two heads ago are done
+    // G_h visible, and every wave's LDS reads of buffer buf from two heads ago are done.
+    // Only LDS is waited for: the g_x / g_e stores of earlier heads stay in flight
+    // (__syncthreads would wait for them, one store latency per head).
+    lds_barrier();
     if (hi + 1 < hpg) {
       load_g(h + 1);
       load_h(h + 1, nxt);
     }
     const uint8_t* sg = sG[buf];
-    const float dec = live ? expf(cur.cl - cur.c) : 0.f;
-    const float w = live ? dec * cur.e : 0.f;
+    float ce = cur.e, cc = cur.c;
+    if (ec8) {
+      if ((hi & 7) == 0) load_ec(h);  // a new group: its values to the wave's table
+      asm volatile("" ::: "memory");  // the table rows are this wave's own: LDS order suffices
+      ce = ecrow[hi & 7];
+      cc = ecrow[8 + (hi & 7)];
+    }
+    const float dec = live ? expf(cur.cl - cc) : 0.f;
+    const float w = live ? dec * ce : 0.f;
 
     // U^T (d x tokens) = G_h B^T: A = G rows (LDS), B = this lane's B row
     f32x16 u[NMD];
@@ -327,9 +368,10 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
       xc[2 * kb + 1][0] = hl ? own[2] : r0;
       xc[2 * kb + 1][1] = hl ? own[3] : r1;
     }
-    // lane (hl, l32) holds U[token t][d = 32 m + c_row(hl, r)]: g_x, g_w
+    // lane (hl, l32) holds U[token t][d = 32 m + c_row(hl, r)]: g_x, g_w. The wave's
+    // g_x rows go to its LDS strip first (8 bytes per lane and piece) ...
     float gw = 0.f;
-    uint16_t* gxp = a.g_x + (int64_t)row * T * H * D + (int64_t)(t * H + h) * D;
+    uint8_t* xs = sX[wave];
 #pragma unroll
     for (int m = 0; m < NMD; ++m)
 #pragma unroll
@@ -338,13 +380,35 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
         const float x0 = __uint_as_float(xv[0] << 16), x1 = __uint_as_float(xv[0] & 0xffff0000u);
         const float x2 = __uint_as_float(xv[1] << 16), x3 = __uint_as_float(xv[1] & 0xffff0000u);
         gw += x0 * u[m][4 * q] + x1 * u[m][4 * q + 1] + x2 * u[m][4 * q + 2] + x3 * u[m][4 * q + 3];
-        if (tv) {
-          u32x2 sv;
-          sv[0] = cvt_pk_bf16(w * u[m][4 * q], w * u[m][4 * q + 1]);
-          sv[1] = cvt_pk_bf16(w * u[m][4 * q + 2], w * u[m][4 * q + 3]);
-          *reinterpret_cast<u32x2*>(gxp + 32 * m + 8 * q + 4 * hl) = sv;
-        }
+        u32x2 sv;
+        sv[0] = cvt_pk_bf16(w * u[m][4 * q], w * u[m][4 * q + 1]);
+        sv[1] = cvt_pk_bf16(w * u[m][4 * q + 2], w * u[m][4 * q + 3]);
+        *reinterpret_cast<u32x2*>(xs + l32 * XS + 2 * (32 * m + 8 * q + 4 * hl)) = sv;
       }
+    // ... and leave it as whole rows: LPR lanes per token row, 16 bytes each (the strip
+    // is this wave's own, and a wave's LDS operations complete in order)
+    {
+      constexpr int LPR = 2 * D / 16, RPI = 64 / LPR;
+      asm volatile("" ::: "memory");
+      // the wave's rows of head h: tokens past T fall outside num_records and are dropped
+      const int tw = bt * BT + 32 * wave;
+      const int nrows = T - tw < 32 ? T - tw : 32;
+      const i32x4 grs = make_rsrc(a.g_x + ((int64_t)row * T + tw) * H * D + (int64_t)h * D,
+                                  nrows > 0 ? (uint32_t)((nrows - 1) * H * D + D) * 2u : 0u);
+#pragma unroll
+      for (int i = 0; i < 32 / RPI; ++i) {
+        const int rr = RPI * i + lane / LPR;
+        const uint8_t* src = xs + rr * XS + 16 * (lane % LPR);
+        u32x4 v;
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8);
+        v[0] = lo[0];
+        v[1] = lo[1];
+        v[2] = hi[0];
+        v[3] = hi[1];
+        buf_store16(grs, (rr * H * D + 8 * (lane % LPR)) * 2, v);
+      }
+    }
     gw += xhalf(gw);
     // each wave stages only its own tokens' strip: no barrier, LDS order suffices
     float* strip = &sE[hl][32 * wave + l32][0];
