@@ -367,7 +367,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     u32x4 pw[2 * MB];   // P_j packed to bf16, one u32x4 per 16-key block
     float rsp[2 * MB];  // partial row sums per 16-key block
 #pragma unroll
-    for (int i = 0; i < 2 * MB; ++i) rsp[i] = 0.f;
+    for (int i = 0; i < 2 * MB; ++i) rsp[i] = -0.f;  // -0 + x == x: the first sums fold away
     auto pair = [&](auto pp) __attribute__((always_inline)) {
       constexpr int pi = decltype(pp)::value;  // pair index: elements 2 pi, 2 pi + 1
       constexpr int kb2 = pi / 4, w = pi % 4;
