@@ -6,7 +6,7 @@ earlier ranks' chunk states) and that state's contribution to the shard's
 outputs and final state. With the P ranks emulated on one GPU the rank axis is
 a leading tensor axis:
 
-* :func:`cp_state_prefix` — ``H_in_r = sum_{j<r} (prod_{j<k<r} A_k) B_j`` for all
+* :func:`cp_state_prefix_all` — ``H_in_r = sum_{j<r} (prod_{j<k<r} A_k) B_j`` for all
   ranks at once, computed by the fp32 linear-scan kernel over the rank axis
   (the all-gather + local loop of ``cp_state_prefix``, strategies/mamba.py:68-98);
 * :func:`mamba2_cp_correction` — ``y += C . (e^{cumA} H_in)`` and
@@ -19,7 +19,8 @@ from __future__ import annotations
 import torch
 
 from ringmaster_amd import abi
-from ringmaster_amd.strategies.state_passing import linear_scan_backward, linear_scan_forward
+from ringmaster_amd.strategies.state_passing import (_group_size, linear_scan_backward,
+                                                     linear_scan_forward)
 
 
 def _prefix_forward(ssm_states, chunk_decays, single_hop):
@@ -67,9 +68,9 @@ class _StatePrefix(torch.autograd.Function):
         return g_states, g_decays, None
 
 
-def cp_state_prefix(ssm_states: torch.Tensor, chunk_decays: torch.Tensor, *,
-                    single_hop: bool = False) -> torch.Tensor:
-    """State entering every rank's shard.
+def cp_state_prefix_all(ssm_states: torch.Tensor, chunk_decays: torch.Tensor, *,
+                        single_hop: bool = False) -> torch.Tensor:
+    """State entering every rank's shard, all ranks at once (the P ranks emulated on one GPU).
 
     ``ssm_states``: fp32 ``[world, b, nheads, head_dim, d_state]``, each rank's local
     final state (computed from h0 = 0); ``chunk_decays``: fp32 ``[world, b, nheads]``,
@@ -83,6 +84,49 @@ def cp_state_prefix(ssm_states: torch.Tensor, chunk_decays: torch.Tensor, *,
     if ssm_states.dtype != torch.float32 or chunk_decays.dtype != torch.float32:
         raise NotImplementedError("the MI355X state passing carries fp32 states")
     return _StatePrefix.apply(ssm_states, chunk_decays, bool(single_hop))
+
+
+def _zero_keep(*tensors):
+    """0 * the sum of the gathered values: the reference's rank 0 adds it to its output so
+    that the all-gather stays in its graph and the gather's backward fires on every rank
+    (strategies/mamba.py:85-86)."""
+    return 0.0 * sum(t.float().sum() for t in tensors)
+
+
+def cp_state_prefix_gathered(gathered_states: torch.Tensor, gathered_decays: torch.Tensor,
+                             rank: int, *, single_hop: bool = False):
+    """One rank's ``(h_prev, zero_keep)`` from the all-gathered pairs, what the reference
+    computes after its all-gather (strategies/mamba.py:82-98): ``gathered_states``
+    ``[world, b, nheads, head_dim, d_state]`` and ``gathered_decays`` ``[world, b,
+    nheads]`` fp32, rank order. ``zero_keep`` is a zero-valued scalar on rank 0 and None
+    elsewhere. A multi-process caller all-gathers (chunk decay, final state) itself and
+    calls this with its rank."""
+    world = gathered_states.shape[0] if gathered_states.dim() == 5 else 0
+    if not 0 <= rank < max(world, 1):
+        raise ValueError(f"rank {rank} outside the {world} gathered ranks")
+    h_prev = cp_state_prefix_all(gathered_states, gathered_decays, single_hop=single_hop)[rank]
+    return h_prev, (_zero_keep(gathered_states, gathered_decays) if rank == 0 else None)
+
+
+def cp_state_prefix(ssm_state: torch.Tensor, chunk_decay: torch.Tensor, group=None, *,
+                    single_hop: bool = False):
+    """Drop-in for the reference's per-rank ``cp_state_prefix(ssm_state, chunk_decay,
+    group, *, single_hop)`` (strategies/mamba.py:68-98): this rank's ``(h_prev,
+    zero_keep)`` for its local final state ``ssm_state`` fp32 ``[b, nheads, head_dim,
+    d_state]`` and chunk decay ``[b, nheads]``. A group of one rank (or None) is the
+    reference's single-rank case: ``h_prev`` is zeros and ``zero_keep`` the zero scalar of
+    rank 0. This one-GPU build runs no collectives, so a group of several ranks raises
+    ``NotImplementedError``: gather the pairs and call :func:`cp_state_prefix_gathered`, or
+    emulate every rank with :func:`cp_state_prefix_all`."""
+    if _group_size(group, "cp_state_prefix(ssm_state, chunk_decay, group)",
+                   "strategies/mamba.py:68", "cp_state_prefix_all") != 1:
+        raise NotImplementedError(
+            "the MI355X build runs no collectives: all-gather (chunk decay, state) and call "
+            "cp_state_prefix_gathered, or emulate the ranks with cp_state_prefix_all")
+    abi.require_device(ssm_state, chunk_decay)
+    if ssm_state.dim() != 4 or chunk_decay.shape != ssm_state.shape[:2]:
+        raise ValueError("ssm_state must be [b, H, d, n] and chunk_decay [b, H]")
+    return cp_state_prefix_gathered(ssm_state[None], chunk_decay[None], 0, single_hop=single_hop)
 
 
 class _DtCumsum(torch.autograd.Function):
@@ -254,7 +298,7 @@ def mamba2_cp_apply(scan_output: torch.Tensor, ssm_state: torch.Tensor, dt: torc
     H, d, n = ssm_state.shape[2:]
     T = dt.shape[2]
     cum_A, decay = mamba2_chunk_decay(dt, A, dt_bias, dt_softplus)          # [P,B,T,H], [P,B,H]
-    h_prev = cp_state_prefix(ssm_state, decay, single_hop=seq_idx is not None)
+    h_prev = cp_state_prefix_all(ssm_state, decay, single_hop=seq_idx is not None)
     if seq_idx is None:
         # every rank's rows in one launch, stacked on the batch axis
         y, h_final = mamba2_cp_correction(

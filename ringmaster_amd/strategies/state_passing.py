@@ -136,12 +136,13 @@ def local_linear_scan(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return _CPLinearScan.apply(a, b, 1, None)
 
 
-def _group_size(group) -> int:
+def _group_size(group, call="cp_linear_scan(a, b, group)",
+                where="strategies/state_passing.py:29", emulate="world=P") -> int:
     if group is None:
         return 1
     if isinstance(group, int):
-        raise TypeError("cp_linear_scan(a, b, group): the third argument is the process group "
-                        "(strategies/state_passing.py:29); emulate P ranks with world=P")
+        raise TypeError(f"{call}: the third argument is the process group ({where}); "
+                        f"emulate P ranks with {emulate}")
     import torch.distributed as dist
 
     return dist.get_world_size(group)

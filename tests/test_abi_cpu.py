@@ -246,6 +246,23 @@ def test_cp_linear_scan_group_argument():
         cp_linear_scan(a, a, world=2, h_in=torch.zeros(1, 2))
 
 
+def test_cp_state_prefix_arguments():
+    """cp_state_prefix(ssm_state, chunk_decay, group, *, single_hop) as in the reference
+    (strategies/mamba.py:68): an integer group is refused, the tensors must live on the
+    GPU, and the gathered form checks the rank against the gathered ranks."""
+    import torch
+
+    from ringmaster_amd.strategies.mamba import cp_state_prefix, cp_state_prefix_gathered
+
+    st, dc = torch.zeros(1, 2, 4, 8), torch.ones(1, 2)
+    with pytest.raises(TypeError, match="cp_state_prefix_all"):
+        cp_state_prefix(st, dc, 2)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        cp_state_prefix(st, dc, None, single_hop=True)
+    with pytest.raises(ValueError, match="rank"):
+        cp_state_prefix_gathered(st[None].expand(3, -1, -1, -1, -1), dc[None].expand(3, -1, -1), 3)
+
+
 def test_zigzag_ring_attention_group_keyword():
     """zigzag_ring_attention accepts the reference's ``group`` keyword (ring/zigzag.py:257);
     the emulated ring takes its ranks on the leading axis, so only None is valid."""

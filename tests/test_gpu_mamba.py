@@ -112,19 +112,52 @@ def test_correction_configs4_full_size():
 
 @pytest.mark.parametrize("world", [1, 2, 5, 8])
 def test_state_prefix_matches_oracle(world):
-    from ringmaster_amd.strategies.mamba import cp_state_prefix
+    from ringmaster_amd.strategies.mamba import cp_state_prefix_all
 
     b, H, d, n = 2, 4, 8, 16
     finals = seeded((world, b, H, d, n), 50)
     decays = torch.rand(world, b, H, generator=torch.Generator().manual_seed(51))
     ref = sp.cp_state_prefix_emulated(list(finals.double()), list(decays.double()))
-    got = cp_state_prefix(finals.cuda(), decays.cuda()).cpu()
+    got = cp_state_prefix_all(finals.cuda(), decays.cuda()).cpu()
     for r in range(world):
         assert_f32_rel(got[r], ref[r], f"h_prev rank {r}")
-    hop = cp_state_prefix(finals.cuda(), decays.cuda(), single_hop=True).cpu()
+    hop = cp_state_prefix_all(finals.cuda(), decays.cuda(), single_hop=True).cpu()
     assert torch.equal(hop[0], torch.zeros_like(hop[0]))
     for r in range(1, world):
         assert torch.equal(hop[r], finals[r - 1])
+
+
+@pytest.mark.parametrize("single_hop", [False, True])
+def test_state_prefix_per_rank_interface(single_hop):
+    """The reference's per-rank return (strategies/mamba.py:68-98): every rank's
+    ``(h_prev, zero_keep)`` from the gathered pairs; zero_keep a zero scalar on rank 0
+    only, whose gradient reaches every gathered entry (as zeros); the single-rank call
+    returns zeros."""
+    from ringmaster_amd.strategies.mamba import cp_state_prefix, cp_state_prefix_gathered
+
+    world, b, H, d, n = 5, 2, 3, 8, 16
+    finals = seeded((world, b, H, d, n), 52).cuda()
+    decays = torch.rand(world, b, H, generator=torch.Generator().manual_seed(53)).cuda()
+    ref = sp.cp_state_prefix_emulated(list(finals.double().cpu()), list(decays.double().cpu()))
+    for r in range(world):
+        h_prev, keep = cp_state_prefix_gathered(finals, decays, r, single_hop=single_hop)
+        want = (finals[r - 1].cpu() if r else torch.zeros_like(finals[0].cpu())) if single_hop \
+            else ref[r]
+        assert_f32_rel(h_prev.cpu(), want, f"h_prev rank {r}")
+        if r == 0:
+            assert keep.dim() == 0 and keep.item() == 0.0
+        else:
+            assert keep is None
+    fs = finals.clone().requires_grad_(True)
+    ds = decays.clone().requires_grad_(True)
+    h_prev, keep = cp_state_prefix_gathered(fs, ds, 0, single_hop=single_hop)
+    (h_prev.sum() + keep).backward()
+    torch.cuda.synchronize()
+    assert fs.grad is not None and not fs.grad.any() and ds.grad is not None
+    h1, k1 = cp_state_prefix(finals[2], decays[2], single_hop=single_hop)
+    assert torch.equal(h1, torch.zeros_like(h1)) and k1.item() == 0.0
+    with pytest.raises(ValueError, match="rank"):
+        cp_state_prefix_gathered(finals, decays, world)
 
 
 # ---- backward: gradients of C, cum_A and h_prev against autograd through the oracle

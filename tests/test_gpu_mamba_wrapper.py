@@ -47,7 +47,7 @@ def test_chunk_decay_values_and_grads(softplus, dt_f32, H):
 
 @pytest.mark.parametrize("single_hop", [False, True])
 def test_state_prefix_grads(single_hop):
-    from ringmaster_amd.strategies.mamba import cp_state_prefix
+    from ringmaster_amd.strategies.mamba import cp_state_prefix_all
 
     P, b, H, d, n = 4, 2, 3, 8, 16
     states = seeded((P, b, H, d, n), 7)
@@ -60,7 +60,7 @@ def test_state_prefix_grads(single_hop):
         ref = torch.stack(sp.cp_state_prefix_emulated(list(sr.unbind(0)), list(dr.unbind(0))))
     (ref * gout.double()).sum().backward()
     sd, dd = states.cuda().requires_grad_(True), decays.cuda().requires_grad_(True)
-    got = cp_state_prefix(sd, dd, single_hop=single_hop)
+    got = cp_state_prefix_all(sd, dd, single_hop=single_hop)
     got.backward(gout.cuda())
     torch.cuda.synchronize()
     assert_f32_rel(got, ref, "h_prev")
