@@ -28,11 +28,13 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 10 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 11 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
                               8: allocation-free Mamba2 correction bwd;
                               9: carried-in state h_in / dh_in of the linear scan;
-                              10: L-parallel linear scan (workspace argument) */
+                              10: L-parallel linear scan (workspace argument);
+                              11: sliding windows, attention head_dim any multiple of 8
+                                  up to 128 */
 
 /* error codes */
 #define RMX_OK 0
@@ -44,6 +46,13 @@ extern "C" {
 #define RMX_MASK_FULL 0   /* every (q, k) pair attends */
 #define RMX_MASK_CAUSAL 1 /* bottom-right aligned causal: k <= q + (sk - sq) */
 #define RMX_MASK_DOC 2    /* q_doc[q] == k_doc[k] && k_gidx[k] <= q_gidx[q] */
+/* A problem's sliding window (has_window = 1) masks every pair further apart than
+ * window_left: pos_q - pos_k > window_left, with the bottom-right aligned positions
+ * pos_q = q + (sk - sq), pos_k = k (ring/kernels.py:68-72), or the global indices
+ * q_gidx / k_gidx under RMX_MASK_DOC (ring/loop.py:185-186). It applies on top of the
+ * mask kind; window_left may be any int32 (a negative bound also masks the diagonal,
+ * which is how one block of a windowed ring sees the window of the global sequence).
+ * Rows left with no key get lse = -inf and out = 0, as with document masks. */
 
 /* forward epilogue modes (online-softmax merge, ring/merge.py:20-31) */
 #define RMX_FWD_WRITE 0       /* out/lse := this block's (out, lse); acc_out (nullable)
@@ -65,7 +74,9 @@ extern "C" {
 
 /* Layout shared by every problem of one batched attention call. */
 typedef struct rmx_attn_layout {
-  int32_t batch, hq, hkv, head_dim; /* hq % hkv == 0 (GQA: kv_head = q_head / (hq/hkv)) */
+  int32_t batch, hq, hkv;           /* hq % hkv == 0 (GQA: kv_head = q_head / (hq/hkv)) */
+  int32_t head_dim;                 /* a multiple of 8, at most 128: the kernels compute at 64
+                                       or 128 and read the columns past head_dim as zeros */
   float scale;                      /* softmax scale (1/sqrt(head_dim) by default) */
   int32_t mask;                     /* RMX_MASK_* */
   /* element strides (batch, seq, head) */
@@ -95,6 +106,8 @@ typedef struct rmx_fwd_problem {
   const int32_t* k_doc;  /* RMX_MASK_DOC: document id of each k row (non-decreasing) */
   int32_t sq, sk;
   int32_t mode;          /* RMX_FWD_* */
+  int32_t has_window;    /* 0: no window; 1: window_left bounds pos_q - pos_k (see above) */
+  int32_t window_left;
 } rmx_fwd_problem;
 
 /* One block-attention backward problem, using the GLOBAL (merged) out/lse. */
@@ -120,6 +133,8 @@ typedef struct rmx_bwd_problem {
   int32_t sq, sk;
   int32_t dq_mode;       /* RMX_GRAD_* */
   int32_t dkv_mode;      /* RMX_GRAD_* */
+  int32_t has_window;    /* as in rmx_fwd_problem: the forward's window of the same block */
+  int32_t window_left;
 } rmx_bwd_problem;
 
 int32_t rmx_abi_version(void);

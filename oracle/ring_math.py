@@ -1,6 +1,7 @@
 """CPU restatement of the reference ring-attention math (test infrastructure only).
 
-Follows ring/kernels.py:52-78 (math_block), ring/merge.py:13-31 (merge),
+Follows ring/kernels.py:52-78 (math_block, with its sliding window), ring/loop.py:175-228
+(the gather ring and the packed gather ring), ring/merge.py:13-31 (merge),
 ring/zigzag.py:40-67,86-120,151-254 (zigzag schedule, forward and reverse-ring
 backward), ring/p2p_attn.py:243-281 (explicit global-lse block backward) and
 ring/varlen_blocks.py:45-80,176-200 (document masks). The P ranks of the ring are
@@ -402,6 +403,51 @@ def distflash_backward(d_outs, qs, ks, vs, outs, lses, *, scaling=None, cu_seqle
             dq[h + d] += a
     return ([t.transpose(1, 2) for t in dq], [t.transpose(1, 2) for t in dk],
             [t.transpose(1, 2) for t in dv])
+
+
+def allgather_ring_forward(qs, ks, vs, *, causal=True, scaling=None, window=None):
+    """The gather ring (ring/loop.py:201-228): rank r attends the gathered K/V of ranks
+    0..r (causal) or of every rank with ONE math_block call, whose bottom-right
+    alignment places rank r's query i at position ``(end - 1) L + i`` against the
+    gathered keys (``end`` = r + 1 causal, P otherwise); a window bounds that position
+    minus the key's global index. qs/ks/vs per-rank [b, H, L, d] -> per-rank out
+    [b, L, H, d] and lse [b, H, L]. Differentiable (torch autograd)."""
+    world = len(qs)
+    outs, lses = [], []
+    for r in range(world):
+        end = r + 1 if causal else world
+        q = qs[r].transpose(1, 2)
+        k = torch.cat([t.transpose(1, 2) for t in ks[:end]], dim=1)
+        v = torch.cat([t.transpose(1, 2) for t in vs[:end]], dim=1)
+        o, lse = math_block(q, k, v, causal=causal, scaling=scaling, window=window)
+        outs.append(o)
+        lses.append(lse)
+    return outs, lses
+
+
+def varlen_ring_forward(qs, ks, vs, cu_seqlens, *, scaling=None, window=None):
+    """The packed gather ring's explicit path (ring/loop.py:175-198), causal: rank r's
+    query at global index ``r L + i`` attends gathered key j when both lie in one
+    document, ``j <= r L + i`` and (window) ``r L + i - j <= window[0]``. Per-rank
+    [b, H, L, d] -> per-rank out [b, L, H, d] and lse [b, H, L]. Differentiable."""
+    world, L = len(qs), qs[0].shape[2]
+    S = world * L
+    doc = doc_ids_from_cu(cu_seqlens)
+    k = torch.cat([t.transpose(1, 2) for t in ks], dim=1)
+    v = torch.cat([t.transpose(1, 2) for t in vs], dim=1)
+    kidx = torch.arange(S)
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(qs[0].shape[-1])
+    outs, lses = [], []
+    for r in range(world):
+        qidx = torch.arange(r * L, r * L + L)
+        allow = (doc[qidx][:, None] == doc[None, :]) & (kidx[None, :] <= qidx[:, None])
+        if window is not None:
+            allow &= qidx[:, None] - kidx[None, :] <= window[0]
+        m = torch.where(allow, torch.zeros(()), torch.full((), NEG_INF))
+        o, lse = masked_block_fwd(qs[r].transpose(1, 2), k, v, m, scale)
+        outs.append(o)
+        lses.append(lse)
+    return outs, lses
 
 
 def full_attention(q, k, v, *, causal=True, scaling=None, cu_seqlens=None):

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
-ABI_VERSION = 10  # RMX_ABI_VERSION of include/ringmaster_amd.h
+ABI_VERSION = 11  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
@@ -66,7 +66,7 @@ class FwdProblem(ctypes.Structure):
         ("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp), ("lse", _vp),
         ("acc_out", _vp), ("acc_lse", _vp),
         ("q_gidx", _vp), ("k_gidx", _vp), ("q_doc", _vp), ("k_doc", _vp),
-        ("sq", _i32), ("sk", _i32), ("mode", _i32),
+        ("sq", _i32), ("sk", _i32), ("mode", _i32), ("has_window", _i32), ("window_left", _i32),
     ]
 
 
@@ -76,6 +76,7 @@ class BwdProblem(ctypes.Structure):
         ("nlse", _vp), ("dq_acc", _vp), ("dq", _vp), ("dk_acc", _vp), ("dv_acc", _vp), ("dk", _vp), ("dv", _vp),
         ("q_gidx", _vp), ("k_gidx", _vp), ("q_doc", _vp), ("k_doc", _vp),
         ("sq", _i32), ("sk", _i32), ("dq_mode", _i32), ("dkv_mode", _i32),
+        ("has_window", _i32), ("window_left", _i32),
     ]
 
 

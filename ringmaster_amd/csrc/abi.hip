@@ -39,8 +39,9 @@ int check_layout(const rmx_attn_layout* L) {
   if (L->hq % L->hkv)
     return fail(RMX_EINVAL, "Query heads must be divisible by KV heads (hq=%d hkv=%d)", L->hq,
                 L->hkv);
-  if (L->head_dim != 64 && L->head_dim != 128)
-    return fail(RMX_EUNSUPPORTED, "head_dim %d is not supported (64 or 128)", L->head_dim);
+  if (L->head_dim <= 0 || L->head_dim > 128 || L->head_dim % 8)
+    return fail(RMX_EUNSUPPORTED, "head_dim %d is not supported (a multiple of 8, at most 128)",
+                L->head_dim);
   if (!(L->scale > 0.f) || !std::isfinite(L->scale))
     return fail(RMX_EINVAL, "softmax scale must be finite and positive (got %g)", (double)L->scale);
   if (L->mask < RMX_MASK_FULL || L->mask > RMX_MASK_DOC)
@@ -77,6 +78,12 @@ int check_span(int64_t rows, int64_t stride_elems, const char* name) {
   return RMX_OK;
 }
 
+int check_window(int has_window, int i) {
+  if (has_window != 0 && has_window != 1)
+    return fail(RMX_EINVAL, "problem %d: has_window must be 0 or 1 (got %d)", i, has_window);
+  return RMX_OK;
+}
+
 int check_doc(const rmx_attn_layout* L, const int32_t* qg, const int32_t* kg, const int32_t* qd,
               const int32_t* kd) {
   if (L->mask != RMX_MASK_DOC) return RMX_OK;
@@ -104,6 +111,7 @@ int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* probl
   for (int i = 0; i < nproblems; ++i) {
     const rmx_fwd_problem& p = problems[i];
     if (p.sq < 0 || p.sk < 0) return fail(RMX_EINVAL, "problem %d: negative length", i);
+    if ((rc = check_window(p.has_window, i))) return rc;
     if (p.sq == 0) continue;
     if ((rc = check_bf16(p.q, "q"))) return rc;
     if ((rc = check_span(p.sq, layout->q_ss, "q"))) return rc;
@@ -166,6 +174,7 @@ int32_t rmx_attn_bwd(const rmx_attn_layout* layout, const rmx_bwd_problem* probl
   for (int i = 0; i < nproblems; ++i) {
     const rmx_bwd_problem& p = problems[i];
     if (p.sq < 0 || p.sk < 0) return fail(RMX_EINVAL, "problem %d: negative length", i);
+    if ((rc = check_window(p.has_window, i))) return rc;
     if (p.sq == 0 || p.sk == 0) continue;
     if ((rc = check_bf16(p.q, "q"))) return rc;
     if ((rc = check_bf16(p.k, "k"))) return rc;

@@ -49,7 +49,11 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layo
   const int part = threadIdx.x % TPR;
   float acc = 0.f;
   int bb = 0, q = 0, h = 0;
-  if (row < rows) {
+  if (row < rows && 8 * part >= L.head_dim) {  // columns past the head dim: nothing to add
+    h = row % L.hq;
+    q = (row / L.hq) % sq;
+    bb = row / (L.hq * sq);
+  } else if (row < rows) {
     h = row % L.hq;
     q = (row / L.hq) % sq;
     bb = row / (L.hq * sq);
@@ -108,7 +112,7 @@ hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int 
                                  int sq, hipStream_t stream) {
   const int64_t rows = (int64_t)L.batch * sq * L.hq;
   if (rows == 0) return hipSuccess;
-  if (L.head_dim == 128)
+  if (L.head_dim > 64)
     launch_delta_t<128>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
   else
     launch_delta_t<64>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
@@ -201,16 +205,26 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
     qg = P.q_gidx[q];
     qd = P.q_doc[q];
   }
-
+  const int D = L.head_dim;        // columns past D (up to HD) load as zeros
+  const int wl = window_bound(P);  // pos_q - pos_k <= wl
   const int off = sk - sq;
+  // this lane's lowest key: key >= q + off - wl (document masks: global index >= qlo)
+  const int qlo = mask == RMX_MASK_DOC ? (qvalid ? clamp_i32((int64_t)qg - wl) : 2147483647)
+                                       : q + off - wl;
+
   const int qlast = (q0 + BQ < sq ? q0 + BQ : sq) - 1;
   const int nkt = (sk + BK - 1) / BK;
   int kt_begin = 0, kt_end = nkt;
   int qg_first = 0, qg_last = 0, qd_first = 0, qd_last = 0;
-  if (mask == RMX_MASK_CAUSAL) {
-    const int kmax = qlast + off;
-    kt_end = kmax < 0 ? 0 : (kmax / BK + 1 < nkt ? kmax / BK + 1 : nkt);
-  } else if (mask == RMX_MASK_DOC) {
+  if (mask != RMX_MASK_DOC) {
+    if (mask == RMX_MASK_CAUSAL) {
+      const int kmax = qlast + off;
+      kt_end = kmax < 0 ? 0 : (kmax / BK + 1 < nkt ? kmax / BK + 1 : nkt);
+    }
+    const int kmin = q0 + off - wl;  // the first query's lowest key
+    kt_begin = kmin <= 0 ? 0 : (kmin / BK < nkt ? kmin / BK : nkt);
+    if (kt_end < kt_begin) kt_end = kt_begin;
+  } else {
     qg_first = P.q_gidx[q0];
     qg_last = P.q_gidx[qlast];
     qd_first = P.q_doc[q0];
@@ -225,7 +239,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
       const int ka = t * BK, kz = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
       const int kga = P.k_gidx[ka], kgz = P.k_gidx[kz];
       const int kda = P.k_doc[ka], kdz = P.k_doc[kz];
-      if (kga <= qg_last && kdz >= qd_first && kda <= qd_last) {
+      if (kga <= qg_last && kdz >= qd_first && kda <= qd_last && (int64_t)kgz >= (int64_t)qg_first - wl) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
       }
@@ -242,14 +256,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   bf16x8 qreg[NKB], doreg[NKB];
   {
     const i32x4 qrs = make_rsrc(P.q + bb * L.q_sb + head * L.q_sh,
-                                span_bytes(sq, 2 * L.q_ss, HD * 2));
+                                span_bytes(sq, 2 * L.q_ss, D * 2));
     const i32x4 ors = make_rsrc(P.dout + bb * L.o_sb + head * L.o_sh,
-                                span_bytes(sq, 2 * L.o_ss, HD * 2));
+                                span_bytes(sq, 2 * L.o_ss, D * 2));
     const int qo = q * (int)(2 * L.q_ss) + 16 * hl, oo = q * (int)(2 * L.o_ss) + 16 * hl;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      qreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(qrs, qo + 32 * kb));
-      doreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(ors, oo + 32 * kb));
+      const int col = 16 * kb + 8 * hl;
+      qreg[kb] = __builtin_bit_cast(bf16x8, cols_below(buf_load16(qrs, qo + 32 * kb), col, D));
+      doreg[kb] = __builtin_bit_cast(bf16x8, cols_below(buf_load16(ors, oo + 32 * kb), col, D));
     }
   }
   const int64_t lrow = bb * L.l_sb + head * L.l_sh + (qvalid ? q : 0);
@@ -258,6 +273,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   const float dlt = qvalid ? P.delta[lrow] : 0.f;
   const int wave_qlast = (qw0 + 31 < sq ? qw0 + 31 : sq - 1);
   const int wave_kmax = mask == RMX_MASK_CAUSAL ? wave_qlast + off : 2147483647;
+  // keys below the window of every query of the wave (the first query's lowest key)
+  const int wave_kmin = mask == RMX_MASK_DOC ? -2147483647 : qw0 + off - wl;
 
   // ---- tile loads: wave w fills 1 KiB pieces w*NDMA .. of the K and V tiles (lane L:
   // row n*RPK + L/CH, swizzled chunk L%CH); wave 0 also the tile's key documents
@@ -265,14 +282,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
   const uint8_t* const kb0 = reinterpret_cast<const uint8_t*>(P.k + bb * L.k_sb + kvh * L.k_sh);
   const uint8_t* const vb0 = reinterpret_cast<const uint8_t*>(P.v + bb * L.v_sb + kvh * L.v_sh);
-  const uint32_t kspan = span_bytes(sk, kss, HD * 2), vspan = span_bytes(sk, vss, HD * 2);
+  const uint32_t kspan = span_bytes(sk, kss, D * 2), vspan = span_bytes(sk, vss, D * 2);
   int vk[NDMA], vv[NDMA];
 #pragma unroll
   for (int i = 0; i < NDMA; ++i) {
     const int n = wave * NDMA + i;
-    const int r = n * RPK + lane / CH, ch = 16 * ((lane % CH) ^ swz_both<HD>(r));
-    vk[i] = r * kss + ch;
-    vv[i] = r * vss + ch;
+    const int r = n * RPK + lane / CH, ch = (lane % CH) ^ swz_both<HD>(r);
+    // chunks of columns past D load from kOutOfRange (zeros)
+    vk[i] = 8 * ch < D ? r * kss + 16 * ch : kOutOfRange;
+    vv[i] = 8 * ch < D ? r * vss + 16 * ch : kOutOfRange;
   }
   constexpr bool DOCDMA = mask == RMX_MASK_DOC;
   // loads per tile and wave: what the end-of-tile wait leaves in flight
@@ -368,13 +386,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
     dma_tile(t + NB - 1);  // into the buffer tile t - 1 used: every wave is past it
     const uint8_t* kt_lds = &sT[buf][0];
 
-    if (k0 <= wave_kmax) {
+    if (k0 <= wave_kmax && k0 + BK > wave_kmin) {
       bool need_mask = (k0 + BK > sk);
       if (mask == RMX_MASK_CAUSAL) need_mask |= (k0 + BK - 1 > qw0 + off);
+      if (mask != RMX_MASK_DOC) need_mask |= (k0 < qw0 + 31 + off - wl);
       if (mask == RMX_MASK_DOC) {
-        const int kgz = sKg[buf][BK - 1];
+        const int kga = sKg[buf][0], kgz = sKg[buf][BK - 1];
         const int kda = sKd[buf][0], kdz = sKd[buf][BK - 1];
-        need_mask |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first);
+        need_mask |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first &&
+                       (int64_t)kga >= (int64_t)qg_last - wl);
       }
 
       f32x16 s[2], dp[2];
@@ -407,9 +427,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
             const int key = k0 + kl;
             bool ok = key < sk;
             if (mask == RMX_MASK_CAUSAL) ok &= key <= q + off;
+            if (mask != RMX_MASK_DOC) ok &= key >= qlo;
             if (mask == RMX_MASK_DOC) {
               const int kd = sKd[buf][kl], kg = sKg[buf][kl];
-              ok &= (kd == qd) & (kg <= qg);
+              ok &= (kd == qd) & (kg <= qg) & (kg >= qlo);
             }
             v[i] = ok ? v[i] : 0.f;
           }
@@ -444,6 +465,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d0 = 32 * db + 8 * j + 4 * hl;
+      if (d0 >= D) continue;  // columns past the head dim are not stored
       f32x4 v;
       v[0] = acc[db][4 * j + 0] * scale;
       v[1] = acc[db][4 * j + 1] * scale;
@@ -536,16 +558,23 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   const bool kvalid = key < sk;
 
   // ---- query-tile range of the workgroup
+  const int D = L.head_dim;        // columns past D (up to HD) load as zeros
+  const int wl = window_bound(P);  // pos_q - pos_k <= wl
   const int off = sk - sq;
   const int klast = (k0 + C::BKV < sk ? k0 + C::BKV : sk) - 1;
   const int nqt = (sq + BQ - 1) / BQ;
   int qt_begin = 0, qt_end = nqt;
   int kg_first = 0, kg_last = 0, kd_first = 0, kd_last = 0;
-  if (mask == RMX_MASK_CAUSAL) {
-    const int qmin = k0 - off;  // first query that sees key k0
-    qt_begin = qmin <= 0 ? 0 : qmin / BQ;
-    if (qt_begin > nqt) qt_begin = nqt;
-  } else if (mask == RMX_MASK_DOC) {
+  if (mask != RMX_MASK_DOC) {
+    if (mask == RMX_MASK_CAUSAL) {
+      const int qmin = k0 - off;  // first query that sees key k0
+      qt_begin = qmin <= 0 ? 0 : qmin / BQ;
+      if (qt_begin > nqt) qt_begin = nqt;
+    }
+    const int qmax = klast + wl - off;  // last query whose window reaches key klast
+    qt_end = qmax < 0 ? 0 : (qmax / BQ + 1 < nqt ? qmax / BQ + 1 : nqt);
+    if (qt_end < qt_begin) qt_end = qt_begin;
+  } else {
     kg_first = P.k_gidx[k0];
     kg_last = P.k_gidx[klast];
     kd_first = P.k_doc[k0];
@@ -558,9 +587,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     int lo = nqt, hi = -1;
     for (int t = tid; t < nqt; t += C::NT) {
       const int qa = t * BQ, qz = (t * BQ + BQ < sq ? t * BQ + BQ : sq) - 1;
-      const int qgz = P.q_gidx[qz];
+      const int qga = P.q_gidx[qa], qgz = P.q_gidx[qz];
       const int qda = P.q_doc[qa], qdz = P.q_doc[qz];
-      if (qgz >= kg_first && qdz >= kd_first && qda <= kd_last) {
+      if (qgz >= kg_first && qdz >= kd_first && qda <= kd_last && (int64_t)qga <= (int64_t)kg_last + wl) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
       }
@@ -603,15 +632,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   const uint8_t* const nb0 = reinterpret_cast<const uint8_t*>(P.nlse + bb * L.l_sb + (int64_t)kvh * G * L.l_sh);
   const uint8_t* const db0 = reinterpret_cast<const uint8_t*>(P.delta + bb * L.l_sb + (int64_t)kvh * G * L.l_sh);
   const int qhs = (int)(2 * L.q_sh), ohs = (int)(2 * L.o_sh), lhs = (int)(4 * L.l_sh);
-  const uint32_t qspan = span_bytes(sq, qss, HD * 2), ospan = span_bytes(sq, oss, HD * 2);
+  const uint32_t qspan = span_bytes(sq, qss, D * 2), ospan = span_bytes(sq, oss, D * 2);
   int vq[C::NDMA], vo[C::NDMA];
 #pragma unroll
   for (int i = 0; i < C::NDMA; ++i) {
     const int n = wave * C::NDMA + i;
-    const int r = n * C::RPK + lane / CH, p = lane % CH;
-    const int ch = 16 * (p ^ swz_both<HD>(r));
-    vq[i] = r * qss + ch;
-    vo[i] = r * oss + ch;
+    const int r = n * C::RPK + lane / CH, ch = (lane % CH) ^ swz_both<HD>(r);
+    // chunks of columns past D load from kOutOfRange (zeros)
+    vq[i] = 8 * ch < D ? r * qss + 16 * ch : kOutOfRange;
+    vo[i] = 8 * ch < D ? r * oss + 16 * ch : kOutOfRange;
   }
   auto dma_tile = [&](int b, Cursor cu, bool live) {
     const int qa = cu.qt * BQ;
@@ -690,12 +719,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   bf16x8 kreg[NKB], vreg[NKB];
   {
     const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
-    const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, HD * 2));
-    const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, HD * 2));
+    const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, D * 2));
+    const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, D * 2));
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      kreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(krs, key * kss + 16 * hl + 32 * kb));
-      vreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(vrs, key * vss + 16 * hl + 32 * kb) ^ 0x80008000u);
+      const int col = 16 * kb + 8 * hl;
+      kreg[kb] = __builtin_bit_cast(bf16x8, cols_below(buf_load16(krs, key * kss + 16 * hl + 32 * kb), col, D));
+      vreg[kb] = __builtin_bit_cast(
+          bf16x8, cols_below(buf_load16(vrs, key * vss + 16 * hl + 32 * kb) ^ 0x80008000u, col, D));
     }
     // MFMA reads its A/B operands from AGPRs as well: K and -V live there, which
     // leaves the VGPRs to the fp32 tiles the VALU works on
@@ -707,6 +738,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     kg = P.k_gidx[key];
     kd = P.k_doc[key];
   }
+  // this lane's highest query: q + off <= key + wl (document masks: global index <= khi)
+  const int khi = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg + wl) : key + wl - off;
+  const int khi_first = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg_first + wl) : 0;
 
   // per-tile metadata in the accumulator / exponent layout: element r of half mb
   // belongs to query 32 mb + sig_row(hl, r), i.e. two runs of 8 queries
@@ -729,13 +763,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   // ---- masking (rare tiles: sequence end, causal diagonal, document boundaries)
   auto need_mask_of = [&](int qa, int slot) -> bool {
     bool m = (kw0 + 32 > sk);
+    const int qz = (qa + BQ < sq ? BQ : sq - qa) - 1;
     if (mask == RMX_MASK_CAUSAL) m |= (wave_klast > qa + off);
+    if (mask != RMX_MASK_DOC) m |= (qa + qz + off - kw0 > wl);
     if (mask == RMX_MASK_DOC) {
-      const int qga = sQg[slot][0];
+      const int qga = sQg[slot][0], qgz = sQg[slot][qz];
       const int qda = sQd[slot][0];
-      const int qz = (qa + BQ < sq ? BQ : sq - qa) - 1;
       const int qdz = sQd[slot][qz];
-      m |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga);
+      m |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga &&
+             qgz <= khi_first);
     }
     return m;
   };
@@ -749,7 +785,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
             const int ql = 32 * mb + sig_row(hl, r);
             bool ok = kvalid;
             if (mask == RMX_MASK_CAUSAL) ok &= key <= qa + ql + off;
-            if (mask == RMX_MASK_DOC) ok &= (sQd[slot][ql] == kd) & (kg <= sQg[slot][ql]);
+            if (mask != RMX_MASK_DOC) ok &= qa + ql <= khi;
+            if (mask == RMX_MASK_DOC)
+              ok &= (sQd[slot][ql] == kd) & (kg <= sQg[slot][ql]) & (sQg[slot][ql] <= khi);
             s[mb][r] = ok ? s[mb][r] : kNegInf;
             nl[mb][r] = fminf(nl[mb][r], 3.0e38f);
           }(),
@@ -967,6 +1005,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       const int d = 32 * db + l32;
+      if (d >= D) continue;  // columns past the head dim are not stored
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kk = kw0 + c_row(hl, r);
@@ -1053,7 +1092,7 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
 
 hipError_t launch_attn_bwd(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                            hipStream_t stream) {
-  if (L.head_dim == 128) return launch_bwd_t<128>(L, probs, n, stream);
+  if (L.head_dim > 64) return launch_bwd_t<128>(L, probs, n, stream);
   return launch_bwd_t<64>(L, probs, n, stream);
 }
 

@@ -103,17 +103,27 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     qg = P.q_gidx[q];
     qd = P.q_doc[q];
   }
+  const int D = L.head_dim;          // columns past D (up to HD) load as zeros
+  const int wl = window_bound(P);    // pos_q - pos_k <= wl
+  // this lane's lowest key: key >= q + off - wl (document masks: global index >= qlo)
+  const int off = sk - sq;
+  const int qlo = mask == RMX_MASK_DOC ? (q < sq ? clamp_i32((int64_t)qg - wl) : 2147483647)
+                                       : q + off - wl;
 
   // ---- key tile range of the workgroup
-  const int off = sk - sq;
   const int qlast = (q0 + C::BQ < sq ? q0 + C::BQ : sq) - 1;
   const int nkt = (sk + BK - 1) / BK;
   int kt_begin = 0, kt_end = nkt;
   int qg_first = 0, qg_last = 0, qd_first = 0, qd_last = 0;
-  if (mask == RMX_MASK_CAUSAL) {
-    const int kmax = qlast + off;
-    kt_end = kmax < 0 ? 0 : (kmax / BK + 1 < nkt ? kmax / BK + 1 : nkt);
-  } else if (mask == RMX_MASK_DOC) {
+  if (mask != RMX_MASK_DOC) {
+    if (mask == RMX_MASK_CAUSAL) {
+      const int kmax = qlast + off;
+      kt_end = kmax < 0 ? 0 : (kmax / BK + 1 < nkt ? kmax / BK + 1 : nkt);
+    }
+    const int kmin = q0 + off - wl;  // the first query's lowest key
+    kt_begin = kmin <= 0 ? 0 : (kmin / BK < nkt ? kmin / BK : nkt);
+    if (kt_end < kt_begin) kt_end = kt_begin;
+  } else {
     qg_first = P.q_gidx[q0];
     qg_last = P.q_gidx[qlast];
     qd_first = P.q_doc[q0];
@@ -126,9 +136,9 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     int lo = nkt, hi = -1;
     for (int t = tid; t < nkt; t += C::NT) {
       const int ka = t * BK, kz = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
-      const int kga = P.k_gidx[ka];
+      const int kga = P.k_gidx[ka], kgz = P.k_gidx[kz];
       const int kda = P.k_doc[ka], kdz = P.k_doc[kz];
-      if (kga <= qg_last && kdz >= qd_first && kda <= qd_last) {
+      if (kga <= qg_last && kdz >= qd_first && kda <= qd_last && (int64_t)kgz >= (int64_t)qg_first - wl) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
       }
@@ -148,25 +158,27 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   bf16x8 qreg[NKB];
   if (ntile > 0) {
     const uint16_t* qb = P.q + bb * L.q_sb + head * L.q_sh;
-    const i32x4 rs = make_rsrc(qb, span_bytes(sq, 2 * L.q_ss, HD * 2));
+    const i32x4 rs = make_rsrc(qb, span_bytes(sq, 2 * L.q_ss, D * 2));
     const int qo = q * (int)(2 * L.q_ss) + 16 * hl;
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) qreg[kb] = __builtin_bit_cast(bf16x8, buf_load16(rs, qo + 32 * kb));
+    for (int kb = 0; kb < NKB; ++kb)
+      qreg[kb] = __builtin_bit_cast(bf16x8, cols_below(buf_load16(rs, qo + 32 * kb), 16 * kb + 8 * hl, D));
   }
 
   // ---- K/V staging: buffer resources over this (batch, kv head)
   const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
-  const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, HD * 2));
-  const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, HD * 2));
+  const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, D * 2));
+  const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, D * 2));
   // DMA of a K (V) tile at key k0 into buffer b: instruction n of the tile fills
-  // LDS bytes [1024 n, 1024 n + 1024), lane L row n*RPK + L/CH, swizzled chunk L%CH
+  // LDS bytes [1024 n, 1024 n + 1024), lane L row n*RPK + L/CH, swizzled chunk L%CH;
+  // chunks of columns past D are loaded from kOutOfRange (zeros)
   auto dma_k = [&](int b, int k0) __attribute__((always_inline)) {
     const uint32_t d = lds_addr(&sK[b][0]);
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       const int n = wave * NDMA + i;
-      const int r = n * C::RPK + lane / CH, p = lane % CH;
-      dma16_async(krs, d + 1024 * n, (k0 + r) * kss + 16 * (p ^ swz_rows<HD>(r)));
+      const int r = n * C::RPK + lane / CH, ch = (lane % CH) ^ swz_rows<HD>(r);
+      dma16_async(krs, d + 1024 * n, 8 * ch < D ? (k0 + r) * kss + 16 * ch : kOutOfRange);
     }
   };
   auto dma_v = [&](int b, int k0) __attribute__((always_inline)) {
@@ -174,8 +186,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       const int n = wave * NDMA + i;
-      const int r = n * C::RPK + lane / CH, p = lane % CH;
-      dma16_async(vrs, d + 1024 * n, (k0 + r) * vss + 16 * (p ^ swz_tr<HD>(r)));
+      const int r = n * C::RPK + lane / CH, ch = (lane % CH) ^ swz_tr<HD>(r);
+      dma16_async(vrs, d + 1024 * n, 8 * ch < D ? (k0 + r) * vss + 16 * ch : kOutOfRange);
     }
   };
   // key metadata of tile t (RMX_MASK_DOC), one dword per lane, by wave 0
@@ -236,17 +248,19 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   };
 
   // ---- masking of a score tile (keys of tile t): out-of-range keys, the causal
-  // diagonal and document boundaries -> -inf. A causal tile past the wave's
-  // diagonal is masked whole and yields P = 0.
+  // diagonal, the window's lower edge and document boundaries -> -inf. A tile past
+  // the wave's diagonal (or below its window) is masked whole and yields P = 0.
   auto need_mask = [&](int t) __attribute__((always_inline)) -> bool {
     const int k0 = (kt_begin + t) * BK;
     bool nm = (k0 + BK > sk);
     if (mask == RMX_MASK_CAUSAL) nm |= (k0 + BK - 1 > qw0 + off);
+    if (mask != RMX_MASK_DOC) nm |= (k0 < qw0 + 31 + off - wl);
     if (mask == RMX_MASK_DOC) {
       const int ds = t & 3;
-      const int kgz = sKg[ds][BK - 1];
+      const int kga = sKg[ds][0], kgz = sKg[ds][BK - 1];
       const int kda = sKd[ds][0], kdz = sKd[ds][BK - 1];
-      nm |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first);
+      nm |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first &&
+              (int64_t)kga >= (int64_t)qg_last - wl);
     }
     return nm;
   };
@@ -258,6 +272,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     const int kbase = k0 + 8 * hl;
     const int lim_sk = sk - kbase;      // kc < lim_sk  <=>  key < sk
     const int lim_c = q + off - kbase;  // kc <= lim_c  <=>  key <= q + off
+    const int lim_w = qlo - kbase;      // kc >= lim_w  <=>  key >= q + off - wl
     const int* kgrow = &sKg[ds][8 * hl];
     const int* kdrow = &sKd[ds][8 * hl];
 #pragma unroll
@@ -267,7 +282,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
         const int kc = 32 * mb + 16 * (r >> 3) + (r & 7);
         bool ok = kc < lim_sk;
         if (mask == RMX_MASK_CAUSAL) ok &= kc <= lim_c;
-        if (mask == RMX_MASK_DOC) ok &= (kdrow[kc] == qd) & (kgrow[kc] <= qg);
+        if (mask != RMX_MASK_DOC) ok &= kc >= lim_w;
+        if (mask == RMX_MASK_DOC) ok &= (kdrow[kc] == qd) & (kgrow[kc] <= qg) & (kgrow[kc] >= qlo);
         sd[mb][r] = ok ? sd[mb][r] : kNegInf;
       }
   };
@@ -501,6 +517,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d0 = 32 * db + 8 * j + 4 * hl;
+      if (d0 >= D) continue;  // columns past the head dim are not stored
       f32x4 v;
       v[0] = o[db][4 * j + 0] * wb;
       v[1] = o[db][4 * j + 1] * wb;
@@ -562,7 +579,7 @@ static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* 
 
 hipError_t launch_attn_fwd(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                            hipStream_t stream) {
-  if (L.head_dim == 128) return launch_fwd_t<128>(L, probs, n, stream);
+  if (L.head_dim > 64) return launch_fwd_t<128>(L, probs, n, stream);
   return launch_fwd_t<64>(L, probs, n, stream);
 }
 

@@ -110,6 +110,31 @@ __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0)
 // Cross-half exchange: value held by lane l ^ 32.
 __device__ __forceinline__ float xhalf(float v) { return __shfl_xor(v, 32, 64); }
 
+// ---------------------------------------------------------------------------
+// Sliding windows and head dims below the kernel's.
+// A problem's window bounds pos_q - pos_k by window_bound(P). kWinMax stands for
+// "no window": the host keeps sq and sk below 2^27 (every (batch, head) slice
+// spans less than 2 GiB), so no pair is further apart than that and the bound
+// arithmetic (positions, offsets and bounds added) stays inside int32.
+constexpr int kWinMax = 1 << 29;
+template <class Prob>
+__device__ __forceinline__ int window_bound(const Prob& P) {
+  if (!P.has_window) return kWinMax;
+  const int w = P.window_left;
+  return w > kWinMax ? kWinMax : (w < -kWinMax ? -kWinMax : w);
+}
+__device__ __forceinline__ int clamp_i32(int64_t v) {
+  return v > 2147483647 ? 2147483647 : (v < -2147483647 ? -2147483647 : (int)v);
+}
+// A buffer offset past every num_records (the host keeps them below 2^31): loads
+// from it return zeros, LDS DMA from it writes zeros.
+constexpr int kOutOfRange = (int)0x80000000u;
+// A 16-byte chunk of 8 columns starting at col: kept when col < D, zeros otherwise.
+__device__ __forceinline__ u32x4 cols_below(u32x4 v, int col, int D) {
+  if (col >= D) v = u32x4{0u, 0u, 0u, 0u};
+  return v;
+}
+
 
 }  // namespace rmx
 

@@ -4,8 +4,11 @@
 (ring/kernels.py:28-85): ``fn(q, k, v, *, causal, scaling, dropout,
 attn_implementation, window) -> (out [b, sq, h, d] in q.dtype, lse [b, h, sq]
 fp32)``, q/k/v ``[b, s, h, d]``, GQA by ``kv_head = q_head // (hq/hkv)``, causal
-bottom-right aligned (ring/kernels.py:64-67). It is autograd-aware like
-``hf_kernels``/``math``; the lse output is not differentiable (as with flash).
+bottom-right aligned (ring/kernels.py:64-67), a sliding window ``(left, right)``
+masking ``pos_q - pos_k > left`` on the same bottom-right aligned positions
+(ring/kernels.py:68-72; ``right`` is not used, as there), head dims that are
+multiples of 8 up to 128. It is autograd-aware like ``hf_kernels``/``math``; the lse
+output is not differentiable (as with flash).
 
 ``flash_ops()`` returns ``(fwd, bwd)`` with the positional signatures of the Dao
 low-level ops that the ring schedules call (ring/p2p_attn.py:27-62,
@@ -24,6 +27,7 @@ from ringmaster_amd.ring import ops
 
 
 def _validate(q, k, v, dropout, window, softcap=0.0, alibi=None):
+    """Checks of the provider contract; returns the window's left bound (None: no window)."""
     abi.require_device(q, k, v)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q/k/v must be [batch, seq, heads, dim]")
@@ -31,16 +35,30 @@ def _validate(q, k, v, dropout, window, softcap=0.0, alibi=None):
         raise ValueError("Query heads must be divisible by KV heads")
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise NotImplementedError(f"mi355x_hip blocks compute in bf16 (got {q.dtype})")
-    if q.shape[-1] not in (64, 128):
-        raise NotImplementedError(f"head_dim {q.shape[-1]} is not supported (64 or 128)")
+    d = q.shape[-1]
+    if d % 8 or d > 128 or k.shape[-1] != d or v.shape[-1] != d:
+        raise NotImplementedError(f"head_dim {d} is not supported (a multiple of 8, at most 128)")
     if dropout:
         raise NotImplementedError("mi355x_hip blocks do not implement attention dropout")
-    if window is not None and tuple(window) not in ((-1, -1),):
-        raise NotImplementedError("mi355x_hip blocks do not implement sliding windows")
     if softcap:
         raise NotImplementedError("mi355x_hip blocks do not implement softcap")
     if alibi is not None:
         raise NotImplementedError("mi355x_hip blocks do not implement ALiBi")
+    return window_left(window)
+
+
+def window_left(window):
+    """The bound on ``pos_q - pos_k`` of a ``(left, right)`` window, or None. ``(-1, -1)``
+    (and None) is no window, as in the Dao ops; a negative ``left`` with a non-negative
+    ``right`` is refused (math_block would mask every key at or before the diagonal)."""
+    if window is None:
+        return None
+    left, right = (int(x) for x in window)
+    if left < 0:
+        if right >= 0:
+            raise NotImplementedError(f"window {tuple(window)}: only left windows are supported")
+        return None
+    return left
 
 
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
@@ -51,21 +69,22 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
-def block_forward(q, k, v, scale: float, causal: bool, keep_f32: bool = False):
+def block_forward(q, k, v, scale: float, causal: bool, keep_f32: bool = False, window=None):
     """(out bf16 [b, sq, hq, d], lse fp32 [b, hq, sq]) of one block; with ``keep_f32`` also
-    the fp32 out (what the backward's delta is computed from)."""
+    the fp32 out (what the backward's delta is computed from). ``window``: bound on
+    ``pos_q - pos_k`` (bottom-right aligned positions) or None."""
     b, sq, hq, d = q.shape
     out = torch.empty((b, sq, hq, d), dtype=torch.bfloat16, device=q.device)
     lse = torch.empty((b, hq, sq), dtype=torch.float32, device=q.device)
     out32 = torch.empty((b, sq, hq, d), dtype=torch.float32, device=q.device) if keep_f32 else None
     ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_WRITE, out=out, lse=lse,
-                             acc_out=out32)],
+                             acc_out=out32, window=window)],
                  scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL)
     return (out, lse, out32) if keep_f32 else (out, lse)
 
 
 def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None, dk=None, dv=None,
-                   out_f32=None):
+                   out_f32=None, window=None):
     """dq, dk, dv (bf16) of one block using the given (global) out/lse; returns delta too.
     ``out_f32`` (the forward's fp32 out), when given, is what delta = rowsum(dout * out) reads;
     otherwise the bf16 ``out`` is used, as a Dao-style backward does."""
@@ -85,7 +104,7 @@ def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None,
     dv_t = dv if (dv is not None and dv.stride() == dk_t.stride()) else torch.empty_like(dk_t)
     ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta, nlse=nlse,
                              dq_mode=abi.GRAD_WRITE_BF16, dkv_mode=abi.GRAD_WRITE_BF16,
-                             dq=dq_t, dk=dk_t, dv=dv_t)],
+                             dq=dq_t, dk=dk_t, dv=dv_t, window=window)],
                  scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL)
     for dst, src in ((dq, dq_t), (dk, dk_t), (dv, dv_t)):
         if dst is not None and dst is not src:
@@ -96,11 +115,11 @@ def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None,
 
 class _HipBlockAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, causal, scale):
+    def forward(ctx, q, k, v, causal, scale, window):
         q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-        out, lse, out32 = block_forward(q, k, v, scale, causal, keep_f32=True)
+        out, lse, out32 = block_forward(q, k, v, scale, causal, keep_f32=True, window=window)
         ctx.save_for_backward(q, k, v, out, lse, out32)
-        ctx.causal, ctx.scale = causal, scale
+        ctx.causal, ctx.scale, ctx.window = causal, scale, window
         ctx.mark_non_differentiable(lse)
         return out, lse
 
@@ -108,16 +127,16 @@ class _HipBlockAttention(torch.autograd.Function):
     def backward(ctx, dout, _dlse):
         q, k, v, out, lse, out32 = ctx.saved_tensors
         dq, dk, dv, _ = block_backward(_kernel_ready(dout), q, k, v, out, lse, ctx.scale,
-                                       ctx.causal, out_f32=out32)
-        return dq, dk, dv, None, None
+                                       ctx.causal, out_f32=out32, window=ctx.window)
+        return dq, dk, dv, None, None, None
 
 
 def mi355x_hip_block(q, k, v, *, causal, scaling, dropout=0.0, attn_implementation=None,
                      window=None):
     """q/k/v: [b, s, h, d] bf16 on the MI355X. Returns (out [b,s,h,d], lse [b,h,s])."""
-    _validate(q, k, v, dropout, window)
+    left = _validate(q, k, v, dropout, window)
     scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
-    return _HipBlockAttention.apply(q, k, v, bool(causal), float(scale))
+    return _HipBlockAttention.apply(q, k, v, bool(causal), float(scale), left)
 
 
 PROVIDERS = {
@@ -129,26 +148,33 @@ PROVIDERS = {
 def _flash_attn_forward(q, k, v, dropout_p, softmax_scale, causal, window_size_left=-1,
                         window_size_right=-1, softcap=0.0, alibi_slopes=None,
                         return_softmax=False):
-    _validate(q, k, v, dropout_p,
-              None if (window_size_left, window_size_right) == (-1, -1)
-              else (window_size_left, window_size_right), softcap, alibi_slopes)
+    _validate(q, k, v, dropout_p, None, softcap, alibi_slopes)
+    left = _dao_window(window_size_left, window_size_right, causal)
     if return_softmax:
         raise NotImplementedError("return_softmax is not supported")
     out, lse = block_forward(_kernel_ready(q), _kernel_ready(k), _kernel_ready(v),
-                             float(softmax_scale), bool(causal))
+                             float(softmax_scale), bool(causal), window=left)
     return out, lse, None, None
 
 
 def _flash_attn_backward(dout, q, k, v, out, lse, dq, dk, dv, dropout_p, softmax_scale, causal,
                          window_size_left=-1, window_size_right=-1, softcap=0.0,
                          alibi_slopes=None, deterministic=False, rng_state=None):
-    _validate(q, k, v, dropout_p,
-              None if (window_size_left, window_size_right) == (-1, -1)
-              else (window_size_left, window_size_right), softcap, alibi_slopes)
+    _validate(q, k, v, dropout_p, None, softcap, alibi_slopes)
+    left = _dao_window(window_size_left, window_size_right, causal)
     _, _, _, delta = block_backward(_kernel_ready(dout), _kernel_ready(q), _kernel_ready(k),
                                     _kernel_ready(v), _kernel_ready(out), lse,
-                                    float(softmax_scale), bool(causal), dq, dk, dv)
+                                    float(softmax_scale), bool(causal), dq, dk, dv, window=left)
     return dq, dk, dv, delta
+
+
+def _dao_window(left, right, causal):
+    """The Dao ops' ``window_size_left/right`` (-1 = unbounded; a causal call has no keys
+    right of the diagonal anyway) as the kernels' bound on ``pos_q - pos_k``."""
+    left, right = int(left), int(right)
+    if right >= 0 and not causal:
+        raise NotImplementedError("windows bounded on the right are not supported")
+    return left if left >= 0 else None
 
 
 def flash_ops():

@@ -12,13 +12,19 @@ Gathering K/V and attending once per rank computes the same blocks as the p2p ri
 (a bottom-right causal mask over ``K[0 : (r + 1) L]`` is the ring's diagonal-causal
 plus full earlier blocks), so both methods run the emulated contiguous ring: on one
 GPU every rank already reads every KV block in place from HBM.
+
+Sliding windows (the gather ring and the packed ring: ring/loop.py:185-186,201-228)
+keep the reference's positions: the gather ring's single block call aligns rank r's
+queries bottom-right against the gathered keys, which for a causal ring is the global
+position ``r L + i`` and for a non-causal ring (all P blocks gathered) ``(P - 1) L + i``;
+the packed ring compares global indices.
 """
 
 from __future__ import annotations
 
 import torch
 
-from ringmaster_amd.ring.kernels import PROVIDERS
+from ringmaster_amd.ring.kernels import PROVIDERS, window_left
 from ringmaster_amd.ring.p2p_attn import contiguous_ring
 from ringmaster_amd.ring.zigzag import doc_for
 
@@ -46,9 +52,15 @@ def ring_attention(q, k, v, *, group=None, causal: bool, scaling=None, dropout: 
                        attn_implementation=attn_implementation, window=window)
         return out.unsqueeze(0)
     if _method(rotate_method) == "allgather":
-        if dropout or window is not None:
-            raise NotImplementedError("dropout and sliding windows are not supported")
-        return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer)
+        if dropout:
+            raise NotImplementedError("dropout is not supported")
+        left = window_left(window)
+        P, L = q.shape[0], q.shape[3]
+        bounds = None
+        if left is not None:  # bottom-right aligned against the gathered keys
+            bounds = [left if causal else left - (P - 1 - r) * L for r in range(P)]
+        return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer,
+                               window=bounds)
     if dropout or window is not None or attn_implementation not in ("flash_attention_2", "math"):
         raise ValueError("P2P Ring requires FA2, zero dropout, and no sliding window")
     return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer)
@@ -61,11 +73,12 @@ def varlen_ring_attention(q, k, v, *, group=None, scaling, cu_seqlens, causal=Tr
     [P, b, L, H, d]."""
     if group is not None:
         raise ValueError("the emulated ring takes the ranks on the leading axis, not a group")
-    if dropout or window is not None:
-        raise NotImplementedError("dropout and sliding windows are not supported")
+    if dropout:
+        raise NotImplementedError("dropout is not supported")
     if not causal:
         raise NotImplementedError("packed (document-masked) blocks are causal in this build")
     if not isinstance(cu_seqlens, torch.Tensor):
         cu_seqlens = torch.as_tensor(cu_seqlens)
+    left = window_left(window)
     return contiguous_ring(q, k, v, causal=True, scaling=scaling, doc=doc_for(cu_seqlens, q),
-                           timer=timer)
+                           timer=timer, window=None if left is None else [left] * q.shape[0])

@@ -32,6 +32,7 @@ class FwdJob:
     k_gidx: torch.Tensor | None = None
     q_doc: torch.Tensor | None = None
     k_doc: torch.Tensor | None = None
+    window: int | None = None  # bound on pos_q - pos_k (global indices with document masks)
 
 
 @dataclasses.dataclass
@@ -55,6 +56,14 @@ class BwdJob:
     k_gidx: torch.Tensor | None = None
     q_doc: torch.Tensor | None = None
     k_doc: torch.Tensor | None = None
+    window: int | None = None
+
+
+def _set_window(p, window):
+    if window is not None:
+        if not -(1 << 31) <= int(window) < (1 << 31):
+            raise ValueError(f"window bound {window} outside int32")
+        p.has_window, p.window_left = 1, int(window)
 
 
 _ROLES = {
@@ -145,6 +154,7 @@ def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int) -> None:
         p.q_gidx, p.k_gidx = _int32(j.q_gidx), _int32(j.k_gidx)
         p.q_doc, p.k_doc = _int32(j.q_doc), _int32(j.k_doc)
         p.sq, p.sk, p.mode = j.q.shape[1], j.k.shape[1], j.mode
+        _set_window(p, j.window)
     abi.check(abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, len(jobs), abi.stream_of(q0)))
 
 
@@ -196,4 +206,5 @@ def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int) -> None:
         p.q_doc, p.k_doc = _int32(j.q_doc), _int32(j.k_doc)
         p.sq, p.sk = j.q.shape[1], j.k.shape[1]
         p.dq_mode, p.dkv_mode = j.dq_mode, j.dkv_mode
+        _set_window(p, j.window)
     abi.check(abi.lib().rmx_attn_bwd(ctypes.byref(lay), arr, len(jobs), abi.stream_of(q0)))

@@ -87,13 +87,19 @@ class _Ctx:
     or "distflash" (contiguous chunks, DistFlash's helper / owner work placement); the
     zigzag and DistFlash rings are causal only."""
 
-    def __init__(self, q, k, scale, doc, layout="zigzag", causal=True):
+    def __init__(self, q, k, scale, doc, layout="zigzag", causal=True, window=None):
         self.P, self.b, self.hq, self.L, self.d = q.shape
         self.hkv = k.shape[2]
         self.half = self.L // 2
         self.scale = scale
         self.doc = doc
         self.layout, self.causal = layout, causal
+        self.window = None if window is None else [int(w) for w in window]
+        if self.window is not None:
+            if len(self.window) != self.P:
+                raise ValueError("the window takes one bound per rank")
+            if layout == "zigzag" and doc is None:
+                raise NotImplementedError("sliding windows run on contiguous shards")
         self.gidx = self.rdoc = None
         if doc is not None:
             self.gidx = _global_rows(layout, self.P, self.L, q.device)
@@ -111,6 +117,21 @@ class _Ctx:
         if self.doc is not None:
             return abi.MASK_DOC
         return abi.MASK_CAUSAL if (self.causal and step == 0) else abi.MASK_FULL
+
+    def block_window(self, bl):
+        """The kernel's window bound for block ``bl`` (None: no window). ``window[r]``
+        bounds ``pos_q - pos_k`` of rank r's queries in global positions: under document
+        masks the kernel compares global indices directly; otherwise its positions are
+        the block's bottom-right aligned ones, which differ from the global difference
+        (contiguous chunks: rank r holds positions r L .. r L + L - 1) by a constant."""
+        if self.window is None:
+            return None
+        w = self.window[bl.rank]
+        if self.doc is not None:
+            return w
+        sq, sk = bl.q_hi - bl.q_lo, bl.k_hi - bl.k_lo
+        shift = (bl.rank * self.L + bl.q_lo) - (bl.kv_rank * self.L + bl.k_lo) - (sk - sq)
+        return w - shift
 
     def idx(self, rank, lo, hi):
         return None if self.gidx is None else self.gidx[rank, lo:hi]
@@ -176,7 +197,7 @@ def _only(blocks, only_ranks):
 
 
 def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=None,
-                 layout: str = "zigzag", causal: bool = True, only_ranks=None):
+                 layout: str = "zigzag", causal: bool = True, only_ranks=None, window=None):
     """Emulated ring forward (zigzag or contiguous layout). q/k/v: [P, b, H, L, d] bf16
     (interface layout per rank).
     Returns (out [P, b, L, H, d] bf16, lse [P, b, H, L] fp32, out32 [P, b, L, H, d] fp32):
@@ -185,9 +206,10 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
     ``only_ranks`` (a set of ranks) launches only the blocks those ranks compute (for
     DistFlash the helper computes blocks of other ranks' queries), each step at the grid
     one GPU of a real P-GPU ring runs; outputs of the blocks left out are then not
-    computed (per-rank timing)."""
+    computed (per-rank timing). ``window`` (contiguous layouts or document masks): one
+    bound per rank on the global ``pos_q - pos_k`` of its queries."""
     timer = timer or _NO_TIMER
-    c = _Ctx(q, k, scale, doc, layout, causal)
+    c = _Ctx(q, k, scale, doc, layout, causal, window)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)  # [P, b, L, H, d] views
     dev = q.device
     out = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.bfloat16, device=dev)
@@ -208,21 +230,23 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
                 acc_out=acc[r][:, qs],
                 acc_lse=None if acc_lse is None else acc_lse[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
-                q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi)))
+                q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi),
+                window=c.block_window(bl)))
         with timer("attn_fwd"):
             ops.attn_fwd(jobs, scale=scale, mask=c.mask(s))
     return out, lse, acc
 
 
 def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | None = None,
-                  timer=None, layout: str = "zigzag", causal: bool = True, only_ranks=None):
+                  timer=None, layout: str = "zigzag", causal: bool = True, only_ranks=None,
+                  window=None):
     """Reverse-ring backward with the global out/lse. dout: [P, b, L, H, d] bf16; out: the
     global out, fp32 (the forward's ``out32``) or bf16, [P, b, L, H, d].
     Returns fp32 (dq [P, b, L, Hq, d], dk, dv [P, b, L, Hkv, d]). Each step launches the
     KV-major dK/dV kernel and the Q-major dQ kernel over all ranks (``only_ranks``: over
     those ranks only, as in :func:`ring_forward`; the gradients are then partial)."""
     timer = timer or _NO_TIMER
-    c = _Ctx(q, k, scale, doc, layout, causal)
+    c = _Ctx(q, k, scale, doc, layout, causal, window)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)
     dev = q.device
     if not dout.is_contiguous():
@@ -251,7 +275,8 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
                 q=qd[r][:, qs], k=kd[kr][:, ks], v=vd[kr][:, ks], dout=dout[r][:, qs],
                 lse=lse[r][:, :, qs], delta=delta[r][:, :, qs], nlse=nlse[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
-                q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi))
+                q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi),
+                window=c.block_window(bl))
             kv_jobs.append(ops.BwdJob(dq_mode=abi.GRAD_NONE, dkv_mode=mode,
                                       dk_acc=dk[kr][:, ks], dv_acc=dv[kr][:, ks], **common))
             q_jobs.append(ops.BwdJob(dq_mode=mode, dkv_mode=abi.GRAD_NONE,
@@ -267,21 +292,21 @@ class EmulatedRing(torch.autograd.Function):
     """The emulated ring (zigzag or contiguous layout) with its reverse-ring backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, doc, timer, layout, causal):
-        out, lse, out32 = ring_forward(q, k, v, scale, doc, timer, layout, causal)
+    def forward(ctx, q, k, v, scale, doc, timer, layout, causal, window=None):
+        out, lse, out32 = ring_forward(q, k, v, scale, doc, timer, layout, causal, window=window)
         ctx.save_for_backward(q, k, v, out32, lse)
         ctx.scale, ctx.doc, ctx.timer = scale, doc, timer
-        ctx.layout, ctx.causal = layout, causal
+        ctx.layout, ctx.causal, ctx.window = layout, causal, window
         return out
 
     @staticmethod
     def backward(ctx, d_out):
         q, k, v, out32, lse = ctx.saved_tensors
         dq, dk, dv = ring_backward(d_out, q, k, v, out32, lse, ctx.scale, ctx.doc, ctx.timer,
-                                   ctx.layout, ctx.causal)
+                                   ctx.layout, ctx.causal, window=ctx.window)
         # fp32 accumulators -> q.dtype, returned in the interface layout [P, b, H, L, d]
         return (dq.to(q.dtype).transpose(2, 3), dk.to(k.dtype).transpose(2, 3),
-                dv.to(v.dtype).transpose(2, 3), None, None, None, None, None)
+                dv.to(v.dtype).transpose(2, 3), None, None, None, None, None, None)
 
 
 def check_ring_inputs(q, k, v):

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 10
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 11
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -55,7 +55,9 @@ def test_host_validation_gqa_divisibility():
 
 
 def test_host_validation_head_dim_and_mask():
-    assert _fwd(_layout(head_dim=96)) == abi.RMX_EUNSUPPORTED
+    assert _fwd(_layout(head_dim=136)) == abi.RMX_EUNSUPPORTED  # above 128
+    assert _fwd(_layout(head_dim=100)) == abi.RMX_EUNSUPPORTED  # not a multiple of 8
+    assert _fwd(_layout(head_dim=96)) == abi.RMX_OK             # zero problems: no launch
     with pytest.raises(NotImplementedError):
         abi.check(abi.RMX_EUNSUPPORTED)
     assert _fwd(_layout(mask=7)) == abi.RMX_EINVAL
@@ -73,6 +75,26 @@ def test_host_validation_problem_fields():
     arr[0].mode = 9
     assert abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, 1, None) == abi.RMX_EINVAL
     assert b"mode" in abi.lib().rmx_last_error()
+
+
+def test_host_validation_window_flag():
+    lay = _layout()
+    arr = (abi.FwdProblem * 1)()
+    arr[0].has_window, arr[0].window_left = 2, 10
+    assert abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, 1, None) == abi.RMX_EINVAL
+    assert b"has_window" in abi.lib().rmx_last_error()
+    barr = (abi.BwdProblem * 1)()
+    barr[0].has_window = -1
+    assert abi.lib().rmx_attn_bwd(ctypes.byref(lay), barr, 1, None) == abi.RMX_EINVAL
+
+
+def test_problem_structs_match_the_header():
+    """The ctypes mirrors have the C layout: the window fields sit at the end of each
+    problem struct (a zero-filled problem has no window)."""
+    assert ctypes.sizeof(abi.FwdProblem) == 11 * 8 + 5 * 4 + 4
+    assert ctypes.sizeof(abi.BwdProblem) == 17 * 8 + 6 * 4
+    assert abi.FwdProblem.has_window.offset == 11 * 8 + 3 * 4
+    assert abi.BwdProblem.has_window.offset == 17 * 8 + 4 * 4
 
 
 def test_host_validation_backward_nlse():

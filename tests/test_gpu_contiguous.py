@@ -103,5 +103,7 @@ def test_p2p_preconditions():
         ring_attention(q, q, q, causal=True, dropout=0.1)
     with pytest.raises(ValueError, match="P2P Ring requires"):
         ring_attention(q, q, q, causal=True, attn_implementation="sdpa")
+    with pytest.raises(ValueError, match="P2P Ring requires"):
+        ring_attention(q, q, q, causal=True, window=(4, 0))
     with pytest.raises(NotImplementedError):
-        ring_attention(q, q, q, causal=True, rotate_method="allgather", window=(4, 0))
+        ring_attention(q, q, q, causal=True, rotate_method="allgather", dropout=0.1)

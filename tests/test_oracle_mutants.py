@@ -45,6 +45,30 @@ def test_block_mutants_are_caught(mutation):
         pin.check_block(fn, True, 4, 2, 3, 7)
 
 
+def _window_block_variant(q, k, v, *, causal, scaling, window, inclusive=False,
+                          top_left=False):
+    qt, kt, vt = (t.transpose(1, 2).double() for t in (q, k, v))
+    rep = qt.shape[1] // kt.shape[1]
+    kt, vt = (t.repeat_interleave(rep, dim=1) for t in (kt, vt))
+    s = (qt @ kt.transpose(-1, -2)) * (scaling if scaling is not None else 1 / math.sqrt(8))
+    sq, sk = s.shape[-2:]
+    if causal:
+        s = s.masked_fill(~torch.ones(sq, sk, dtype=torch.bool).tril(sk - sq), float("-inf"))
+    iq = torch.arange(sq)[:, None] + (0 if top_left else sk - sq)
+    ik = torch.arange(sk)[None, :]
+    far = iq - ik >= window[0] if inclusive else iq - ik > window[0]
+    s = s.masked_fill(far, float("-inf"))
+    return (torch.softmax(s, -1) @ vt).transpose(1, 2), torch.logsumexp(s, -1)
+
+
+@pytest.mark.parametrize("mutation", ["inclusive_bound", "top_left_window"])
+def test_window_mutants_are_caught(mutation):
+    kw = {"inclusive_bound": dict(inclusive=True), "top_left_window": dict(top_left=True)}[mutation]
+    pin.check_window_block(_window_block_variant, True, 4, 9, 1)
+    with pytest.raises(AssertionError):
+        pin.check_window_block(lambda *a, **k: _window_block_variant(*a, **k, **kw), True, 4, 9, 1)
+
+
 def test_merge_mutants_are_caught():
     def flipped(out, lse, block_out, block_lse):  # exp(new - blk) instead of exp(blk - new)
         block_lse = rm.lse_to_bshd(block_lse, block_out)

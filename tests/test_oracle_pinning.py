@@ -21,8 +21,10 @@ def rnd(*shape, seed, dtype=torch.float64):
     return torch.randn(*shape, generator=g, dtype=dtype)
 
 
-def brute_block(q, k, v, causal, scale):
-    """Pure-Python loops over (b, h, i): softmax by its definition, fp64."""
+def brute_block(q, k, v, causal, scale, left=None):
+    """Pure-Python loops over (b, h, i): softmax by its definition, fp64, over the keys
+    j of row i that the causal rule (j <= i + sk - sq) and the window (i + sk - sq - j
+    <= left) leave."""
     b, sq, hq, d = q.shape
     sk, hkv = k.shape[1], k.shape[2]
     out = torch.zeros(b, sq, hq, d, dtype=torch.float64)
@@ -31,7 +33,9 @@ def brute_block(q, k, v, causal, scale):
         for h in range(hq):
             kh = h // (hq // hkv)
             for i in range(sq):
-                js = [j for j in range(sk) if (not causal) or j <= i + (sk - sq)]
+                pos = i + (sk - sq)
+                js = [j for j in range(sk) if ((not causal) or j <= pos)
+                      and (left is None or pos - j <= left)]
                 s = [float((q[bi, i, h] * k[bi, j, kh]).sum()) * scale for j in js]
                 m = max(s)
                 w = [math.exp(x - m) for x in s]
@@ -64,6 +68,81 @@ def test_math_block_vs_sdpa(causal):
     ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
                                          is_causal=causal, scale=0.3, enable_gqa=True)
     assert torch.allclose(out.double(), ref.transpose(1, 2), atol=TOL32)
+
+
+@pytest.mark.parametrize("causal,sq,sk,left", [
+    (True, 7, 7, 2), (False, 7, 7, 3), (True, 4, 9, 1), (False, 4, 9, 0), (False, 9, 4, 2),
+    (True, 6, 6, 0)])
+def test_math_block_window_vs_brute_force(causal, sq, sk, left):
+    """The window of ring/kernels.py:68-72 (bottom-right aligned positions) against the
+    row loop over the keys it leaves."""
+    check_window_block(rm.math_block, causal, sq, sk, left)
+
+
+def check_window_block(block_fn, causal, sq, sk, left):
+    q, k, v = rnd(1, sq, 4, 8, seed=15), rnd(1, sk, 2, 8, seed=16), rnd(1, sk, 2, 8, seed=17)
+    out, lse = block_fn(q, k, v, causal=causal, scaling=None, window=(left, 0))
+    ref_out, ref_lse = brute_block(q, k, v, causal, 1.0 / math.sqrt(8), left)
+    assert torch.allclose(out.double(), ref_out, atol=TOL32, rtol=TOL32)
+    assert torch.allclose(lse.double(), ref_lse, atol=TOL32, rtol=TOL32)
+
+
+def test_math_block_window_special_cases():
+    """A window covering every key is no window; a causal window of 0 on a square block
+    leaves each query its own key: out = v, lse = scale q.k."""
+    q, k, v = rnd(1, 6, 2, 8, seed=18), rnd(1, 6, 2, 8, seed=19), rnd(1, 6, 2, 8, seed=20)
+    for causal in (False, True):
+        wide, _ = rm.math_block(q, k, v, causal=causal, scaling=0.4, window=(5, 0))
+        plain, _ = rm.math_block(q, k, v, causal=causal, scaling=0.4)
+        assert torch.allclose(wide, plain, atol=TOL32)
+    out, lse = rm.math_block(q, k, v, causal=True, scaling=0.4, window=(0, 0))
+    assert torch.allclose(out.double(), v, atol=TOL32)
+    assert torch.allclose(lse.double(), 0.4 * (q * k).sum(-1).transpose(1, 2), atol=TOL32)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_allgather_ring_window_positions(causal):
+    """The gather ring's one block per rank (ring/loop.py:201-228): causal, rank r's
+    query i sits at global position r L + i, so the ranks together are the global
+    windowed attention (brute force over the whole sequence); non-causal, every rank's
+    queries sit at (P - 1) L + i against all keys."""
+    P, L, left = 3, 4, 5
+    qs = [rnd(1, 2, L, 8, seed=21 + r) for r in range(P)]
+    ks = [rnd(1, 1, L, 8, seed=31 + r) for r in range(P)]
+    vs = [rnd(1, 1, L, 8, seed=41 + r) for r in range(P)]
+    outs, lses = rm.allgather_ring_forward(qs, ks, vs, causal=causal, scaling=None, window=(left, 0))
+    kf = torch.cat([t.transpose(1, 2) for t in ks], 1)
+    vf = torch.cat([t.transpose(1, 2) for t in vs], 1)
+    sc = 1.0 / math.sqrt(8)
+    if causal:
+        qf = torch.cat([t.transpose(1, 2) for t in qs], 1)
+        ref_o, ref_l = brute_block(qf, kf, vf, True, sc, left)
+        for r in range(P):
+            assert torch.allclose(outs[r].double(), ref_o[:, r * L:(r + 1) * L], atol=TOL32)
+            assert torch.allclose(lses[r].double(), ref_l[:, :, r * L:(r + 1) * L], atol=TOL32)
+    else:
+        for r in range(P):
+            ref_o, ref_l = brute_block(qs[r].transpose(1, 2), kf, vf, False, sc, left)
+            assert torch.allclose(outs[r].double(), ref_o, atol=TOL32)
+            assert torch.allclose(lses[r].double(), ref_l, atol=TOL32)
+
+
+def test_varlen_ring_window_equals_per_document():
+    """The packed gather ring with a window (ring/loop.py:175-198) is, per document, the
+    causal windowed attention of that document alone."""
+    P, L, left = 2, 8, 3
+    cu = torch.tensor([0, 5, 11, 16])
+    qs = [rnd(1, 2, L, 8, seed=51 + r) for r in range(P)]
+    ks = [rnd(1, 2, L, 8, seed=61 + r) for r in range(P)]
+    vs = [rnd(1, 2, L, 8, seed=71 + r) for r in range(P)]
+    outs, lses = rm.varlen_ring_forward(qs, ks, vs, cu, scaling=None, window=(left, 0))
+    out = torch.cat(outs, 1)
+    lse = torch.cat(lses, 2)
+    qf, kf, vf = (torch.cat([t.transpose(1, 2) for t in ts], 1) for ts in (qs, ks, vs))
+    for a, b in zip(cu[:-1].tolist(), cu[1:].tolist()):
+        ref_o, ref_l = brute_block(qf[:, a:b], kf[:, a:b], vf[:, a:b], True, 1 / math.sqrt(8), left)
+        assert torch.allclose(out[:, a:b].double(), ref_o, atol=TOL32)
+        assert torch.allclose(lse[:, :, a:b].double(), ref_l, atol=TOL32)
 
 
 def check_merge(merge_fn):
