@@ -28,19 +28,23 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 11 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 12 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
                               8: allocation-free Mamba2 correction bwd;
                               9: carried-in state h_in / dh_in of the linear scan;
                               10: L-parallel linear scan (workspace argument);
                               11: sliding windows, attention head_dim any multiple of 8
-                                  up to 128 */
+                                  up to 128; 12: fp16 attention (layout dtype) */
 
 /* error codes */
 #define RMX_OK 0
 #define RMX_EINVAL (-1)   /* bad argument: maps to ValueError */
 #define RMX_EUNSUPPORTED (-2) /* valid but not implemented here: NotImplementedError */
 #define RMX_EDEVICE (-3)  /* HIP runtime / launch failure: RuntimeError */
+
+/* 16-bit element types of q, k, v, out, dout and the 16-bit gradients of one attention call */
+#define RMX_DTYPE_BF16 0
+#define RMX_DTYPE_F16 1
 
 /* block mask kinds (ring/kernels.py:64-67, ring/varlen_blocks.py:51-58) */
 #define RMX_MASK_FULL 0   /* every (q, k) pair attends */
@@ -79,6 +83,8 @@ typedef struct rmx_attn_layout {
                                        or 128 and read the columns past head_dim as zeros */
   float scale;                      /* softmax scale (1/sqrt(head_dim) by default) */
   int32_t mask;                     /* RMX_MASK_* */
+  int32_t dtype;                    /* RMX_DTYPE_*: the 16-bit tensors ("bf16" below) hold this
+                                       type; accumulators, lse and delta stay fp32 */
   /* element strides (batch, seq, head) */
   int64_t q_sb, q_ss, q_sh;
   int64_t k_sb, k_ss, k_sh;
@@ -182,11 +188,15 @@ int32_t rmx_attn_bwd(const rmx_attn_layout* layout, const rmx_bwd_problem* probl
  * Standalone online-softmax merge, `update_out_and_lse` (ring/merge.py:20-31):
  *   new = logaddexp(lse, blk_lse); out = e^(lse-new) out + e^(blk_lse-new) blk_out.
  * out: fp32 [b, s, h, d] (strides o_*), lse: fp32 [b, s, h] (strides l_*),
- * blk_out: bf16 (blk_is_f32 == 0) or fp32 [b, s, h, d] (strides bo_*),
+ * blk_out: [b, s, h, d] (strides bo_*) of type blk_type, RMX_BLK_BF16 (0), RMX_BLK_F32 (1)
+ * or RMX_BLK_F16 (2),
  * blk_lse: fp32 [b, h, s] (strides bl_*). init != 0: out/lse := block
  * (the `out is None` branch, ring/merge.py:27-28). Updated in place.
  */
-int32_t rmx_lse_merge(float* out, float* lse, const void* blk_out, int32_t blk_is_f32,
+#define RMX_BLK_BF16 0
+#define RMX_BLK_F32 1
+#define RMX_BLK_F16 2
+int32_t rmx_lse_merge(float* out, float* lse, const void* blk_out, int32_t blk_type,
                       const float* blk_lse, int32_t batch, int32_t seq, int32_t heads,
                       int32_t head_dim, const int64_t* o_strides /*3*/,
                       const int64_t* l_strides /*3*/, const int64_t* bo_strides /*3*/,

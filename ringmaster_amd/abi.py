@@ -17,12 +17,15 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
-ABI_VERSION = 11  # RMX_ABI_VERSION of include/ringmaster_amd.h
+ABI_VERSION = 12  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
 RMX_EUNSUPPORTED = -2
 RMX_EDEVICE = -3
+
+DTYPE_BF16 = 0
+DTYPE_F16 = 1
 
 MASK_FULL = 0
 MASK_CAUSAL = 1
@@ -49,7 +52,7 @@ _vp = ctypes.c_void_p
 class AttnLayout(ctypes.Structure):
     _fields_ = [
         ("batch", _i32), ("hq", _i32), ("hkv", _i32), ("head_dim", _i32),
-        ("scale", ctypes.c_float), ("mask", _i32),
+        ("scale", ctypes.c_float), ("mask", _i32), ("dtype", _i32),
         ("q_sb", _i64), ("q_ss", _i64), ("q_sh", _i64),
         ("k_sb", _i64), ("k_ss", _i64), ("k_sh", _i64),
         ("v_sb", _i64), ("v_ss", _i64), ("v_sh", _i64),

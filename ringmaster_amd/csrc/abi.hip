@@ -46,6 +46,8 @@ int check_layout(const rmx_attn_layout* L) {
     return fail(RMX_EINVAL, "softmax scale must be finite and positive (got %g)", (double)L->scale);
   if (L->mask < RMX_MASK_FULL || L->mask > RMX_MASK_DOC)
     return fail(RMX_EINVAL, "unknown mask kind %d", L->mask);
+  if (L->dtype != RMX_DTYPE_BF16 && L->dtype != RMX_DTYPE_F16)
+    return fail(RMX_EINVAL, "unknown element type %d", L->dtype);
   const int64_t bf[] = {L->q_sb, L->q_ss, L->q_sh, L->k_sb, L->k_ss, L->k_sh,
                         L->v_sb, L->v_ss, L->v_sh, L->o_sb, L->o_ss, L->o_sh,
                         L->dk_sb, L->dk_ss, L->dk_sh};
@@ -216,7 +218,7 @@ int32_t rmx_attn_bwd(const rmx_attn_layout* layout, const rmx_bwd_problem* probl
   return RMX_OK;
 }
 
-int32_t rmx_lse_merge(float* out, float* lse, const void* blk_out, int32_t blk_is_f32,
+int32_t rmx_lse_merge(float* out, float* lse, const void* blk_out, int32_t blk_type,
                       const float* blk_lse, int32_t batch, int32_t seq, int32_t heads,
                       int32_t head_dim, const int64_t* o_strides, const int64_t* l_strides,
                       const int64_t* bo_strides, const int64_t* bl_strides, int32_t init,
@@ -224,6 +226,8 @@ int32_t rmx_lse_merge(float* out, float* lse, const void* blk_out, int32_t blk_i
   if (batch < 0 || seq < 0 || heads < 0) return fail(RMX_EINVAL, "negative shape");
   if (head_dim <= 0 || head_dim % 8)
     return fail(RMX_EUNSUPPORTED, "head_dim must be a positive multiple of 8 (got %d)", head_dim);
+  if (blk_type < RMX_BLK_BF16 || blk_type > RMX_BLK_F16)
+    return fail(RMX_EINVAL, "unknown block type %d", blk_type);
   if ((int64_t)batch * seq * heads == 0) return RMX_OK;
   if (!out || !lse || !blk_out || !blk_lse) return fail(RMX_EINVAL, "NULL tensor pointer");
   if (!o_strides || !l_strides || !bo_strides || !bl_strides)
@@ -232,10 +236,10 @@ int32_t rmx_lse_merge(float* out, float* lse, const void* blk_out, int32_t blk_i
     return fail(RMX_EINVAL, "out and blk_out must be 16-byte aligned");
   for (int i = 0; i < 3; ++i) {
     if (o_strides[i] % 4) return fail(RMX_EINVAL, "out strides must be multiples of 4");
-    if (bo_strides[i] % (blk_is_f32 ? 4 : 8))
+    if (bo_strides[i] % (blk_type == RMX_BLK_F32 ? 4 : 8))
       return fail(RMX_EINVAL, "blk_out strides must keep 16-byte alignment");
   }
-  return dev_status(rmx::launch_lse_merge(out, lse, blk_out, blk_is_f32, blk_lse, batch, seq, heads,
+  return dev_status(rmx::launch_lse_merge(out, lse, blk_out, blk_type, blk_lse, batch, seq, heads,
                                           head_dim, o_strides, l_strides, bo_strides, bl_strides,
                                           init, (hipStream_t)stream),
                     "rmx_lse_merge launch");

@@ -36,7 +36,7 @@ struct BwdParams {
 // rounding of out (up to |dout|*|out|*2^-9 per element) out of dS = P (dP - delta).
 // With nlse, the same pass writes nlse = -lse log2(e) (the per-query exponent
 // offset of the dK/dV kernel) at the same [b, h, s] position.
-template <int HD, bool OUT_F32>
+template <int HD, bool OUT_F32, int DT>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layout L,
                                                              const void* __restrict__ out,
                                                              const uint16_t* __restrict__ dout,
@@ -74,14 +74,14 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layo
       const u32x4 a = ld16(reinterpret_cast<const uint16_t*>(out) + off);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        o[2 * i] = __uint_as_float(a[i] << 16);
-        o[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+        o[2 * i] = e2f<DT>(a[i] & 0xffffu);
+        o[2 * i + 1] = e2f<DT>(a[i] >> 16);
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      acc += o[2 * i] * __uint_as_float(b[i] << 16);
-      acc += o[2 * i + 1] * __uint_as_float(b[i] & 0xffff0000u);
+      acc += o[2 * i] * e2f<DT>(b[i] & 0xffffu);
+      acc += o[2 * i + 1] * e2f<DT>(b[i] >> 16);
     }
   }
 #pragma unroll
@@ -93,18 +93,18 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layo
   }
 }
 
-template <int HD>
+template <int HD, int DT>
 static void launch_delta_t(const rmx_attn_layout& L, const void* out, int out_f32,
                            const uint16_t* dout, float* delta, const float* lse, float* nlse,
                            int sq, int64_t rows, hipStream_t stream) {
   constexpr int RPB = 256 / (HD / 8);  // rows per block
   const int grid = (int)((rows + RPB - 1) / RPB);
   if (out_f32)
-    hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, true>), dim3(grid), dim3(256), 0, stream, L, out,
-                       dout, delta, lse, nlse, sq);
-  else
-    hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, false>), dim3(grid), dim3(256), 0, stream, L,
+    hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, true, DT>), dim3(grid), dim3(256), 0, stream, L,
                        out, dout, delta, lse, nlse, sq);
+  else
+    hipLaunchKernelGGL((attn_bwd_delta_kernel<HD, false, DT>), dim3(grid), dim3(256), 0, stream,
+                       L, out, dout, delta, lse, nlse, sq);
 }
 
 hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int out_f32,
@@ -112,15 +112,21 @@ hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int 
                                  int sq, hipStream_t stream) {
   const int64_t rows = (int64_t)L.batch * sq * L.hq;
   if (rows == 0) return hipSuccess;
-  if (L.head_dim > 64)
-    launch_delta_t<128>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
+  const bool f16 = L.dtype == RMX_DTYPE_F16;
+  if (L.head_dim > 64 && f16)
+    launch_delta_t<128, RMX_DTYPE_F16>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
+  else if (L.head_dim > 64)
+    launch_delta_t<128, RMX_DTYPE_BF16>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
+  else if (f16)
+    launch_delta_t<64, RMX_DTYPE_F16>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
   else
-    launch_delta_t<64>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
+    launch_delta_t<64, RMX_DTYPE_BF16>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------- shared helpers
 // Write a 4-float run of a gradient row according to the output mode.
+template <int DT>
 __device__ __forceinline__ void grad_store4(int mode, float* acc, uint16_t* bf, f32x4 v) {
   if (mode == RMX_GRAD_WRITE_F32) {
     *reinterpret_cast<f32x4*>(acc) = v;
@@ -129,8 +135,8 @@ __device__ __forceinline__ void grad_store4(int mode, float* acc, uint16_t* bf, 
   } else {
     if (mode == RMX_GRAD_ACC_FINAL) v += *reinterpret_cast<const f32x4*>(acc);
     u32x2 w;
-    w[0] = pack_bf2(v[0], v[1]);
-    w[1] = pack_bf2(v[2], v[3]);
+    w[0] = cvt_pk<DT>(v[0], v[1]);
+    w[1] = cvt_pk<DT>(v[2], v[3]);
     *reinterpret_cast<u32x2*>(bf) = w;
   }
 }
@@ -160,7 +166,7 @@ struct BwdTiles {
 // (swizzle folded in) plus a compile-time offset below 64 KiB, with no address
 // arithmetic in the loop. Tiles past the end are issued as zero-length loads,
 // which keeps every wait count static.
-template <int HD, int MASK>
+template <int HD, int MASK, int DT>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm) {
   using T = BwdTiles<HD>;
   constexpr int NW = 8, NT = NW * 64, BQ = 32 * NW, BK = 64;
@@ -407,8 +413,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
-          s[mb] = mfma32(row_op(kt_lds, kb, mb), qreg[kb], s[mb]);
-          dp[mb] = mfma32(vrow_op(buf, kb, mb), doreg[kb], dp[mb]);
+          s[mb] = mfma32t<DT>(row_op(kt_lds, kb, mb), qreg[kb], s[mb]);
+          dp[mb] = mfma32t<DT>(vrow_op(buf, kb, mb), doreg[kb], dp[mb]);
         }
       }
 
@@ -437,7 +443,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] *= dp[mb][b8 + i] - dlt;
-        dsb[kb2] = pack8_hw(v);
+        dsb[kb2] = pack8t<DT>(v);
       }
 
       // dQ^T += K^T dS^T
@@ -445,7 +451,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
       for (int kb2 = 0; kb2 < 4; ++kb2)
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-          acc[db] = mfma32(tr_op(kt_lds, kb2, db), dsb[kb2], acc[db]);
+          acc[db] = mfma32t<DT>(tr_op(kt_lds, kb2, db), dsb[kb2], acc[db]);
     }
     tile_barrier();
   };
@@ -471,7 +477,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
       v[1] = acc[db][4 * j + 1] * scale;
       v[2] = acc[db][4 * j + 2] * scale;
       v[3] = acc[db][4 * j + 3] * scale;
-      grad_store4(P.dq_mode, arow ? arow + d0 : nullptr, brow ? brow + d0 : nullptr, v);
+      grad_store4<DT>(P.dq_mode, arow ? arow + d0 : nullptr, brow ? brow + d0 : nullptr, v);
     }
 }
 
@@ -525,7 +531,7 @@ struct DkdvCfg {
   static_assert(NS == 2 * NKB && NS == 4 * NDB, "phase shapes");
 };
 
-template <int HD, int MASK>
+template <int HD, int MASK, int DT>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams prm) {
   using C = DkdvCfg<HD>;
   constexpr int BQ = C::BQ, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB, NS = C::NS;
@@ -853,7 +859,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32(row_op(sQ[0], kb, mb), kreg[kb], s[mb]);
+      for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32t<DT>(row_op(sQ[0], kb, mb), kreg[kb], s[mb]);
     pin_v(s);
     load_rows(sM[0], nl);
     load_rows(sM[0] + BQ, dp);
@@ -876,7 +882,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       v1 *= y[mb][r + 1];
     }
     u32x4 u = __builtin_bit_cast(u32x4, op);
-    uint32_t pk = cvt_pk_bf16(v0, v1);
+    uint32_t pk = cvt_pk<DT>(v0, v1);
     asm volatile("" : "+v"(pk));
     u[w] = pk;
     op = __builtin_bit_cast(bf16x8, u);
@@ -912,14 +918,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       __builtin_amdgcn_sched_barrier(0);
       const bf16x8 a = ops[T % RING];
       if constexpr (ph == 0) {
-        dp[t & 1] = mfma32(a, vreg[t >> 1], dp[t & 1]);
+        dp[t & 1] = mfma32t<DT>(a, vreg[t >> 1], dp[t & 1]);
       } else if constexpr (ph == 1) {
-        dv[t % NDB] = mfma32(pt[t / NDB], a, dv[t % NDB]);
+        dv[t % NDB] = mfma32t<DT>(pt[t / NDB], a, dv[t % NDB]);
       } else if constexpr (ph == 2) {
-        dk[t % NDB] = mfma32(dst[t / NDB], a, dk[t % NDB]);
+        dk[t % NDB] = mfma32t<DT>(dst[t / NDB], a, dk[t % NDB]);
       } else {
         if constexpr (t < 2) s[t] = zero16();
-        s[t & 1] = mfma32(a, kreg[t >> 1], s[t & 1]);
+        s[t & 1] = mfma32t<DT>(a, kreg[t >> 1], s[t & 1]);
         if constexpr (t == NS - 1) pin_v(s);
       }
       if constexpr (ph == 0) {
@@ -1018,16 +1024,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
         } else if (mode == RMX_GRAD_ACC_F32) {
           gacc[ao] += gv;
         } else if (mode == RMX_GRAD_ACC_FINAL) {
-          gbf[bo] = f2bf(gacc[ao] + gv);
+          gbf[bo] = f2e<DT>(gacc[ao] + gv);
         } else {
-          gbf[bo] = f2bf(gv);
+          gbf[bo] = f2e<DT>(gv);
         }
       }
     }
   }
 }
 
-template <int HD>
+template <int HD, int DT>
 static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                                hipStream_t stream) {
   constexpr int BQ_DQ = 256, BKV = DkdvCfg<HD>::BKV;
@@ -1069,22 +1075,22 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
   if (tk > 0) {
     const dim3 grid(tk);
     if (L.mask == RMX_MASK_CAUSAL)
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL, DT>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     else if (L.mask == RMX_MASK_DOC)
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_DOC>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_DOC, DT>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     else
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_FULL>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_FULL, DT>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (tq > 0) {
     const dim3 grid(tq);
     if (L.mask == RMX_MASK_CAUSAL)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_CAUSAL>), grid, dim3(512), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_CAUSAL, DT>), grid, dim3(512), 0, stream, pq);
     else if (L.mask == RMX_MASK_DOC)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_DOC>), grid, dim3(512), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_DOC, DT>), grid, dim3(512), 0, stream, pq);
     else
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_FULL>), grid, dim3(512), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_FULL, DT>), grid, dim3(512), 0, stream, pq);
     return hipGetLastError();
   }
   return hipSuccess;
@@ -1092,8 +1098,11 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
 
 hipError_t launch_attn_bwd(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                            hipStream_t stream) {
-  if (L.head_dim > 64) return launch_bwd_t<128>(L, probs, n, stream);
-  return launch_bwd_t<64>(L, probs, n, stream);
+  if (L.dtype == RMX_DTYPE_F16)
+    return L.head_dim > 64 ? launch_bwd_t<128, RMX_DTYPE_F16>(L, probs, n, stream)
+                           : launch_bwd_t<64, RMX_DTYPE_F16>(L, probs, n, stream);
+  return L.head_dim > 64 ? launch_bwd_t<128, RMX_DTYPE_BF16>(L, probs, n, stream)
+                         : launch_bwd_t<64, RMX_DTYPE_BF16>(L, probs, n, stream);
 }
 
 }  // namespace rmx

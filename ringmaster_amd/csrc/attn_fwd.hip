@@ -66,7 +66,7 @@ struct FwdCfg {
 
 constexpr float kRescaleSlack = 8.0f;  // log2 units: P <= 2^8 between rescales
 
-template <int HD, int MASK>
+template <int HD, int MASK, int DT>
 __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   using C = FwdCfg<HD>;
   constexpr int BK = C::BK, MB = C::MB, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB;
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
 #pragma unroll
     for (int t = 0; t < NKB; ++t)
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) sA[mb] = mfma32(k_op(0, t, mb), qreg[t], sA[mb]);
+      for (int mb = 0; mb < MB; ++mb) sA[mb] = mfma32t<DT>(k_op(0, t, mb), qreg[t], sA[mb]);
     if (need_mask(0)) {
       keep_branch();
       apply_mask(0, sA);
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   // ---- iteration j: S_j (masked, its max folded into m_run) is in sc.
   //   region 1: S_{j+1} = K_{j+1} Q^T into sn (NKB steps of MB MFMAs), with the
   //             exponentials of the first 3/4 of S_j (pairs of elements ->
-  //             v_cvt_pk_bf16_f32 -> P_j);
+  //             the 16-bit packing (v_cvt_pk_bf16_f32 for bf16) -> P_j);
   //   region 2: O += V_j^T P_j (PVS steps of two MFMAs), with the last quarter
   //             of the exponentials (ahead of the PV MFMAs that use them) and
   //             the row max of S_{j+1};
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
       const float x0 = fast_exp2(fmaf(sc[kb2 >> 1][8 * (kb2 & 1) + 2 * w], c, -mbase));
       const float x1 = fast_exp2(fmaf(sc[kb2 >> 1][8 * (kb2 & 1) + 2 * w + 1], c, -mbase));
       float rs = rsp[kb2] + (x0 + x1);
-      uint32_t pk = cvt_pk_bf16(x0, x1);
+      uint32_t pk = cvt_pk<DT>(x0, x1);
       // pin the results here: otherwise the compiler sinks the exponentials to
       // their first use (after the region) and the step has no VALU work
       asm volatile("" : "+v"(rs), "+v"(pk));
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) sn[mb] = mfma32(ka[t % (KD + 1)][mb], qreg[t], sn[mb]);
+            for (int mb = 0; mb < MB; ++mb) sn[mb] = mfma32t<DT>(ka[t % (KD + 1)][mb], qreg[t], sn[mb]);
             [&]<int... Q>(std::integer_sequence<int, Q...>) __attribute__((always_inline)) {
               (pair(std::integral_constant<int, P1 * t / NKB + Q>{}), ...);
             }(std::make_integer_sequence<int, P1 * (t + 1) / NKB - P1 * t / NKB>{});
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
 #pragma unroll
             for (int v = 0; v < 2; ++v) {
               const int idx = pv_idx(u, v);
-              o[idx % NDB] = mfma32(va[u % (VD + 1)][v], __builtin_bit_cast(bf16x8, pw[idx / NDB]), o[idx % NDB]);
+              o[idx % NDB] = mfma32t<DT>(va[u % (VD + 1)][v], __builtin_bit_cast(bf16x8, pw[idx / NDB]), o[idx % NDB]);
             }
             // the remaining pairs, all before step PV3 (which starts on pb[3])
             if constexpr (u < PV3) {
@@ -532,8 +532,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
       if (accrow) *reinterpret_cast<f32x4*>(accrow + d0) = v;
       if (P.mode == RMX_FWD_WRITE || P.mode == RMX_FWD_ACC_FINAL) {
         u32x2 w;
-        w[0] = cvt_pk_bf16(v[0], v[1]);
-        w[1] = cvt_pk_bf16(v[2], v[3]);
+        w[0] = cvt_pk<DT>(v[0], v[1]);
+        w[1] = cvt_pk<DT>(v[2], v[3]);
         *reinterpret_cast<u32x2*>(orow + d0) = w;
       }
     }
@@ -546,7 +546,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   }
 }
 
-template <int HD>
+template <int HD, int DT>
 static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                                hipStream_t stream) {
   constexpr int BQ = FwdCfg<HD>::BQ;
@@ -566,21 +566,24 @@ static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* 
   const int grid = plan_workgroups(prm.map, n, groups, ntile);
   if (grid == 0) return hipSuccess;
   if (L.mask == RMX_MASK_CAUSAL)
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_CAUSAL>), dim3(grid), dim3(FwdCfg<HD>::NT), 0,
-                       stream, prm);
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_CAUSAL, DT>), dim3(grid),
+                       dim3(FwdCfg<HD>::NT), 0, stream, prm);
   else if (L.mask == RMX_MASK_DOC)
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_DOC>), dim3(grid), dim3(FwdCfg<HD>::NT), 0,
-                       stream, prm);
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_DOC, DT>), dim3(grid), dim3(FwdCfg<HD>::NT),
+                       0, stream, prm);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_FULL>), dim3(grid), dim3(FwdCfg<HD>::NT), 0,
-                       stream, prm);
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_FULL, DT>), dim3(grid),
+                       dim3(FwdCfg<HD>::NT), 0, stream, prm);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_fwd(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                            hipStream_t stream) {
-  if (L.head_dim > 64) return launch_fwd_t<128>(L, probs, n, stream);
-  return launch_fwd_t<64>(L, probs, n, stream);
+  if (L.dtype == RMX_DTYPE_F16)
+    return L.head_dim > 64 ? launch_fwd_t<128, RMX_DTYPE_F16>(L, probs, n, stream)
+                           : launch_fwd_t<64, RMX_DTYPE_F16>(L, probs, n, stream);
+  return L.head_dim > 64 ? launch_fwd_t<128, RMX_DTYPE_BF16>(L, probs, n, stream)
+                         : launch_fwd_t<64, RMX_DTYPE_BF16>(L, probs, n, stream);
 }
 
 }  // namespace rmx

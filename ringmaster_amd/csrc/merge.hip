@@ -2,7 +2,7 @@
 //   new = logaddexp(lse, blk_lse)
 //   out = exp(lse - new) * out + exp(blk_lse - new) * blk_out
 // out fp32 [b,s,h,d], lse fp32 [b,s,h] (the reference's [b,s,h,1]), blk_out
-// bf16 or fp32 [b,s,h,d], blk_lse fp32 [b,h,s] (flash layout, transposed on
+// bf16, fp16 or fp32 [b,s,h,d], blk_lse fp32 [b,h,s] (flash layout, transposed on
 // the fly as _lse_to_bshd does). One thread owns 8 channels of one row; the
 // threads of a row share the row's two lse loads through the L1. Up to 2^31
 // threads the launch is one thread per 8 channels with 32-bit index math.
@@ -12,8 +12,8 @@
 
 namespace rmx {
 
-// Merge of the 8 channels [8 part, 8 part + 8) of row (b, s, h).
-template <bool BLK_F32>
+// Merge of the 8 channels [8 part, 8 part + 8) of row (b, s, h). BLK: RMX_BLK_*.
+template <int BLK>
 __device__ __forceinline__ void merge8(float* __restrict__ out, float* __restrict__ lse,
                                        const void* __restrict__ blk,
                                        const float* __restrict__ blk_lse, int b, int s, int h,
@@ -25,7 +25,7 @@ __device__ __forceinline__ void merge8(float* __restrict__ out, float* __restric
   float* op = out + b * os0 + s * os1 + h * os2 + 8 * part;
   float* lp = lse + b * ls0 + s * ls1 + h * ls2;
   float bv[8];
-  if (BLK_F32) {
+  if (BLK == RMX_BLK_F32) {
     const float* bp = reinterpret_cast<const float*>(blk) + b * bs0 + s * bs1 + h * bs2 + 8 * part;
     const f32x4 x0 = *reinterpret_cast<const f32x4*>(bp);
     const f32x4 x1 = *reinterpret_cast<const f32x4*>(bp + 4);
@@ -38,10 +38,11 @@ __device__ __forceinline__ void merge8(float* __restrict__ out, float* __restric
     const uint16_t* bp =
         reinterpret_cast<const uint16_t*>(blk) + b * bs0 + s * bs1 + h * bs2 + 8 * part;
     const u32x4 w = ld16(bp);
+    constexpr int DT = BLK == RMX_BLK_F16 ? RMX_DTYPE_F16 : RMX_DTYPE_BF16;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      bv[2 * i] = __uint_as_float(w[i] << 16);
-      bv[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      bv[2 * i] = e2f<DT>(w[i] & 0xffffu);
+      bv[2 * i + 1] = e2f<DT>(w[i] >> 16);
     }
   }
   f32x4 r0, r1;
@@ -75,7 +76,7 @@ __device__ __forceinline__ void merge8(float* __restrict__ out, float* __restric
 }
 
 // Up to 2^31 threads: one thread per 8 channels, 32-bit index arithmetic.
-template <bool BLK_F32>
+template <int BLK>
 __global__ __launch_bounds__(256) void lse_merge_kernel32(
     float* __restrict__ out, float* __restrict__ lse, const void* __restrict__ blk,
     const float* __restrict__ blk_lse, uint32_t n, FastDiv f_tpr, FastDiv f_heads, FastDiv f_seq,
@@ -89,11 +90,11 @@ __global__ __launch_bounds__(256) void lse_merge_kernel32(
   const uint32_t h = row - rs * f_heads.d;
   const uint32_t b = fdiv(rs, f_seq);
   const uint32_t s = rs - b * f_seq.d;
-  merge8<BLK_F32>(out, lse, blk, blk_lse, (int)b, (int)s, (int)h, (int)part, os0, os1, os2, ls0,
+  merge8<BLK>(out, lse, blk, blk_lse, (int)b, (int)s, (int)h, (int)part, os0, os1, os2, ls0,
                   ls1, ls2, bs0, bs1, bs2, bl0, bl1, init);
 }
 
-template <bool BLK_F32>
+template <int BLK>
 __global__ __launch_bounds__(256) void lse_merge_kernel(float* __restrict__ out,
                                                         float* __restrict__ lse,
                                                         const void* __restrict__ blk,
@@ -112,12 +113,12 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(float* __restrict__ out,
     const int h = (int)(row % heads);
     const int s = (int)((row / heads) % seq);
     const int b = (int)(row / ((int64_t)heads * seq));
-    merge8<BLK_F32>(out, lse, blk, blk_lse, b, s, h, part, os0, os1, os2, ls0, ls1, ls2, bs0, bs1,
+    merge8<BLK>(out, lse, blk, blk_lse, b, s, h, part, os0, os1, os2, ls0, ls1, ls2, bs0, bs1,
                     bs2, bl0, bl1, init);
   }
 }
 
-hipError_t launch_lse_merge(float* out, float* lse, const void* blk_out, int blk_is_f32,
+hipError_t launch_lse_merge(float* out, float* lse, const void* blk_out, int blk_type,
                             const float* blk_lse, int batch, int seq, int heads, int head_dim,
                             const int64_t* os, const int64_t* ls, const int64_t* bos,
                             const int64_t* bls, int init, hipStream_t stream) {
@@ -127,27 +128,32 @@ hipError_t launch_lse_merge(float* out, float* lse, const void* blk_out, int blk
     const FastDiv ft = make_fastdiv((uint32_t)(head_dim / 8)), fh = make_fastdiv((uint32_t)heads),
                   fs = make_fastdiv((uint32_t)seq);
     const dim3 grid((unsigned)((n + 255) / 256));
-    if (blk_is_f32)
-      hipLaunchKernelGGL(lse_merge_kernel32<true>, grid, dim3(256), 0, stream, out, lse, blk_out,
-                         blk_lse, (uint32_t)n, ft, fh, fs, os[0], os[1], os[2], ls[0], ls[1], ls[2],
-                         bos[0], bos[1], bos[2], bls[0], bls[1], init);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, out, lse, blk_out, blk_lse,
+                         (uint32_t)n, ft, fh, fs, os[0], os[1], os[2], ls[0], ls[1], ls[2], bos[0],
+                         bos[1], bos[2], bls[0], bls[1], init);
+    };
+    if (blk_type == RMX_BLK_F32)
+      go(lse_merge_kernel32<RMX_BLK_F32>);
+    else if (blk_type == RMX_BLK_F16)
+      go(lse_merge_kernel32<RMX_BLK_F16>);
     else
-      hipLaunchKernelGGL(lse_merge_kernel32<false>, grid, dim3(256), 0, stream, out, lse, blk_out,
-                         blk_lse, (uint32_t)n, ft, fh, fs, os[0], os[1], os[2], ls[0], ls[1], ls[2],
-                         bos[0], bos[1], bos[2], bls[0], bls[1], init);
+      go(lse_merge_kernel32<RMX_BLK_BF16>);
     return hipGetLastError();
   }
   int64_t blocks = (n + 255) / 256;
   if (blocks > 256 * 64) blocks = 256 * 64;
-  if (blk_is_f32) {
-    hipLaunchKernelGGL(lse_merge_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, out,
-                       lse, blk_out, blk_lse, batch, seq, heads, head_dim, os[0], os[1], os[2],
-                       ls[0], ls[1], ls[2], bos[0], bos[1], bos[2], bls[0], bls[1], init);
-  } else {
-    hipLaunchKernelGGL(lse_merge_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, out,
-                       lse, blk_out, blk_lse, batch, seq, heads, head_dim, os[0], os[1], os[2],
-                       ls[0], ls[1], ls[2], bos[0], bos[1], bos[2], bls[0], bls[1], init);
-  }
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, out, lse, blk_out,
+                       blk_lse, batch, seq, heads, head_dim, os[0], os[1], os[2], ls[0], ls[1],
+                       ls[2], bos[0], bos[1], bos[2], bls[0], bls[1], init);
+  };
+  if (blk_type == RMX_BLK_F32)
+    go(lse_merge_kernel<RMX_BLK_F32>);
+  else if (blk_type == RMX_BLK_F16)
+    go(lse_merge_kernel<RMX_BLK_F16>);
+  else
+    go(lse_merge_kernel<RMX_BLK_BF16>);
   return hipGetLastError();
 }
 

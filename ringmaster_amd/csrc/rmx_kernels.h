@@ -15,7 +15,7 @@ hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int 
                                  int sq, hipStream_t stream);
 hipError_t launch_attn_bwd(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                            hipStream_t stream);
-hipError_t launch_lse_merge(float* out, float* lse, const void* blk_out, int blk_is_f32,
+hipError_t launch_lse_merge(float* out, float* lse, const void* blk_out, int blk_type,
                             const float* blk_lse, int batch, int seq, int heads, int head_dim,
                             const int64_t* os, const int64_t* ls, const int64_t* bos,
                             const int64_t* bls, int init, hipStream_t stream);
@@ -135,6 +135,56 @@ inline int plan_workgroups(WgMapParams& m, int n, const int* groups, const int* 
   for (int i = n; i <= RMX_MAX_BATCHED; ++i) m.start[i] = acc;
   m.total = acc;
   return m.balanced ? 8 * acc : acc;
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit element types of the attention kernels (RMX_DTYPE_BF16, RMX_DTYPE_F16).
+// Operands travel as bf16x8 bit patterns in both cases (loads, LDS tiles, transposed
+// reads and the sign flip of V are bit operations on 16-bit lanes); only the MFMA and
+// the fp32 <-> 16-bit conversions (round to nearest even) depend on the type.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma32t(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  if constexpr (DT == RMX_DTYPE_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// Two floats -> two packed 16-bit elements (lo in bits 0..15).
+template <int DT>
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+  if constexpr (DT == RMX_DTYPE_F16) {
+    const f32x2 f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+  } else {
+    return cvt_pk_bf16(lo, hi);
+  }
+}
+template <int DT>
+__device__ __forceinline__ uint16_t f2e(float f) {
+  if constexpr (DT == RMX_DTYPE_F16)
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  else
+    return f2bf(f);
+}
+template <int DT>
+__device__ __forceinline__ float e2f(uint32_t bits16) {
+  if constexpr (DT == RMX_DTYPE_F16)
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+  else
+    return bf2f((uint16_t)bits16);
+}
+template <int DT>
+__device__ __forceinline__ bf16x8 pack8t(const float* v) {
+  u32x4 u;
+  u[0] = cvt_pk<DT>(v[0], v[1]);
+  u[1] = cvt_pk<DT>(v[2], v[3]);
+  u[2] = cvt_pk<DT>(v[4], v[5]);
+  u[3] = cvt_pk<DT>(v[6], v[7]);
+  return __builtin_bit_cast(bf16x8, u);
 }
 
 // Host side: order[] = problem indices sorted by cost[] descending (stable).

@@ -7,8 +7,8 @@ fp32)``, q/k/v ``[b, s, h, d]``, GQA by ``kv_head = q_head // (hq/hkv)``, causal
 bottom-right aligned (ring/kernels.py:64-67), a sliding window ``(left, right)``
 masking ``pos_q - pos_k > left`` on the same bottom-right aligned positions
 (ring/kernels.py:68-72; ``right`` is not used, as there), head dims that are
-multiples of 8 up to 128. It is autograd-aware like ``hf_kernels``/``math``; the lse
-output is not differentiable (as with flash).
+multiples of 8 up to 128, bf16 or fp16. It is autograd-aware like ``hf_kernels``/``math``;
+the lse output is not differentiable (as with flash).
 
 ``flash_ops()`` returns ``(fwd, bwd)`` with the positional signatures of the Dao
 low-level ops that the ring schedules call (ring/p2p_attn.py:27-62,
@@ -33,8 +33,10 @@ def _validate(q, k, v, dropout, window, softcap=0.0, alibi=None):
         raise ValueError("q/k/v must be [batch, seq, heads, dim]")
     if q.shape[2] % k.shape[2]:
         raise ValueError("Query heads must be divisible by KV heads")
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
-        raise NotImplementedError(f"mi355x_hip blocks compute in bf16 (got {q.dtype})")
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError(f"mi355x_hip blocks compute in bf16 or fp16 (got {q.dtype})")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q, k and v must share their dtype ({q.dtype}, {k.dtype}, {v.dtype})")
     d = q.shape[-1]
     if d % 8 or d > 128 or k.shape[-1] != d or v.shape[-1] != d:
         raise NotImplementedError(f"head_dim {d} is not supported (a multiple of 8, at most 128)")
@@ -70,11 +72,11 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
 
 
 def block_forward(q, k, v, scale: float, causal: bool, keep_f32: bool = False, window=None):
-    """(out bf16 [b, sq, hq, d], lse fp32 [b, hq, sq]) of one block; with ``keep_f32`` also
+    """(out [b, sq, hq, d] in q's dtype, lse fp32 [b, hq, sq]) of one block; with ``keep_f32`` also
     the fp32 out (what the backward's delta is computed from). ``window``: bound on
     ``pos_q - pos_k`` (bottom-right aligned positions) or None."""
     b, sq, hq, d = q.shape
-    out = torch.empty((b, sq, hq, d), dtype=torch.bfloat16, device=q.device)
+    out = torch.empty((b, sq, hq, d), dtype=q.dtype, device=q.device)
     lse = torch.empty((b, hq, sq), dtype=torch.float32, device=q.device)
     out32 = torch.empty((b, sq, hq, d), dtype=torch.float32, device=q.device) if keep_f32 else None
     ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_WRITE, out=out, lse=lse,
@@ -85,9 +87,9 @@ def block_forward(q, k, v, scale: float, causal: bool, keep_f32: bool = False, w
 
 def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None, dk=None, dv=None,
                    out_f32=None, window=None):
-    """dq, dk, dv (bf16) of one block using the given (global) out/lse; returns delta too.
+    """dq, dk, dv (q's dtype) of one block using the given (global) out/lse; returns delta too.
     ``out_f32`` (the forward's fp32 out), when given, is what delta = rowsum(dout * out) reads;
-    otherwise the bf16 ``out`` is used, as a Dao-style backward does."""
+    otherwise the 16-bit ``out`` is used, as a Dao-style backward does."""
     b, sq, hq, d = q.shape
     hkv = k.shape[2]
     if dout.stride() != out.stride():
@@ -100,7 +102,7 @@ def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None,
     ops.attn_bwd_delta(out if out_f32 is None else out_f32, dout, delta, hkv, lse=lse, nlse=nlse)
     dq_t = dq if (dq is not None and dq.stride() == dout.stride()) else torch.empty_like(dout)
     dk_t = dk if (dk is not None and dk.is_contiguous()) else torch.empty(
-        k.shape, dtype=torch.bfloat16, device=k.device)
+        k.shape, dtype=k.dtype, device=k.device)
     dv_t = dv if (dv is not None and dv.stride() == dk_t.stride()) else torch.empty_like(dk_t)
     ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta, nlse=nlse,
                              dq_mode=abi.GRAD_WRITE_BF16, dkv_mode=abi.GRAD_WRITE_BF16,
@@ -133,7 +135,7 @@ class _HipBlockAttention(torch.autograd.Function):
 
 def mi355x_hip_block(q, k, v, *, causal, scaling, dropout=0.0, attn_implementation=None,
                      window=None):
-    """q/k/v: [b, s, h, d] bf16 on the MI355X. Returns (out [b,s,h,d], lse [b,h,s])."""
+    """q/k/v: [b, s, h, d] bf16 or fp16 on the MI355X. Returns (out [b,s,h,d], lse [b,h,s])."""
     left = _validate(q, k, v, dropout, window)
     scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
     return _HipBlockAttention.apply(q, k, v, bool(causal), float(scale), left)

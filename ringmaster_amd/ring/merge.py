@@ -29,8 +29,9 @@ def update_out_and_lse(out, lse, block_out: torch.Tensor, block_lse: torch.Tenso
     b, s, h, d = block_out.shape
     if block_lse.shape != (b, h, s):
         raise ValueError(f"block_lse must be [b, h, s] = {(b, h, s)} (got {tuple(block_lse.shape)})")
-    if block_out.dtype not in (torch.bfloat16, torch.float32):
-        raise NotImplementedError(f"block_out dtype {block_out.dtype} (bf16 or fp32)")
+    blk_types = {torch.bfloat16: 0, torch.float32: 1, torch.float16: 2}  # RMX_BLK_*
+    if block_out.dtype not in blk_types:
+        raise NotImplementedError(f"block_out dtype {block_out.dtype} (bf16, fp16 or fp32)")
     if block_out.stride(-1) != 1 or block_out.data_ptr() % 16:
         block_out = block_out.contiguous()
     if block_lse.dtype != torch.float32 or block_lse.stride(-1) != 1:
@@ -48,7 +49,7 @@ def update_out_and_lse(out, lse, block_out: torch.Tensor, block_lse: torch.Tenso
     lib = abi.lib()
     abi.check(lib.rmx_lse_merge(
         out.data_ptr(), lse3.data_ptr(), block_out.data_ptr(),
-        int(block_out.dtype == torch.float32), block_lse.data_ptr(), b, s, h, d,
+        blk_types[block_out.dtype], block_lse.data_ptr(), b, s, h, d,
         abi.i64_array(out.stride()[:3]), abi.i64_array(lse3.stride()),
         abi.i64_array(block_out.stride()[:3]), abi.i64_array(block_lse.stride()[:2]),
         int(init), abi.stream_of(block_out)))

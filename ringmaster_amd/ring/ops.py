@@ -66,38 +66,49 @@ def _set_window(p, window):
         p.has_window, p.window_left = 1, int(window)
 
 
+_H = None  # the call's 16-bit element type (bf16 or fp16), the dtype of q
+
 _ROLES = {
     # role -> (layout field prefix, number of strides, dtype)
-    "q": ("q", 3, torch.bfloat16),
-    "k": ("k", 3, torch.bfloat16),
-    "v": ("v", 3, torch.bfloat16),
-    "out": ("o", 3, torch.bfloat16),
-    "dout": ("o", 3, torch.bfloat16),
-    "dq": ("o", 3, torch.bfloat16),
+    "q": ("q", 3, _H),
+    "k": ("k", 3, _H),
+    "v": ("v", 3, _H),
+    "out": ("o", 3, _H),
+    "dout": ("o", 3, _H),
+    "dq": ("o", 3, _H),
     "acc_out": ("a", 3, torch.float32),
     "dq_acc": ("a", 3, torch.float32),
     "lse": ("l", 2, torch.float32),
     "acc_lse": ("l", 2, torch.float32),
     "delta": ("l", 2, torch.float32),
     "nlse": ("l", 2, torch.float32),
-    "dk": ("dk", 3, torch.bfloat16),
-    "dv": ("dk", 3, torch.bfloat16),
+    "dk": ("dk", 3, _H),
+    "dv": ("dk", 3, _H),
     "dk_acc": ("ka", 3, torch.float32),
     "dv_acc": ("ka", 3, torch.float32),
 }
 
+_DTYPES = {torch.bfloat16: abi.DTYPE_BF16, torch.float16: abi.DTYPE_F16}
 
-def _fill_layout(jobs, batch, hq, hkv, head_dim, scale, mask) -> abi.AttnLayout:
+
+def _fill_layout(jobs, batch, hq, hkv, head_dim, scale, mask, half=None) -> abi.AttnLayout:
+    """The call's layout; ``half`` (default: the first job's q dtype) is the 16-bit type
+    of q/k/v/out/dout and the 16-bit gradients."""
+    half = half if half is not None else jobs[0].q.dtype
+    if half not in _DTYPES:
+        raise NotImplementedError(f"attention computes in bf16 or fp16 (got {half})")
     lay = abi.AttnLayout()
     lay.batch, lay.hq, lay.hkv, lay.head_dim = batch, hq, hkv, head_dim
     lay.scale = float(scale)
     lay.mask = mask
+    lay.dtype = _DTYPES[half]
     seen: dict[str, tuple] = {}
     for job in jobs:
         for role, (prefix, n, dtype) in _ROLES.items():
             t = getattr(job, role, None)
             if t is None:
                 continue
+            dtype = half if dtype is _H else dtype
             if t.dtype != dtype:
                 raise ValueError(f"{role} must be {dtype} (got {t.dtype})")
             abi.require_device(t)
@@ -160,16 +171,16 @@ def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int) -> None:
 
 def attn_bwd_delta(out: torch.Tensor, dout: torch.Tensor, delta: torch.Tensor, hkv: int,
                    lse: torch.Tensor | None = None, nlse: torch.Tensor | None = None) -> None:
-    """delta[b, h, s] = sum_d dout * out (fp32). dout: [b, s, h, d] bf16; out: bf16 with the
-    strides of dout, or the fp32 final out (any strides with a contiguous dim). With ``nlse``
+    """delta[b, h, s] = sum_d dout * out (fp32). dout: [b, s, h, d] bf16 or fp16; out: the same
+    type with the strides of dout, or the fp32 final out (any strides with a contiguous dim). With ``nlse``
     (and the global ``lse``), also nlse = -lse * log2(e), which the dK/dV kernel reads; lse,
     delta and nlse must share their strides."""
     batch, sq, hq, d = dout.shape
     if out.shape != dout.shape:
         raise ValueError("out and dout must share their shape")
     f32 = out.dtype == torch.float32
-    if not f32 and out.stride() != dout.stride():
-        raise ValueError("bf16 out and dout must share strides")
+    if not f32 and (out.stride() != dout.stride() or out.dtype != dout.dtype):
+        raise ValueError("a 16-bit out must share dout's type and strides")
     if (nlse is None) != (lse is None):
         raise ValueError("lse and nlse go together")
     job = FwdJob(q=dout, k=dout[:, :0, :hkv], v=dout[:, :0, :hkv], out=dout, lse=delta,

@@ -212,7 +212,7 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
     c = _Ctx(q, k, scale, doc, layout, causal, window)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)  # [P, b, L, H, d] views
     dev = q.device
-    out = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=q.dtype, device=dev)
     lse = torch.empty((c.P, c.b, c.hq, c.L), dtype=torch.float32, device=dev)
     acc = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=torch.float32, device=dev)
     acc_lse = None
@@ -316,8 +316,10 @@ def check_ring_inputs(q, k, v):
         raise ValueError("q/k/v must be [world, b, H, L, d]")
     if q.shape[2] % k.shape[2]:
         raise ValueError("Query heads must be divisible by KV heads")
-    if q.dtype != torch.bfloat16:
-        raise NotImplementedError("the MI355X ring computes in bf16")
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError("the MI355X ring computes in bf16 or fp16")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share their dtype")
 
 
 def check_cu_seqlens(cu_seqlens, total: int) -> None:

@@ -6,6 +6,10 @@ import torch
 BF16_MAX_ABS = 2e-2
 BF16_REL_L2 = 1e-2
 F32_REL = 1e-4
+# fp16 outputs (10 mantissa bits, 8 times bf16's resolution): a bar 4 times tighter in both
+# measures, floored at two fp16 ulps of the value (2^-9 |ref|) for gradients above 2
+F16_MAX_ABS = 5e-3
+F16_REL_L2 = 2.5e-3
 
 
 def seeded(shape, seed, scale=1.0):
@@ -16,6 +20,12 @@ def seeded(shape, seed, scale=1.0):
 def bf16_pair(shape, seed, scale=1.0):
     """(fp32 CPU tensor holding bf16-representable values, bf16 device tensor)."""
     x = seeded(shape, seed, scale).to(torch.bfloat16)
+    return x.float(), x.cuda()
+
+
+def f16_pair(shape, seed, scale=1.0):
+    """(fp32 CPU tensor holding fp16-representable values, fp16 device tensor)."""
+    x = seeded(shape, seed, scale).to(torch.float16)
     return x.float(), x.cuda()
 
 
@@ -52,3 +62,17 @@ def assert_f32_rel(got, ref, what="", tol=F32_REL):
     err = ((got[fin] - ref[fin]).abs() / ref[fin].abs().clamp_min(1.0)).max().item() \
         if fin.any() else 0.0
     assert err < tol, f"{what}: rel err {err:.3e}"
+
+
+def assert_f16_close(got, ref, what=""):
+    """fp16 result vs an fp32 reference: per element |got - ref| < max(5e-3, 2^-9 |ref|)
+    and rel-L2 < 2.5e-3."""
+    got = got.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    assert got.shape == ref.shape, f"{what}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
+    assert torch.isfinite(got).all(), f"{what}: non-finite values"
+    diff = (got - ref).abs()
+    over = (diff / torch.clamp(ref.abs() * 2.0 ** -9, min=F16_MAX_ABS)).max().item()
+    rl = rel_l2(got, ref)
+    assert over < 1 and rl < F16_REL_L2, \
+        f"{what}: max-abs {diff.max().item():.3e} ({over:.2f} of the bar) rel-L2 {rl:.3e}"

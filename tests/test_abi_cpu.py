@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 11
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 12
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -75,6 +75,16 @@ def test_host_validation_problem_fields():
     arr[0].mode = 9
     assert abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, 1, None) == abi.RMX_EINVAL
     assert b"mode" in abi.lib().rmx_last_error()
+
+
+def test_host_validation_dtype_and_merge_type():
+    assert _fwd(_layout(dtype=2)) == abi.RMX_EINVAL
+    assert b"element type" in abi.lib().rmx_last_error()
+    assert _fwd(_layout(dtype=abi.DTYPE_F16)) == abi.RMX_OK  # no problems: no launch
+    st = abi.i64_array((0, 0, 0))
+    assert abi.lib().rmx_lse_merge(16, 16, 16, 3, 16, 1, 1, 1, 8, st, st, st, st, 1, None) \
+        == abi.RMX_EINVAL
+    assert b"block type" in abi.lib().rmx_last_error()
 
 
 def test_host_validation_window_flag():
