@@ -28,13 +28,14 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 12 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 13 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
                               8: allocation-free Mamba2 correction bwd;
                               9: carried-in state h_in / dh_in of the linear scan;
                               10: L-parallel linear scan (workspace argument);
                               11: sliding windows, attention head_dim any multiple of 8
-                                  up to 128; 12: fp16 attention (layout dtype) */
+                                  up to 128; 12: fp16 attention (layout dtype);
+                              13: attention dropout */
 
 /* error codes */
 #define RMX_OK 0
@@ -50,6 +51,12 @@ extern "C" {
 #define RMX_MASK_FULL 0   /* every (q, k) pair attends */
 #define RMX_MASK_CAUSAL 1 /* bottom-right aligned causal: k <= q + (sk - sq) */
 #define RMX_MASK_DOC 2    /* q_doc[q] == k_doc[k] && k_gidx[k] <= q_gidx[q] */
+/* RMX_DROPOUT: with dropout_p > 0, element (b, h, q, k) of a problem (h the q head) is kept when
+ *   fmix32(bhmix ^ (q + drop_q0) * 0x85ebca77 ^ (k + drop_k0) * 0xc2b2ae3d) >= floor(p * 2^32),
+ *   bhmix = fmix32(drop_seed_lo ^ fmix32(drop_seed_hi ^ (b * hq + h) * 0x9e3779b9)),
+ * all arithmetic mod 2^32, fmix32 the MurmurHash3 32-bit finalizer; kept probabilities are
+ * scaled by 1 / (1 - p) and lse is the undropped one (the Dao flash-attention semantics).
+ * The backward must get the forward's layout seed and each problem's drop_q0 / drop_k0. */
 /* A problem's sliding window (has_window = 1) masks every pair further apart than
  * window_left: pos_q - pos_k > window_left, with the bottom-right aligned positions
  * pos_q = q + (sk - sq), pos_k = k (ring/kernels.py:68-72), or the global indices
@@ -85,6 +92,10 @@ typedef struct rmx_attn_layout {
   int32_t mask;                     /* RMX_MASK_* */
   int32_t dtype;                    /* RMX_DTYPE_*: the 16-bit tensors ("bf16" below) hold this
                                        type; accumulators, lse and delta stay fp32 */
+  float dropout_p;                  /* attention dropout probability in [0, 1); 0: none. The
+                                       mask is a hash of (drop_seed, batch, q head, query, key),
+                                       see RMX_DROPOUT below; RMX_MASK_FULL / _CAUSAL only */
+  uint32_t drop_seed_lo, drop_seed_hi;
   /* element strides (batch, seq, head) */
   int64_t q_sb, q_ss, q_sh;
   int64_t k_sb, k_ss, k_sh;
@@ -114,6 +125,7 @@ typedef struct rmx_fwd_problem {
   int32_t mode;          /* RMX_FWD_* */
   int32_t has_window;    /* 0: no window; 1: window_left bounds pos_q - pos_k (see above) */
   int32_t window_left;
+  int32_t drop_q0, drop_k0; /* dropout coordinates of the first query / key (RMX_DROPOUT) */
 } rmx_fwd_problem;
 
 /* One block-attention backward problem, using the GLOBAL (merged) out/lse. */
@@ -141,6 +153,7 @@ typedef struct rmx_bwd_problem {
   int32_t dkv_mode;      /* RMX_GRAD_* */
   int32_t has_window;    /* as in rmx_fwd_problem: the forward's window of the same block */
   int32_t window_left;
+  int32_t drop_q0, drop_k0; /* as in rmx_fwd_problem: the forward's dropout coordinates */
 } rmx_bwd_problem;
 
 int32_t rmx_abi_version(void);

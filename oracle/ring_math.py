@@ -14,14 +14,64 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 NEG_INF = float("-inf")
 
 
+# ---------------------------------------------------------------- dropout mask
+# The reference drops attention probabilities with torch's RNG (ring/kernels.py:74-75),
+# which no other implementation reproduces. The MI355X kernels draw a counter-based mask
+# instead: element (b, h, q, k) is kept when fmix32(bhmix ^ q C_Q ^ k C_K) >= floor(p 2^32)
+# (fmix32: the MurmurHash3 finalizer), with the same 1 / (1 - p) scaling of the kept
+# probabilities and the undropped lse. The functions below restate that mask, so the
+# dropped math of a given seed is checked exactly; its agreement with torch's dropout is
+# distributional only (keep rate, unbiasedness).
+DROP_Q, DROP_K, DROP_BH = 0x85EBCA77, 0xC2B2AE3D, 0x9E3779B9
+
+
+def fmix32(x):
+    """MurmurHash3's 32-bit finalizer on a numpy uint32 array."""
+    x = np.asarray(x, dtype=np.uint32)
+    with np.errstate(over="ignore"):
+        x = x ^ (x >> np.uint32(16))
+        x = x * np.uint32(0x85EBCA6B)
+        x = x ^ (x >> np.uint32(13))
+        x = x * np.uint32(0xC2B2AE35)
+        x = x ^ (x >> np.uint32(16))
+    return x
+
+
+def dropout_keep(seed, bh, q_pos, k_pos, p):
+    """Keep mask [len(q_pos), len(k_pos)] (bool) of the (batch, head) pair bh = b Hq + h:
+    fmix32(bhmix ^ q DROP_Q ^ k DROP_K) >= floor(p 2^32),
+    bhmix = fmix32(seed_lo ^ fmix32(seed_hi ^ bh DROP_BH)), arithmetic mod 2^32."""
+    seed = int(seed) & ((1 << 64) - 1)
+    lo, hi = np.uint32(seed & 0xFFFFFFFF), np.uint32(seed >> 32)
+    with np.errstate(over="ignore"):
+        bhmix = fmix32(lo ^ fmix32(hi ^ (np.uint32(bh) * np.uint32(DROP_BH))))
+        qt = np.asarray(q_pos, dtype=np.int64).astype(np.uint32) * np.uint32(DROP_Q)
+        kt = np.asarray(k_pos, dtype=np.int64).astype(np.uint32) * np.uint32(DROP_K)
+    u = fmix32(bhmix ^ qt[:, None] ^ kt[None, :])
+    thr = min(int(float(p) * 4294967296.0), 0xFFFFFFFF)
+    return u >= np.uint32(thr)
+
+
+def dropout_scale_mask(seed, b, hq, sq, sk, p, q0=0, k0=0):
+    """fp32 [b, hq, sq, sk]: 1 / (1 - p) where kept, 0 where dropped."""
+    keep = np.stack([np.stack([dropout_keep(seed, bi * hq + h, np.arange(sq) + q0,
+                                            np.arange(sk) + k0, p) for h in range(hq)])
+                     for bi in range(b)])
+    return torch.from_numpy(keep.astype(np.float32)) / (1.0 - float(p))
+
+
 # ---------------------------------------------------------------- blocks
-def math_block(q, k, v, *, causal, scaling, dropout=0.0, window=None):
-    """Explicit-softmax block (ring/kernels.py:52-78). q/k/v [b, s, h, d] -> (out, lse)."""
+def math_block(q, k, v, *, causal, scaling, dropout=0.0, window=None, drop_seed=None,
+               drop_q0=0, drop_k0=0):
+    """Explicit-softmax block (ring/kernels.py:52-78). q/k/v [b, s, h, d] -> (out, lse).
+    With ``dropout`` and ``drop_seed`` the probabilities are dropped by the hash mask of
+    that seed (coordinates offset by drop_q0 / drop_k0) instead of torch's RNG."""
     qt, kt, vt = (t.transpose(1, 2).float() for t in (q, k, v))
     if qt.shape[1] != kt.shape[1]:
         if qt.shape[1] % kt.shape[1]:
@@ -41,7 +91,10 @@ def math_block(q, k, v, *, causal, scaling, dropout=0.0, window=None):
         scores = scores.masked_fill(iq - ik > left, NEG_INF)
     lse = torch.logsumexp(scores, dim=-1)
     probs = torch.exp(scores - lse.unsqueeze(-1))
-    if dropout:
+    if dropout and drop_seed is not None:
+        b, hq = probs.shape[0], probs.shape[1]
+        probs = probs * dropout_scale_mask(drop_seed, b, hq, sq, sk, dropout, drop_q0, drop_k0)
+    elif dropout:
         probs = torch.nn.functional.dropout(probs, p=dropout)
     out = probs @ vt
     return out.transpose(1, 2).to(q.dtype), lse
@@ -405,12 +458,14 @@ def distflash_backward(d_outs, qs, ks, vs, outs, lses, *, scaling=None, cu_seqle
             [t.transpose(1, 2) for t in dv])
 
 
-def allgather_ring_forward(qs, ks, vs, *, causal=True, scaling=None, window=None):
+def allgather_ring_forward(qs, ks, vs, *, causal=True, scaling=None, window=None, dropout=0.0,
+                           drop_seed=None):
     """The gather ring (ring/loop.py:201-228): rank r attends the gathered K/V of ranks
     0..r (causal) or of every rank with ONE math_block call, whose bottom-right
     alignment places rank r's query i at position ``(end - 1) L + i`` against the
     gathered keys (``end`` = r + 1 causal, P otherwise); a window bounds that position
-    minus the key's global index. qs/ks/vs per-rank [b, H, L, d] -> per-rank out
+    minus the key's global index. With dropout and ``drop_seed``: the hash mask over
+    (global query r L + i, gathered key). qs/ks/vs per-rank [b, H, L, d] -> per-rank out
     [b, L, H, d] and lse [b, H, L]. Differentiable (torch autograd)."""
     world = len(qs)
     outs, lses = [], []
@@ -419,7 +474,9 @@ def allgather_ring_forward(qs, ks, vs, *, causal=True, scaling=None, window=None
         q = qs[r].transpose(1, 2)
         k = torch.cat([t.transpose(1, 2) for t in ks[:end]], dim=1)
         v = torch.cat([t.transpose(1, 2) for t in vs[:end]], dim=1)
-        o, lse = math_block(q, k, v, causal=causal, scaling=scaling, window=window)
+        L = q.shape[1]
+        o, lse = math_block(q, k, v, causal=causal, scaling=scaling, window=window,
+                            dropout=dropout, drop_seed=drop_seed, drop_q0=r * L)
         outs.append(o)
         lses.append(lse)
     return outs, lses

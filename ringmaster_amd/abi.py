@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
-ABI_VERSION = 12  # RMX_ABI_VERSION of include/ringmaster_amd.h
+ABI_VERSION = 13  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
@@ -53,6 +53,8 @@ class AttnLayout(ctypes.Structure):
     _fields_ = [
         ("batch", _i32), ("hq", _i32), ("hkv", _i32), ("head_dim", _i32),
         ("scale", ctypes.c_float), ("mask", _i32), ("dtype", _i32),
+        ("dropout_p", ctypes.c_float), ("drop_seed_lo", ctypes.c_uint32),
+        ("drop_seed_hi", ctypes.c_uint32),
         ("q_sb", _i64), ("q_ss", _i64), ("q_sh", _i64),
         ("k_sb", _i64), ("k_ss", _i64), ("k_sh", _i64),
         ("v_sb", _i64), ("v_ss", _i64), ("v_sh", _i64),
@@ -70,6 +72,7 @@ class FwdProblem(ctypes.Structure):
         ("acc_out", _vp), ("acc_lse", _vp),
         ("q_gidx", _vp), ("k_gidx", _vp), ("q_doc", _vp), ("k_doc", _vp),
         ("sq", _i32), ("sk", _i32), ("mode", _i32), ("has_window", _i32), ("window_left", _i32),
+        ("drop_q0", _i32), ("drop_k0", _i32),
     ]
 
 
@@ -79,7 +82,7 @@ class BwdProblem(ctypes.Structure):
         ("nlse", _vp), ("dq_acc", _vp), ("dq", _vp), ("dk_acc", _vp), ("dv_acc", _vp), ("dk", _vp), ("dv", _vp),
         ("q_gidx", _vp), ("k_gidx", _vp), ("q_doc", _vp), ("k_doc", _vp),
         ("sq", _i32), ("sk", _i32), ("dq_mode", _i32), ("dkv_mode", _i32),
-        ("has_window", _i32), ("window_left", _i32),
+        ("has_window", _i32), ("window_left", _i32), ("drop_q0", _i32), ("drop_k0", _i32),
     ]
 
 

@@ -28,6 +28,8 @@ struct BwdParams {
   rmx_bwd_problem P[RMX_MAX_BATCHED];  // in launch order (longest workgroups first)
   WgMapParams map;  // dQ: groups (batch, q head) x query tiles; dK/dV: (batch, kv head) x key tiles
   float scale_log2;
+  uint32_t drop_thr;  // dropout: keep when the element's hash >= drop_thr
+  float drop_scale;   // 1 / (1 - p)
 };
 
 // ---------------------------------------------------------------- delta
@@ -166,7 +168,7 @@ struct BwdTiles {
 // (swizzle folded in) plus a compile-time offset below 64 KiB, with no address
 // arithmetic in the loop. Tiles past the end are issued as zero-length loads,
 // which keeps every wait count static.
-template <int HD, int MASK, int DT>
+template <int HD, int MASK, int DT, bool DROP>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm) {
   using T = BwdTiles<HD>;
   constexpr int NW = 8, NT = NW * 64, BQ = 32 * NW, BK = 64;
@@ -217,6 +219,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
   // this lane's lowest key: key >= q + off - wl (document masks: global index >= qlo)
   const int qlo = mask == RMX_MASK_DOC ? (qvalid ? clamp_i32((int64_t)qg - wl) : 2147483647)
                                        : q + off - wl;
+  // dropout: this lane's query term of the mask hash (the forward's)
+  const uint32_t dq_term = DROP ? drop_bhmix(L, bb, head) ^ (uint32_t)(q + P.drop_q0) * kDropQ : 0u;
 
   const int qlast = (q0 + BQ < sq ? q0 + BQ : sq) - 1;
   const int nkt = (sk + BK - 1) / BK;
@@ -441,8 +445,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm
             v[i] = ok ? v[i] : 0.f;
           }
         }
+        if constexpr (DROP) {
+          // dS = P (M dP / (1 - p) - delta): dP of a dropped element is 0
+          const uint32_t kd = ((uint32_t)(k0 + 8 * hl + P.drop_k0) + 16 * kb2) * kDropK;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] *= dp[mb][b8 + i] - dlt;
+          for (int i = 0; i < 8; ++i) {
+            const float m = drop_keep(dq_term, kd + (uint32_t)i * kDropK, prm.drop_thr)
+                                ? prm.drop_scale : 0.f;
+            v[i] *= fmaf(dp[mb][b8 + i], m, -dlt);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] *= dp[mb][b8 + i] - dlt;
+        }
         dsb[kb2] = pack8t<DT>(v);
       }
 
@@ -531,7 +546,7 @@ struct DkdvCfg {
   static_assert(NS == 2 * NKB && NS == 4 * NDB, "phase shapes");
 };
 
-template <int HD, int MASK, int DT>
+template <int HD, int MASK, int DT, bool DROP>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams prm) {
   using C = DkdvCfg<HD>;
   constexpr int BQ = C::BQ, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB, NS = C::NS;
@@ -748,6 +763,26 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   const int khi = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg + wl) : key + wl - off;
   const int khi_first = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg_first + wl) : 0;
 
+  // dropout: the keep bits of a tile's 32 elements of this lane (bit 16 mb + r: query
+  // 32 mb + sig_row(hl, r) of the tile, key `key`), hashed as the forward does
+  const uint32_t dk_term = DROP ? (uint32_t)(key + P.drop_k0) * kDropK : 0u;
+  const uint32_t dq_hl = (uint32_t)(8 * hl) * kDropQ;
+  // bits [E0, E1) of the tile at query row qa of q head `hi` (of this kv head's group)
+  auto drop_bits = [&](uint32_t& mw, int qa, int hi, auto e0c, auto e1c) __attribute__((always_inline)) {
+    constexpr int E0 = decltype(e0c)::value, E1 = decltype(e1c)::value;
+    const uint32_t bk = drop_bhmix(L, bb, kvh * G + hi) ^ dk_term;
+    const uint32_t base = (uint32_t)(qa + P.drop_q0) * kDropQ + dq_hl;
+    [&]<int... E>(std::integer_sequence<int, E...>) __attribute__((always_inline)) {
+      (
+          [&] {
+            constexpr int e = E0 + E, mb = e >> 4, r = e & 15;
+            constexpr uint32_t qc = (uint32_t)(32 * mb + 16 * (r >> 3) + (r & 7)) * kDropQ;
+            if (drop_keep(bk, base + qc, prm.drop_thr)) mw |= 1u << e;
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, E1 - E0>{});
+  };
+
   // per-tile metadata in the accumulator / exponent layout: element r of half mb
   // belongs to query 32 mb + sig_row(hl, r), i.e. two runs of 8 queries
   auto load_rows = [&](const float* m, f32x16* dst) {
@@ -819,6 +854,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   doc_store(0);
 
   f32x16 dv[NDB], dk[NDB], s[2], dp[2], nl[2];
+  // dropout: delta of the tile's rows (the dP' accumulator then starts at 0, see pack_pair)
+  // and the keep bits of the current and the next tile
+  f32x16 dl[DROP ? 2 : 1];
+  uint32_t mw = 0, mw_next = 0;
   // register classes: S, P and dP' (read by the VALU) in VGPRs; the unit is built with
   // VGPR-form MFMAs, and the register allocator places the dV/dK accumulators
 #pragma unroll
@@ -862,7 +901,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32t<DT>(row_op(sQ[0], kb, mb), kreg[kb], s[mb]);
     pin_v(s);
     load_rows(sM[0], nl);
-    load_rows(sM[0] + BQ, dp);
+    if constexpr (DROP) {
+      load_rows(sM[0] + BQ, dl);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) dp[mb] = zero16();
+      drop_bits(mw, cur.qt * BQ, cur.hi, std::integral_constant<int, 0>{},
+                std::integral_constant<int, 32>{});
+    } else {
+      load_rows(sM[0] + BQ, dp);
+    }
     pin_v(dp);
     if (need_mask_of(cur.qt * BQ, 0)) {
       keep_branch();
@@ -873,11 +920,24 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   }
 
   // pack elements 2w, 2w + 1 of 8-row block blk (rows 32 (blk / 2) + sig_row(hl,
-  // 8 (blk % 2) + ..)) of x (times y when given) into word w of op
+  // 8 (blk % 2) + ..)) of x (times y when given) into word w of op. With dropout
+  // (keep scale m = M / (1 - p)): P^T packs P m, and (P dP')^T packs
+  // P (delta + m y) with y = -dO V^T, i.e. P (delta - M dP / (1 - p))
   auto pack_pair = [&](bf16x8& op, const f32x16* x, const f32x16* y, int blk, int w) {
     const int mb = blk >> 1, r = 8 * (blk & 1) + 2 * w;
     float v0 = x[mb][r], v1 = x[mb][r + 1];
-    if (y) {
+    if constexpr (DROP) {
+      const int e = 16 * mb + r;
+      const float m0 = (mw >> e) & 1u ? prm.drop_scale : 0.f;
+      const float m1 = (mw >> (e + 1)) & 1u ? prm.drop_scale : 0.f;
+      if (y) {
+        v0 *= fmaf(m0, y[mb][r], dl[mb][r]);
+        v1 *= fmaf(m1, y[mb][r + 1], dl[mb][r + 1]);
+      } else {
+        v0 *= m0;
+        v1 *= m1;
+      }
+    } else if (y) {
       v0 *= y[mb][r];
       v1 *= y[mb][r + 1];
     }
@@ -893,6 +953,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     constexpr int BN = (B + 1) % NB;
     if (j + 1 < ntile) doc_load(nx1);
     bf16x8 pt[4], dst[4];
+    int qa_next = 0;  // first query of tile j + 1 (set at the hand-over, read in phase 3)
     auto step = [&](auto Tc) __attribute__((always_inline)) {
       constexpr int T = decltype(Tc)::value;
       constexpr int ph = T / NS, t = T % NS;
@@ -911,7 +972,17 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
           if (i < 8)
             load_rows_part(sM[BN], nl, i);
           else
-            load_rows_part(sM[BN] + BQ, dp, i - 8);
+            load_rows_part(sM[BN] + BQ, DROP ? dl : dp, i - 8);
+        }
+        if constexpr (DROP) {
+          // dP' of tile j + 1 starts at 0; its keep bits, 32 / NS per step
+          if constexpr (t == 0) {
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) dp[mb] = zero16();
+            mw_next = 0;
+          }
+          drop_bits(mw_next, qa_next, cur.hi, std::integral_constant<int, 32 * t / NS>{},
+                    std::integral_constant<int, 32 * (t + 1) / NS>{});
         }
         if constexpr (t == NS - 1) pin_v(dp);
       }
@@ -978,7 +1049,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     if (j + 1 < ntile) doc_store(BN);
     wait_vm_barrier<2 * C::NDMA>();
     dma_tile((B + 3) % NB, nx3, j + 3 < ntile);
-    const int qa_next = nx1.qt * BQ;
+    qa_next = nx1.qt * BQ;
     cur = nx1;
     nx1 = nx2;
     nx2 = nx3;
@@ -992,6 +1063,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       keep_branch();
       apply_mask(qa_next, BN, s, nl);
     }
+    if constexpr (DROP) mw = mw_next;
   };
   for (int j = 0; j < ntile; j += NB) {
     tile(std::integral_constant<int, 0>{}, j);
@@ -1033,7 +1105,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   }
 }
 
-template <int HD, int DT>
+template <int HD, int DT, bool DROP>
 static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                                hipStream_t stream) {
   constexpr int BQ_DQ = 256, BKV = DkdvCfg<HD>::BKV;
@@ -1041,6 +1113,10 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
   pq.L = L;
   pk.L = L;
   pq.scale_log2 = pk.scale_log2 = L.scale * kLog2e;
+  drop_params(L.dropout_p, &pq.drop_thr, &pq.drop_scale);
+  pk.drop_thr = pq.drop_thr;
+  pk.drop_scale = pq.drop_scale;
+  if (DROP && L.mask == RMX_MASK_DOC) return hipErrorInvalidValue;  // refused by the host
   // problems with an empty side or a skipped gradient get no workgroups there;
   // the others run longest workgroups first (dQ: key tiles, dK/dV: query tiles x group)
   const int G = L.hq / L.hkv;
@@ -1075,22 +1151,22 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
   if (tk > 0) {
     const dim3 grid(tk);
     if (L.mask == RMX_MASK_CAUSAL)
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL, DT>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL, DT, DROP>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     else if (L.mask == RMX_MASK_DOC)
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_DOC, DT>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_DOC, DT, false>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     else
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_FULL, DT>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_FULL, DT, DROP>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (tq > 0) {
     const dim3 grid(tq);
     if (L.mask == RMX_MASK_CAUSAL)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_CAUSAL, DT>), grid, dim3(512), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_CAUSAL, DT, DROP>), grid, dim3(512), 0, stream, pq);
     else if (L.mask == RMX_MASK_DOC)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_DOC, DT>), grid, dim3(512), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_DOC, DT, false>), grid, dim3(512), 0, stream, pq);
     else
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_FULL, DT>), grid, dim3(512), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_FULL, DT, DROP>), grid, dim3(512), 0, stream, pq);
     return hipGetLastError();
   }
   return hipSuccess;
@@ -1098,11 +1174,19 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
 
 hipError_t launch_attn_bwd(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                            hipStream_t stream) {
-  if (L.dtype == RMX_DTYPE_F16)
-    return L.head_dim > 64 ? launch_bwd_t<128, RMX_DTYPE_F16>(L, probs, n, stream)
-                           : launch_bwd_t<64, RMX_DTYPE_F16>(L, probs, n, stream);
-  return L.head_dim > 64 ? launch_bwd_t<128, RMX_DTYPE_BF16>(L, probs, n, stream)
-                         : launch_bwd_t<64, RMX_DTYPE_BF16>(L, probs, n, stream);
+  const bool big = L.head_dim > 64, f16 = L.dtype == RMX_DTYPE_F16, drop = L.dropout_p > 0.f;
+  if (drop) {
+    if (f16)
+      return big ? launch_bwd_t<128, RMX_DTYPE_F16, true>(L, probs, n, stream)
+                 : launch_bwd_t<64, RMX_DTYPE_F16, true>(L, probs, n, stream);
+    return big ? launch_bwd_t<128, RMX_DTYPE_BF16, true>(L, probs, n, stream)
+               : launch_bwd_t<64, RMX_DTYPE_BF16, true>(L, probs, n, stream);
+  }
+  if (f16)
+    return big ? launch_bwd_t<128, RMX_DTYPE_F16, false>(L, probs, n, stream)
+               : launch_bwd_t<64, RMX_DTYPE_F16, false>(L, probs, n, stream);
+  return big ? launch_bwd_t<128, RMX_DTYPE_BF16, false>(L, probs, n, stream)
+             : launch_bwd_t<64, RMX_DTYPE_BF16, false>(L, probs, n, stream);
 }
 
 }  // namespace rmx

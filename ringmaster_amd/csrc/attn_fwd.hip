@@ -45,6 +45,8 @@ struct FwdParams {
   rmx_fwd_problem P[RMX_MAX_BATCHED];  // in launch order (longest workgroups first)
   WgMapParams map;                     // groups = (batch, q head), tiles = query tiles
   float scale_log2;
+  uint32_t drop_thr;  // dropout: keep when the element's hash >= drop_thr
+  float drop_scale;   // 1 / (1 - p)
 };
 
 template <int HD>
@@ -66,7 +68,7 @@ struct FwdCfg {
 
 constexpr float kRescaleSlack = 8.0f;  // log2 units: P <= 2^8 between rescales
 
-template <int HD, int MASK, int DT>
+template <int HD, int MASK, int DT, bool DROP>
 __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   using C = FwdCfg<HD>;
   constexpr int BK = C::BK, MB = C::MB, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB;
@@ -109,6 +111,12 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   const int off = sk - sq;
   const int qlo = mask == RMX_MASK_DOC ? (q < sq ? clamp_i32((int64_t)qg - wl) : 2147483647)
                                        : q + off - wl;
+  // dropout: this lane's query term of the mask hash, and the key offset of the problem
+  uint32_t dq_term = 0, dk_off = 0;
+  if constexpr (DROP) {
+    dq_term = drop_bhmix(L, bb, head) ^ (uint32_t)(q + P.drop_q0) * kDropQ;
+    dk_off = (uint32_t)P.drop_k0;
+  }
 
   // ---- key tile range of the workgroup
   const int qlast = (q0 + C::BQ < sq ? q0 + C::BQ : sq) - 1;
@@ -380,6 +388,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
     const int kbi = (j + 1) & 3;
     const bool live = j + 1 < ntile;
     const float mbase = (m_run == kNegInf) ? 0.f : m_run;
+    // dropout: key term of this lane's first key of tile j (keys kd0 + 16 kb2 + 2 w + e)
+    const uint32_t kd0 = DROP ? ((uint32_t)((kt_begin + j) * BK + 8 * hl) + dk_off) * kDropK : 0u;
     u32x4 pw[2 * MB];   // P_j packed to bf16, one u32x4 per 16-key block
     float rsp[2 * MB];  // partial row sums per 16-key block
 #pragma unroll
@@ -389,8 +399,16 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
       constexpr int kb2 = pi / 4, w = pi % 4;
       const float x0 = fast_exp2(fmaf(sc[kb2 >> 1][8 * (kb2 & 1) + 2 * w], c, -mbase));
       const float x1 = fast_exp2(fmaf(sc[kb2 >> 1][8 * (kb2 & 1) + 2 * w + 1], c, -mbase));
-      float rs = rsp[kb2] + (x0 + x1);
-      uint32_t pk = cvt_pk<DT>(x0, x1);
+      float rs = rsp[kb2] + (x0 + x1);  // the softmax normaliser: undropped
+      uint32_t pk;
+      if constexpr (DROP) {
+        constexpr uint32_t c0 = (uint32_t)(16 * kb2 + 2 * w) * kDropK, c1 = c0 + kDropK;
+        const float y0 = drop_keep(dq_term, kd0 + c0, prm.drop_thr) ? x0 * prm.drop_scale : 0.f;
+        const float y1 = drop_keep(dq_term, kd0 + c1, prm.drop_thr) ? x1 * prm.drop_scale : 0.f;
+        pk = cvt_pk<DT>(y0, y1);
+      } else {
+        pk = cvt_pk<DT>(x0, x1);
+      }
       // pin the results here: otherwise the compiler sinks the exponentials to
       // their first use (after the region) and the step has no VALU work
       asm volatile("" : "+v"(rs), "+v"(pk));
@@ -546,13 +564,14 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   }
 }
 
-template <int HD, int DT>
+template <int HD, int DT, bool DROP>
 static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                                hipStream_t stream) {
   constexpr int BQ = FwdCfg<HD>::BQ;
   FwdParams prm;
   prm.L = L;
   prm.scale_log2 = L.scale * kLog2e;
+  drop_params(L.dropout_p, &prm.drop_thr, &prm.drop_scale);
   // longest workgroups (most key tiles) first
   long long cost[RMX_MAX_BATCHED];
   int order[RMX_MAX_BATCHED], groups[RMX_MAX_BATCHED], ntile[RMX_MAX_BATCHED];
@@ -566,24 +585,34 @@ static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* 
   const int grid = plan_workgroups(prm.map, n, groups, ntile);
   if (grid == 0) return hipSuccess;
   if (L.mask == RMX_MASK_CAUSAL)
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_CAUSAL, DT>), dim3(grid),
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_CAUSAL, DT, DROP>), dim3(grid),
                        dim3(FwdCfg<HD>::NT), 0, stream, prm);
+  else if (L.mask == RMX_MASK_DOC && DROP)  // not instantiated (refused by the host)
+    return hipErrorInvalidValue;
   else if (L.mask == RMX_MASK_DOC)
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_DOC, DT>), dim3(grid), dim3(FwdCfg<HD>::NT),
-                       0, stream, prm);
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_DOC, DT, false>), dim3(grid),
+                       dim3(FwdCfg<HD>::NT), 0, stream, prm);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_FULL, DT>), dim3(grid),
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_FULL, DT, DROP>), dim3(grid),
                        dim3(FwdCfg<HD>::NT), 0, stream, prm);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_fwd(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                            hipStream_t stream) {
-  if (L.dtype == RMX_DTYPE_F16)
-    return L.head_dim > 64 ? launch_fwd_t<128, RMX_DTYPE_F16>(L, probs, n, stream)
-                           : launch_fwd_t<64, RMX_DTYPE_F16>(L, probs, n, stream);
-  return L.head_dim > 64 ? launch_fwd_t<128, RMX_DTYPE_BF16>(L, probs, n, stream)
-                         : launch_fwd_t<64, RMX_DTYPE_BF16>(L, probs, n, stream);
+  const bool big = L.head_dim > 64, f16 = L.dtype == RMX_DTYPE_F16, drop = L.dropout_p > 0.f;
+  if (drop) {
+    if (f16)
+      return big ? launch_fwd_t<128, RMX_DTYPE_F16, true>(L, probs, n, stream)
+                 : launch_fwd_t<64, RMX_DTYPE_F16, true>(L, probs, n, stream);
+    return big ? launch_fwd_t<128, RMX_DTYPE_BF16, true>(L, probs, n, stream)
+               : launch_fwd_t<64, RMX_DTYPE_BF16, true>(L, probs, n, stream);
+  }
+  if (f16)
+    return big ? launch_fwd_t<128, RMX_DTYPE_F16, false>(L, probs, n, stream)
+               : launch_fwd_t<64, RMX_DTYPE_F16, false>(L, probs, n, stream);
+  return big ? launch_fwd_t<128, RMX_DTYPE_BF16, false>(L, probs, n, stream)
+             : launch_fwd_t<64, RMX_DTYPE_BF16, false>(L, probs, n, stream);
 }
 
 }  // namespace rmx

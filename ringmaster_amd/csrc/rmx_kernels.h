@@ -187,6 +187,46 @@ __device__ __forceinline__ bf16x8 pack8t(const float* v) {
   return __builtin_bit_cast(bf16x8, u);
 }
 
+// ---------------------------------------------------------------------------
+// Attention dropout. Element (batch b, q head h, query q, key k) of a call with
+// dropout is kept when
+//   fmix32(bhmix ^ (q + q0) * kDropQ ^ (k + k0) * kDropK) >= threshold,
+//   bhmix = fmix32(seed_lo ^ fmix32(seed_hi ^ (b * hq + h) * kDropBH)),
+// with fmix32 the MurmurHash3 finalizer, threshold = floor(p 2^32) and (q0, k0) the
+// problem's coordinate offsets (a ring block's place in the gathered sequence).
+// Kept probabilities are scaled by 1 / (1 - p); lse is that of the undropped scores.
+// Every element is its own counter, so each kernel evaluates the mask in whatever
+// lane layout it holds the scores in, and the forward and both backward kernels
+// agree on it bit for bit.
+constexpr uint32_t kDropQ = 0x85ebca77u, kDropK = 0xc2b2ae3du, kDropBH = 0x9e3779b9u;
+__device__ __forceinline__ uint32_t fmix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x85ebca6bu;
+  x ^= x >> 13;
+  x *= 0xc2b2ae35u;
+  x ^= x >> 16;
+  return x;
+}
+__device__ __forceinline__ uint32_t drop_bhmix(const rmx_attn_layout& L, int bb, int head) {
+  return fmix32(L.drop_seed_lo ^ fmix32(L.drop_seed_hi ^ (uint32_t)(bb * L.hq + head) * kDropBH));
+}
+// qterm = bhmix ^ (q + q0) * kDropQ, kterm = (k + k0) * kDropK
+__device__ __forceinline__ bool drop_keep(uint32_t qterm, uint32_t kterm, uint32_t thr) {
+  return fmix32(qterm ^ kterm) >= thr;
+}
+
+// Host side: the keep threshold floor(p 2^32) and the scale 1 / (1 - p) of dropout p.
+inline void drop_params(float p, uint32_t* thr, float* scale) {
+  if (!(p > 0.f)) {
+    *thr = 0u;
+    *scale = 1.f;
+    return;
+  }
+  const double t = (double)p * 4294967296.0;
+  *thr = t >= 4294967295.0 ? 4294967295u : (uint32_t)t;
+  *scale = (float)(1.0 / (1.0 - (double)p));
+}
+
 // Host side: order[] = problem indices sorted by cost[] descending (stable).
 inline void order_by_cost(int n, const long long* cost, int* order) {
   for (int i = 0; i < n; ++i) order[i] = i;

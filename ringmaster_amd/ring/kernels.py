@@ -7,8 +7,10 @@ fp32)``, q/k/v ``[b, s, h, d]``, GQA by ``kv_head = q_head // (hq/hkv)``, causal
 bottom-right aligned (ring/kernels.py:64-67), a sliding window ``(left, right)``
 masking ``pos_q - pos_k > left`` on the same bottom-right aligned positions
 (ring/kernels.py:68-72; ``right`` is not used, as there), head dims that are
-multiples of 8 up to 128, bf16 or fp16. It is autograd-aware like ``hf_kernels``/``math``;
-the lse output is not differentiable (as with flash).
+multiples of 8 up to 128, bf16 or fp16, and attention dropout (the Dao semantics: kept
+probabilities scaled by 1 / (1 - p), lse undropped; the mask is the kernels' hash of
+(seed, batch, head, query, key), so the backward replays it exactly). It is autograd-aware
+like ``hf_kernels``/``math``; the lse output is not differentiable (as with flash).
 
 ``flash_ops()`` returns ``(fwd, bwd)`` with the positional signatures of the Dao
 low-level ops that the ring schedules call (ring/p2p_attn.py:27-62,
@@ -40,13 +42,19 @@ def _validate(q, k, v, dropout, window, softcap=0.0, alibi=None):
     d = q.shape[-1]
     if d % 8 or d > 128 or k.shape[-1] != d or v.shape[-1] != d:
         raise NotImplementedError(f"head_dim {d} is not supported (a multiple of 8, at most 128)")
-    if dropout:
-        raise NotImplementedError("mi355x_hip blocks do not implement attention dropout")
+    if not 0.0 <= float(dropout) < 1.0:
+        raise ValueError(f"dropout must lie in [0, 1) (got {dropout})")
     if softcap:
         raise NotImplementedError("mi355x_hip blocks do not implement softcap")
     if alibi is not None:
         raise NotImplementedError("mi355x_hip blocks do not implement ALiBi")
     return window_left(window)
+
+
+def new_dropout_seed() -> int:
+    """A 64-bit dropout seed from torch's default CPU generator (reproducible under
+    ``torch.manual_seed``; no device synchronization)."""
+    return int(torch.randint(-(1 << 63), (1 << 63) - 1, (1,), dtype=torch.int64)) & ((1 << 64) - 1)
 
 
 def window_left(window):
@@ -71,22 +79,24 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
-def block_forward(q, k, v, scale: float, causal: bool, keep_f32: bool = False, window=None):
+def block_forward(q, k, v, scale: float, causal: bool, keep_f32: bool = False, window=None,
+                  dropout=None):
     """(out [b, sq, hq, d] in q's dtype, lse fp32 [b, hq, sq]) of one block; with ``keep_f32`` also
     the fp32 out (what the backward's delta is computed from). ``window``: bound on
-    ``pos_q - pos_k`` (bottom-right aligned positions) or None."""
+    ``pos_q - pos_k`` (bottom-right aligned positions) or None; ``dropout``: None or
+    (p, seed)."""
     b, sq, hq, d = q.shape
     out = torch.empty((b, sq, hq, d), dtype=q.dtype, device=q.device)
     lse = torch.empty((b, hq, sq), dtype=torch.float32, device=q.device)
     out32 = torch.empty((b, sq, hq, d), dtype=torch.float32, device=q.device) if keep_f32 else None
     ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_WRITE, out=out, lse=lse,
                              acc_out=out32, window=window)],
-                 scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL)
+                 scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL, dropout=dropout)
     return (out, lse, out32) if keep_f32 else (out, lse)
 
 
 def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None, dk=None, dv=None,
-                   out_f32=None, window=None):
+                   out_f32=None, window=None, dropout=None):
     """dq, dk, dv (q's dtype) of one block using the given (global) out/lse; returns delta too.
     ``out_f32`` (the forward's fp32 out), when given, is what delta = rowsum(dout * out) reads;
     otherwise the 16-bit ``out`` is used, as a Dao-style backward does."""
@@ -107,7 +117,7 @@ def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None,
     ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta, nlse=nlse,
                              dq_mode=abi.GRAD_WRITE_BF16, dkv_mode=abi.GRAD_WRITE_BF16,
                              dq=dq_t, dk=dk_t, dv=dv_t, window=window)],
-                 scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL)
+                 scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL, dropout=dropout)
     for dst, src in ((dq, dq_t), (dk, dk_t), (dv, dv_t)):
         if dst is not None and dst is not src:
             dst.copy_(src)
@@ -117,11 +127,12 @@ def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None,
 
 class _HipBlockAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, causal, scale, window):
+    def forward(ctx, q, k, v, causal, scale, window, dropout):
         q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-        out, lse, out32 = block_forward(q, k, v, scale, causal, keep_f32=True, window=window)
+        out, lse, out32 = block_forward(q, k, v, scale, causal, keep_f32=True, window=window,
+                                        dropout=dropout)
         ctx.save_for_backward(q, k, v, out, lse, out32)
-        ctx.causal, ctx.scale, ctx.window = causal, scale, window
+        ctx.causal, ctx.scale, ctx.window, ctx.dropout = causal, scale, window, dropout
         ctx.mark_non_differentiable(lse)
         return out, lse
 
@@ -129,16 +140,23 @@ class _HipBlockAttention(torch.autograd.Function):
     def backward(ctx, dout, _dlse):
         q, k, v, out, lse, out32 = ctx.saved_tensors
         dq, dk, dv, _ = block_backward(_kernel_ready(dout), q, k, v, out, lse, ctx.scale,
-                                       ctx.causal, out_f32=out32, window=ctx.window)
-        return dq, dk, dv, None, None, None
+                                       ctx.causal, out_f32=out32, window=ctx.window,
+                                       dropout=ctx.dropout)
+        return dq, dk, dv, None, None, None, None
 
 
 def mi355x_hip_block(q, k, v, *, causal, scaling, dropout=0.0, attn_implementation=None,
-                     window=None):
-    """q/k/v: [b, s, h, d] bf16 or fp16 on the MI355X. Returns (out [b,s,h,d], lse [b,h,s])."""
+                     window=None, dropout_seed=None):
+    """q/k/v: [b, s, h, d] bf16 or fp16 on the MI355X. Returns (out [b,s,h,d], lse [b,h,s]).
+    ``dropout`` > 0 drops attention probabilities with the kernels' hash mask, seeded by
+    ``dropout_seed`` (default: drawn from torch's CPU generator); the backward replays the
+    same mask."""
     left = _validate(q, k, v, dropout, window)
     scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
-    return _HipBlockAttention.apply(q, k, v, bool(causal), float(scale), left)
+    drop = None
+    if dropout:
+        drop = (float(dropout), new_dropout_seed() if dropout_seed is None else int(dropout_seed))
+    return _HipBlockAttention.apply(q, k, v, bool(causal), float(scale), left, drop)
 
 
 PROVIDERS = {
@@ -154,9 +172,16 @@ def _flash_attn_forward(q, k, v, dropout_p, softmax_scale, causal, window_size_l
     left = _dao_window(window_size_left, window_size_right, causal)
     if return_softmax:
         raise NotImplementedError("return_softmax is not supported")
+    rng_state, drop = None, None
+    if dropout_p:
+        seed = new_dropout_seed()
+        drop = (float(dropout_p), seed)
+        # the Dao ops' rng_state: the seed (as the signed int64 of its 64 bits) and an offset
+        rng_state = torch.tensor([seed - (1 << 64) if seed >= (1 << 63) else seed, 0],
+                                 dtype=torch.int64)
     out, lse = block_forward(_kernel_ready(q), _kernel_ready(k), _kernel_ready(v),
-                             float(softmax_scale), bool(causal), window=left)
-    return out, lse, None, None
+                             float(softmax_scale), bool(causal), window=left, dropout=drop)
+    return out, lse, None, rng_state
 
 
 def _flash_attn_backward(dout, q, k, v, out, lse, dq, dk, dv, dropout_p, softmax_scale, causal,
@@ -164,9 +189,15 @@ def _flash_attn_backward(dout, q, k, v, out, lse, dq, dk, dv, dropout_p, softmax
                          alibi_slopes=None, deterministic=False, rng_state=None):
     _validate(q, k, v, dropout_p, None, softcap, alibi_slopes)
     left = _dao_window(window_size_left, window_size_right, causal)
+    drop = None
+    if dropout_p:
+        if rng_state is None:
+            raise ValueError("a backward with dropout needs the forward's rng_state")
+        drop = (float(dropout_p), int(torch.as_tensor(rng_state).flatten()[0]) & ((1 << 64) - 1))
     _, _, _, delta = block_backward(_kernel_ready(dout), _kernel_ready(q), _kernel_ready(k),
                                     _kernel_ready(v), _kernel_ready(out), lse,
-                                    float(softmax_scale), bool(causal), dq, dk, dv, window=left)
+                                    float(softmax_scale), bool(causal), dq, dk, dv, window=left,
+                                    dropout=drop)
     return dq, dk, dv, delta
 
 

@@ -17,14 +17,15 @@ Sliding windows (the gather ring and the packed ring: ring/loop.py:185-186,201-2
 keep the reference's positions: the gather ring's single block call aligns rank r's
 queries bottom-right against the gathered keys, which for a causal ring is the global
 position ``r L + i`` and for a non-causal ring (all P blocks gathered) ``(P - 1) L + i``;
-the packed ring compares global indices.
+the packed ring compares global indices. Dropout in the gather ring draws one mask over
+(global query, gathered key) pairs per call; its blocks take their coordinates from it.
 """
 
 from __future__ import annotations
 
 import torch
 
-from ringmaster_amd.ring.kernels import PROVIDERS, window_left
+from ringmaster_amd.ring.kernels import PROVIDERS, new_dropout_seed, window_left
 from ringmaster_amd.ring.p2p_attn import contiguous_ring
 from ringmaster_amd.ring.zigzag import doc_for
 
@@ -52,15 +53,16 @@ def ring_attention(q, k, v, *, group=None, causal: bool, scaling=None, dropout: 
                        attn_implementation=attn_implementation, window=window)
         return out.unsqueeze(0)
     if _method(rotate_method) == "allgather":
-        if dropout:
-            raise NotImplementedError("dropout is not supported")
+        if not 0.0 <= float(dropout) < 1.0:
+            raise ValueError(f"dropout must lie in [0, 1) (got {dropout})")
+        drop = (float(dropout), new_dropout_seed()) if dropout else None
         left = window_left(window)
         P, L = q.shape[0], q.shape[3]
         bounds = None
         if left is not None:  # bottom-right aligned against the gathered keys
             bounds = [left if causal else left - (P - 1 - r) * L for r in range(P)]
         return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer,
-                               window=bounds)
+                               window=bounds, dropout=drop)
     if dropout or window is not None or attn_implementation not in ("flash_attention_2", "math"):
         raise ValueError("P2P Ring requires FA2, zero dropout, and no sliding window")
     return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer)
@@ -74,7 +76,7 @@ def varlen_ring_attention(q, k, v, *, group=None, scaling, cu_seqlens, causal=Tr
     if group is not None:
         raise ValueError("the emulated ring takes the ranks on the leading axis, not a group")
     if dropout:
-        raise NotImplementedError("dropout is not supported")
+        raise NotImplementedError("dropout with document masks is not implemented")
     if not causal:
         raise NotImplementedError("packed (document-masked) blocks are causal in this build")
     if not isinstance(cu_seqlens, torch.Tensor):

@@ -33,6 +33,8 @@ class FwdJob:
     q_doc: torch.Tensor | None = None
     k_doc: torch.Tensor | None = None
     window: int | None = None  # bound on pos_q - pos_k (global indices with document masks)
+    drop_q0: int = 0  # dropout coordinates of the first query / key
+    drop_k0: int = 0
 
 
 @dataclasses.dataclass
@@ -57,13 +59,31 @@ class BwdJob:
     q_doc: torch.Tensor | None = None
     k_doc: torch.Tensor | None = None
     window: int | None = None
+    drop_q0: int = 0
+    drop_k0: int = 0
 
 
-def _set_window(p, window):
-    if window is not None:
-        if not -(1 << 31) <= int(window) < (1 << 31):
-            raise ValueError(f"window bound {window} outside int32")
-        p.has_window, p.window_left = 1, int(window)
+def _i32_field(v, what):
+    v = int(v)
+    if not -(1 << 31) <= v < (1 << 31):
+        raise ValueError(f"{what} {v} outside int32")
+    return v
+
+
+def _set_problem_extras(p, job):
+    if job.window is not None:
+        p.has_window, p.window_left = 1, _i32_field(job.window, "window bound")
+    p.drop_q0 = _i32_field(job.drop_q0, "dropout query offset")
+    p.drop_k0 = _i32_field(job.drop_k0, "dropout key offset")
+
+
+def _set_dropout(lay, dropout):
+    """``dropout``: None or (p, seed), seed a 64-bit integer."""
+    if dropout is None or not dropout[0]:
+        return
+    p, seed = float(dropout[0]), int(dropout[1]) & ((1 << 64) - 1)
+    lay.dropout_p = p
+    lay.drop_seed_lo, lay.drop_seed_hi = seed & 0xFFFFFFFF, seed >> 32
 
 
 _H = None  # the call's 16-bit element type (bf16 or fp16), the dtype of q
@@ -147,8 +167,9 @@ def _int32(t):
     return t.data_ptr()
 
 
-def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int) -> None:
-    """Launch the batched block forward (rmx_attn_fwd) for ``jobs``."""
+def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int, dropout=None) -> None:
+    """Launch the batched block forward (rmx_attn_fwd) for ``jobs``; ``dropout`` is None or
+    (p, seed)."""
     if not jobs:
         return
     q0, k0 = jobs[0].q, jobs[0].k
@@ -156,6 +177,7 @@ def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int) -> None:
     for j in jobs:
         _check_shapes(j.q, j.k, j.v, batch, hq, hkv, d)
     lay = _fill_layout(jobs, batch, hq, hkv, d, scale, mask)
+    _set_dropout(lay, dropout)
     arr = (abi.FwdProblem * len(jobs))()
     for i, j in enumerate(jobs):
         p = arr[i]
@@ -165,7 +187,7 @@ def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int) -> None:
         p.q_gidx, p.k_gidx = _int32(j.q_gidx), _int32(j.k_gidx)
         p.q_doc, p.k_doc = _int32(j.q_doc), _int32(j.k_doc)
         p.sq, p.sk, p.mode = j.q.shape[1], j.k.shape[1], j.mode
-        _set_window(p, j.window)
+        _set_problem_extras(p, j)
     abi.check(abi.lib().rmx_attn_fwd(ctypes.byref(lay), arr, len(jobs), abi.stream_of(q0)))
 
 
@@ -196,8 +218,9 @@ def attn_bwd_delta(out: torch.Tensor, dout: torch.Tensor, delta: torch.Tensor, h
                                            abi.ptr(nlse), sq, abi.stream_of(dout)))
 
 
-def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int) -> None:
-    """Launch the batched block backward (rmx_attn_bwd) for ``jobs``."""
+def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int, dropout=None) -> None:
+    """Launch the batched block backward (rmx_attn_bwd) for ``jobs``; ``dropout`` must be the
+    forward's (p, seed) and each job the forward's dropout offsets."""
     if not jobs:
         return
     q0, k0 = jobs[0].q, jobs[0].k
@@ -205,6 +228,7 @@ def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int) -> None:
     for j in jobs:
         _check_shapes(j.q, j.k, j.v, batch, hq, hkv, d)
     lay = _fill_layout(jobs, batch, hq, hkv, d, scale, mask)
+    _set_dropout(lay, dropout)
     arr = (abi.BwdProblem * len(jobs))()
     for i, j in enumerate(jobs):
         p = arr[i]
@@ -217,5 +241,5 @@ def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int) -> None:
         p.q_doc, p.k_doc = _int32(j.q_doc), _int32(j.k_doc)
         p.sq, p.sk = j.q.shape[1], j.k.shape[1]
         p.dq_mode, p.dkv_mode = j.dq_mode, j.dkv_mode
-        _set_window(p, j.window)
+        _set_problem_extras(p, j)
     abi.check(abi.lib().rmx_attn_bwd(ctypes.byref(lay), arr, len(jobs), abi.stream_of(q0)))

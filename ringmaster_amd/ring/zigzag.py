@@ -87,7 +87,8 @@ class _Ctx:
     or "distflash" (contiguous chunks, DistFlash's helper / owner work placement); the
     zigzag and DistFlash rings are causal only."""
 
-    def __init__(self, q, k, scale, doc, layout="zigzag", causal=True, window=None):
+    def __init__(self, q, k, scale, doc, layout="zigzag", causal=True, window=None,
+                 dropout=None):
         self.P, self.b, self.hq, self.L, self.d = q.shape
         self.hkv = k.shape[2]
         self.half = self.L // 2
@@ -95,6 +96,9 @@ class _Ctx:
         self.doc = doc
         self.layout, self.causal = layout, causal
         self.window = None if window is None else [int(w) for w in window]
+        self.dropout = dropout  # None or (p, seed): one mask over (rank's query, gathered key)
+        if dropout is not None and (layout == "zigzag" or doc is not None):
+            raise NotImplementedError("dropout runs on dense contiguous shards")
         if self.window is not None:
             if len(self.window) != self.P:
                 raise ValueError("the window takes one bound per rank")
@@ -132,6 +136,11 @@ class _Ctx:
         sq, sk = bl.q_hi - bl.q_lo, bl.k_hi - bl.k_lo
         shift = (bl.rank * self.L + bl.q_lo) - (bl.kv_rank * self.L + bl.k_lo) - (sk - sq)
         return w - shift
+
+    def block_drop(self, bl):
+        """Dropout coordinates of block ``bl``: the global index of its first query row and of
+        its first key (contiguous chunks), so every block of a ring draws from one mask."""
+        return bl.rank * self.L + bl.q_lo, bl.kv_rank * self.L + bl.k_lo
 
     def idx(self, rank, lo, hi):
         return None if self.gidx is None else self.gidx[rank, lo:hi]
@@ -197,7 +206,8 @@ def _only(blocks, only_ranks):
 
 
 def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=None,
-                 layout: str = "zigzag", causal: bool = True, only_ranks=None, window=None):
+                 layout: str = "zigzag", causal: bool = True, only_ranks=None, window=None,
+                 dropout=None):
     """Emulated ring forward (zigzag or contiguous layout). q/k/v: [P, b, H, L, d] bf16
     (interface layout per rank).
     Returns (out [P, b, L, H, d] bf16, lse [P, b, H, L] fp32, out32 [P, b, L, H, d] fp32):
@@ -209,7 +219,7 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
     computed (per-rank timing). ``window`` (contiguous layouts or document masks): one
     bound per rank on the global ``pos_q - pos_k`` of its queries."""
     timer = timer or _NO_TIMER
-    c = _Ctx(q, k, scale, doc, layout, causal, window)
+    c = _Ctx(q, k, scale, doc, layout, causal, window, dropout)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)  # [P, b, L, H, d] views
     dev = q.device
     out = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=q.dtype, device=dev)
@@ -231,22 +241,22 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
                 acc_lse=None if acc_lse is None else acc_lse[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
                 q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi),
-                window=c.block_window(bl)))
+                window=c.block_window(bl), **dict(zip(("drop_q0", "drop_k0"), c.block_drop(bl)))))
         with timer("attn_fwd"):
-            ops.attn_fwd(jobs, scale=scale, mask=c.mask(s))
+            ops.attn_fwd(jobs, scale=scale, mask=c.mask(s), dropout=c.dropout)
     return out, lse, acc
 
 
 def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | None = None,
                   timer=None, layout: str = "zigzag", causal: bool = True, only_ranks=None,
-                  window=None):
+                  window=None, dropout=None):
     """Reverse-ring backward with the global out/lse. dout: [P, b, L, H, d] bf16; out: the
     global out, fp32 (the forward's ``out32``) or bf16, [P, b, L, H, d].
     Returns fp32 (dq [P, b, L, Hq, d], dk, dv [P, b, L, Hkv, d]). Each step launches the
     KV-major dK/dV kernel and the Q-major dQ kernel over all ranks (``only_ranks``: over
     those ranks only, as in :func:`ring_forward`; the gradients are then partial)."""
     timer = timer or _NO_TIMER
-    c = _Ctx(q, k, scale, doc, layout, causal, window)
+    c = _Ctx(q, k, scale, doc, layout, causal, window, dropout)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)
     dev = q.device
     if not dout.is_contiguous():
@@ -276,15 +286,15 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
                 lse=lse[r][:, :, qs], delta=delta[r][:, :, qs], nlse=nlse[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
                 q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi),
-                window=c.block_window(bl))
+                window=c.block_window(bl), **dict(zip(("drop_q0", "drop_k0"), c.block_drop(bl))))
             kv_jobs.append(ops.BwdJob(dq_mode=abi.GRAD_NONE, dkv_mode=mode,
                                       dk_acc=dk[kr][:, ks], dv_acc=dv[kr][:, ks], **common))
             q_jobs.append(ops.BwdJob(dq_mode=mode, dkv_mode=abi.GRAD_NONE,
                                      dq_acc=dq[r][:, qs], **common))
         with timer("attn_bwd_dkdv"):
-            ops.attn_bwd(kv_jobs, scale=scale, mask=c.mask(s))
+            ops.attn_bwd(kv_jobs, scale=scale, mask=c.mask(s), dropout=c.dropout)
         with timer("attn_bwd_dq"):
-            ops.attn_bwd(q_jobs, scale=scale, mask=c.mask(s))
+            ops.attn_bwd(q_jobs, scale=scale, mask=c.mask(s), dropout=c.dropout)
     return dq, dk, dv
 
 
@@ -292,21 +302,22 @@ class EmulatedRing(torch.autograd.Function):
     """The emulated ring (zigzag or contiguous layout) with its reverse-ring backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, doc, timer, layout, causal, window=None):
-        out, lse, out32 = ring_forward(q, k, v, scale, doc, timer, layout, causal, window=window)
+    def forward(ctx, q, k, v, scale, doc, timer, layout, causal, window=None, dropout=None):
+        out, lse, out32 = ring_forward(q, k, v, scale, doc, timer, layout, causal, window=window,
+                                       dropout=dropout)
         ctx.save_for_backward(q, k, v, out32, lse)
         ctx.scale, ctx.doc, ctx.timer = scale, doc, timer
-        ctx.layout, ctx.causal, ctx.window = layout, causal, window
+        ctx.layout, ctx.causal, ctx.window, ctx.dropout = layout, causal, window, dropout
         return out
 
     @staticmethod
     def backward(ctx, d_out):
         q, k, v, out32, lse = ctx.saved_tensors
         dq, dk, dv = ring_backward(d_out, q, k, v, out32, lse, ctx.scale, ctx.doc, ctx.timer,
-                                   ctx.layout, ctx.causal, window=ctx.window)
+                                   ctx.layout, ctx.causal, window=ctx.window, dropout=ctx.dropout)
         # fp32 accumulators -> q.dtype, returned in the interface layout [P, b, H, L, d]
         return (dq.to(q.dtype).transpose(2, 3), dk.to(k.dtype).transpose(2, 3),
-                dv.to(v.dtype).transpose(2, 3), None, None, None, None, None, None)
+                dv.to(v.dtype).transpose(2, 3), None, None, None, None, None, None, None)
 
 
 def check_ring_inputs(q, k, v):

@@ -36,9 +36,9 @@ def rel_l2(got, ref):
 
 def assert_bf16_close(got, ref, what="", ulp_floor=False):
     """bf16 result vs an fp32 reference: max-abs < 2e-2 and rel-L2 < 1e-2. With
-    ``ulp_floor`` the max-abs bar of an element is max(2e-2, 2^-7 |ref|), one to two bf16
-    ulps of the value: for GQA-folded gradients, which reach |x| > 4 where one bf16 ulp
-    (2^-5) alone exceeds 2e-2."""
+    ``ulp_floor`` (True, or a number n of ulps) the max-abs bar of an element is
+    max(2e-2, n 2^-7 |ref|), n to 2n bf16 ulps of the value: for GQA-folded gradients,
+    which reach |x| > 4 where one bf16 ulp (2^-5) alone exceeds 2e-2."""
     got = got.detach().float().cpu()
     ref = ref.detach().float().cpu()
     assert got.shape == ref.shape, f"{what}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
@@ -47,7 +47,8 @@ def assert_bf16_close(got, ref, what="", ulp_floor=False):
     err = diff.max().item()
     rl = rel_l2(got, ref)
     if ulp_floor:
-        over = (diff / torch.clamp(ref.abs() * 2.0 ** -7, min=BF16_MAX_ABS)).max().item()
+        ulps = 1.0 if ulp_floor is True else float(ulp_floor)
+        over = (diff / torch.clamp(ref.abs() * ulps * 2.0 ** -7, min=BF16_MAX_ABS)).max().item()
         assert over < 1 and rl < BF16_REL_L2, \
             f"{what}: max-abs {err:.3e} ({over:.2f} of the ulp-floored bar) rel-L2 {rl:.3e}"
         return

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 12
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 13
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -87,6 +87,14 @@ def test_host_validation_dtype_and_merge_type():
     assert b"block type" in abi.lib().rmx_last_error()
 
 
+def test_host_validation_dropout():
+    assert _fwd(_layout(dropout_p=1.0)) == abi.RMX_EINVAL
+    assert _fwd(_layout(dropout_p=-0.1)) == abi.RMX_EINVAL
+    assert b"dropout_p" in abi.lib().rmx_last_error()
+    assert _fwd(_layout(dropout_p=0.1, mask=abi.MASK_DOC)) == abi.RMX_EUNSUPPORTED
+    assert _fwd(_layout(dropout_p=0.1, drop_seed_lo=5, drop_seed_hi=7)) == abi.RMX_OK
+
+
 def test_host_validation_window_flag():
     lay = _layout()
     arr = (abi.FwdProblem * 1)()
@@ -99,12 +107,14 @@ def test_host_validation_window_flag():
 
 
 def test_problem_structs_match_the_header():
-    """The ctypes mirrors have the C layout: the window fields sit at the end of each
-    problem struct (a zero-filled problem has no window)."""
-    assert ctypes.sizeof(abi.FwdProblem) == 11 * 8 + 5 * 4 + 4
-    assert ctypes.sizeof(abi.BwdProblem) == 17 * 8 + 6 * 4
+    """The ctypes mirrors have the C layout: the window and dropout fields sit at the end
+    of each problem struct (a zero-filled problem has no window and no offsets)."""
+    assert ctypes.sizeof(abi.FwdProblem) == 11 * 8 + 7 * 4 + 4
+    assert ctypes.sizeof(abi.BwdProblem) == 17 * 8 + 8 * 4
     assert abi.FwdProblem.has_window.offset == 11 * 8 + 3 * 4
     assert abi.BwdProblem.has_window.offset == 17 * 8 + 4 * 4
+    assert abi.FwdProblem.drop_k0.offset == 11 * 8 + 6 * 4
+    assert abi.AttnLayout.q_sb.offset == 40  # after the dtype, dropout and seed words
 
 
 def test_host_validation_backward_nlse():

@@ -32,7 +32,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _zigzag_rows(world, half):
-    return [torch.tensor(rm.zigzag_gidx(r, half, world)) for r in range(world)]
+    return [rm.zigzag_gidx(r, half, world) for r in range(world)]
 
 
 def _ring_vs_oracle(world, half, hq, hkv, d, cu=None, seed=0):

@@ -105,5 +105,10 @@ def test_p2p_preconditions():
         ring_attention(q, q, q, causal=True, attn_implementation="sdpa")
     with pytest.raises(ValueError, match="P2P Ring requires"):
         ring_attention(q, q, q, causal=True, window=(4, 0))
-    with pytest.raises(NotImplementedError):
-        ring_attention(q, q, q, causal=True, rotate_method="allgather", dropout=0.1)
+    with pytest.raises(ValueError, match="dropout"):
+        ring_attention(q, q, q, causal=True, rotate_method="allgather", dropout=1.0)
+    from ringmaster_amd.ring import varlen_ring_attention
+
+    cu = torch.tensor([0, 64, 128], dtype=torch.int32, device="cuda")
+    with pytest.raises(NotImplementedError, match="document"):
+        varlen_ring_attention(q, q, q, scaling=None, cu_seqlens=cu, dropout=0.1)

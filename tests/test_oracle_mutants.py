@@ -69,6 +69,24 @@ def test_window_mutants_are_caught(mutation):
         pin.check_window_block(lambda *a, **k: _window_block_variant(*a, **k, **kw), True, 4, 9, 1)
 
 
+def test_dropout_unscaled_mutant_is_caught():
+    """Dropping without the 1 / (1 - p) rescale biases the output low."""
+    def unscaled(q, k, v, *, causal, scaling, dropout, drop_seed):
+        qt, kt, vt = (t.transpose(1, 2).double() for t in (q, k, v))
+        s = (qt @ kt.transpose(-1, -2)) * (1 / math.sqrt(qt.shape[-1]))
+        sq, sk = s.shape[-2:]
+        if causal:
+            s = s.masked_fill(~torch.ones(sq, sk, dtype=torch.bool).tril(sk - sq), float("-inf"))
+        lse = torch.logsumexp(s, -1)
+        pm = torch.exp(s - lse[..., None])
+        pm = pm * rm.dropout_scale_mask(drop_seed, s.shape[0], s.shape[1], sq, sk, dropout).double() \
+            * (1 - dropout)
+        return (pm @ vt).transpose(1, 2), lse
+
+    with pytest.raises(AssertionError):
+        pin.check_dropout_unbiased(unscaled)
+
+
 def test_merge_mutants_are_caught():
     def flipped(out, lse, block_out, block_lse):  # exp(new - blk) instead of exp(blk - new)
         block_lse = rm.lse_to_bshd(block_lse, block_out)

@@ -145,6 +145,117 @@ def test_varlen_ring_window_equals_per_document():
         assert torch.allclose(lse[:, :, a:b].double(), ref_l, atol=TOL32)
 
 
+def _fmix32_int(x):
+    """MurmurHash3's fmix32 on a Python int (an implementation independent of numpy's
+    wrap-around arithmetic)."""
+    m = 0xFFFFFFFF
+    x &= m
+    x ^= x >> 16
+    x = (x * 0x85EBCA6B) & m
+    x ^= x >> 13
+    x = (x * 0xC2B2AE35) & m
+    x ^= x >> 16
+    return x
+
+
+def test_fmix32_matches_integer_arithmetic_and_is_a_bijection():
+    import numpy as np
+
+    g = np.random.default_rng(0)
+    xs = np.concatenate([g.integers(0, 1 << 32, 2000, dtype=np.uint64).astype(np.uint32),
+                         np.array([0, 1, 0x7FFFFFFF, 0x80000000, 0xFFFFFFFF], dtype=np.uint32)])
+    got = rm.fmix32(xs)
+    assert [int(v) for v in got] == [_fmix32_int(int(x)) for x in xs]
+    # each step (xor-shift, odd multiply) is invertible: no two inputs share an output
+    assert len(np.unique(rm.fmix32(np.arange(1 << 20, dtype=np.uint32)))) == 1 << 20
+
+
+def test_dropout_keep_matches_its_definition():
+    """dropout_keep on a few elements, recomputed from the formula with Python ints."""
+    seed, bh, p = 0x0123456789ABCDEF, 7, 0.3
+    keep = rm.dropout_keep(seed, bh, [0, 5, 1000], [3, 64, 77777], p)
+    bhmix = _fmix32_int((seed & 0xFFFFFFFF) ^ _fmix32_int((seed >> 32) ^ (bh * 0x9E3779B9)))
+    thr = int(p * 2 ** 32)
+    for i, q in enumerate([0, 5, 1000]):
+        for j, k in enumerate([3, 64, 77777]):
+            u = _fmix32_int(bhmix ^ ((q * 0x85EBCA77) & 0xFFFFFFFF) ^ ((k * 0xC2B2AE3D) & 0xFFFFFFFF))
+            assert bool(keep[i, j]) == (u >= thr)
+
+
+@pytest.mark.parametrize("p", [0.1, 0.3, 0.7])
+def test_dropout_keep_rate_and_independence(p):
+    """Keep rate 1 - p within 5 sigma over 4M elements; neighbouring elements (along q and
+    along k) and two heads kept together at rate (1 - p)^2, as independent draws are."""
+    import numpy as np
+
+    n = 2048
+    keep = rm.dropout_keep(99, 3, np.arange(n), np.arange(n), p)
+    sig = math.sqrt(p * (1 - p) / keep.size)
+    assert abs(keep.mean() - (1 - p)) < 5 * sig
+    pair_sig = math.sqrt((1 - p) ** 2 * (1 - (1 - p) ** 2) / keep.size)
+    assert abs((keep[:, 1:] & keep[:, :-1]).mean() - (1 - p) ** 2) < 6 * pair_sig
+    assert abs((keep[1:] & keep[:-1]).mean() - (1 - p) ** 2) < 6 * pair_sig
+    other = rm.dropout_keep(99, 4, np.arange(n), np.arange(n), p)
+    assert abs((keep & other).mean() - (1 - p) ** 2) < 6 * pair_sig
+    rows = keep.mean(1)  # per-row rates: binomial spread, no biased rows
+    assert rows.std() < 1.5 * math.sqrt(p * (1 - p) / n)
+
+
+def check_dropout_unbiased(block_fn):
+    """Averaged over seeds, the dropped block equals the undropped one (E[M / (1 - p)] = 1,
+    lse undropped)."""
+    p = 0.25
+    q, k, v = rnd(1, 16, 2, 8, seed=80), rnd(1, 16, 2, 8, seed=81), rnd(1, 16, 2, 8, seed=82)
+    ref, ref_lse = rm.math_block(q, k, v, causal=True, scaling=None)
+    acc = torch.zeros_like(ref, dtype=torch.float64)
+    n = 400
+    for sd in range(n):
+        o, lse = block_fn(q, k, v, causal=True, scaling=None, dropout=p, drop_seed=sd)
+        assert torch.allclose(lse.double(), ref_lse.double(), atol=TOL32)
+        acc += o.double()
+    # standard error of the mean of out_i = sum_j P_ij m_ij v_j, m in {0, 1/(1-p)}:
+    # Var = sum_j P_ij^2 v_j^2 p / (1 - p)
+    scores = q.transpose(1, 2).double() @ k.transpose(1, 2).double().transpose(-1, -2)
+    pr = torch.exp(scores / math.sqrt(8) - ref_lse[..., None].double())
+    pr = pr.masked_fill(~torch.ones(16, 16, dtype=torch.bool).tril(), 0.0)
+    var = (pr ** 2) @ (v.transpose(1, 2).double() ** 2) * p / (1 - p)
+    se = (var / n).sqrt().transpose(1, 2)
+    z = ((acc / n - ref.double()).abs() / (se + 1e-9)).max().item()
+    assert z < 5.5, f"mean of dropped outputs is {z:.1f} standard errors off"
+
+
+def test_dropout_block_unbiased_and_lse_undropped():
+    check_dropout_unbiased(rm.math_block)
+
+
+def test_dropout_block_gradients_are_the_derivative():
+    """The dropped block's autograd gradients against finite differences (fp64, one seed)."""
+    q, k, v = (rnd(1, 5, 2, 4, seed=s).requires_grad_(True) for s in (83, 84, 85))
+
+    def f(q, k, v):
+        return rm.math_block(q, k, v, causal=False, scaling=0.7, dropout=0.4, drop_seed=5,
+                             drop_q0=3, drop_k0=11)[0].double()
+
+    qt, kt, vt = (t.detach().double().requires_grad_(True) for t in (q, k, v))
+    # the oracle computes in fp32: gradcheck an fp64 copy of its dropped path, then check
+    # the oracle's own autograd against that copy's gradients
+    assert torch.autograd.gradcheck(_math_block_f64, (qt, kt, vt), eps=1e-6, atol=1e-5)
+    f(q, k, v).sum().backward()
+    _math_block_f64(qt, kt, vt).sum().backward()
+    for a, b in ((q, qt), (k, kt), (v, vt)):
+        assert torch.allclose(a.grad.double(), b.grad, atol=1e-4)
+
+
+def _math_block_f64(q, k, v):
+    """math_block's dropped path in fp64 (same mask), for gradcheck."""
+    qt, kt, vt = (t.transpose(1, 2) for t in (q, k, v))
+    scores = (qt @ kt.transpose(-1, -2)) * 0.7
+    lse = torch.logsumexp(scores, dim=-1)
+    probs = torch.exp(scores - lse.unsqueeze(-1))
+    probs = probs * rm.dropout_scale_mask(5, 1, 2, 5, 5, 0.4, 3, 11).double()
+    return (probs @ vt).transpose(1, 2)
+
+
 def check_merge(merge_fn):
     """merge(attn(Q, K1), attn(Q, K2)) == attn(Q, [K1; K2]) in out and lse."""
     q = rnd(1, 6, 2, 8, seed=7)
