@@ -12,11 +12,14 @@
 // the MFMA (mamba-ssm's chunk-state kernel scales B instead: the two differ by the
 // bf16 rounding of one factor of each product); sums are fp32.
 //
-// Forward: a workgroup = 4 waves over one (row, head, token half). Each stage
-// stages 64 tokens of w*x and of B in LDS (rows padded so the transposed reads
-// are free of bank conflicts); both MFMA operands are token-major, so they come
-// from ds_read_b64_tr_b16 (S = (wX)^T B: M = head dim, N = state, K = tokens).
-// Each wave owns D*N/4096 of the 32x32 output tiles, all in one row block.
+// Forward: a workgroup = 4 waves over one (row, pair of heads (or one head), token
+// half). Each stage stages 64 tokens of w*x and of B in LDS (rows padded so the
+// transposed reads are free of bank conflicts); both MFMA operands are token-major,
+// so they come from ds_read_b64_tr_b16 (S = (wX)^T B: M = head dim, N = state,
+// K = tokens). Each wave owns D*N/4096 of the 32x32 output tiles of each head, all in
+// one row block. Two heads read 256 contiguous bytes of a token's x row where one
+// head reads 128 at the token stride (a strided copy of 128-byte rows runs at half
+// the HBM rate of one of 512-byte rows), and share each B operand read.
 //
 // Backward (given G = dL/dS fp32): a workgroup = 8 waves x 32 tokens of one
 // (row, group); it loops over the group's heads, staging G_h in LDS as bf16:
@@ -94,15 +97,19 @@ __device__ __forceinline__ u32x4 scale_bf16x8(const u32x4& v, float w) {
 }
 
 // ---------------------------------------------------------------- forward
-template <int D, int N>
+template <int D, int N, int HPW>
 __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs a) {
   constexpr int TK = 64;                                // tokens per stage
   constexpr int XS = padded_stride<2 * D>(), BS = padded_stride<2 * N>();
   constexpr int NBN = N / 32;                           // 32-wide state blocks
-  constexpr int TPW = (D / 32) * NBN / 4;               // output tiles per wave
-  constexpr int XCH = TK * D / 8 / 256, BCH = TK * N / 8 / 256;  // 16-B chunks per thread
+  constexpr int TPW = (D / 32) * NBN / 4;               // output tiles per wave and head
+  constexpr int XR = HPW * D / 8;                       // 16-B chunks of a token's x row
+  constexpr int XCH = TK * XR / 256, BCH = TK * N / 8 / 256;  // 16-B chunks per thread
   static_assert(TPW >= 1 && NBN % TPW == 0 && XCH >= 1 && BCH >= 1, "tile split");
-  __shared__ __attribute__((aligned(16))) uint8_t sX[TK * XS];
+  // HPW consecutive heads of one group per workgroup: a token's x row of those heads is
+  // HPW * 2D contiguous bytes (rows of 128 bytes at the token stride read at half the
+  // rate of 512-byte ones), and one B operand read serves every head
+  __shared__ __attribute__((aligned(16))) uint8_t sX[HPW][TK * XS];
   __shared__ __attribute__((aligned(16))) uint8_t sB[TK * BS];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -113,9 +120,10 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
   const int nwg = gridDim.x;
   const int k = (nwg % 8 == 0) ? (int)(blockIdx.x % 8) * (nwg / 8) + (int)(blockIdx.x / 8)
                                : (int)blockIdx.x;
-  const int h = k % a.H;
-  const int split = (k / a.H) % a.split;
-  const int row = k / (a.H * a.split);
+  const int nhb = a.H / HPW;
+  const int h = (k % nhb) * HPW;  // first head of the workgroup
+  const int split = (k / nhb) % a.split;
+  const int row = k / (nhb * a.split);
   const int g = h / (a.H / a.G);
   const int T = a.T;
   // tokens of this workgroup: whole stages, the last split takes the remainder
@@ -126,7 +134,9 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
   const int st_begin = st_lo > t0 / TK ? st_lo : t0 / TK;
 
   const int64_t th = (int64_t)row * T * a.H + h;  // (row, t = 0, h) in [rows, T, H]
-  const float cl = a.cum_A[th + (int64_t)(T - 1) * a.H];
+  float cl[HPW];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) cl[j] = a.cum_A[th + (int64_t)(T - 1) * a.H + j];
   const i32x4 xrs = make_rsrc(a.x + (int64_t)row * T * a.H * D, (uint32_t)T * a.H * D * 2);
   const i32x4 brs = make_rsrc(a.B + (int64_t)row * T * a.G * N, (uint32_t)T * a.G * N * 2);
 
@@ -142,9 +152,9 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
     const int tb = st * TK;
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int c = tid + 256 * i, t = tb + c / (D / 8);
-      r.x[i] = buf_load16(xrs, ((t * a.H + h) * D + 8 * (c % (D / 8))) * 2);
-      const int64_t o = th + (int64_t)(t < T ? t : T - 1) * a.H;
+      const int c = tid + 256 * i, t = tb + c / XR, j = (c % XR) / (D / 8);
+      r.x[i] = buf_load16(xrs, ((t * a.H + h) * D + 8 * (c % XR)) * 2);
+      const int64_t o = th + (int64_t)(t < T ? t : T - 1) * a.H + j;
       r.e[i] = a.e[o];
       r.c[i] = a.cum_A[o];
     }
@@ -157,9 +167,14 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
   auto store = [&](int st, const Regs& r) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int c = tid + 256 * i, t = st * TK + c / (D / 8);
-      const float w = (t >= t0 && t < T) ? r.e[i] * expf(cl - r.c[i]) : 0.f;
-      st16(sX + (c / (D / 8)) * XS + 16 * (c % (D / 8)), scale_bf16x8(r.x[i], w));
+      const int c = tid + 256 * i, t = st * TK + c / XR, j = (c % XR) / (D / 8);
+      // XR is a power of two and c % XR a multiple of D / 8 per head: j is wave-uniform
+      // only when XR >= 64; the head's cum_A at T-1 is picked per lane
+      float clj = cl[0];
+#pragma unroll
+      for (int jj = 1; jj < HPW; ++jj) clj = j == jj ? cl[jj] : clj;
+      const float w = (t >= t0 && t < T) ? r.e[i] * expf(clj - r.c[i]) : 0.f;
+      st16(sX[j] + (c / XR) * XS + 16 * (c % (D / 8)), scale_bf16x8(r.x[i], w));
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
@@ -169,16 +184,23 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
   };
 
   const int mb = (wave * TPW) / NBN, nb0 = (wave * TPW) % NBN;
-  f32x16 acc[TPW];
+  f32x16 acc[HPW][TPW];
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) acc[i] = zero16();
+  for (int j = 0; j < HPW; ++j)
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) acc[j][i] = zero16();
   auto compute = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < TK / 16; ++ks) {
-      const bf16x8 av = tr_tokens<XS>(sX, 16 * ks, 32 * mb, lane);
+      bf16x8 av[HPW];
 #pragma unroll
-      for (int i = 0; i < TPW; ++i)
-        acc[i] = mfma32(av, tr_tokens<BS>(sB, 16 * ks, 32 * (nb0 + i), lane), acc[i]);
+      for (int j = 0; j < HPW; ++j) av[j] = tr_tokens<XS>(sX[j], 16 * ks, 32 * mb, lane);
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        const bf16x8 bv = tr_tokens<BS>(sB, 16 * ks, 32 * (nb0 + i), lane);
+#pragma unroll
+        for (int j = 0; j < HPW; ++j) acc[j][i] = mfma32(av[j], bv, acc[j][i]);
+      }
     }
   };
   if (st_begin < st_hi) load(st_begin, rg);
@@ -192,17 +214,20 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
 
   // lane (hl, l32), reg r: d = 32 mb + c_row(hl, r), n = 32 nb + l32
   const int hl = lane >> 5, l32 = lane & 31;
-  float* out = a.state + ((int64_t)row * a.H + h) * D * N;
 #pragma unroll
-  for (int i = 0; i < TPW; ++i)
+  for (int j = 0; j < HPW; ++j) {
+    float* out = a.state + ((int64_t)row * a.H + h + j) * D * N;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float* p = out + (32 * mb + c_row(hl, r)) * N + 32 * (nb0 + i) + l32;
-      if (a.split == 1)
-        *p = acc[i][r];
-      else
-        atomicAdd(p, acc[i][r]);  // two splits onto zero: exact in either order
-    }
+    for (int i = 0; i < TPW; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float* p = out + (32 * mb + c_row(hl, r)) * N + 32 * (nb0 + i) + l32;
+        if (a.split == 1)
+          *p = acc[j][i][r];
+        else
+          atomicAdd(p, acc[j][i][r]);  // two splits onto zero: exact in either order
+      }
+  }
 }
 
 __global__ void zero_f32_kernel(float* p, int64_t n) {
@@ -460,8 +485,16 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
 // ---------------------------------------------------------------- launchers
 template <int D, int N>
 static void launch_fwd_dn(const StateArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((mamba2_chunk_state_kernel<D, N>), dim3((unsigned)(a.rows * a.H * a.split)),
-                     dim3(256), 0, stream, a);
+  // two heads per workgroup where that keeps three workgroups per CU (at configs[4]:
+  // 163 us against 205 us for one head; four heads per workgroup fit one workgroup per
+  // CU and ran 216 us)
+  if (D * N <= 64 * 128 && (a.H / a.G) % 2 == 0) {
+    hipLaunchKernelGGL((mamba2_chunk_state_kernel<D, N, 2>),
+                       dim3((unsigned)(a.rows * (a.H / 2) * a.split)), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((mamba2_chunk_state_kernel<D, N, 1>),
+                       dim3((unsigned)(a.rows * a.H * a.split)), dim3(256), 0, stream, a);
+  }
 }
 template <int D, int N>
 static void launch_bwd_dn(const StateArgs& a, hipStream_t stream) {

@@ -13,8 +13,10 @@ pytestmark = pytest.mark.gpu
 
 # (rows, T, H, D, G, N): ragged T, both state and head sizes, one or two groups, the
 # two-workgroup split (T >= 1024 with few rows), a single token
+# the forward runs two heads per workgroup when a group has an even number of heads
+# (D * N <= 64 * 128), one otherwise: (6 heads, 2 groups) takes the one-head path
 CASES = [(2, 200, 8, 64, 2, 128), (1, 2048, 4, 64, 1, 64), (2, 130, 4, 128, 2, 64),
-         (1, 300, 2, 128, 1, 128), (1, 1, 2, 64, 1, 64)]
+         (1, 300, 2, 128, 1, 128), (1, 1, 2, 64, 1, 64), (1, 333, 6, 64, 2, 128)]
 
 
 def _weights(R, T, H, seed):
