@@ -436,11 +436,14 @@ def chunk_state_workload(steps, warmup):
                                              cum.data_ptr(), None, state.data_ptr(), P, T, H,
                                              D, G, N, st))
 
+    ws_bytes = lib.rmx_mamba2_chunk_state_bwd_workspace(P, H, D, N)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda") if ws_bytes else None
+
     def bwd():
         abi.check(lib.rmx_mamba2_chunk_state_bwd(
             x.data_ptr(), B.data_ptr(), e.data_ptr(), cum.data_ptr(), None, gst.data_ptr(),
             g_x.data_ptr(), g_B.data_ptr(), g_e.data_ptr(), g_cum.data_ptr(), P, T, H, D, G, N,
-            st))
+            abi.ptr(ws), ws_bytes, st))
 
     fwd_ms = _time(fwd, steps, warmup)
     bwd_ms = _time(bwd, steps, warmup)

@@ -28,14 +28,15 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 13 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 14 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
                               8: allocation-free Mamba2 correction bwd;
                               9: carried-in state h_in / dh_in of the linear scan;
                               10: L-parallel linear scan (workspace argument);
                               11: sliding windows, attention head_dim any multiple of 8
                                   up to 128; 12: fp16 attention (layout dtype);
-                              13: attention dropout */
+                              13: attention dropout;
+                              14: workspace of the Mamba2 shard-state backward */
 
 /* error codes */
 #define RMX_OK 0
@@ -399,13 +400,20 @@ int32_t rmx_mamba2_chunk_state(const uint16_t* x, const uint16_t* B, const float
  * state): writes g_x (bf16, like x), g_B (bf16, like B), g_e and g_cum_A (fp32
  * [rows, T, H]). g_cum_A[r, T-1, h] is left as -g_w w of that token; the full
  * entry is sum_{t<T-1} g_w w = -sum_{t<T-1} g_cum_A[r, t, h], which the caller
- * writes (every weight depends on cum_A at T-1).
+ * writes (every weight depends on cum_A at T-1). workspace (nullable) of at least
+ * rmx_mamba2_chunk_state_bwd_workspace(...) bytes, 16-byte aligned: with it (and a
+ * nonzero size: head_dim 64), g_state is first converted to bf16 there and the kernel moves two
+ * heads per step, reading G by LDS DMA; without it the one-head form runs. Both give
+ * the same results up to fp32 summation order.
  */
+size_t rmx_mamba2_chunk_state_bwd_workspace(int32_t rows, int32_t nheads, int32_t head_dim,
+                                            int32_t d_state);
 int32_t rmx_mamba2_chunk_state_bwd(const uint16_t* x, const uint16_t* B, const float* e,
                                    const float* cum_A, const int32_t* t0, const float* g_state,
                                    uint16_t* g_x, uint16_t* g_B, float* g_e, float* g_cum_A,
                                    int32_t rows, int32_t T, int32_t nheads, int32_t head_dim,
-                                   int32_t ngroups, int32_t d_state, void* stream);
+                                   int32_t ngroups, int32_t d_state, void* workspace,
+                                   size_t workspace_bytes, void* stream);
 
 /*
  * Mamba2 context-parallel causal conv1d with the halo (mamba.py:46-101, the conv

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
-ABI_VERSION = 13  # RMX_ABI_VERSION of include/ringmaster_amd.h
+ABI_VERSION = 14  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
@@ -112,7 +112,8 @@ SIGNATURES = {
     "rmx_mamba2_dt_cumsum_bwd": (_i32, [_vp, _i32, _vp, _vp, _i32] + [_vp] * 7
                                  + [_i32, _i32, _i32, _vp]),
     "rmx_mamba2_chunk_state": (_i32, [_vp] * 6 + [_i32] * 6 + [_vp]),
-    "rmx_mamba2_chunk_state_bwd": (_i32, [_vp] * 10 + [_i32] * 6 + [_vp]),
+    "rmx_mamba2_chunk_state_bwd_workspace": (ctypes.c_size_t, [_i32] * 4),
+    "rmx_mamba2_chunk_state_bwd": (_i32, [_vp] * 10 + [_i32] * 6 + [_vp, ctypes.c_size_t, _vp]),
     "rmx_causal_conv1d_cp": (_i32, [_vp] * 5 + [_i32] * 6 + [_vp]),
     "rmx_causal_conv1d_cp_bwd": (_i32, [_vp] * 8 + [_i32] * 6 + [_vp]),
 }

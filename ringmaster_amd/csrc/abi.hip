@@ -559,20 +559,37 @@ int32_t rmx_mamba2_chunk_state(const uint16_t* x, const uint16_t* B, const float
                     "rmx_mamba2_chunk_state launch");
 }
 
+size_t rmx_mamba2_chunk_state_bwd_workspace(int32_t rows, int32_t nheads, int32_t head_dim,
+                                            int32_t d_state) {
+  if (rows <= 0 || nheads <= 0) return 0;
+  if ((head_dim != 64 && head_dim != 128) || (d_state != 64 && d_state != 128)) return 0;
+  return rmx::mamba2_chunk_state_bwd_workspace(rows, nheads, head_dim, d_state);
+}
+
 int32_t rmx_mamba2_chunk_state_bwd(const uint16_t* x, const uint16_t* B, const float* e,
                                    const float* cum_A, const int32_t* t0, const float* g_state,
                                    uint16_t* g_x, uint16_t* g_B, float* g_e, float* g_cum_A,
                                    int32_t rows, int32_t T, int32_t nheads, int32_t head_dim,
-                                   int32_t ngroups, int32_t d_state, void* stream) {
+                                   int32_t ngroups, int32_t d_state, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
   int rc = check_state(x, B, e, cum_A, rows, T, nheads, head_dim, ngroups, d_state);
   if (rc) return rc;
   if ((int64_t)rows * T * nheads == 0) return RMX_OK;
   if (!g_state || !g_x || !g_B || !g_e || !g_cum_A) return fail(RMX_EINVAL, "NULL tensor pointer");
   if (!aligned(g_state, 16) || !aligned(g_x, 8) || !aligned(g_B, 8))
     return fail(RMX_EINVAL, "g_state must be 16-byte and g_x, g_B 8-byte aligned");
+  const size_t need = rmx::mamba2_chunk_state_bwd_workspace(rows, nheads, head_dim, d_state);
+  if (workspace && need > 0) {
+    if (workspace_bytes < need)
+      return fail(RMX_EINVAL, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
+    if (!aligned(workspace, 16)) return fail(RMX_EINVAL, "workspace must be 16-byte aligned");
+    if ((int64_t)T * nheads * head_dim * 2 >= ((int64_t)1 << 31))
+      return fail(RMX_EINVAL, "a row of x spans 2 GiB or more");
+  }
   return dev_status(rmx::launch_mamba2_chunk_state_bwd(x, B, e, cum_A, t0, g_state, g_x, g_B,
                                                        g_e, g_cum_A, rows, T, nheads, head_dim,
-                                                       ngroups, d_state, (hipStream_t)stream),
+                                                       ngroups, d_state, need > 0 ? workspace : nullptr,
+                                                       (hipStream_t)stream),
                     "rmx_mamba2_chunk_state_bwd launch");
 }
 

@@ -482,6 +482,288 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
   }
 }
 
+// ---------------------------------------------------------------- backward, two heads per step
+// The backward above moves a token's x and g_x row of ONE head (128 bytes at the
+// token stride) per step; a strided copy of such rows runs at half the HBM rate of
+// one of 256-byte rows. This form moves two adjacent heads per step: a workgroup =
+// 8 waves = 4 token waves (32 tokens each, 128 tokens) x 2 head slots, step i doing
+// head 2i of the group in slot 0 and 2i + 1 in slot 1, the same math per (token,
+// head) as above. G arrives as bf16 rows [rows, H, D, N] (g_state_bf16_kernel fills
+// a caller workspace) by LDS DMA one step ahead, so no registers carry it. A step:
+//   wait for everything this wave issued (G of this step, its x rows, the previous
+//   step's stores) and barrier; store the previous step's g_x rows (staged in the
+//   wave's LDS strip) and the g_e / g_cum_A strips of an 8-head group the previous
+//   step finished; load the step's e / cum_A table; DMA the next step's G, load its
+//   x rows; compute.
+// Each slot sums its own heads' g_B in registers; the two sums meet in LDS at the end.
+template <int D, int N>
+__global__ __launch_bounds__(512) void mamba2_chunk_state_bwd2_kernel(const StateArgs a,
+                                                                       const uint16_t* gws) {
+  constexpr int NW = 8, BT = 128;                 // 4 token waves x 2 head slots
+  constexpr int GS = 2 * N, GT = D * GS;          // a G_h tile: D rows of N bf16, swizzled
+  constexpr int NMD = D / 32, NKN = N / 16;       // GEMM 1 (U): M blocks, k-steps
+  constexpr int NMN = N / 32, NKD = D / 16;       // GEMM 2 (g_B): M blocks, k-steps
+  constexpr int PPW = GT / 1024 / 4;              // 1 KiB DMA pieces per wave and step
+  constexpr int XS = 2 * D + 8;
+  static_assert(PPW >= 1 && GT % 4096 == 0, "G tile split");
+  static_assert(2 * 2 * GT >= BT * N * 4, "g_B meeting place");
+  __shared__ __attribute__((aligned(1024))) uint8_t sG[2][2][GT];  // [step parity][slot]
+  __shared__ __attribute__((aligned(16))) float sE[2][2][BT][8];   // [group parity][e, cum][token][head]
+  __shared__ __attribute__((aligned(16))) uint8_t sX[NW][32 * XS];
+  __shared__ float sEC[NW * 32][17];
+
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tw = wave & 3, hs = wave >> 2;  // token wave, head slot
+  const int nbt = (a.T + BT - 1) / BT;
+  const int bt = blockIdx.x % nbt;
+  const int rg = blockIdx.x / nbt;
+  const int g = rg % a.G, row = rg / a.G;
+  const int T = a.T, H = a.H, hpg = H / a.G;
+  const int nstep = (hpg + 1) / 2;
+  const int tb = bt * BT + 32 * tw;  // first token of this wave
+  const int t = tb + l32;            // this lane's token
+  const bool tv = t < T;
+  const int t0 = a.t0 ? a.t0[row] : 0;
+  const bool live = tv && t >= t0;
+
+  bf16x8 bop[NKN];
+  {
+    const i32x4 brs = make_rsrc(a.B + (int64_t)row * T * a.G * N, (uint32_t)T * a.G * N * 2);
+#pragma unroll
+    for (int kb = 0; kb < NKN; ++kb)
+      bop[kb] = __builtin_bit_cast(bf16x8, buf_load16(brs, ((t * a.G + g) * N + 16 * kb + 8 * hl) * 2));
+  }
+  const i32x4 xrs = make_rsrc(a.x + (int64_t)row * T * H * D, (uint32_t)T * H * D * 2);
+  f32x16 gb[NMN];
+#pragma unroll
+  for (int i = 0; i < NMN; ++i) gb[i] = zero16();
+
+  // G DMA: the 4 waves of slot s fill its tile, wave piece (tw PPW + j); lane L of piece p
+  // writes LDS bytes 1024 p + 16 L (row d, chunk position c) from global chunk c ^ swz(d)
+  int goff[PPW];
+#pragma unroll
+  for (int j = 0; j < PPW; ++j) {
+    const int byte = 1024 * (tw * PPW + j) + 16 * lane;
+    const int d = byte / GS, c = (byte % GS) / 16;
+    goff[j] = d * GS + 16 * (c ^ swz_both<N>(d));
+  }
+  auto dma_g = [&](int i, int buf) __attribute__((always_inline)) {
+    const int hh = 2 * i + hs;  // this slot's head of step i (none past the group)
+    const bool on = hh < hpg;
+    const uint16_t* base = gws + ((int64_t)row * H + g * hpg + (on ? hh : 0)) * D * N;
+    const i32x4 rs = make_rsrc(base, on ? (uint32_t)GT : 0u);
+    const uint32_t dst = lds_addr(&sG[buf][hs][0]);
+#pragma unroll
+    for (int j = 0; j < PPW; ++j) dma16_async(rs, dst + 1024 * (tw * PPW + j), goff[j]);
+  };
+
+  struct HeadRegs {
+    u32x4 x[NKD];
+    float e, c, cl;
+  };
+  HeadRegs hr[2];
+  const bool ec8 = ((H | hpg | g * hpg) & 7) == 0;
+  float* ecrow = sEC[32 * wave + l32];
+  auto load_ec = [&](int h0) __attribute__((always_inline)) {
+    const float* src = (hl ? a.cum_A : a.e) + ((int64_t)row * T + (tv ? t : 0)) * H + h0;
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
+    const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ecrow[8 * hl + i] = v0[i];
+      ecrow[8 * hl + 4 + i] = v1[i];
+    }
+  };
+  auto load_h = [&](int h, HeadRegs& r) __attribute__((always_inline)) {
+    const int xo = (t * H + h) * D;
+#pragma unroll
+    for (int kb = 0; kb < NKD; ++kb) r.x[kb] = buf_load16(xrs, (xo + 16 * kb + 8 * hl) * 2);
+    const int64_t th = (int64_t)row * T * H + h;
+    if (!ec8) {
+      r.e = a.e[th + (int64_t)(tv ? t : 0) * H];
+      r.c = a.cum_A[th + (int64_t)(tv ? t : 0) * H];
+    }
+    r.cl = a.cum_A[th + (int64_t)(T - 1) * H];
+  };
+  // this wave's g_x rows of head h, staged in its LDS strip, as whole rows: tokens past T
+  // fall outside num_records and are dropped
+  auto store_gx = [&](int h) __attribute__((always_inline)) {
+    constexpr int LPR = 2 * D / 16, RPI = 64 / LPR;
+    const int nrows = T - tb < 32 ? T - tb : 32;
+    const i32x4 grs = make_rsrc(a.g_x + ((int64_t)row * T + tb) * H * D + (int64_t)h * D,
+                                nrows > 0 ? (uint32_t)((nrows - 1) * H * D + D) * 2u : 0u);
+    const uint8_t* xs = sX[wave];
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int rr = RPI * i + lane / LPR;
+      const uint8_t* src = xs + rr * XS + 16 * (lane % LPR);
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8);
+      u32x4 v;
+      v[0] = lo[0];
+      v[1] = lo[1];
+      v[2] = hi[0];
+      v[3] = hi[1];
+      buf_store16(grs, (rr * H * D + 8 * (lane % LPR)) * 2, v);
+    }
+  };
+  // g_e (lane half 0) / g_cum_A (half 1) of the 8-head group k (heads 8k .. 8k + cnt - 1
+  // of the group), both slots' columns, stored by slot 0
+  auto store_strip = [&](int k, int cnt) __attribute__((always_inline)) {
+    if (hs != 0 || !tv) return;
+    const float* strip = &sE[k & 1][hl][32 * tw + l32][0];
+    const int h0 = g * hpg + 8 * k;
+    float* dst = (hl ? a.g_cum : a.g_e) + (int64_t)row * T * H + (int64_t)t * H + h0;
+    if (cnt == 8 && ((H | h0) & 3) == 0) {  // 16-byte aligned rows
+      *reinterpret_cast<f32x4*>(dst) = *reinterpret_cast<const f32x4*>(strip);
+      *reinterpret_cast<f32x4*>(dst + 4) = *reinterpret_cast<const f32x4*>(strip + 4);
+    } else {
+      for (int j = 0; j < cnt; ++j) dst[j] = strip[j];
+    }
+  };
+
+  auto step = [&](int i, const HeadRegs& cur, HeadRegs& nxt) __attribute__((always_inline)) {
+    const int buf = i & 1, hh = 2 * i + hs, h = g * hpg + hh;
+    const bool on = hh < hpg;
+    wait_vm_barrier<0>();
+    if (i > 0) {
+      if (hh - 2 < hpg) store_gx(h - 2);
+      if (((2 * i) & 7) == 0) store_strip(i / 4 - 1, 8);
+    }
+    float ce = cur.e, cc = cur.c;
+    if (ec8 && ((2 * i) & 7) == 0) load_ec(g * hpg + 2 * i);
+    if (i + 1 < nstep) {
+      dma_g(i + 1, buf ^ 1);
+      if (hh + 2 < hpg) load_h(h + 2, nxt);
+    }
+    if (!on) return;
+    if (ec8) {
+      asm volatile("" ::: "memory");  // the table rows are this wave's own: LDS order suffices
+      ce = ecrow[hh & 7];
+      cc = ecrow[8 + (hh & 7)];
+    }
+    const uint8_t* sg = sG[buf][hs];
+    const float dec = live ? expf(cur.cl - cc) : 0.f;
+    const float w = live ? dec * ce : 0.f;
+
+    // U^T (d x tokens) = G_h B^T: A = G rows (LDS), B = this lane's B row
+    f32x16 u[NMD];
+#pragma unroll
+    for (int m = 0; m < NMD; ++m) {
+      u[m] = zero16();
+#pragma unroll
+      for (int kb = 0; kb < NKN; ++kb) {
+        const int gr = 32 * m + l32;
+        const bf16x8 ga = __builtin_bit_cast(
+            bf16x8, ld16(sg + gr * GS + 16 * ((2 * kb + hl) ^ swz_both<N>(gr))));
+        u[m] = mfma32(ga, bop[kb], u[m]);
+      }
+    }
+    // x in the C layout of U (see the backward above)
+    u32x2 xc[D / 8];
+#pragma unroll
+    for (int kb = 0; kb < NKD; ++kb) {
+      const u32x4 own = cur.x[kb];
+      const uint32_t s0 = hl ? own[0] : own[2], s1 = hl ? own[1] : own[3];
+      const uint32_t r0 = (uint32_t)__shfl_xor((int)s0, 32, 64);
+      const uint32_t r1 = (uint32_t)__shfl_xor((int)s1, 32, 64);
+      xc[2 * kb][0] = hl ? r0 : own[0];
+      xc[2 * kb][1] = hl ? r1 : own[1];
+      xc[2 * kb + 1][0] = hl ? own[2] : r0;
+      xc[2 * kb + 1][1] = hl ? own[3] : r1;
+    }
+    float gw = 0.f;
+    uint8_t* xs = sX[wave];
+#pragma unroll
+    for (int m = 0; m < NMD; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x2 xv = xc[4 * m + q];
+        const float x0 = __uint_as_float(xv[0] << 16), x1 = __uint_as_float(xv[0] & 0xffff0000u);
+        const float x2 = __uint_as_float(xv[1] << 16), x3 = __uint_as_float(xv[1] & 0xffff0000u);
+        gw += x0 * u[m][4 * q] + x1 * u[m][4 * q + 1] + x2 * u[m][4 * q + 2] + x3 * u[m][4 * q + 3];
+        u32x2 sv;
+        sv[0] = cvt_pk_bf16(w * u[m][4 * q], w * u[m][4 * q + 1]);
+        sv[1] = cvt_pk_bf16(w * u[m][4 * q + 2], w * u[m][4 * q + 3]);
+        *reinterpret_cast<u32x2*>(xs + l32 * XS + 2 * (32 * m + 8 * q + 4 * hl)) = sv;
+      }
+    gw += xhalf(gw);
+    sE[(hh >> 3) & 1][hl][32 * tw + l32][hh & 7] = hl ? -gw * w : gw * dec;
+
+    // g_B^T (state x tokens) += G_h^T (w x)^T: A = G^T by transposed reads, B = w x
+#pragma unroll
+    for (int m = 0; m < NMN; ++m)
+#pragma unroll
+      for (int kb = 0; kb < NKD; ++kb)
+        gb[m] = mfma32(tr_tokens_swz<GS>(sg, 16 * kb, 32 * m, lane),
+                       __builtin_bit_cast(bf16x8, scale_bf16x8(cur.x[kb], w)), gb[m]);
+  };
+
+  dma_g(0, 0);
+  if (hs < hpg) load_h(g * hpg + hs, hr[0]);
+  for (int i = 0; i < nstep; i += 2) {
+    step(i, hr[0], hr[1]);
+    if (i + 1 < nstep) step(i + 1, hr[1], hr[0]);
+  }
+  // the last step's g_x rows and the last (possibly partial) group's strips
+  wait_vm_barrier<0>();
+  {
+    const int hh = 2 * (nstep - 1) + hs;
+    if (hh < hpg) store_gx(g * hpg + hh);
+    const int k = (hpg - 1) / 8;
+    store_strip(k, hpg - 8 * k);
+  }
+  // g_B: slot 1's sums meet slot 0's in LDS (transposed, [n][token], conflict-free)
+  float* sgb = reinterpret_cast<float*>(&sG[0][0][0]);
+  if (hs == 1) {
+#pragma unroll
+    for (int m = 0; m < NMN; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sgb[(32 * m + c_row(hl, r)) * BT + 32 * tw + l32] = gb[m][r];
+  }
+  lds_barrier();
+  if (hs == 0 && tv) {
+    uint16_t* gbp = a.g_B + ((int64_t)row * T * a.G + (int64_t)t * a.G + g) * N;
+#pragma unroll
+    for (int m = 0; m < NMN; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int n = 32 * m + 8 * q + 4 * hl + k;
+          v[k] = gb[m][4 * q + k] + sgb[n * BT + 32 * tw + l32];
+        }
+        u32x2 st;
+        st[0] = cvt_pk_bf16(v[0], v[1]);
+        st[1] = cvt_pk_bf16(v[2], v[3]);
+        *reinterpret_cast<u32x2*>(gbp + 32 * m + 8 * q + 4 * hl) = st;
+      }
+  }
+}
+
+// G = dL/dS (fp32) -> bf16 rows of the same layout, for the two-head backward's DMA
+__global__ void g_state_bf16_kernel(const float* __restrict__ g, uint16_t* __restrict__ o,
+                                    int64_t n8) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const f32x4 a = *reinterpret_cast<const f32x4*>(g + 8 * i);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(g + 8 * i + 4);
+  u32x4 u;
+  u[0] = cvt_pk_bf16(a[0], a[1]);
+  u[1] = cvt_pk_bf16(a[2], a[3]);
+  u[2] = cvt_pk_bf16(b[0], b[1]);
+  u[3] = cvt_pk_bf16(b[2], b[3]);
+  *reinterpret_cast<u32x4*>(o + 8 * i) = u;
+}
+
+size_t mamba2_chunk_state_bwd_workspace(int rows, int H, int D, int N) {
+  // the two-head form runs where its LDS fits: head_dim 64 (d_state 64 or 128)
+  if (D != 64) return 0;
+  return (size_t)rows * H * D * N * 2;
+}
+
 // ---------------------------------------------------------------- launchers
 template <int D, int N>
 static void launch_fwd_dn(const StateArgs& a, hipStream_t stream) {
@@ -540,7 +822,7 @@ hipError_t launch_mamba2_chunk_state_bwd(const uint16_t* x, const uint16_t* B, c
                                          const float* cum_A, const int32_t* t0,
                                          const float* g_state, uint16_t* g_x, uint16_t* g_B,
                                          float* g_e, float* g_cum, int rows, int T, int H, int D,
-                                         int G, int N, hipStream_t stream) {
+                                         int G, int N, void* workspace, hipStream_t stream) {
   StateArgs a{};
   a.x = x;
   a.B = B;
@@ -557,6 +839,20 @@ hipError_t launch_mamba2_chunk_state_bwd(const uint16_t* x, const uint16_t* B, c
   a.H = H;
   a.G = G;
   a.split = 1;
+  if (workspace && mamba2_chunk_state_bwd_workspace(rows, H, D, N) > 0) {
+    uint16_t* gws = static_cast<uint16_t*>(workspace);
+    const int64_t n8 = (int64_t)rows * H * D * N / 8;
+    hipLaunchKernelGGL(g_state_bf16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
+                       stream, g_state, gws, n8);
+    const unsigned grid = (unsigned)(rows * G * ((T + 127) / 128));
+    if (N == 128)
+      hipLaunchKernelGGL((mamba2_chunk_state_bwd2_kernel<64, 128>), dim3(grid), dim3(512), 0,
+                         stream, a, gws);
+    else
+      hipLaunchKernelGGL((mamba2_chunk_state_bwd2_kernel<64, 64>), dim3(grid), dim3(512), 0,
+                         stream, a, gws);
+    return hipGetLastError();
+  }
   RMX_STATE_DISPATCH(launch_bwd_dn, D, N, a, stream)
   return hipGetLastError();
 }

@@ -68,11 +68,12 @@ hipError_t launch_mamba2_chunk_state(const uint16_t* x, const uint16_t* B, const
                                      const float* cum_A, const int32_t* t0, float* state,
                                      int rows, int T, int H, int D, int G, int N,
                                      hipStream_t stream);
+size_t mamba2_chunk_state_bwd_workspace(int rows, int H, int D, int N);
 hipError_t launch_mamba2_chunk_state_bwd(const uint16_t* x, const uint16_t* B, const float* e,
                                          const float* cum_A, const int32_t* t0,
                                          const float* g_state, uint16_t* g_x, uint16_t* g_B,
                                          float* g_e, float* g_cum, int rows, int T, int H, int D,
-                                         int G, int N, hipStream_t stream);
+                                         int G, int N, void* workspace, hipStream_t stream);
 hipError_t launch_causal_conv1d_cp(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                                    const int32_t* doc, uint16_t* y, int world, int batch, int C,
                                    int L, int W, int act, hipStream_t stream);

@@ -211,10 +211,13 @@ class _ChunkState(torch.autograd.Function):
         g_x, g_B = torch.empty_like(x), torch.empty_like(B)
         g_e = torch.empty((rows, T, H), dtype=torch.float32, device=x.device)
         g_cum = torch.empty_like(g_e)
-        abi.check(abi.lib().rmx_mamba2_chunk_state_bwd(
+        lib = abi.lib()
+        ws_bytes = lib.rmx_mamba2_chunk_state_bwd_workspace(rows, H, D, N)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+        abi.check(lib.rmx_mamba2_chunk_state_bwd(
             x.data_ptr(), B.data_ptr(), e.data_ptr(), cum_A.data_ptr(), abi.ptr(t0),
             g.data_ptr(), g_x.data_ptr(), g_B.data_ptr(), g_e.data_ptr(), g_cum.data_ptr(),
-            rows, T, H, D, G, N, abi.stream_of(x)))
+            rows, T, H, D, G, N, abi.ptr(ws), ws_bytes, abi.stream_of(x)))
         if T:
             # every weight exp(cum_A[T-1] - cum_A[t]) also depends on cum_A[T-1]
             g_cum[:, T - 1] = -g_cum[:, :T - 1].sum(1)

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 13
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 14
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -224,12 +224,19 @@ def test_host_validation_chunk_state():
     assert lib.rmx_mamba2_chunk_state(8, p, p, p, None, p, 1, 8, 4, 64, 1, 64, None) \
         == abi.RMX_EINVAL  # x not 16-byte aligned
     assert lib.rmx_mamba2_chunk_state_bwd(p, p, p, p, None, None, p, p, p, p, 1, 8, 4, 64, 1, 64,
-                                          None) == abi.RMX_EINVAL  # no g_state
+                                          None, 0, None) == abi.RMX_EINVAL  # no g_state
+    # the two-head form's workspace: bf16 G, where its LDS fits (head_dim 64)
+    assert lib.rmx_mamba2_chunk_state_bwd_workspace(8, 64, 64, 128) == 8 * 64 * 64 * 128 * 2
+    assert lib.rmx_mamba2_chunk_state_bwd_workspace(8, 64, 128, 128) == 0
+    assert lib.rmx_mamba2_chunk_state_bwd_workspace(8, 64, 32, 128) == 0
+    assert lib.rmx_mamba2_chunk_state_bwd(p, p, p, p, None, p, p, p, p, p, 1, 8, 4, 64, 1, 64,
+                                          p, 100, None) == abi.RMX_EINVAL  # workspace too small
+    assert b"workspace" in lib.rmx_last_error()
     # empty problems are no-ops
     assert lib.rmx_mamba2_chunk_state(None, None, None, None, None, None, 0, 8, 4, 64, 1, 64,
                                       None) == abi.RMX_OK
     assert lib.rmx_mamba2_chunk_state_bwd(None, None, None, None, None, None, None, None, None,
-                                          None, 2, 0, 4, 64, 1, 64, None) == abi.RMX_OK
+                                          None, 2, 0, 4, 64, 1, 64, None, 0, None) == abi.RMX_OK
 
 
 def test_host_validation_correction_bwd_noalloc():

@@ -83,16 +83,22 @@ def test_chunk_state_forward(R, T, H, D, G, N, docs):
 # backward extras: groups of 12 heads (32-byte g_e / g_cum_A rows at aligned head
 # offsets, then a partial group), 10 heads (the second group starts unaligned), and
 # the configs[4] layout (64 heads in one group) on a shorter shard
+# groups of 12 and 10 heads: 8-head strips ending part-way; (1, 300, 3, 64, 1, 128): an
+# odd head count (the second head slot idles in the last step, no 8-head tables)
 BWD_CASES = CASES[:4] + [(1, 256, 24, 64, 2, 128), (1, 160, 20, 64, 2, 64),
-                         (2, 512, 64, 64, 1, 128)]
+                         (2, 512, 64, 64, 1, 128), (1, 300, 3, 64, 1, 128)]
 
 
+@pytest.mark.parametrize("two_heads", [True, False])
 @pytest.mark.parametrize("docs", [None, (100,)])
 @pytest.mark.parametrize("R,T,H,D,G,N", BWD_CASES)
-def test_chunk_state_backward_raw(R, T, H, D, G, N, docs):
+def test_chunk_state_backward_raw(R, T, H, D, G, N, docs, two_heads):
+    """Both forms of the backward: with the bf16 workspace (two heads per step, G by LDS
+    DMA; where D * N <= 64 * 128) and without it (one head per step)."""
     from ringmaster_amd import abi
 
-    print(f"case bwd R={R} T={T} H={H} D={D} G={G} N={N} docs={docs}", flush=True)
+    print(f"case bwd R={R} T={T} H={H} D={D} G={G} N={N} docs={docs} two_heads={two_heads}",
+          flush=True)
     x = seeded((R, T, H, D), 11).to(torch.bfloat16)
     B = seeded((R, T, G, N), 12).to(torch.bfloat16)
     e, cum = _weights(R, T, H, 13)
@@ -108,10 +114,13 @@ def test_chunk_state_backward_raw(R, T, H, D, G, N, docs):
     g_x, g_B = torch.empty_like(xd), torch.empty_like(Bd)
     g_e = torch.empty_like(ed)
     g_cum = torch.empty_like(ed)
-    abi.check(abi.lib().rmx_mamba2_chunk_state_bwd(
+    lib = abi.lib()
+    ws_bytes = lib.rmx_mamba2_chunk_state_bwd_workspace(R, H, D, N) if two_heads else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda") if ws_bytes else None
+    abi.check(lib.rmx_mamba2_chunk_state_bwd(
         xd.data_ptr(), Bd.data_ptr(), ed.data_ptr(), cd.data_ptr(), abi.ptr(t0d),
         gsd.data_ptr(), g_x.data_ptr(), g_B.data_ptr(), g_e.data_ptr(), g_cum.data_ptr(),
-        R, T, H, D, G, N, abi.stream_of(xd)))
+        R, T, H, D, G, N, abi.ptr(ws), ws_bytes, abi.stream_of(xd)))
     g_cum[:, T - 1] = -g_cum[:, :T - 1].sum(1)
     torch.cuda.synchronize()
     for name, got, ref in zip(("g_x", "g_B", "g_e", "g_cum_A"), (g_x, g_B, g_e, g_cum),
