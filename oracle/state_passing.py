@@ -6,7 +6,8 @@ of tests/test_mamba_cp.py:16-32, and ``cp_state_prefix`` / ``mamba2_cp_correctio
 (strategies/mamba.py:68-139), and the shard final state the CP scan wrapper gathers
 (``final`` of mamba.py:113-141,160-172, computed there by mamba-ssm's
 ``mamba_chunk_scan_combined``, a dependency absent from the reference tree).
-Autograd-capable (torch ops only).
+Autograd-capable (torch ops only); ``linear_scan_grads`` also gives the scan's gradients
+from the explicit adjoint recurrence, for sequences too long for an autograd graph.
 """
 
 from __future__ import annotations
@@ -63,6 +64,28 @@ def rank_linear_scan(a, b, h_in):
     (strategies/state_passing.py:38-39,59): the zero-init local scan corrected by
     ``cumprod(a) * h_in``. a, b: [batch, L_local, d]; h_in: [batch, d]."""
     return local_linear_scan(a, b) + torch.cumprod(a, dim=1) * h_in.unsqueeze(1)
+
+
+def linear_scan_grads(a, b, dh, h_in=None):
+    """h_t = a_t h_{t-1} + b_t from ``h_in`` (zero when None) and its gradients from the
+    adjoint recurrence g_t = dh_t + a_{t+1} g_{t+1}: db_t = g_t, da_t = g_t h_{t-1},
+    dh_in = a_0 g_0. Explicit (no autograd graph), vectorised over batch and channels with
+    a loop over t, for long sequences. a, b, dh: [batch, L, d]; returns (h, da, db, dh_in)."""
+    bsz, L, d = b.shape
+    prev = torch.zeros_like(b[:, 0]) if h_in is None else h_in.clone()
+    h_in0 = prev.clone()
+    h = torch.empty_like(b)
+    for t in range(L):
+        prev = a[:, t] * prev + b[:, t]
+        h[:, t] = prev
+    db = torch.empty_like(b)
+    g = torch.zeros_like(b[:, 0])
+    for t in range(L - 1, -1, -1):
+        g = dh[:, t] + (a[:, t + 1] * g if t + 1 < L else 0)
+        db[:, t] = g
+    h_before = torch.cat([h_in0[:, None], h[:, :-1]], dim=1)
+    da = db * h_before
+    return h, da, db, (a[:, 0] * db[:, 0] if L else torch.zeros_like(h_in0))
 
 
 def scan_prefix(a, b, world):

@@ -31,6 +31,7 @@ hipError_t launch_linear_scan_bwd(const float* a, const float* h, const float* h
 // L-parallel (chained) scan: channel tiling, chunk length and workspace layout of one shape
 struct ScanChunkPlan {
   int V, amode, cw_log2, lg_log2, CT, TC, ntiles, nchunks;
+  bool two_pass;  // reduce-then-rescan instead of the single pass with look-back
   size_t words_off, bytes;
 };
 ScanChunkPlan scan_chunk_plan(int batch, int L, int d, int groups);

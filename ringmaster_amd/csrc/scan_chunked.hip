@@ -28,6 +28,16 @@
 // after kSpinCap polls takes NaN as its carried-in state, so the outputs show the
 // failure and every workgroup still ends.
 //
+// A single pass costs about 200 ns of latency per chunk of a chain, which dominates when
+// few channels run over a long sequence (L = 65536, d = 256: 1024 chunks, 0.26 ms for
+// 30 us of traffic). There the same per-chunk code runs as reduce-then-rescan: pass 1
+// publishes each chunk's pair and stops, a fold kernel composes each channel's chain of
+// pairs in blocks (a wave per channel, a shuffle scan over 64 lanes of 16 chunks each)
+// and publishes the state after every chunk, and pass 2 rescans every chunk from the
+// state before it. The fold associates the chain differently from the look-back, so the
+// two forms differ in rounding (each is deterministic); the price is reading a and x
+// twice. The plan picks the form from the measured costs.
+//
 // The backward is the same machinery over the reversed sequence:
 //   g_t = dh_t + a_{t+1} g_{t+1}   (a scan from the end with decay a_{t+1}),
 //   db_t = g_t,  da_t += sum_group g_t h_{t-1} (h_{-1} = h_in),  dh_in = a_0 g_0.
@@ -75,7 +85,9 @@ __device__ __forceinline__ float word_val(uint64_t w) { return __uint_as_float((
 // Channel tile CT = CW * V with CW = 2^cw_log2 lanes per token group; a wave
 // holds 64 / CW token groups of kU tokens. lg_log2: lanes sharing one decay
 // group inside a token group (da reduction in the backward), -1 = none shared.
-template <int AMODE, int V, bool BWD>
+// PASS 0: single pass with look-back; 1: publish the chunk's pair only; 2: outputs from
+// the state the fold kernel left for the previous chunk.
+template <int AMODE, int V, bool BWD, int PASS>
 __global__ __launch_bounds__(256) void linear_scan_chunked_kernel(
     const float* __restrict__ a, const float* __restrict__ x, const float* __restrict__ hin,
     const float* __restrict__ hfwd, float* __restrict__ y, float* __restrict__ da,
@@ -89,9 +101,12 @@ __global__ __launch_bounds__(256) void linear_scan_chunked_kernel(
   __shared__ float s_totB[kWaves][256];
   __shared__ float s_carry[256];
 
-  if (threadIdx.x == 0) s_ticket = atomicAdd(w.counter, 1);
-  __syncthreads();
-  const int ticket = s_ticket;
+  if (PASS == 0) {
+    if (threadIdx.x == 0) s_ticket = atomicAdd(w.counter, 1);
+    __syncthreads();
+  }
+  // no chunk waits for another in passes 1 and 2: the dispatch order needs no ticket
+  const int ticket = PASS == 0 ? s_ticket : (int)blockIdx.x;
   const int nchains = batch * w.ntiles;
   const int chunk = ticket / nchains;
   const int chain = ticket - chunk * nchains;
@@ -215,11 +230,34 @@ __global__ __launch_bounds__(256) void linear_scan_chunked_kernel(
   }
 
   // chip: publish the chunk's pair, look back, publish the carried-out state
-  if (wv == 0) {
-    const int64_t s0 = (int64_t)chain * w.nchunks;
-    auto word = [&](int64_t k, int kind, int v) {
-      return w.words + ((s0 + k) * 3 + kind) * CT + cl * V + v;
-    };
+  const int64_t s0 = (int64_t)chain * w.nchunks;
+  auto word = [&](int64_t k, int kind, int v) {
+    return w.words + ((s0 + k) * 3 + kind) * CT + cl * V + v;
+  };
+  if (PASS == 1) {  // the chunk's pair for the fold kernel: nothing else
+    if (wv == 0 && tgw == 0 && cv) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        put_word(word(chunk, kWordA, v), CA[AMODE == 1 ? v : 0]);
+        put_word(word(chunk, kWordB, v), CB[v]);
+      }
+    }
+    return;
+  }
+  if (PASS == 2) {  // the state after the previous chunk, from the fold kernel
+    if (wv == 0 && tgw == 0) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        float X = 0.f;
+        if (chunk == 0)
+          X = (!BWD && hin && cv) ? hin[(int64_t)bb * d + c + v] : 0.f;
+        else if (cv)
+          X = word_val(get_word(word(chunk - 1, kWordS, v)));
+        s_carry[cl * V + v] = X;
+      }
+    }
+  }
+  if (PASS == 0 && wv == 0) {
     if (tgw == 0 && cv) {
 #pragma unroll
       for (int v = 0; v < V; ++v) {
@@ -378,6 +416,63 @@ __global__ void linear_scan_chunk_state_kernel(const uint64_t* __restrict__ word
   cp[d] = B;
 }
 
+// Reduce-then-rescan fold: each channel's chain of chunk pairs in scan order, the state
+// after chunk k published for chunk k + 1, S_{-1} = h_in (forward) or 0 (backward). One
+// wave per (chain, channel of the tile); the chain is taken in rounds of 64 x kFoldK
+// chunks: lane l composes its kFoldK consecutive pairs into one (all its loads issued at
+// once), a shuffle scan composes the 64 lanes' pairs, and each lane re-runs its chunks
+// from the state entering them. A round costs one load latency, not kFoldK x 64.
+constexpr int kFoldK = 16;
+
+__global__ __launch_bounds__(256) void linear_scan_chain_fold_kernel(
+    uint64_t* __restrict__ words, const float* __restrict__ hin, int batch, int d, int ntiles,
+    int nchunks, int CT) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = blockIdx.x * (int64_t)(blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (i >= (int64_t)batch * ntiles * CT) return;  // uniform over the wave
+  const int cc = (int)(i % CT);
+  const int64_t chain = i / CT;
+  const int bb = (int)(chain / ntiles), tile = (int)(chain % ntiles);
+  const int c = tile * CT + cc;
+  if (c >= d) return;
+  float carry = hin ? hin[(int64_t)bb * d + c] : 0.f;
+  uint64_t* w0 = words + (chain * nchunks * 3) * CT + cc;
+  for (int base = 0; base < nchunks; base += 64 * kFoldK) {
+    const int k0 = base + lane * kFoldK;
+    float Ak[kFoldK], Bk[kFoldK];
+#pragma unroll
+    for (int j = 0; j < kFoldK; ++j) {
+      const bool in = k0 + j < nchunks;
+      const uint64_t* wk = w0 + (int64_t)(in ? k0 + j : 0) * 3 * CT;
+      Ak[j] = in ? word_val(wk[kWordA * CT]) : 1.f;
+      Bk[j] = in ? word_val(wk[kWordB * CT]) : 0.f;
+    }
+    float PA = 1.f, PB = 0.f;  // the lane's chunks composed: x -> PA x + PB
+#pragma unroll
+    for (int j = 0; j < kFoldK; ++j) {
+      PB = __builtin_fmaf(Ak[j], PB, Bk[j]);
+      PA *= Ak[j];
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {  // inclusive: this lane's map after the lower ones
+      const float oA = __shfl_up(PA, off), oB = __shfl_up(PB, off);
+      if (lane >= off) {
+        PB = __builtin_fmaf(PA, oB, PB);
+        PA *= oA;
+      }
+    }
+    const float eA = __shfl_up(PA, 1), eB = __shfl_up(PB, 1);
+    float S = lane == 0 ? carry : __builtin_fmaf(eA, carry, eB);
+    const float next = __shfl(__builtin_fmaf(PA, carry, PB), 63);
+#pragma unroll
+    for (int j = 0; j < kFoldK; ++j) {
+      S = __builtin_fmaf(Ak[j], S, Bk[j]);
+      if (k0 + j < nchunks) put_word(w0 + (int64_t)(k0 + j) * 3 * CT + kWordS * CT, S);
+    }
+    carry = next;
+  }
+}
+
 __global__ void fill_zero_u32x4_kernel(u32x4* p, int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -413,6 +508,14 @@ ScanChunkPlan scan_chunk_plan(int batch, int L, int d, int groups) {
   p.lg_log2 = -1;
   if (lg > 1 && (lg & (lg - 1)) == 0 && (lanes_per_group % lg == 0)) p.lg_log2 = __builtin_ctz(lg);
   const int64_t slots = (int64_t)batch * p.ntiles * p.nchunks;
+  // Measured costs: the single pass takes its traffic plus about 200 ns per chunk of the
+  // chain (each chunk waits for its predecessor's published state); reduce-then-rescan
+  // reads the inputs twice (1.5x the forward's 8 bytes per element, at about 4.67 TB/s:
+  // elems / 584 ns) plus about 20 us of fold and launches. Two passes when
+  // 200 ns * nchunks > elems / 1168 ns + 20 us (both sides times 1168 below): few
+  // channels over long sequences.
+  const int64_t elems = (int64_t)batch * L * d;
+  p.two_pass = (int64_t)p.nchunks * 233600 > elems + (int64_t)20000 * 1168;
   p.words_off = 256;  // the ticket counter, then the words
   p.bytes = p.words_off + (size_t)slots * 3 * p.CT * 8;
   return p;
@@ -424,19 +527,15 @@ static ChunkWork carve(const ScanChunkPlan& p, void* ws) {
                    p.ntiles, p.nchunks};
 }
 
-template <bool BWD>
-static hipError_t launch_chunked(const ScanChunkPlan& p, const float* a, const float* x,
-                                 const float* hin, const float* hfwd, float* y, float* da,
-                                 float* dhin, void* ws, int batch, int L, int d, int groups,
-                                 hipStream_t stream) {
-  const ChunkWork w = carve(p, ws);
-  const int64_t n16 = (int64_t)(p.bytes / 16);  // the counter and every word
-  hipLaunchKernelGGL(fill_zero_u32x4_kernel, dim3((unsigned)std::min<int64_t>((n16 + 255) / 256, 2048)),
-                     dim3(256), 0, stream, reinterpret_cast<u32x4*>(ws), n16);
+template <bool BWD, int PASS>
+static void launch_pass(const ScanChunkPlan& p, const float* a, const float* x, const float* hin,
+                        const float* hfwd, float* y, float* da, float* dhin, const ChunkWork& w,
+                        int batch, int L, int d, int groups, hipStream_t stream) {
   const unsigned grid = (unsigned)((int64_t)batch * p.ntiles * p.nchunks);
-#define RMX_CHUNKED(AM, VV)                                                                     \
-  hipLaunchKernelGGL((linear_scan_chunked_kernel<AM, VV, BWD>), dim3(grid), dim3(256), 0, stream, \
-                     a, x, hin, hfwd, y, da, dhin, w, batch, L, d, groups, p.cw_log2, p.lg_log2)
+#define RMX_CHUNKED(AM, VV)                                                                      \
+  hipLaunchKernelGGL((linear_scan_chunked_kernel<AM, VV, BWD, PASS>), dim3(grid), dim3(256), 0,   \
+                     stream, a, x, hin, hfwd, y, da, dhin, w, batch, L, d, groups, p.cw_log2,     \
+                     p.lg_log2)
   if (p.amode == 1) {
     if (p.V == 4) RMX_CHUNKED(1, 4);
     else RMX_CHUNKED(1, 2);
@@ -446,6 +545,26 @@ static hipError_t launch_chunked(const ScanChunkPlan& p, const float* a, const f
     else RMX_CHUNKED(0, 1);
   }
 #undef RMX_CHUNKED
+}
+
+template <bool BWD>
+static hipError_t launch_chunked(const ScanChunkPlan& p, const float* a, const float* x,
+                                 const float* hin, const float* hfwd, float* y, float* da,
+                                 float* dhin, void* ws, int batch, int L, int d, int groups,
+                                 hipStream_t stream) {
+  const ChunkWork w = carve(p, ws);
+  const int64_t n16 = (int64_t)(p.bytes / 16);  // the counter and every word
+  hipLaunchKernelGGL(fill_zero_u32x4_kernel, dim3((unsigned)std::min<int64_t>((n16 + 255) / 256, 2048)),
+                     dim3(256), 0, stream, reinterpret_cast<u32x4*>(ws), n16);
+  if (!p.two_pass) {
+    launch_pass<BWD, 0>(p, a, x, hin, hfwd, y, da, dhin, w, batch, L, d, groups, stream);
+    return hipGetLastError();
+  }
+  launch_pass<BWD, 1>(p, a, x, hin, hfwd, y, da, dhin, w, batch, L, d, groups, stream);
+  const int64_t nf = (int64_t)batch * p.ntiles * p.CT;
+  hipLaunchKernelGGL(linear_scan_chain_fold_kernel, dim3((unsigned)((nf + 3) / 4)), dim3(256),
+                     0, stream, w.words, BWD ? nullptr : hin, batch, d, p.ntiles, p.nchunks, p.CT);
+  launch_pass<BWD, 2>(p, a, x, hin, hfwd, y, da, dhin, w, batch, L, d, groups, stream);
   return hipGetLastError();
 }
 

@@ -4,6 +4,9 @@
 channels: every channel tiling / decay mode of the kernel, ragged last chunks, a
 carried-in state and its gradient, shard chunk states, and the full L = 65536 case.
 
+Few chains with many chunks run as reduce-then-rescan, the others as one pass with
+decoupled look-back; both fold the same chain of chunk pairs.
+
 Decays close to 1 (a carried state falls to about e^-2 over one chunk) make the state
 carried across chunks matter: a look-back that dropped or reordered a chunk would be
 off by O(1). Such recurrences sum fp32 terms over the decay's memory, W = 1 / (1 - a)
@@ -57,6 +60,11 @@ def _inputs(batch, L, d, groups, seed, weak=True):
 
 def _oracle(a, b, dh, h_in, world):
     d, groups = b.shape[2], a.shape[2]
+    if world == 1:  # one rank: the recurrence from h_in with its explicit adjoint
+        af = a.repeat_interleave(d // groups, dim=2).double()
+        h, da, db, dhin = sp.linear_scan_grads(af, b.double(), dh.double(),
+                                               None if h_in is None else h_in.double())
+        return h, da.reshape(*a.shape, d // groups).sum(-1), db, None if h_in is None else dhin
     af = a.repeat_interleave(d // groups, dim=2).double().requires_grad_(True)
     bf = b.double().requires_grad_(True)
     if h_in is None:
@@ -147,6 +155,28 @@ def test_chunked_scan_long_sequence():
     a, b, dh, tol = _inputs(1, 65536, 256, 8, seed=45)
     h = _check(a, b, dh, tol, world=8, tag="L=65536")
     assert torch.isfinite(h).all()
+
+
+@pytest.mark.parametrize("d,groups,with_h_in", [(256, 8, True), (512, 8, False),
+                                                (256, 256, False)])
+def test_chunked_scan_reduce_then_rescan(d, groups, with_h_in):
+    """Shapes with few chains (here 1 or 2) and more than 256 chunks run as
+    reduce-then-rescan (each chunk's pair, a fold of each channel's chain of pairs, a
+    rescan from the folded state): values and gradients against fp64 (grouped and
+    elementwise decay, a carried-in state), and bit-equal repeated calls."""
+    L = 16500
+    # the two-pass side of the plan: a chain of hundreds of chunks over little data
+    assert -(-L // _chunk_tokens(1, d, groups)) > 256 and L * d < 3e7
+    a, b, dh, tol = _inputs(1, L, d, groups, seed=47 + d)
+    h_in = torch.randn(1, d, generator=torch.Generator().manual_seed(48)) if with_h_in else None
+    _check(a, b, dh, tol, h_in=h_in, tag=f"two-pass d={d} G={groups} L={L}")
+    from ringmaster_amd.strategies.state_passing import linear_scan_forward
+
+    ad, bd = a.cuda(), b.cuda()
+    h1 = linear_scan_forward(ad, bd, algo="chunked")
+    h2 = linear_scan_forward(ad, bd, algo="chunked")
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h2)
 
 
 def test_chunked_scan_repeated_calls_reuse_workspace():

@@ -722,6 +722,28 @@ def test_rank_linear_scan_is_the_recurrence_from_h_in():
     assert torch.allclose(stitched, sp.cp_linear_scan_emulated(a, b, world), atol=1e-12)
 
 
+@pytest.mark.parametrize("with_h_in", [False, True])
+def test_linear_scan_grads_is_autograd_of_the_scan(with_h_in):
+    """The explicit adjoint scan (values, da, db, dh_in) against torch autograd through
+    the per-token recurrence of local_linear_scan / rank_linear_scan (fp64), also at L = 1."""
+    g = torch.Generator().manual_seed(5)
+    for bsz, L, d in ((2, 37, 6), (1, 1, 3)):
+        a = (torch.rand(bsz, L, d, generator=g, dtype=torch.float64) * 1.2 - 0.1).requires_grad_(True)
+        b = torch.randn(bsz, L, d, generator=g, dtype=torch.float64).requires_grad_(True)
+        dh = torch.randn(bsz, L, d, generator=g, dtype=torch.float64)
+        h_in = torch.randn(bsz, d, generator=g, dtype=torch.float64).requires_grad_(True)
+        ref = sp.rank_linear_scan(a, b, h_in) if with_h_in else sp.local_linear_scan(a, b)
+        wrt = (a, b, h_in) if with_h_in else (a, b)
+        grads = torch.autograd.grad(ref, wrt, dh)
+        h, da, db, dhin = sp.linear_scan_grads(a.detach(), b.detach(), dh,
+                                               h_in.detach() if with_h_in else None)
+        assert torch.allclose(h, ref, atol=1e-12, rtol=1e-12)
+        assert torch.allclose(da, grads[0], atol=1e-12, rtol=1e-12)
+        assert torch.allclose(db, grads[1], atol=1e-12, rtol=1e-12)
+        if with_h_in:
+            assert torch.allclose(dhin, grads[2], atol=1e-12, rtol=1e-12)
+
+
 def test_effective_dt_rules():
     """The shard scan's step (mamba.py:143-148) against values fixed by the reference's
     text: the bias is added with or without softplus, negative steps clamp to the default
