@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 14 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 15 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
                               8: allocation-free Mamba2 correction bwd;
                               9: carried-in state h_in / dh_in of the linear scan;
@@ -36,7 +36,8 @@ extern "C" {
                               11: sliding windows, attention head_dim any multiple of 8
                                   up to 128; 12: fp16 attention (layout dtype);
                               13: attention dropout;
-                              14: workspace of the Mamba2 shard-state backward */
+                              14: workspace of the Mamba2 shard-state backward;
+                              15: attention head_dim up to 256 */
 
 /* error codes */
 #define RMX_OK 0
@@ -87,8 +88,8 @@ extern "C" {
 /* Layout shared by every problem of one batched attention call. */
 typedef struct rmx_attn_layout {
   int32_t batch, hq, hkv;           /* hq % hkv == 0 (GQA: kv_head = q_head / (hq/hkv)) */
-  int32_t head_dim;                 /* a multiple of 8, at most 128: the kernels compute at 64
-                                       or 128 and read the columns past head_dim as zeros */
+  int32_t head_dim;                 /* a multiple of 8, at most 256: the kernels compute at 64,
+                                       128 or 256 and read the columns past head_dim as zeros */
   float scale;                      /* softmax scale (1/sqrt(head_dim) by default) */
   int32_t mask;                     /* RMX_MASK_* */
   int32_t dtype;                    /* RMX_DTYPE_*: the 16-bit tensors ("bf16" below) hold this

@@ -39,8 +39,8 @@ int check_layout(const rmx_attn_layout* L) {
   if (L->hq % L->hkv)
     return fail(RMX_EINVAL, "Query heads must be divisible by KV heads (hq=%d hkv=%d)", L->hq,
                 L->hkv);
-  if (L->head_dim <= 0 || L->head_dim > 128 || L->head_dim % 8)
-    return fail(RMX_EUNSUPPORTED, "head_dim %d is not supported (a multiple of 8, at most 128)",
+  if (L->head_dim <= 0 || L->head_dim > 256 || L->head_dim % 8)
+    return fail(RMX_EUNSUPPORTED, "head_dim %d is not supported (a multiple of 8, at most 256)",
                 L->head_dim);
   if (!(L->scale > 0.f) || !std::isfinite(L->scale))
     return fail(RMX_EINVAL, "softmax scale must be finite and positive (got %g)", (double)L->scale);

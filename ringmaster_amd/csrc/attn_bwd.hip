@@ -115,7 +115,11 @@ hipError_t launch_attn_bwd_delta(const rmx_attn_layout& L, const void* out, int 
   const int64_t rows = (int64_t)L.batch * sq * L.hq;
   if (rows == 0) return hipSuccess;
   const bool f16 = L.dtype == RMX_DTYPE_F16;
-  if (L.head_dim > 64 && f16)
+  if (L.head_dim > 128 && f16)
+    launch_delta_t<256, RMX_DTYPE_F16>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
+  else if (L.head_dim > 128)
+    launch_delta_t<256, RMX_DTYPE_BF16>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
+  else if (L.head_dim > 64 && f16)
     launch_delta_t<128, RMX_DTYPE_F16>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
   else if (L.head_dim > 64)
     launch_delta_t<128, RMX_DTYPE_BF16>(L, out, out_f32, dout, delta, lse, nlse, sq, rows, stream);
@@ -168,16 +172,26 @@ struct BwdTiles {
 // (swizzle folded in) plus a compile-time offset below 64 KiB, with no address
 // arithmetic in the loop. Tiles past the end are issued as zero-length loads,
 // which keeps every wait count static.
+// At head dim 256 a workgroup is 4 waves (one per SIMD: Q, dO and the dQ accumulator
+// take 256 registers) with two tile buffers (a K or V tile is then 32 KiB).
+template <int HD>
+struct DqCfg {
+  static constexpr int NW = HD == 256 ? 4 : 8;  // waves per workgroup
+  static constexpr int NT = NW * 64;
+  static constexpr int BQ = 32 * NW;            // queries per workgroup
+  static constexpr int NB = HD == 256 ? 2 : RMX_DQ_NB;
+};
+
 template <int HD, int MASK, int DT, bool DROP>
-__global__ __launch_bounds__(512, 1) void attn_bwd_dq_kernel(const BwdParams prm) {
+__global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const BwdParams prm) {
   using T = BwdTiles<HD>;
-  constexpr int NW = 8, NT = NW * 64, BQ = 32 * NW, BK = 64;
+  constexpr int NW = DqCfg<HD>::NW, NT = DqCfg<HD>::NT, BQ = DqCfg<HD>::BQ, BK = 64;
   constexpr int CH = T::CH, NKB = T::NKB, NDB = T::NDB;
   constexpr int RB = HD * 2;              // LDS row bytes (unpadded, swizzled)
   constexpr int KT = BK * RB;             // bytes of one K (or V) tile
   constexpr int RPK = 1024 / RB;          // rows per 1 KiB DMA instruction
   constexpr int NDMA = KT / 1024 / NW;    // DMA instructions per wave, tile and operand
-  constexpr int NB = RMX_DQ_NB;           // tile buffers
+  constexpr int NB = DqCfg<HD>::NB;       // tile buffers
   // K tiles at [0, NB KT), V tiles after them; V rows get their own base register when
   // the last V tile would sit past the 16-bit LDS instruction offset
   constexpr bool VBASE = 2 * NB * KT - KT / 2 > 65535;
@@ -1105,10 +1119,428 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   }
 }
 
+// ---------------------------------------------------------------- dK, dV at head dim 256
+// The pipelined kernel above does not fit at head dim 256: its four 64-query Q/dO tile
+// buffers take 256 KiB of LDS at 512-byte rows, and K, -V and a wave's dK and dV
+// accumulators (32 keys x 256 columns each) take 384 registers before S and dP'.
+// This form computes the same per-element math with 32-query tiles and the K block
+// resident in LDS. One workgroup = 128 keys of one (problem, batch, kv head), 4 waves
+// (one per SIMD); wave w owns keys k0 + 32 w .. + 31 and, per (q head, query tile):
+//   S   = Q K^T          A = Q rows (LDS, rows sigma-permuted), B = K rows (LDS)
+//   dP' = delta - dO V^T A = dO rows (LDS), B = -V (registers); the accumulator
+//                        starts at delta (at 0 with dropout: delta enters the packs)
+//   P   = exp2(S c + nl)  (masked pairs: S := -inf first, nl kept finite)
+//   dV += P^T dO         A = P^T (registers), B = dO^T (transposed LDS reads)
+//   dK -= (P dP')^T Q    A = (P dP')^T, B = Q^T (transposed LDS reads)
+// 64 MFMAs per tile and wave. The K block arrives once by LDS DMA (64 KiB, rows
+// swizzled by their index mod 16, conflict-free for reads of one chunk of 16 rows);
+// Q/dO tiles (+ nl, delta) by LDS DMA into two buffers, tile j + 1 in flight while
+// tile j is computed, one barrier per tile.
+template <int MASK, int DT, bool DROP>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdParams prm) {
+  constexpr int HD = 256, NW = 4, NT = 64 * NW, BKV = 32 * NW, BQ = 32, NB = 2;
+  constexpr int CH = HD / 8, RB = 2 * HD, QT = BQ * RB, RPK = 1024 / RB;
+  constexpr int NDMA = QT / 1024 / NW;        // DMA instructions per wave, tile and operand
+  constexpr int KDMA = BKV * RB / 1024 / NW;  // DMA instructions per wave for the K block
+  constexpr int NKB = HD / 16, NDB = HD / 32;
+  static_assert(NDMA >= 1 && QT % (1024 * NW) == 0 && KDMA >= 1, "tile split");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t sK[BKV * RB];
+  __shared__ __attribute__((aligned(1024))) uint8_t sQ[NB][QT];
+  __shared__ __attribute__((aligned(1024))) uint8_t sO[NB][QT];
+  __shared__ __attribute__((aligned(256))) float sM[NB][2][64];  // nl, delta (a DMA writes 64)
+  __shared__ int sQg[NB][BQ];
+  __shared__ int sQd[NB][BQ];
+  __shared__ int sRange[2];
+
+  const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
+  if (!wc.valid) return;
+  const rmx_attn_layout& L = prm.L;
+  const rmx_bwd_problem& P = prm.P[wc.p];
+  const int kvh = wc.group % L.hkv;
+  const int bb = wc.group / L.hkv;
+  const int G = L.hq / L.hkv;
+  const int sq = P.sq, sk = P.sk;
+  constexpr int mask = MASK;
+  const int k0 = wc.tile * BKV;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int kw0 = k0 + 32 * wave;  // first key of this wave
+  const int key = kw0 + l32;
+  const bool kvalid = key < sk;
+
+  // ---- query-tile range of the workgroup (as in the kernel above)
+  const int D = L.head_dim;        // columns past D (up to HD) load as zeros
+  const int wl = window_bound(P);  // pos_q - pos_k <= wl
+  const int off = sk - sq;
+  const int klast = (k0 + BKV < sk ? k0 + BKV : sk) - 1;
+  const int nqt = (sq + BQ - 1) / BQ;
+  int qt_begin = 0, qt_end = nqt;
+  int kg_first = 0, kg_last = 0, kd_first = 0, kd_last = 0;
+  if (mask != RMX_MASK_DOC) {
+    if (mask == RMX_MASK_CAUSAL) {
+      const int qmin = k0 - off;  // first query that sees key k0
+      qt_begin = qmin <= 0 ? 0 : qmin / BQ;
+      if (qt_begin > nqt) qt_begin = nqt;
+    }
+    const int qmax = klast + wl - off;  // last query whose window reaches key klast
+    qt_end = qmax < 0 ? 0 : (qmax / BQ + 1 < nqt ? qmax / BQ + 1 : nqt);
+    if (qt_end < qt_begin) qt_end = qt_begin;
+  } else {
+    kg_first = P.k_gidx[k0];
+    kg_last = P.k_gidx[klast];
+    kd_first = P.k_doc[k0];
+    kd_last = P.k_doc[klast];
+    if (tid == 0) {
+      sRange[0] = nqt;
+      sRange[1] = -1;
+    }
+    __syncthreads();
+    int lo = nqt, hi = -1;
+    for (int t = tid; t < nqt; t += NT) {
+      const int qa = t * BQ, qz = (t * BQ + BQ < sq ? t * BQ + BQ : sq) - 1;
+      const int qga = P.q_gidx[qa], qgz = P.q_gidx[qz];
+      const int qda = P.q_doc[qa], qdz = P.q_doc[qz];
+      if (qgz >= kg_first && qdz >= kd_first && qda <= kd_last && (int64_t)qga <= (int64_t)kg_last + wl) {
+        lo = t < lo ? t : lo;
+        hi = t > hi ? t : hi;
+      }
+    }
+    if (lo < nqt) atomicMin(&sRange[0], lo);
+    if (hi >= 0) atomicMax(&sRange[1], hi);
+    __syncthreads();
+    qt_begin = sRange[0];
+    qt_end = sRange[1] + 1;
+    if (qt_end < qt_begin) qt_end = qt_begin;
+  }
+  const int ntile = (qt_end - qt_begin) * G;  // (q head, query tile) pairs, q head major
+  // no query tile: accumulated dK and dV keep their values
+  if (ntile == 0 && P.dkv_mode == RMX_GRAD_ACC_F32) return;
+  const int wave_klast = (kw0 + 31 < sk ? kw0 + 31 : sk - 1);
+
+  struct Cursor {
+    int qt, hi;
+  };
+  auto advance = [&](Cursor c) -> Cursor {
+    if (++c.qt == qt_end) {
+      c.qt = qt_begin;
+      ++c.hi;
+    }
+    return c;
+  };
+
+  // ---- tile loads: wave 0 loads the tile's nl and delta, every wave its share of the
+  // Q and dO rows (instruction n fills LDS bytes [1024 n, 1024 n + 1024), lane L row
+  // n*RPK + L/CH, swizzled chunk L%CH); rows past the end read as zeros
+  const int qss = (int)(2 * L.q_ss), oss = (int)(2 * L.o_ss);
+  const uint8_t* const qb0 = reinterpret_cast<const uint8_t*>(P.q + bb * L.q_sb + (int64_t)kvh * G * L.q_sh);
+  const uint8_t* const ob0 = reinterpret_cast<const uint8_t*>(P.dout + bb * L.o_sb + (int64_t)kvh * G * L.o_sh);
+  const uint8_t* const nb0 = reinterpret_cast<const uint8_t*>(P.nlse + bb * L.l_sb + (int64_t)kvh * G * L.l_sh);
+  const uint8_t* const db0 = reinterpret_cast<const uint8_t*>(P.delta + bb * L.l_sb + (int64_t)kvh * G * L.l_sh);
+  const int qhs = (int)(2 * L.q_sh), ohs = (int)(2 * L.o_sh), lhs = (int)(4 * L.l_sh);
+  const uint32_t qspan = span_bytes(sq, qss, D * 2), ospan = span_bytes(sq, oss, D * 2);
+  int vq[NDMA], vo[NDMA];
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int n = wave * NDMA + i;
+    const int r = n * RPK + lane / CH, ch = (lane % CH) ^ swz_both<HD>(r);
+    vq[i] = 8 * ch < D ? r * qss + 16 * ch : kOutOfRange;
+    vo[i] = 8 * ch < D ? r * oss + 16 * ch : kOutOfRange;
+  }
+  auto dma_tile = [&](int b, Cursor cu) {
+    const int qa = cu.qt * BQ;
+    if (wave == 0) {
+      const int lo = cu.hi * lhs + 4 * qa;
+      const uint32_t n = 4u * (uint32_t)(sq - qa);
+      dma4_async(make_rsrc(nb0 + lo, n), lds_addr(&sM[b][0][0]), 4 * lane);
+      dma4_async(make_rsrc(db0 + lo, n), lds_addr(&sM[b][1][0]), 4 * lane);
+    }
+    const i32x4 qrs = make_rsrc(qb0 + cu.hi * qhs + qa * qss, qspan - (uint32_t)(qa * qss));
+    const i32x4 ors = make_rsrc(ob0 + cu.hi * ohs + qa * oss, ospan - (uint32_t)(qa * oss));
+    const uint32_t qd = lds_addr(&sQ[b][0]), od = lds_addr(&sO[b][0]);
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      const int n = wave * NDMA + i;
+      dma16_async(qrs, qd + 1024 * n, vq[i]);
+      dma16_async(ors, od + 1024 * n, vo[i]);
+    }
+  };
+  int nqg = 0, nqd = 0;
+  auto doc_load = [&](Cursor cu) {
+    if (mask == RMX_MASK_DOC && tid < BQ) {
+      const int qq = cu.qt * BQ + tid;
+      if (qq < sq) {
+        nqg = P.q_gidx[qq];
+        nqd = P.q_doc[qq];
+      } else {
+        nqg = -2147483647;  // rows past the end: masked
+        nqd = -1;
+      }
+    }
+  };
+  auto doc_store = [&](int slot) {
+    if (mask == RMX_MASK_DOC && tid < BQ) {
+      sQg[slot][tid] = nqg;
+      sQd[slot][tid] = nqd;
+    }
+  };
+
+  // ---- the K block (rows k0 .. k0 + BKV - 1) into LDS, once; -V of this wave's keys in
+  // registers (lane: key row, dims 16 kb + 8 hl ..), MFMA operands from AGPRs
+  {
+    const int kss = (int)(2 * L.k_ss);
+    const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, D * 2));
+    const uint32_t kd = lds_addr(sK);
+#pragma unroll
+    for (int i = 0; i < KDMA; ++i) {
+      const int n = wave * KDMA + i;
+      const int r = n * RPK + lane / CH, c = (lane % CH) ^ (r & 15);
+      dma16_async(krs, kd + 1024 * n, 8 * c < D ? (k0 + r) * kss + 16 * c : kOutOfRange);
+    }
+  }
+  bf16x8 vreg[NKB];
+  {
+    const int vss = (int)(2 * L.v_ss);
+    const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, D * 2));
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int col = 16 * kb + 8 * hl;
+      vreg[kb] = __builtin_bit_cast(
+          bf16x8, cols_below(buf_load16(vrs, key * vss + 16 * hl + 32 * kb) ^ 0x80008000u, col, D));
+    }
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) asm volatile("" : "+a"(vreg[kb]));
+  }
+  int kg = 2147483647, kd = -2;
+  if (mask == RMX_MASK_DOC && kvalid) {
+    kg = P.k_gidx[key];
+    kd = P.k_doc[key];
+  }
+  // this lane's highest query: q + off <= key + wl (document masks: global index <= khi)
+  const int khi = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg + wl) : key + wl - off;
+  const int khi_first = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg_first + wl) : 0;
+
+  // per-lane LDS byte offsets, swizzle folded in. A chunk index below 16 keeps a
+  // lane's offset inside a row's first 256 bytes, so the upper 8 chunk pairs of a row
+  // (k-steps 8..15, d blocks 4..7) are the lower ones plus 256: compile-time offsets.
+  //   raddr: Q / dO rows (A of S, dP'): query row sigma(l32), chunk 2 kb + hl
+  //   kaddr: K rows (B of S): key row 32 wave + l32, chunk 2 kb + hl
+  //   taddr: transposed reads (B of dV, dK): query rows 16 kb2 + 8 hl + 4 t + (m >> 2),
+  //          columns 32 db + 16 x + 4 (m & 3) .. + 3, m = lane & 15, x = (lane >> 4) & 1
+  int raddr[8], kaddr[8], taddr[2][4];
+  {
+    const int sr = sigma(l32);
+    const int rbase = sr * RB + 16 * (hl ^ swz_both<HD>(sr));
+    const int kr = 32 * wave + l32;
+    const int kbase = kr * RB + 16 * (hl ^ (kr & 15));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      raddr[i] = rbase ^ (32 * i);
+      kaddr[i] = kbase ^ (32 * i);
+    }
+    const int m16 = lane & 15, x16 = (lane >> 4) & 1;
+    const int cc = 2 * x16 + ((m16 & 3) >> 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = 8 * hl + 4 * t + (m16 >> 2);
+      const int base = r * RB + 16 * (cc ^ swz_both<HD>(r)) + 8 * (m16 & 1);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) taddr[t][db] = base ^ (64 * db);
+    }
+  }
+  auto row_op = [&](const uint8_t* tile, int kb) -> bf16x8 {
+    return __builtin_bit_cast(
+        bf16x8, *reinterpret_cast<const u32x4*>(tile + raddr[kb & 7] + 256 * (kb >> 3)));
+  };
+  auto k_op = [&](int kb) -> bf16x8 {
+    return __builtin_bit_cast(
+        bf16x8, *reinterpret_cast<const u32x4*>(sK + kaddr[kb & 7] + 256 * (kb >> 3)));
+  };
+  auto tr_op = [&](const uint8_t* tile, int kb2, int db) -> bf16x8 {
+    const uint8_t* p = tile + 16 * kb2 * RB + 256 * (db >> 2);
+    return join_bf16x8(lds_read_tr(reinterpret_cast<const uint16_t*>(p + taddr[0][db & 3])),
+                       lds_read_tr(reinterpret_cast<const uint16_t*>(p + taddr[1][db & 3])));
+  };
+
+  // dropout: the keep bits of a tile's 16 elements of this lane (bit r: query
+  // sig_row(hl, r) of the tile, key `key`), hashed as the forward does
+  const uint32_t dk_term = DROP ? (uint32_t)(key + P.drop_k0) * kDropK : 0u;
+  auto drop_word = [&](int qa, int hi) -> uint32_t {
+    uint32_t mw = 0;
+    const uint32_t bk = drop_bhmix(L, bb, kvh * G + hi) ^ dk_term;
+    const uint32_t base = (uint32_t)(qa + P.drop_q0) * kDropQ + (uint32_t)(8 * hl) * kDropQ;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const uint32_t qc = (uint32_t)(16 * (r >> 3) + (r & 7)) * kDropQ;
+      if (drop_keep(bk, base + qc, prm.drop_thr)) mw |= 1u << r;
+    }
+    return mw;
+  };
+  // per-query metadata in the accumulator layout: element r is query sig_row(hl, r)
+  auto load_rows = [&](const float* m, f32x16& dst) {
+#pragma unroll
+    for (int h8 = 0; h8 < 2; ++h8) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(m + 16 * h8 + 8 * hl);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(m + 16 * h8 + 8 * hl + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dst[8 * h8 + i] = a[i];
+        dst[8 * h8 + 4 + i] = b[i];
+      }
+    }
+  };
+  auto need_mask_of = [&](int qa, int slot) -> bool {
+    bool m = (kw0 + 32 > sk);
+    const int qz = (qa + BQ < sq ? BQ : sq - qa) - 1;
+    if (mask == RMX_MASK_CAUSAL) m |= (wave_klast > qa + off);
+    if (mask != RMX_MASK_DOC) m |= (qa + qz + off - kw0 > wl);
+    if (mask == RMX_MASK_DOC) {
+      const int qga = sQg[slot][0], qgz = sQg[slot][qz];
+      const int qda = sQd[slot][0], qdz = sQd[slot][qz];
+      m |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga &&
+             qgz <= khi_first);
+    }
+    return m;
+  };
+  auto apply_mask = [&](int qa, int slot, f32x16& s, f32x16& nl) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ql = sig_row(hl, r);
+      bool ok = kvalid;
+      if (mask == RMX_MASK_CAUSAL) ok &= key <= qa + ql + off;
+      if (mask != RMX_MASK_DOC) ok &= qa + ql <= khi;
+      if (mask == RMX_MASK_DOC)
+        ok &= (sQd[slot][ql] == kd) & (kg <= sQg[slot][ql]) & (sQg[slot][ql] <= khi);
+      s[r] = ok ? s[r] : kNegInf;
+      nl[r] = fminf(nl[r], 3.0e38f);
+    }
+  };
+  // P^T (y == nullptr) or (P dP')^T block ks: words w = elements 8 ks + 2 w, + 1. With
+  // dropout (keep scale m = M / (1 - p)): P m, and P (delta + m y) with y = -dO V^T
+  auto pack = [&](const f32x16& x, const f32x16* y, const f32x16& dl, uint32_t mw, int ks) {
+    u32x4 u;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int r = 8 * ks + 2 * w;
+      float v0 = x[r], v1 = x[r + 1];
+      if constexpr (DROP) {
+        const float m0 = (mw >> r) & 1u ? prm.drop_scale : 0.f;
+        const float m1 = (mw >> (r + 1)) & 1u ? prm.drop_scale : 0.f;
+        if (y) {
+          v0 *= fmaf(m0, (*y)[r], dl[r]);
+          v1 *= fmaf(m1, (*y)[r + 1], dl[r + 1]);
+        } else {
+          v0 *= m0;
+          v1 *= m1;
+        }
+      } else if (y) {
+        v0 *= (*y)[r];
+        v1 *= (*y)[r + 1];
+      }
+      u[w] = cvt_pk<DT>(v0, v1);
+    }
+    return __builtin_bit_cast(bf16x8, u);
+  };
+
+  // ---- prologue: the K block, tiles 0 and 1 issued; tile 0's documents in LDS
+  Cursor cur = {qt_begin, 0};
+  Cursor nx1 = advance(cur), nx2 = advance(nx1);
+  if (ntile > 0) dma_tile(0, cur);
+  if (ntile > 1) dma_tile(1, nx1);
+  doc_load(cur);
+  doc_store(0);
+  wait_all_loads();
+  lds_barrier();
+
+  f32x16 dv[NDB], dk[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    dv[db] = zero16();
+    dk[db] = zero16();
+  }
+  const float c = prm.scale_log2;
+  for (int j = 0; j < ntile; ++j) {
+    const int b = j & 1;
+    const int qa = cur.qt * BQ;
+    if (j + 1 < ntile) doc_load(nx1);
+    f32x16 s = zero16(), dp, nl, dl;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) s = mfma32t<DT>(row_op(sQ[b], kb), k_op(kb), s);
+    if constexpr (DROP) {
+      load_rows(&sM[b][1][0], dl);
+      dp = zero16();
+    } else {
+      load_rows(&sM[b][1][0], dp);
+    }
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) dp = mfma32t<DT>(row_op(sO[b], kb), vreg[kb], dp);
+    load_rows(&sM[b][0][0], nl);
+    if (need_mask_of(qa, b)) apply_mask(qa, b, s, nl);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], c, nl[r]));
+    const uint32_t mw = DROP ? drop_word(qa, cur.hi) : 0u;
+    bf16x8 pt[2], dst[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      pt[ks] = pack(s, nullptr, dl, mw, ks);
+      dst[ks] = pack(s, &dp, dl, mw, ks);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) dv[db] = mfma32t<DT>(pt[ks], tr_op(sO[b], ks, db), dv[db]);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) dk[db] = mfma32t<DT>(dst[ks], tr_op(sQ[b], ks, db), dk[db]);
+    // hand-over: tile j + 1 has landed in every wave and buffer b is free for tile j + 2
+    if (j + 1 < ntile) doc_store(b ^ 1);
+    wait_vm_barrier<0>();
+    if (j + 2 < ntile) dma_tile(b, nx2);
+    cur = nx1;
+    nx1 = nx2;
+    nx2 = advance(nx2);
+  }
+  wait_all_loads();
+
+  // ---- epilogue: lane (hl, l32) holds column d = 32 db + l32 of keys kw0 + c_row(hl, r)
+  const int mode = P.dkv_mode;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const float sc = g == 0 ? 1.f : -L.scale;
+    float* gacc = g == 0 ? P.dv_acc : P.dk_acc;
+    uint16_t* gbf = g == 0 ? P.dv : P.dk;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int d = 32 * db + l32;
+      if (d >= D) continue;  // columns past the head dim are not stored
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk = kw0 + c_row(hl, r);
+        if (kk >= sk) continue;
+        const float gv = (g == 0 ? dv[db][r] : dk[db][r]) * sc;
+        const int64_t ao = bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + d;
+        const int64_t bo = bb * L.dk_sb + (int64_t)kk * L.dk_ss + kvh * L.dk_sh + d;
+        if (mode == RMX_GRAD_WRITE_F32) {
+          gacc[ao] = gv;
+        } else if (mode == RMX_GRAD_ACC_F32) {
+          gacc[ao] += gv;
+        } else if (mode == RMX_GRAD_ACC_FINAL) {
+          gbf[bo] = f2e<DT>(gacc[ao] + gv);
+        } else {
+          gbf[bo] = f2e<DT>(gv);
+        }
+      }
+    }
+  }
+}
+
 template <int HD, int DT, bool DROP>
 static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                                hipStream_t stream) {
-  constexpr int BQ_DQ = 256, BKV = DkdvCfg<HD>::BKV;
+  constexpr int BQ_DQ = DqCfg<HD>::BQ, BKV = HD == 256 ? 128 : DkdvCfg<HD>::BKV;
   BwdParams pq, pk;
   pq.L = L;
   pk.L = L;
@@ -1148,7 +1580,18 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
     ntile[i] = (pk.P[i].sk + BKV - 1) / BKV;
   }
   const int tk = plan_workgroups(pk.map, nk, groups, ntile);
-  if (tk > 0) {
+  if (tk > 0 && HD == 256) {
+    const dim3 grid(tk);
+    if (L.mask == RMX_MASK_CAUSAL)
+      hipLaunchKernelGGL((attn_bwd_dkdv_d256_kernel<RMX_MASK_CAUSAL, DT, DROP>), grid, dim3(256), 0, stream, pk);
+    else if (L.mask == RMX_MASK_DOC)
+      hipLaunchKernelGGL((attn_bwd_dkdv_d256_kernel<RMX_MASK_DOC, DT, false>), grid, dim3(256), 0, stream, pk);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkdv_d256_kernel<RMX_MASK_FULL, DT, DROP>), grid, dim3(256), 0, stream, pk);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  } else if constexpr (HD != 256) {
+    if (tk > 0) {
     const dim3 grid(tk);
     if (L.mask == RMX_MASK_CAUSAL)
       hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL, DT, DROP>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
@@ -1158,35 +1601,37 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
       hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_FULL, DT, DROP>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    }
   }
   if (tq > 0) {
     const dim3 grid(tq);
     if (L.mask == RMX_MASK_CAUSAL)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_CAUSAL, DT, DROP>), grid, dim3(512), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_CAUSAL, DT, DROP>), grid, dim3(DqCfg<HD>::NT), 0, stream, pq);
     else if (L.mask == RMX_MASK_DOC)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_DOC, DT, false>), grid, dim3(512), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_DOC, DT, false>), grid, dim3(DqCfg<HD>::NT), 0, stream, pq);
     else
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_FULL, DT, DROP>), grid, dim3(512), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_FULL, DT, DROP>), grid, dim3(DqCfg<HD>::NT), 0, stream, pq);
     return hipGetLastError();
   }
   return hipSuccess;
 }
 
+template <int DT, bool DROP>
+static hipError_t launch_bwd_hd(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
+                                hipStream_t stream) {
+  if (L.head_dim > 128) return launch_bwd_t<256, DT, DROP>(L, probs, n, stream);
+  if (L.head_dim > 64) return launch_bwd_t<128, DT, DROP>(L, probs, n, stream);
+  return launch_bwd_t<64, DT, DROP>(L, probs, n, stream);
+}
+
 hipError_t launch_attn_bwd(const rmx_attn_layout& L, const rmx_bwd_problem* probs, int n,
                            hipStream_t stream) {
-  const bool big = L.head_dim > 64, f16 = L.dtype == RMX_DTYPE_F16, drop = L.dropout_p > 0.f;
-  if (drop) {
-    if (f16)
-      return big ? launch_bwd_t<128, RMX_DTYPE_F16, true>(L, probs, n, stream)
-                 : launch_bwd_t<64, RMX_DTYPE_F16, true>(L, probs, n, stream);
-    return big ? launch_bwd_t<128, RMX_DTYPE_BF16, true>(L, probs, n, stream)
-               : launch_bwd_t<64, RMX_DTYPE_BF16, true>(L, probs, n, stream);
-  }
-  if (f16)
-    return big ? launch_bwd_t<128, RMX_DTYPE_F16, false>(L, probs, n, stream)
-               : launch_bwd_t<64, RMX_DTYPE_F16, false>(L, probs, n, stream);
-  return big ? launch_bwd_t<128, RMX_DTYPE_BF16, false>(L, probs, n, stream)
-             : launch_bwd_t<64, RMX_DTYPE_BF16, false>(L, probs, n, stream);
+  const bool f16 = L.dtype == RMX_DTYPE_F16, drop = L.dropout_p > 0.f;
+  if (drop)
+    return f16 ? launch_bwd_hd<RMX_DTYPE_F16, true>(L, probs, n, stream)
+               : launch_bwd_hd<RMX_DTYPE_BF16, true>(L, probs, n, stream);
+  return f16 ? launch_bwd_hd<RMX_DTYPE_F16, false>(L, probs, n, stream)
+             : launch_bwd_hd<RMX_DTYPE_BF16, false>(L, probs, n, stream);
 }
 
 }  // namespace rmx

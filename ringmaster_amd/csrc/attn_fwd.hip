@@ -9,7 +9,9 @@
 //
 // Work decomposition: one workgroup = 8 waves = 256 queries of one
 // (problem, batch, head); each wave owns 32 queries and walks the key tiles
-// (64 keys) that the mask leaves.
+// (64 keys) that the mask leaves. At head dim 256 a workgroup is 4 waves (one per
+// SIMD: the Q operand and the O accumulator alone take 192 registers) and a key tile
+// 32 keys (the seven tile buffers then take 112 KiB of LDS).
 //
 // Each wave runs a software pipeline over the key tiles (v_mfma_f32_32x32x16_bf16);
 // iteration j holds S_j = (K_j Q^T)^T (masked, its row max folded in) and does
@@ -51,10 +53,10 @@ struct FwdParams {
 
 template <int HD>
 struct FwdCfg {
-  static constexpr int NW = 8;                // waves per workgroup
+  static constexpr int NW = HD == 256 ? 4 : 8;  // waves per workgroup
   static constexpr int NT = NW * 64;
   static constexpr int BQ = 32 * NW;          // queries per workgroup
-  static constexpr int BK = 64;               // keys per tile
+  static constexpr int BK = HD == 256 ? 32 : 64;  // keys per tile
   static constexpr int MB = BK / 32;          // 32-key blocks of S^T per tile
   static constexpr int CH = HD / 8;           // 16-byte chunks per row
   static constexpr int RB = HD * 2;           // LDS row bytes (unpadded, swizzled)
@@ -63,13 +65,14 @@ struct FwdCfg {
   static constexpr int NDMA = KT / 1024 / NW; // DMA instructions per wave per tile (K; same for V)
   static constexpr int NKB = HD / 16;         // k-steps of S^T
   static constexpr int NDB = HD / 32;         // 32-row blocks of O^T
+  static constexpr int MDOC = BK < 64 ? 64 : BK;  // key metadata slots (a DMA writes 64)
   static_assert(NDMA >= 1 && KT % (1024 * NW) == 0, "tile split");
 };
 
 constexpr float kRescaleSlack = 8.0f;  // log2 units: P <= 2^8 between rescales
 
 template <int HD, int MASK, int DT, bool DROP>
-__global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
+__global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdParams prm) {
   using C = FwdCfg<HD>;
   constexpr int BK = C::BK, MB = C::MB, NKB = C::NKB, NDB = C::NDB, CH = C::CH, RB = C::RB;
   constexpr int NDMA = C::NDMA;
@@ -77,8 +80,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   __shared__ __attribute__((aligned(1024))) uint8_t sK[4][C::KT];
   __shared__ __attribute__((aligned(1024))) uint8_t sV[3][C::KT];
   // RMX_MASK_DOC: global index and document of the keys of tile t, in slot t % 4
-  __shared__ __attribute__((aligned(256))) int sKg[4][BK];
-  __shared__ __attribute__((aligned(256))) int sKd[4][BK];
+  __shared__ __attribute__((aligned(256))) int sKg[4][C::MDOC];
+  __shared__ __attribute__((aligned(256))) int sKd[4][C::MDOC];
   __shared__ int sRange[2];
 
   const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
@@ -360,7 +363,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
       keep_branch();
       apply_mask(0, sA);
     }
-    float mx = tile_max_part(sA, 0, 32);
+    float mx = tile_max_part(sA, 0, 16 * MB);
     mx = fmaxf(mx, xhalf(mx)) * c;
     rescale(mx, true);
   }
@@ -378,9 +381,12 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
   constexpr int PVS = (2 * MB * NDB) / 2;  // PV steps (two MFMAs each)
   constexpr int NPAIR = MB * 8;            // element pairs per lane (32 scores)
   constexpr int P1 = NPAIR * 3 / 4;        // pairs done in region 1
-  constexpr int PV3 = PVS * 3 / 4;         // first PV step that needs pb[3]
+  // first PV step that reads the last P block (its MFMAs go over the blocks in order):
+  // every pair of that block is packed before it
+  constexpr int PV3 = (2 * MB - 1) * NDB / 2;
   constexpr int KD = 3, VD = 3;            // operand prefetch depth (steps) of regions 1 and 2
   static_assert(VD <= NKB && VD < PVS && 2 * MB * KD <= 15 && 4 * VD <= 15, "lgkmcnt range");
+  static_assert(P1 >= 4 * (2 * MB - 1) && PV3 >= 1, "P blocks packed before their MFMAs");
   auto pv_idx = [](int u, int v) { return 2 * u + v; };  // PV MFMA: kb2 = idx / NDB, db = idx % NDB
   auto iter = [&](int j, int vbj, f32x16* sc, f32x16* sn) __attribute__((always_inline)) {
     const int vb2 = vbj == 0 ? 2 : vbj - 1;  // (j + 2) % 3
@@ -471,14 +477,14 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(const FwdParams prm) {
               const int idx = pv_idx(u, v);
               o[idx % NDB] = mfma32t<DT>(va[u % (VD + 1)][v], __builtin_bit_cast(bf16x8, pw[idx / NDB]), o[idx % NDB]);
             }
-            // the remaining pairs, all before step PV3 (which starts on pb[3])
+            // the remaining pairs, all before step PV3 (which starts on the last block)
             if constexpr (u < PV3) {
               [&]<int... Q>(std::integer_sequence<int, Q...>) __attribute__((always_inline)) {
                 (pair(std::integral_constant<int, P1 + (NPAIR - P1) * u / PV3 + Q>{}), ...);
               }(std::make_integer_sequence<int, (NPAIR - P1) * (u + 1) / PV3 - (NPAIR - P1) * u / PV3>{});
             }
-            // row max of S_{j+1}, 32 / PVS scores per step
-            mpart[u] = tile_max_part(sn, 32 * u / PVS, 32 * (u + 1) / PVS);
+            // row max of S_{j+1}, 16 MB / PVS scores per step
+            mpart[u] = tile_max_part(sn, 16 * MB * u / PVS, 16 * MB * (u + 1) / PVS);
             asm volatile("" : "+v"(mpart[u]));
             __builtin_amdgcn_sched_barrier(0);
           }(),
@@ -598,21 +604,22 @@ static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* 
   return hipGetLastError();
 }
 
+template <int DT, bool DROP>
+static hipError_t launch_fwd_hd(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
+                                hipStream_t stream) {
+  if (L.head_dim > 128) return launch_fwd_t<256, DT, DROP>(L, probs, n, stream);
+  if (L.head_dim > 64) return launch_fwd_t<128, DT, DROP>(L, probs, n, stream);
+  return launch_fwd_t<64, DT, DROP>(L, probs, n, stream);
+}
+
 hipError_t launch_attn_fwd(const rmx_attn_layout& L, const rmx_fwd_problem* probs, int n,
                            hipStream_t stream) {
-  const bool big = L.head_dim > 64, f16 = L.dtype == RMX_DTYPE_F16, drop = L.dropout_p > 0.f;
-  if (drop) {
-    if (f16)
-      return big ? launch_fwd_t<128, RMX_DTYPE_F16, true>(L, probs, n, stream)
-                 : launch_fwd_t<64, RMX_DTYPE_F16, true>(L, probs, n, stream);
-    return big ? launch_fwd_t<128, RMX_DTYPE_BF16, true>(L, probs, n, stream)
-               : launch_fwd_t<64, RMX_DTYPE_BF16, true>(L, probs, n, stream);
-  }
-  if (f16)
-    return big ? launch_fwd_t<128, RMX_DTYPE_F16, false>(L, probs, n, stream)
-               : launch_fwd_t<64, RMX_DTYPE_F16, false>(L, probs, n, stream);
-  return big ? launch_fwd_t<128, RMX_DTYPE_BF16, false>(L, probs, n, stream)
-             : launch_fwd_t<64, RMX_DTYPE_BF16, false>(L, probs, n, stream);
+  const bool f16 = L.dtype == RMX_DTYPE_F16, drop = L.dropout_p > 0.f;
+  if (drop)
+    return f16 ? launch_fwd_hd<RMX_DTYPE_F16, true>(L, probs, n, stream)
+               : launch_fwd_hd<RMX_DTYPE_BF16, true>(L, probs, n, stream);
+  return f16 ? launch_fwd_hd<RMX_DTYPE_F16, false>(L, probs, n, stream)
+             : launch_fwd_hd<RMX_DTYPE_BF16, false>(L, probs, n, stream);
 }
 
 }  // namespace rmx

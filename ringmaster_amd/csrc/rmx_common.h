@@ -282,21 +282,24 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// XOR swizzles of the 16-byte chunks of unpadded LDS rows (HD bf16 per row).
+// XOR swizzles of the 16-byte chunks of unpadded LDS rows (HD bf16 per row). A row
+// of 128 or 256 elements starts at bank 0 (256 or 512 bytes), and a chunk's banks
+// depend on its index mod 16 only, so both use the same swizzles (values below 16:
+// bit 4 of a 256-element row's chunk index is kept).
 // Row reads (16 bytes of 16 consecutive rows, rows permuted by sigma):
 template <int HD>
 __device__ __forceinline__ int swz_rows(int r) {
-  return HD == 128 ? sigma(r & 15) : ((r >> 1) & 7);
+  return HD >= 128 ? sigma(r & 15) : ((r >> 1) & 7);
 }
 // Transposed reads (ds_read_b64_tr_b16 over 4 consecutive rows, 64 bytes each):
 template <int HD>
 __device__ __forceinline__ int swz_tr(int r) {
-  return HD == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+  return HD >= 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
 }
 // Both kinds of read on the same tile:
 template <int HD>
 __device__ __forceinline__ int swz_both(int r) {
-  return HD == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+  return HD >= 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
 }
 
 }  // namespace rmx

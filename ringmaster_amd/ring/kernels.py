@@ -7,7 +7,7 @@ fp32)``, q/k/v ``[b, s, h, d]``, GQA by ``kv_head = q_head // (hq/hkv)``, causal
 bottom-right aligned (ring/kernels.py:64-67), a sliding window ``(left, right)``
 masking ``pos_q - pos_k > left`` on the same bottom-right aligned positions
 (ring/kernels.py:68-72; ``right`` is not used, as there), head dims that are
-multiples of 8 up to 128, bf16 or fp16, and attention dropout (the Dao semantics: kept
+multiples of 8 up to 256, bf16 or fp16, and attention dropout (the Dao semantics: kept
 probabilities scaled by 1 / (1 - p), lse undropped; the mask is the kernels' hash of
 (seed, batch, head, query, key), so the backward replays it exactly). It is autograd-aware
 like ``hf_kernels``/``math``; the lse output is not differentiable (as with flash).
@@ -40,8 +40,8 @@ def _validate(q, k, v, dropout, window, softcap=0.0, alibi=None):
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"q, k and v must share their dtype ({q.dtype}, {k.dtype}, {v.dtype})")
     d = q.shape[-1]
-    if d % 8 or d > 128 or k.shape[-1] != d or v.shape[-1] != d:
-        raise NotImplementedError(f"head_dim {d} is not supported (a multiple of 8, at most 128)")
+    if d % 8 or d > 256 or k.shape[-1] != d or v.shape[-1] != d:
+        raise NotImplementedError(f"head_dim {d} is not supported (a multiple of 8, at most 256)")
     if not 0.0 <= float(dropout) < 1.0:
         raise ValueError(f"dropout must lie in [0, 1) (got {dropout})")
     if softcap:

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 14
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 15
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -55,7 +55,9 @@ def test_host_validation_gqa_divisibility():
 
 
 def test_host_validation_head_dim_and_mask():
-    assert _fwd(_layout(head_dim=136)) == abi.RMX_EUNSUPPORTED  # above 128
+    assert _fwd(_layout(head_dim=264)) == abi.RMX_EUNSUPPORTED  # above 256
+    assert _fwd(_layout(head_dim=136)) == abi.RMX_OK            # zero problems: no launch
+    assert _fwd(_layout(head_dim=256)) == abi.RMX_OK
     assert _fwd(_layout(head_dim=100)) == abi.RMX_EUNSUPPORTED  # not a multiple of 8
     assert _fwd(_layout(head_dim=96)) == abi.RMX_OK             # zero problems: no launch
     with pytest.raises(NotImplementedError):
