@@ -523,13 +523,15 @@ def mamba_bwd_workload(steps, warmup):
             "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
 
 
-def block_workload(steps, warmup):
+def block_workload(steps, warmup, D=128):
     """one non-causal ring step, Hq=32/Hkv=8, 16384^2, D=128, fwd+bwd, merged
-    into a running fp32 (out, lse) from a prior step."""
+    into a running fp32 (out, lse) from a prior step. With D=256 the same step at head dim
+    256 with half the heads (Hq=16/Hkv=4: the same FLOPs), on the head-dim-256 kernels."""
     from ringmaster_amd import abi
     from ringmaster_amd.ring import ops
 
-    S, Hq, Hkv, D = 16384, 32, 8, 128
+    S = 16384
+    Hq, Hkv = (32, 8) if D == 128 else (16, 4)
     sc = 1.0 / math.sqrt(D)
     q, k, v = _gen((1, S, Hq, D), 1, scale=sc), _gen((1, S, Hkv, D), 2, scale=sc), \
         _gen((1, S, Hkv, D), 3, scale=sc)
@@ -712,6 +714,8 @@ def main():
         extras["mamba2_chunk_state_configs4"] = chunk_state_workload(20, 3)
         torch.cuda.empty_cache()
         extras["block_configs1"] = block_workload(3, 1)
+        torch.cuda.empty_cache()
+        extras["block_configs1_d256"] = block_workload(3, 1, D=256)
         torch.cuda.empty_cache()
         extras["varlen_configs3"] = varlen_workload(3, 1)
         torch.cuda.empty_cache()
