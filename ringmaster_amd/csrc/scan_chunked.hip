@@ -32,11 +32,11 @@
 // few channels run over a long sequence (L = 65536, d = 256: 1024 chunks, 0.26 ms for
 // 30 us of traffic). There the same per-chunk code runs as reduce-then-rescan: pass 1
 // publishes each chunk's pair and stops, a fold kernel composes each channel's chain of
-// pairs in blocks (a wave per channel, a shuffle scan over 64 lanes of 16 chunks each)
+// pairs in 64 segments (16 channels per workgroup, the segments' maps combined in LDS)
 // and publishes the state after every chunk, and pass 2 rescans every chunk from the
-// state before it. The fold associates the chain differently from the look-back, so the
-// two forms differ in rounding (each is deterministic); the price is reading a and x
-// twice. The plan picks the form from the measured costs.
+// state before it. The fold associates the chain differently from the
+// look-back, so the two forms differ in rounding (each is deterministic); the price is
+// reading a and x twice. The plan picks the form from the measured costs.
 //
 // The backward is the same machinery over the reversed sequence:
 //   g_t = dh_t + a_{t+1} g_{t+1}   (a scan from the end with decay a_{t+1}),
@@ -417,59 +417,63 @@ __global__ void linear_scan_chunk_state_kernel(const uint64_t* __restrict__ word
 }
 
 // Reduce-then-rescan fold: each channel's chain of chunk pairs in scan order, the state
-// after chunk k published for chunk k + 1, S_{-1} = h_in (forward) or 0 (backward). One
-// wave per (chain, channel of the tile); the chain is taken in rounds of 64 x kFoldK
-// chunks: lane l composes its kFoldK consecutive pairs into one (all its loads issued at
-// once), a shuffle scan composes the 64 lanes' pairs, and each lane re-runs its chunks
-// from the state entering them. A round costs one load latency, not kFoldK x 64.
-constexpr int kFoldK = 16;
+// after chunk k published for chunk k + 1, S_{-1} = h_in (forward) or 0 (backward). A
+// workgroup takes kFoldCh channels of one chain and cuts the chain into kFoldSegs
+// segments; lane (s, ch) of wave w owns channel ch of segment 4 w + s, so a pair load is
+// four 128-byte rows of the words. Each lane composes its segment's pairs (kFoldBatch
+// loads in flight), the segments' maps meet in LDS, and each lane rescans its segment
+// from the state entering it: two load round trips per kFoldBatch chunks of a segment.
+constexpr int kFoldWaves = 16, kFoldSub = 4, kFoldCh = 64 / kFoldSub;
+constexpr int kFoldSegs = kFoldWaves * kFoldSub, kFoldBatch = 16;
 
-__global__ __launch_bounds__(256) void linear_scan_chain_fold_kernel(
+__global__ __launch_bounds__(64 * kFoldWaves) void linear_scan_chain_fold_kernel(
     uint64_t* __restrict__ words, const float* __restrict__ hin, int batch, int d, int ntiles,
     int nchunks, int CT) {
-  const int lane = threadIdx.x & 63;
-  const int64_t i = blockIdx.x * (int64_t)(blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (i >= (int64_t)batch * ntiles * CT) return;  // uniform over the wave
-  const int cc = (int)(i % CT);
-  const int64_t chain = i / CT;
+  __shared__ float s_a[kFoldSegs][kFoldCh], s_b[kFoldSegs][kFoldCh];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int ch = lane % kFoldCh, g = w * kFoldSub + lane / kFoldCh;  // channel, segment
+  const int ngrp = (CT + kFoldCh - 1) / kFoldCh;
+  const int64_t chain = blockIdx.x / ngrp;
+  const int cc = kFoldCh * (int)(blockIdx.x % ngrp) + ch;
   const int bb = (int)(chain / ntiles), tile = (int)(chain % ntiles);
   const int c = tile * CT + cc;
-  if (c >= d) return;
-  float carry = hin ? hin[(int64_t)bb * d + c] : 0.f;
-  uint64_t* w0 = words + (chain * nchunks * 3) * CT + cc;
-  for (int base = 0; base < nchunks; base += 64 * kFoldK) {
-    const int k0 = base + lane * kFoldK;
-    float Ak[kFoldK], Bk[kFoldK];
+  const bool on = cc < CT && c < d;
+  const int seg = (nchunks + kFoldSegs - 1) / kFoldSegs;
+  const int k_lo = g * seg < nchunks ? g * seg : nchunks;
+  const int k_hi = k_lo + seg < nchunks ? k_lo + seg : nchunks;
+  uint64_t* w0 = words + (chain * nchunks * 3) * CT + (on ? cc : 0);
+  auto load = [&](int k, float* A, float* B) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < kFoldK; ++j) {
-      const bool in = k0 + j < nchunks;
-      const uint64_t* wk = w0 + (int64_t)(in ? k0 + j : 0) * 3 * CT;
-      Ak[j] = in ? word_val(wk[kWordA * CT]) : 1.f;
-      Bk[j] = in ? word_val(wk[kWordB * CT]) : 0.f;
+    for (int j = 0; j < kFoldBatch; ++j) {
+      const bool in = on && k + j < k_hi;
+      const uint64_t* wk = w0 + (int64_t)(in ? k + j : 0) * 3 * CT;
+      A[j] = in ? word_val(wk[kWordA * CT]) : 1.f;
+      B[j] = in ? word_val(wk[kWordB * CT]) : 0.f;
     }
-    float PA = 1.f, PB = 0.f;  // the lane's chunks composed: x -> PA x + PB
+  };
+  float PA = 1.f, PB = 0.f;  // the segment composed: x -> PA x + PB
+  for (int k = k_lo; k < k_hi; k += kFoldBatch) {
+    float A[kFoldBatch], B[kFoldBatch];
+    load(k, A, B);
 #pragma unroll
-    for (int j = 0; j < kFoldK; ++j) {
-      PB = __builtin_fmaf(Ak[j], PB, Bk[j]);
-      PA *= Ak[j];
+    for (int j = 0; j < kFoldBatch; ++j) {
+      PB = __builtin_fmaf(A[j], PB, B[j]);
+      PA *= A[j];
     }
+  }
+  s_a[g][ch] = PA;
+  s_b[g][ch] = PB;
+  __syncthreads();
+  float S = on && hin ? hin[(int64_t)bb * d + c] : 0.f;
+  for (int v = 0; v < g; ++v) S = __builtin_fmaf(s_a[v][ch], S, s_b[v][ch]);
+  for (int k = k_lo; k < k_hi; k += kFoldBatch) {
+    float A[kFoldBatch], B[kFoldBatch];
+    load(k, A, B);
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {  // inclusive: this lane's map after the lower ones
-      const float oA = __shfl_up(PA, off), oB = __shfl_up(PB, off);
-      if (lane >= off) {
-        PB = __builtin_fmaf(PA, oB, PB);
-        PA *= oA;
-      }
+    for (int j = 0; j < kFoldBatch; ++j) {
+      S = __builtin_fmaf(A[j], S, B[j]);
+      if (on && k + j < k_hi) put_word(w0 + (int64_t)(k + j) * 3 * CT + kWordS * CT, S);
     }
-    const float eA = __shfl_up(PA, 1), eB = __shfl_up(PB, 1);
-    float S = lane == 0 ? carry : __builtin_fmaf(eA, carry, eB);
-    const float next = __shfl(__builtin_fmaf(PA, carry, PB), 63);
-#pragma unroll
-    for (int j = 0; j < kFoldK; ++j) {
-      S = __builtin_fmaf(Ak[j], S, Bk[j]);
-      if (k0 + j < nchunks) put_word(w0 + (int64_t)(k0 + j) * 3 * CT + kWordS * CT, S);
-    }
-    carry = next;
   }
 }
 
@@ -553,16 +557,19 @@ static hipError_t launch_chunked(const ScanChunkPlan& p, const float* a, const f
                                  float* dhin, void* ws, int batch, int L, int d, int groups,
                                  hipStream_t stream) {
   const ChunkWork w = carve(p, ws);
-  const int64_t n16 = (int64_t)(p.bytes / 16);  // the counter and every word
-  hipLaunchKernelGGL(fill_zero_u32x4_kernel, dim3((unsigned)std::min<int64_t>((n16 + 255) / 256, 2048)),
-                     dim3(256), 0, stream, reinterpret_cast<u32x4*>(ws), n16);
   if (!p.two_pass) {
+    // the ticket counter and the tags of every word start at zero (reduce-then-rescan
+    // writes every word it reads first and takes no tickets)
+    const int64_t n16 = (int64_t)(p.bytes / 16);
+    hipLaunchKernelGGL(fill_zero_u32x4_kernel,
+                       dim3((unsigned)std::min<int64_t>((n16 + 255) / 256, 2048)), dim3(256), 0,
+                       stream, reinterpret_cast<u32x4*>(ws), n16);
     launch_pass<BWD, 0>(p, a, x, hin, hfwd, y, da, dhin, w, batch, L, d, groups, stream);
     return hipGetLastError();
   }
   launch_pass<BWD, 1>(p, a, x, hin, hfwd, y, da, dhin, w, batch, L, d, groups, stream);
-  const int64_t nf = (int64_t)batch * p.ntiles * p.CT;
-  hipLaunchKernelGGL(linear_scan_chain_fold_kernel, dim3((unsigned)((nf + 3) / 4)), dim3(256),
+  const int64_t nf = (int64_t)batch * p.ntiles * ((p.CT + kFoldCh - 1) / kFoldCh);
+  hipLaunchKernelGGL(linear_scan_chain_fold_kernel, dim3((unsigned)nf), dim3(64 * kFoldWaves),
                      0, stream, w.words, BWD ? nullptr : hin, batch, d, p.ntiles, p.nchunks, p.CT);
   launch_pass<BWD, 2>(p, a, x, hin, hfwd, y, da, dhin, w, batch, L, d, groups, stream);
   return hipGetLastError();
