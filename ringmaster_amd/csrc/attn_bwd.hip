@@ -1145,9 +1145,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
   constexpr int NKB = HD / 16, NDB = HD / 32;
   static_assert(NDMA >= 1 && QT % (1024 * NW) == 0 && KDMA >= 1, "tile split");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t sK[BKV * RB];
-  __shared__ __attribute__((aligned(1024))) uint8_t sQ[NB][QT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sO[NB][QT];
+  // the K block, then the Q and dO tiles; at the end it stages dK and dV rows (128 KiB)
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[BKV * RB + 2 * NB * QT];
+  static_assert(BKV * HD * 4 <= BKV * RB + 2 * NB * QT, "gradient staging");
+  uint8_t* const sK = smem;
+  uint8_t(*const sQ)[QT] = reinterpret_cast<uint8_t(*)[QT]>(smem + BKV * RB);
+  uint8_t(*const sO)[QT] = reinterpret_cast<uint8_t(*)[QT]>(smem + BKV * RB + NB * QT);
   __shared__ __attribute__((aligned(256))) float sM[NB][2][64];  // nl, delta (a DMA writes 64)
   __shared__ int sQg[NB][BQ];
   __shared__ int sQd[NB][BQ];
@@ -1505,36 +1508,47 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
   }
   wait_all_loads();
 
-  // ---- epilogue: lane (hl, l32) holds column d = 32 db + l32 of keys kw0 + c_row(hl, r)
+  // ---- epilogue: lane (hl, l32) holds column d = 32 db + l32 of keys kw0 + c_row(hl, r).
+  // Each gradient is staged through LDS as [key][d] fp32 rows (the tiles are dead) and
+  // stored as 4-column runs of whole rows: one mode test per run, not per element.
   const int mode = P.dkv_mode;
+  float* const stg = reinterpret_cast<float*>(smem);
+  const int col = 4 * (tid & 63), rw = tid >> 6;  // columns col .. col + 3 of rows rw + 4 i
+  auto store = [&](const f32x16* acc, float sc, float* gacc, uint16_t* gbf) {
+    __syncthreads();  // every wave is past its last tile reads (or the previous gradient)
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const float sc = g == 0 ? 1.f : -L.scale;
-    float* gacc = g == 0 ? P.dv_acc : P.dk_acc;
-    uint16_t* gbf = g == 0 ? P.dv : P.dk;
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int d = 32 * db + l32;
-      if (d >= D) continue;  // columns past the head dim are not stored
+      for (int r = 0; r < 16; ++r)
+        stg[(32 * wave + c_row(hl, r)) * HD + 32 * db + l32] = acc[db][r] * sc;
+    __syncthreads();
+    if (col >= D) return;  // columns past the head dim are not stored
+    const bool vf = ((uintptr_t)gacc & 15) == 0, vb = ((uintptr_t)gbf & 7) == 0;
+    for (int row = rw; row < BKV && k0 + row < sk; row += 4) {
+      const int kk = k0 + row;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(stg + row * HD + col);
+      float* ga = gacc ? gacc + bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + col : nullptr;
+      uint16_t* gb = gbf ? gbf + bb * L.dk_sb + (int64_t)kk * L.dk_ss + kvh * L.dk_sh + col : nullptr;
+      if (vf && vb) {
+        grad_store4<DT>(mode, ga, gb, v);
+        continue;
+      }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kk = kw0 + c_row(hl, r);
-        if (kk >= sk) continue;
-        const float gv = (g == 0 ? dv[db][r] : dk[db][r]) * sc;
-        const int64_t ao = bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + d;
-        const int64_t bo = bb * L.dk_sb + (int64_t)kk * L.dk_ss + kvh * L.dk_sh + d;
+      for (int e = 0; e < 4; ++e) {  // a caller pointer below vector alignment
         if (mode == RMX_GRAD_WRITE_F32) {
-          gacc[ao] = gv;
+          ga[e] = v[e];
         } else if (mode == RMX_GRAD_ACC_F32) {
-          gacc[ao] += gv;
+          ga[e] += v[e];
         } else if (mode == RMX_GRAD_ACC_FINAL) {
-          gbf[bo] = f2e<DT>(gacc[ao] + gv);
+          gb[e] = f2e<DT>(ga[e] + v[e]);
         } else {
-          gbf[bo] = f2e<DT>(gv);
+          gb[e] = f2e<DT>(v[e]);
         }
       }
     }
-  }
+  };
+  store(dv, 1.f, P.dv_acc, P.dv);
+  store(dk, -L.scale, P.dk_acc, P.dk);
 }
 
 template <int HD, int DT, bool DROP>

@@ -147,3 +147,46 @@ def test_varlen_ring_head_dim_256():
         assert_bf16_close(qd.grad[r], refs[0][r].grad, f"dq rank {r}")
         assert_bf16_close(kd.grad[r], refs[1][r].grad, f"dk rank {r}")
         assert_bf16_close(vd.grad[r], refs[2][r].grad, f"dv rank {r}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_dkdv_head_dim_256_unaligned_gradient_buffers(causal):
+    """dK/dV written into caller buffers below vector alignment (fp32 views 4 bytes and bf16
+    views 2 bytes past an aligned base: the ABI asks only for element-aligned strides) equal,
+    bit for bit, the same gradients written into aligned buffers."""
+    from ringmaster_amd import abi
+    from ringmaster_amd.ring import ops
+    from ringmaster_amd.ring.kernels import block_forward
+
+    b, sq, sk, hq, hkv, d = 1, 200, 264, 4, 2, 256
+    print(f"case unaligned dkdv causal={causal} d={d}", flush=True)
+    _, q = bf16_pair((b, sq, hq, d), 21)
+    _, k = bf16_pair((b, sk, hkv, d), 22)
+    _, v = bf16_pair((b, sk, hkv, d), 23)
+    _, do = bf16_pair((b, sq, hq, d), 24)
+    sc = d ** -0.5
+    mask = abi.MASK_CAUSAL if causal else abi.MASK_FULL
+    out, lse, out32 = block_forward(q, k, v, sc, causal, keep_f32=True)
+    delta = torch.empty((b, hq, sq), device="cuda")
+    nlse = torch.empty_like(delta)
+    ops.attn_bwd_delta(out32, do, delta, hkv, lse=lse, nlse=nlse)
+    n = b * sk * hkv * d
+    shape = (b, sk, hkv, d)
+
+    def run(off, f32):
+        dt = torch.float32 if f32 else torch.bfloat16
+        bufs = [torch.zeros(n + 8, dtype=dt, device="cuda") for _ in range(2)]
+        dk, dv = (t[off:off + n].view(shape) for t in bufs)
+        kw = dict(dk_acc=dk, dv_acc=dv) if f32 else dict(dk=dk, dv=dv)
+        ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=do, lse=lse, delta=delta, nlse=nlse,
+                                 dq_mode=abi.GRAD_NONE,
+                                 dkv_mode=abi.GRAD_WRITE_F32 if f32 else abi.GRAD_WRITE_BF16,
+                                 **kw)], scale=sc, mask=mask)
+        torch.cuda.synchronize()
+        return dk.clone(), dv.clone()
+
+    for f32 in (True, False):
+        ak, av = run(0, f32)
+        uk, uv = run(1, f32)
+        assert torch.equal(ak, uk) and torch.equal(av, uv), f"f32={f32}"
+        assert ak.abs().sum() > 0
