@@ -1,0 +1,114 @@
+"""A seeded sweep of block shapes through the provider on the MI355X vs the CPU oracle (fp32).
+
+Each case draws batch 1-2, query and key lengths from 1 to 700 (ragged against every tile
+size, sk < sq included: bottom-right causal then leaves the first rows without keys, out 0 and
+lse -inf), GQA ratios 1-8, head dims that are multiples of 8 up to 256 (all three kernel
+sets), causal or not, a window or none, bf16 or fp16, and dropout or none, and checks out,
+lse and the three gradients against ``math_block`` (ring/kernels.py:52-78) at the bf16 / fp16
+bars (bf16 gradient bars floored at two ulps of the value and one of the tensor's largest:
+sums over up to 700 rows and 8 folded heads, see ``check``). The draw is fixed (numpy seed 20261202), so a failure names a reproducible case."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ring_math as rm
+from tests.gpu_util import (assert_bf16_close, assert_f16_close, assert_f32_rel, bf16_pair,
+                            f16_pair, rel_l2)
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(n=48, seed=20261202):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2]))
+        g = int(rng.choice([1, 2, 4, 8]))
+        d = int(rng.choice([8, 40, 64, 72, 128, 136, 200, 256]))
+        sq = int(rng.choice([1, 2, 31, 64, 65, 129, 257, 300, 511, 700]))
+        sk = int(rng.choice([1, 3, 32, 64, 100, 128, 250, 513, 700]))
+        causal = bool(rng.random() < 0.5)
+        left = int(rng.choice([0, 5, 63, 200])) if rng.random() < 0.3 else None
+        half = "f16" if rng.random() < 0.25 else "bf16"
+        p = float(rng.choice([0.1, 0.3])) if rng.random() < 0.2 else 0.0
+        b = int(rng.choice([1, 2]))
+        out.append((i, b, sq, sk, hkv * g, hkv, d, causal, left, half, p))
+    return out
+
+
+def _id(c):
+    i, b, sq, sk, hq, hkv, d, causal, left, half, p = c
+    return f"{i}-b{b}-q{sq}-k{sk}-h{hq}:{hkv}-d{d}-{'c' if causal else 'f'}-w{left}-{half}-p{p}"
+
+
+@pytest.mark.parametrize("case", _cases(), ids=_id)
+def test_block_sweep(case):
+    from ringmaster_amd.ring.kernels import mi355x_hip_block
+
+    i, b, sq, sk, hq, hkv, d, causal, left, half, p = case
+    print(f"case sweep {_id(case)}", flush=True)
+    f16 = half == "f16"
+    pair = f16_pair if f16 else bf16_pair
+    close = assert_f16_close if f16 else assert_bf16_close
+    window = None if left is None else (left, 0)
+    qf, qd = pair((b, sq, hq, d), 100 + i)
+    kf, kd = pair((b, sk, hkv, d), 200 + i)
+    vf, vd = pair((b, sk, hkv, d), 300 + i)
+    dof, dod = pair((b, sq, hq, d), 400 + i)
+    for t in (qd, kd, vd):
+        t.requires_grad_(True)
+    seed = 777 + i if p else None
+    out, lse = mi355x_hip_block(qd, kd, vd, causal=causal, scaling=None, window=window,
+                                dropout=p, dropout_seed=seed)
+    out.backward(dod)
+    torch.cuda.synchronize()
+    # rows without any key (bottom-right causal with sk < sq): the prefix i < sq - sk. The
+    # oracle runs on the other rows, which keep their positions (and dropout coordinates,
+    # drop_q0 = s0) as a block of sk rows; the kernels give those rows out 0, lse -inf and
+    # dq 0 (the convention of the reference's masked blocks, ring/varlen_blocks.py:70-79)
+    s0 = sq - sk if causal and sq > sk else 0
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf[:, s0:], kf, vf))
+    ref, ref_lse = rm.math_block(qr, kr, vr, causal=causal, scaling=None, window=window,
+                                 dropout=p, drop_seed=seed, drop_q0=s0)
+    ref.backward(dof[:, s0:])
+    got_l = lse.detach().cpu()
+    assert torch.isneginf(got_l[:, :, :s0]).all(), "rows without keys: lse"
+    assert torch.equal(out[:, :s0].float().cpu(), torch.zeros_like(out[:, :s0].float().cpu()))
+    assert torch.equal(qd.grad[:, :s0].float().cpu(), torch.zeros_like(qd.grad[:, :s0].float().cpu()))
+    if s0 == sq:
+        return
+    assert_f32_rel(got_l[:, :, s0:], ref_lse, "lse")
+
+    def check(got, ref, what, grad):
+        # references that are exactly 0 in exact arithmetic (one key per row: dS = 0) get the
+        # max-abs bar only. bf16 gradients are sums over up to 700 rows (and 8 folded heads)
+        # of terms whose P / dS operands the backward's GEMMs take in bf16, so their error
+        # scales with the summands, not with a result that cancels: the max-abs bar of an
+        # element is floored at two bf16 ulps of it and one ulp of the tensor's largest value
+        ref = ref.detach().float()
+        if ref.abs().max().item() < 1e-3:
+            bar = 5e-3 if f16 else 2e-2
+            err = (got.detach().float().cpu() - ref).abs().max().item()
+            assert err < bar, f"{what}: max-abs {err:.3e} against a zero reference"
+        elif f16 or not grad:
+            close(got, ref, what)
+        else:
+            g = got.detach().float().cpu()
+            assert torch.isfinite(g).all(), f"{what}: non-finite values"
+            diff = (g - ref).abs()
+            bar = torch.maximum(ref.abs() * 2.0 ** -6,
+                                torch.full_like(ref, ref.abs().max().item() * 2.0 ** -7))
+            bar = bar.clamp_min(2e-2)
+            over = (diff / bar).max().item()
+            rl = rel_l2(g, ref)
+            assert over < 1 and rl < 1e-2, \
+                f"{what}: max-abs {diff.max().item():.3e} ({over:.2f} of the bar) rel-L2 {rl:.3e}"
+
+    check(out[:, s0:], ref, "out", False)
+    check(qd.grad[:, s0:], qr.grad, "dq", True)
+    check(kd.grad, kr.grad, "dk", True)
+    check(vd.grad, vr.grad, "dv", True)
+    assert math.isfinite(float(out.detach().float().abs().sum()))
