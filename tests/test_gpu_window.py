@@ -4,7 +4,7 @@ The provider contract's ``window`` (ring/kernels.py:68-72: ``pos_q - pos_k > lef
 bottom-right aligned) on single blocks and through the Dao op pair, the gather ring and
 the packed gather ring with windows (ring/loop.py:175-228), and head dims that are
 multiples of 8 up to 128 (the kernels compute at 64 or 128 and read the columns past
-head_dim as zeros)."""
+head_dim as zeros; head dims above 128: tests/test_gpu_head256.py)."""
 
 import pytest
 import torch
