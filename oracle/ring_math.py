@@ -43,9 +43,16 @@ def fmix32(x):
     return x
 
 
+def drop_p32(p):
+    """The dropout probability as the C ABI carries it (the layout's fp32 ``dropout_p``):
+    the mask's threshold and the keep scale are those of this value (0.3 -> 0.30000001...,
+    whose threshold floor(p 2^32) is 52 counts above the float64 one's)."""
+    return float(np.float32(p))
+
+
 def dropout_keep(seed, bh, q_pos, k_pos, p):
     """Keep mask [len(q_pos), len(k_pos)] (bool) of the (batch, head) pair bh = b Hq + h:
-    fmix32(bhmix ^ q DROP_Q ^ k DROP_K) >= floor(p 2^32),
+    fmix32(bhmix ^ q DROP_Q ^ k DROP_K) >= floor(p32 2^32) with p32 = drop_p32(p),
     bhmix = fmix32(seed_lo ^ fmix32(seed_hi ^ bh DROP_BH)), arithmetic mod 2^32."""
     seed = int(seed) & ((1 << 64) - 1)
     lo, hi = np.uint32(seed & 0xFFFFFFFF), np.uint32(seed >> 32)
@@ -54,16 +61,16 @@ def dropout_keep(seed, bh, q_pos, k_pos, p):
         qt = np.asarray(q_pos, dtype=np.int64).astype(np.uint32) * np.uint32(DROP_Q)
         kt = np.asarray(k_pos, dtype=np.int64).astype(np.uint32) * np.uint32(DROP_K)
     u = fmix32(bhmix ^ qt[:, None] ^ kt[None, :])
-    thr = min(int(float(p) * 4294967296.0), 0xFFFFFFFF)
+    thr = min(int(drop_p32(p) * 4294967296.0), 0xFFFFFFFF)
     return u >= np.uint32(thr)
 
 
 def dropout_scale_mask(seed, b, hq, sq, sk, p, q0=0, k0=0):
-    """fp32 [b, hq, sq, sk]: 1 / (1 - p) where kept, 0 where dropped."""
+    """fp32 [b, hq, sq, sk]: 1 / (1 - p32) where kept, 0 where dropped (p32 = drop_p32(p))."""
     keep = np.stack([np.stack([dropout_keep(seed, bi * hq + h, np.arange(sq) + q0,
                                             np.arange(sk) + k0, p) for h in range(hq)])
                      for bi in range(b)])
-    return torch.from_numpy(keep.astype(np.float32)) / (1.0 - float(p))
+    return torch.from_numpy(keep.astype(np.float32)) / (1.0 - drop_p32(p))
 
 
 # ---------------------------------------------------------------- blocks

@@ -59,13 +59,19 @@ def test_dropout_block_fp16_window():
     _block(True, 4, 2, 300, 300, 128, 0.25, seed=77, window=(90, 0), half=torch.float16)
 
 
-def test_dropout_mask_bits_exact():
+@pytest.mark.parametrize("b,hq,sq,sk,p,seed", [
+    (2, 2, 512, 128, 0.4, 0xDEADBEEFCAFE),
+    # element (b 1, h 8, q 202, k 74) hashes between floor(p 2^32) of the fp32 p the ABI
+    # carries and that of the float64 p: dropped by the fp32 threshold
+    (2, 16, 256, 128, 0.3, 1145),
+])
+def test_dropout_mask_bits_exact(b, hq, sq, sk, p, seed):
     """q = 0 makes every probability 1 / sk; with V = I (sk = d) the output row q is the
     mask row scaled by 1 / (sk (1 - p)), so the kernel's keep bits are read off the output
-    and compared with the oracle's hash, bit for bit (two heads, two batch rows)."""
+    and compared with the oracle's hash, bit for bit (every head and batch row)."""
     from ringmaster_amd.ring.kernels import mi355x_hip_block
 
-    b, hq, sq, sk, p, seed = 2, 2, 512, 128, 0.4, 0xDEADBEEFCAFE
+    print(f"case dropout mask bits b={b} hq={hq} sq={sq} sk={sk} p={p} seed={seed}", flush=True)
     q = torch.zeros(b, sq, hq, sk, dtype=torch.bfloat16, device="cuda")
     k = torch.zeros(b, sk, hq, sk, dtype=torch.bfloat16, device="cuda")
     v = torch.eye(sk, dtype=torch.bfloat16, device="cuda")[None, :, None, :].expand(b, sk, hq, sk)
@@ -78,6 +84,8 @@ def test_dropout_mask_bits_exact():
             want = rm.dropout_keep(seed, bi * hq + h, np.arange(sq), np.arange(sk), p)
             assert np.array_equal(got[bi, :, h].numpy(), want), f"mask of (b={bi}, h={h})"
     assert abs(got.float().mean().item() - (1 - p)) < 0.01
+    if seed == 1145:
+        assert not bool(got[1, 202, 8, 74])
 
 
 def test_dropout_seed_determinism():

@@ -171,15 +171,27 @@ def test_fmix32_matches_integer_arithmetic_and_is_a_bijection():
 
 
 def test_dropout_keep_matches_its_definition():
-    """dropout_keep on a few elements, recomputed from the formula with Python ints."""
+    """dropout_keep on a few elements, recomputed from the formula with Python ints; the
+    threshold is floor(p 2^32) of p as the C ABI's fp32 ``dropout_p`` holds it (struct
+    round trip), and an element whose hash falls between that threshold and the float64 one
+    is dropped."""
+    import struct
+
     seed, bh, p = 0x0123456789ABCDEF, 7, 0.3
     keep = rm.dropout_keep(seed, bh, [0, 5, 1000], [3, 64, 77777], p)
     bhmix = _fmix32_int((seed & 0xFFFFFFFF) ^ _fmix32_int((seed >> 32) ^ (bh * 0x9E3779B9)))
-    thr = int(p * 2 ** 32)
+    p32 = struct.unpack("f", struct.pack("f", p))[0]
+    thr = int(p32 * 2 ** 32)
+    assert thr == 1288490240 and int(p * 2 ** 32) == 1288490188
     for i, q in enumerate([0, 5, 1000]):
         for j, k in enumerate([3, 64, 77777]):
             u = _fmix32_int(bhmix ^ ((q * 0x85EBCA77) & 0xFFFFFFFF) ^ ((k * 0xC2B2AE3D) & 0xFFFFFFFF))
             assert bool(keep[i, j]) == (u >= thr)
+    # seed 1145, bh 24, query 202, key 74: hash 1288490235, between the two thresholds
+    u = _fmix32_int(_fmix32_int((1145 & 0xFFFFFFFF) ^ _fmix32_int(0 ^ (24 * 0x9E3779B9)))
+                    ^ ((202 * 0x85EBCA77) & 0xFFFFFFFF) ^ ((74 * 0xC2B2AE3D) & 0xFFFFFFFF))
+    assert 1288490188 <= u < 1288490240
+    assert not rm.dropout_keep(1145, 24, [202], [74], 0.3)[0, 0]
 
 
 @pytest.mark.parametrize("p", [0.1, 0.3, 0.7])
