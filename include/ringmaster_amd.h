@@ -56,8 +56,9 @@ extern "C" {
 /* RMX_DROPOUT: with dropout_p > 0, element (b, h, q, k) of a problem (h the q head) is kept when
  *   fmix32(bhmix ^ (q + drop_q0) * 0x85ebca77 ^ (k + drop_k0) * 0xc2b2ae3d) >= floor(p * 2^32),
  *   bhmix = fmix32(drop_seed_lo ^ fmix32(drop_seed_hi ^ (b * hq + h) * 0x9e3779b9)),
- * all arithmetic mod 2^32, fmix32 the MurmurHash3 32-bit finalizer; kept probabilities are
- * scaled by 1 / (1 - p) and lse is the undropped one (the Dao flash-attention semantics).
+ * all arithmetic mod 2^32, fmix32 the MurmurHash3 32-bit finalizer, p the float dropout_p
+ * (floor of its exact value times 2^32); kept probabilities are scaled by 1 / (1 - p) and lse
+ * is the undropped one (the Dao flash-attention semantics).
  * The backward must get the forward's layout seed and each problem's drop_q0 / drop_k0. */
 /* A problem's sliding window (has_window = 1) masks every pair further apart than
  * window_left: pos_q - pos_k > window_left, with the bottom-right aligned positions
