@@ -173,19 +173,22 @@ struct BwdTiles {
 // arithmetic in the loop. Tiles past the end are issued as zero-length loads,
 // which keeps every wait count static.
 // At head dim 256 a workgroup is 4 waves (one per SIMD: Q, dO and the dQ accumulator
-// take 256 registers) with two tile buffers (a K or V tile is then 32 KiB).
+// take 256 registers) and a key tile 32 keys, so four K/V buffers (16 KiB each) fit.
 template <int HD>
 struct DqCfg {
   static constexpr int NW = HD == 256 ? 4 : 8;  // waves per workgroup
   static constexpr int NT = NW * 64;
   static constexpr int BQ = 32 * NW;            // queries per workgroup
-  static constexpr int NB = HD == 256 ? 2 : RMX_DQ_NB;
+  static constexpr int BK = HD == 256 ? 32 : 64;  // keys per tile
+  static constexpr int NB = HD == 256 ? 4 : RMX_DQ_NB;
+  static constexpr int MDOC = BK < 64 ? 64 : BK;  // key metadata slots (a DMA writes 64)
 };
 
 template <int HD, int MASK, int DT, bool DROP>
 __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const BwdParams prm) {
   using T = BwdTiles<HD>;
-  constexpr int NW = DqCfg<HD>::NW, NT = DqCfg<HD>::NT, BQ = DqCfg<HD>::BQ, BK = 64;
+  constexpr int NW = DqCfg<HD>::NW, NT = DqCfg<HD>::NT, BQ = DqCfg<HD>::BQ, BK = DqCfg<HD>::BK;
+  constexpr int MBK = BK / 32, KB2 = BK / 16;  // 32-key blocks of S^T, 16-key steps of dQ
   constexpr int CH = T::CH, NKB = T::NKB, NDB = T::NDB;
   constexpr int RB = HD * 2;              // LDS row bytes (unpadded, swizzled)
   constexpr int KT = BK * RB;             // bytes of one K (or V) tile
@@ -198,8 +201,8 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
   static_assert(NDMA >= 1 && KT % (1024 * NW) == 0, "tile split");
 
   __shared__ __attribute__((aligned(1024))) uint8_t sT[2 * NB][KT];  // K tiles, then V tiles
-  __shared__ __attribute__((aligned(256))) int sKg[NB][BK];
-  __shared__ __attribute__((aligned(256))) int sKd[NB][BK];
+  __shared__ __attribute__((aligned(256))) int sKg[NB][DqCfg<HD>::MDOC];
+  __shared__ __attribute__((aligned(256))) int sKd[NB][DqCfg<HD>::MDOC];
   __shared__ int sRange[2];
 
   const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
@@ -421,24 +424,24 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
                        (int64_t)kga >= (int64_t)qg_last - wl);
       }
 
-      f32x16 s[2], dp[2];
+      f32x16 s[MBK], dp[MBK];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < MBK; ++mb) {
         s[mb] = zero16();
         dp[mb] = zero16();
       }
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
+        for (int mb = 0; mb < MBK; ++mb) {
           s[mb] = mfma32t<DT>(row_op(kt_lds, kb, mb), qreg[kb], s[mb]);
           dp[mb] = mfma32t<DT>(vrow_op(buf, kb, mb), doreg[kb], dp[mb]);
         }
       }
 
-      bf16x8 dsb[4];
+      bf16x8 dsb[KB2];
 #pragma unroll
-      for (int kb2 = 0; kb2 < 4; ++kb2) {
+      for (int kb2 = 0; kb2 < KB2; ++kb2) {
         const int mb = kb2 >> 1, b8 = 8 * (kb2 & 1);
         float v[8];
 #pragma unroll
@@ -477,7 +480,7 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
 
       // dQ^T += K^T dS^T
 #pragma unroll
-      for (int kb2 = 0; kb2 < 4; ++kb2)
+      for (int kb2 = 0; kb2 < KB2; ++kb2)
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
           acc[db] = mfma32t<DT>(tr_op(kt_lds, kb2, db), dsb[kb2], acc[db]);
