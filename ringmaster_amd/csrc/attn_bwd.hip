@@ -498,6 +498,18 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
   const float scale = L.scale;
   float* arow = P.dq_acc ? P.dq_acc + bb * L.a_sb + (int64_t)q * L.a_ss + head * L.a_sh : nullptr;
   uint16_t* brow = P.dq ? P.dq + bb * L.o_sb + (int64_t)q * L.o_ss + head * L.o_sh : nullptr;
+  // the accumulating modes read all of the row's prior values before the first store (one
+  // wait, not one memory round trip per 4 columns: see the dK/dV epilogue)
+  const int mode = P.dq_mode;
+  const bool rd = mode == RMX_GRAD_ACC_F32 || mode == RMX_GRAD_ACC_FINAL;
+  f32x4 prev[NDB][4];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d0 = 32 * db + 8 * j + 4 * hl;
+      prev[db][j] = rd && d0 < D ? *reinterpret_cast<const f32x4*>(arow + d0) : f32x4{};
+    }
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -509,7 +521,11 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
       v[1] = acc[db][4 * j + 1] * scale;
       v[2] = acc[db][4 * j + 2] * scale;
       v[3] = acc[db][4 * j + 3] * scale;
-      grad_store4<DT>(P.dq_mode, arow ? arow + d0 : nullptr, brow ? brow + d0 : nullptr, v);
+      if (rd) v += prev[db][j];
+      // the prior value is added: the store is a write (f32) or a conversion (16-bit)
+      grad_store4<DT>(mode == RMX_GRAD_ACC_F32 ? RMX_GRAD_WRITE_F32
+                      : mode == RMX_GRAD_ACC_FINAL ? RMX_GRAD_WRITE_BF16 : mode,
+                      arow ? arow + d0 : nullptr, brow ? brow + d0 : nullptr, v);
     }
 }
 
@@ -1090,8 +1106,29 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   }
   wait_all_loads();  // zero-length loads issued past the end
 
-  // ---- epilogue: lane (hl, l32) holds column d = 32 db + l32 of keys kw0 + c_row(hl, r)
+  // ---- epilogue: lane (hl, l32) holds column d = 32 db + l32 of keys kw0 + c_row(hl, r).
+  // The accumulating modes read all of the lane's prior dV and dK values before the first
+  // store: element by element, each read would wait for the store before it (the compiler
+  // cannot tell that they touch different elements), one memory round trip per element.
   const int mode = P.dkv_mode;
+  const bool rd = mode == RMX_GRAD_ACC_F32 || mode == RMX_GRAD_ACC_FINAL;
+  float prev[2][NDB][16];
+  if (rd) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const float* gacc = g == 0 ? P.dv_acc : P.dk_acc;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const int d = 32 * db + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = kw0 + c_row(hl, r);
+          const int64_t ao = bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + d;
+          prev[g][db][r] = d < D && kk < sk ? gacc[ao] : 0.f;
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
     const float sc = g == 0 ? 1.f : -L.scale;
@@ -1111,9 +1148,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
         if (mode == RMX_GRAD_WRITE_F32) {
           gacc[ao] = gv;
         } else if (mode == RMX_GRAD_ACC_F32) {
-          gacc[ao] += gv;
+          gacc[ao] = prev[g][db][r] + gv;
         } else if (mode == RMX_GRAD_ACC_FINAL) {
-          gbf[bo] = f2e<DT>(gacc[ao] + gv);
+          gbf[bo] = f2e<DT>(prev[g][db][r] + gv);
         } else {
           gbf[bo] = f2e<DT>(gv);
         }
@@ -1527,15 +1564,43 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
     __syncthreads();
     if (col >= D) return;  // columns past the head dim are not stored
     const bool vf = ((uintptr_t)gacc & 15) == 0, vb = ((uintptr_t)gbf & 7) == 0;
+    auto gptr = [&](int kk) {
+      return gacc ? gacc + bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + col : nullptr;
+    };
+    auto bptr = [&](int kk) {
+      return gbf ? gbf + bb * L.dk_sb + (int64_t)kk * L.dk_ss + kvh * L.dk_sh + col : nullptr;
+    };
+    if (vf && vb) {
+      // the accumulating modes read the prior values of 16 of the thread's rows before
+      // their first store (one wait per 16 rows, not one memory round trip per row)
+      const bool rd = mode == RMX_GRAD_ACC_F32 || mode == RMX_GRAD_ACC_FINAL;
+      const int wmode = mode == RMX_GRAD_ACC_F32 ? RMX_GRAD_WRITE_F32
+                        : mode == RMX_GRAD_ACC_FINAL ? RMX_GRAD_WRITE_BF16 : mode;
+      constexpr int RUN = 16;
+#pragma unroll
+      for (int i0 = 0; i0 < BKV / 4; i0 += RUN) {
+        f32x4 prev[RUN];
+#pragma unroll
+        for (int i = 0; i < RUN; ++i) {
+          const int kk = k0 + rw + 4 * (i0 + i);
+          prev[i] = rd && kk < sk ? *reinterpret_cast<const f32x4*>(gptr(kk)) : f32x4{};
+        }
+#pragma unroll
+        for (int i = 0; i < RUN; ++i) {
+          const int row = rw + 4 * (i0 + i), kk = k0 + row;
+          if (kk >= sk) return;
+          f32x4 v = *reinterpret_cast<const f32x4*>(stg + row * HD + col);
+          if (rd) v += prev[i];
+          grad_store4<DT>(wmode, gptr(kk), bptr(kk), v);
+        }
+      }
+      return;
+    }
     for (int row = rw; row < BKV && k0 + row < sk; row += 4) {
       const int kk = k0 + row;
       const f32x4 v = *reinterpret_cast<const f32x4*>(stg + row * HD + col);
-      float* ga = gacc ? gacc + bb * L.ka_sb + (int64_t)kk * L.ka_ss + kvh * L.ka_sh + col : nullptr;
-      uint16_t* gb = gbf ? gbf + bb * L.dk_sb + (int64_t)kk * L.dk_ss + kvh * L.dk_sh + col : nullptr;
-      if (vf && vb) {
-        grad_store4<DT>(mode, ga, gb, v);
-        continue;
-      }
+      float* ga = gptr(kk);
+      uint16_t* gb = bptr(kk);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {  // a caller pointer below vector alignment
         if (mode == RMX_GRAD_WRITE_F32) {

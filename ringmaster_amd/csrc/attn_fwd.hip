@@ -519,7 +519,21 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
   const float lse_b = lt > 0.f ? (m_run + fast_log2(lt)) * kLn2 : kNegInf;
   const int64_t lrow = bb * L.l_sb + head * L.l_sh + q;
   float wa = 0.f, wb = 1.f, lnew = lse_b;
-  if (P.mode == RMX_FWD_ACC_MERGE || P.mode == RMX_FWD_ACC_FINAL) {
+  float* accrow = P.acc_out ? P.acc_out + bb * L.a_sb + (int64_t)q * L.a_ss + head * L.a_sh : nullptr;
+  uint16_t* orow = P.out ? P.out + bb * L.o_sb + (int64_t)q * L.o_ss + head * L.o_sh : nullptr;
+  // the merging modes read the row's running out (and lse) before the first store: one
+  // wait, not one memory round trip per 4 columns (the compiler keeps a read of accrow
+  // after every earlier store to it)
+  const bool rd = P.mode == RMX_FWD_ACC_MERGE || P.mode == RMX_FWD_ACC_FINAL;
+  f32x4 prev[NDB][4];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d0 = 32 * db + 8 * j + 4 * hl;
+      prev[db][j] = rd && d0 < D ? *reinterpret_cast<const f32x4*>(accrow + d0) : f32x4{};
+    }
+  if (rd) {
     const float la = P.acc_lse[lrow];
     const float mxl = fmaxf(la, lse_b);
     if (mxl == kNegInf) {
@@ -534,8 +548,6 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
     }
   }
   wb *= inv;
-  float* accrow = P.acc_out ? P.acc_out + bb * L.a_sb + (int64_t)q * L.a_ss + head * L.a_sh : nullptr;
-  uint16_t* orow = P.out ? P.out + bb * L.o_sb + (int64_t)q * L.o_ss + head * L.o_sh : nullptr;
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -547,10 +559,7 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
       v[1] = o[db][4 * j + 1] * wb;
       v[2] = o[db][4 * j + 2] * wb;
       v[3] = o[db][4 * j + 3] * wb;
-      if (P.mode == RMX_FWD_ACC_MERGE || P.mode == RMX_FWD_ACC_FINAL) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(accrow + d0);
-        v += a * wa;
-      }
+      if (rd) v += prev[db][j] * wa;
       // every mode leaves the fp32 result in acc_out when it is given (WRITE and
       // ACC_FINAL: the final out in fp32, which the backward's delta reads)
       if (accrow) *reinterpret_cast<f32x4*>(accrow + d0) = v;

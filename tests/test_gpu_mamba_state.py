@@ -85,11 +85,12 @@ def test_chunk_state_forward(R, T, H, D, G, N, docs):
 # the configs[4] layout (64 heads in one group) on a shorter shard
 # groups of 12 and 10 heads: 8-head strips ending part-way; (1, 300, 3, 64, 1, 128): an
 # odd head count (the second head slot idles in the last step, no 8-head tables)
-# (2, 512, 64, ...) and (1, 384, 32, ...): 8 and 2 groups of 8 heads per C group, so the
-# two-head backward starts its workgroups at rotated head groups
+# (2, 512, 64, ...) and (1, 384, 32, ...): 8 and 2 groups of 8 heads per C group, so
+# both backward forms start their workgroups at rotated head groups; (1, 600, 16, 128,
+# ...): the same in the one-head form at head_dim 128 (three token blocks)
 BWD_CASES = CASES[:4] + [(1, 256, 24, 64, 2, 128), (1, 160, 20, 64, 2, 64),
                          (2, 512, 64, 64, 1, 128), (1, 300, 3, 64, 1, 128),
-                         (1, 384, 32, 64, 2, 128)]
+                         (1, 384, 32, 64, 2, 128), (1, 600, 16, 128, 1, 64)]
 
 
 @pytest.mark.parametrize("two_heads", [True, False])
