@@ -543,8 +543,8 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
 //   dK -= (P dP')^T Q       A = (P dP')^T, B = Q^T (transposed LDS reads)
 // (dS = P (dP - delta) = -P dP'; the sign goes into the final scale of dK.)
 // A tile is a software pipeline of four phases of NS = HD/8 steps, one MFMA per
-// step, each step's VALU work issued under its MFMA and its LDS operand read six
-// to seven steps ahead, in pairs every other step (across phase and tile
+// step, each step's VALU work issued under its MFMA and its LDS operand read eight
+// to nine steps ahead, in pairs every other step (across phase and tile
 // boundaries):
 //   phase 0: dP'_j           | exponentials of S_j rows 0..31, P^T block 0
 //   phase 1: dV_j            | exponentials of rows 32..63, P^T blocks 1..3,
@@ -907,8 +907,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
 
   // operand read-ahead (steps). Reads come in pairs every other step, the later step's
   // operand first: the wait before an even step's MFMA then also covers the next step's
-  // operand, so one s_waitcnt serves two MFMAs.
-  constexpr int KD = 6, RING = 8;
+  // operand, so one s_waitcnt serves two MFMAs. Eight steps ahead measured 1.2% faster per
+  // configs[2] launch than six (an 8-slot ring), twelve and fourteen 2-7% slower.
+  constexpr int KD = 8, RING = 16;
   // the ring's slots line up across tiles: a tile is 4 NS steps
   static_assert((4 * NS) % RING == 0 && KD + 2 <= RING && KD % 2 == 0,
                 "operand ring size must divide the tile's steps");
