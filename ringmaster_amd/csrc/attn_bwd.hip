@@ -908,7 +908,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   // operand read-ahead (steps). Reads come in pairs every other step, the later step's
   // operand first: the wait before an even step's MFMA then also covers the next step's
   // operand, so one s_waitcnt serves two MFMAs. Eight steps ahead measured 1.2% faster per
-  // configs[2] launch than six (an 8-slot ring), twelve and fourteen 2-7% slower.
+  // configs[2] launch than six (an 8-slot ring), twelve and fourteen 2-7% slower (ten
+  // crashes the ROCm 7.2 device compiler).
   constexpr int KD = 8, RING = 16;
   // the ring's slots line up across tiles: a tile is 4 NS steps
   static_assert((4 * NS) % RING == 0 && KD + 2 <= RING && KD % 2 == 0,
