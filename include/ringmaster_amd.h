@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 15 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 16 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
                               8: allocation-free Mamba2 correction bwd;
                               9: carried-in state h_in / dh_in of the linear scan;
@@ -37,7 +37,9 @@ extern "C" {
                                   up to 128; 12: fp16 attention (layout dtype);
                               13: attention dropout;
                               14: workspace of the Mamba2 shard-state backward;
-                              15: attention head_dim up to 256 */
+                              15: attention head_dim up to 256;
+                              16: per-batch-row document metadata (layout m_sb),
+                                  dropout with document masks */
 
 /* error codes */
 #define RMX_OK 0
@@ -52,7 +54,8 @@ extern "C" {
 /* block mask kinds (ring/kernels.py:64-67, ring/varlen_blocks.py:51-58) */
 #define RMX_MASK_FULL 0   /* every (q, k) pair attends */
 #define RMX_MASK_CAUSAL 1 /* bottom-right aligned causal: k <= q + (sk - sq) */
-#define RMX_MASK_DOC 2    /* q_doc[q] == k_doc[k] && k_gidx[k] <= q_gidx[q] */
+#define RMX_MASK_DOC 2    /* q_doc[q] == k_doc[k] && k_gidx[k] <= q_gidx[q]; the four arrays
+                             advance by the layout's m_sb per batch row */
 /* RMX_DROPOUT: with dropout_p > 0, element (b, h, q, k) of a problem (h the q head) is kept when
  *   fmix32(bhmix ^ (q + drop_q0) * 0x85ebca77 ^ (k + drop_k0) * 0xc2b2ae3d) >= floor(p * 2^32),
  *   bhmix = fmix32(drop_seed_lo ^ fmix32(drop_seed_hi ^ (b * hq + h) * 0x9e3779b9)),
@@ -97,7 +100,7 @@ typedef struct rmx_attn_layout {
                                        type; accumulators, lse and delta stay fp32 */
   float dropout_p;                  /* attention dropout probability in [0, 1); 0: none. The
                                        mask is a hash of (drop_seed, batch, q head, query, key),
-                                       see RMX_DROPOUT below; RMX_MASK_FULL / _CAUSAL only */
+                                       see RMX_DROPOUT below */
   uint32_t drop_seed_lo, drop_seed_hi;
   /* element strides (batch, seq, head) */
   int64_t q_sb, q_ss, q_sh;
@@ -108,6 +111,9 @@ typedef struct rmx_attn_layout {
   int64_t l_sb, l_sh;         /* lse, acc_lse, delta: [batch, head, seq], seq stride 1 */
   int64_t dk_sb, dk_ss, dk_sh; /* bf16 dk/dv outputs */
   int64_t ka_sb, ka_ss, ka_sh; /* fp32 dk/dv accumulators */
+  int64_t m_sb;               /* RMX_MASK_DOC: int32 element stride between the batch rows of
+                                 q_gidx, k_gidx, q_doc and k_doc (0: every row shares them;
+                                 ring/loop.py:178 gives each packed row its own documents) */
 } rmx_attn_layout;
 
 /* One block-attention forward problem: q[sq] attends k/v[sk]. */
@@ -119,8 +125,12 @@ typedef struct rmx_fwd_problem {
   float* lse;           /* fp32 [b, hq, sq], may be NULL in ACC_INIT/ACC_MERGE */
   float* acc_out;       /* fp32 running out (ACC_* modes) */
   float* acc_lse;       /* fp32 running lse (ACC_* modes) */
-  const int32_t* q_gidx; /* RMX_MASK_DOC: global token index of each q row (strictly increasing) */
-  const int32_t* k_gidx; /* RMX_MASK_DOC: global token index of each k row (strictly increasing) */
+  const int32_t* q_gidx; /* RMX_MASK_DOC: global token index of each q row (non-decreasing) */
+  const int32_t* k_gidx; /* RMX_MASK_DOC: global token index of each k row (non-decreasing).
+                            The kernels only compare it with q_gidx (k_gidx <= q_gidx, and the
+                            window on q_gidx - k_gidx): a caller that passes each key's document
+                            start instead gets same-document attention without the causal
+                            bound (the non-causal packed ring, ring/loop.py:149,183-184) */
   const int32_t* q_doc;  /* RMX_MASK_DOC: document id of each q row (non-decreasing), i.e.
                             doc_ids_from_cu(cu_seqlens)[q_gidx] (ring/varlen_blocks.py:45-48) */
   const int32_t* k_doc;  /* RMX_MASK_DOC: document id of each k row (non-decreasing) */

@@ -489,14 +489,20 @@ def allgather_ring_forward(qs, ks, vs, *, causal=True, scaling=None, window=None
     return outs, lses
 
 
-def varlen_ring_forward(qs, ks, vs, cu_seqlens, *, scaling=None, window=None):
-    """The packed gather ring's explicit path (ring/loop.py:175-198), causal: rank r's
-    query at global index ``r L + i`` attends gathered key j when both lie in one
-    document, ``j <= r L + i`` and (window) ``r L + i - j <= window[0]``. Per-rank
-    [b, H, L, d] -> per-rank out [b, L, H, d] and lse [b, H, L]. Differentiable."""
-    world, L = len(qs), qs[0].shape[2]
+def varlen_ring_forward(qs, ks, vs, cu_seqlens, *, scaling=None, causal=True, window=None,
+                        dropout=0.0, drop_seed=None):
+    """The packed gather ring's explicit path (ring/loop.py:103-198, the math branch
+    :178-198). ``cu_seqlens`` covers the b S tokens of the flattened batch and is reshaped
+    to one document list per batch row (:178). Rank r's query at global index ``r L + i``
+    of row ``row`` attends gathered key j of the same row when both lie in one document
+    (:182), ``j <= r L + i`` when ``causal`` (:183-184) and ``r L + i - j <= window[0]``
+    when a window is given (:185-186). With ``dropout`` and ``drop_seed`` the kept
+    probabilities follow the hash mask of that seed over (row, head, r L + i, j) instead of
+    SDPA's RNG (:189-197). Per-rank [b, H, L, d] -> per-rank out [b, L, H, d] and lse
+    [b, H, L]. Differentiable (torch autograd)."""
+    world, b, L = len(qs), qs[0].shape[0], qs[0].shape[2]
     S = world * L
-    doc = doc_ids_from_cu(cu_seqlens)
+    doc = doc_ids_from_cu(cu_seqlens).reshape(b, S)
     k = torch.cat([t.transpose(1, 2) for t in ks], dim=1)
     v = torch.cat([t.transpose(1, 2) for t in vs], dim=1)
     kidx = torch.arange(S)
@@ -504,12 +510,26 @@ def varlen_ring_forward(qs, ks, vs, cu_seqlens, *, scaling=None, window=None):
     outs, lses = [], []
     for r in range(world):
         qidx = torch.arange(r * L, r * L + L)
-        allow = (doc[qidx][:, None] == doc[None, :]) & (kidx[None, :] <= qidx[:, None])
+        allow = doc[:, qidx, None] == doc[:, None, :]  # [b, L, S]
+        if causal:
+            allow &= (kidx[None, :] <= qidx[:, None])[None]
         if window is not None:
-            allow &= qidx[:, None] - kidx[None, :] <= window[0]
-        m = torch.where(allow, torch.zeros(()), torch.full((), NEG_INF))
-        o, lse = masked_block_fwd(qs[r].transpose(1, 2), k, v, m, scale)
-        outs.append(o)
+            allow &= (qidx[:, None] - kidx[None, :] <= window[0])[None]
+        m = torch.where(allow, torch.zeros(()), torch.full((), NEG_INF))[:, None]
+        q = qs[r].transpose(1, 2)
+        hq = q.shape[2]
+        qf = q.transpose(1, 2).float()
+        kf = _repeat_kv(k, hq).transpose(1, 2).float()
+        vf = _repeat_kv(v, hq).transpose(1, 2).float()
+        scores = (qf @ kf.transpose(-1, -2)) * scale + m
+        lse = torch.logsumexp(scores, dim=-1)
+        safe = torch.where(torch.isinf(lse), torch.zeros_like(lse), lse)
+        p = torch.exp(scores - safe.unsqueeze(-1))
+        if dropout and drop_seed is not None:
+            p = p * dropout_scale_mask(drop_seed, b, hq, L, S, dropout, q0=r * L, k0=0)
+        elif dropout:
+            p = torch.nn.functional.dropout(p, p=dropout)
+        outs.append((p @ vf).transpose(1, 2).to(q.dtype))
         lses.append(lse)
     return outs, lses
 

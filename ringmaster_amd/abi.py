@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
-ABI_VERSION = 15  # RMX_ABI_VERSION of include/ringmaster_amd.h
+ABI_VERSION = 16  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
@@ -63,6 +63,7 @@ class AttnLayout(ctypes.Structure):
         ("l_sb", _i64), ("l_sh", _i64),
         ("dk_sb", _i64), ("dk_ss", _i64), ("dk_sh", _i64),
         ("ka_sb", _i64), ("ka_ss", _i64), ("ka_sh", _i64),
+        ("m_sb", _i64),
     ]
 
 

@@ -50,8 +50,7 @@ int check_layout(const rmx_attn_layout* L) {
     return fail(RMX_EINVAL, "unknown element type %d", L->dtype);
   if (!(L->dropout_p >= 0.f && L->dropout_p < 1.f))
     return fail(RMX_EINVAL, "dropout_p must lie in [0, 1) (got %g)", (double)L->dropout_p);
-  if (L->dropout_p > 0.f && L->mask == RMX_MASK_DOC)
-    return fail(RMX_EUNSUPPORTED, "dropout with document masks is not implemented");
+  if (L->m_sb < 0) return fail(RMX_EINVAL, "m_sb must be non-negative (got %lld)", (long long)L->m_sb);
   const int64_t bf[] = {L->q_sb, L->q_ss, L->q_sh, L->k_sb, L->k_ss, L->k_sh,
                         L->v_sb, L->v_ss, L->v_sh, L->o_sb, L->o_ss, L->o_sh,
                         L->dk_sb, L->dk_ss, L->dk_sh};

@@ -213,6 +213,12 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
   const int qt = nqt - 1 - wc.tile;  // heaviest causal tiles first
   const int head = wc.group % L.hq;
   const int bb = wc.group / L.hq;
+  // document metadata of this batch row (RMX_MASK_DOC; m_sb = 0: shared by every row)
+  const int64_t moff = MASK == RMX_MASK_DOC ? bb * L.m_sb : 0;
+  const int32_t* const qgid = P.q_gidx + moff;
+  const int32_t* const kgid = P.k_gidx + moff;
+  const int32_t* const qdoc = P.q_doc + moff;
+  const int32_t* const kdoc = P.k_doc + moff;
   const int kvh = head / (L.hq / L.hkv);
   const int sq = P.sq, sk = P.sk;
   constexpr int mask = MASK;
@@ -227,8 +233,8 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
 
   int qg = -2147483647, qd = -1;
   if (mask == RMX_MASK_DOC && qvalid) {
-    qg = P.q_gidx[q];
-    qd = P.q_doc[q];
+    qg = qgid[q];
+    qd = qdoc[q];
   }
   const int D = L.head_dim;        // columns past D (up to HD) load as zeros
   const int wl = window_bound(P);  // pos_q - pos_k <= wl
@@ -252,10 +258,10 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
     kt_begin = kmin <= 0 ? 0 : (kmin / BK < nkt ? kmin / BK : nkt);
     if (kt_end < kt_begin) kt_end = kt_begin;
   } else {
-    qg_first = P.q_gidx[q0];
-    qg_last = P.q_gidx[qlast];
-    qd_first = P.q_doc[q0];
-    qd_last = P.q_doc[qlast];
+    qg_first = qgid[q0];
+    qg_last = qgid[qlast];
+    qd_first = qdoc[q0];
+    qd_last = qdoc[qlast];
     if (tid == 0) {
       sRange[0] = nkt;
       sRange[1] = -1;
@@ -264,8 +270,8 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
     int lo = nkt, hi = -1;
     for (int t = tid; t < nkt; t += NT) {
       const int ka = t * BK, kz = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
-      const int kga = P.k_gidx[ka], kgz = P.k_gidx[kz];
-      const int kda = P.k_doc[ka], kdz = P.k_doc[kz];
+      const int kga = kgid[ka], kgz = kgid[kz];
+      const int kda = kdoc[ka], kdz = kdoc[kz];
       if (kga <= qg_last && kdz >= qd_first && kda <= qd_last && (int64_t)kgz >= (int64_t)qg_first - wl) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
@@ -327,8 +333,8 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
     const int ka = (kt_begin + (live ? t : 0)) * BK;
     if (DOCDMA && wave == 0) {
       const uint32_t n = live ? 4u * (uint32_t)(sk - ka) : 0u;
-      dma4_async(make_rsrc(P.k_gidx + ka, n), lds_addr(&sKg[b][0]), 4 * lane);
-      dma4_async(make_rsrc(P.k_doc + ka, n), lds_addr(&sKd[b][0]), 4 * lane);
+      dma4_async(make_rsrc(kgid + ka, n), lds_addr(&sKg[b][0]), 4 * lane);
+      dma4_async(make_rsrc(kdoc + ka, n), lds_addr(&sKd[b][0]), 4 * lane);
     }
     const i32x4 krs = make_rsrc(kb0 + (int64_t)ka * kss, live ? kspan - (uint32_t)(ka * kss) : 0u);
     const i32x4 vrs = make_rsrc(vb0 + (int64_t)ka * vss, live ? vspan - (uint32_t)(ka * vss) : 0u);
@@ -599,6 +605,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   const rmx_bwd_problem& P = prm.P[wc.p];
   const int kvh = wc.group % L.hkv;
   const int bb = wc.group / L.hkv;
+  // document metadata of this batch row (RMX_MASK_DOC; m_sb = 0: shared by every row)
+  const int64_t moff = MASK == RMX_MASK_DOC ? bb * L.m_sb : 0;
+  const int32_t* const qgid = P.q_gidx + moff;
+  const int32_t* const kgid = P.k_gidx + moff;
+  const int32_t* const qdoc = P.q_doc + moff;
+  const int32_t* const kdoc = P.k_doc + moff;
   const int G = L.hq / L.hkv;
   const int sq = P.sq, sk = P.sk;
   constexpr int mask = MASK;
@@ -629,10 +641,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     qt_end = qmax < 0 ? 0 : (qmax / BQ + 1 < nqt ? qmax / BQ + 1 : nqt);
     if (qt_end < qt_begin) qt_end = qt_begin;
   } else {
-    kg_first = P.k_gidx[k0];
-    kg_last = P.k_gidx[klast];
-    kd_first = P.k_doc[k0];
-    kd_last = P.k_doc[klast];
+    kg_first = kgid[k0];
+    kg_last = kgid[klast];
+    kd_first = kdoc[k0];
+    kd_last = kdoc[klast];
     if (tid == 0) {
       sRange[0] = nqt;
       sRange[1] = -1;
@@ -641,8 +653,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     int lo = nqt, hi = -1;
     for (int t = tid; t < nqt; t += C::NT) {
       const int qa = t * BQ, qz = (t * BQ + BQ < sq ? t * BQ + BQ : sq) - 1;
-      const int qga = P.q_gidx[qa], qgz = P.q_gidx[qz];
-      const int qda = P.q_doc[qa], qdz = P.q_doc[qz];
+      const int qga = qgid[qa], qgz = qgid[qz];
+      const int qda = qdoc[qa], qdz = qdoc[qz];
       if (qgz >= kg_first && qdz >= kd_first && qda <= kd_last && (int64_t)qga <= (int64_t)kg_last + wl) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
@@ -722,8 +734,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     if (mask == RMX_MASK_DOC && tid < BQ) {
       const int qq = cu.qt * BQ + tid;
       if (qq < sq) {
-        nqg = P.q_gidx[qq];
-        nqd = P.q_doc[qq];
+        nqg = qgid[qq];
+        nqd = qdoc[qq];
       } else {
         nqg = -2147483647;  // rows past the end: masked
         nqd = -1;
@@ -789,8 +801,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   }
   int kg = 2147483647, kd = -2;
   if (mask == RMX_MASK_DOC && kvalid) {
-    kg = P.k_gidx[key];
-    kd = P.k_doc[key];
+    kg = kgid[key];
+    kd = kdoc[key];
   }
   // this lane's highest query: q + off <= key + wl (document masks: global index <= khi)
   const int khi = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg + wl) : key + wl - off;
@@ -1204,6 +1216,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
   const rmx_bwd_problem& P = prm.P[wc.p];
   const int kvh = wc.group % L.hkv;
   const int bb = wc.group / L.hkv;
+  // document metadata of this batch row (RMX_MASK_DOC; m_sb = 0: shared by every row)
+  const int64_t moff = MASK == RMX_MASK_DOC ? bb * L.m_sb : 0;
+  const int32_t* const qgid = P.q_gidx + moff;
+  const int32_t* const kgid = P.k_gidx + moff;
+  const int32_t* const qdoc = P.q_doc + moff;
+  const int32_t* const kdoc = P.k_doc + moff;
   const int G = L.hq / L.hkv;
   const int sq = P.sq, sk = P.sk;
   constexpr int mask = MASK;
@@ -1234,10 +1252,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
     qt_end = qmax < 0 ? 0 : (qmax / BQ + 1 < nqt ? qmax / BQ + 1 : nqt);
     if (qt_end < qt_begin) qt_end = qt_begin;
   } else {
-    kg_first = P.k_gidx[k0];
-    kg_last = P.k_gidx[klast];
-    kd_first = P.k_doc[k0];
-    kd_last = P.k_doc[klast];
+    kg_first = kgid[k0];
+    kg_last = kgid[klast];
+    kd_first = kdoc[k0];
+    kd_last = kdoc[klast];
     if (tid == 0) {
       sRange[0] = nqt;
       sRange[1] = -1;
@@ -1246,8 +1264,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
     int lo = nqt, hi = -1;
     for (int t = tid; t < nqt; t += NT) {
       const int qa = t * BQ, qz = (t * BQ + BQ < sq ? t * BQ + BQ : sq) - 1;
-      const int qga = P.q_gidx[qa], qgz = P.q_gidx[qz];
-      const int qda = P.q_doc[qa], qdz = P.q_doc[qz];
+      const int qga = qgid[qa], qgz = qgid[qz];
+      const int qda = qdoc[qa], qdz = qdoc[qz];
       if (qgz >= kg_first && qdz >= kd_first && qda <= kd_last && (int64_t)qga <= (int64_t)kg_last + wl) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
@@ -1317,8 +1335,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
     if (mask == RMX_MASK_DOC && tid < BQ) {
       const int qq = cu.qt * BQ + tid;
       if (qq < sq) {
-        nqg = P.q_gidx[qq];
-        nqd = P.q_doc[qq];
+        nqg = qgid[qq];
+        nqd = qdoc[qq];
       } else {
         nqg = -2147483647;  // rows past the end: masked
         nqd = -1;
@@ -1360,8 +1378,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
   }
   int kg = 2147483647, kd = -2;
   if (mask == RMX_MASK_DOC && kvalid) {
-    kg = P.k_gidx[key];
-    kd = P.k_doc[key];
+    kg = kgid[key];
+    kd = kdoc[key];
   }
   // this lane's highest query: q + off <= key + wl (document masks: global index <= khi)
   const int khi = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg + wl) : key + wl - off;
@@ -1632,7 +1650,6 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
   drop_params(L.dropout_p, &pq.drop_thr, &pq.drop_scale);
   pk.drop_thr = pq.drop_thr;
   pk.drop_scale = pq.drop_scale;
-  if (DROP && L.mask == RMX_MASK_DOC) return hipErrorInvalidValue;  // refused by the host
   // problems with an empty side or a skipped gradient get no workgroups there;
   // the others run longest workgroups first (dQ: key tiles, dK/dV: query tiles x group)
   const int G = L.hq / L.hkv;
@@ -1669,7 +1686,7 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
     if (L.mask == RMX_MASK_CAUSAL)
       hipLaunchKernelGGL((attn_bwd_dkdv_d256_kernel<RMX_MASK_CAUSAL, DT, DROP>), grid, dim3(256), 0, stream, pk);
     else if (L.mask == RMX_MASK_DOC)
-      hipLaunchKernelGGL((attn_bwd_dkdv_d256_kernel<RMX_MASK_DOC, DT, false>), grid, dim3(256), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_d256_kernel<RMX_MASK_DOC, DT, DROP>), grid, dim3(256), 0, stream, pk);
     else
       hipLaunchKernelGGL((attn_bwd_dkdv_d256_kernel<RMX_MASK_FULL, DT, DROP>), grid, dim3(256), 0, stream, pk);
     hipError_t e = hipGetLastError();
@@ -1680,7 +1697,7 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
     if (L.mask == RMX_MASK_CAUSAL)
       hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_CAUSAL, DT, DROP>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     else if (L.mask == RMX_MASK_DOC)
-      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_DOC, DT, false>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
+      hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_DOC, DT, DROP>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     else
       hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HD, RMX_MASK_FULL, DT, DROP>), grid, dim3(DkdvCfg<HD>::NT), 0, stream, pk);
     hipError_t e = hipGetLastError();
@@ -1692,7 +1709,7 @@ static hipError_t launch_bwd_t(const rmx_attn_layout& L, const rmx_bwd_problem* 
     if (L.mask == RMX_MASK_CAUSAL)
       hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_CAUSAL, DT, DROP>), grid, dim3(DqCfg<HD>::NT), 0, stream, pq);
     else if (L.mask == RMX_MASK_DOC)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_DOC, DT, false>), grid, dim3(DqCfg<HD>::NT), 0, stream, pq);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_DOC, DT, DROP>), grid, dim3(DqCfg<HD>::NT), 0, stream, pq);
     else
       hipLaunchKernelGGL((attn_bwd_dq_kernel<HD, RMX_MASK_FULL, DT, DROP>), grid, dim3(DqCfg<HD>::NT), 0, stream, pq);
     return hipGetLastError();

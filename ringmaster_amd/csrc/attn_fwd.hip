@@ -92,6 +92,12 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
   const int qt = nqt - 1 - wc.tile;  // heaviest causal tiles first
   const int head = wc.group % L.hq;
   const int bb = wc.group / L.hq;
+  // document metadata of this batch row (RMX_MASK_DOC; m_sb = 0: shared by every row)
+  const int64_t moff = MASK == RMX_MASK_DOC ? bb * L.m_sb : 0;
+  const int32_t* const qgid = P.q_gidx + moff;
+  const int32_t* const kgid = P.k_gidx + moff;
+  const int32_t* const qdoc = P.q_doc + moff;
+  const int32_t* const kdoc = P.k_doc + moff;
   const int kvh = head / (L.hq / L.hkv);
   const int sq = P.sq, sk = P.sk;
   constexpr int mask = MASK;
@@ -105,8 +111,8 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
 
   int qg = -2147483647, qd = -1;
   if (mask == RMX_MASK_DOC && q < sq) {
-    qg = P.q_gidx[q];
-    qd = P.q_doc[q];
+    qg = qgid[q];
+    qd = qdoc[q];
   }
   const int D = L.head_dim;          // columns past D (up to HD) load as zeros
   const int wl = window_bound(P);    // pos_q - pos_k <= wl
@@ -135,10 +141,10 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
     kt_begin = kmin <= 0 ? 0 : (kmin / BK < nkt ? kmin / BK : nkt);
     if (kt_end < kt_begin) kt_end = kt_begin;
   } else {
-    qg_first = P.q_gidx[q0];
-    qg_last = P.q_gidx[qlast];
-    qd_first = P.q_doc[q0];
-    qd_last = P.q_doc[qlast];
+    qg_first = qgid[q0];
+    qg_last = qgid[qlast];
+    qd_first = qdoc[q0];
+    qd_last = qdoc[qlast];
     if (tid == 0) {
       sRange[0] = nkt;
       sRange[1] = -1;
@@ -147,8 +153,8 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
     int lo = nkt, hi = -1;
     for (int t = tid; t < nkt; t += C::NT) {
       const int ka = t * BK, kz = (t * BK + BK < sk ? t * BK + BK : sk) - 1;
-      const int kga = P.k_gidx[ka], kgz = P.k_gidx[kz];
-      const int kda = P.k_doc[ka], kdz = P.k_doc[kz];
+      const int kga = kgid[ka], kgz = kgid[kz];
+      const int kda = kdoc[ka], kdz = kdoc[kz];
       if (kga <= qg_last && kdz >= qd_first && kda <= qd_last && (int64_t)kgz >= (int64_t)qg_first - wl) {
         lo = t < lo ? t : lo;
         hi = t > hi ? t : hi;
@@ -205,8 +211,8 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
   constexpr bool DOCDMA = mask == RMX_MASK_DOC;
   i32x4 kgrs = {0, 0, 0, 0}, kdrs = {0, 0, 0, 0};
   if (DOCDMA) {
-    kgrs = make_rsrc(P.k_gidx, 4u * (uint32_t)sk);
-    kdrs = make_rsrc(P.k_doc, 4u * (uint32_t)sk);
+    kgrs = make_rsrc(kgid, 4u * (uint32_t)sk);
+    kdrs = make_rsrc(kdoc, 4u * (uint32_t)sk);
   }
   auto dma_doc = [&](int t) __attribute__((always_inline)) {
     if (DOCDMA && wave == 0) {
@@ -602,10 +608,8 @@ static hipError_t launch_fwd_t(const rmx_attn_layout& L, const rmx_fwd_problem* 
   if (L.mask == RMX_MASK_CAUSAL)
     hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_CAUSAL, DT, DROP>), dim3(grid),
                        dim3(FwdCfg<HD>::NT), 0, stream, prm);
-  else if (L.mask == RMX_MASK_DOC && DROP)  // not instantiated (refused by the host)
-    return hipErrorInvalidValue;
   else if (L.mask == RMX_MASK_DOC)
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_DOC, DT, false>), dim3(grid),
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_DOC, DT, DROP>), dim3(grid),
                        dim3(FwdCfg<HD>::NT), 0, stream, prm);
   else
     hipLaunchKernelGGL((attn_fwd_kernel<HD, RMX_MASK_FULL, DT, DROP>), dim3(grid),

@@ -51,10 +51,37 @@ def _validate(q, k, v, dropout, window, softcap=0.0, alibi=None):
     return window_left(window)
 
 
-def new_dropout_seed() -> int:
-    """A 64-bit dropout seed from torch's default CPU generator (reproducible under
-    ``torch.manual_seed``; no device synchronization)."""
-    return int(torch.randint(-(1 << 63), (1 << 63) - 1, (1,), dtype=torch.int64)) & ((1 << 64) - 1)
+_M64 = (1 << 64) - 1
+
+
+def _splitmix64(x: int) -> int:
+    """SplitMix64's output function (Steele, Lea and Flood, 2014) on a 64-bit integer."""
+    x = (x + 0x9E3779B97F4A7C15) & _M64
+    x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & _M64
+    return x ^ (x >> 31)
+
+
+def dropout_rng_state(device=None) -> tuple[int, int]:
+    """Draw dropout randomness the way flash attention does: the (seed, offset) of the
+    device's default generator, whose offset the call advances by 4 (one philox step).
+    ``torch.manual_seed`` resets both, so the draws are reproducible, and torch's CPU
+    generator (the stream of samplers and other host randomness) is left untouched."""
+    idx = torch.cuda.current_device() if device is None else torch.device(device).index
+    gen = torch.cuda.default_generators[torch.cuda.current_device() if idx is None else idx]
+    seed, offset = gen.initial_seed(), gen.get_offset()
+    gen.set_offset(offset + 4)
+    return int(seed) & _M64, int(offset)
+
+
+def seed_of_rng_state(seed: int, offset: int) -> int:
+    """The kernels' 64-bit mask seed of a generator (seed, offset) pair."""
+    return _splitmix64(_splitmix64(seed) ^ offset)
+
+
+def new_dropout_seed(device=None) -> int:
+    """A 64-bit dropout mask seed from the device generator (see ``dropout_rng_state``)."""
+    return seed_of_rng_state(*dropout_rng_state(device))
 
 
 def window_left(window):
@@ -155,7 +182,8 @@ def mi355x_hip_block(q, k, v, *, causal, scaling, dropout=0.0, attn_implementati
     scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
     drop = None
     if dropout:
-        drop = (float(dropout), new_dropout_seed() if dropout_seed is None else int(dropout_seed))
+        drop = (float(dropout),
+                new_dropout_seed(q.device) if dropout_seed is None else int(dropout_seed))
     return _HipBlockAttention.apply(q, k, v, bool(causal), float(scale), left, drop)
 
 
@@ -174,10 +202,11 @@ def _flash_attn_forward(q, k, v, dropout_p, softmax_scale, causal, window_size_l
         raise NotImplementedError("return_softmax is not supported")
     rng_state, drop = None, None
     if dropout_p:
-        seed = new_dropout_seed()
-        drop = (float(dropout_p), seed)
-        # the Dao ops' rng_state: the seed (as the signed int64 of its 64 bits) and an offset
-        rng_state = torch.tensor([seed - (1 << 64) if seed >= (1 << 63) else seed, 0],
+        gseed, goff = dropout_rng_state(q.device)
+        drop = (float(dropout_p), seed_of_rng_state(gseed, goff))
+        # the Dao ops' rng_state: the generator's (seed, offset) as int64 (the seed's 64 bits
+        # read as signed), on the host, so the backward reads it without a device sync
+        rng_state = torch.tensor([gseed - (1 << 64) if gseed >= (1 << 63) else gseed, goff],
                                  dtype=torch.int64)
     out, lse = block_forward(_kernel_ready(q), _kernel_ready(k), _kernel_ready(v),
                              float(softmax_scale), bool(causal), window=left, dropout=drop)
@@ -193,7 +222,8 @@ def _flash_attn_backward(dout, q, k, v, out, lse, dq, dk, dv, dropout_p, softmax
     if dropout_p:
         if rng_state is None:
             raise ValueError("a backward with dropout needs the forward's rng_state")
-        drop = (float(dropout_p), int(torch.as_tensor(rng_state).flatten()[0]) & ((1 << 64) - 1))
+        st = torch.as_tensor(rng_state).flatten().tolist()
+        drop = (float(dropout_p), seed_of_rng_state(int(st[0]) & _M64, int(st[1])))
     _, _, _, delta = block_backward(_kernel_ready(dout), _kernel_ready(q), _kernel_ready(k),
                                     _kernel_ready(v), _kernel_ready(out), lse,
                                     float(softmax_scale), bool(causal), dq, dk, dv, window=left,

@@ -5,7 +5,7 @@ single block call, ``rotate_method="allgather"`` is the gather-then-attend ring
 (:201-228), anything else (the reference's ``alltoall``) is the p2p ring with its
 preconditions (FA2-class implementation, zero dropout, no window: :52-57).
 ``varlen_ring_attention`` attends within each packed document over the gathered K/V
-(:102-198). Inputs are the per-rank interface tensors ``[b, H, L, d]`` stacked on a
+(:102-198), each batch row with its own documents. Inputs are the per-rank interface tensors ``[b, H, L, d]`` stacked on a
 leading rank axis; outputs are ``[P, b, L, H, d]``.
 
 Gathering K/V and attending once per rank computes the same blocks as the p2p ring
@@ -55,7 +55,7 @@ def ring_attention(q, k, v, *, group=None, causal: bool, scaling=None, dropout: 
     if _method(rotate_method) == "allgather":
         if not 0.0 <= float(dropout) < 1.0:
             raise ValueError(f"dropout must lie in [0, 1) (got {dropout})")
-        drop = (float(dropout), new_dropout_seed()) if dropout else None
+        drop = (float(dropout), new_dropout_seed(q.device)) if dropout else None
         left = window_left(window)
         P, L = q.shape[0], q.shape[3]
         bounds = None
@@ -70,17 +70,24 @@ def ring_attention(q, k, v, *, group=None, causal: bool, scaling=None, dropout: 
 
 def varlen_ring_attention(q, k, v, *, group=None, scaling, cu_seqlens, causal=True,
                           dropout=0.0, window=None, attn_implementation="math", timer=None):
-    """Packed documents over contiguous shards: each query attends the earlier keys of
-    its own document (global positions ``r * L + i``). q/k/v: [P, b, H, L, d]; returns
-    [P, b, L, H, d]."""
+    """Packed documents over contiguous shards (ring/loop.py:103-198): ``cu_seqlens`` covers
+    the ``b S`` tokens of the flattened batch (``S = P L``), and batch row ``i`` packs the
+    documents of tokens ``[i S, (i + 1) S)`` (:178). A query at global position ``r L + i``
+    of its row attends the keys of its own document in that row: the earlier ones
+    (``causal``, :183-184), or all of them (``causal=False``, keys up to the document end as
+    in :149), within ``window[0]`` positions behind it when a window is given (:185-186).
+    ``dropout`` drops probabilities with the kernels' hash mask over (row, head, global query,
+    gathered key). q/k/v: [P, b, H, L, d]; returns [P, b, L, H, d]."""
     if group is not None:
         raise ValueError("the emulated ring takes the ranks on the leading axis, not a group")
-    if dropout:
-        raise NotImplementedError("dropout with document masks is not implemented")
-    if not causal:
-        raise NotImplementedError("packed (document-masked) blocks are causal in this build")
+    if not 0.0 <= float(dropout) < 1.0:
+        raise ValueError(f"dropout must lie in [0, 1) (got {dropout})")
     if not isinstance(cu_seqlens, torch.Tensor):
         cu_seqlens = torch.as_tensor(cu_seqlens)
     left = window_left(window)
-    return contiguous_ring(q, k, v, causal=True, scaling=scaling, doc=doc_for(cu_seqlens, q),
-                           timer=timer, window=None if left is None else [left] * q.shape[0])
+    if left is not None and not causal:
+        raise NotImplementedError("sliding windows on a non-causal packed ring are not supported")
+    drop = (float(dropout), new_dropout_seed(q.device)) if dropout else None
+    return contiguous_ring(q, k, v, causal=bool(causal), scaling=scaling,
+                           doc=doc_for(cu_seqlens, q, rows=q.shape[1]), timer=timer,
+                           window=None if left is None else [left] * q.shape[0], dropout=drop)

@@ -28,6 +28,7 @@ class FwdJob:
     lse: torch.Tensor | None = None
     acc_out: torch.Tensor | None = None
     acc_lse: torch.Tensor | None = None
+    # document-mask metadata: [sq] / [sk], or [batch, sq] / [batch, sk] per batch row
     q_gidx: torch.Tensor | None = None
     k_gidx: torch.Tensor | None = None
     q_doc: torch.Tensor | None = None
@@ -161,10 +162,34 @@ def _check_shapes(q, k, v, batch, hq, hkv, d):
 def _int32(t):
     if t is None:
         return None
-    if t.dtype != torch.int32 or not t.is_contiguous():
-        raise ValueError("index tensors must be contiguous int32")
+    if t.dtype != torch.int32 or t.stride(-1) != 1:
+        raise ValueError("index tensors must be int32 with a contiguous last axis")
     abi.require_device(t)
     return t.data_ptr()
+
+
+_META = ("q_gidx", "k_gidx", "q_doc", "k_doc")
+
+
+def _set_meta_stride(lay, jobs, batch):
+    """Document-mask metadata is [n] (every batch row shares it) or [batch, n] (per row,
+    ring/loop.py:178): the layout's m_sb is the row stride, which all of a call's
+    per-row arrays must share."""
+    strides = set()
+    for j in jobs:
+        for name in _META:
+            t = getattr(j, name)
+            if t is None:
+                continue
+            if t.dim() == 1 or (t.dim() == 2 and t.shape[0] == 1):
+                strides.add(0)
+            elif t.dim() == 2 and t.shape[0] == batch:
+                strides.add(t.stride(0))
+            else:
+                raise ValueError(f"{name} must be [n] or [batch, n] (got {tuple(t.shape)})")
+    if len(strides) > 1:
+        raise ValueError("the document metadata of one call must share its row stride")
+    lay.m_sb = int(strides.pop()) if strides else 0
 
 
 def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int, dropout=None) -> None:
@@ -178,6 +203,7 @@ def attn_fwd(jobs: list[FwdJob], *, scale: float, mask: int, dropout=None) -> No
         _check_shapes(j.q, j.k, j.v, batch, hq, hkv, d)
     lay = _fill_layout(jobs, batch, hq, hkv, d, scale, mask)
     _set_dropout(lay, dropout)
+    _set_meta_stride(lay, jobs, batch)
     arr = (abi.FwdProblem * len(jobs))()
     for i, j in enumerate(jobs):
         p = arr[i]
@@ -229,6 +255,7 @@ def attn_bwd(jobs: list[BwdJob], *, scale: float, mask: int, dropout=None) -> No
         _check_shapes(j.q, j.k, j.v, batch, hq, hkv, d)
     lay = _fill_layout(jobs, batch, hq, hkv, d, scale, mask)
     _set_dropout(lay, dropout)
+    _set_meta_stride(lay, jobs, batch)
     arr = (abi.BwdProblem * len(jobs))()
     for i, j in enumerate(jobs):
         p = arr[i]

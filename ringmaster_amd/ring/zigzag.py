@@ -97,18 +97,34 @@ class _Ctx:
         self.layout, self.causal = layout, causal
         self.window = None if window is None else [int(w) for w in window]
         self.dropout = dropout  # None or (p, seed): one mask over (rank's query, gathered key)
-        if dropout is not None and (layout == "zigzag" or doc is not None):
-            raise NotImplementedError("dropout runs on dense contiguous shards")
+        if dropout is not None and layout == "zigzag":
+            raise NotImplementedError("dropout runs on contiguous shards")
         if self.window is not None:
             if len(self.window) != self.P:
                 raise ValueError("the window takes one bound per rank")
             if layout == "zigzag" and doc is None:
                 raise NotImplementedError("sliding windows run on contiguous shards")
-        self.gidx = self.rdoc = None
+        self.gidx = self.kgidx = self.rdoc = None
         if doc is not None:
-            self.gidx = _global_rows(layout, self.P, self.L, q.device)
-            # document id of every local row of every rank: [P, L]
-            self.rdoc = doc[self.gidx.long()].to(torch.int32).contiguous()
+            # doc: [S] (every batch row packs the same documents) or [b, S] (each row its
+            # own, ring/loop.py:178). Per rank and row: the global index of every local row
+            # and its document id, [P, 1 or b, L] (the kernels step by L per batch row)
+            if not causal and layout != "contiguous":
+                raise NotImplementedError("non-causal document masks run on contiguous shards")
+            d2 = doc if doc.dim() == 2 else doc[None]
+            if d2.shape[0] not in (1, self.b):
+                raise ValueError(f"per-row documents must cover {self.b} rows (got {d2.shape[0]})")
+            rows32 = _global_rows(layout, self.P, self.L, q.device)
+            rows = rows32.long()
+            bm = d2.shape[0]
+            self.rdoc = d2[:, rows].permute(1, 0, 2).to(torch.int32).contiguous()
+            self.gidx = rows32[:, None, :].expand(self.P, bm, self.L).contiguous()
+            self.kgidx = self.gidx
+            if not causal:
+                # a key's bound is the first index of its document in its row: every query
+                # of the document passes k_gidx <= q_gidx (ring/loop.py:149,183-184)
+                start = torch.searchsorted(d2.contiguous(), d2.contiguous(), right=False)
+                self.kgidx = start[:, rows].permute(1, 0, 2).to(torch.int32).contiguous()
 
     def schedule(self, split_final: bool):
         if self.layout == "zigzag":
@@ -143,10 +159,13 @@ class _Ctx:
         return bl.rank * self.L + bl.q_lo, bl.kv_rank * self.L + bl.k_lo
 
     def idx(self, rank, lo, hi):
-        return None if self.gidx is None else self.gidx[rank, lo:hi]
+        return None if self.gidx is None else self.gidx[rank, :, lo:hi]
+
+    def kidx(self, rank, lo, hi):
+        return None if self.kgidx is None else self.kgidx[rank, :, lo:hi]
 
     def docs(self, rank, lo, hi):
-        return None if self.rdoc is None else self.rdoc[rank, lo:hi]
+        return None if self.rdoc is None else self.rdoc[rank, :, lo:hi]
 
 
 class KernelTimer:
@@ -239,7 +258,7 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
                 out=out[r][:, qs], lse=lse[r][:, :, qs],
                 acc_out=acc[r][:, qs],
                 acc_lse=None if acc_lse is None else acc_lse[r][:, :, qs],
-                q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
+                q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.kidx(kr, bl.k_lo, bl.k_hi),
                 q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi),
                 window=c.block_window(bl), **dict(zip(("drop_q0", "drop_k0"), c.block_drop(bl)))))
         with timer("attn_fwd"):
@@ -284,7 +303,7 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
             common = dict(
                 q=qd[r][:, qs], k=kd[kr][:, ks], v=vd[kr][:, ks], dout=dout[r][:, qs],
                 lse=lse[r][:, :, qs], delta=delta[r][:, :, qs], nlse=nlse[r][:, :, qs],
-                q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.idx(kr, bl.k_lo, bl.k_hi),
+                q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.kidx(kr, bl.k_lo, bl.k_hi),
                 q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi),
                 window=c.block_window(bl), **dict(zip(("drop_q0", "drop_k0"), c.block_drop(bl))))
             kv_jobs.append(ops.BwdJob(dq_mode=abi.GRAD_NONE, dkv_mode=mode,
@@ -345,17 +364,23 @@ def check_cu_seqlens(cu_seqlens, total: int) -> None:
         raise ValueError("cu_seqlens must not decrease")
 
 
-def doc_for(cu_seqlens, q):
-    """Per-token document ids of the packed sequence (None when not packed). A host
-    ``cu_seqlens`` is checked to cover the sequence; a device one is read without a
-    synchronization and must end at the sequence length, which the environment variable
-    ``RINGMASTER_AMD_DEBUG=1`` checks too (at the cost of a device-to-host copy)."""
+def doc_for(cu_seqlens, q, rows: int = 1):
+    """Per-token document ids of the packed sequence (None when not packed): [S] over the
+    sequence S = P L that every batch row shares (the zigzag and DistFlash rings,
+    ring/zigzag.py:89-90), or with ``rows`` = b, [b, S] over ``cu_seqlens`` covering the
+    b S tokens of the flattened batch, row ``i`` taking tokens ``[i S, (i + 1) S)`` (the
+    packed contiguous ring, ring/loop.py:178). A host ``cu_seqlens`` is checked to cover
+    the sequence; a device one is read without a synchronization and must end at that
+    length, which the environment variable ``RINGMASTER_AMD_DEBUG=1`` checks too (at the
+    cost of a device-to-host copy)."""
     if cu_seqlens is None:
         return None
-    total = q.shape[0] * q.shape[3]
+    seq = q.shape[0] * q.shape[3]
+    total = rows * seq
     if cu_seqlens.device.type == "cpu" or os.environ.get("RINGMASTER_AMD_DEBUG") == "1":
         check_cu_seqlens(cu_seqlens, total)
-    return doc_ids_from_cu(cu_seqlens, q.device, total)
+    doc = doc_ids_from_cu(cu_seqlens, q.device, total)
+    return doc.reshape(rows, seq) if rows > 1 else doc
 
 
 def zigzag_ring_attention(q, k, v, *, group=None, scaling=None, cu_seqlens=None, timer=None):

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 15
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 16
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -93,7 +93,7 @@ def test_host_validation_dropout():
     assert _fwd(_layout(dropout_p=1.0)) == abi.RMX_EINVAL
     assert _fwd(_layout(dropout_p=-0.1)) == abi.RMX_EINVAL
     assert b"dropout_p" in abi.lib().rmx_last_error()
-    assert _fwd(_layout(dropout_p=0.1, mask=abi.MASK_DOC)) == abi.RMX_EUNSUPPORTED
+    assert _fwd(_layout(dropout_p=0.1, mask=abi.MASK_DOC)) == abi.RMX_OK  # no problems: no launch
     assert _fwd(_layout(dropout_p=0.1, drop_seed_lo=5, drop_seed_hi=7)) == abi.RMX_OK
 
 
@@ -117,6 +117,14 @@ def test_problem_structs_match_the_header():
     assert abi.BwdProblem.has_window.offset == 17 * 8 + 4 * 4
     assert abi.FwdProblem.drop_k0.offset == 11 * 8 + 6 * 4
     assert abi.AttnLayout.q_sb.offset == 40  # after the dtype, dropout and seed words
+    assert abi.AttnLayout.m_sb.offset == 40 + 23 * 8  # after the 23 tensor strides
+    assert ctypes.sizeof(abi.AttnLayout) == 40 + 24 * 8
+
+
+def test_host_validation_metadata_stride():
+    assert _fwd(_layout(mask=abi.MASK_DOC, m_sb=-1)) == abi.RMX_EINVAL
+    assert b"m_sb" in abi.lib().rmx_last_error()
+    assert _fwd(_layout(mask=abi.MASK_DOC, m_sb=4096)) == abi.RMX_OK
 
 
 def test_host_validation_backward_nlse():

@@ -114,7 +114,10 @@ def test_dropout_dao_ops_rng_state():
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     bwd(do, q, k, v, out, lse, dq, dk, dv, 0.2, 0.125, True, -1, -1, 0.0, None, False, rng_state)
     torch.cuda.synchronize()
-    seed = int(rng_state[0]) & ((1 << 64) - 1)
+    from ringmaster_amd.ring.kernels import seed_of_rng_state
+
+    # rng_state: the device generator's (seed, offset), as flash returns it
+    seed = seed_of_rng_state(int(rng_state[0]) & ((1 << 64) - 1), int(rng_state[1]))
     qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf, kf, vf))
     ref, ref_lse = rm.math_block(qr, kr, vr, causal=True, scaling=0.125, dropout=0.2,
                                  drop_seed=seed)
@@ -159,3 +162,24 @@ def test_dropout_allgather_ring(causal):
         assert_bf16_close(dev[0].grad[r], refs[0][r].grad, f"dq rank {r}")
         assert_bf16_close(dev[1].grad[r], refs[1][r].grad, f"dk rank {r}", ulp_floor=True)
         assert_bf16_close(dev[2].grad[r], refs[2][r].grad, f"dv rank {r}", ulp_floor=True)
+
+
+def test_dropout_seeds_leave_the_cpu_stream_alone():
+    """Dropout draws its seed from the device generator's (seed, offset), as flash does: the
+    CPU generator's stream is unchanged, consecutive calls get different masks, and
+    torch.manual_seed makes the draws repeat."""
+    from ringmaster_amd.ring.kernels import mi355x_hip_block, new_dropout_seed
+
+    _, q = bf16_pair((1, 128, 2, 64), 21)
+    torch.manual_seed(7)
+    expect = torch.rand(4)
+    torch.manual_seed(7)
+    a, _ = mi355x_hip_block(q, q, q, causal=True, scaling=None, dropout=0.25)
+    b, _ = mi355x_hip_block(q, q, q, causal=True, scaling=None, dropout=0.25)
+    assert torch.equal(torch.rand(4), expect)
+    torch.manual_seed(7)
+    a2, _ = mi355x_hip_block(q, q, q, causal=True, scaling=None, dropout=0.25)
+    torch.cuda.synchronize()
+    assert torch.equal(a, a2) and not torch.equal(a, b)
+    torch.manual_seed(7)
+    assert new_dropout_seed() != new_dropout_seed()

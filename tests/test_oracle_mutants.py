@@ -286,3 +286,34 @@ def test_unshard_mutant_is_caught():
 
     with pytest.raises(AssertionError):
         check_shard_batch(osh.zigzag_shard_batch, reversed_ranks)
+
+
+def _varlen_shared_documents(qs, ks, vs, cu, *, causal):
+    """Mutant: every batch row packed with row 0's documents (the mask of ring/loop.py:182
+    built from the first S ids only)."""
+    P, L = len(qs), qs[0].shape[2]
+    S = P * L
+    cu0 = torch.tensor([c for c in cu.tolist() if c <= S] + ([S] if S not in cu.tolist() else []))
+    b = qs[0].shape[0]
+    outs = [[] for _ in range(P)]
+    lses = [[] for _ in range(P)]
+    for row in range(b):
+        o, l = rm.varlen_ring_forward([t[row:row + 1] for t in qs], [t[row:row + 1] for t in ks],
+                                      [t[row:row + 1] for t in vs], cu0, causal=causal)
+        for r in range(P):
+            outs[r].append(o[r])
+            lses[r].append(l[r])
+    return [torch.cat(o) for o in outs], [torch.cat(x) for x in lses]
+
+
+def _varlen_causal_ignored(qs, ks, vs, cu, *, causal):
+    """Mutant: the causal flag dropped (every packed ring causal)."""
+    return rm.varlen_ring_forward(qs, ks, vs, cu, causal=True)
+
+
+@pytest.mark.parametrize("mutant,causal", [(_varlen_shared_documents, True),
+                                            (_varlen_shared_documents, False),
+                                            (_varlen_causal_ignored, False)])
+def test_varlen_row_mutants_are_caught(mutant, causal):
+    with pytest.raises(AssertionError):
+        pin.check_varlen_rows(mutant, causal)

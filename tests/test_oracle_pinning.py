@@ -145,6 +145,74 @@ def test_varlen_ring_window_equals_per_document():
         assert torch.allclose(lse[:, :, a:b].double(), ref_l, atol=TOL32)
 
 
+def _varlen_rows_case(b=2, P=2, L=8, hq=2, hkv=1, d=8):
+    """Per-row documents (ring/loop.py:178): row 0 packs [5, 6, 5], row 1 [9, 7]; the
+    flattened cu_seqlens covers both rows."""
+    cu = torch.tensor([0, 5, 11, 16, 25, 32])
+    qs = [rnd(b, hq, L, d, seed=81 + r).requires_grad_(True) for r in range(P)]
+    ks = [rnd(b, hkv, L, d, seed=91 + r).requires_grad_(True) for r in range(P)]
+    vs = [rnd(b, hkv, L, d, seed=101 + r).requires_grad_(True) for r in range(P)]
+    return cu, qs, ks, vs
+
+
+def check_varlen_rows(fwd, causal):
+    """``fwd(qs, ks, vs, cu, causal=...)`` against brute-force attention of every document
+    alone in its own row (fp64 loops), values; and its autograd gradients against those of
+    per-document attention (fp64 torch)."""
+    cu, qs, ks, vs = _varlen_rows_case()
+    b, P, L = qs[0].shape[0], len(qs), qs[0].shape[2]
+    S = P * L
+    outs, lses = fwd(qs, ks, vs, cu, causal=causal)
+    out, lse = torch.cat(outs, 1), torch.cat(lses, 2)
+    qf, kf, vf = (torch.cat([t.transpose(1, 2) for t in ts], 1) for ts in (qs, ks, vs))
+    sc = 1 / math.sqrt(qf.shape[-1])
+    bounds = cu.tolist()
+    ref = torch.zeros_like(out, dtype=torch.float64)
+    for row in range(b):
+        for a, z in zip(bounds[:-1], bounds[1:]):
+            lo, hi = max(a, row * S) - row * S, min(z, (row + 1) * S) - row * S
+            if lo >= hi:
+                continue
+            ro, rl = brute_block(qf[row:row + 1, lo:hi].detach(), kf[row:row + 1, lo:hi].detach(),
+                                 vf[row:row + 1, lo:hi].detach(), causal, sc)
+            assert torch.allclose(out[row:row + 1, lo:hi].detach().double(), ro, atol=TOL32)
+            assert torch.allclose(lse[row:row + 1, :, lo:hi].detach().double(), rl, atol=TOL32)
+            # differentiable per-document reference for the gradients
+            qd, kd, vd = qf[row:row + 1, lo:hi], kf[row:row + 1, lo:hi], vf[row:row + 1, lo:hi]
+            od, _ = rm.full_attention(qd, kd, vd, causal=causal, scaling=sc)
+            ref[row:row + 1, lo:hi] = od
+    dout = rnd(*out.shape, seed=111)
+    g_ref = torch.autograd.grad((ref * dout).sum(), [*qs, *ks, *vs])
+    g_got = torch.autograd.grad((out * dout).sum(), [*qs, *ks, *vs])
+    for a, z in zip(g_got, g_ref):
+        assert torch.allclose(a, z, atol=TOL32)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_ring_per_row_documents(causal):
+    """The packed ring gives each batch row its own documents (ring/loop.py:178) and, with
+    ``causal=False``, every key of the query's document (:149,183-184)."""
+    check_varlen_rows(rm.varlen_ring_forward, causal)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_ring_dropout_coordinates(causal):
+    """One document per row: the packed ring with a dropout seed equals the gather ring
+    with that seed (the same mask over (row, head, r L + i, gathered key))."""
+    P, L, b, p, seed = 3, 8, 2, 0.3, 1234
+    cu = torch.tensor([0, P * L, 2 * P * L])
+    qs = [rnd(b, 2, L, 8, seed=121 + r) for r in range(P)]
+    ks = [rnd(b, 2, L, 8, seed=131 + r) for r in range(P)]
+    vs = [rnd(b, 2, L, 8, seed=141 + r) for r in range(P)]
+    o1, l1 = rm.varlen_ring_forward(qs, ks, vs, cu, causal=causal, dropout=p, drop_seed=seed)
+    o2, l2 = rm.allgather_ring_forward(qs, ks, vs, causal=causal, dropout=p, drop_seed=seed)
+    o0, _ = rm.varlen_ring_forward(qs, ks, vs, cu, causal=causal)
+    for r in range(P):
+        assert torch.allclose(o1[r], o2[r], atol=TOL32)
+        assert torch.allclose(l1[r], l2[r], atol=TOL32)
+        assert not torch.allclose(o1[r], o0[r], atol=1e-3)  # the mask drops something
+
+
 def _fmix32_int(x):
     """MurmurHash3's fmix32 on a Python int (an implementation independent of numpy's
     wrap-around arithmetic)."""
