@@ -636,6 +636,26 @@ def profile_workload():
     print("profile: calibration copies of 1073741824 bytes done", flush=True)
 
 
+def profile_hbm_workload():
+    """The HBM-bound kernels at their bench shapes (shard q/k/v, the standalone merge, the
+    configs[4] scan fwd/bwd, the long-L chained scans, the Mamba2 correction fwd/bwd, the CP
+    conv fwd/bwd and the shard state fwd/bwd), each launched a few times, then the 1 GiB
+    copy calibration: the run the rocprofv3 FETCH_SIZE / WRITE_SIZE passes count."""
+    for name, fn in (("shard", shard_workload), ("merge", merge_workload),
+                     ("scan", scan_workload), ("scan_long", scan_long_workload),
+                     ("mamba_fwd", mamba_workload), ("mamba_bwd", mamba_bwd_workload),
+                     ("conv", conv_workload), ("chunk_state", chunk_state_workload)):
+        fn(2, 1)
+        torch.cuda.empty_cache()
+        print(f"profile-hbm: {name} done", flush=True)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    _sync()
+    print("profile-hbm: calibration copies of 1073741824 bytes done", flush=True)
+
+
 def _traffic(kernel):
     """HBM bytes per launch of ``kernel`` measured by rocprofv3 (profiles/traffic.json), or None."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
@@ -646,6 +666,29 @@ def _traffic(kernel):
         return None
     entry = data.get("kernels", {}).get(kernel)
     return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def _attach_counters(extras):
+    """Each HBM extra gets the rocprofv3-counted bytes of its call and their ratio to the
+    algorithmic bytes (profiles/traffic.json "hbm_kernels"; a key "x.fwd" goes to
+    extras["x"] with a "_fwd" suffix)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            calls = json.load(f)["hbm_kernels"]["calls"]
+    except (OSError, ValueError, KeyError):
+        return
+    for key, c in calls.items():
+        parts = key.split(".")
+        suffix = ""
+        if parts[-1] in ("fwd", "bwd"):
+            suffix = "_" + parts.pop()
+        node = extras
+        for p in parts:
+            node = node.get(p) if isinstance(node, dict) else None
+        if isinstance(node, dict):
+            node["counter_bytes" + suffix] = c["hbm_bytes"]
+            node["counter_over_algorithmic" + suffix] = c["counter_over_algorithmic"]
 
 
 def _clocks():
@@ -667,6 +710,8 @@ def main():
     ap.add_argument("--cpu-heads", type=int, default=1)
     ap.add_argument("--profile", action="store_true",
                     help="one ring step + copy calibration, for rocprofv3 counter passes")
+    ap.add_argument("--profile-hbm", action="store_true",
+                    help="the HBM-bound kernels + copy calibration, for rocprofv3 counter passes")
     ap.add_argument("--gemm-ceiling", action="store_true",
                     help="time torch bf16 GEMMs (hipBLASLt) at 8192^3 and 16384^3 and exit")
     ap.add_argument("--per-rank", action="store_true",
@@ -683,6 +728,9 @@ def main():
 
     if args.profile:
         profile_workload()
+        return
+    if args.profile_hbm:
+        profile_hbm_workload()
         return
     if args.gemm_ceiling:
         print(json.dumps({"gemm_ceiling": gemm_ceiling()}))
@@ -723,6 +771,7 @@ def main():
         torch.cuda.empty_cache()
         extras["per_rank_configs2"] = per_rank_workload(3, 1)
         torch.cuda.empty_cache()
+    _attach_counters(extras)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_heads)
 
     value = ring["flops"] / (ring["ms"] * 1e-3) / 1e12

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 16 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 17 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
                               8: allocation-free Mamba2 correction bwd;
                               9: carried-in state h_in / dh_in of the linear scan;
@@ -39,7 +39,8 @@ extern "C" {
                               14: workspace of the Mamba2 shard-state backward;
                               15: attention head_dim up to 256;
                               16: per-batch-row document metadata (layout m_sb),
-                                  dropout with document masks */
+                                  dropout with document masks;
+                                  17: rmx_linear_scan_status */
 
 /* error codes */
 #define RMX_OK 0
@@ -282,6 +283,15 @@ size_t rmx_linear_scan_workspace(int32_t batch, int32_t L, int32_t d, int32_t gr
                                  int32_t* chunk_tokens);
 
 /*
+ * Status of the last rmx_linear_scan_fwd / _bwd call that used this workspace: synchronizes
+ * the stream, then returns RMX_EDEVICE when a chunk of the L-parallel scan gave up waiting
+ * for its predecessor's state (after about 0.3 s of polls; its carried state and the
+ * outputs after it are NaN), RMX_OK otherwise (and for a NULL workspace). No reference
+ * counterpart: the reference's sequential loop cannot stall.
+ */
+int32_t rmx_linear_scan_status(const void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Gradient of rmx_linear_scan_fwd (what autograd through the reference's loop, cumprod
  * and the all-gather's all-reduce backward computes): given dh, the forward's h and h_in
  * (nullable), writes db [batch, L, d], ADDS da [batch, L, groups] (caller zero-fills da)
@@ -348,7 +358,7 @@ int32_t rmx_mamba2_cp_correction_bwd(const uint16_t* gy, const float* ghf, const
  * shares that GPU's array and its contents (none of which needs to start at zero), so
  * calls that overlap on one GPU (from other streams or threads) race. The array's
  * device address is looked up once per device, on the first call with that device
- * current; the stream must belong to the current device.
+ * current; the stream must belong to the current device (RMX_EINVAL otherwise).
  */
 #define RMX_MAMBA2_BWD_SCRATCH_MAX ((size_t)96 << 20)
 int32_t rmx_mamba2_cp_correction_bwd_noalloc(const uint16_t* gy, const float* ghf,

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
-ABI_VERSION = 16  # RMX_ABI_VERSION of include/ringmaster_amd.h
+ABI_VERSION = 17  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
@@ -102,6 +102,7 @@ SIGNATURES = {
     "rmx_zigzag_scatter": (_i32, [_vp, _vp, _i32, _i32, _i32, _i64, _i64, _vp]),
     "rmx_linear_scan_fwd": (_i32, [_vp] * 5 + [_i32] * 5 + [_vp, ctypes.c_size_t, _vp]),
     "rmx_linear_scan_workspace": (ctypes.c_size_t, [_i32] * 4 + [ctypes.POINTER(_i32)]),
+    "rmx_linear_scan_status": (_i32, [_vp, ctypes.c_size_t, _vp]),
     "rmx_linear_scan_bwd": (_i32, [_vp] * 7 + [_i32] * 5 + [_vp, ctypes.c_size_t, _vp]),
     "rmx_mamba2_cp_correction": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
                                         _i32, _i32, _i32, _vp]),

@@ -310,6 +310,18 @@ size_t rmx_linear_scan_workspace(int32_t batch, int32_t L, int32_t d, int32_t gr
   return p.bytes;
 }
 
+int32_t rmx_linear_scan_status(const void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace) return RMX_OK;
+  if (workspace_bytes < 256) return fail(RMX_EINVAL, "workspace of %zu bytes is too small", workspace_bytes);
+  hipError_t e;
+  const int flag = rmx::read_linear_scan_failure(workspace, (hipStream_t)stream, &e);
+  if (e != hipSuccess) return dev_status(e, "linear scan status");
+  if (flag)
+    return fail(RMX_EDEVICE, "the L-parallel linear scan's look-back gave up waiting for a chunk "
+                             "(its outputs hold NaN)");
+  return RMX_OK;
+}
+
 int32_t rmx_linear_scan_fwd(const float* a, const float* b, const float* h_in, float* h,
                             float* chunk_state, int32_t batch, int32_t L, int32_t d, int32_t groups,
                             int32_t world, void* workspace, size_t workspace_bytes, void* stream) {
@@ -478,6 +490,19 @@ int32_t rmx_mamba2_cp_correction_bwd_noalloc(const uint16_t* gy, const float* gh
                 "the shape needs a %zu-byte workspace, above the %zu bytes of the allocation-free "
                 "entry point's scratch array (use rmx_mamba2_cp_correction_bwd with a workspace)",
                 need, (size_t)RMX_MAMBA2_BWD_SCRATCH_MAX);
+  // the scratch array is per device: the stream must run on the current one
+  int cur = 0;
+  if ((rc = dev_status(hipGetDevice(&cur), "hipGetDevice"))) return rc;
+  if (stream) {
+    hipDevice_t sd = 0;
+    if ((rc = dev_status(hipStreamGetDevice((hipStream_t)stream, &sd), "hipStreamGetDevice")))
+      return rc;
+    if ((int)sd != cur)
+      return fail(RMX_EINVAL,
+                  "the stream belongs to device %d but the current device is %d (the "
+                  "allocation-free entry point uses the current device's scratch array)",
+                  (int)sd, cur);
+  }
   void* ws = nullptr;
   rc = dev_status(rmx::mamba2_bwd_scratch(&ws), "scratch array lookup (hipGetSymbolAddress)");
   if (rc) return rc;

@@ -39,6 +39,8 @@ hipError_t launch_linear_scan_fwd_chunked(const ScanChunkPlan& p, const float* a
                                           const float* hin, float* h, float* cs, void* ws,
                                           int batch, int L, int d, int groups, int world,
                                           hipStream_t stream);
+// the failure word of an L-parallel scan's workspace (after a stream synchronize)
+int read_linear_scan_failure(const void* ws, hipStream_t stream, hipError_t* err);
 hipError_t launch_linear_scan_bwd_chunked(const ScanChunkPlan& p, const float* a, const float* h,
                                           const float* hin, const float* dh, float* da, float* db,
                                           float* dhin, void* ws, int batch, int L, int d,

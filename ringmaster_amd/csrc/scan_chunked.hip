@@ -25,8 +25,9 @@
 // state per channel.
 //
 // The look-back wait is bounded: a chunk whose predecessor has published nothing
-// after kSpinCap polls takes NaN as its carried-in state, so the outputs show the
-// failure and every workgroup still ends.
+// after kSpinCap polls takes NaN as its carried-in state and sets the workspace's
+// failure word (next to the ticket counter), so the outputs show the failure, the
+// host can read it back (rmx_linear_scan_status), and every workgroup still ends.
 //
 // A single pass costs about 200 ns of latency per chunk of a chain, which dominates when
 // few channels run over a long sequence (L = 65536, d = 256: 1024 chunks, 0.26 ms for
@@ -60,7 +61,7 @@ constexpr int kSpinCap = 1 << 22;  // look-back polls before giving up (about 0.
 // write back the whole L2 of the XCD, full of the streaming outputs) and polling no
 // cache invalidation. The workspace is zeroed before every call.
 struct ChunkWork {
-  int* counter;     // chunk tickets in dispatch order
+  int* counter;     // chunk tickets in dispatch order; counter[1]: the failure word
   uint64_t* words;  // [chains * nchunks][3][CT]: A, B of the chunk's pair, state after it
   int ntiles, nchunks;
 };
@@ -105,6 +106,8 @@ __global__ __launch_bounds__(256) void linear_scan_chunked_kernel(
     if (threadIdx.x == 0) s_ticket = atomicAdd(w.counter, 1);
     __syncthreads();
   }
+  // reduce-then-rescan never polls: clear a failure word an earlier call may have left
+  if (PASS == 1 && blockIdx.x == 0 && threadIdx.x == 0) w.counter[1] = 0;
   // no chunk waits for another in passes 1 and 2: the dispatch order needs no ticket
   const int ticket = PASS == 0 ? s_ticket : (int)blockIdx.x;
   const int nchains = batch * w.ntiles;
@@ -312,6 +315,7 @@ __global__ __launch_bounds__(256) void linear_scan_chunked_kernel(
       if (!ok) {
 #pragma unroll
         for (int v = 0; v < V; ++v) X[v] = __builtin_nanf("");
+        if (tgw == 0) atomicOr(w.counter + 1, 1);
       }
     }
     if (tgw == 0) {
@@ -520,7 +524,7 @@ ScanChunkPlan scan_chunk_plan(int batch, int L, int d, int groups) {
   // channels over long sequences.
   const int64_t elems = (int64_t)batch * L * d;
   p.two_pass = (int64_t)p.nchunks * 233600 > elems + (int64_t)20000 * 1168;
-  p.words_off = 256;  // the ticket counter, then the words
+  p.words_off = 256;  // the ticket counter and the failure word, then the words
   p.bytes = p.words_off + (size_t)slots * 3 * p.CT * 8;
   return p;
 }
@@ -588,6 +592,14 @@ hipError_t launch_linear_scan_fwd_chunked(const ScanChunkPlan& p, const float* a
                      0, stream, w.words, cs, batch, d, p.ntiles, p.nchunks, p.CT, world,
                      (L / world) / p.TC);
   return hipGetLastError();
+}
+
+int read_linear_scan_failure(const void* ws, hipStream_t stream, hipError_t* err) {
+  int flag = 0;
+  *err = hipMemcpyAsync(&flag, reinterpret_cast<const int*>(ws) + 1, sizeof(int),
+                        hipMemcpyDeviceToHost, stream);
+  if (*err == hipSuccess) *err = hipStreamSynchronize(stream);
+  return flag;
 }
 
 hipError_t launch_linear_scan_bwd_chunked(const ScanChunkPlan& p, const float* a, const float* h,

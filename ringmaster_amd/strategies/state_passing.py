@@ -14,6 +14,7 @@ Mamba2 head decay broadcast over headdim x d_state); ``b`` is ``[batch, L, d]``.
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -73,6 +74,13 @@ def _workspace(algo, batch, L, d, groups, world, chunk_state, device):
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
+def _debug_status(ws, like):
+    """With ``RINGMASTER_AMD_DEBUG=1``, wait for an L-parallel scan and raise RuntimeError if
+    one of its chunks gave up waiting for its predecessor (its outputs then hold NaN)."""
+    if ws is not None and os.environ.get("RINGMASTER_AMD_DEBUG") == "1":
+        abi.check(abi.lib().rmx_linear_scan_status(ws.data_ptr(), ws.numel(), abi.stream_of(like)))
+
+
 def linear_scan_forward(a, b, world: int = 1, return_chunk_state: bool = False, h_in=None,
                         algo: str = "auto"):
     """h for the whole ``[batch, L, d]`` input split into ``world`` shards, from ``h_in``
@@ -91,6 +99,7 @@ def linear_scan_forward(a, b, world: int = 1, return_chunk_state: bool = False, 
                                             h.data_ptr(), abi.ptr(cs), batch, L, d, groups,
                                             world, abi.ptr(ws), 0 if ws is None else ws.numel(),
                                             abi.stream_of(b)))
+    _debug_status(ws, b)
     return (h, cs) if return_chunk_state else h
 
 
@@ -112,6 +121,7 @@ def linear_scan_backward(a, h, dh, world: int = 1, h_in=None, algo: str = "auto"
                                             abi.ptr(dh_in), batch, L, d, groups, world,
                                             abi.ptr(ws), 0 if ws is None else ws.numel(),
                                             abi.stream_of(h)))
+    _debug_status(ws, h)
     return (da, db) if h_in is None else (da, db, dh_in)
 
 

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 16
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 17
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -334,3 +334,12 @@ def test_zigzag_ring_attention_group_keyword():
         zigzag_ring_attention(q, q, q, group=object())
     with pytest.raises(RuntimeError, match="ROCm device"):
         zigzag_ring_attention(q, q, q, group=None)
+
+
+def test_linear_scan_status_host_checks():
+    """No workspace: nothing to report; a workspace smaller than its header is refused
+    before any device access."""
+    lib = abi.lib()
+    assert lib.rmx_linear_scan_status(None, 0, None) == abi.RMX_OK
+    assert lib.rmx_linear_scan_status(16, 8, None) == abi.RMX_EINVAL
+    assert b"too small" in lib.rmx_last_error()

@@ -190,3 +190,38 @@ def test_chunked_scan_repeated_calls_reuse_workspace():
     h2 = linear_scan_forward(ad, bd, algo="chunked")
     torch.cuda.synchronize()
     assert torch.equal(h1, h2)
+
+
+def test_chunked_scan_status_word(monkeypatch):
+    """rmx_linear_scan_status: OK after a normal single-pass call; a failure word (what a
+    chunk that gives up waiting sets, forced here from the host) comes back as RMX_EDEVICE,
+    and under RINGMASTER_AMD_DEBUG=1 the wrapper raises RuntimeError; the next call clears
+    it again."""
+    import ctypes
+
+    from ringmaster_amd import abi
+    from ringmaster_amd.strategies import state_passing as stp
+
+    a, b, _, _ = _inputs(1, 5000, 64, 4, seed=47)
+    ad, bd = a.cuda(), b.cuda()
+    batch, L, d = bd.shape
+    tc = ctypes.c_int32(0)
+    nbytes = abi.lib().rmx_linear_scan_workspace(batch, L, d, 4, ctypes.byref(tc))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    h = torch.empty_like(bd)
+    args = (ad.data_ptr(), bd.data_ptr(), None, h.data_ptr(), None, batch, L, d, 4, 1,
+            ws.data_ptr(), nbytes, abi.stream_of(bd))
+    assert abi.lib().rmx_linear_scan_fwd(*args) == abi.RMX_OK
+    lib = abi.lib()
+    assert lib.rmx_linear_scan_status(ws.data_ptr(), nbytes, abi.stream_of(bd)) == abi.RMX_OK
+    ws.view(torch.int32)[1] = 1
+    assert lib.rmx_linear_scan_status(ws.data_ptr(), nbytes, abi.stream_of(bd)) == abi.RMX_EDEVICE
+    assert b"gave up" in lib.rmx_last_error()
+    with pytest.raises(RuntimeError, match="gave up"):
+        monkeypatch.setenv("RINGMASTER_AMD_DEBUG", "1")
+        stp._debug_status(ws, bd)
+    assert lib.rmx_linear_scan_fwd(*args) == abi.RMX_OK  # cleared at the start of the call
+    assert lib.rmx_linear_scan_status(ws.data_ptr(), nbytes, abi.stream_of(bd)) == abi.RMX_OK
+    h2 = stp.linear_scan_forward(ad, bd, algo="chunked")  # debug mode: checked, no error
+    torch.cuda.synchronize()
+    assert torch.equal(h, h2)
