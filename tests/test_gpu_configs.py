@@ -283,3 +283,54 @@ def test_configs3_full_size_rows():
             ref_o[i] = torch.einsum("hk,khd->hd", torch.softmax(sc_, dim=1), vc[s0:p + 1])
         assert_bf16_close(out[r][0][local.cuda()][:, heads], ref_o, f"out rows rank {r}")
         assert_f32_rel(lse[r][0][heads][:, local.cuda()], ref_l, f"lse rows rank {r}")
+
+
+def test_configs3_full_size_group():
+    """configs[3] at full size (P=4, S=65536, Hq=32, Hkv=8, the 25 seed-5 lognormal
+    documents), forward and reverse-ring backward: every row of KV group 5 (q heads 20-23)
+    against per-document causal attention in fp32 on the GPU (ring/zigzag.py:86-120,170-209,
+    ring/varlen_blocks.py:176-200): out and dq of the four heads, and the GQA-folded dk, dv."""
+    from ringmaster_amd.ring.zigzag import doc_ids_from_cu, ring_backward, ring_forward
+
+    P, S, Hq, Hkv, D = 4, 65536, 32, 8, 128
+    L, half, G = S // P, S // (2 * P), Hq // Hkv
+    scale = 1.0 / math.sqrt(D)
+    cu = _lognormal_docs(S, median=2048, lo=128, hi=16384)
+    print(f"case configs[3] full size fwd+bwd: {cu.numel() - 1} documents", flush=True)
+    qg, kg, vg = _gen((1, S, Hq, D), 1), _gen((1, S, Hkv, D), 2), _gen((1, S, Hkv, D), 3)
+    dog = _gen((1, S, Hq, D), 4)
+    idx = _zigzag_rows(P, half)
+    rows_dev = torch.stack(idx).cuda()
+    shard = lambda t: t[0][rows_dev].unsqueeze(1).transpose(2, 3).contiguous()  # noqa: E731
+    q, k, v = shard(qg), shard(kg), shard(vg)
+    dout = dog[0][rows_dev].unsqueeze(1).contiguous()                       # [P, 1, L, Hq, D]
+    doc = doc_ids_from_cu(cu.cuda(), "cuda", S)
+    out, lse, out32 = ring_forward(q, k, v, scale, doc)
+    dq, dk, dv = ring_backward(dout, q, k, v, out32, lse, scale, doc)
+    torch.cuda.synchronize()
+    del q, k, v, dout
+
+    flat = rows_dev.reshape(-1)
+
+    def unshard(t, h):
+        full = torch.empty(S, D, device="cuda")
+        full[flat] = t[:, 0, :, h].reshape(-1, D).float()
+        return full
+
+    g = 5
+    K, V = kg[0, :, g].float(), vg[0, :, g].float()
+    rdK, rdV = torch.zeros(S, D, device="cuda"), torch.zeros(S, D, device="cuda")
+    bounds = cu.tolist()
+    for h in range(G * g, G * g + G):
+        Q, dO = qg[0, :, h].float(), dog[0, :, h].float()
+        ro, rdq = torch.empty(S, D, device="cuda"), torch.empty(S, D, device="cuda")
+        for a, b in zip(bounds[:-1], bounds[1:]):
+            o, _, dqd, dkd, dvd = _reference_head(Q[a:b], K[a:b], V[a:b], dO[a:b], scale,
+                                                  causal=True)
+            ro[a:b], rdq[a:b] = o, dqd
+            rdK[a:b] += dkd
+            rdV[a:b] += dvd
+        assert_bf16_close(unshard(out32, h), ro, f"out head {h}")
+        assert_bf16_close(unshard(dq, h), rdq, f"dq head {h}")
+    assert_bf16_close(unshard(dk, g), rdK, f"dk kv head {g}")
+    assert_bf16_close(unshard(dv, g), rdV, f"dv kv head {g}")
