@@ -54,6 +54,22 @@ def _time(fn, steps, warmup):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
+def _time_gpu(fn, steps, warmup):
+    """Mean ms per call from HIP events recorded on the current stream around ``steps``
+    back-to-back calls (the GPU's time, launch gaps included, not the host's)."""
+    for _ in range(warmup):
+        fn()
+    _sync()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    _sync()
+    return e0.elapsed_time(e1) / steps
+
+
 class ClockSampler:
     """Samples the GPU's current shader clock (``rocm-smi --showclocks``, read from sysfs, no
     GPU work) from a background thread while a timed region runs: the clock under load, which
@@ -317,7 +333,7 @@ def shard_workload(steps, warmup):
     P, S, H, D = 8, 131072, 16, 128
     xs = [_gen((1, S, H, D), i) for i in (1, 2, 3)]
     nbytes = 3 * 2 * xs[0].numel() * 2
-    ms = _time(lambda: [zigzag_shard(x, P) for x in xs], steps, warmup)
+    ms = _time_gpu(lambda: [zigzag_shard(x, P) for x in xs], steps, warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
     del xs
     return {"ms": round(ms, 4), "bytes": nbytes, "GB/s": round(gbs, 1),
@@ -333,7 +349,7 @@ def merge_workload(steps, warmup):
     blk = _gen((1, S, H, D), 8)
     blk_lse = _gen((1, H, S), 9, torch.float32)
     nbytes = 677_380_096
-    ms = _time(lambda: update_out_and_lse(out, lse, blk, blk_lse), steps, warmup)
+    ms = _time_gpu(lambda: update_out_and_lse(out, lse, blk, blk_lse), steps, warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"ms": round(ms, 4), "bytes": nbytes, "GB/s": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
@@ -350,8 +366,8 @@ def scan_workload(steps, warmup):
     b = torch.randn(1, L, d, generator=g, device="cuda")  # chunk states
     dh = torch.randn(1, L, d, generator=g, device="cuda")
     h = linear_scan_forward(a, b, P)
-    fwd_ms = _time(lambda: linear_scan_forward(a, b, P), steps, warmup)
-    bwd_ms = _time(lambda: linear_scan_backward(a, h, dh, P), steps, warmup)
+    fwd_ms = _time_gpu(lambda: linear_scan_forward(a, b, P), steps, warmup)
+    bwd_ms = _time_gpu(lambda: linear_scan_backward(a, h, dh, P), steps, warmup)
     fb, bb = 1_073_807_360, 1_610_612_736
     tot = fb + bb
     gbs = tot / ((fwd_ms + bwd_ms) * 1e-3) / 1e9
@@ -375,8 +391,8 @@ def scan_long_workload(steps, warmup):
         b = torch.randn(B, L, d, generator=g, device="cuda")
         dh = torch.randn(B, L, d, generator=g, device="cuda")
         h = linear_scan_forward(a, b, algo="chunked")
-        fwd_ms = _time(lambda: linear_scan_forward(a, b, algo="chunked"), steps, warmup)
-        bwd_ms = _time(lambda: linear_scan_backward(a, h, dh, algo="chunked"), steps, warmup)
+        fwd_ms = _time_gpu(lambda: linear_scan_forward(a, b, algo="chunked"), steps, warmup)
+        bwd_ms = _time_gpu(lambda: linear_scan_backward(a, h, dh, algo="chunked"), steps, warmup)
         n = B * L * d * 4
         fb, bb = 2 * n + a.numel() * 4, 3 * n + 2 * a.numel() * 4
         res[f"B{B}_L{L}_d{d}_G{G}"] = {
@@ -403,7 +419,7 @@ def mamba_workload(steps, warmup):
     cum_A = torch.cumsum(A * dt, dim=1)
     h_prev = _gen((P, H, D, N), 12, torch.float32)
     h_final = _gen((P, H, D, N), 13, torch.float32)
-    ms = _time(lambda: mamba2_cp_correction(out, h_final, C, cum_A, h_prev, H, D), steps, warmup)
+    ms = _time_gpu(lambda: mamba2_cp_correction(out, h_final, C, cum_A, h_prev, H, D), steps, warmup)
     # read out + write y (bf16), read C, cum_A, h_prev, read + write h_final
     nbytes = 2 * out.numel() * 2 + C.numel() * 2 + cum_A.numel() * 4 + 3 * h_prev.numel() * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -445,8 +461,8 @@ def chunk_state_workload(steps, warmup):
             g_x.data_ptr(), g_B.data_ptr(), g_e.data_ptr(), g_cum.data_ptr(), P, T, H, D, G, N,
             abi.ptr(ws), ws_bytes, st))
 
-    fwd_ms = _time(fwd, steps, warmup)
-    bwd_ms = _time(bwd, steps, warmup)
+    fwd_ms = _time_gpu(fwd, steps, warmup)
+    bwd_ms = _time_gpu(bwd, steps, warmup)
     small = e.numel() * 4
     fwd_bytes = x.numel() * 2 + B.numel() * 2 + 2 * small + state.numel() * 4
     bwd_bytes = 2 * x.numel() * 2 + 2 * B.numel() * 2 + 4 * small + gst.numel() * 4
@@ -472,9 +488,9 @@ def conv_workload(steps, warmup):
     w = _gen((C, W), 15, scale=0.5).requires_grad_(True)
     b = _gen((C,), 16).requires_grad_(True)
     dy = _gen((P, 1, C, T), 17)
-    fwd_ms = _time(lambda: causal_conv1d_cp(x, w, b, "silu"), steps, warmup)
+    fwd_ms = _time_gpu(lambda: causal_conv1d_cp(x, w, b, "silu"), steps, warmup)
     y = causal_conv1d_cp(x, w, b, "silu")
-    tot_ms = _time(lambda: torch.autograd.grad(causal_conv1d_cp(x, w, b, "silu"), (x, w, b), dy),
+    tot_ms = _time_gpu(lambda: torch.autograd.grad(causal_conv1d_cp(x, w, b, "silu"), (x, w, b), dy),
                    steps, warmup)
     bwd_ms = tot_ms - fwd_ms
     n = x.numel() * 2
@@ -516,7 +532,7 @@ def mamba_bwd_workload(steps, warmup):
             None, gC.data_ptr(), gA.data_ptr(), gH.data_ptr(), ws.data_ptr(), ws_bytes,
             P, T, H, D, 1, N, stream))
 
-    ms = _time(run, steps, warmup)
+    ms = _time_gpu(run, steps, warmup)
     nbytes = gy.numel() * 2 + 2 * C.numel() * 2 + 2 * cum_A.numel() * 4 + 3 * h_prev.numel() * 4
     flops = 7 * 2 * P * T * H * D * N
     return {"ms": round(ms, 4), "bytes": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
