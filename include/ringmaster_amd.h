@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RMX_ABI_VERSION 17 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
+#define RMX_ABI_VERSION 18 /* 3: Mamba2 correction bwd; 4: nlse; 5: CP conv1d; 6: dt cumsum;
                               7: effective dt in/out of the dt cumsum, shard final state;
                               8: allocation-free Mamba2 correction bwd;
                               9: carried-in state h_in / dh_in of the linear scan;
@@ -40,7 +40,8 @@ extern "C" {
                               15: attention head_dim up to 256;
                               16: per-batch-row document metadata (layout m_sb),
                                   dropout with document masks;
-                                  17: rmx_linear_scan_status */
+                              17: rmx_linear_scan_status;
+                              18: right-bounded windows (problem window_right) */
 
 /* error codes */
 #define RMX_OK 0
@@ -54,7 +55,8 @@ extern "C" {
 
 /* block mask kinds (ring/kernels.py:64-67, ring/varlen_blocks.py:51-58) */
 #define RMX_MASK_FULL 0   /* every (q, k) pair attends */
-#define RMX_MASK_CAUSAL 1 /* bottom-right aligned causal: k <= q + (sk - sq) */
+#define RMX_MASK_CAUSAL 1 /* bottom-right aligned causal: k <= q + (sk - sq) + window_right
+                             (window_right = 0: causal attention) */
 #define RMX_MASK_DOC 2    /* q_doc[q] == k_doc[k] && k_gidx[k] <= q_gidx[q]; the four arrays
                              advance by the layout's m_sb per batch row */
 /* RMX_DROPOUT: with dropout_p > 0, element (b, h, q, k) of a problem (h the q head) is kept when
@@ -70,7 +72,10 @@ extern "C" {
  * q_gidx / k_gidx under RMX_MASK_DOC (ring/loop.py:185-186). It applies on top of the
  * mask kind; window_left may be any int32 (a negative bound also masks the diagonal,
  * which is how one block of a windowed ring sees the window of the global sequence).
- * Rows left with no key get lse = -inf and out = 0, as with document masks. */
+ * Rows left with no key get lse = -inf and out = 0, as with document masks.
+ * A window bounded on the right as well (flash attention's window_size = (left, right),
+ * right >= 0, on a non-causal block: pos_k - pos_q > right masked) runs as RMX_MASK_CAUSAL
+ * with window_right = right; window_right must be 0 under the other mask kinds. */
 
 /* forward epilogue modes (online-softmax merge, ring/merge.py:20-31) */
 #define RMX_FWD_WRITE 0       /* out/lse := this block's (out, lse); acc_out (nullable)
@@ -140,6 +145,8 @@ typedef struct rmx_fwd_problem {
   int32_t has_window;    /* 0: no window; 1: window_left bounds pos_q - pos_k (see above) */
   int32_t window_left;
   int32_t drop_q0, drop_k0; /* dropout coordinates of the first query / key (RMX_DROPOUT) */
+  int32_t window_right;  /* RMX_MASK_CAUSAL: pos_k - pos_q <= window_right, 0 <= window_right
+                            <= 2^28 (0: causal); 0 under the other mask kinds */
 } rmx_fwd_problem;
 
 /* One block-attention backward problem, using the GLOBAL (merged) out/lse. */
@@ -168,6 +175,7 @@ typedef struct rmx_bwd_problem {
   int32_t has_window;    /* as in rmx_fwd_problem: the forward's window of the same block */
   int32_t window_left;
   int32_t drop_q0, drop_k0; /* as in rmx_fwd_problem: the forward's dropout coordinates */
+  int32_t window_right;  /* as in rmx_fwd_problem: the forward's right bound */
 } rmx_bwd_problem;
 
 int32_t rmx_abi_version(void);

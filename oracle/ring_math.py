@@ -1,6 +1,7 @@
 """CPU restatement of the reference ring-attention math (test infrastructure only).
 
-Follows ring/kernels.py:52-78 (math_block, with its sliding window), ring/loop.py:175-228
+Follows ring/kernels.py:52-78 (math_block, with its sliding window; ``flash=True``: the
+flash provider's window, ring/kernels.py:37-38), ring/loop.py:175-228
 (the gather ring and the packed gather ring), ring/merge.py:13-31 (merge),
 ring/zigzag.py:40-67,86-120,151-254 (zigzag schedule, forward and reverse-ring
 backward), ring/p2p_attn.py:243-281 (explicit global-lse block backward) and
@@ -74,11 +75,31 @@ def dropout_scale_mask(seed, b, hq, sq, sk, p, q0=0, k0=0):
 
 
 # ---------------------------------------------------------------- blocks
+def flash_window(window, causal, sk):
+    """The (left, right) bounds that flash attention 2 applies for ``window_size`` (the
+    flash provider hands the window to ``flash_attn_func``, ring/kernels.py:37-38; the
+    library is not installed here, so its published argument rules are restated): a bound
+    of at least sk keys counts as -1; causal sets right to 0; then a -1 bound facing a
+    non-negative one becomes sk. Returns (left, right), None for a side left unbounded."""
+    lo, hi = (int(x) for x in window)
+    lo = -1 if lo >= sk else lo
+    hi = -1 if hi >= sk else hi
+    if causal:
+        hi = 0
+    if lo < 0 <= hi:
+        lo = sk
+    if hi < 0 <= lo:
+        hi = sk
+    return (lo if lo >= 0 else None), (hi if hi >= 0 else None)
+
+
 def math_block(q, k, v, *, causal, scaling, dropout=0.0, window=None, drop_seed=None,
-               drop_q0=0, drop_k0=0):
+               drop_q0=0, drop_k0=0, flash=False):
     """Explicit-softmax block (ring/kernels.py:52-78). q/k/v [b, s, h, d] -> (out, lse).
     With ``dropout`` and ``drop_seed`` the probabilities are dropped by the hash mask of
-    that seed (coordinates offset by drop_q0 / drop_k0) instead of torch's RNG."""
+    that seed (coordinates offset by drop_q0 / drop_k0) instead of torch's RNG. ``flash``:
+    the window is the flash provider's (``flash_window``: pos_q - pos_k > left and
+    pos_k - pos_q > right masked) instead of math_block's left bound."""
     qt, kt, vt = (t.transpose(1, 2).float() for t in (q, k, v))
     if qt.shape[1] != kt.shape[1]:
         if qt.shape[1] % kt.shape[1]:
@@ -92,10 +113,16 @@ def math_block(q, k, v, *, causal, scaling, dropout=0.0, window=None, drop_seed=
         keep = torch.ones(sq, sk, dtype=torch.bool).tril(sk - sq)
         scores = scores.masked_fill(~keep, NEG_INF)
     if window is not None:
-        left = window[0]
         iq = torch.arange(sq).unsqueeze(1) + (sk - sq)
         ik = torch.arange(sk).unsqueeze(0)
-        scores = scores.masked_fill(iq - ik > left, NEG_INF)
+        if flash:
+            left, right = flash_window(window, causal, sk)
+            if left is not None:
+                scores = scores.masked_fill(iq - ik > left, NEG_INF)
+            if right is not None:
+                scores = scores.masked_fill(ik - iq > right, NEG_INF)
+        else:
+            scores = scores.masked_fill(iq - ik > window[0], NEG_INF)
     lse = torch.logsumexp(scores, dim=-1)
     probs = torch.exp(scores - lse.unsqueeze(-1))
     if dropout and drop_seed is not None:
@@ -466,12 +493,13 @@ def distflash_backward(d_outs, qs, ks, vs, outs, lses, *, scaling=None, cu_seqle
 
 
 def allgather_ring_forward(qs, ks, vs, *, causal=True, scaling=None, window=None, dropout=0.0,
-                           drop_seed=None):
+                           drop_seed=None, flash=False):
     """The gather ring (ring/loop.py:201-228): rank r attends the gathered K/V of ranks
     0..r (causal) or of every rank with ONE math_block call, whose bottom-right
     alignment places rank r's query i at position ``(end - 1) L + i`` against the
     gathered keys (``end`` = r + 1 causal, P otherwise); a window bounds that position
-    minus the key's global index. With dropout and ``drop_seed``: the hash mask over
+    minus the key's global index (``flash``: the flash provider's window, bounded on both
+    sides). With dropout and ``drop_seed``: the hash mask over
     (global query r L + i, gathered key). qs/ks/vs per-rank [b, H, L, d] -> per-rank out
     [b, L, H, d] and lse [b, H, L]. Differentiable (torch autograd)."""
     world = len(qs)
@@ -483,7 +511,7 @@ def allgather_ring_forward(qs, ks, vs, *, causal=True, scaling=None, window=None
         v = torch.cat([t.transpose(1, 2) for t in vs[:end]], dim=1)
         L = q.shape[1]
         o, lse = math_block(q, k, v, causal=causal, scaling=scaling, window=window,
-                            dropout=dropout, drop_seed=drop_seed, drop_q0=r * L)
+                            dropout=dropout, drop_seed=drop_seed, drop_q0=r * L, flash=flash)
         outs.append(o)
         lses.append(lse)
     return outs, lses

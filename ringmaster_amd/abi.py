@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libringmaster_amd.so"
-ABI_VERSION = 17  # RMX_ABI_VERSION of include/ringmaster_amd.h
+ABI_VERSION = 18  # RMX_ABI_VERSION of include/ringmaster_amd.h
 
 RMX_OK = 0
 RMX_EINVAL = -1
@@ -73,7 +73,7 @@ class FwdProblem(ctypes.Structure):
         ("acc_out", _vp), ("acc_lse", _vp),
         ("q_gidx", _vp), ("k_gidx", _vp), ("q_doc", _vp), ("k_doc", _vp),
         ("sq", _i32), ("sk", _i32), ("mode", _i32), ("has_window", _i32), ("window_left", _i32),
-        ("drop_q0", _i32), ("drop_k0", _i32),
+        ("drop_q0", _i32), ("drop_k0", _i32), ("window_right", _i32),
     ]
 
 
@@ -84,6 +84,7 @@ class BwdProblem(ctypes.Structure):
         ("q_gidx", _vp), ("k_gidx", _vp), ("q_doc", _vp), ("k_doc", _vp),
         ("sq", _i32), ("sk", _i32), ("dq_mode", _i32), ("dkv_mode", _i32),
         ("has_window", _i32), ("window_left", _i32), ("drop_q0", _i32), ("drop_k0", _i32),
+        ("window_right", _i32),
     ]
 
 

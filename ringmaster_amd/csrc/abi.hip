@@ -83,9 +83,14 @@ int check_span(int64_t rows, int64_t stride_elems, const char* name) {
   return RMX_OK;
 }
 
-int check_window(int has_window, int i) {
+int check_window(const rmx_attn_layout* L, int has_window, int window_right, int i) {
   if (has_window != 0 && has_window != 1)
     return fail(RMX_EINVAL, "problem %d: has_window must be 0 or 1 (got %d)", i, has_window);
+  if (window_right < 0 || window_right > (1 << 28))
+    return fail(RMX_EINVAL, "problem %d: window_right must lie in [0, 2^28] (got %d)", i,
+                window_right);
+  if (window_right != 0 && L->mask != RMX_MASK_CAUSAL)
+    return fail(RMX_EINVAL, "problem %d: window_right needs RMX_MASK_CAUSAL", i);
   return RMX_OK;
 }
 
@@ -116,7 +121,7 @@ int32_t rmx_attn_fwd(const rmx_attn_layout* layout, const rmx_fwd_problem* probl
   for (int i = 0; i < nproblems; ++i) {
     const rmx_fwd_problem& p = problems[i];
     if (p.sq < 0 || p.sk < 0) return fail(RMX_EINVAL, "problem %d: negative length", i);
-    if ((rc = check_window(p.has_window, i))) return rc;
+    if ((rc = check_window(layout, p.has_window, p.window_right, i))) return rc;
     if (p.sq == 0) continue;
     if ((rc = check_bf16(p.q, "q"))) return rc;
     if ((rc = check_span(p.sq, layout->q_ss, "q"))) return rc;
@@ -179,7 +184,7 @@ int32_t rmx_attn_bwd(const rmx_attn_layout* layout, const rmx_bwd_problem* probl
   for (int i = 0; i < nproblems; ++i) {
     const rmx_bwd_problem& p = problems[i];
     if (p.sq < 0 || p.sk < 0) return fail(RMX_EINVAL, "problem %d: negative length", i);
-    if ((rc = check_window(p.has_window, i))) return rc;
+    if ((rc = check_window(layout, p.has_window, p.window_right, i))) return rc;
     if (p.sq == 0 || p.sk == 0) continue;
     if ((rc = check_bf16(p.q, "q"))) return rc;
     if ((rc = check_bf16(p.k, "k"))) return rc;

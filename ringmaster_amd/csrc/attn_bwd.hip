@@ -237,8 +237,8 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
     qd = qdoc[q];
   }
   const int D = L.head_dim;        // columns past D (up to HD) load as zeros
-  const int wl = window_bound(P);  // pos_q - pos_k <= wl
-  const int off = sk - sq;
+  const int wl = window_bound(P) + diag_shift<MASK>(P);  // window: q + off - key <= wl
+  const int off = sk - sq + diag_shift<MASK>(P);  // the diagonal: key == q + off
   // this lane's lowest key: key >= q + off - wl (document masks: global index >= qlo)
   const int qlo = mask == RMX_MASK_DOC ? (qvalid ? clamp_i32((int64_t)qg - wl) : 2147483647)
                                        : q + off - wl;
@@ -625,8 +625,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
 
   // ---- query-tile range of the workgroup
   const int D = L.head_dim;        // columns past D (up to HD) load as zeros
-  const int wl = window_bound(P);  // pos_q - pos_k <= wl
-  const int off = sk - sq;
+  const int wl = window_bound(P) + diag_shift<MASK>(P);  // window: q + off - key <= wl
+  const int off = sk - sq + diag_shift<MASK>(P);  // the diagonal: key == q + off
   const int klast = (k0 + C::BKV < sk ? k0 + C::BKV : sk) - 1;
   const int nqt = (sq + BQ - 1) / BQ;
   int qt_begin = 0, qt_end = nqt;
@@ -1236,8 +1236,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
 
   // ---- query-tile range of the workgroup (as in the kernel above)
   const int D = L.head_dim;        // columns past D (up to HD) load as zeros
-  const int wl = window_bound(P);  // pos_q - pos_k <= wl
-  const int off = sk - sq;
+  const int wl = window_bound(P) + diag_shift<MASK>(P);  // window: q + off - key <= wl
+  const int off = sk - sq + diag_shift<MASK>(P);  // the diagonal: key == q + off
   const int klast = (k0 + BKV < sk ? k0 + BKV : sk) - 1;
   const int nqt = (sq + BQ - 1) / BQ;
   int qt_begin = 0, qt_end = nqt;

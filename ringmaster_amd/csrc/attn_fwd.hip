@@ -115,9 +115,9 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
     qd = qdoc[q];
   }
   const int D = L.head_dim;          // columns past D (up to HD) load as zeros
-  const int wl = window_bound(P);    // pos_q - pos_k <= wl
+  const int wl = window_bound(P) + diag_shift<MASK>(P);  // window: q + off - key <= wl
   // this lane's lowest key: key >= q + off - wl (document masks: global index >= qlo)
-  const int off = sk - sq;
+  const int off = sk - sq + diag_shift<MASK>(P);  // the diagonal: key == q + off
   const int qlo = mask == RMX_MASK_DOC ? (q < sq ? clamp_i32((int64_t)qg - wl) : 2147483647)
                                        : q + off - wl;
   // dropout: this lane's query term of the mask hash, and the key offset of the problem

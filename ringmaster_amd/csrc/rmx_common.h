@@ -19,6 +19,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/ringmaster_amd.h"
+
 namespace rmx {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -122,6 +124,15 @@ __device__ __forceinline__ int window_bound(const Prob& P) {
   if (!P.has_window) return kWinMax;
   const int w = P.window_left;
   return w > kWinMax ? kWinMax : (w < -kWinMax ? -kWinMax : w);
+}
+// A right-bounded window (RMX_MASK_CAUSAL with window_right = R: pos_k - pos_q <= R) is
+// the causal mask with its diagonal moved R keys to the right. The kernels take positions
+// relative to that diagonal: off = sk - sq + R and the left bound wl + R, so every causal
+// and window test (key <= q + off, q + off - key <= wl) reads as for R = 0. The host keeps
+// R in [0, 2^28], so the shifted bounds stay inside int32 with kWinMax.
+template <int MASK, class Prob>
+__device__ __forceinline__ int diag_shift(const Prob& P) {
+  return MASK == RMX_MASK_CAUSAL ? P.window_right : 0;
 }
 __device__ __forceinline__ int clamp_i32(int64_t v) {
   return v > 2147483647 ? 2147483647 : (v < -2147483647 ? -2147483647 : (int)v);

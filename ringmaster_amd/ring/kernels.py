@@ -4,9 +4,13 @@
 (ring/kernels.py:28-85): ``fn(q, k, v, *, causal, scaling, dropout,
 attn_implementation, window) -> (out [b, sq, h, d] in q.dtype, lse [b, h, sq]
 fp32)``, q/k/v ``[b, s, h, d]``, GQA by ``kv_head = q_head // (hq/hkv)``, causal
-bottom-right aligned (ring/kernels.py:64-67), a sliding window ``(left, right)``
-masking ``pos_q - pos_k > left`` on the same bottom-right aligned positions
-(ring/kernels.py:68-72; ``right`` is not used, as there), head dims that are
+bottom-right aligned (ring/kernels.py:64-67), a sliding window ``(left, right)`` with
+flash attention's semantics (the ``window_size`` that the flash provider passes on,
+ring/kernels.py:37-38): ``pos_q - pos_k > left`` and ``pos_k - pos_q > right`` masked on
+the same bottom-right aligned positions, a negative bound or one of at least ``sk`` keys
+unbounded, and ``right`` 0 under ``causal`` (the math provider, ring/kernels.py:68-72,
+reads ``left`` only: the two agree wherever ``right`` is unbounded or the call causal),
+head dims that are
 multiples of 8 up to 256, bf16 or fp16, and attention dropout (the Dao semantics: kept
 probabilities scaled by 1 / (1 - p), lse undropped; the mask is the kernels' hash of
 (seed, batch, head, query, key), so the backward replays it exactly). It is autograd-aware
@@ -28,8 +32,8 @@ from ringmaster_amd import abi
 from ringmaster_amd.ring import ops
 
 
-def _validate(q, k, v, dropout, window, softcap=0.0, alibi=None):
-    """Checks of the provider contract; returns the window's left bound (None: no window)."""
+def _validate(q, k, v, dropout, softcap=0.0, alibi=None):
+    """Checks of the provider contract."""
     abi.require_device(q, k, v)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q/k/v must be [batch, seq, heads, dim]")
@@ -48,7 +52,6 @@ def _validate(q, k, v, dropout, window, softcap=0.0, alibi=None):
         raise NotImplementedError("mi355x_hip blocks do not implement softcap")
     if alibi is not None:
         raise NotImplementedError("mi355x_hip blocks do not implement ALiBi")
-    return window_left(window)
 
 
 _M64 = (1 << 64) - 1
@@ -84,10 +87,29 @@ def new_dropout_seed(device=None) -> int:
     return seed_of_rng_state(*dropout_rng_state(device))
 
 
+def window_bounds(window, causal: bool, sk: int | None = None):
+    """Flash attention's ``window_size = (left, right)`` as the kernels' bounds ``(left,
+    right)``: ``left`` on ``pos_q - pos_k``, ``right`` on ``pos_k - pos_q``, None where
+    unbounded. The rules of flash attention 2's window arguments: a negative bound is
+    unbounded, so is a bound of at least ``sk`` keys, a causal call is bounded at right = 0
+    by its mask (``right`` is then None), and a window bounded on the left only is bounded
+    on the right at ``sk`` (which masks keys only for rows of a block with sq > sk + 1).
+    Without ``sk`` (blocks with sq <= sk) the last two rules change nothing."""
+    if window is None:
+        return None, None
+    left, right = (int(x) for x in window)
+    if sk is not None:
+        left, right = (-1 if x >= sk else x for x in (left, right))
+        if left >= 0 and right < 0:
+            right = sk
+    return (left if left >= 0 else None), (None if causal or right < 0 else right)
+
+
 def window_left(window):
-    """The bound on ``pos_q - pos_k`` of a ``(left, right)`` window, or None. ``(-1, -1)``
-    (and None) is no window, as in the Dao ops; a negative ``left`` with a non-negative
-    ``right`` is refused (math_block would mask every key at or before the diagonal)."""
+    """The packed ring's window (its math path reads ``window[0]`` only, ring/loop.py:
+    185-186): the bound on ``pos_q - pos_k``, or None. ``(-1, -1)`` (and None) is no
+    window; a negative ``left`` with a non-negative ``right`` is refused (the math path
+    would mask every key at or before the diagonal)."""
     if window is None:
         return None
     left, right = (int(x) for x in window)
@@ -106,24 +128,37 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
+def _mask_of(causal: bool, right):
+    """The kernels' mask kind and right bound: a right-bounded window runs as the causal
+    mask with its diagonal moved ``right`` keys to the right."""
+    if causal:
+        return abi.MASK_CAUSAL, 0
+    if right is None:
+        return abi.MASK_FULL, 0
+    if right < 0:
+        raise ValueError(f"right window bound {right} < 0")
+    return abi.MASK_CAUSAL, min(int(right), 1 << 28)  # sk < 2^27: past that, unbounded
+
+
 def block_forward(q, k, v, scale: float, causal: bool, keep_f32: bool = False, window=None,
-                  dropout=None):
+                  dropout=None, right=None):
     """(out [b, sq, hq, d] in q's dtype, lse fp32 [b, hq, sq]) of one block; with ``keep_f32`` also
     the fp32 out (what the backward's delta is computed from). ``window``: bound on
-    ``pos_q - pos_k`` (bottom-right aligned positions) or None; ``dropout``: None or
-    (p, seed)."""
+    ``pos_q - pos_k`` (bottom-right aligned positions) or None; ``right``: bound on
+    ``pos_k - pos_q`` of a non-causal block or None; ``dropout``: None or (p, seed)."""
     b, sq, hq, d = q.shape
     out = torch.empty((b, sq, hq, d), dtype=q.dtype, device=q.device)
     lse = torch.empty((b, hq, sq), dtype=torch.float32, device=q.device)
     out32 = torch.empty((b, sq, hq, d), dtype=torch.float32, device=q.device) if keep_f32 else None
+    mask, shift = _mask_of(causal, right)
     ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_WRITE, out=out, lse=lse,
-                             acc_out=out32, window=window)],
-                 scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL, dropout=dropout)
+                             acc_out=out32, window=window, right=shift)],
+                 scale=scale, mask=mask, dropout=dropout)
     return (out, lse, out32) if keep_f32 else (out, lse)
 
 
 def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None, dk=None, dv=None,
-                   out_f32=None, window=None, dropout=None):
+                   out_f32=None, window=None, dropout=None, right=None):
     """dq, dk, dv (q's dtype) of one block using the given (global) out/lse; returns delta too.
     ``out_f32`` (the forward's fp32 out), when given, is what delta = rowsum(dout * out) reads;
     otherwise the 16-bit ``out`` is used, as a Dao-style backward does."""
@@ -141,10 +176,11 @@ def block_backward(dout, q, k, v, out, lse, scale: float, causal: bool, dq=None,
     dk_t = dk if (dk is not None and dk.is_contiguous()) else torch.empty(
         k.shape, dtype=k.dtype, device=k.device)
     dv_t = dv if (dv is not None and dv.stride() == dk_t.stride()) else torch.empty_like(dk_t)
+    mask, shift = _mask_of(causal, right)
     ops.attn_bwd([ops.BwdJob(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta, nlse=nlse,
                              dq_mode=abi.GRAD_WRITE_BF16, dkv_mode=abi.GRAD_WRITE_BF16,
-                             dq=dq_t, dk=dk_t, dv=dv_t, window=window)],
-                 scale=scale, mask=abi.MASK_CAUSAL if causal else abi.MASK_FULL, dropout=dropout)
+                             dq=dq_t, dk=dk_t, dv=dv_t, window=window, right=shift)],
+                 scale=scale, mask=mask, dropout=dropout)
     for dst, src in ((dq, dq_t), (dk, dk_t), (dv, dv_t)):
         if dst is not None and dst is not src:
             dst.copy_(src)
@@ -156,8 +192,9 @@ class _HipBlockAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, causal, scale, window, dropout):
         q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-        out, lse, out32 = block_forward(q, k, v, scale, causal, keep_f32=True, window=window,
-                                        dropout=dropout)
+        left, right = window
+        out, lse, out32 = block_forward(q, k, v, scale, causal, keep_f32=True, window=left,
+                                        dropout=dropout, right=right)
         ctx.save_for_backward(q, k, v, out, lse, out32)
         ctx.causal, ctx.scale, ctx.window, ctx.dropout = causal, scale, window, dropout
         ctx.mark_non_differentiable(lse)
@@ -167,8 +204,8 @@ class _HipBlockAttention(torch.autograd.Function):
     def backward(ctx, dout, _dlse):
         q, k, v, out, lse, out32 = ctx.saved_tensors
         dq, dk, dv, _ = block_backward(_kernel_ready(dout), q, k, v, out, lse, ctx.scale,
-                                       ctx.causal, out_f32=out32, window=ctx.window,
-                                       dropout=ctx.dropout)
+                                       ctx.causal, out_f32=out32, window=ctx.window[0],
+                                       dropout=ctx.dropout, right=ctx.window[1])
         return dq, dk, dv, None, None, None, None
 
 
@@ -178,13 +215,14 @@ def mi355x_hip_block(q, k, v, *, causal, scaling, dropout=0.0, attn_implementati
     ``dropout`` > 0 drops attention probabilities with the kernels' hash mask, seeded by
     ``dropout_seed`` (default: drawn from torch's CPU generator); the backward replays the
     same mask."""
-    left = _validate(q, k, v, dropout, window)
+    _validate(q, k, v, dropout)
+    bounds = window_bounds(window, bool(causal), k.shape[1])
     scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
     drop = None
     if dropout:
         drop = (float(dropout),
                 new_dropout_seed(q.device) if dropout_seed is None else int(dropout_seed))
-    return _HipBlockAttention.apply(q, k, v, bool(causal), float(scale), left, drop)
+    return _HipBlockAttention.apply(q, k, v, bool(causal), float(scale), bounds, drop)
 
 
 PROVIDERS = {
@@ -196,8 +234,8 @@ PROVIDERS = {
 def _flash_attn_forward(q, k, v, dropout_p, softmax_scale, causal, window_size_left=-1,
                         window_size_right=-1, softcap=0.0, alibi_slopes=None,
                         return_softmax=False):
-    _validate(q, k, v, dropout_p, None, softcap, alibi_slopes)
-    left = _dao_window(window_size_left, window_size_right, causal)
+    _validate(q, k, v, dropout_p, softcap, alibi_slopes)
+    left, right = window_bounds((window_size_left, window_size_right), bool(causal), k.shape[1])
     if return_softmax:
         raise NotImplementedError("return_softmax is not supported")
     rng_state, drop = None, None
@@ -209,15 +247,16 @@ def _flash_attn_forward(q, k, v, dropout_p, softmax_scale, causal, window_size_l
         rng_state = torch.tensor([gseed - (1 << 64) if gseed >= (1 << 63) else gseed, goff],
                                  dtype=torch.int64)
     out, lse = block_forward(_kernel_ready(q), _kernel_ready(k), _kernel_ready(v),
-                             float(softmax_scale), bool(causal), window=left, dropout=drop)
+                             float(softmax_scale), bool(causal), window=left, dropout=drop,
+                             right=right)
     return out, lse, None, rng_state
 
 
 def _flash_attn_backward(dout, q, k, v, out, lse, dq, dk, dv, dropout_p, softmax_scale, causal,
                          window_size_left=-1, window_size_right=-1, softcap=0.0,
                          alibi_slopes=None, deterministic=False, rng_state=None):
-    _validate(q, k, v, dropout_p, None, softcap, alibi_slopes)
-    left = _dao_window(window_size_left, window_size_right, causal)
+    _validate(q, k, v, dropout_p, softcap, alibi_slopes)
+    left, right = window_bounds((window_size_left, window_size_right), bool(causal), k.shape[1])
     drop = None
     if dropout_p:
         if rng_state is None:
@@ -227,17 +266,8 @@ def _flash_attn_backward(dout, q, k, v, out, lse, dq, dk, dv, dropout_p, softmax
     _, _, _, delta = block_backward(_kernel_ready(dout), _kernel_ready(q), _kernel_ready(k),
                                     _kernel_ready(v), _kernel_ready(out), lse,
                                     float(softmax_scale), bool(causal), dq, dk, dv, window=left,
-                                    dropout=drop)
+                                    dropout=drop, right=right)
     return dq, dk, dv, delta
-
-
-def _dao_window(left, right, causal):
-    """The Dao ops' ``window_size_left/right`` (-1 = unbounded; a causal call has no keys
-    right of the diagonal anyway) as the kernels' bound on ``pos_q - pos_k``."""
-    left, right = int(left), int(right)
-    if right >= 0 and not causal:
-        raise NotImplementedError("windows bounded on the right are not supported")
-    return left if left >= 0 else None
 
 
 def flash_ops():

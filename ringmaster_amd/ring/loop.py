@@ -17,7 +17,9 @@ Sliding windows (the gather ring and the packed ring: ring/loop.py:185-186,201-2
 keep the reference's positions: the gather ring's single block call aligns rank r's
 queries bottom-right against the gathered keys, which for a causal ring is the global
 position ``r L + i`` and for a non-causal ring (all P blocks gathered) ``(P - 1) L + i``;
-the packed ring compares global indices. Dropout in the gather ring draws one mask over
+there the window is the block provider's, flash attention's ``(left, right)`` (a
+non-causal ring bounded on the right too); the packed ring compares global indices and
+reads ``left`` only, as its math path does (:185-186). Dropout in the gather ring draws one mask over
 (global query, gathered key) pairs per call; its blocks take their coordinates from it.
 """
 
@@ -25,7 +27,7 @@ from __future__ import annotations
 
 import torch
 
-from ringmaster_amd.ring.kernels import PROVIDERS, new_dropout_seed, window_left
+from ringmaster_amd.ring.kernels import PROVIDERS, new_dropout_seed, window_bounds, window_left
 from ringmaster_amd.ring.p2p_attn import contiguous_ring
 from ringmaster_amd.ring.zigzag import doc_for
 
@@ -56,13 +58,17 @@ def ring_attention(q, k, v, *, group=None, causal: bool, scaling=None, dropout: 
         if not 0.0 <= float(dropout) < 1.0:
             raise ValueError(f"dropout must lie in [0, 1) (got {dropout})")
         drop = (float(dropout), new_dropout_seed(q.device)) if dropout else None
-        left = window_left(window)
+        # the block provider's window (flash semantics); rank r's L queries sit bottom-right
+        # against at least L gathered keys, so bounds of sk keys or more change nothing
+        left, right = window_bounds(window, bool(causal))
         P, L = q.shape[0], q.shape[3]
-        bounds = None
+        bounds = rights = None
         if left is not None:  # bottom-right aligned against the gathered keys
             bounds = [left if causal else left - (P - 1 - r) * L for r in range(P)]
+        if right is not None:  # non-causal: query i of rank r at (P - 1) L + i
+            rights = [right + (P - 1 - r) * L for r in range(P)]
         return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer,
-                               window=bounds, dropout=drop)
+                               window=bounds, dropout=drop, right=rights)
     if dropout or window is not None or attn_implementation not in ("flash_attention_2", "math"):
         raise ValueError("P2P Ring requires FA2, zero dropout, and no sliding window")
     return contiguous_ring(q, k, v, causal=causal, scaling=scaling, timer=timer)

@@ -36,6 +36,7 @@ class FwdJob:
     window: int | None = None  # bound on pos_q - pos_k (global indices with document masks)
     drop_q0: int = 0  # dropout coordinates of the first query / key
     drop_k0: int = 0
+    right: int = 0  # causal masks: bound on pos_k - pos_q (0: causal attention)
 
 
 @dataclasses.dataclass
@@ -62,6 +63,7 @@ class BwdJob:
     window: int | None = None
     drop_q0: int = 0
     drop_k0: int = 0
+    right: int = 0
 
 
 def _i32_field(v, what):
@@ -76,6 +78,7 @@ def _set_problem_extras(p, job):
         p.has_window, p.window_left = 1, _i32_field(job.window, "window bound")
     p.drop_q0 = _i32_field(job.drop_q0, "dropout query offset")
     p.drop_k0 = _i32_field(job.drop_k0, "dropout key offset")
+    p.window_right = _i32_field(job.right, "right window bound")
 
 
 def _set_dropout(lay, dropout):

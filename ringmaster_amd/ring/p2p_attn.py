@@ -18,17 +18,20 @@ from ringmaster_amd.ring.zigzag import EmulatedRing, check_ring_inputs
 
 
 def contiguous_ring(q, k, v, *, causal: bool, scaling=None, doc=None, timer=None, window=None,
-                    dropout=None):
+                    dropout=None, right=None):
     """q/k/v: [P, b, H, L, d] bf16, rank r's contiguous interface tensors stacked on
     dim 0. Returns out [P, b, L, H, d]. ``doc``: per-token document ids of the packed
     sequence, [S] or [b, S] per batch row (document-masked blocks; without ``causal`` every
     key of the query's document). ``window``: one bound per rank on the global
-    ``pos_q - pos_k`` of its queries (sliding windows), or None. ``dropout``: None or
-    (p, seed), one mask over (global query, global key) for every block."""
+    ``pos_q - pos_k`` of its queries (sliding windows), or None; ``right`` (non-causal rings
+    without documents): one bound per rank on the global ``pos_k - pos_q``, or None.
+    ``dropout``: None or (p, seed), one mask over (global query, global key) for every
+    block."""
     check_ring_inputs(q, k, v)
     scale = scaling if scaling is not None else 1.0 / math.sqrt(q.shape[-1])
     return EmulatedRing.apply(q, k, v, float(scale), doc, timer, "contiguous", bool(causal),
-                              None if window is None else tuple(int(w) for w in window), dropout)
+                              None if window is None else tuple(int(w) for w in window), dropout,
+                              None if right is None else tuple(int(w) for w in right))
 
 
 def ring_p2p_attention(q, k, v, *, group=None, causal, scaling, timer=None):

@@ -88,7 +88,7 @@ class _Ctx:
     zigzag and DistFlash rings are causal only."""
 
     def __init__(self, q, k, scale, doc, layout="zigzag", causal=True, window=None,
-                 dropout=None):
+                 dropout=None, right=None):
         self.P, self.b, self.hq, self.L, self.d = q.shape
         self.hkv = k.shape[2]
         self.half = self.L // 2
@@ -96,6 +96,14 @@ class _Ctx:
         self.doc = doc
         self.layout, self.causal = layout, causal
         self.window = None if window is None else [int(w) for w in window]
+        # right: one bound per rank on the global pos_k - pos_q of its queries (non-causal)
+        self.right = None if right is None else [int(w) for w in right]
+        if self.right is not None:
+            if len(self.right) != self.P:
+                raise ValueError("the right window takes one bound per rank")
+            if causal or layout != "contiguous" or doc is not None:
+                raise NotImplementedError("right-bounded windows run on non-causal contiguous "
+                                          "rings without document masks")
         self.dropout = dropout  # None or (p, seed): one mask over (rank's query, gathered key)
         if dropout is not None and layout == "zigzag":
             raise NotImplementedError("dropout runs on contiguous shards")
@@ -136,6 +144,8 @@ class _Ctx:
     def mask(self, step: int) -> int:
         if self.doc is not None:
             return abi.MASK_DOC
+        if self.right is not None:  # every block: the causal mask, its diagonal shifted
+            return abi.MASK_CAUSAL
         return abi.MASK_CAUSAL if (self.causal and step == 0) else abi.MASK_FULL
 
     def block_window(self, bl):
@@ -152,6 +162,20 @@ class _Ctx:
         sq, sk = bl.q_hi - bl.q_lo, bl.k_hi - bl.k_lo
         shift = (bl.rank * self.L + bl.q_lo) - (bl.kv_rank * self.L + bl.k_lo) - (sk - sq)
         return w - shift
+
+    def block_right(self, bl):
+        """The kernel's right bound (the causal diagonal's shift) for block ``bl``: 0 when
+        the ring has no right bound. ``right[r]`` bounds ``pos_k - pos_q`` of rank r's
+        queries in global positions; the block's bottom-right aligned difference differs
+        from it by the same constant as in :meth:`block_window`, with the opposite sign."""
+        if self.right is None:
+            return 0
+        sq, sk = bl.q_hi - bl.q_lo, bl.k_hi - bl.k_lo
+        shift = (bl.rank * self.L + bl.q_lo) - (bl.kv_rank * self.L + bl.k_lo) - (sk - sq)
+        r = self.right[bl.rank] + shift
+        if r < 0:
+            raise NotImplementedError(f"block ({bl.rank}, {bl.kv_rank}): right bound {r} < 0")
+        return min(r, 1 << 28)
 
     def block_drop(self, bl):
         """Dropout coordinates of block ``bl``: the global index of its first query row and of
@@ -226,7 +250,7 @@ def _only(blocks, only_ranks):
 
 def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=None,
                  layout: str = "zigzag", causal: bool = True, only_ranks=None, window=None,
-                 dropout=None):
+                 dropout=None, right=None):
     """Emulated ring forward (zigzag or contiguous layout). q/k/v: [P, b, H, L, d] bf16
     (interface layout per rank).
     Returns (out [P, b, L, H, d] bf16, lse [P, b, H, L] fp32, out32 [P, b, L, H, d] fp32):
@@ -236,9 +260,10 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
     DistFlash the helper computes blocks of other ranks' queries), each step at the grid
     one GPU of a real P-GPU ring runs; outputs of the blocks left out are then not
     computed (per-rank timing). ``window`` (contiguous layouts or document masks): one
-    bound per rank on the global ``pos_q - pos_k`` of its queries."""
+    bound per rank on the global ``pos_q - pos_k`` of its queries; ``right`` (non-causal
+    contiguous rings): one bound per rank on the global ``pos_k - pos_q``."""
     timer = timer or _NO_TIMER
-    c = _Ctx(q, k, scale, doc, layout, causal, window, dropout)
+    c = _Ctx(q, k, scale, doc, layout, causal, window, dropout, right)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)  # [P, b, L, H, d] views
     dev = q.device
     out = torch.empty((c.P, c.b, c.L, c.hq, c.d), dtype=q.dtype, device=dev)
@@ -260,7 +285,8 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
                 acc_lse=None if acc_lse is None else acc_lse[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.kidx(kr, bl.k_lo, bl.k_hi),
                 q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi),
-                window=c.block_window(bl), **dict(zip(("drop_q0", "drop_k0"), c.block_drop(bl)))))
+                window=c.block_window(bl), right=c.block_right(bl),
+                **dict(zip(("drop_q0", "drop_k0"), c.block_drop(bl)))))
         with timer("attn_fwd"):
             ops.attn_fwd(jobs, scale=scale, mask=c.mask(s), dropout=c.dropout)
     return out, lse, acc
@@ -268,14 +294,14 @@ def ring_forward(q, k, v, scale: float, doc: torch.Tensor | None = None, timer=N
 
 def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | None = None,
                   timer=None, layout: str = "zigzag", causal: bool = True, only_ranks=None,
-                  window=None, dropout=None):
+                  window=None, dropout=None, right=None):
     """Reverse-ring backward with the global out/lse. dout: [P, b, L, H, d] bf16; out: the
     global out, fp32 (the forward's ``out32``) or bf16, [P, b, L, H, d].
     Returns fp32 (dq [P, b, L, Hq, d], dk, dv [P, b, L, Hkv, d]). Each step launches the
     KV-major dK/dV kernel and the Q-major dQ kernel over all ranks (``only_ranks``: over
     those ranks only, as in :func:`ring_forward`; the gradients are then partial)."""
     timer = timer or _NO_TIMER
-    c = _Ctx(q, k, scale, doc, layout, causal, window, dropout)
+    c = _Ctx(q, k, scale, doc, layout, causal, window, dropout, right)
     qd, kd, vd = q.transpose(2, 3), k.transpose(2, 3), v.transpose(2, 3)
     dev = q.device
     if not dout.is_contiguous():
@@ -305,7 +331,8 @@ def ring_backward(dout, q, k, v, out, lse, scale: float, doc: torch.Tensor | Non
                 lse=lse[r][:, :, qs], delta=delta[r][:, :, qs], nlse=nlse[r][:, :, qs],
                 q_gidx=c.idx(r, bl.q_lo, bl.q_hi), k_gidx=c.kidx(kr, bl.k_lo, bl.k_hi),
                 q_doc=c.docs(r, bl.q_lo, bl.q_hi), k_doc=c.docs(kr, bl.k_lo, bl.k_hi),
-                window=c.block_window(bl), **dict(zip(("drop_q0", "drop_k0"), c.block_drop(bl))))
+                window=c.block_window(bl), right=c.block_right(bl),
+                **dict(zip(("drop_q0", "drop_k0"), c.block_drop(bl))))
             kv_jobs.append(ops.BwdJob(dq_mode=abi.GRAD_NONE, dkv_mode=mode,
                                       dk_acc=dk[kr][:, ks], dv_acc=dv[kr][:, ks], **common))
             q_jobs.append(ops.BwdJob(dq_mode=mode, dkv_mode=abi.GRAD_NONE,
@@ -321,22 +348,25 @@ class EmulatedRing(torch.autograd.Function):
     """The emulated ring (zigzag or contiguous layout) with its reverse-ring backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, doc, timer, layout, causal, window=None, dropout=None):
+    def forward(ctx, q, k, v, scale, doc, timer, layout, causal, window=None, dropout=None,
+                right=None):
         out, lse, out32 = ring_forward(q, k, v, scale, doc, timer, layout, causal, window=window,
-                                       dropout=dropout)
+                                       dropout=dropout, right=right)
         ctx.save_for_backward(q, k, v, out32, lse)
         ctx.scale, ctx.doc, ctx.timer = scale, doc, timer
         ctx.layout, ctx.causal, ctx.window, ctx.dropout = layout, causal, window, dropout
+        ctx.right = right
         return out
 
     @staticmethod
     def backward(ctx, d_out):
         q, k, v, out32, lse = ctx.saved_tensors
         dq, dk, dv = ring_backward(d_out, q, k, v, out32, lse, ctx.scale, ctx.doc, ctx.timer,
-                                   ctx.layout, ctx.causal, window=ctx.window, dropout=ctx.dropout)
+                                   ctx.layout, ctx.causal, window=ctx.window, dropout=ctx.dropout,
+                                   right=ctx.right)
         # fp32 accumulators -> q.dtype, returned in the interface layout [P, b, H, L, d]
         return (dq.to(q.dtype).transpose(2, 3), dk.to(k.dtype).transpose(2, 3),
-                dv.to(v.dtype).transpose(2, 3), None, None, None, None, None, None, None)
+                dv.to(v.dtype).transpose(2, 3), None, None, None, None, None, None, None, None)
 
 
 def check_ring_inputs(q, k, v):

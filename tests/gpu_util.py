@@ -77,3 +77,17 @@ def assert_f16_close(got, ref, what=""):
     rl = rel_l2(got, ref)
     assert over < 1 and rl < F16_REL_L2, \
         f"{what}: max-abs {diff.max().item():.3e} ({over:.2f} of the bar) rel-L2 {rl:.3e}"
+
+
+def keyless_prefix(sq, sk, causal, window=None):
+    """The number of leading rows of a block that attend no key: with a right bound R on
+    ``pos_k - pos_q`` (causal: R = 0; a flash window's right bound) the rows with
+    ``q + sk - sq + R < 0``, none without one (a left bound never empties a row, since
+    every bottom-right aligned ``pos_q`` is at most sk - 1). The kernels give those rows
+    out 0, lse -inf and dq 0; the oracle runs on the others, whose positions are kept."""
+    from oracle import ring_math as rm
+
+    right = 0 if causal else None
+    if window is not None:
+        right = rm.flash_window(window, causal, sk)[1]
+    return min(sq, max(0, sq - sk - right)) if right is not None else 0

@@ -7,6 +7,7 @@ import re
 from pathlib import Path
 
 import pytest
+import torch
 
 from ringmaster_amd import abi
 
@@ -29,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = abi.lib()
-    assert lib.rmx_abi_version() == abi.ABI_VERSION == 17
+    assert lib.rmx_abi_version() == abi.ABI_VERSION == 18
     assert isinstance(lib.rmx_last_error(), bytes)
 
 
@@ -108,14 +109,37 @@ def test_host_validation_window_flag():
     assert abi.lib().rmx_attn_bwd(ctypes.byref(lay), barr, 1, None) == abi.RMX_EINVAL
 
 
+def test_host_validation_window_right():
+    """window_right (the shift of the causal diagonal) lies in [0, 2^28] and needs the
+    causal mask kind; the checks run before any pointer is read."""
+    lib = abi.lib()
+    for mask, right, rc in ((abi.MASK_CAUSAL, -1, abi.RMX_EINVAL),
+                            (abi.MASK_CAUSAL, (1 << 28) + 1, abi.RMX_EINVAL),
+                            (abi.MASK_FULL, 5, abi.RMX_EINVAL),
+                            (abi.MASK_DOC, 5, abi.RMX_EINVAL),
+                            (abi.MASK_CAUSAL, 1 << 28, abi.RMX_OK),
+                            (abi.MASK_CAUSAL, 0, abi.RMX_OK)):
+        lay = _layout(mask=mask, m_sb=0)
+        arr = (abi.FwdProblem * 1)()
+        arr[0].window_right = right  # sq = sk = 0: validated, nothing launched
+        assert lib.rmx_attn_fwd(ctypes.byref(lay), arr, 1, None) == rc, (mask, right)
+        if rc:
+            assert b"window_right" in lib.rmx_last_error()
+        barr = (abi.BwdProblem * 1)()
+        barr[0].window_right = right
+        assert lib.rmx_attn_bwd(ctypes.byref(lay), barr, 1, None) == rc, (mask, right)
+
+
 def test_problem_structs_match_the_header():
     """The ctypes mirrors have the C layout: the window and dropout fields sit at the end
     of each problem struct (a zero-filled problem has no window and no offsets)."""
-    assert ctypes.sizeof(abi.FwdProblem) == 11 * 8 + 7 * 4 + 4
-    assert ctypes.sizeof(abi.BwdProblem) == 17 * 8 + 8 * 4
+    assert ctypes.sizeof(abi.FwdProblem) == 11 * 8 + 8 * 4
+    assert ctypes.sizeof(abi.BwdProblem) == 17 * 8 + 9 * 4 + 4
     assert abi.FwdProblem.has_window.offset == 11 * 8 + 3 * 4
     assert abi.BwdProblem.has_window.offset == 17 * 8 + 4 * 4
     assert abi.FwdProblem.drop_k0.offset == 11 * 8 + 6 * 4
+    assert abi.FwdProblem.window_right.offset == 11 * 8 + 7 * 4
+    assert abi.BwdProblem.window_right.offset == 17 * 8 + 8 * 4
     assert abi.AttnLayout.q_sb.offset == 40  # after the dtype, dropout and seed words
     assert abi.AttnLayout.m_sb.offset == 40 + 23 * 8  # after the 23 tensor strides
     assert ctypes.sizeof(abi.AttnLayout) == 40 + 24 * 8
@@ -343,3 +367,43 @@ def test_linear_scan_status_host_checks():
     assert lib.rmx_linear_scan_status(None, 0, None) == abi.RMX_OK
     assert lib.rmx_linear_scan_status(16, 8, None) == abi.RMX_EINVAL
     assert b"too small" in lib.rmx_last_error()
+
+
+def _band(sq, sk, causal, left, right):
+    """The kept (q, k) pairs of a block under a causal flag and bounds (None: unbounded)
+    on pos_q - pos_k and pos_k - pos_q, bottom-right aligned positions."""
+    iq = torch.arange(sq)[:, None] + (sk - sq)
+    ik = torch.arange(sk)[None, :]
+    keep = torch.ones(sq, sk, dtype=torch.bool)
+    if causal:
+        keep &= ik <= iq
+    if left is not None:
+        keep &= iq - ik <= left
+    if right is not None:
+        keep &= ik - iq <= right
+    return keep
+
+
+def test_window_bounds_keep_the_flash_pairs():
+    """The provider's window resolution (host logic that picks the kernels' mask kind and
+    bounds) keeps exactly the pairs of the oracle's flash-attention window rules, over a
+    grid of block shapes and windows; the gather ring's form (no sk) agrees wherever
+    sq <= sk."""
+    from oracle import ring_math as rm
+    from ringmaster_amd.ring.kernels import _mask_of, window_bounds
+
+    for sq, sk in ((5, 5), (3, 8), (8, 3), (9, 4), (1, 6), (6, 1), (7, 6)):
+        for causal in (False, True):
+            for w in ((-1, -1), (0, 0), (2, -1), (-1, 2), (1, 3), (3, 1), (sk, 0), (0, sk),
+                      (sk + 2, sk + 2), (-5, 4), (7, -3)):
+                left, right = window_bounds(w, causal, sk)
+                mask, shift = _mask_of(causal, right)
+                # the causal mask kind keeps k <= q + (sk - sq) + shift
+                got = _band(sq, sk, False, left, shift if mask == abi.MASK_CAUSAL else None)
+                ref = _band(sq, sk, causal, *rm.flash_window(w, causal, sk))
+                assert torch.equal(got, ref), (sq, sk, causal, w)
+                if sq <= sk:
+                    left2, right2 = window_bounds(w, causal)
+                    mask2, shift2 = _mask_of(causal, right2)
+                    got2 = _band(sq, sk, False, left2, shift2 if mask2 == abi.MASK_CAUSAL else None)
+                    assert torch.equal(got2, ref), (sq, sk, causal, w)

@@ -35,7 +35,7 @@ def _block(causal, hq, hkv, sq, sk, d, p, seed, window=None, half=torch.bfloat16
     torch.cuda.synchronize()
     qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf, kf, vf))
     ref, ref_lse = rm.math_block(qr, kr, vr, causal=causal, scaling=None, dropout=p,
-                                 drop_seed=seed, window=window)
+                                 drop_seed=seed, window=window, flash=True)
     ref.backward(dof)
     close(out, ref, "out")
     assert_f32_rel(lse, ref_lse, "lse (undropped)")
@@ -57,6 +57,10 @@ def test_dropout_block(causal, hq, hkv, sq, sk, d, p):
 
 def test_dropout_block_fp16_window():
     _block(True, 4, 2, 300, 300, 128, 0.25, seed=77, window=(90, 0), half=torch.float16)
+
+
+def test_dropout_block_right_window():
+    _block(False, 4, 2, 300, 280, 128, 0.2, seed=91, window=(50, 20))
 
 
 @pytest.mark.parametrize("b,hq,sq,sk,p,seed", [

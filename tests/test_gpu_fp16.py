@@ -29,7 +29,8 @@ def _block(causal, hq, hkv, sq, sk, d, window=None, b=1, seed=0):
     torch.cuda.synchronize()
     assert out.dtype == torch.float16 and qd.grad.dtype == torch.float16
     qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf, kf, vf))
-    ref, ref_lse = rm.math_block(qr, kr, vr, causal=causal, scaling=None, window=window)
+    ref, ref_lse = rm.math_block(qr, kr, vr, causal=causal, scaling=None, window=window,
+                                 flash=True)
     ref.backward(dof)
     assert_f16_close(out, ref, "out")
     assert_f32_rel(lse, ref_lse, "lse")
@@ -51,6 +52,7 @@ def test_fp16_block(causal, hq, hkv, sq, sk, d):
 
 def test_fp16_block_window():
     _block(True, 4, 2, 400, 400, 128, window=(100, 0))
+    _block(False, 4, 2, 256, 300, 128, window=(-1, 33))  # bounded on the right only
 
 
 def test_fp16_dao_ops():

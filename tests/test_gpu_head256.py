@@ -37,7 +37,7 @@ def _block(causal, hq, hkv, sq, sk, d, window=None, b=1, seed=0, half=torch.bflo
     torch.cuda.synchronize()
     qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf, kf, vf))
     ref, ref_lse = rm.math_block(qr, kr, vr, causal=causal, scaling=None, window=window,
-                                 dropout=dropout, drop_seed=seed_d)
+                                 dropout=dropout, drop_seed=seed_d, flash=True)
     ref.backward(dof)
     close(out, ref, "out")
     assert_f32_rel(lse, ref_lse, "lse")
@@ -63,6 +63,8 @@ def test_block_head_dim_above_128(causal, hq, hkv, sq, sk, d):
 def test_block_head_dim_256_batch2_window():
     _block(True, 4, 2, 400, 400, 256, window=(90, 0), b=2)
     _block(False, 2, 2, 190, 260, 256, window=(70, 0), seed=5)
+    _block(False, 2, 2, 190, 260, 256, window=(-1, 40), seed=6)  # right-bounded only
+    _block(False, 2, 1, 260, 190, 256, window=(64, 90), seed=7)  # both bounds, sk < sq
 
 
 def test_block_head_dim_256_fp16():

@@ -3,7 +3,9 @@
 Each case draws batch 1-2, query and key lengths from 1 to 700 (ragged against every tile
 size, sk < sq included: bottom-right causal then leaves the first rows without keys, out 0 and
 lse -inf), GQA ratios 1-8, head dims that are multiples of 8 up to 256 (all three kernel
-sets), causal or not, a window or none, bf16 or fp16, and dropout or none, and checks out,
+sets), causal or not, a window or none (flash attention's ``(left, right)``: every other
+non-causal windowed case bounded on the right too, the others by the left bound and flash's
+right bound at sk), bf16 or fp16, and dropout or none, and checks out,
 lse and the three gradients against ``math_block`` (ring/kernels.py:52-78) at the bf16 / fp16
 bars: max(2e-2, two ulps of the element) for bf16 gradients (5e-3 and fp16 ulps for fp16),
 wider only for the dK of the named cancellation cases (``_CANCEL``). The draw is fixed (numpy
@@ -17,7 +19,7 @@ import torch
 
 from oracle import ring_math as rm
 from tests.gpu_util import (assert_bf16_close, assert_f16_close, assert_f32_rel, bf16_pair,
-                            f16_pair, rel_l2)
+                            f16_pair, keyless_prefix, rel_l2)
 
 pytestmark = pytest.mark.gpu
 
@@ -36,13 +38,16 @@ def _cases(n=48, seed=20261202):
         half = "f16" if rng.random() < 0.25 else "bf16"
         p = float(rng.choice([0.1, 0.3])) if rng.random() < 0.2 else 0.0
         b = int(rng.choice([1, 2]))
-        out.append((i, b, sq, sk, hkv * g, hkv, d, causal, left, half, p))
+        # the right bound: derived from the index, so the draws above stay as they were
+        right = (7 * i) % 61 if (left is not None and not causal and i % 2) else -1
+        out.append((i, b, sq, sk, hkv * g, hkv, d, causal, left, right, half, p))
     return out
 
 
 def _id(c):
-    i, b, sq, sk, hq, hkv, d, causal, left, half, p = c
-    return f"{i}-b{b}-q{sq}-k{sk}-h{hq}:{hkv}-d{d}-{'c' if causal else 'f'}-w{left}-{half}-p{p}"
+    i, b, sq, sk, hq, hkv, d, causal, left, right, half, p = c
+    win = f"w{left}" + (f",{right}" if right >= 0 else "")
+    return f"{i}-b{b}-q{sq}-k{sk}-h{hq}:{hkv}-d{d}-{'c' if causal else 'f'}-{win}-{half}-p{p}"
 
 
 # Cases whose dK and dV sum many query rows onto few keys (700 queries onto 3 keys; 511
@@ -95,12 +100,12 @@ def _grad_spread(qf, kf, vf, dof, causal, left):
 def test_block_sweep(case):
     from ringmaster_amd.ring.kernels import mi355x_hip_block
 
-    i, b, sq, sk, hq, hkv, d, causal, left, half, p = case
+    i, b, sq, sk, hq, hkv, d, causal, left, right, half, p = case
     print(f"case sweep {_id(case)}", flush=True)
     f16 = half == "f16"
     pair = f16_pair if f16 else bf16_pair
     close = assert_f16_close if f16 else assert_bf16_close
-    window = None if left is None else (left, 0)
+    window = None if left is None else (left, right)
     qf, qd = pair((b, sq, hq, d), 100 + i)
     kf, kd = pair((b, sk, hkv, d), 200 + i)
     vf, vd = pair((b, sk, hkv, d), 300 + i)
@@ -112,14 +117,14 @@ def test_block_sweep(case):
                                 dropout=p, dropout_seed=seed)
     out.backward(dod)
     torch.cuda.synchronize()
-    # rows without any key (bottom-right causal with sk < sq): the prefix i < sq - sk. The
-    # oracle runs on the other rows, which keep their positions (and dropout coordinates,
-    # drop_q0 = s0) as a block of sk rows; the kernels give those rows out 0, lse -inf and
-    # dq 0 (the convention of the reference's masked blocks, ring/varlen_blocks.py:70-79)
-    s0 = sq - sk if causal and sq > sk else 0
+    # rows without any key (a right bound R with sk + R < sq, R = 0 for causal blocks): the
+    # prefix i < sq - sk - R. The oracle runs on the other rows, which keep their positions
+    # (and dropout coordinates, drop_q0 = s0); the kernels give those rows out 0, lse -inf
+    # and dq 0 (the convention of the reference's masked blocks, ring/varlen_blocks.py:70-79)
+    s0 = keyless_prefix(sq, sk, causal, window)
     qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf[:, s0:], kf, vf))
     ref, ref_lse = rm.math_block(qr, kr, vr, causal=causal, scaling=None, window=window,
-                                 dropout=p, drop_seed=seed, drop_q0=s0)
+                                 dropout=p, drop_seed=seed, drop_q0=s0, flash=True)
     ref.backward(dof[:, s0:])
     got_l = lse.detach().cpu()
     assert torch.isneginf(got_l[:, :, :s0]).all(), "rows without keys: lse"

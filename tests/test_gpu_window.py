@@ -1,7 +1,10 @@
 """Sliding windows and head dims other than 64/128 on the MI355X vs the CPU oracle (fp32).
 
-The provider contract's ``window`` (ring/kernels.py:68-72: ``pos_q - pos_k > left`` masked,
-bottom-right aligned) on single blocks and through the Dao op pair, the gather ring and
+The provider contract's ``window`` on single blocks and through the Dao op pair: flash
+attention's ``window_size = (left, right)`` (the flash provider passes it on,
+ring/kernels.py:37-38; ``pos_q - pos_k > left`` and ``pos_k - pos_q > right`` masked,
+bottom-right aligned, causal calls bounded at right = 0; the oracle is ``math_block`` with
+``flash=True``, which reads ``left`` as ring/kernels.py:68-72 does), the gather ring and
 the packed gather ring with windows (ring/loop.py:175-228), and head dims that are
 multiples of 8 up to 128 (the kernels compute at 64 or 128 and read the columns past
 head_dim as zeros; head dims above 128: tests/test_gpu_head256.py)."""
@@ -10,7 +13,7 @@ import pytest
 import torch
 
 from oracle import ring_math as rm
-from tests.gpu_util import assert_bf16_close, assert_f32_rel, bf16_pair
+from tests.gpu_util import assert_bf16_close, assert_f32_rel, bf16_pair, keyless_prefix
 
 pytestmark = pytest.mark.gpu
 
@@ -29,25 +32,32 @@ def _block(causal, hq, hkv, sq, sk, d, window, b=1, seed=0):
     out, lse = mi355x_hip_block(qd, kd, vd, causal=causal, scaling=None, window=window)
     out.backward(dod)
     torch.cuda.synchronize()
-    qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf, kf, vf))
-    ref, ref_lse = rm.math_block(qr, kr, vr, causal=causal, scaling=None, window=window)
-    ref.backward(dof)
-    assert_bf16_close(out, ref, "out")
-    assert_f32_rel(lse, ref_lse, "lse")
-    assert_bf16_close(qd.grad, qr.grad, "dq")
+    s0 = keyless_prefix(sq, sk, causal, window)
+    assert torch.isneginf(lse[:, :, :s0].cpu()).all(), "rows without keys: lse"
+    assert not out[:, :s0].float().abs().sum().item(), "rows without keys: out"
+    assert not qd.grad[:, :s0].float().abs().sum().item(), "rows without keys: dq"
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf[:, s0:], kf, vf))
+    ref, ref_lse = rm.math_block(qr, kr, vr, causal=causal, scaling=None, window=window,
+                                 flash=True)
+    ref.backward(dof[:, s0:])
+    assert_bf16_close(out[:, s0:], ref, "out")
+    assert_f32_rel(lse[:, :, s0:], ref_lse, "lse")
+    assert_bf16_close(qd.grad[:, s0:], qr.grad, "dq")
     assert_bf16_close(kd.grad, kr.grad, "dk", ulp_floor=hq != hkv)
     assert_bf16_close(vd.grad, vr.grad, "dv", ulp_floor=hq != hkv)
 
 
-@pytest.mark.parametrize("causal,hq,hkv,sq,sk,d,left", [
-    (True, 2, 2, 300, 300, 128, 64),     # the window's edge crosses key tiles
-    (True, 4, 2, 200, 517, 64, 100),     # bottom-right aligned, sq < sk
-    (False, 2, 1, 256, 256, 128, 17),    # non-causal: only the left edge
-    (True, 2, 2, 1100, 1100, 128, 255),  # whole key tiles below the window skipped
-    (False, 4, 4, 320, 96, 128, 40),     # sk < sq: rows near the end keep few keys
+@pytest.mark.parametrize("causal,hq,hkv,sq,sk,d,left,right", [
+    (True, 2, 2, 300, 300, 128, 64, 0),     # the window's edge crosses key tiles
+    (True, 4, 2, 200, 517, 64, 100, 0),     # bottom-right aligned, sq < sk
+    (False, 2, 1, 256, 256, 128, 17, -1),   # non-causal: only the left edge
+    (True, 2, 2, 1100, 1100, 128, 255, 0),  # whole key tiles below the window skipped
+    (False, 4, 4, 320, 96, 128, 40, -1),    # sk < sq: flash bounds the right at sk keys
+    (False, 2, 1, 256, 256, 128, 17, 0),    # non-causal (17, 0): the causal band
+    (False, 4, 4, 320, 96, 128, 40, 0),     # sk < sq, right 0: the first 224 rows keyless
 ])
-def test_block_window(causal, hq, hkv, sq, sk, d, left):
-    _block(causal, hq, hkv, sq, sk, d, (left, 0))
+def test_block_window(causal, hq, hkv, sq, sk, d, left, right):
+    _block(causal, hq, hkv, sq, sk, d, (left, right))
 
 
 def test_block_window_zero_attends_itself():
@@ -107,15 +117,53 @@ def test_dao_ops_window():
     bwd(do, q, k, v, out, lse, dq, dk, dv, 0.0, 0.125, True, 90, 0, 0.0, None, False, None)
     torch.cuda.synchronize()
     qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf, kf, vf))
-    ref, ref_lse = rm.math_block(qr, kr, vr, causal=True, scaling=0.125, window=(90, 0))
+    ref, ref_lse = rm.math_block(qr, kr, vr, causal=True, scaling=0.125, window=(90, 0),
+                                 flash=True)
     ref.backward(dof)
     assert_bf16_close(out, ref, "out")
     assert_f32_rel(lse, ref_lse, "lse")
     assert_bf16_close(dq, qr.grad, "dq")
     assert_bf16_close(dk, kr.grad, "dk", ulp_floor=True)
     assert_bf16_close(dv, vr.grad, "dv", ulp_floor=True)
-    with pytest.raises(NotImplementedError, match="right"):
-        fwd(q, k, v, 0.0, 0.125, False, 90, 5, 0.0, None, False)
+
+
+def test_dao_ops_right_window():
+    """The Dao op pair with window_size_right on a non-causal block (the flash provider's
+    (left, right), GQA 2:1, sq != sk)."""
+    from ringmaster_amd.ring.kernels import flash_ops
+
+    fwd, bwd = flash_ops()
+    print("case dao right window 260x300 (40, 25)", flush=True)
+    qf, q = bf16_pair((1, 260, 4, 128), 21)
+    kf, k = bf16_pair((1, 300, 2, 128), 22)
+    vf, v = bf16_pair((1, 300, 2, 128), 23)
+    dof, do = bf16_pair((1, 260, 4, 128), 24)
+    out, lse, _, _ = fwd(q, k, v, 0.0, 0.125, False, 40, 25, 0.0, None, False)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    bwd(do, q, k, v, out, lse, dq, dk, dv, 0.0, 0.125, False, 40, 25, 0.0, None, False, None)
+    torch.cuda.synchronize()
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf, kf, vf))
+    ref, ref_lse = rm.math_block(qr, kr, vr, causal=False, scaling=0.125, window=(40, 25),
+                                 flash=True)
+    ref.backward(dof)
+    assert_bf16_close(out, ref, "out")
+    assert_f32_rel(lse, ref_lse, "lse")
+    assert_bf16_close(dq, qr.grad, "dq")
+    assert_bf16_close(dk, kr.grad, "dk", ulp_floor=True)
+    assert_bf16_close(dv, vr.grad, "dv", ulp_floor=True)
+
+
+@pytest.mark.parametrize("hq,hkv,sq,sk,d,window", [
+    (2, 2, 300, 300, 128, (-1, 0)),     # right 0 alone: the causal block
+    (4, 2, 200, 517, 64, (-1, 70)),     # right only, sq < sk
+    (2, 1, 513, 400, 128, (33, 100)),   # both bounds, sk < sq: the first 13 rows keyless
+    (2, 2, 1100, 1100, 128, (64, 64)),  # symmetric band: whole key tiles skipped both sides
+    (4, 4, 96, 320, 40, (0, 5)),        # a narrow band at head dim 40
+])
+def test_block_right_window(hq, hkv, sq, sk, d, window):
+    """Non-causal blocks bounded on the right: the kernels run the causal mask with its
+    diagonal moved right by the bound."""
+    _block(False, hq, hkv, sq, sk, d, window)
 
 
 # ---- rings
@@ -145,16 +193,25 @@ def _check_ring(fn, ref_fn, world, L, hq=2, hkv=2, d=128, seed=0, what=""):
         assert_bf16_close(vd.grad[r], refs[2][r].grad, f"dv rank {r}", ulp_floor=hq != hkv)
 
 
-@pytest.mark.parametrize("causal,left", [(True, 150), (True, 40), (False, 300), (False, 700)])
-def test_allgather_ring_window(causal, left):
+@pytest.mark.parametrize("causal,left,right", [
+    (True, 150, 0), (True, 40, 0), (False, 300, -1), (False, 700, -1),
+    (False, 300, 0),    # non-causal, right 0: the band behind rank r's position (P-1) L + i
+    (False, 100, 200),  # both bounds: every block of a rank masked on its own side
+    (False, -1, 50),    # bounded on the right only
+])
+def test_allgather_ring_window(causal, left, right):
+    """The gather ring hands the window to one block call over the gathered keys
+    (ring/loop.py:218-228), so the block provider's (flash) window applies at the
+    bottom-right aligned positions."""
     from ringmaster_amd.ring import ring_attention
 
     world, L = 4, 128
+    w = (left, right)
     _check_ring(lambda q, k, v: ring_attention(q, k, v, causal=causal, rotate_method="allgather",
-                                               window=(left, 0)),
+                                               window=w),
                 lambda qs, ks, vs: rm.allgather_ring_forward(qs, ks, vs, causal=causal,
-                                                             window=(left, 0)),
-                world, L, hq=4, hkv=2, what=f"allgather causal={causal} window={left}")
+                                                             window=w, flash=True),
+                world, L, hq=4, hkv=2, what=f"allgather causal={causal} window={w}")
 
 
 def test_varlen_ring_window():

@@ -21,10 +21,11 @@ def rnd(*shape, seed, dtype=torch.float64):
     return torch.randn(*shape, generator=g, dtype=dtype)
 
 
-def brute_block(q, k, v, causal, scale, left=None):
+def brute_block(q, k, v, causal, scale, left=None, right=None):
     """Pure-Python loops over (b, h, i): softmax by its definition, fp64, over the keys
     j of row i that the causal rule (j <= i + sk - sq) and the window (i + sk - sq - j
-    <= left) leave."""
+    <= left, j - (i + sk - sq) <= right) leave; a row left without keys gets out 0 and
+    lse -inf."""
     b, sq, hq, d = q.shape
     sk, hkv = k.shape[1], k.shape[2]
     out = torch.zeros(b, sq, hq, d, dtype=torch.float64)
@@ -35,7 +36,11 @@ def brute_block(q, k, v, causal, scale, left=None):
             for i in range(sq):
                 pos = i + (sk - sq)
                 js = [j for j in range(sk) if ((not causal) or j <= pos)
-                      and (left is None or pos - j <= left)]
+                      and (left is None or pos - j <= left)
+                      and (right is None or j - pos <= right)]
+                if not js:
+                    lse[bi, h, i] = -math.inf
+                    continue
                 s = [float((q[bi, i, h] * k[bi, j, kh]).sum()) * scale for j in js]
                 m = max(s)
                 w = [math.exp(x - m) for x in s]
@@ -100,6 +105,62 @@ def test_math_block_window_special_cases():
     assert torch.allclose(lse.double(), 0.4 * (q * k).sum(-1).transpose(1, 2), atol=TOL32)
 
 
+# flash attention 2's window arguments, worked by hand from its published rules (a bound
+# of at least sk keys is -1; causal sets right 0; a -1 facing a bound >= 0 becomes sk):
+# (causal, sq, sk, window) -> (left, right) as math_block(flash=True) applies them
+_FLASH_BOUNDS = [
+    (False, 7, 7, (3, -1), (3, 7)),    # left only: right bounded at sk (no effect here)
+    (False, 7, 7, (-1, 2), (7, 2)),    # right only
+    (False, 7, 7, (2, 1), (2, 1)),     # a band around the diagonal
+    (True, 7, 7, (3, 5), (3, 0)),      # causal: right 0 whatever was asked
+    (True, 6, 9, (-1, -1), (9, 0)),    # causal, no window: plain causal
+    (False, 4, 9, (10, 3), (9, 3)),    # left >= sk is -1, then sk
+    (False, 9, 4, (2, -1), (2, 4)),    # sq > sk + 1: the right bound sk empties rows 0..2
+    (False, 9, 4, (1, 0), (1, 0)),     # non-causal (l, 0): causal band, rows 0..4 keyless
+    (False, 5, 5, (-1, -1), (None, None)),
+    (False, 5, 5, (6, 9), (None, None)),  # both bounds past sk: no window
+]
+
+
+@pytest.mark.parametrize("causal,sq,sk,window,bounds", _FLASH_BOUNDS)
+def test_flash_window_vs_brute_force(causal, sq, sk, window, bounds):
+    """The flash provider's window (ring/kernels.py:37-38 hands it to flash_attn_func):
+    the bounds against the hand-worked table, and the block against the row loop over the
+    keys they leave (rows left without keys: lse -inf, compared on the others)."""
+    assert rm.flash_window(window, causal, sk) == bounds
+    q, k, v = rnd(1, sq, 4, 8, seed=85), rnd(1, sk, 2, 8, seed=86), rnd(1, sk, 2, 8, seed=87)
+    out, lse = rm.math_block(q, k, v, causal=causal, scaling=None, window=window, flash=True)
+    ref_out, ref_lse = brute_block(q, k, v, causal, 1.0 / math.sqrt(8), *bounds)
+    rows = torch.isfinite(ref_lse[0, 0])
+    assert torch.isneginf(lse[:, :, ~rows]).all()
+    assert torch.allclose(out[:, rows].double(), ref_out[:, rows], atol=TOL32, rtol=TOL32)
+    assert torch.allclose(lse[:, :, rows].double(), ref_lse[:, :, rows], atol=TOL32, rtol=TOL32)
+
+
+def test_flash_window_special_cases():
+    """Where the flash window reduces to known forms: (l, -1) with sq <= sk is math_block's
+    window l; a non-causal (-1, 0) is the causal block; a causal call ignores the right
+    bound; a symmetric band (w, w) is SDPA with the band mask built from tril and triu."""
+    q, k, v = rnd(1, 6, 2, 8, seed=88), rnd(1, 9, 2, 8, seed=89), rnd(1, 9, 2, 8, seed=90)
+    for causal in (False, True):
+        a, la = rm.math_block(q, k, v, causal=causal, scaling=0.4, window=(2, -1), flash=True)
+        b, lb = rm.math_block(q, k, v, causal=causal, scaling=0.4, window=(2, 0))
+        assert torch.allclose(a, b, atol=TOL32) and torch.allclose(la, lb, atol=TOL32)
+    a, _ = rm.math_block(q, k, v, causal=False, scaling=0.4, window=(-1, 0), flash=True)
+    b, _ = rm.math_block(q, k, v, causal=True, scaling=0.4)
+    assert torch.allclose(a, b, atol=TOL32)
+    a, _ = rm.math_block(q, k, v, causal=True, scaling=0.4, window=(3, 4), flash=True)
+    b, _ = rm.math_block(q, k, v, causal=True, scaling=0.4, window=(3, 0))
+    assert torch.allclose(a, b, atol=TOL32)
+    w, sq, sk = 2, 6, 9
+    ones = torch.ones(sq, sk, dtype=torch.bool)
+    band = ones.tril(sk - sq + w) & ones.triu(sk - sq - w)
+    out, _ = rm.math_block(q, k, v, causal=False, scaling=0.4, window=(w, w), flash=True)
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                         attn_mask=band, scale=0.4)
+    assert torch.allclose(out.double(), ref.transpose(1, 2), atol=TOL32)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_allgather_ring_window_positions(causal):
     """The gather ring's one block per rank (ring/loop.py:201-228): causal, rank r's
@@ -125,6 +186,24 @@ def test_allgather_ring_window_positions(causal):
             ref_o, ref_l = brute_block(qs[r].transpose(1, 2), kf, vf, False, sc, left)
             assert torch.allclose(outs[r].double(), ref_o, atol=TOL32)
             assert torch.allclose(lses[r].double(), ref_l, atol=TOL32)
+
+
+def test_allgather_ring_flash_window_positions():
+    """The gather ring with the flash provider's window, non-causal: rank r's queries at
+    (P - 1) L + i against every gathered key, bounded on both sides (brute force)."""
+    P, L, left, right = 3, 4, 5, 2
+    qs = [rnd(1, 2, L, 8, seed=91 + r) for r in range(P)]
+    ks = [rnd(1, 1, L, 8, seed=94 + r) for r in range(P)]
+    vs = [rnd(1, 1, L, 8, seed=97 + r) for r in range(P)]
+    outs, lses = rm.allgather_ring_forward(qs, ks, vs, causal=False, scaling=None,
+                                           window=(left, right), flash=True)
+    kf = torch.cat([t.transpose(1, 2) for t in ks], 1)
+    vf = torch.cat([t.transpose(1, 2) for t in vs], 1)
+    for r in range(P):
+        ref_o, ref_l = brute_block(qs[r].transpose(1, 2), kf, vf, False, 1.0 / math.sqrt(8),
+                                   left, right)
+        assert torch.allclose(outs[r].double(), ref_o, atol=TOL32)
+        assert torch.allclose(lses[r].double(), ref_l, atol=TOL32)
 
 
 def test_varlen_ring_window_equals_per_document():
