@@ -35,7 +35,11 @@ COMMON_FLAGS = ["-O3", "-std=c++20", "-fPIC", f"--offload-arch={ARCH}", "-Wall",
 # AGPR-copy rewrite still places the operands pinned to AGPRs there. The head-dim-256
 # backward (attn_bwd) keeps the compiler's choice: its dK and dV accumulators fill the
 # AGPRs, and there its dQ kernel measured 15% faster than with VGPR-form MFMAs.
-UNIT_FLAGS = {"attn_bwd_vf": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# attn_fwd: VGPR-form MFMAs change only the head-dim-256 forward (59-65 AGPRs in use
+# against 147; the 64 and 128 code is identical), whose configs[1]-shaped step measured
+# 0.8% faster.
+_VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+UNIT_FLAGS = {"attn_bwd_vf": _VGPR_FORM, "attn_fwd": _VGPR_FORM}
 
 
 def _sources():

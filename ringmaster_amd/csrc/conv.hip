@@ -8,9 +8,10 @@
 //   y[g] = act(z[g]),  act = identity or silu
 // (causal_conv1d_fn's published semantics: a depthwise conv1d with W-1 zeros of
 // left padding). HBM-bound: a thread owns runs of 8 consecutive tokens of one
-// (shard, batch, channel) row and reads each with the 8 before as 16-byte loads;
-// a workgroup covers consecutive runs of one row, so the row's coordinates,
-// weights and bias are scalar.
+// (shard, batch, channel) row and reads each as a 16-byte load, with the halo tokens
+// before it from the lane below (forward) or the chunks either side (backward); a
+// workgroup covers consecutive runs of one row, so the row's coordinates, weights and bias
+// are scalar.
 #include "rmx_kernels.h"
 
 namespace rmx {
@@ -107,20 +108,53 @@ __device__ __forceinline__ void chunk(const ConvArgs& a, const uint16_t* base, c
   }
 }
 
+// Forward: the W-1 tokens before a run are the last tokens of the run of the lane below
+// (a wave's runs are consecutive runs of one row). They pass between lanes by shuffles;
+// only the wave's first lane loads the previous chunk, issued with the run's own loads
+// (one memory round trip), so every chunk is read once from the L2 instead of twice, and
+// y leaves by non-temporal stores: 0.235-0.24 against 0.26-0.27 ms at configs[4]. The
+// backward's form of it (the previous and next chunks of x and the next of dy shuffled,
+// the wave's edge lanes loading theirs) measured 0.59 against 0.45 ms and was not kept.
+// v[0..7] := the previous chunk: its last W-1 tokens from the lane below, all of it from
+// pv (the loaded chunk) on the wave's first lane
+template <int W, bool DOC>
+__device__ __forceinline__ void halo_prev(const float* pv, const int* pd, float* v, int* d) {
+  const bool first = (threadIdx.x & 63) == 0;
+#pragma unroll
+  for (int i = 9 - W; i < 8; ++i) {
+    const float x = __shfl_up(v[8 + i], 1, 64);
+    v[i] = first ? pv[i] : x;
+    if (DOC) {
+      const int id = __shfl_up(d[8 + i], 1, 64);
+      d[i] = first ? pd[i] : id;
+    }
+  }
+}
 template <int W, bool DOC>
 __global__ __launch_bounds__(256) void causal_conv1d_fwd_kernel(const ConvArgs a) {
   constexpr int R = kConvRunsFwd;
-  float xv[R][16];
-  int dv[R][16];
+  const bool first = (threadIdx.x & 63) == 0;
+  float xv[R][16], pv[R][8];
+  int dv[R][16], pd[R][8];
   ConvRun rr[R];
 #pragma unroll
   for (int k = 0; k < R; ++k) {
     rr[k] = conv_run<R>(a, k);
-    if (rr[k].valid) {
-      chunk<DOC>(a, a.x, rr[k], -1, xv[k], dv[k]);
-      chunk<DOC>(a, a.x, rr[k], 0, xv[k] + 8, dv[k] + 8);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      xv[k][i] = 0.f;
+      dv[k][i] = 0;
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pv[k][i] = 0.f;
+      pd[k][i] = 0;
+    }
+    if (rr[k].valid) chunk<DOC>(a, a.x, rr[k], 0, xv[k] + 8, dv[k] + 8);
+    if (first && rr[k].valid) chunk<DOC>(a, a.x, rr[k], -1, pv[k], pd[k]);
   }
+#pragma unroll
+  for (int k = 0; k < R; ++k) halo_prev<W, DOC>(pv[k], pd[k], xv[k], dv[k]);
   const int c = rr[0].c;
   float w[W];
 #pragma unroll
@@ -144,7 +178,7 @@ __global__ __launch_bounds__(256) void causal_conv1d_fwd_kernel(const ConvArgs a
     u32x4 o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = pack_bf2(y[2 * i], y[2 * i + 1]);
-    *reinterpret_cast<u32x4*>(a.y + rr[k].rowoff + rr[k].t0) = o;
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(a.y + rr[k].rowoff + rr[k].t0));
   }
 }
 
