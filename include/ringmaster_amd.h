@@ -340,7 +340,7 @@ int32_t rmx_mamba2_cp_correction(const uint16_t* out, uint16_t* y, const float* 
  * as in the forward. Outputs: gC bf16 like C, g_cumA fp32 like cum_A, g_hprev
  * fp32 like h_prev. workspace: device memory of at least
  * rmx_mamba2_cp_correction_bwd_workspace(...) bytes (block partials of dL/dh_prev,
- * h_prev^T split into bf16 hi/lo, e^{cum_A} transposed); its contents on entry
+ * h_prev^T split into three bf16 parts, e^{cum_A} transposed); its contents on entry
  * do not matter. head_dim in {64, 128}; d_state in {64, 128}; the head slices
  * of 64 channels come in fours from one C group ((nheads / ngroups) divisible by
  * 4 at head_dim 64, by 2 at head_dim 128); otherwise RMX_EUNSUPPORTED.

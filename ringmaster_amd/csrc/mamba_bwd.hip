@@ -10,17 +10,23 @@
 //   dH_in[h,d,n] = sum_t e[t,h] G[t,h,d] C[t,g(h),n]
 //                  + [state updated] exp(cumA[T-1,h]) Gs[h,d,n]
 // (dout = G and dh_final = Gs pass through; the state is updated unless a batch
-// row's last token starts a fresh sequence, :131). Four launches:
-//  1. prep: H_in^T split into bf16 hi + lo ([B,H,n,d]) and e transposed to [B,H,T];
-//  2. unit kernel: per head slice of 64 channels walking a token block, S on MFMA
-//     (H_in hi/lo from registers, as in the forward), dcumA, and the block's
+// row's last token starts a fresh sequence, :131). With P[t,h,n] = sum_d G[t,h,d]
+// H_in[h,d,n], both dC and the sum in dcumA are contractions of P:
+//   dC[t,g,n] = sum_{h in g} e[t,h] P[t,h,n],  sum_d G S = sum_n C[t,g(h),n] P[t,h,n].
+// Four launches:
+//  1. prep: H_in^T split into three bf16 parts hi + mid + lo ([B,H,n,d]) and e
+//     transposed to [B,H,T];
+//  2. unit kernel: per head slice of 64 channels walking a token block, the block's
 //     dH_in partial (G e split into bf16 hi + lo, times C) on MFMA;
-//  3. reduce: dH_in = sum of the block partials + the state term, and the state
-//     term of dcumA;
-//  4. dC kernel: per 256-token tile of one group, all heads' G H_in^T products
-//     on MFMA (H_in^T hi/lo staged per 64-channel chunk in LDS), scaled by e.
+//  3. dC kernel: per 256-token tile of one group, every head's P^T = H_in^T G^T on
+//     MFMA (the three parts of H_in^T staged per 64-channel chunk in LDS), dC += e P
+//     and dcumA = e sum_n C P (C of the tile's tokens in registers);
+//  4. reduce: dH_in = sum of the block partials + the state term, and the state
+//     term of dcumA.
 // Every fp32 result is formed from exact bf16 x bf16 products with fp32
-// accumulation (the hi/lo splits carry ~16 mantissa bits of the fp32 factors).
+// accumulation (the hi/lo splits carry ~16 mantissa bits of the fp32 factors, three
+// parts ~24: dcumA contracts P against C once more, and a two-part residual of 2^-18
+// times that cancellation would miss 1e-4).
 #include <mutex>
 #include <type_traits>
 
@@ -40,13 +46,14 @@ struct MambaBwdArgs {
   float* g_hprev;
   float* part;      // [ntb][B][H][d][n] dH_in partials of the unit kernel's token blocks
   uint16_t* ht_hi;  // [B][H][n][d]
+  uint16_t* ht_mid;
   uint16_t* ht_lo;
   float* eT;        // [B][H][T]
   int batch, T, nheads, head_dim, ngroups, d_state, ntb;
 };
 
 constexpr int kMambaBwdTokensPerWg = 4096;  // unit kernel token block
-constexpr int kMambaBwdCTokens = 256;       // dC kernel token tile (4 waves x 64)
+constexpr int kMambaBwdCTokens = 256;       // dC kernel token tile (8 waves x 32)
 
 // Chunk swizzle for LDS tiles read both row-wise (8 consecutive rows, one
 // 16-byte chunk each) and by ds_read_b64_tr_b16 (4 consecutive rows, one
@@ -87,7 +94,7 @@ __device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
 }
 
 // ---------------------------------------------------------------------------
-// 1. prep: grid (H, B), 256 threads. H_in[b,h] ([d][n] fp32) -> [n][d] bf16 hi/lo
+// 1. prep: grid (H, B), 256 threads. H_in[b,h] ([d][n] fp32) -> [n][d] bf16 hi, mid, lo
 // through LDS, and eT[b,h,:] = mask * exp(cumA[b,:,h]).
 template <int HD, int N>
 __global__ __launch_bounds__(256) void mamba2_bwd_prep_kernel(const MambaBwdArgs a) {
@@ -97,15 +104,24 @@ __global__ __launch_bounds__(256) void mamba2_bwd_prep_kernel(const MambaBwdArgs
   const int64_t hb = ((int64_t)bb * H + h) * HD * N;
   for (int i = tid; i < HD * N; i += 256) st[i / N][i % N] = a.h_prev[hb + i];
   __syncthreads();
-  // thread -> (n, 8 consecutive d): 16-byte hi and lo stores
+  // thread -> (n, 8 consecutive d): 16-byte hi, mid and lo stores
   for (int i = tid; i < N * (HD / 8); i += 256) {
     const int n = i / (HD / 8), d0 = 8 * (i % (HD / 8));
-    float v[8];
+    float v[8], r[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = st[d0 + k][n];
-    bf16x8 hi, lo;
-    split8(v, hi, lo);
+    bf16x8 hi, mid, lo, unused;
+    split8(v, hi, mid);
+    const u32x4 h4 = __builtin_bit_cast(u32x4, hi), m4 = __builtin_bit_cast(u32x4, mid);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      r[2 * k] = v[2 * k] - __uint_as_float(h4[k] << 16) - __uint_as_float(m4[k] << 16);
+      r[2 * k + 1] = v[2 * k + 1] - __uint_as_float(h4[k] & 0xffff0000u) -
+                     __uint_as_float(m4[k] & 0xffff0000u);
+    }
+    split8(r, lo, unused);
     *reinterpret_cast<bf16x8*>(a.ht_hi + hb + (int64_t)n * HD + d0) = hi;
+    *reinterpret_cast<bf16x8*>(a.ht_mid + hb + (int64_t)n * HD + d0) = mid;
     *reinterpret_cast<bf16x8*>(a.ht_lo + hb + (int64_t)n * HD + d0) = lo;
   }
   float* et = a.eT + ((int64_t)bb * H + h) * T;
@@ -121,11 +137,6 @@ __global__ __launch_bounds__(256) void mamba2_bwd_prep_kernel(const MambaBwdArgs
 // 128: half a head); a workgroup holds 4 units of heads in one C group and
 // walks kMambaBwdTokensPerWg tokens, 32 per step, with the forward's DMA rings
 // (C and aux shared, G per wave, two steps ahead). Per wave and step:
-//   S^T (64 ch x 32 tok) = H_in C^T        48 MFMAs: H_in = hi + mid + lo, three
-//       bf16 parts (residual ~2^-27: dcumA contracts S against G once more, so the
-//       forward's two-part split would leave ~2^-18 x a cancellation factor);
-//       hi and mid in registers, lo re-read from this wave's LDS every step
-//   dcumA[t] = e[t] sum_d G[t,d] S[t,d]    (lane = token; one cross-half add)
 //   dH^T partial (64 ch x N) += (G e)^T C  4 N/32 MFMAs per 16 tokens: A = G^T e
 //       split into hi/lo (transposed reads of the G stage), B = C (transposed
 //       reads of the C stage)
@@ -133,32 +144,26 @@ __global__ __launch_bounds__(256) void mamba2_bwd_prep_kernel(const MambaBwdArgs
 // whole walk: one wave per SIMD, accumulators in AGPRs.
 template <int N>
 struct MambaBwdUnitCfg {
-  static constexpr int SL = 64, NDB = 2, NS = N / 16, CHC = N / 8, CHO = 8, NI = 4, NB = N / 32;
+  static constexpr int SL = 64, NDB = 2, CHC = N / 8, CHO = 8, NI = 4, NB = N / 32;
   static constexpr int ND = N / 64;            // C DMA instructions per wave and step
   static constexpr int CS = 32 * N * 2;        // C stage bytes (= ND * 4 KB)
   static constexpr int OS = 32 * SL * 2;       // G stage bytes per wave
   static constexpr int XS = 2 * 4 * 256;       // cum_A + seq_idx stage
   static constexpr int NDMA = ND + NI + 2;
   static constexpr int EW = 4 * 32 * 4;        // e of the step's tokens, per wave
-  static constexpr int RING = 3 * CS + 4 * 3 * OS + 3 * XS + EW;
-  static constexpr int HSCR = 4 * 32 * N * 4;  // H_in transpose scratch
-  static constexpr int H3 = 64 * N * 2;        // third bf16 part of H_in, per wave
-  static constexpr int LDS = (RING > HSCR ? RING : HSCR) + 4 * H3;
+  static constexpr int LDS = 3 * CS + 4 * 3 * OS + 3 * XS + EW;
 };
 
 template <int N>
 __global__ __launch_bounds__(256, 1) void mamba2_bwd_unit_kernel(const MambaBwdArgs a, const int nug) {
   using F = MambaBwdUnitCfg<N>;
-  constexpr int SL = F::SL, NDB = F::NDB, NS = F::NS, CHC = F::CHC, CHO = F::CHO, NI = F::NI;
+  constexpr int SL = F::SL, NDB = F::NDB, CHC = F::CHC, CHO = F::CHO, NI = F::NI;
   constexpr int NB = F::NB, ND = F::ND, CS = F::CS, OS = F::OS, XS = F::XS;
   __shared__ __attribute__((aligned(16))) uint8_t smem[F::LDS];
   uint8_t* const sC = smem;
   uint8_t* const sO = smem + 3 * CS;
   uint8_t* const sX = sO + 4 * 3 * OS;
   float* const sE = reinterpret_cast<float*>(sX + 3 * XS);  // [4 waves][32]
-  constexpr int RS = F::RING > F::HSCR ? F::RING : F::HSCR;
-  // third part of H_in: [64 rows][N] bf16 per wave, 16-byte chunks swizzled by swz_row
-  uint16_t* const sH3 = reinterpret_cast<uint16_t*>(smem + RS);
 
   const int ntb = a.ntb;
   int id = blockIdx.x;
@@ -176,49 +181,6 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_unit_kernel(const MambaBwdA
   const int tend = tbeg + kMambaBwdTokensPerWg < T ? tbeg + kMambaBwdTokensPerWg : T;
   const int nstep = (tend - tbeg + 31) / 32;
   const int64_t HHD = (int64_t)H * HD;
-  const int64_t hbase = (((int64_t)bb * H + h) * HD + (int64_t)sl * SL) * N;
-
-  // ---- H_in -> registers (hi, mid; coalesced loads, LDS transpose as in the
-  // forward) and this wave's LDS (lo)
-  bf16x8 ahi[NDB][NS], alo[NDB][NS];
-  uint16_t* const h3w = sH3 + wave * (64 * N);
-  {
-    uint16_t* const shi = reinterpret_cast<uint16_t*>(smem + wave * (32 * N * 4));
-    uint16_t* const slo = shi + 32 * N;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int64_t blk = hbase + (int64_t)32 * db * N;
-      f32x4 xs[N / 8];
-#pragma unroll
-      for (int q = 0; q < N / 8; ++q)
-        xs[q] = *reinterpret_cast<const f32x4*>(a.h_prev + blk + 4 * (64 * q + lane));
-#pragma unroll
-      for (int q = 0; q < N / 8; ++q) {
-        const int p = 64 * q + lane, row = p / (N / 4), n0 = 4 * (p % (N / 4));
-        u32x2 hi, lo, l3;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const float x0 = xs[q][2 * i], x1 = xs[q][2 * i + 1];
-          hi[i] = cvt_pk_bf16(x0, x1);
-          const float r0 = x0 - __uint_as_float(hi[i] << 16), r1 = x1 - __uint_as_float(hi[i] & 0xffff0000u);
-          lo[i] = cvt_pk_bf16(r0, r1);
-          l3[i] = cvt_pk_bf16(r0 - __uint_as_float(lo[i] << 16), r1 - __uint_as_float(lo[i] & 0xffff0000u));
-        }
-        const int off = row * N + 8 * ((n0 >> 3) ^ (swz_row(row) & (CHC - 1))) + (n0 & 4);
-        *reinterpret_cast<u32x2*>(shi + off) = hi;
-        *reinterpret_cast<u32x2*>(slo + off) = lo;
-        *reinterpret_cast<u32x2*>(h3w + 32 * db * N + off) = l3;
-      }
-      const int arow = sigma(l32);
-#pragma unroll
-      for (int ks = 0; ks < NS; ++ks) {
-        const int off = arow * N + 8 * ((2 * ks + hl) ^ (swz_row(arow) & (CHC - 1)));
-        ahi[db][ks] = *reinterpret_cast<const bf16x8*>(shi + off);
-        alo[db][ks] = *reinterpret_cast<const bf16x8*>(slo + off);
-      }
-    }
-  }
-  lds_barrier();
 
   const int cstride = G * N * 2, ostride = (int)(HHD * 2);
   const uint32_t cspan = span_bytes(T, cstride, N * 2), aspan = (uint32_t)T * (uint32_t)H * 4u;
@@ -258,18 +220,11 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_unit_kernel(const MambaBwdA
 
   issue(0, tbeg);
   if (nstep > 1) issue(1, tbeg + 32);
-  // vmcnt budget at the top of step s: what was issued after step s's DMA (the
-  // dcumA stores of steps s-2 and s-1, one per wave and step, and step s+1's DMA)
-  constexpr int K0 = F::NDMA, K1 = F::NDMA + 1, KS = F::NDMA + 2;
-  float* const gca_row = a.g_cumA + (int64_t)bb * T * H + h;
   float* const ew = sE + 32 * wave;
   for (int s = 0; s < nstep; ++s) {
-    if (s >= 2 && s + 1 < nstep)
-      wait_vm_barrier<KS>();
-    else if (s == 1 && nstep > 2)
-      wait_vm_barrier<K1>();
-    else if (s == 0 && nstep > 1)
-      wait_vm_barrier<K0>();
+    // at the top of step s, only step s + 1's DMA was issued after step s's
+    if (s + 1 < nstep)
+      wait_vm_barrier<F::NDMA>();
     else
       wait_vm_barrier<0>();
     if (s + 2 < nstep) issue((s + 2) % 3, tbeg + 32 * (s + 2));
@@ -277,26 +232,6 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_unit_kernel(const MambaBwdA
     const uint8_t* cst = sC + st * CS;
     const uint8_t* ost = sO + (wave * 3 + st) * OS;
 
-    // S^T = H_in C^T
-    f32x16 acc[NDB];
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) acc[db] = zero16();
-    const int arow = sigma(l32);
-#pragma unroll
-    for (int ks = 0; ks < NS; ++ks) {
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(cst + l32 * (CHC * 16) +
-                                                        16 * ((2 * ks + hl) ^ swz_pair(l32)));
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) acc[db] = mfma32(ahi[db][ks], b, acc[db]);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) acc[db] = mfma32(alo[db][ks], b, acc[db]);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(
-            h3w + (32 * db + arow) * N + 8 * ((2 * ks + hl) ^ (swz_row(arow) & (CHC - 1))));
-        acc[db] = mfma32(a3, b, acc[db]);
-      }
-    }
     // e of token l32 (0 past the block end: those rows belong to the next block)
     const uint8_t* xst = sX + st * XS;
     const float ca = reinterpret_cast<const float*>(xst)[64 * (l32 >> 3) + (l32 & 7) * hpw + hw];
@@ -304,29 +239,6 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_unit_kernel(const MambaBwdA
     const bool live = t0 + l32 < tend;
     const float e = (sq != 0 || !live) ? 0.f : expf(ca);
     if (hl == 0) ew[l32] = e;
-
-    // dcumA: lane (hl, l32) reg r of block db = channel 32 db + 16 (r / 8) + 8 hl + r % 8
-    float dot = 0.f;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int c = 4 * db + 2 * half + hl;
-        const u32x4 gv = *reinterpret_cast<const u32x4*>(ost + 16 * (l32 * CHO + (c ^ swz_pair(l32))));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          dot += __uint_as_float(gv[i] << 16) * acc[db][8 * half + 2 * i];
-          dot += __uint_as_float(gv[i] & 0xffff0000u) * acc[db][8 * half + 2 * i + 1];
-        }
-      }
-    dot += xhalf(dot);
-    if (hl == 0 && live) {
-      float* dst = gca_row + (int64_t)(t0 + l32) * H;
-      if (uph == 1)
-        *dst = e * dot;
-      else
-        unsafeAtomicAdd(dst, e * dot);  // hardware fp32 add; two addends per element: order-free
-    }
 
     // dH^T += (G e)^T C over the step's 32 tokens (two k-steps of 16)
 #pragma unroll
@@ -371,9 +283,9 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_unit_kernel(const MambaBwdA
 }
 
 // ---------------------------------------------------------------------------
-// 3. reduce: grid (H, B), 256 threads. dH_in = sum of the block partials
+// 4. reduce: grid (H, B), 256 threads. dH_in = sum of the block partials
 // (+ exp(cumA[T-1]) Gs when the state is updated), and the state's term of
-// dcumA[T-1] = exp(cumA[T-1]) sum Gs H_in (added after the unit kernel).
+// dcumA[T-1] = exp(cumA[T-1]) sum Gs H_in (added after the dC kernel).
 template <int HD, int N>
 __global__ __launch_bounds__(256) void mamba2_bwd_reduce_kernel(const MambaBwdArgs a) {
   __shared__ float red[4];
@@ -408,33 +320,36 @@ __global__ __launch_bounds__(256) void mamba2_bwd_reduce_kernel(const MambaBwdAr
 }
 
 // ---------------------------------------------------------------------------
-// 4. dC kernel: one workgroup = 4 waves x 64 tokens of one (batch, group); the
-// contraction runs over the group's (head, channel) pairs in chunks of 64
+// 3. dC kernel: one workgroup = 8 waves (two per SIMD) x 32 tokens of one (batch,
+// group); the contraction runs over the group's (head, channel) pairs in chunks of 64
 // channels (one head at head_dim 64, half a head at 128). Per chunk and wave:
-//   P^T (N x 64 tok) = H_in^T G^T   A = H_in^T rows (hi and lo, LDS, sigma-
-//                                    permuted), B = G rows (LDS)   4 N/32 MFMAs
+//   P^T (N x 32 tok) = H_in^T G^T   A = H_in^T rows (hi, mid and lo, LDS, sigma-
+//                                    permuted), B = G rows (LDS)   3 N/32 MFMAs per
+//                                    k-step of 16 channels
 //   dC^T += e P^T                   (lane = token: one e per lane and chunk)
-// The next chunk's H_in^T (shared) and G (per wave) tiles load by DMA during
-// the current one; e comes from the transposed eT rows.
+//   q    += sum_n C P               (C of the lane's token and rows, registers)
+// and after a head's last chunk dcumA[t,h] = e q (both lane halves' rows). The next
+// chunk's H_in^T (shared) and G (per wave) tiles load by DMA during the current one,
+// its e (from the transposed eT rows) into registers.
 template <int N>
 struct MambaBwdCCfg {
+  static constexpr int NW = 8;                 // waves, 32 tokens each
   static constexpr int NB = N / 32, CH = 8;    // 64 channels = 8 chunks per row
-  static constexpr int HS = 2 * N * 128;       // H_in^T chunk stage: hi + lo, N rows x 128 B
-  static constexpr int GS = 64 * 128;          // G chunk stage per wave: 64 tokens x 128 B
-  static constexpr int ES = 4 * 256;           // e of the 256 tokens
-  static constexpr int NDH = HS / 4096;        // H DMA instructions per wave (4 waves x 1 KB)
-  static constexpr int NDMA = NDH + 8 + 1;     // + G (8 KB per wave) + e
-  static constexpr int LDS = 2 * HS + 4 * 2 * GS + 2 * ES;
+  static constexpr int HS = 3 * N * 128;       // H_in^T chunk stage: hi, mid, lo, N rows x 128 B
+  static constexpr int GS = 32 * 128;          // G chunk stage per wave: 32 tokens x 128 B
+  static constexpr int NDH = HS / (1024 * NW); // H DMA instructions per wave
+  static constexpr int LDS = 2 * HS + NW * 2 * GS;
+  static_assert(HS % (1024 * NW) == 0 && (N * CH / 64) % NW == 0,
+                "a plane is whole DMA instructions of every wave");
 };
 
 template <int N>
-__global__ __launch_bounds__(256, 1) void mamba2_bwd_c_kernel(const MambaBwdArgs a, const int ntt) {
+__global__ __launch_bounds__(512, 1) void mamba2_bwd_c_kernel(const MambaBwdArgs a, const int ntt) {
   using F = MambaBwdCCfg<N>;
-  constexpr int NB = F::NB, CH = F::CH, HS = F::HS, GS = F::GS, ES = F::ES, NDH = F::NDH;
+  constexpr int NW = F::NW, NB = F::NB, CH = F::CH, HS = F::HS, GS = F::GS, NDH = F::NDH;
   __shared__ __attribute__((aligned(16))) uint8_t smem[F::LDS];
-  uint8_t* const sH = smem;                 // [2][HS]: hi [N][64] then lo [N][64]
-  uint8_t* const sG = smem + 2 * HS;        // [4 waves][2][GS]
-  uint8_t* const sEt = sG + 4 * 2 * GS;     // [2][ES]
+  uint8_t* const sH = smem;                 // [2][HS]: hi [N][64], mid, lo
+  uint8_t* const sG = smem + 2 * HS;        // [NW waves][2][GS]
 
   int id = blockIdx.x;
   const int nwg = gridDim.x;
@@ -446,91 +361,106 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_c_kernel(const MambaBwdArgs
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int t0 = tt * kMambaBwdCTokens;
+  const int t = t0 + 32 * wave + l32;  // this lane's token
   const int64_t HHD = (int64_t)H * HD;
   const int ostride = (int)(HHD * 2);
 
   const i32x4 rG = make_rsrc(a.gy + (int64_t)bb * T * HHD, span_bytes(T, ostride, (int)(HHD * 2)));
-  const uint32_t ldsH = lds_addr(sH), ldsG = lds_addr(sG + wave * 2 * GS), ldsE = lds_addr(sEt);
+  const uint32_t ldsH = lds_addr(sH), ldsG = lds_addr(sG + wave * 2 * GS);
   // chunk j: head hg = g * hpg + j / cph, channels 64 (j % cph) .. + 63
   auto issue = [&](int st, int j) __attribute__((always_inline)) {
     const int hg = g * hpg + j / cph, c0 = 64 * (j % cph);
-    const uint16_t* hhi = a.ht_hi + ((int64_t)bb * H + hg) * N * HD + c0;
-    const uint16_t* hlo = a.ht_lo + ((int64_t)bb * H + hg) * N * HD + c0;
-    const i32x4 rh = make_rsrc(hhi, span_bytes(N, HD * 2, 128));
-    const i32x4 rl = make_rsrc(hlo, span_bytes(N, HD * 2, 128));
+    const int64_t ho = ((int64_t)bb * H + hg) * N * HD + c0;
+    const i32x4 rh = make_rsrc(a.ht_hi + ho, span_bytes(N, HD * 2, 128));
+    const i32x4 rm = make_rsrc(a.ht_mid + ho, span_bytes(N, HD * 2, 128));
+    const i32x4 rl = make_rsrc(a.ht_lo + ho, span_bytes(N, HD * 2, 128));
 #pragma unroll
     for (int i = 0; i < NDH; ++i) {
-      const int p = (i * 4 + wave) * 64 + lane;      // 16-byte slot of the stage
-      const bool lo = (i * 4 + wave) * 64 >= N * CH;  // second half of the stage: lo plane
-      const int q = lo ? p - N * CH : p, row = q / CH, pc = q % CH;
+      const int n = i * NW + wave;                 // 1 KB DMA instruction of the stage
+      const int plane = n * 64 / (N * CH);         // one plane per instruction
+      const int q = n * 64 + lane - plane * N * CH, row = q / CH, pc = q % CH;
       const int off = row * (HD * 2) + 16 * (pc ^ swz_row(row));
-      // one resource per instruction: the planes split at an instruction boundary
-      dma16_async(lo ? rl : rh, ldsH + st * HS + (i * 4 + wave) * 1024, off);
+      dma16_async(plane == 0 ? rh : (plane == 1 ? rm : rl), ldsH + st * HS + n * 1024, off);
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < GS / 1024; ++k) {
       const int p = 64 * k + lane, row = p / CH, pc = p % CH;
       dma16_async(rG, ldsG + st * GS + 1024 * k,
-                  (t0 + 64 * wave + row) * ostride + 2 * (hg * HD + c0) + 16 * (pc ^ (row & 7)));
+                  (t0 + 32 * wave + row) * ostride + 2 * (hg * HD + c0) + 16 * (pc ^ (row & 7)));
     }
-    const i32x4 re = make_rsrc(a.eT + ((int64_t)bb * H + hg) * T, (uint32_t)T * 4u);
-    dma4_async(re, ldsE + st * ES + 256 * wave, (t0 + 64 * wave + lane) * 4);
+  };
+  // e of the lane's token for the head of chunk j (0 past the sequence end)
+  auto load_e = [&](int j) __attribute__((always_inline)) -> float {
+    const float* et = a.eT + ((int64_t)bb * H + g * hpg + j / cph) * T;
+    return t < T ? et[t] : 0.f;
   };
 
-  f32x16 acc[2][NB];  // dC^T: [token block][n block]
+  // C of the lane's P rows n = 32 nb + 16 half + 8 hl .. + 7
+  u32x4 cv[NB][2];
+  {
+    const uint16_t* crow = a.C + (((int64_t)bb * T + (t < T ? t : 0)) * a.ngroups + g) * N + 8 * hl;
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[cb][nb] = zero16();
+      for (int half = 0; half < 2; ++half)
+        cv[nb][half] = t < T ? *reinterpret_cast<const u32x4*>(crow + 32 * nb + 16 * half) : u32x4{};
+  }
+
+  f32x16 acc[NB];  // dC^T: [n block]
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = zero16();
+  float q = 0.f;
 
   issue(0, 0);
+  float ecur = load_e(0), enext = 0.f;
   const int arow = sigma(l32);
   for (int j = 0; j < nchunk; ++j) {
     wait_vm_barrier<0>();
-    if (j + 1 < nchunk) issue((j + 1) & 1, j + 1);
+    if (j + 1 < nchunk) {
+      issue((j + 1) & 1, j + 1);
+      enext = load_e(j + 1);
+    }
     const uint8_t* hst = sH + (j & 1) * HS;
     const uint8_t* gst = sG + (wave * 2 + (j & 1)) * GS;
-    const float* est = reinterpret_cast<const float*>(sEt + (j & 1) * ES) + 64 * wave;
-    f32x16 p[2][NB];
+    f32x16 p[NB];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) p[cb][nb] = zero16();
+    for (int nb = 0; nb < NB; ++nb) p[nb] = zero16();
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      bf16x8 gb[2];
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const int row = 32 * cb + l32;
-        gb[cb] = *reinterpret_cast<const bf16x8*>(gst + row * 128 + 16 * ((2 * ks + hl) ^ (row & 7)));
-      }
+      const bf16x8 gb =
+          *reinterpret_cast<const bf16x8*>(gst + l32 * 128 + 16 * ((2 * ks + hl) ^ (l32 & 7)));
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const int row = 32 * nb + arow;
         const int off = row * 128 + 16 * ((2 * ks + hl) ^ swz_row(row));
-        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(hst + off);
-        const bf16x8 al = *reinterpret_cast<const bf16x8*>(hst + N * 128 + off);
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          p[cb][nb] = mfma32(ah, gb[cb], p[cb][nb]);
-          p[cb][nb] = mfma32(al, gb[cb], p[cb][nb]);
-        }
+        for (int part = 0; part < 3; ++part)
+          p[nb] = mfma32(*reinterpret_cast<const bf16x8*>(hst + part * N * 128 + off), gb, p[nb]);
       }
     }
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const float e = est[32 * cb + l32];
+    for (int nb = 0; nb < NB; ++nb) {
+      acc[nb] += ecur * p[nb];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[cb][nb] += e * p[cb][nb];
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t c2 = cv[nb][half][w];
+          q = fmaf(__uint_as_float(c2 << 16), p[nb][8 * half + 2 * w], q);
+          q = fmaf(__uint_as_float(c2 & 0xffff0000u), p[nb][8 * half + 2 * w + 1], q);
+        }
     }
+    if (j % cph == cph - 1) {  // the head's last chunk: dcumA of its tokens
+      const float tot = q + xhalf(q);
+      if (hl == 0 && t < T) a.g_cumA[((int64_t)bb * T + t) * H + g * hpg + j / cph] = ecur * tot;
+      q = 0.f;
+    }
+    ecur = enext;
   }
 
-  // dC[b, t, g, n]: lane (hl, l32) reg r of (cb, nb) = token 64 wave + 32 cb + l32,
+  // dC[b, t, g, n]: lane (hl, l32) reg r of nb = token 32 wave + l32,
   // n = 32 nb + 16 (r / 8) + 8 hl + r % 8 (sigma-permuted A rows)
-#pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    const int t = t0 + 64 * wave + 32 * cb + l32;
-    if (t >= T) continue;
+  if (t < T) {
     uint16_t* dst = a.gC + (((int64_t)bb * T + t) * a.ngroups + g) * N + 8 * hl;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -538,15 +468,10 @@ __global__ __launch_bounds__(256, 1) void mamba2_bwd_c_kernel(const MambaBwdArgs
       for (int half = 0; half < 2; ++half) {
         float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = acc[cb][nb][8 * half + i];
+        for (int i = 0; i < 8; ++i) v[i] = acc[nb][8 * half + i];
         *reinterpret_cast<bf16x8*>(dst + 32 * nb + 16 * half) = pack8_hw(v);
       }
   }
-}
-
-__global__ void mamba2_bwd_zero_kernel(float* p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -584,7 +509,7 @@ hipError_t mamba2_bwd_scratch(void** out) {
 size_t mamba2_bwd_workspace(int batch, int T, int nheads, int head_dim, int d_state) {
   const size_t state = (size_t)batch * nheads * head_dim * d_state;
   const size_t ntb = (size_t)((T + kMambaBwdTokensPerWg - 1) / kMambaBwdTokensPerWg);
-  return ntb * state * 4 + 2 * state * 2 + (size_t)batch * nheads * T * 4 + 256;
+  return ntb * state * 4 + 3 * state * 2 + (size_t)batch * nheads * T * 4 + 256;
 }
 
 hipError_t launch_mamba2_correction_bwd(const uint16_t* gy, const float* ghf, const uint16_t* C,
@@ -600,21 +525,20 @@ hipError_t launch_mamba2_correction_bwd(const uint16_t* gy, const float* ghf, co
                  reinterpret_cast<float*>(ws),
                  reinterpret_cast<uint16_t*>(ws + ntb * state * 4),
                  reinterpret_cast<uint16_t*>(ws + ntb * state * 4 + state * 2),
-                 reinterpret_cast<float*>(ws + ntb * state * 4 + state * 4),
+                 reinterpret_cast<uint16_t*>(ws + ntb * state * 4 + state * 4),
+                 reinterpret_cast<float*>(ws + ntb * state * 4 + state * 6),
                  batch, T, nheads, head_dim, ngroups, d_state, ntb};
   const int uph = head_dim / 64, nug = nheads * uph / 4;
   const int ntt = (T + kMambaBwdCTokens - 1) / kMambaBwdCTokens;
   auto run = [&](auto hd, auto n) {
     constexpr int HDc = decltype(hd)::value, Nc = decltype(n)::value;
     hipLaunchKernelGGL((mamba2_bwd_prep_kernel<HDc, Nc>), dim3(nheads, batch), dim3(256), 0, stream, a);
-    if (uph == 2)  // two units per head add into dcumA (a fill kernel, not a memset node)
-      hipLaunchKernelGGL(mamba2_bwd_zero_kernel, dim3(1024), dim3(256), 0, stream, g_cumA,
-                         (int64_t)batch * T * nheads);
     hipLaunchKernelGGL((mamba2_bwd_unit_kernel<Nc>), dim3((unsigned)(nug * ntb * batch)), dim3(256), 0,
                        stream, a, nug);
+    // the dC kernel writes dcumA, to which the reduce then adds the state term
+    hipLaunchKernelGGL((mamba2_bwd_c_kernel<Nc>), dim3((unsigned)(ntt * ngroups * batch)),
+                       dim3(64 * MambaBwdCCfg<Nc>::NW), 0, stream, a, ntt);
     hipLaunchKernelGGL((mamba2_bwd_reduce_kernel<HDc, Nc>), dim3(nheads, batch), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL((mamba2_bwd_c_kernel<Nc>), dim3((unsigned)(ntt * ngroups * batch)), dim3(256), 0,
-                       stream, a, ntt);
     return hipGetLastError();
   };
   if (head_dim == 64)
