@@ -144,6 +144,10 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
     qg = qgid[q];
     qd = qdoc[q];
   }
+  // document bounds of this wave's 32 queries (lanes 0 and 31; rows past sq read as
+  // document -1): the per-tile mask test is the wave's, not the workgroup's
+  const int wqg_first = __builtin_amdgcn_readlane(qg, 0), wqg_last = __builtin_amdgcn_readlane(qg, 31);
+  const int wqd_first = __builtin_amdgcn_readlane(qd, 0), wqd_last = __builtin_amdgcn_readlane(qd, 31);
   const int D = L.head_dim;        // columns past D (up to HD) load as zeros
   const int wl = window_bound(P) + diag_shift<MASK>(P);  // window: q + off - key <= wl
   const int off = sk - sq + diag_shift<MASK>(P);  // the diagonal: key == q + off
@@ -334,8 +338,8 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
       if (mask == RMX_MASK_DOC) {
         const int kga = sKg[buf][0], kgz = sKg[buf][BK - 1];
         const int kda = sKd[buf][0], kdz = sKd[buf][BK - 1];
-        need_mask |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first &&
-                       (int64_t)kga >= (int64_t)qg_last - wl);
+        need_mask |= !(kda == kdz && kda == wqd_first && wqd_first == wqd_last && kgz <= wqg_first &&
+                       (int64_t)kga >= (int64_t)wqg_last - wl);
       }
 
       f32x16 s[MBK], dp[MBK];
@@ -714,7 +718,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
   }
   // this lane's highest query: q + off <= key + wl (document masks: global index <= khi)
   const int khi = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg + wl) : key + wl - off;
-  const int khi_first = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg_first + wl) : 0;
+  // document bounds of this wave's 32 keys (lanes 0 and 31; keys past sk read as
+  // document -2): the per-tile mask test is the wave's, not the workgroup's
+  const int wkg_last = __builtin_amdgcn_readlane(kg, 31);
+  const int wkd_first = __builtin_amdgcn_readlane(kd, 0), wkd_last = __builtin_amdgcn_readlane(kd, 31);
+  const int wkhi_first =
+      mask == RMX_MASK_DOC ? clamp_i32((int64_t)__builtin_amdgcn_readlane(kg, 0) + wl) : 0;
 
   // dropout: the keep bits of a tile's 32 elements of this lane (bit 16 mb + r: query
   // 32 mb + sig_row(hl, r) of the tile, key `key`), hashed as the forward does
@@ -764,8 +773,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
       const int qga = sQg[slot][0], qgz = sQg[slot][qz];
       const int qda = sQd[slot][0];
       const int qdz = sQd[slot][qz];
-      m |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga &&
-             qgz <= khi_first);
+      m |= !(qda == qdz && qda == wkd_first && wkd_first == wkd_last && wkg_last <= qga &&
+             qgz <= wkhi_first);
     }
     return m;
   };
@@ -1297,7 +1306,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
   }
   // this lane's highest query: q + off <= key + wl (document masks: global index <= khi)
   const int khi = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg + wl) : key + wl - off;
-  const int khi_first = mask == RMX_MASK_DOC ? clamp_i32((int64_t)kg_first + wl) : 0;
+  // document bounds of this wave's 32 keys (lanes 0 and 31; keys past sk read as
+  // document -2): the per-tile mask test is the wave's, not the workgroup's
+  const int wkg_last = __builtin_amdgcn_readlane(kg, 31);
+  const int wkd_first = __builtin_amdgcn_readlane(kd, 0), wkd_last = __builtin_amdgcn_readlane(kd, 31);
+  const int wkhi_first =
+      mask == RMX_MASK_DOC ? clamp_i32((int64_t)__builtin_amdgcn_readlane(kg, 0) + wl) : 0;
 
   // per-lane LDS byte offsets, swizzle folded in. A chunk index below 16 keeps a
   // lane's offset inside a row's first 256 bytes, so the upper 8 chunk pairs of a row
@@ -1365,8 +1379,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_d256_kernel(const BwdPar
     if (mask == RMX_MASK_DOC) {
       const int qga = sQg[slot][0], qgz = sQg[slot][qz];
       const int qda = sQd[slot][0], qdz = sQd[slot][qz];
-      m |= !(qda == qdz && qda == kd_first && kd_first == kd_last && kg_last <= qga &&
-             qgz <= khi_first);
+      m |= !(qda == qdz && qda == wkd_first && wkd_first == wkd_last && wkg_last <= qga &&
+             qgz <= wkhi_first);
     }
     return m;
   };

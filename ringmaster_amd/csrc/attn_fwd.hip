@@ -170,6 +170,12 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
   const int ntile = kt_end - kt_begin;
   // no key tile: a merge into the running (out, lse) leaves it as it is
   if (ntile == 0 && P.mode == RMX_FWD_ACC_MERGE) return;
+  // document bounds of this wave's 32 queries (lanes 0 and 31; rows past sq read as
+  // document -1, so a tile with them takes the masked path): a tile whose keys all lie in
+  // the wave's one document, at or before its first query and inside the window of its
+  // last, needs no mask for this wave, whatever the rest of the workgroup's queries see
+  const int wqg_first = __builtin_amdgcn_readlane(qg, 0), wqg_last = __builtin_amdgcn_readlane(qg, 31);
+  const int wqd_first = __builtin_amdgcn_readlane(qd, 0), wqd_last = __builtin_amdgcn_readlane(qd, 31);
 
   // ---- Q operand (B of S^T = K Q^T): lane holds Q[q][16kb + 8hl .. +7]
   bf16x8 qreg[NKB];
@@ -276,8 +282,8 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
       const int ds = t & 3;
       const int kga = sKg[ds][0], kgz = sKg[ds][BK - 1];
       const int kda = sKd[ds][0], kdz = sKd[ds][BK - 1];
-      nm |= !(kda == kdz && kda == qd_first && qd_first == qd_last && kgz <= qg_first &&
-              (int64_t)kga >= (int64_t)qg_last - wl);
+      nm |= !(kda == kdz && kda == wqd_first && wqd_first == wqd_last && kgz <= wqg_first &&
+              (int64_t)kga >= (int64_t)wqg_last - wl);
     }
     return nm;
   };
