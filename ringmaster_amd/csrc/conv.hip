@@ -114,7 +114,9 @@ __device__ __forceinline__ void chunk(const ConvArgs& a, const uint16_t* base, c
 // (one memory round trip), so every chunk is read once from the L2 instead of twice, and
 // y leaves by non-temporal stores: 0.235-0.24 against 0.26-0.27 ms at configs[4]. The
 // backward's form of it (the previous and next chunks of x and the next of dy shuffled,
-// the wave's edge lanes loading theirs) measured 0.59 against 0.45 ms and was not kept.
+// the wave's edge lanes loading theirs) measured 0.59 against 0.45 ms and was not kept. The
+// backward's dx also leaves by non-temporal stores (0.453 -> 0.442 ms); non-temporal loads of
+// x or dy measured no gain in either direction.
 // v[0..7] := the previous chunk: its last W-1 tokens from the lane below, all of it from
 // pv (the loaded chunk) on the wave's first lane
 template <int W, bool DOC>
@@ -252,7 +254,7 @@ __global__ __launch_bounds__(256) void causal_conv1d_bwd_kernel(const ConvArgs a
     u32x4 o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = pack_bf2(dx[2 * i], dx[2 * i + 1]);
-    *reinterpret_cast<u32x4*>(a.y + rr[k].rowoff + rr[k].t0) = o;
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(a.y + rr[k].rowoff + rr[k].t0));
   }
   // dw / db: the workgroup's runs share one channel; one atomic per wave
   // (invalid lanes hold zeros)

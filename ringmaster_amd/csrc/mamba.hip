@@ -195,7 +195,8 @@ __global__ __launch_bounds__(256) void mamba2_correction_kernel(const MambaCorrA
 //    runs of 8 consecutive channels of one token; out + dY is formed in place in
 //    the out stage (same 16-byte slots), then re-read row-wise and stored as
 //    full 128-byte lines through a buffer resource that drops rows past the
-//    range end.
+//    range end. out is read and y written with the non-temporal cache policy
+//    (each byte is touched once): 0.215 -> 0.203 ms at 8 x 8192 tokens x 64 heads.
 // Workgroups are renumbered so that consecutive logical ids land on the same
 // XCD, unit groups fastest: the workgroups running together on an XCD cover
 // whole token rows of out / y (every head) for a few token blocks of one batch
@@ -350,8 +351,8 @@ __global__ __launch_bounds__(256, 2) void mamba2_correction_stream_kernel(const 
 #pragma unroll
     for (int k = 0; k < NI; ++k) {
       const int p = 64 * k + lane, row = p / CHO, pc = p % CHO;
-      dma16_async(rO, ldsO + st * OS + 1024 * k,
-                  (t0 + row) * ostride + 16 * (pc ^ swz_chunks<CHO>(row)));
+      dma16_async_nt(rO, ldsO + st * OS + 1024 * k,
+                     (t0 + row) * ostride + 16 * (pc ^ swz_chunks<CHO>(row)));
     }
     dma4_async(rA, ldsX + st * XS + 256 * wave,
                xa_live ? (t0 + xa_tok) * (H * 4) + 4 * xa_head : (int)aspan);
@@ -418,7 +419,7 @@ __global__ __launch_bounds__(256, 2) void mamba2_correction_stream_kernel(const 
     for (int k = 0; k < NI; ++k) {
       const int p = 64 * k + lane, row = p / CHO, pc = p % CHO;
       const u32x4 yv = *reinterpret_cast<const u32x4*>(ost + 16 * p);
-      buf_store16(rY, (32 * s + row) * ostride + 16 * (pc ^ swz_chunks<CHO>(row)), yv);
+      buf_store16_nt(rY, (32 * s + row) * ostride + 16 * (pc ^ swz_chunks<CHO>(row)), yv);
     }
   }
 }

@@ -19,7 +19,9 @@
 // K = tokens). Each wave owns D*N/4096 of the 32x32 output tiles of each head, all in
 // one row block. Two heads read 256 contiguous bytes of a token's x row where one
 // head reads 128 at the token stride (a strided copy of 128-byte rows runs at half
-// the HBM rate of one of 512-byte rows), and share each B operand read.
+// the HBM rate of one of 512-byte rows), and share each B operand read. x is read
+// with the non-temporal cache policy (each byte once): 0.166 -> 0.155 ms at 8 x 8192
+// tokens x 64 heads.
 //
 // Backward (given G = dL/dS fp32): a workgroup = 8 waves x 32 tokens of one
 // (row, group); it loops over the group's heads, staging G_h in LDS as bf16:
@@ -33,6 +35,8 @@
 // whole rows (a store of 8-byte pieces of 32 rows 8 KiB apart was the kernel's
 // main cost), and reads e / cum_A 32 bytes (8 heads) per token at a time into an
 // LDS table (4-byte reads per head fetched each 128-byte line again and again).
+// g_x leaves by non-temporal stores (0.318 -> 0.307 ms at 8 x 8192 tokens x 64 heads);
+// non-temporal x loads measured slower here (0.343 ms).
 #include "rmx_kernels.h"
 
 namespace rmx {
@@ -153,7 +157,7 @@ __global__ __launch_bounds__(256) void mamba2_chunk_state_kernel(const StateArgs
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
       const int c = tid + 256 * i, t = tb + c / XR, j = (c % XR) / (D / 8);
-      r.x[i] = buf_load16(xrs, ((t * a.H + h) * D + 8 * (c % XR)) * 2);
+      r.x[i] = buf_load16_nt(xrs, ((t * a.H + h) * D + 8 * (c % XR)) * 2);  // read once
       const int64_t o = th + (int64_t)(t < T ? t : T - 1) * a.H + j;
       r.e[i] = a.e[o];
       r.c[i] = a.cum_A[o];
@@ -431,7 +435,7 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd_kernel(const State
         v[1] = lo[1];
         v[2] = hi[0];
         v[3] = hi[1];
-        buf_store16(grs, (rr * H * D + 8 * (lane % LPR)) * 2, v);
+        buf_store16_nt(grs, (rr * H * D + 8 * (lane % LPR)) * 2, v);
       }
     }
     gw += xhalf(gw);
@@ -615,7 +619,7 @@ __global__ __launch_bounds__(512) void mamba2_chunk_state_bwd2_kernel(const Stat
       v[1] = lo[1];
       v[2] = hi[0];
       v[3] = hi[1];
-      buf_store16(grs, (rr * H * D + 8 * (lane % LPR)) * 2, v);
+      buf_store16_nt(grs, (rr * H * D + 8 * (lane % LPR)) * 2, v);
     }
   };
   // g_e (lane half 0) / g_cum_A (half 1) of the 8-head group k (heads 8k .. 8k + cnt - 1

@@ -174,6 +174,10 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t num_bytes)
 __device__ __forceinline__ u32x4 buf_load16(const i32x4& rsrc, int byte_off) {
   return llvm_raw_buffer_load_v4(rsrc, byte_off, 0, 0);
 }
+// Non-temporal form (cache policy NT), for data the grid reads once.
+__device__ __forceinline__ u32x4 buf_load16_nt(const i32x4& rsrc, int byte_off) {
+  return llvm_raw_buffer_load_v4(rsrc, byte_off, 0, 2);
+}
 
 // Stores at or past num_records are dropped by the hardware, so a tile's rows
 // past the end of its range need no branch (and every wave issues the same
@@ -182,6 +186,12 @@ __device__ void llvm_raw_buffer_store_v4(u32x4 data, i32x4 rsrc, int voffset, in
                                          int aux) __asm("llvm.amdgcn.raw.buffer.store.v4i32");
 __device__ __forceinline__ void buf_store16(const i32x4& rsrc, int byte_off, const u32x4& v) {
   llvm_raw_buffer_store_v4(v, rsrc, byte_off, 0, 0);
+}
+// Non-temporal form (cache policy NT) for data written once and not read back by
+// this kernel: whole 128-byte lines stream out without displacing reused lines.
+// A store that covers only part of a line is slower in this form.
+__device__ __forceinline__ void buf_store16_nt(const i32x4& rsrc, int byte_off, const u32x4& v) {
+  llvm_raw_buffer_store_v4(v, rsrc, byte_off, 0, 2);
 }
 
 // Bytes a buffer over `rows` rows of `row_bytes` at stride `stride_bytes` must cover.
@@ -257,6 +267,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 __device__ __forceinline__ void dma16_async(const i32x4& rsrc, uint32_t lds, int byte_off) {
   asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(rsrc),
+               "{m0}"(lds)
+               : "memory");
+}
+// Non-temporal form, for operands read once by the whole grid (a streamed input).
+__device__ __forceinline__ void dma16_async_nt(const i32x4& rsrc, uint32_t lds, int byte_off) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds" ::"v"(byte_off), "s"(rsrc),
                "{m0}"(lds)
                : "memory");
 }
