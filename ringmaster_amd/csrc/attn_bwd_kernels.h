@@ -74,6 +74,12 @@ struct BwdTiles {
 //   per configs[2] ring launch)
 //   dQ^T += K^T dS^T  A = K^T by transposed reads of the K tile, B = dS^T
 //                                                            16 MFMAs
+// The S^T MFMAs of a tile come first; the exponentials of P then issue under the dP^T
+// MFMAs, a share per MFMA step (fenced steps, the V row operand read one step ahead), and
+// the dS products and packs under the dQ MFMAs: 10.36-10.40 -> 10.15-10.18 ms per configs[2]
+// ring launch (10.50-10.59 -> 10.40-10.47 on a second box) against S^T and dP^T interleaved
+// with the exponentials after them. An explicit read-ahead ring for the S^T / dP^T row
+// operands of that form (1 or 2 steps) measured the same or slower.
 // K/V tiles (and the key documents) arrive by LDS DMA into NB buffers, tile
 // t + NB - 1 issued while tile t is computed, one barrier per tile. Rows are
 // unpadded with their 16-byte chunks XOR-swizzled by swz_both, so the K row reads,
@@ -354,12 +360,34 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
         dp[mb] = DROP ? zero16() : ndl;
       }
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int mb = 0; mb < MBK; ++mb) {
-          s[mb] = mfma32t<DT>(row_op(kt_lds, kb, mb), qreg[kb], s[mb]);
-          dp[mb] = mfma32t<DT>(vrow_op(buf, kb, mb), doreg[kb], dp[mb]);
-        }
+        for (int mb = 0; mb < MBK; ++mb) s[mb] = mfma32t<DT>(row_op(kt_lds, kb, mb), qreg[kb], s[mb]);
+      __builtin_amdgcn_sched_barrier(0);
+      // dP^T in NKB * MBK steps (kb, mb), each with its share of the exponentials of P
+      // (pinned in their step: the compiler would sink them past the mask branch to their
+      // use); the V row operand is read one step ahead
+      float pr[MBK][16];
+      {
+        constexpr int NSD = NKB * MBK;
+        bf16x8 opv[2];
+        opv[0] = vrow_op(buf, 0, 0);
+        [&]<int... U>(std::integer_sequence<int, U...>) __attribute__((always_inline)) {
+          (
+              [&] {
+                constexpr int u = U;
+                if constexpr (u + 1 < NSD) opv[(u + 1) & 1] = vrow_op(buf, (u + 1) / MBK, (u + 1) % MBK);
+                __builtin_amdgcn_sched_barrier(0);
+                dp[u % MBK] = mfma32t<DT>(opv[u & 1], doreg[u / MBK], dp[u % MBK]);
+#pragma unroll
+                for (int e = 16 * MBK * u / NSD; e < 16 * MBK * (u + 1) / NSD; ++e) {
+                  pr[e / 16][e % 16] = fast_exp2(fmaf(s[e / 16][e % 16], c, -lse2));
+                  asm volatile("" : "+v"(pr[e / 16][e % 16]));
+                }
+                __builtin_amdgcn_sched_barrier(0);
+              }(),
+              ...);
+        }(std::make_integer_sequence<int, NSD>{});
       }
 
       bf16x8 dsb[KB2];
@@ -368,7 +396,7 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
         const int mb = kb2 >> 1, b8 = 8 * (kb2 & 1);
         float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = fast_exp2(fmaf(s[mb][b8 + i], c, -lse2));
+        for (int i = 0; i < 8; ++i) v[i] = pr[mb][b8 + i];
         if (need_mask) {
         keep_branch();
 #pragma unroll
