@@ -501,7 +501,12 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
 //   phase 1: dV_j            | exponentials of rows 32..63, P^T blocks 1..3,
 //                              (P dP')^T block 0
 //   -- barrier: tile j + 1 landed; tile j - 3's buffer takes tile j + 3
-//   phase 2: dK_j            | (P dP')^T blocks 1..3
+//   phase 2: dK_j            | (P dP')^T blocks 1..3, the loads of tile j + 3 (one
+//                              DMA instruction per step: 15.54-15.62 -> 15.43-15.49 ms
+//                              per configs[2] ring launch against all of them ahead
+//                              of the phase; the dropout kernels keep that form, since
+//                              ROCm 7.2's AGPR-copy MFMA rewrite crashes on them
+//                              with the spread one)
 //   phase 3: S_{j+1}         | (reads of nl and delta of tile j + 1)
 // S_{j+1} reuses the registers of P_j (dead after phase 2). Masked tiles (rare)
 // get S := -inf on their masked pairs before their exponentials, with nl clamped
@@ -653,6 +658,27 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     vq[i] = 8 * ch < D ? r * qss + 16 * ch : kOutOfRange;
     vo[i] = 8 * ch < D ? r * oss + 16 * ch : kOutOfRange;
   }
+  // part p of a tile's loads into buffer b: p = 0 also the metadata (wave 0), then the
+  // wave's Q rows (p < NDMA) or dO rows; all 2 NDMA parts make the tile
+  auto dma_part = [&](int b, Cursor cu, bool live, int p) __attribute__((always_inline)) {
+    const int qa = cu.qt * BQ;
+    const int hi = live ? cu.hi : 0;
+    if (p == 0 && wave == 0) {
+      const int lo = hi * lhs + 4 * qa;
+      const uint32_t n = live ? 4u * (uint32_t)(sq - qa) : 0u;
+      const uint32_t m = lds_addr(sM[b]);
+      dma4_async(make_rsrc(nb0 + lo, n), m, 4 * lane);
+      dma4_async(make_rsrc(db0 + lo, n), m + 4 * BQ, 4 * lane);
+    }
+    if (p < C::NDMA) {
+      const i32x4 qrs = make_rsrc(qb0 + hi * qhs + qa * qss, live ? qspan - (uint32_t)(qa * qss) : 0u);
+      dma16_async(qrs, lds_addr(sQ[b]) + 1024 * (wave * C::NDMA + p), vq[p]);
+    } else {
+      const int i = p - C::NDMA;
+      const i32x4 ors = make_rsrc(ob0 + hi * ohs + qa * oss, live ? ospan - (uint32_t)(qa * oss) : 0u);
+      dma16_async(ors, lds_addr(sO[b]) + 1024 * (wave * C::NDMA + i), vo[i]);
+    }
+  };
   auto dma_tile = [&](int b, Cursor cu, bool live) {
     const int qa = cu.qt * BQ;
     const int hi = live ? cu.hi : 0;
@@ -951,6 +977,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     if (j + 1 < ntile) doc_load(nx1);
     bf16x8 pt[4], dst[4];
     int qa_next = 0;  // first query of tile j + 1 (set at the hand-over, read in phase 3)
+    Cursor dcu = nx3;  // tile j + 3: its loads issue one part per step early in phase 2
+    const bool dlive = j + 3 < ntile;
     auto step = [&](auto Tc) __attribute__((always_inline)) {
       constexpr int T = decltype(Tc)::value;
       constexpr int ph = T / NS, t = T % NS;
@@ -991,6 +1019,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
         dv[t % NDB] = mfma32t<DT>(pt[t / NDB], a, dv[t % NDB]);
       } else if constexpr (ph == 2) {
         dk[t % NDB] = mfma32t<DT>(dst[t / NDB], a, dk[t % NDB]);
+        // tile j + 3's loads (its buffer is free since the hand-over barrier), one part
+        // per step under the dK MFMAs rather than all of them ahead of the first one
+        if constexpr (!DROP && t < 2 * C::NDMA) dma_part((B + 3) % NB, dcu, dlive, t);
       } else {
         if constexpr (t < 2) s[t] = zero16();
         s[t & 1] = mfma32t<DT>(a, kreg[t >> 1], s[t & 1]);
@@ -1045,7 +1076,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const BwdParams p
     // buffer (last read in phase 2 of tile j - 3) takes tile j + 3
     if (j + 1 < ntile) doc_store(BN);
     wait_vm_barrier<2 * C::NDMA>();
-    dma_tile((B + 3) % NB, nx3, j + 3 < ntile);
+    if constexpr (DROP) dma_tile((B + 3) % NB, nx3, j + 3 < ntile);
     qa_next = nx1.qt * BQ;
     cur = nx1;
     nx1 = nx2;

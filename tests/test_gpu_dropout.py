@@ -106,9 +106,51 @@ def test_dropout_seed_determinism():
     assert not torch.equal(a, c)
 
 
+def _drop_grad_bar(qf, kf, vf, dof, p, seed, scale):
+    """Per-element bars of dK and dV [b, sk, hkv, d] for a causal dropout block: max(2e-2,
+    two bf16 ulps of the element) plus the rounding the backward adds before its sums, from
+    fp64 summands: it takes (P M)^T and dS = P (M dP - delta) as bf16 operands (2^-9
+    relative each, M the kept mask times 1 / (1 - p)), so dK gains up to 4 2^-8
+    RSS_q(scale dS Q) and dV 4 2^-8 RSS_q(P M dO), over the queries and folded heads.
+    Elements whose summands cancel (|dK| far below the sum of |summands|) need that term:
+    the two-ulp bar alone is a bar on the result's own size."""
+    q, k, v, do = (t.double() for t in (qf, kf, vf, dof))
+    b, sq, hq, d = q.shape
+    sk, hkv = k.shape[1], k.shape[2]
+    g = hq // hkv
+    kx, vx = k.repeat_interleave(g, 2), v.repeat_interleave(g, 2)
+    s = torch.einsum("bqhd,bkhd->bhqk", q, kx) * scale
+    s = s.masked_fill(torch.ones(sq, sk, dtype=torch.bool).triu(sk - sq + 1), float("-inf"))
+    pr = torch.softmax(s, -1)
+    m = rm.dropout_scale_mask(seed, b, hq, sq, sk, p).double()
+    dpm = m * torch.einsum("bqhd,bkhd->bhqk", do, vx)
+    out = torch.einsum("bhqk,bkhd->bqhd", pr * m, vx)
+    dlt = (do * out).sum(-1).transpose(1, 2)[..., None]
+    ds = pr * (dpm - dlt)
+
+    def fold(x, y):
+        return torch.einsum("bhqk,bqhd->bkhd", x, y).unflatten(2, (hkv, g)).sum(3)
+
+    extra_k = 4 * 2.0 ** -8 * scale * fold(ds ** 2, q ** 2).sqrt()
+    extra_v = 4 * 2.0 ** -8 * fold((pr * m) ** 2, do ** 2).sqrt()
+    return extra_k.float(), extra_v.float()
+
+
+def _close_with(got, ref, extra, what):
+    g, r = got.detach().float().cpu(), ref.detach().float().cpu()
+    diff = (g - r).abs()
+    bar = (r.abs() * 2 * 2.0 ** -7).clamp_min(2e-2) + extra
+    over = (diff / bar).max().item()
+    rl = float(((g - r).norm() / r.norm().clamp_min(1e-30)).item())
+    assert over < 1 and rl < 1e-2, f"{what}: max-abs {diff.max().item():.3e} ({over:.2f} of the bar) rel-L2 {rl:.3e}"
+
+
 def test_dropout_dao_ops_rng_state():
     from ringmaster_amd.ring.kernels import flash_ops
 
+    # the mask follows the device generator's (seed, offset): seed it, so the case does not
+    # depend on how many draws earlier tests made
+    torch.cuda.manual_seed(20)
     fwd, bwd = flash_ops()
     qf, q = bf16_pair((1, 192, 4, 128), 11)
     kf, k = bf16_pair((1, 192, 2, 128), 12)
@@ -129,10 +171,11 @@ def test_dropout_dao_ops_rng_state():
     assert_bf16_close(out, ref, "out")
     assert_f32_rel(lse, ref_lse, "lse")
     assert_bf16_close(dq, qr.grad, "dq")
-    # GQA-folded and with kept probabilities scaled by 1 / (1 - p) = 1.25 before their bf16
-    # rounding, dK / dV values near 3 carry up to two bf16 ulps (2^-6 each) of error
-    assert_bf16_close(dk, kr.grad, "dk", ulp_floor=2)
-    assert_bf16_close(dv, vr.grad, "dv", ulp_floor=2)
+    # GQA-folded, with kept probabilities scaled by 1 / (1 - p) = 1.25: dK / dV values near 3
+    # (two bf16 ulps of 2^-6 each) and elements whose summands cancel
+    extra_k, extra_v = _drop_grad_bar(qf, kf, vf, dof, 0.2, seed, 0.125)
+    _close_with(dk, kr.grad, extra_k, "dk")
+    _close_with(dv, vr.grad, extra_v, "dv")
     with pytest.raises(ValueError, match="rng_state"):
         bwd(do, q, k, v, out, lse, dq, dk, dv, 0.2, 0.125, True, -1, -1, 0.0, None, False, None)
 
