@@ -74,12 +74,13 @@ struct BwdTiles {
 //   per configs[2] ring launch)
 //   dQ^T += K^T dS^T  A = K^T by transposed reads of the K tile, B = dS^T
 //                                                            16 MFMAs
-// The S^T MFMAs of a tile come first; the exponentials of P then issue under the dP^T
-// MFMAs, a share per MFMA step (fenced steps, the V row operand read one step ahead), and
-// the dS products and packs under the dQ MFMAs: 10.36-10.40 -> 10.15-10.18 ms per configs[2]
-// ring launch (10.50-10.59 -> 10.40-10.47 on a second box) against S^T and dP^T interleaved
-// with the exponentials after them. An explicit read-ahead ring for the S^T / dP^T row
-// operands of that form (1 or 2 steps) measured the same or slower.
+// Per tile the S^T MFMAs run block by block (32 keys each), then the dP^T MFMAs; the
+// exponentials of P of each S^T block issue under the MFMAs that follow it, a share per
+// fenced step (operands read one step ahead), and the dS products and packs under the dQ
+// MFMAs. Against S^T and dP^T interleaved with all the exponentials after them: 10.36-10.40
+// -> 10.15-10.18 ms per configs[2] ring launch with the exponentials under dP^T only
+// (10.50-10.59 -> 10.40-10.47 on a second box), then 10.38 -> 10.08-10.22 with them
+// spread from the second S^T block on. A read-ahead ring of 2 steps measured slower.
 // K/V tiles (and the key documents) arrive by LDS DMA into NB buffers, tile
 // t + NB - 1 issued while tile t is computed, one barrier per tile. Rows are
 // unpadded with their 16-byte chunks XOR-swizzled by swz_both, so the K row reads,
@@ -359,35 +360,47 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
         s[mb] = zero16();
         dp[mb] = DROP ? zero16() : ndl;
       }
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-        for (int mb = 0; mb < MBK; ++mb) s[mb] = mfma32t<DT>(row_op(kt_lds, kb, mb), qreg[kb], s[mb]);
-      __builtin_amdgcn_sched_barrier(0);
-      // dP^T in NKB * MBK steps (kb, mb), each with its share of the exponentials of P
-      // (pinned in their step: the compiler would sink them past the mask branch to their
-      // use); the V row operand is read one step ahead
+      // S^T block by block (32 keys each), then dP^T; the exponentials of P of block mb
+      // issue under the MFMAs of block mb + 1 (the last block's under dP^T), a share per
+      // fenced step, pinned there (the compiler would sink them past the mask branch to
+      // their use). Operands are read one step ahead.
       float pr[MBK][16];
       {
-        constexpr int NSD = NKB * MBK;
-        bf16x8 opv[2];
-        opv[0] = vrow_op(buf, 0, 0);
+        constexpr int NSS = NKB * MBK, NST = 2 * NSS;  // S^T steps, all steps
+        // step u < NSS: S^T block u / NKB, k-step u % NKB; else dP^T (kb, mb) of u - NSS
+        auto op_of = [&](int u) __attribute__((always_inline)) -> bf16x8 {
+          if (u < NSS) return row_op(kt_lds, u % NKB, u / NKB);
+          const int w = u - NSS;
+          return vrow_op(buf, w / MBK, w % MBK);
+        };
+        bf16x8 opr[2];
+        opr[0] = op_of(0);
         [&]<int... U>(std::integer_sequence<int, U...>) __attribute__((always_inline)) {
           (
               [&] {
                 constexpr int u = U;
-                if constexpr (u + 1 < NSD) opv[(u + 1) & 1] = vrow_op(buf, (u + 1) / MBK, (u + 1) % MBK);
+                if constexpr (u + 1 < NST) opr[(u + 1) & 1] = op_of(u + 1);
                 __builtin_amdgcn_sched_barrier(0);
-                dp[u % MBK] = mfma32t<DT>(opv[u & 1], doreg[u / MBK], dp[u % MBK]);
+                if constexpr (u < NSS) {
+                  s[u / NKB] = mfma32t<DT>(opr[u & 1], qreg[u % NKB], s[u / NKB]);
+                } else {
+                  constexpr int w = u - NSS;
+                  dp[w % MBK] = mfma32t<DT>(opr[u & 1], doreg[w / MBK], dp[w % MBK]);
+                }
+                // exponentials of block eb, spread over the steps of the next block (or dP^T)
+                constexpr int eb = u < NSS ? u / NKB - 1 : MBK - 1;
+                constexpr int n0 = u < NSS ? u % NKB : u - NSS, nn = u < NSS ? NKB : NSS;
+                if constexpr (eb >= 0) {
 #pragma unroll
-                for (int e = 16 * MBK * u / NSD; e < 16 * MBK * (u + 1) / NSD; ++e) {
-                  pr[e / 16][e % 16] = fast_exp2(fmaf(s[e / 16][e % 16], c, -lse2));
-                  asm volatile("" : "+v"(pr[e / 16][e % 16]));
+                  for (int e = 16 * n0 / nn; e < 16 * (n0 + 1) / nn; ++e) {
+                    pr[eb][e] = fast_exp2(fmaf(s[eb][e], c, -lse2));
+                    asm volatile("" : "+v"(pr[eb][e]));
+                  }
                 }
                 __builtin_amdgcn_sched_barrier(0);
               }(),
               ...);
-        }(std::make_integer_sequence<int, NSD>{});
+        }(std::make_integer_sequence<int, NST>{});
       }
 
       bf16x8 dsb[KB2];
