@@ -192,6 +192,7 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
   const int kss = (int)(2 * L.k_ss), vss = (int)(2 * L.v_ss);
   const i32x4 krs = make_rsrc(P.k + bb * L.k_sb + kvh * L.k_sh, span_bytes(sk, kss, D * 2));
   const i32x4 vrs = make_rsrc(P.v + bb * L.v_sb + kvh * L.v_sh, span_bytes(sk, vss, D * 2));
+  const i32x4 krs0 = make_rsrc(P.k, 0u), vrs0 = make_rsrc(P.v, 0u);  // zero-length loads
   // DMA of a K (V) tile at key k0 into buffer b: instruction n of the tile fills
   // LDS bytes [1024 n, 1024 n + 1024), lane L row n*RPK + L/CH, swizzled chunk L%CH;
   // chunks of columns past D are loaded from kOutOfRange (zeros)
@@ -212,6 +213,18 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
       const int r = n * C::RPK + lane / CH, ch = (lane % CH) ^ swz_tr<HD>(r);
       dma16_async(vrs, d + 1024 * n, 8 * ch < D ? (k0 + r) * vss + 16 * ch : kOutOfRange);
     }
+  };
+  // instruction i of a K (V) tile's DMA through resource rs (num_records 0 past the end:
+  // the buffer gets zeros and no memory is read)
+  auto dma_k_part = [&](const i32x4& rs, int b, int k0, int i) __attribute__((always_inline)) {
+    const int n = wave * NDMA + i;
+    const int r = n * C::RPK + lane / CH, ch = (lane % CH) ^ swz_rows<HD>(r);
+    dma16_async(rs, lds_addr(&sK[b][0]) + 1024 * n, 8 * ch < D ? (k0 + r) * kss + 16 * ch : kOutOfRange);
+  };
+  auto dma_v_part = [&](const i32x4& rs, int b, int k0, int i) __attribute__((always_inline)) {
+    const int n = wave * NDMA + i;
+    const int r = n * C::RPK + lane / CH, ch = (lane % CH) ^ swz_tr<HD>(r);
+    dma16_async(rs, lds_addr(&sV[b][0]) + 1024 * n, 8 * ch < D ? (k0 + r) * vss + 16 * ch : kOutOfRange);
   };
   // key metadata of tile t (RMX_MASK_DOC), one dword per lane, by wave 0
   constexpr bool DOCDMA = mask == RMX_MASK_DOC;
@@ -343,8 +356,9 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
   }
   wait_all_loads();
   __syncthreads();
-  // loads issued at iteration j (j = -1: here): K_{j+3} into K buffer (j+3) % 4,
-  // V_{j+2} into V buffer (j+2) % 3; iteration j + 2 is the first to read them
+  // loads of iteration j: K_{j+3} into K buffer (j+3) % 4, V_{j+2} into V buffer
+  // (j+2) % 3; iteration j + 2 is the first to read them. This form issues them for
+  // j = -1, here; the iterations issue theirs inside region 1 (below)
   auto issue = [&](int j, int vb2) __attribute__((always_inline)) {
     if (j + 3 < ntile) {
       dma_k((j + 3) & 3, (kt_begin + j + 3) * BK);
@@ -353,17 +367,12 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
     if (j + 2 < ntile) dma_v(vb2, (kt_begin + j + 2) * BK);
   };
   // end of iteration j: everything but the loads issued at iteration j has landed
+  // (every iteration issues the same loads, zero-length past the end)
   auto barrier_wait = [&](int j) __attribute__((always_inline)) {
-    if (j + 3 < ntile) {
-      if (DOCDMA && wave == 0)
-        wait_vm_barrier<2 * NDMA + 2>();
-      else
-        wait_vm_barrier<2 * NDMA>();
-    } else if (j + 2 < ntile) {
-      wait_vm_barrier<NDMA>();
-    } else {
-      wait_vm_barrier<0>();
-    }
+    if (DOCDMA && wave == 0)
+      wait_vm_barrier<2 * NDMA + 2>();
+    else
+      wait_vm_barrier<2 * NDMA>();
   };
   issue(-1, 1);
   if (ntile > 0) {
@@ -399,10 +408,17 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
   constexpr int KD = 3, VD = 3;            // operand prefetch depth (steps) of regions 1 and 2
   static_assert(VD <= NKB && VD < PVS && 2 * MB * KD <= 15 && 4 * VD <= 15, "lgkmcnt range");
   static_assert(P1 >= 4 * (2 * MB - 1) && PV3 >= 1, "P blocks packed before their MFMAs");
+  static_assert(2 * NDMA <= NKB, "a tile's loads fit the steps of region 1");
   auto pv_idx = [](int u, int v) { return 2 * u + v; };  // PV MFMA: kb2 = idx / NDB, db = idx % NDB
   auto iter = [&](int j, int vbj, f32x16* sc, f32x16* sn) __attribute__((always_inline)) {
     const int vb2 = vbj == 0 ? 2 : vbj - 1;  // (j + 2) % 3
-    issue(j, vb2);
+    // this iteration's loads, K_{j+3} (and its documents) then V_{j+2}, one DMA instruction
+    // per step of region 1 after the step's MFMAs (8.26-8.28 -> 8.20 ms per configs[2] ring
+    // launch against all of them, behind branches, ahead of region 1)
+    const bool klive = j + 3 < ntile, vlive = j + 2 < ntile;
+    const i32x4 krs_j = klive ? krs : krs0, vrs_j = vlive ? vrs : vrs0;
+    const int kk0 = (kt_begin + (klive ? j + 3 : 0)) * BK, vk0 = (kt_begin + (vlive ? j + 2 : 0)) * BK;
+    const int kbuf = (j + 3) & 3;
     const int kbi = (j + 1) & 3;
     const bool live = j + 1 < ntile;
     const float mbase = (m_run == kNegInf) ? 0.f : m_run;
@@ -458,6 +474,17 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) sn[mb] = mfma32t<DT>(ka[t % (KD + 1)][mb], qreg[t], sn[mb]);
+            if constexpr (t < NDMA)
+              dma_k_part(krs_j, kbuf, kk0, t);
+            else if constexpr (t < 2 * NDMA)
+              dma_v_part(vrs_j, vb2, vk0, t - NDMA);
+            if constexpr (t == 0 && DOCDMA) {
+              if (wave == 0) {
+                const int b3 = (j + 3) & 3;
+                dma4_async(klive ? kgrs : krs0, lds_addr(&sKg[b3][0]), 4 * (kk0 + lane));
+                dma4_async(klive ? kdrs : krs0, lds_addr(&sKd[b3][0]), 4 * (kk0 + lane));
+              }
+            }
             [&]<int... Q>(std::integer_sequence<int, Q...>) __attribute__((always_inline)) {
               (pair(std::integral_constant<int, P1 * t / NKB + Q>{}), ...);
             }(std::make_integer_sequence<int, P1 * (t + 1) / NKB - P1 * t / NKB>{});
@@ -523,6 +550,7 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
     iter(j + 1, vbj, sB, sA);
     vbj = vbj == 2 ? 0 : vbj + 1;
   }
+  wait_all_loads();  // the zero-length loads past the end
 
   // ---- epilogue: normalise, lse, merge
   const float lt = l_run + xhalf(l_run);
