@@ -10,7 +10,7 @@
 //  * thread: U consecutive tokens of V channels, scanned from zero in registers;
 //  * wavefront: the token groups of a wave (lanes with the same channels) fold
 //    their pairs by an inclusive scan over lanes, log2 shuffle steps;
-//  * workgroup: the four waves' totals fold through LDS into the chunk's pair;
+//  * workgroup: the eight waves' totals fold through LDS into the chunk's pair;
 //  * chip: chunks fold in sequence order by decoupled look-back. A workgroup
 //    takes its chunk from a ticket counter, so every earlier chunk belongs to a
 //    workgroup that is already running; it publishes its pair, walks back over the
@@ -52,7 +52,10 @@ namespace rmx {
 namespace {
 
 constexpr int kU = 16;             // tokens per thread
-constexpr int kWaves = 4;          // waves per workgroup, token-ordered
+// waves per workgroup, token-ordered: 8 against 4 halves the chunks of a chain (and its
+// look-back words and latency): 1.24 -> 0.96 / 2.00 -> 1.60 ms fwd / bwd at L = 131072, d = 4096;
+// 16 spills (368 bytes in the backward) and ran the backward 2.5 ms
+constexpr int kWaves = 8;
 constexpr int kSpinCap = 1 << 22;  // look-back polls before giving up (about 0.3 s)
 
 // Cross-workgroup words: a 32-bit value with a nonzero tag in the upper half, written
@@ -89,7 +92,7 @@ __device__ __forceinline__ float word_val(uint64_t w) { return __uint_as_float((
 // PASS 0: single pass with look-back; 1: publish the chunk's pair only; 2: outputs from
 // the state the fold kernel left for the previous chunk.
 template <int AMODE, int V, bool BWD, int PASS>
-__global__ __launch_bounds__(256) void linear_scan_chunked_kernel(
+__global__ __launch_bounds__(64 * kWaves) void linear_scan_chunked_kernel(
     const float* __restrict__ a, const float* __restrict__ x, const float* __restrict__ hin,
     const float* __restrict__ hfwd, float* __restrict__ y, float* __restrict__ da,
     float* __restrict__ dhin, ChunkWork w, int batch, int L, int d, int groups, int cw_log2,
@@ -541,7 +544,7 @@ static void launch_pass(const ScanChunkPlan& p, const float* a, const float* x, 
                         int batch, int L, int d, int groups, hipStream_t stream) {
   const unsigned grid = (unsigned)((int64_t)batch * p.ntiles * p.nchunks);
 #define RMX_CHUNKED(AM, VV)                                                                      \
-  hipLaunchKernelGGL((linear_scan_chunked_kernel<AM, VV, BWD, PASS>), dim3(grid), dim3(256), 0,   \
+  hipLaunchKernelGGL((linear_scan_chunked_kernel<AM, VV, BWD, PASS>), dim3(grid), dim3(64 * kWaves), 0, \
                      stream, a, x, hin, hfwd, y, da, dhin, w, batch, L, d, groups, p.cw_log2,     \
                      p.lg_log2)
   if (p.amode == 1) {

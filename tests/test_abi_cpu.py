@@ -194,15 +194,15 @@ def test_scan_workspace_plan_and_checks():
     lib = abi.lib()
     tc = ctypes.c_int32(0)
     need = lib.rmx_linear_scan_workspace(1, 65536, 256, 8, ctypes.byref(tc))
-    # 256 channels: one 64-lane x 4-channel token group per wave, 4 waves x 16 tokens
-    assert tc.value == 64
-    slots = 65536 // 64
+    # 256 channels: one 64-lane x 4-channel token group per wave, 8 waves x 16 tokens
+    assert tc.value == 128
+    slots = 65536 // 128
     assert need >= 256 + slots * 4 + slots * 256 * 12
     assert lib.rmx_linear_scan_workspace(1, 0, 256, 8, None) == 0
     assert lib.rmx_linear_scan_workspace(1, 4096, 3, 2, None) == 0  # groups must divide d
     # d = 1: one channel per token group, 64 token groups per wave
     lib.rmx_linear_scan_workspace(2, 65536, 1, 1, ctypes.byref(tc))
-    assert tc.value == 4 * 64 * 16
+    assert tc.value == 8 * 64 * 16
     # a workspace below the plan's size is refused before any launch
     assert lib.rmx_linear_scan_fwd(16, 16, None, 16, None, 1, 65536, 256, 8, 1, 16, need - 1,
                                    None) == abi.RMX_EINVAL
