@@ -95,12 +95,12 @@ __device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
 
 // ---------------------------------------------------------------------------
 // 1. prep: grid (H, B), 256 threads. H_in[b,h] ([d][n] fp32) -> [n][d] bf16 hi, mid, lo
-// through LDS, and eT[b,h,:] = mask * exp(cumA[b,:,h]).
+// through LDS. (eT comes from its own kernel, below.)
 template <int HD, int N>
 __global__ __launch_bounds__(256) void mamba2_bwd_prep_kernel(const MambaBwdArgs a) {
   __shared__ float st[HD][N + 1];
   const int h = blockIdx.x, bb = blockIdx.y, tid = threadIdx.x;
-  const int H = a.nheads, T = a.T;
+  const int H = a.nheads;
   const int64_t hb = ((int64_t)bb * H + h) * HD * N;
   for (int i = tid; i < HD * N; i += 256) st[i / N][i % N] = a.h_prev[hb + i];
   __syncthreads();
@@ -124,11 +124,34 @@ __global__ __launch_bounds__(256) void mamba2_bwd_prep_kernel(const MambaBwdArgs
     *reinterpret_cast<bf16x8*>(a.ht_mid + hb + (int64_t)n * HD + d0) = mid;
     *reinterpret_cast<bf16x8*>(a.ht_lo + hb + (int64_t)n * HD + d0) = lo;
   }
-  float* et = a.eT + ((int64_t)bb * H + h) * T;
-  for (int t = tid; t < T; t += 256) {
-    const int64_t tok = (int64_t)bb * T + t;
-    const bool live = !a.seq_idx || a.seq_idx[tok] == 0;
-    et[t] = live ? expf(a.cum_A[tok * H + h]) : 0.f;
+}
+
+// 1b. eT[b,h,t] = mask * exp(cumA[b,t,h]): grid (ceil(T / 64), B), 256 threads; a tile of
+// 64 tokens x 64 heads goes through LDS, so the reads take whole token rows of cum_A and
+// the writes whole 256-byte runs of eT (one workgroup per head read cum_A 4 bytes per
+// token, 256 bytes apart: 43 -> 27 us for both kernels at 8 x 8192 tokens x 64 heads).
+__global__ __launch_bounds__(256) void mamba2_bwd_et_kernel(const MambaBwdArgs a) {
+  __shared__ float st[64][65];
+  const int t0 = blockIdx.x * 64, bb = blockIdx.y, tid = threadIdx.x;
+  const int H = a.nheads, T = a.T;
+  for (int h0 = 0; h0 < H; h0 += 64) {
+    const int hn = H - h0 < 64 ? H - h0 : 64;
+    for (int i = tid; i < 64 * 64; i += 256) {
+      const int tt = i >> 6, hh = i & 63, t = t0 + tt;
+      float v = 0.f;
+      if (t < T && hh < hn) {
+        const int64_t tok = (int64_t)bb * T + t;
+        const bool live = !a.seq_idx || a.seq_idx[tok] == 0;
+        v = live ? expf(a.cum_A[tok * H + h0 + hh]) : 0.f;
+      }
+      st[tt][hh] = v;
+    }
+    __syncthreads();
+    for (int i = tid; i < 64 * 64; i += 256) {
+      const int hh = i >> 6, tt = i & 63, t = t0 + tt;
+      if (t < T && hh < hn) a.eT[((int64_t)bb * H + h0 + hh) * T + t] = st[tt][hh];
+    }
+    __syncthreads();
   }
 }
 
@@ -535,6 +558,8 @@ hipError_t launch_mamba2_correction_bwd(const uint16_t* gy, const float* ghf, co
   auto run = [&](auto hd, auto n) {
     constexpr int HDc = decltype(hd)::value, Nc = decltype(n)::value;
     hipLaunchKernelGGL((mamba2_bwd_prep_kernel<HDc, Nc>), dim3(nheads, batch), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(mamba2_bwd_et_kernel, dim3((unsigned)((T + 63) / 64), batch), dim3(256), 0,
+                       stream, a);
     hipLaunchKernelGGL((mamba2_bwd_unit_kernel<Nc>), dim3((unsigned)(nug * ntb * batch)), dim3(256), 0,
                        stream, a, nug);
     // the dC kernel writes dcumA, to which the reduce then adds the state term
