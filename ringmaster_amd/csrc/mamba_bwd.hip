@@ -13,9 +13,9 @@
 // row's last token starts a fresh sequence, :131). With P[t,h,n] = sum_d G[t,h,d]
 // H_in[h,d,n], both dC and the sum in dcumA are contractions of P:
 //   dC[t,g,n] = sum_{h in g} e[t,h] P[t,h,n],  sum_d G S = sum_n C[t,g(h),n] P[t,h,n].
-// Four launches:
-//  1. prep: H_in^T split into three bf16 parts hi + mid + lo ([B,H,n,d]) and e
-//     transposed to [B,H,T];
+// Five launches:
+//  1. prep: H_in^T split into three bf16 parts hi + mid + lo ([B,H,n,d]); then e
+//     transposed to [B,H,T] by a kernel of its own (64-token x 64-head tiles);
 //  2. unit kernel: per head slice of 64 channels walking a token block, the block's
 //     dH_in partial (G e split into bf16 hi + lo, times C) on MFMA;
 //  3. dC kernel: per 256-token tile of one group, every head's P^T = H_in^T G^T on
