@@ -117,7 +117,9 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
   constexpr bool VBASE = 2 * NB * KT - KT / 2 > 65535;
   static_assert(NDMA >= 1 && KT % (1024 * NW) == 0, "tile split");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t sT[2 * NB][KT];  // K tiles, then V tiles
+  // K tiles, then V tiles; the epilogue stages the dQ rows here (NW x 32 x HD fp32)
+  constexpr int NTB = 2 * NB > NW * 32 * HD * 4 / KT ? 2 * NB : NW * 32 * HD * 4 / KT;
+  __shared__ __attribute__((aligned(1024))) uint8_t sT[NTB][KT];
   __shared__ __attribute__((aligned(256))) int sKg[NB][DqCfg<HD>::MDOC];
   __shared__ __attribute__((aligned(256))) int sKd[NB][DqCfg<HD>::MDOC];
   __shared__ int sRange[2];
@@ -458,39 +460,64 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
   }
   wait_all_loads();  // the zero-length loads past the end
 
-  if (!qvalid) return;
+  // ---- epilogue. Lane (hl, l32) holds dQ^T of the wave's query row l32, columns
+  // 32 db + 8 j + 4 hl .. + 3: stored from there, one instruction writes 32 bytes of each
+  // of 32 rows and every 128-byte line is assembled from four partial writes, which in
+  // lockstep launches reached HBM about twice. The rows go through LDS instead (each wave
+  // its own [32][HD] fp32 region in the tile buffers, 16-byte chunks XOR-swizzled by row)
+  // and come back as whole rows per store instruction (64 / (HD / 4) rows).
+  constexpr int CPR = HD / 4;   // 16-byte chunks per fp32 row
+  constexpr int RPI = 64 / CPR;  // rows per store instruction
+  constexpr int NI = 32 / RPI;   // store instructions per wave
+  constexpr int GI = NI < 16 ? NI : 16;  // rows read back (and prior values loaded) per group
+  static_assert(NW * 32 * HD * 4 <= (int)sizeof(sT) && CPR <= 64 && NI % GI == 0, "dQ staging");
+  __syncthreads();  // every wave is past its reads of the last tiles and its loads have landed
+  uint8_t* const stg = &sT[0][0] + wave * (32 * HD * 4);
   const float scale = L.scale;
-  float* arow = P.dq_acc ? P.dq_acc + bb * L.a_sb + (int64_t)q * L.a_ss + head * L.a_sh : nullptr;
-  uint16_t* brow = P.dq ? P.dq + bb * L.o_sb + (int64_t)q * L.o_ss + head * L.o_sh : nullptr;
-  // the accumulating modes read all of the row's prior values before the first store (one
-  // wait, not one memory round trip per 4 columns: see the dK/dV epilogue)
-  const int mode = P.dq_mode;
-  const bool rd = mode == RMX_GRAD_ACC_F32 || mode == RMX_GRAD_ACC_FINAL;
-  f32x4 prev[NDB][4];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int d0 = 32 * db + 8 * j + 4 * hl;
-      prev[db][j] = rd && d0 < D ? *reinterpret_cast<const f32x4*>(arow + d0) : f32x4{};
-    }
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d0 = 32 * db + 8 * j + 4 * hl;
-      if (d0 >= D) continue;  // columns past the head dim are not stored
+      const int cw = 8 * db + 2 * j + hl;  // columns 4 cw .. 4 cw + 3
       f32x4 v;
       v[0] = acc[db][4 * j + 0] * scale;
       v[1] = acc[db][4 * j + 1] * scale;
       v[2] = acc[db][4 * j + 2] * scale;
       v[3] = acc[db][4 * j + 3] * scale;
-      if (rd) v += prev[db][j];
-      // the prior value is added: the store is a write (f32) or a conversion (16-bit)
-      grad_store4<DT>(mode == RMX_GRAD_ACC_F32 ? RMX_GRAD_WRITE_F32
-                      : mode == RMX_GRAD_ACC_FINAL ? RMX_GRAD_WRITE_BF16 : mode,
-                      arow ? arow + d0 : nullptr, brow ? brow + d0 : nullptr, v);
+      *reinterpret_cast<f32x4*>(stg + l32 * (HD * 4) + 16 * (cw ^ (l32 % CPR))) = v;
     }
+  __syncthreads();
+  // lane: chunk ch of row RPI i + lane / CPR; rows past sq and columns past D are not stored
+  const int ch = lane % CPR, rr = lane / CPR;
+  const bool colok = 4 * ch < D;
+  float* const abase = P.dq_acc ? P.dq_acc + bb * L.a_sb + head * L.a_sh + 4 * ch : nullptr;
+  uint16_t* const bbase = P.dq ? P.dq + bb * L.o_sb + head * L.o_sh + 4 * ch : nullptr;
+  // the accumulating modes read a group's prior values before its first store (one wait,
+  // not one memory round trip per row)
+  const int mode = P.dq_mode;
+  const bool rd = mode == RMX_GRAD_ACC_F32 || mode == RMX_GRAD_ACC_FINAL;
+  // the prior value is added: the store is a write (f32) or a conversion (16-bit)
+  const int wmode = mode == RMX_GRAD_ACC_F32 ? RMX_GRAD_WRITE_F32
+                    : mode == RMX_GRAD_ACC_FINAL ? RMX_GRAD_WRITE_BF16 : mode;
+#pragma unroll
+  for (int g = 0; g < NI; g += GI) {
+    f32x4 v[GI], prev[GI];
+#pragma unroll
+    for (int i = 0; i < GI; ++i) {
+      const int row = RPI * (g + i) + rr, qq = qw0 + row;
+      v[i] = *reinterpret_cast<const f32x4*>(stg + row * (HD * 4) + 16 * (ch ^ (row % CPR)));
+      prev[i] = rd && colok && qq < sq ? *reinterpret_cast<const f32x4*>(abase + (int64_t)qq * L.a_ss)
+                                       : f32x4{};
+    }
+#pragma unroll
+    for (int i = 0; i < GI; ++i) {
+      const int qq = qw0 + RPI * (g + i) + rr;
+      if (!colok || qq >= sq) continue;
+      if (rd) v[i] += prev[i];
+      grad_store4<DT>(wmode, abase ? abase + (int64_t)qq * L.a_ss : nullptr,
+                      bbase ? bbase + (int64_t)qq * L.o_ss : nullptr, v[i]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------- dK, dV (KV-major, one wave per SIMD)

@@ -78,11 +78,13 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
   constexpr int NDMA = C::NDMA;
 
   __shared__ __attribute__((aligned(1024))) uint8_t sK[4][C::KT];
-  __shared__ __attribute__((aligned(1024))) uint8_t sV[3][C::KT];
+  // (the fourth V buffer is for the epilogue: eight tile buffers stage the out rows)
+  __shared__ __attribute__((aligned(1024))) uint8_t sV[4][C::KT];
   // RMX_MASK_DOC: global index and document of the keys of tile t, in slot t % 4
   __shared__ __attribute__((aligned(256))) int sKg[4][C::MDOC];
   __shared__ __attribute__((aligned(256))) int sKd[4][C::MDOC];
   __shared__ int sRange[2];
+  __shared__ float sWa[C::NW][32];  // epilogue: weight of each row's running out
 
   const WgCoord wc = map_workgroup(prm.map, blockIdx.x);
   if (!wc.valid) return;
@@ -552,28 +554,20 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
   }
   wait_all_loads();  // the zero-length loads past the end
 
-  // ---- epilogue: normalise, lse, merge
+  // ---- epilogue: normalise, lse, merge. Lane (hl, l32) holds O^T of the wave's query row
+  // l32, columns 32 db + 8 j + 4 hl .. + 3: stored from there, one instruction writes 32
+  // (or 16) bytes of each of 32 rows and every line is assembled from partial writes, which
+  // reached HBM up to 2.6 times. The rows go through LDS instead (each wave its own [32][HD]
+  // fp32 region in the K/V buffers, 16-byte chunks XOR-swizzled by row) and come back as
+  // whole rows per store instruction (64 / (HD / 4) rows).
   const float lt = l_run + xhalf(l_run);
-  if (q >= sq) return;
+  const bool qok = q < sq;
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   const float lse_b = lt > 0.f ? (m_run + fast_log2(lt)) * kLn2 : kNegInf;
-  const int64_t lrow = bb * L.l_sb + head * L.l_sh + q;
-  float wa = 0.f, wb = 1.f, lnew = lse_b;
-  float* accrow = P.acc_out ? P.acc_out + bb * L.a_sb + (int64_t)q * L.a_ss + head * L.a_sh : nullptr;
-  uint16_t* orow = P.out ? P.out + bb * L.o_sb + (int64_t)q * L.o_ss + head * L.o_sh : nullptr;
-  // the merging modes read the row's running out (and lse) before the first store: one
-  // wait, not one memory round trip per 4 columns (the compiler keeps a read of accrow
-  // after every earlier store to it)
+  const int64_t lrow = bb * L.l_sb + head * L.l_sh + (qok ? q : 0);
   const bool rd = P.mode == RMX_FWD_ACC_MERGE || P.mode == RMX_FWD_ACC_FINAL;
-  f32x4 prev[NDB][4];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d0 = 32 * db + 8 * j + 4 * hl;
-      prev[db][j] = rd && d0 < D ? *reinterpret_cast<const f32x4*>(accrow + d0) : f32x4{};
-    }
-  if (rd) {
+  float wa = 0.f, wb = 1.f, lnew = lse_b;
+  if (rd && qok) {
     const float la = P.acc_lse[lrow];
     const float mxl = fmaxf(la, lse_b);
     if (mxl == kNegInf) {
@@ -588,33 +582,69 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, 1) void attn_fwd_kernel(const FwdPa
     }
   }
   wb *= inv;
+  if (hl == 0 && qok) {
+    if (P.mode == RMX_FWD_ACC_INIT || P.mode == RMX_FWD_ACC_MERGE) {
+      P.acc_lse[lrow] = lnew;
+    } else if (P.lse) {
+      P.lse[lrow] = lnew;
+    }
+  }
+  constexpr int CPR = HD / 4;   // 16-byte chunks per fp32 row
+  constexpr int RPI = 64 / CPR;  // rows per store instruction
+  constexpr int NI = 32 / RPI;   // store instructions per wave
+  constexpr int GI = NI < 16 ? NI : 16;  // rows read back (and running out loaded) per group
+  constexpr int SW = 32 * HD * 4;        // staging bytes per wave
+  static_assert(SW % C::KT == 0 && C::NW * SW <= 8 * C::KT && CPR <= 64 && NI % GI == 0,
+                "out staging");
+  __syncthreads();  // every wave is past its reads of the last tiles and its loads have landed
+  const int sb = wave * (SW / C::KT);  // first of the wave's tile buffers (K buffers, then V)
+  uint8_t* const stg = sb < 4 ? &sK[sb][0] : &sV[sb - 4][0];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int d0 = 32 * db + 8 * j + 4 * hl;
-      if (d0 >= D) continue;  // columns past the head dim are not stored
+      const int cw = 8 * db + 2 * j + hl;  // columns 4 cw .. 4 cw + 3
       f32x4 v;
       v[0] = o[db][4 * j + 0] * wb;
       v[1] = o[db][4 * j + 1] * wb;
       v[2] = o[db][4 * j + 2] * wb;
       v[3] = o[db][4 * j + 3] * wb;
-      if (rd) v += prev[db][j] * wa;
+      *reinterpret_cast<f32x4*>(stg + l32 * (HD * 4) + 16 * (cw ^ (l32 % CPR))) = v;
+    }
+  if (hl == 0) sWa[wave][l32] = wa;
+  __syncthreads();
+  // lane: chunk ch of row RPI i + lane / CPR; rows past sq and columns past D are not stored
+  const int ch = lane % CPR, rr = lane / CPR;
+  const bool colok = 4 * ch < D;
+  float* const abase = P.acc_out ? P.acc_out + bb * L.a_sb + head * L.a_sh + 4 * ch : nullptr;
+  uint16_t* const obase = P.out ? P.out + bb * L.o_sb + head * L.o_sh + 4 * ch : nullptr;
+  const bool wout = P.mode == RMX_FWD_WRITE || P.mode == RMX_FWD_ACC_FINAL;
+  // the merging modes read a group's running out before its first store (one wait, not
+  // one memory round trip per row)
+#pragma unroll
+  for (int g = 0; g < NI; g += GI) {
+    f32x4 v[GI], prev[GI];
+#pragma unroll
+    for (int i = 0; i < GI; ++i) {
+      const int row = RPI * (g + i) + rr, qq = qw0 + row;
+      v[i] = *reinterpret_cast<const f32x4*>(stg + row * (HD * 4) + 16 * (ch ^ (row % CPR)));
+      prev[i] = rd && colok && qq < sq ? *reinterpret_cast<const f32x4*>(abase + (int64_t)qq * L.a_ss)
+                                       : f32x4{};
+    }
+#pragma unroll
+    for (int i = 0; i < GI; ++i) {
+      const int row = RPI * (g + i) + rr, qq = qw0 + row;
+      if (!colok || qq >= sq) continue;
+      if (rd) v[i] += prev[i] * sWa[wave][row];
       // every mode leaves the fp32 result in acc_out when it is given (WRITE and
       // ACC_FINAL: the final out in fp32, which the backward's delta reads)
-      if (accrow) *reinterpret_cast<f32x4*>(accrow + d0) = v;
-      if (P.mode == RMX_FWD_WRITE || P.mode == RMX_FWD_ACC_FINAL) {
+      if (abase) *reinterpret_cast<f32x4*>(abase + (int64_t)qq * L.a_ss) = v[i];
+      if (wout) {
         u32x2 w;
-        w[0] = cvt_pk<DT>(v[0], v[1]);
-        w[1] = cvt_pk<DT>(v[2], v[3]);
-        *reinterpret_cast<u32x2*>(orow + d0) = w;
+        w[0] = cvt_pk<DT>(v[i][0], v[i][1]);
+        w[1] = cvt_pk<DT>(v[i][2], v[i][3]);
+        *reinterpret_cast<u32x2*>(obase + (int64_t)qq * L.o_ss) = w;
       }
-    }
-  if (hl == 0) {
-    if (P.mode == RMX_FWD_ACC_INIT || P.mode == RMX_FWD_ACC_MERGE) {
-      P.acc_lse[lrow] = lnew;
-    } else if (P.lse) {
-      P.lse[lrow] = lnew;
     }
   }
 }
