@@ -26,7 +26,9 @@ namespace rmx {
 // OUT_F32, the fp32 merged output (a_* strides): the fp32 form keeps the bf16
 // rounding of out (up to |dout|*|out|*2^-9 per element) out of dS = P (dP - delta).
 // With nlse, the same pass writes nlse = -lse log2(e) (the per-query exponent
-// offset of the dK/dV kernel) at the same [b, h, s] position.
+// offset of the dK/dV kernel) at the same [b, h, s] position. Rows run query-fastest
+// (row = (b, h, q)), so the 4-byte delta, lse and nlse words of neighbouring rows share
+// cache lines; head-fastest rows put each word on its own line (8x the written bytes).
 template <int HD, bool OUT_F32, int DT>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layout L,
                                                              const void* __restrict__ out,
@@ -41,12 +43,12 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const rmx_attn_layo
   float acc = 0.f;
   int bb = 0, q = 0, h = 0;
   if (row < rows && 8 * part >= L.head_dim) {  // columns past the head dim: nothing to add
-    h = row % L.hq;
-    q = (row / L.hq) % sq;
+    q = row % sq;
+    h = (row / sq) % L.hq;
     bb = row / (L.hq * sq);
   } else if (row < rows) {
-    h = row % L.hq;
-    q = (row / L.hq) % sq;
+    q = row % sq;
+    h = (row / sq) % L.hq;
     bb = row / (L.hq * sq);
     const int64_t off = bb * L.o_sb + (int64_t)q * L.o_ss + h * L.o_sh + 8 * part;
     const u32x4 b = ld16(dout + off);
