@@ -383,12 +383,18 @@ __global__ __launch_bounds__(DqCfg<HD>::NT, 1) void attn_bwd_dq_kernel(const Bwd
                 constexpr int u = U;
                 if constexpr (u + 1 < NST) opr[(u + 1) & 1] = op_of(u + 1);
                 __builtin_amdgcn_sched_barrier(0);
+                // the step's MFMA issues at raised wave priority, ahead of the other wave's
+                // VALU work on the SIMD (10.14-10.60 -> 10.09-10.50 ms per configs[2] ring
+                // launch on two boxes; the same around the dQ^T MFMAs, or in the forward's
+                // regions, measured 4-5% slower)
+                __builtin_amdgcn_s_setprio(1);
                 if constexpr (u < NSS) {
                   s[u / NKB] = mfma32t<DT>(opr[u & 1], qreg[u % NKB], s[u / NKB]);
                 } else {
                   constexpr int w = u - NSS;
                   dp[w % MBK] = mfma32t<DT>(opr[u & 1], doreg[w / MBK], dp[w % MBK]);
                 }
+                __builtin_amdgcn_s_setprio(0);
                 // exponentials of block eb, spread over the steps of the next block (or dP^T)
                 constexpr int eb = u < NSS ? u / NKB - 1 : MBK - 1;
                 constexpr int n0 = u < NSS ? u % NKB : u - NSS, nn = u < NSS ? NKB : NSS;
