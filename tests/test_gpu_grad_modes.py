@@ -19,8 +19,11 @@ from tests.gpu_util import bf16_pair, f16_pair
 pytestmark = pytest.mark.gpu
 
 
+# head dims 96 and 200 leave the last 16-byte column chunks of the 128- and 256-wide kernels
+# past the head dim, which the row-staged dQ epilogue must not store in any mode
 @pytest.mark.parametrize("d,causal,half", [(64, True, torch.bfloat16), (128, False, torch.bfloat16),
-                                           (128, True, torch.float16), (256, True, torch.bfloat16)])
+                                           (128, True, torch.float16), (256, True, torch.bfloat16),
+                                           (96, False, torch.bfloat16), (200, True, torch.bfloat16)])
 def test_accumulating_gradient_modes_are_one_add(d, causal, half):
     from ringmaster_amd import abi
     from ringmaster_amd.ring import ops
@@ -75,3 +78,92 @@ def test_accumulating_gradient_modes_are_one_add(d, causal, half):
             ulp16 = ulp16.clamp_min(2.0 ** -24)  # fp16 subnormal spacing below 2^-14
         assert ((f.float() - e).abs() <= ulp16 + bar).all(), f"{name}: ACC_FINAL off the sum by > 1 ulp"
         assert torch.equal(w, gr.to(half)), f"{name}: WRITE_BF16 differs from the rounded gradient"
+
+
+@pytest.mark.parametrize("d", [96, 200])
+def test_row_stores_stay_inside_the_head_dim(d):
+    """The forward and dQ epilogues stage their rows through LDS and store 16-byte chunks of
+    whole rows; at d = 96 and 200 (the 128- and 256-wide kernels) the last chunks lie past
+    the head dim and are not stored. Every forward mode (WRITE, ACC_INIT, ACC_MERGE,
+    ACC_FINAL) and every dQ mode writes into views of buffers padded past d with a sentinel:
+    the padding keeps the sentinel, and the values equal those of contiguous outputs bit
+    for bit."""
+    from ringmaster_amd import abi
+    from ringmaster_amd.ring import ops
+
+    b, sq, sk, hq, hkv, pad, sentinel = 2, 333, 300, 4, 2, 40, 1024.0
+    print(f"case padded rows d={d}", flush=True)
+    _, q = bf16_pair((b, sq, hq, d), 41)
+    _, k = bf16_pair((b, sk, hkv, d), 42)
+    _, v = bf16_pair((b, sk, hkv, d), 43)
+    _, do = bf16_pair((b, sq, hq, d), 44)
+    sc = d ** -0.5
+    mask = abi.MASK_FULL
+    bufs = []
+
+    def out_like(dtype, padded, fill=None):
+        shape = (b, sq, hq, d + (pad if padded else 0))
+        buf = torch.full(shape, sentinel, dtype=dtype, device="cuda")
+        view = buf[..., :d]
+        if fill is not None:
+            view.copy_(fill)
+        if padded:
+            bufs.append(buf)
+        return view
+
+    def lse_like(fill=None):
+        t = torch.empty((b, hq, sq), device="cuda")
+        if fill is not None:
+            t.copy_(fill)
+        return t
+
+    def forward_modes(padded):
+        res = []
+        out, acc = out_like(torch.bfloat16, padded), out_like(torch.float32, padded)
+        lse = lse_like()
+        ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_WRITE, out=out, lse=lse, acc_out=acc)],
+                     scale=sc, mask=mask)
+        res += [out.clone(), acc.clone(), lse.clone()]
+        acc, acc_lse = out_like(torch.float32, padded), lse_like()
+        ops.attn_fwd([ops.FwdJob(q=q, k=k, v=v, mode=abi.FWD_ACC_INIT, acc_out=acc, acc_lse=acc_lse)],
+                     scale=sc, mask=mask)
+        res += [acc.clone(), acc_lse.clone()]
+        ops.attn_fwd([ops.FwdJob(q=q, k=torch.flip(k, dims=[1]), v=v, mode=abi.FWD_ACC_MERGE, acc_out=acc,
+                                 acc_lse=acc_lse)], scale=sc, mask=mask)
+        res += [acc.clone(), acc_lse.clone()]
+        out = out_like(torch.bfloat16, padded)
+        ops.attn_fwd([ops.FwdJob(q=q, k=k, v=torch.flip(v, dims=[1]), mode=abi.FWD_ACC_FINAL, out=out,
+                                 acc_out=acc, acc_lse=acc_lse)], scale=sc, mask=mask)
+        res += [out.clone(), acc.clone()]
+        torch.cuda.synchronize()
+        return res, lse
+
+    ref, lse = forward_modes(False)
+    got, _ = forward_modes(True)
+    for i, (a, g) in enumerate(zip(ref, got)):
+        assert torch.equal(a, g), f"forward result {i} differs with padded outputs"
+
+    out32 = ref[1]
+    delta, nlse = lse_like(), lse_like()
+    ops.attn_bwd_delta(out32, do, delta, hkv, lse=lse, nlse=nlse)
+    g = torch.Generator(device="cuda").manual_seed(45)
+    prior = torch.randn((b, sq, hq, d), generator=g, device="cuda")
+
+    def dq_modes(padded):
+        dout = out_like(torch.bfloat16, padded, do)
+        common = dict(q=q, k=k, v=v, dout=dout, lse=lse, delta=delta, nlse=nlse, dkv_mode=abi.GRAD_NONE)
+        res = []
+        for mode in (abi.GRAD_WRITE_F32, abi.GRAD_ACC_F32, abi.GRAD_ACC_FINAL, abi.GRAD_WRITE_BF16):
+            acc = out_like(torch.float32, padded, prior) if mode != abi.GRAD_WRITE_BF16 else None
+            dq = out_like(torch.bfloat16, padded)
+            ops.attn_bwd([ops.BwdJob(dq_mode=mode, dq_acc=acc, dq=dq, **common)], scale=sc, mask=mask)
+            torch.cuda.synchronize()
+            res += [dq.clone()] + ([acc.clone()] if acc is not None else [])
+        return res
+
+    ref = dq_modes(False)
+    got = dq_modes(True)
+    for i, (a, g) in enumerate(zip(ref, got)):
+        assert torch.equal(a, g), f"dq result {i} differs with padded outputs"
+    for buf in bufs:
+        assert (buf[..., d:] == sentinel).all(), "a store reached the padding past the head dim"
